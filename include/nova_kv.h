@@ -1,0 +1,184 @@
+/*
+ * nova_kv.h — C ABI of the MI355X (gfx950) int8 KV-cache decode path.
+ *
+ * Every entry point takes raw device pointers, element counts/strides and a
+ * hipStream_t passed as `void*` (the caller's current stream; pass the stream
+ * that torch is capturing on to record the launch into a hipGraph). Nothing
+ * here allocates device memory, synchronizes the device or reads device memory
+ * on the host, so every call is safe inside stream capture. Scratch memory
+ * (`workspace`, `counters`) is owned by the caller.
+ *
+ * Return value: NKV_OK, or a NKV_ERR_* code; `nkv_last_error()` then returns
+ * a message for the calling thread. Launches are asynchronous: a fault inside
+ * a kernel surfaces at the next synchronizing HIP call, as for any HIP kernel.
+ *
+ * Tensor layouts follow the reference (batch 1): codes `[H_kv, L, D]` uint8,
+ * rulers `[H_kv, ceil(L/64), D]` fp16, ring `[H_kv, 64, D]` fp16, device
+ * scalars are single int64 values. fp16 buffers are typed `uint16_t`.
+ *
+ * Each declaration names the reference interface it replaces (file:line of
+ * captain-wangrun-cn/Nova).
+ */
+#ifndef NOVA_KV_H
+#define NOVA_KV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NKV_ABI_VERSION 1
+
+#define NKV_OK 0
+#define NKV_ERR_INVALID 1     /* argument outside what the reference accepts */
+#define NKV_ERR_UNSUPPORTED 2 /* accepted by the reference, not built for this GPU path */
+#define NKV_ERR_HIP 3         /* HIP launch/runtime error */
+
+#define NKV_F16 0
+#define NKV_BF16 1
+#define NKV_F32 2
+
+#define NKV_AXIS_CHANNEL 0
+#define NKV_AXIS_TOKEN 1
+
+/* ABI version of the loaded library (NKV_ABI_VERSION at build time). */
+int nkv_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* nkv_last_error(void);
+
+/*
+ * Asymmetric int8 quantization, one (min, step) ruler per group.
+ * Replaces `kvquant.quantize_int8(x, group_size, axis)` (src/nova/kvquant.py:118-149).
+ *
+ * x: `rows` slabs of `[n, dim]` (dim contiguous, token stride = dim), slab
+ * stride `x_row_stride` elements; dtype NKV_F16 / NKV_BF16 / NKV_F32.
+ * axis NKV_AXIS_TOKEN: groups of `group` tokens per channel (0 = all n),
+ *   rulers `[rows, ceil(n/group), dim]`, the last group ruled by its real
+ *   tokens (the reference's replicate pad, kvquant.py:138-143).
+ * axis NKV_AXIS_CHANNEL: groups of `group` channels per token (0 = all dim),
+ *   rulers `[rows, n, dim/group]`.
+ * codes: uint8 slabs of `[n, dim]`, slab stride `codes_row_stride`.
+ * mins/steps: fp16 slabs, slab stride `scale_row_stride`.
+ * step = max((max-min)/255, 1e-8) in fp32, code = clamp(rint((x-min)/step), 0, 255),
+ * min/step stored as fp16 (round to nearest even) — bit-exact with the reference.
+ */
+int nkv_quantize_int8(const void* x, int x_dtype, int64_t x_row_stride, int64_t rows, int64_t n,
+                      int64_t dim, int64_t group, int axis, uint8_t* codes,
+                      int64_t codes_row_stride, uint16_t* mins, uint16_t* steps,
+                      int64_t scale_row_stride, void* stream);
+
+/*
+ * Inverse of nkv_quantize_int8: out = round(fp32(code)*fp32(step) + fp32(min)) in
+ * `out_dtype` (NKV_F16 / NKV_BF16 / NKV_F32).
+ * Replaces `kvquant.dequantize_int8` (src/nova/kvquant.py:152-176).
+ * Same slab/stride conventions as nkv_quantize_int8; `out` slab stride is
+ * `out_row_stride` elements.
+ */
+int nkv_dequantize_int8(const uint8_t* codes, int64_t codes_row_stride, const uint16_t* mins,
+                        const uint16_t* steps, int64_t scale_row_stride, int64_t rows, int64_t n,
+                        int64_t dim, int64_t group, int axis, void* out, int out_dtype,
+                        int64_t out_row_stride, void* stream);
+
+/*
+ * Split-K int8 decode attention for one layer, `int8t64` cache, head_dim 128.
+ * Replaces `kvattn.int8_attn_decode` (src/nova/kvattn.py:281-427), i.e. the
+ * Triton `_int8_attn_partial_kernel` + `_int8_attn_combine_kernel`
+ * (kvattn.py:110-253), and — when `tail_k` is given — `tail_attend` plus the
+ * log-sum-exp merge of `KVInt8Cache.attend` (kvattn.py:447-482, 835-862).
+ *
+ * q [hq, 128] fp16 (RoPE applied); hq % hkv == 0, hq/hkv <= 16.
+ * Prefix: tokens [0, used) of the int8 cache, limited to `prefix_groups`
+ *   whole rulers; the values come from `used_dev` / `prefix_groups_dev`
+ *   (device int64) when non-NULL, else from `used` / `prefix_groups`.
+ * Tail (optional, tail_k != NULL): the 64-slot fp16 ring; slot i holds
+ *   position p = u - ((u - i) mod 64), u = *written_dev - 1, and takes part iff
+ *   used <= p <= u and p >= *first_dev.
+ * out [hq, 128] fp16 = softmax(q k^T / sqrt(128)) v over prefix U tail.
+ * lse_out [hq] fp32 (may be NULL) = log-sum-exp of the scaled scores; an empty
+ *   key set gives out 0 and lse -inf (kvattn.py:244-253).
+ * workspace: >= nkv_attn_workspace_bytes(hkv, hq, n_parts) bytes of device memory.
+ * counters: >= hkv uint32, zero before the first call; every call leaves them zero.
+ * n_parts: work units per KV head (fixed for a captured graph); 0 picks one from
+ *   `capacity` (or from `used` when no device scalar is given).
+ * Calls that overlap on one GPU must not share `counters` or `workspace`.
+ */
+int nkv_attn_decode_t64(const uint16_t* q, const uint8_t* kq, const uint16_t* kmn,
+                        const uint16_t* kst, const uint8_t* vq, const uint16_t* vmn,
+                        const uint16_t* vst, int64_t hq, int64_t hkv, int64_t head_dim,
+                        int64_t capacity, int64_t used, int64_t prefix_groups,
+                        const int64_t* used_dev, const int64_t* prefix_groups_dev,
+                        const uint16_t* tail_k, const uint16_t* tail_v,
+                        const int64_t* written_dev, const int64_t* first_dev, uint16_t* out,
+                        float* lse_out, void* workspace, int64_t workspace_bytes,
+                        uint32_t* counters, int64_t n_parts, void* stream);
+
+/* Bytes of `workspace` that nkv_attn_decode_t64 / nkv_decode_step_t64 need. */
+int64_t nkv_attn_workspace_bytes(int64_t hkv, int64_t hq, int64_t n_parts);
+
+/* The n_parts value that `n_parts = 0` resolves to for `groups` rulers per head. */
+int64_t nkv_attn_default_parts(int64_t hkv, int64_t groups);
+
+/*
+ * Streaming append of one decode token into the int8 cache of one layer.
+ * Replaces `KVInt8Cache.update` on the decode path with `_quantize_ring` and
+ * `_sync_scalars` (src/nova/kvattn.py:668-743, 699-710): writes k/v into ring
+ * slot pos%64, requantizes all 64 ring slots (in slot order) into ruler group
+ * pos//64, and sets written = pos+1, qlen = 64*floor(written/64), pg = qlen/64.
+ * k_new/v_new: [hkv, 128] fp16 with head stride `kv_head_stride` elements.
+ */
+int nkv_append_t64(const uint16_t* k_new, const uint16_t* v_new, int64_t kv_head_stride,
+                   uint8_t* kq, uint16_t* kmn, uint16_t* kst, uint8_t* vq, uint16_t* vmn,
+                   uint16_t* vst, uint16_t* tail_k, uint16_t* tail_v, const int64_t* pos_dev,
+                   int64_t* written_dev, int64_t* qlen_dev, int64_t* pg_dev, int64_t hkv,
+                   int64_t head_dim, int64_t capacity, void* stream);
+
+/*
+ * One decode step of one layer in a single launch: nkv_append_t64 followed by
+ * nkv_attn_decode_t64 over the int8 prefix and the ring, with identical results
+ * to the two-call sequence up to float summation order. Replaces the
+ * `KVInt8Cache.update` + `KVInt8Cache.attend` pair that `LeanAttention.forward`
+ * issues per layer (src/nova/layers.py:132-136).
+ */
+int nkv_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                        int64_t kv_head_stride, uint8_t* kq, uint16_t* kmn, uint16_t* kst,
+                        uint8_t* vq, uint16_t* vmn, uint16_t* vst, uint16_t* tail_k,
+                        uint16_t* tail_v, const int64_t* pos_dev, const int64_t* first_dev,
+                        int64_t* written_dev, int64_t* qlen_dev, int64_t* pg_dev, int64_t hq,
+                        int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out,
+                        float* lse_out, void* workspace, int64_t workspace_bytes,
+                        uint32_t* counters, int64_t n_parts, void* stream);
+
+/*
+ * fp16 ring attention with a boolean slot mask and its log-sum-exp.
+ * Replaces `kvattn.tail_attend(q, k, v, tail_mask)` (src/nova/kvattn.py:447-482).
+ * q [hq, 128]; k/v [hkv, slots, 128] fp16 (slots <= 64); mask [slots] uint8 (0/1);
+ * out [hq, 128] fp16; lse [hq] fp32. An all-false mask gives out 0, lse -inf.
+ */
+int nkv_tail_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                    const uint8_t* mask, int64_t hq, int64_t hkv, int64_t head_dim,
+                    int64_t slots, uint16_t* out, float* lse, void* workspace,
+                    int64_t workspace_bytes, uint32_t* counters, void* stream);
+
+/*
+ * Ring validity mask from the device scalars.
+ * Replaces `KVInt8Cache.ring_mask` (src/nova/kvattn.py:819-833).
+ * mask[i] = (qlen <= p <= u) && (p >= first), p = u - ((u - i) mod slots),
+ * u = *written_dev - 1; mask is uint8 [slots].
+ */
+int nkv_ring_mask(const int64_t* written_dev, const int64_t* qlen_dev, const int64_t* first_dev,
+                  int64_t slots, uint8_t* mask, void* stream);
+
+/*
+ * Plain device copy (16-byte vector loads and stores). Used to calibrate the
+ * HBM traffic counters (FETCH_SIZE / WRITE_SIZE) against a known byte count;
+ * no counterpart in the reference. nbytes must be a multiple of 16.
+ */
+int nkv_copy_bytes(const void* src, void* dst, int64_t nbytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NOVA_KV_H */

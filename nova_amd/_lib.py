@@ -1,0 +1,131 @@
+"""ctypes binding of ``libnova_kv.so`` (the C ABI declared in ``include/nova_kv.h``).
+
+The library is loaded after ``torch`` so that its ``libamdhip64.so.7`` dependency
+resolves to the HIP runtime torch already mapped (same soname): device pointers
+and ``hipStream_t`` handles from torch are then valid inside the library.
+
+There is no fallback: if the library is missing, or the process has no GPU, the
+calls raise ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import c_float, c_int, c_int64, c_void_p
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libnova_kv.so"
+
+NKV_OK = 0
+NKV_ERR_INVALID = 1
+NKV_ERR_UNSUPPORTED = 2
+NKV_ERR_HIP = 3
+
+NKV_F16, NKV_BF16, NKV_F32 = 0, 1, 2
+NKV_AXIS_CHANNEL, NKV_AXIS_TOKEN = 0, 1
+
+P = c_void_p
+I64 = c_int64
+
+# name -> (restype, argtypes); must match include/nova_kv.h
+SIGNATURES = {
+    "nkv_abi_version": (c_int, []),
+    "nkv_last_error": (ctypes.c_char_p, []),
+    "nkv_quantize_int8": (c_int, [P, c_int, I64, I64, I64, I64, I64, c_int, P, I64, P, P, I64, P]),
+    "nkv_dequantize_int8": (c_int, [P, I64, P, P, I64, I64, I64, I64, I64, c_int, P, c_int, I64, P]),
+    "nkv_attn_decode_t64": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P,
+                                    P, P, P, I64, P, I64, P]),
+    "nkv_attn_workspace_bytes": (I64, [I64, I64, I64]),
+    "nkv_attn_default_parts": (I64, [I64, I64]),
+    "nkv_append_t64": (c_int, [P, P, I64, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, P]),
+    "nkv_decode_step_t64": (c_int, [P, P, P, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64,
+                                    P, P, P, I64, P, I64, P]),
+    "nkv_tail_attend": (c_int, [P, P, P, P, I64, I64, I64, I64, P, P, P, I64, P, P]),
+    "nkv_ring_mask": (c_int, [P, P, P, I64, P, P]),
+    "nkv_copy_bytes": (c_int, [P, P, I64, P]),
+}
+
+ABI_VERSION = 1
+
+_lib = None
+_lock = threading.Lock()
+
+
+class NovaKVError(RuntimeError):
+    """A failing ``nkv_*`` call; ``code`` is the NKV_ERR_* status."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(msg)
+        self.code = code
+
+
+def load(require_gpu: bool = True):
+    """Load (once) and return the ctypes handle of ``libnova_kv.so``."""
+    global _lib
+    if require_gpu and not torch.cuda.is_available():
+        raise RuntimeError("nova_amd needs a ROCm GPU (gfx950); none is visible to torch")
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m nova_amd.build`")
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            if lib.nkv_abi_version() != ABI_VERSION:
+                raise RuntimeError(f"libnova_kv ABI {lib.nkv_abi_version()} != {ABI_VERSION}: rebuild it")
+            _lib = lib
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Call ``name``; raise ``ValueError`` (invalid argument), ``NotImplementedError``
+    (unsupported here) or ``NovaKVError`` (HIP failure) on a nonzero status."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != NKV_OK:
+        msg = lib.nkv_last_error().decode("utf-8", "replace")
+        if rc == NKV_ERR_INVALID:
+            raise ValueError(f"{name}: {msg}")
+        if rc == NKV_ERR_UNSUPPORTED:
+            raise NotImplementedError(f"{name}: {msg}")
+        raise NovaKVError(rc, f"{name}: {msg}")
+
+
+def stream_ptr(device: torch.device | None = None) -> int:
+    """The current torch stream of ``device`` as a raw ``hipStream_t``."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+# per-device zero-initialised counters for standalone calls (the kernels leave them zero)
+_COUNTERS: dict[str, torch.Tensor] = {}
+_WORKSPACES: dict[str, torch.Tensor] = {}
+
+
+def counters(device: torch.device, n: int) -> torch.Tensor:
+    key = str(device)
+    c = _COUNTERS.get(key)
+    if c is None or c.numel() < n:
+        c = torch.zeros(max(n, 64), dtype=torch.int32, device=device)
+        _COUNTERS[key] = c
+    return c
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A cached per-device byte workspace of at least ``nbytes`` (grown eagerly, never inside capture)."""
+    key = str(device)
+    w = _WORKSPACES.get(key)
+    if w is None or w.numel() < nbytes:
+        w = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = w
+    return w

@@ -1,0 +1,110 @@
+"""The C ABI library loads on a CPU-only host and exports exactly what include/nova_kv.h declares.
+
+No kernel is launched here: only host-side functions (version, workspace sizing) and
+argument validation that returns before any launch are called.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "nova_kv.h"
+
+
+def _declared() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(nkv_[a-z0-9_]+)\s*\(", text))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from nova_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.fail("nova_amd/libnova_kv.so is not built (python -m nova_amd.build)")
+    return _lib.load(require_gpu=False)
+
+
+def test_header_declares_the_path():
+    names = _declared()
+    for must in ("nkv_quantize_int8", "nkv_dequantize_int8", "nkv_attn_decode_t64", "nkv_append_t64",
+                 "nkv_decode_step_t64", "nkv_tail_attend", "nkv_ring_mask"):
+        assert must in names
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    from nova_amd import _lib
+
+    names = _declared()
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in nova_kv.h but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == names
+
+
+def test_abi_version_and_host_helpers(lib):
+    from nova_amd import _lib
+
+    assert lib.nkv_abi_version() == _lib.ABI_VERSION
+    # 32K tokens = 512 rulers per head: 64 parts per head over 8 heads
+    assert lib.nkv_attn_default_parts(8, 512) == 64
+    assert lib.nkv_attn_default_parts(8, 1) == 1
+    per_part = 8 * 4 * 130 * 4
+    assert lib.nkv_attn_workspace_bytes(8, 32, 64) == 65 * per_part
+
+
+def test_only_one_hip_runtime_is_mapped(lib):
+    """torch's libamdhip64 and the library's must be one and the same mapping."""
+    maps = Path("/proc/self/maps").read_text().splitlines()
+    paths = {ln.split()[-1] for ln in maps if "libamdhip64" in ln}
+    assert len(paths) == 1, paths
+
+
+def test_validation_errors_return_before_launch(lib):
+    """Bad arguments come back as status codes with a message; nothing is launched."""
+    from nova_amd import _lib
+
+    rc = lib.nkv_quantize_int8(None, 7, 0, 1, 1, 128, 64, 1, None, 0, None, None, 0, None)
+    assert rc == _lib.NKV_ERR_INVALID
+    assert b"dtype" in lib.nkv_last_error()
+    rc = lib.nkv_quantize_int8(None, 0, 0, 1, 1, 128, 64, 5, None, 0, None, None, 0, None)
+    assert rc == _lib.NKV_ERR_INVALID and b"axis" in lib.nkv_last_error()
+    # Q heads not divisible by KV heads, head_dim other than 128
+    args = [None] * 7 + [30, 8, 128, 64, 64, 1, None, None, None, None, None, None, None, None, None, 1 << 20,
+                         None, 0, None]
+    assert lib.nkv_attn_decode_t64(*args) == _lib.NKV_ERR_INVALID
+    assert b"divisible" in lib.nkv_last_error()
+    args[7], args[9] = 32, 64
+    assert lib.nkv_attn_decode_t64(*args) == _lib.NKV_ERR_UNSUPPORTED
+    assert b"head_dim" in lib.nkv_last_error()
+    assert lib.nkv_copy_bytes(None, None, 15, None) == _lib.NKV_ERR_INVALID
+    assert lib.nkv_ring_mask(None, None, None, 64, None, None) == _lib.NKV_ERR_INVALID
+
+
+def test_product_path_refuses_to_run_without_gpu():
+    import torch
+
+    from nova_amd import _lib
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    with pytest.raises(RuntimeError, match="GPU"):
+        _lib.load()
+
+
+def test_ctypes_argument_counts_match_header():
+    """Each declaration's parameter count equals its ctypes argtypes length."""
+    from nova_amd import _lib
+
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    for m in re.finditer(r"\b(nkv_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        name, params = m.group(1), m.group(2).strip()
+        n = 0 if params in ("", "void") else params.count(",") + 1
+        assert len(_lib.SIGNATURES[name][1]) == n, name
+    assert ctypes.sizeof(ctypes.c_void_p) == 8
