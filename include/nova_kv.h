@@ -6,7 +6,7 @@
  * that torch is capturing on to record the launch into a hipGraph). Nothing
  * here allocates device memory, synchronizes the device or reads device memory
  * on the host, so every call is safe inside stream capture. Scratch memory
- * (`workspace`, `counters`) is owned by the caller.
+ * (`workspace`) is owned by the caller.
  *
  * Return value: NKV_OK, or a NKV_ERR_* code; `nkv_last_error()` then returns
  * a message for the calling thread. Launches are asynchronous: a fault inside
@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 1
+#define NKV_ABI_VERSION 2
 
 #define NKV_OK 0
 #define NKV_ERR_INVALID 1     /* argument outside what the reference accepts */
@@ -87,6 +87,9 @@ int nkv_dequantize_int8(const uint8_t* codes, int64_t codes_row_stride, const ui
  * Triton `_int8_attn_partial_kernel` + `_int8_attn_combine_kernel`
  * (kvattn.py:110-253), and — when `tail_k` is given — `tail_attend` plus the
  * log-sum-exp merge of `KVInt8Cache.attend` (kvattn.py:447-482, 835-862).
+ * Two launches on `stream`: the prefix kernel (hkv * n_parts workgroups, one
+ * partial each into `workspace`), then the tail kernel (hkv workgroups: ring,
+ * merge, out / lse).
  *
  * q [hq, 128] fp16 (RoPE applied); hq % hkv == 0, hq/hkv <= 16.
  * Prefix: tokens [0, used) of the int8 cache, limited to `prefix_groups`
@@ -98,11 +101,11 @@ int nkv_dequantize_int8(const uint8_t* codes, int64_t codes_row_stride, const ui
  * out [hq, 128] fp16 = softmax(q k^T / sqrt(128)) v over prefix U tail.
  * lse_out [hq] fp32 (may be NULL) = log-sum-exp of the scaled scores; an empty
  *   key set gives out 0 and lse -inf (kvattn.py:244-253).
- * workspace: >= nkv_attn_workspace_bytes(hkv, hq, n_parts) bytes of device memory.
- * counters: >= hkv uint32, zero before the first call; every call leaves them zero.
- * n_parts: work units per KV head (fixed for a captured graph); 0 picks one from
- *   `capacity` (or from `used` when no device scalar is given).
- * Calls that overlap on one GPU must not share `counters` or `workspace`.
+ * workspace: >= nkv_attn_workspace_bytes(hkv, hq, n_parts) bytes of device memory,
+ *   16-byte aligned.
+ * n_parts: prefix work units per KV head (fixed for a captured graph); 0 picks one
+ *   from `capacity` (or from `used` when no device scalar is given).
+ * Calls that overlap on one GPU must not share `workspace`.
  */
 int nkv_attn_decode_t64(const uint16_t* q, const uint8_t* kq, const uint16_t* kmn,
                         const uint16_t* kst, const uint8_t* vq, const uint16_t* vmn,
@@ -112,7 +115,7 @@ int nkv_attn_decode_t64(const uint16_t* q, const uint8_t* kq, const uint16_t* km
                         const uint16_t* tail_k, const uint16_t* tail_v,
                         const int64_t* written_dev, const int64_t* first_dev, uint16_t* out,
                         float* lse_out, void* workspace, int64_t workspace_bytes,
-                        uint32_t* counters, int64_t n_parts, void* stream);
+                        int64_t n_parts, void* stream);
 
 /* Bytes of `workspace` that nkv_attn_decode_t64 / nkv_decode_step_t64 need. */
 int64_t nkv_attn_workspace_bytes(int64_t hkv, int64_t hq, int64_t n_parts);
@@ -135,11 +138,13 @@ int nkv_append_t64(const uint16_t* k_new, const uint16_t* v_new, int64_t kv_head
                    int64_t head_dim, int64_t capacity, void* stream);
 
 /*
- * One decode step of one layer in a single launch: nkv_append_t64 followed by
- * nkv_attn_decode_t64 over the int8 prefix and the ring, with identical results
- * to the two-call sequence up to float summation order. Replaces the
- * `KVInt8Cache.update` + `KVInt8Cache.attend` pair that `LeanAttention.forward`
- * issues per layer (src/nova/layers.py:132-136).
+ * One decode step of one layer: nkv_append_t64 followed by nkv_attn_decode_t64
+ * over the int8 prefix and the ring, with the same cache state and scalars as the
+ * two-call sequence and the same output up to float summation order. Two launches:
+ * the prefix kernel, then the tail kernel, which also performs the append (its
+ * group is not read by the prefix kernel). Replaces the `KVInt8Cache.update` +
+ * `KVInt8Cache.attend` pair that `LeanAttention.forward` issues per layer
+ * (src/nova/layers.py:132-136).
  */
 int nkv_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                         int64_t kv_head_stride, uint8_t* kq, uint16_t* kmn, uint16_t* kst,
@@ -148,7 +153,7 @@ int nkv_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t
                         int64_t* written_dev, int64_t* qlen_dev, int64_t* pg_dev, int64_t hq,
                         int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out,
                         float* lse_out, void* workspace, int64_t workspace_bytes,
-                        uint32_t* counters, int64_t n_parts, void* stream);
+                        int64_t n_parts, void* stream);
 
 /*
  * fp16 ring attention with a boolean slot mask and its log-sum-exp.
@@ -158,8 +163,7 @@ int nkv_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t
  */
 int nkv_tail_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                     const uint8_t* mask, int64_t hq, int64_t hkv, int64_t head_dim,
-                    int64_t slots, uint16_t* out, float* lse, void* workspace,
-                    int64_t workspace_bytes, uint32_t* counters, void* stream);
+                    int64_t slots, uint16_t* out, float* lse, void* stream);
 
 /*
  * Ring validity mask from the device scalars.
@@ -176,6 +180,15 @@ int nkv_ring_mask(const int64_t* written_dev, const int64_t* qlen_dev, const int
  * no counterpart in the reference. nbytes must be a multiple of 16.
  */
 int nkv_copy_bytes(const void* src, void* dst, int64_t nbytes, void* stream);
+
+/*
+ * Read-bandwidth probe: `blocks` workgroups of 256 lanes read `nbytes` from `src` with
+ * 16-byte loads and write one XOR checksum per workgroup to sink[blocks]. Times the
+ * HBM read ceiling a single launch of a given size reaches, the counterpart of the
+ * reference's read-and-reduce ceiling bench (src/diagnostics/bench_int8_unpack.py:58-102).
+ * nbytes must be a multiple of 16.
+ */
+int nkv_read_bw(const void* src, int64_t nbytes, uint32_t* sink, int64_t blocks, void* stream);
 
 #ifdef __cplusplus
 }

@@ -37,18 +37,19 @@ SIGNATURES = {
     "nkv_quantize_int8": (c_int, [P, c_int, I64, I64, I64, I64, I64, c_int, P, I64, P, P, I64, P]),
     "nkv_dequantize_int8": (c_int, [P, I64, P, P, I64, I64, I64, I64, I64, c_int, P, c_int, I64, P]),
     "nkv_attn_decode_t64": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P,
-                                    P, P, P, I64, P, I64, P]),
+                                    P, P, P, I64, I64, P]),
     "nkv_attn_workspace_bytes": (I64, [I64, I64, I64]),
     "nkv_attn_default_parts": (I64, [I64, I64]),
     "nkv_append_t64": (c_int, [P, P, I64, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, P]),
     "nkv_decode_step_t64": (c_int, [P, P, P, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64,
-                                    P, P, P, I64, P, I64, P]),
-    "nkv_tail_attend": (c_int, [P, P, P, P, I64, I64, I64, I64, P, P, P, I64, P, P]),
+                                    P, P, P, I64, I64, P]),
+    "nkv_tail_attend": (c_int, [P, P, P, P, I64, I64, I64, I64, P, P, P]),
     "nkv_ring_mask": (c_int, [P, P, P, I64, P, P]),
     "nkv_copy_bytes": (c_int, [P, P, I64, P]),
+    "nkv_read_bw": (c_int, [P, I64, P, I64, P]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 _lock = threading.Lock()
@@ -107,18 +108,7 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
-# per-device zero-initialised counters for standalone calls (the kernels leave them zero)
-_COUNTERS: dict[str, torch.Tensor] = {}
 _WORKSPACES: dict[str, torch.Tensor] = {}
-
-
-def counters(device: torch.device, n: int) -> torch.Tensor:
-    key = str(device)
-    c = _COUNTERS.get(key)
-    if c is None or c.numel() < n:
-        c = torch.zeros(max(n, 64), dtype=torch.int32, device=device)
-        _COUNTERS[key] = c
-    return c
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:

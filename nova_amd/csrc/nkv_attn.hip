@@ -1,40 +1,72 @@
 // Split-K int8 decode attention, ring append and the fused decode step (gfx950, wave64).
 //
 // Work decomposition. One launch covers one layer. Workgroup `bid` serves KV head
-// `bid % hkv` (with 8 KV heads every workgroup of a head lands on the same XCD, so
-// its partials stay in one L2) and part `bid / hkv`. Parts 0..n_parts-1 split the
-// whole 64-token groups of the int8 prefix evenly; part n_parts (when present) is
-// the ring worker: it appends the new token and requantizes the ring (fused step),
-// then attends over the ring or over the group the ring just completed. Each of
-// the 4 waves of a workgroup runs its own online softmax over every 4th group of
-// the workgroup's range; the waves merge through LDS, the workgroup writes one
-// (m, l, acc) partial, and the last workgroup of the head to finish (an atomic
-// counter that it also resets) merges the partials and writes out / lse.
+// `bid % hkv` and part `bid / hkv`: with 8 KV heads, consecutive workgroups land on the
+// 8 XCDs round-robin, so every workgroup of a head runs on one XCD and its partials
+// stay in that XCD's L2. Parts 0..n_parts-1 split the whole 64-token groups of the
+// int8 prefix evenly; part n_parts (when present) is the ring worker: it appends the
+// new token and requantizes the ring (fused step), then attends over the ring or over
+// the group the ring just completed.
+//
+// Streaming. Each of the 4 waves of a workgroup owns every 4th group of the
+// workgroup's range and a private two-stage ring of LDS buffers. A group is moved
+// HBM -> LDS by 20 asynchronous `global_load_lds_dwordx4` (K codes 8 x 1 KiB, V codes
+// 8 x 1 KiB, the four fp16 rulers 4 x 256 B); while a wave computes one group the next one is
+// in flight. Those loads are issued from inline assembly, and the wave waits for
+// them with an explicit `s_waitcnt vmcnt(n)`: left to the compiler, a wait for all
+// outstanding loads would be placed before every LDS read and serialize the stream.
+// Rows are stored with their 16-byte chunks XOR-swizzled by `swz(row)`, which makes
+// both LDS read patterns below free of bank conflicts.
 //
 // Per 64-token group and wave (D = 128, up to 16 query heads per KV head):
-//   S^T[token][head] = K[token][:] . Q[head][:]  — 4 token blocks x 8 k-steps of
-//     v_mfma_f32_16x16x16f16; K rows are dequantized in registers with packed
-//     fp16 math: fp16(code * step16 + min16) with one rounding (the reference
-//     computes the same product exactly in fp32 and rounds the sum to fp16).
+//   S^T[token][head] = K[token][:] . Q[head][:] — 4 token blocks x 4 k-steps of
+//     v_mfma_f32_16x16x32_f16. K codes are read with ds_read_b128 and dequantized in
+//     registers with packed fp16 math: fp16(code * step16 + min16), one rounding.
 //   online softmax in the log2 domain, fp32, over the 16 scores a lane holds.
-//   O[head][dim] += P[head][token] . V[token][dim] — P is split into two fp16
-//     halves (hi + lo, scaled by 2^15 so small weights keep 22 bits) and V codes
-//     are byte-transposed in registers into the MFMA B layout.
-// The P operand of the PV product is exactly the S^T output layout, so no data
-// moves between the two products.
+//   O[head][dim] += P[head][token] . V[token][dim] — 2 token blocks of 32 x 8 dim
+//     blocks. P is split into two fp16 halves (hi + lo, scaled by 2^15 so that small
+//     weights keep 22 bits). ds_read_b64_tr_b8 delivers the V codes already
+//     transposed into the MFMA B layout (8 tokens of one dim per lane), so all 8 codes
+//     of a lane share one ruler.
+// The P operand of the PV product is exactly the S^T output layout of two token
+// blocks, so no data moves between the two products.
 #include "nkv_common.h"
 
 namespace nkv {
 
+#ifndef NKV_WAVES
+#define NKV_WAVES 8
+#endif
+#ifndef NKV_STAGES
+#define NKV_STAGES 1
+#endif
+
 constexpr int D = 128;
-constexpr int GT = 64;      // tokens per ruler group == ring slots
-constexpr int WAVES = 4;    // waves per workgroup
+constexpr int GT = 64;              // tokens per ruler group == ring slots
+constexpr int WAVES = NKV_WAVES;    // waves per workgroup
 constexpr int THREADS = 64 * WAVES;
+constexpr int STAGES = NKV_STAGES;  // LDS buffers per wave
+constexpr int CODE_BYTES = GT * D;                        // one tensor's codes of one group
+constexpr int RULER_BYTES = 4 * D * 2;                    // kst, kmn, vst, vmn of one group
+constexpr int STAGE_BYTES = 2 * CODE_BYTES + RULER_BYTES;  // 17 KiB
+constexpr int LDS_BYTES = WAVES * STAGES * STAGE_BYTES;   // 136 KiB
+constexpr int RING_BYTES = GT * D * 2;                    // one fp16 ring tensor of one head
+constexpr int DMA_PER_GROUP = 2 * (CODE_BYTES / 1024) + 4;
 constexpr float P_SCALE = 32768.0f;       // 2^15
 constexpr float INV_P_SCALE = 1.0f / 32768.0f;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 constexpr float NEG_INF = -__builtin_huge_valf();
+
+static_assert(DMA_PER_GROUP == 20, "the vmcnt immediates below assume 20 loads per group");
+static_assert(STAGES == 1 || STAGES == 2, "one or two LDS stages per wave");
+static_assert(LDS_BYTES <= 160 * 1024, "LDS of one workgroup");
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef int v2i_t __attribute__((vector_size(8)));
+typedef __attribute__((address_space(3))) v2i_t lds_v2i_t;
 
 enum TailMode : int { TAIL_NONE = 0, TAIL_MASK = 1, TAIL_SCALARS = 2, TAIL_FUSED = 3 };
 
@@ -64,17 +96,41 @@ struct AttnArgs {
   int64_t capacity, ngroups_cap;
   int64_t tail_slots;
   int hq, hkv, gq;
-  int n_parts, nslots;
+  int n_parts;
   int tail_mode;
   float sl2;  // softmax scale * log2(e)
   uint16_t* out;
   float* lse;
   float* ws;
-  uint32_t* counters;
 };
 
+// XOR key of the 16-byte chunk positions of LDS row `row` (a token within its group).
+// K reads (16 consecutive rows, one chunk) and V transpose reads (rows 4g + {0..3} of
+// two 16-row blocks, one chunk) both hit 16 distinct bank positions per 16 lanes.
+__device__ __forceinline__ int swz(int row) { return ((row >> 1) & 7) ^ (((row >> 4) & 1) << 2); }
+
+// fp16 ring tensor in LDS: row r (256 B) keeps its 16-byte chunk c at position c ^ (r & 15),
+// so the 16 rows a K operand read touches land on 16 distinct banks.
+__device__ __forceinline__ int ring_chunk_pos(int row, int chunk) { return chunk ^ (row & 15); }
+
+// Reductions over the 4 lanes {l, l^16, l^32, l^48} with the gfx950 permlane swaps (VALU
+// only, no LDS round trip). permlane16_swap(x, x) returns rows (0,0,2,2) and (1,1,3,3) of
+// x, permlane32_swap(x, x) its lower and upper halves twice.
+__device__ __forceinline__ float max4rows(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum4rows(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Online-softmax state of one wave. m, l: head (lane & 15), log2 domain.
-// acc[cb][i]: head 4*(lane>>4) + i, dim 8*(lane&15) + cb, scaled by 2^15.
+// acc[cb][i]: head 4*(lane>>4) + i, dim 16*cb + (lane&15), scaled by 2^15.
 struct WaveState {
   float m, l;
   float4_t acc[8];
@@ -87,136 +143,199 @@ __device__ __forceinline__ void state_init(WaveState& st) {
   for (int cb = 0; cb < 8; ++cb) st.acc[cb] = float4_t{0.f, 0.f, 0.f, 0.f};
 }
 
-__device__ __forceinline__ half2_t bcast_half(uint32_t w, int hi) {
-  return as_h2(perm(w, w, hi ? 0x03020302u : 0x01000100u));
+__device__ __forceinline__ float4_t mfma32(half8_t a, half8_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// Q as the MFMA B operand: lane (c, g) holds head c's dims 16g + 64hh + 4j + [0..3]
-// for k-step 4hh + j (zero rows for c >= gq).
-__device__ __forceinline__ void load_q(const AttnArgs& a, int h, half4_t (&qb)[8]) {
+__device__ __forceinline__ half8_t as_h8(uint4 w) { return __builtin_bit_cast(half8_t, w); }
+
+// 8 codes (bytes of w0, w1) -> fp16(code * st + mn) per element, rulers per element.
+__device__ __forceinline__ half8_t dq8(uint32_t w0, uint32_t w1, uint4 st, uint4 mn) {
+  const half2_t a = __builtin_elementwise_fma(codes_to_h2(w0, kSelB01), as_h2(st.x), as_h2(mn.x));
+  const half2_t b = __builtin_elementwise_fma(codes_to_h2(w0, kSelB23), as_h2(st.y), as_h2(mn.y));
+  const half2_t c = __builtin_elementwise_fma(codes_to_h2(w1, kSelB01), as_h2(st.z), as_h2(mn.z));
+  const half2_t d = __builtin_elementwise_fma(codes_to_h2(w1, kSelB23), as_h2(st.w), as_h2(mn.w));
+  return half8_t{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+// 8 codes sharing one ruler (st, mn given as half2 splats).
+__device__ __forceinline__ half8_t dq8_splat(uint32_t w0, uint32_t w1, half2_t st, half2_t mn) {
+  const half2_t a = __builtin_elementwise_fma(codes_to_h2(w0, kSelB01), st, mn);
+  const half2_t b = __builtin_elementwise_fma(codes_to_h2(w0, kSelB23), st, mn);
+  const half2_t c = __builtin_elementwise_fma(codes_to_h2(w1, kSelB01), st, mn);
+  const half2_t d = __builtin_elementwise_fma(codes_to_h2(w1, kSelB23), st, mn);
+  return half8_t{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+// Q as the B operand of v_mfma_f32_16x16x32_f16: lane (c, g) holds head c's dims
+// 16g + 64hh + 8e + [0..7] for k-step 2hh + e (zeros for c >= gq).
+__device__ __forceinline__ void load_q(const AttnArgs& a, int h, half8_t (&qb)[4]) {
   const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    uint4 w0 = {0, 0, 0, 0}, w1 = {0, 0, 0, 0};
-    if (c < a.gq) {
-      const uint16_t* row = a.q + (int64_t)(h * a.gq + c) * D + 16 * g + 64 * hh;
-      w0 = *reinterpret_cast<const uint4*>(row);
-      w1 = *reinterpret_cast<const uint4*>(row + 8);
-    }
-    const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const half2_t lo = as_h2(w[2 * j]), hi = as_h2(w[2 * j + 1]);
-      qb[4 * hh + j] = half4_t{lo.x, lo.y, hi.x, hi.y};
-    }
+  for (int k = 0; k < 4; ++k) {
+    uint4 w = {0, 0, 0, 0};
+    if (c < a.gq) w = *reinterpret_cast<const uint4*>(a.q + (int64_t)(h * a.gq + c) * D + 16 * g + 64 * (k >> 1) + 8 * (k & 1));
+    qb[k] = as_h8(w);
   }
+  // Make the compiler complete these loads here, before the untracked LDS streams start:
+  // a wait it placed later would also wait for every group in flight.
+  asm volatile("" ::"v"(qb[0]), "v"(qb[1]), "v"(qb[2]), "v"(qb[3]));
 }
 
-// Online-softmax update with the 16 masked scores s[b][i] (token 16b + 4g + i, head c),
-// returns P split into hi/lo fp16 A operands and rescales the accumulator.
-__device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[4][4], half4_t (&phi)[4],
-                                             half4_t (&plo)[4]) {
+// ---------------------------------------------------------------- HBM -> LDS streaming
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_void_t*)p;
+}
+
+// A pointer the wave holds in common, moved to scalar registers.
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
+}
+
+// One `global_load_lds_dwordx4`: lane L's 16 bytes at sbase + voff land at LDS byte
+// address lds + 16 * L (sbase and lds are wave-uniform).
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
+}
+
+// Issue the 20 loads of group `grp` of head h into the LDS stage at byte address `st`.
+// LDS row r, chunk position p holds chunk p ^ swz(r) of token row r. Rows at or beyond
+// the cache capacity are never read (the last row is repeated).
+__device__ __forceinline__ void issue_group(const AttnArgs& a, int h, int64_t grp, uint32_t st) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t0 = grp * GT;
+  const int rows = (int)min<int64_t>(GT, a.capacity - t0);
+  const void* kb = uniform_ptr(a.kq + ((int64_t)h * a.capacity + t0) * D);
+  const void* vb = uniform_ptr(a.vq + ((int64_t)h * a.capacity + t0) * D);
+  st = __builtin_amdgcn_readfirstlane(st);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // earlier reads of this stage are done
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    const uint32_t off = (uint32_t)(min(row, rows - 1) * D + (((lane & 7) ^ swz(row)) << 4));
+    dma16(kb, off, st + 1024 * j);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    const uint32_t off = (uint32_t)(min(row, rows - 1) * D + (((lane & 7) ^ swz(row)) << 4));
+    dma16(vb, off, st + CODE_BYTES + 1024 * j);
+  }
+  // rulers: one load per tensor, lanes 16w..16w+15 active for tensor w (kst, kmn, vst, vmn),
+  // so that every base address stays in scalar registers
+  const int64_t ro = ((int64_t)h * a.ngroups_cap + grp) * D;
+  const uint32_t roff = (uint32_t)(8 * (lane & 15)) * 2;
+  const int which = lane >> 4;
+  if (which == 0) dma16(uniform_ptr(a.kst + ro), roff, st + 2 * CODE_BYTES);
+  if (which == 1) dma16(uniform_ptr(a.kmn + ro), roff, st + 2 * CODE_BYTES);
+  if (which == 2) dma16(uniform_ptr(a.vst + ro), roff, st + 2 * CODE_BYTES);
+  if (which == 3) dma16(uniform_ptr(a.vmn + ro), roff, st + 2 * CODE_BYTES);
+}
+
+__device__ __forceinline__ void wait_groups_all_but_one() { asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); }
+__device__ __forceinline__ void wait_groups_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// ---------------------------------------------------------------- one group's attention
+
+// Online-softmax update with the 16 masked scores s[b][i] (token 16b + 4g + i, head c);
+// returns P of token blocks (0,1) and (2,3) split into hi/lo fp16 A operands and
+// rescales the accumulator when a running maximum moved.
+__device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[4][4], half8_t (&phi)[2],
+                                             half8_t (&plo)[2], int gq) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
   float mloc = NEG_INF;
 #pragma unroll
   for (int b = 0; b < 4; ++b)
 #pragma unroll
     for (int i = 0; i < 4; ++i) mloc = fmaxf(mloc, s[b][i]);
-  mloc = fmaxf(mloc, shfl_xor(mloc, 16));
-  mloc = fmaxf(mloc, shfl_xor(mloc, 32));
+  mloc = max4rows(mloc);
   const float m_new = fmaxf(st.m, mloc);
   const float m_use = m_new == NEG_INF ? 0.0f : m_new;
   const float alpha = __builtin_amdgcn_exp2f(st.m - m_use);
   float lsum = 0.0f;
+  _Float16 hi[2][8], lo[2][8];
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
-    float p[4];
+    float q[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      p[i] = __builtin_amdgcn_exp2f(s[b][i] - m_use);
-      lsum += p[i];
+      const float p = __builtin_amdgcn_exp2f(s[b][i] - m_use);
+      lsum += p;
+      q[i] = p * P_SCALE;
     }
-    const float q0 = p[0] * P_SCALE, q1 = p[1] * P_SCALE, q2 = p[2] * P_SCALE, q3 = p[3] * P_SCALE;
-    const half2_t h01 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(q0, q1));
-    const half2_t h23 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(q2, q3));
-    const half2_t l01 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(q0 - (float)h01.x, q1 - (float)h01.y));
-    const half2_t l23 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(q2 - (float)h23.x, q3 - (float)h23.y));
-    phi[b] = half4_t{h01.x, h01.y, h23.x, h23.y};
-    plo[b] = half4_t{l01.x, l01.y, l23.x, l23.y};
+#pragma unroll
+    for (int i = 0; i < 4; i += 2) {
+      const half2_t h = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(q[i], q[i + 1]));
+      const half2_t l = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(q[i] - (float)h.x, q[i + 1] - (float)h.y));
+      hi[b >> 1][4 * (b & 1) + i] = h.x;
+      hi[b >> 1][4 * (b & 1) + i + 1] = h.y;
+      lo[b >> 1][4 * (b & 1) + i] = l.x;
+      lo[b >> 1][4 * (b & 1) + i + 1] = l.y;
+    }
   }
-  lsum += shfl_xor(lsum, 16);
-  lsum += shfl_xor(lsum, 32);
-  st.l = st.l * alpha + lsum;
+#pragma unroll
+  for (int B = 0; B < 2; ++B) {
+    phi[B] = half8_t{hi[B][0], hi[B][1], hi[B][2], hi[B][3], hi[B][4], hi[B][5], hi[B][6], hi[B][7]};
+    plo[B] = half8_t{lo[B][0], lo[B][1], lo[B][2], lo[B][3], lo[B][4], lo[B][5], lo[B][6], lo[B][7]};
+  }
+  st.l = st.l * alpha + sum4rows(lsum);
+  const bool moved = st.m != m_new;
   st.m = m_new;
-  // accumulator rows belong to head 4g + i; its alpha sits in lane 4g + i
+  // accumulator rows belong to head 4g + i; its alpha sits in lane 4g + i. Nothing to do
+  // while no maximum of the wave moved (alpha == 1 in every lane).
+  if (__builtin_amdgcn_ballot_w64(moved) == 0) return;
+  if (gq <= 4) {
+    // rows of g >= 1 are padding heads: one scalar alpha per row
+    float ai[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float ai = shfl(alpha, 4 * g + i);
+    for (int i = 0; i < 4; ++i) ai[i] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(alpha), i));
 #pragma unroll
-    for (int cb = 0; cb < 8; ++cb) st.acc[cb][i] *= ai;
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb) st.acc[cb][i] *= ai[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float ai = shfl(alpha, 4 * g + i);
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb) st.acc[cb][i] *= ai;
+    }
   }
 }
 
-// One 64-token group of the int8 cache: tokens [t0, t0 + 64) of head h, `nvalid` of them
-// valid. Rows at or beyond `capacity` are never loaded.
-__device__ __forceinline__ void attend_group_int8(const AttnArgs& a, WaveState& st,
-                                                  const half4_t (&qb)[8], int h, int64_t grp,
-                                                  int nvalid) {
+// One 64-token int8 group resident in an LDS stage, `nvalid` of its tokens valid.
+__device__ __forceinline__ void attend_stage(const AttnArgs& a, WaveState& st, const half8_t (&qb)[4],
+                                             const uint8_t* stage, int nvalid) {
   const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-  const int64_t t0 = grp * GT;
-  const int64_t last = a.capacity - 1;
-  const uint8_t* kq_h = a.kq + (int64_t)h * a.capacity * D;
-  const uint8_t* vq_h = a.vq + (int64_t)h * a.capacity * D;
-  const int64_t ro = ((int64_t)h * a.ngroups_cap + grp) * D;
-
-  // ---- loads
-  uint4 kc[4][2];
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const int64_t row = min(t0 + 16 * b + c, last);
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-      kc[b][hh] = *reinterpret_cast<const uint4*>(kq_h + row * D + 16 * g + 64 * hh);
-  }
-  uint2 vc[4][4];
-#pragma unroll
-  for (int b = 0; b < 4; ++b)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t row = min(t0 + 16 * b + 4 * g + r, last);
-      vc[b][r] = *reinterpret_cast<const uint2*>(vq_h + row * D + 8 * c);
-    }
-  uint32_t ksw[2][8], kmw[2][8];
-#pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    const uint4* ps = reinterpret_cast<const uint4*>(a.kst + ro + 16 * g + 64 * hh);
-    const uint4* pm = reinterpret_cast<const uint4*>(a.kmn + ro + 16 * g + 64 * hh);
-    const uint4 s0 = ps[0], s1 = ps[1], m0 = pm[0], m1 = pm[1];
-    ksw[hh][0] = s0.x; ksw[hh][1] = s0.y; ksw[hh][2] = s0.z; ksw[hh][3] = s0.w;
-    ksw[hh][4] = s1.x; ksw[hh][5] = s1.y; ksw[hh][6] = s1.z; ksw[hh][7] = s1.w;
-    kmw[hh][0] = m0.x; kmw[hh][1] = m0.y; kmw[hh][2] = m0.z; kmw[hh][3] = m0.w;
-    kmw[hh][4] = m1.x; kmw[hh][5] = m1.y; kmw[hh][6] = m1.z; kmw[hh][7] = m1.w;
-  }
-  const uint4 vsu = *reinterpret_cast<const uint4*>(a.vst + ro + 8 * c);
-  const uint4 vmu = *reinterpret_cast<const uint4*>(a.vmn + ro + 8 * c);
+  const uint16_t* rks = reinterpret_cast<const uint16_t*>(stage + 2 * CODE_BYTES);
+  const uint16_t* rkm = rks + D;
+  const uint16_t* rvs = rks + 2 * D;
+  const uint16_t* rvm = rks + 3 * D;
 
   // ---- S^T = K Q^T
+  uint4 kst4[2][2], kmn4[2][2];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      kst4[hh][e] = *reinterpret_cast<const uint4*>(rks + 16 * g + 64 * hh + 8 * e);
+      kmn4[hh][e] = *reinterpret_cast<const uint4*>(rkm + 16 * g + 64 * hh + 8 * e);
+    }
   float4_t S[4];
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     S[b] = float4_t{0.f, 0.f, 0.f, 0.f};
+    const int row = 16 * b + c;
+    const int key = swz(row);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
-      const uint32_t kw[4] = {kc[b][hh].x, kc[b][hh].y, kc[b][hh].z, kc[b][hh].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const half2_t k01 = __builtin_elementwise_fma(codes_to_h2(kw[j], kSelB01),
-                                                      as_h2(ksw[hh][2 * j]), as_h2(kmw[hh][2 * j]));
-        const half2_t k23 = __builtin_elementwise_fma(codes_to_h2(kw[j], kSelB23),
-                                                      as_h2(ksw[hh][2 * j + 1]), as_h2(kmw[hh][2 * j + 1]));
-        S[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(half4_t{k01.x, k01.y, k23.x, k23.y},
-                                                     qb[4 * hh + j], S[b], 0, 0, 0);
-      }
+      const uint4 kw = *reinterpret_cast<const uint4*>(stage + row * D + (((g + 4 * hh) ^ key) << 4));
+      S[b] = mfma32(dq8(kw.x, kw.y, kst4[hh][0], kmn4[hh][0]), qb[2 * hh], S[b]);
+      S[b] = mfma32(dq8(kw.z, kw.w, kst4[hh][1], kmn4[hh][1]), qb[2 * hh + 1], S[b]);
     }
   }
   float s[4][4];
@@ -225,134 +344,178 @@ __device__ __forceinline__ void attend_group_int8(const AttnArgs& a, WaveState& 
 #pragma unroll
     for (int i = 0; i < 4; ++i) s[b][i] = (16 * b + 4 * g + i) < nvalid ? S[b][i] * a.sl2 : NEG_INF;
 
-  half4_t phi[4], plo[4];
-  softmax_step(st, s, phi, plo);
+  half8_t phi[2], plo[2];
+  softmax_step(st, s, phi, plo, a.gq);
 
-  // ---- O += P V. Invalid tokens carry p = 0; their codes are zeroed so that a
-  // garbage ruler cannot turn 0 * v into NaN.
-  const uint32_t vsw[4] = {vsu.x, vsu.y, vsu.z, vsu.w};
-  const uint32_t vmw[4] = {vmu.x, vmu.y, vmu.z, vmu.w};
+  // ---- O += P V. Lane (c, g) of a transpose read supplies row k(g, c >> 1) and half
+  // (c & 1) of the 16-dim chunk; it receives dim 16cb + c of the 8 tokens k(g, 0..7),
+  // k(g, r) = 16 * (2B + (r >> 2)) + 4g + (r & 3), the token order of P's k-slots.
+  half2_t vsp[8], vmp[8];
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    uint32_t lo[4], hi[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const bool ok = (16 * b + 4 * g + r) < nvalid;
-      lo[r] = ok ? vc[b][r].x : 0u;
-      hi[r] = ok ? vc[b][r].y : 0u;
-    }
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const uint32_t w0 = half ? hi[0] : lo[0], w1 = half ? hi[1] : lo[1];
-      const uint32_t w2 = half ? hi[2] : lo[2], w3 = half ? hi[3] : lo[3];
-      const uint32_t t01a = perm(w1, w0, 0x05010400u), t01b = perm(w1, w0, 0x07030602u);
-      const uint32_t t23a = perm(w3, w2, 0x05010400u), t23b = perm(w3, w2, 0x07030602u);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int cb = 4 * half + k;
-        const uint32_t x01 = (k < 2) ? t01a : t01b;
-        const uint32_t x23 = (k < 2) ? t23a : t23b;
-        const uint32_t sel = (k & 1) ? kSelB23 : kSelB01;
-        const half2_t stp = bcast_half(vsw[cb >> 1], cb & 1);
-        const half2_t mnp = bcast_half(vmw[cb >> 1], cb & 1);
-        const half2_t v01 = __builtin_elementwise_fma(codes_to_h2(x01, sel), stp, mnp);
-        const half2_t v23 = __builtin_elementwise_fma(codes_to_h2(x23, sel), stp, mnp);
-        const half4_t vb = half4_t{v01.x, v01.y, v23.x, v23.y};
-        st.acc[cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi[b], vb, st.acc[cb], 0, 0, 0);
-        st.acc[cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo[b], vb, st.acc[cb], 0, 0, 0);
-      }
-    }
+  for (int cb = 0; cb < 8; ++cb) {
+    const _Float16 vs = __builtin_bit_cast(_Float16, rvs[16 * cb + c]);
+    const _Float16 vm = __builtin_bit_cast(_Float16, rvm[16 * cb + c]);
+    vsp[cb] = half2_t{vs, vs};
+    vmp[cb] = half2_t{vm, vm};
   }
-}
-
-// The fp16 ring (slots [0, tail_slots)) of head h; slot validity from `valid_bits`
-// (bit i = slot i takes part).
-__device__ __forceinline__ void attend_ring_f16(const AttnArgs& a, WaveState& st,
-                                                const half4_t (&qb)[8], int h, uint64_t valid_bits) {
-  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-  const int64_t last = a.tail_slots - 1;
-  const uint16_t* k_h = a.tail_k + (int64_t)h * a.tail_slots * D;
-  const uint16_t* v_h = a.tail_v + (int64_t)h * a.tail_slots * D;
-
-  float4_t S[4];
+  const int r = c >> 1;
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    S[b] = float4_t{0.f, 0.f, 0.f, 0.f};
-    const int64_t row = min((int64_t)(16 * b + c), last);
+  for (int B = 0; B < 2; ++B) {
+    const int row = 16 * (2 * B + (r >> 2)) + 4 * g + (r & 3);
+    const int key = swz(row);
+    const uint8_t* rowp = stage + CODE_BYTES + row * D + 8 * (c & 1);
+    // invalid tokens of a partial group get code 0 (finite value, weight 0)
+    u32x2 keep = {~0u, ~0u};
+    if (nvalid < GT) {
+      uint32_t m[2] = {0u, 0u};
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const uint4* p = reinterpret_cast<const uint4*>(k_h + row * D + 16 * g + 64 * hh);
-      const uint4 w0 = p[0], w1 = p[1];
-      const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const half2_t lo = as_h2(w[2 * j]), hi = as_h2(w[2 * j + 1]);
-        S[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(half4_t{lo.x, lo.y, hi.x, hi.y},
-                                                     qb[4 * hh + j], S[b], 0, 0, 0);
+      for (int rr = 0; rr < 8; ++rr) {
+        const int tok = 16 * (2 * B + (rr >> 2)) + 4 * g + (rr & 3);
+        if (tok < nvalid) m[rr >> 2] |= 0xffu << (8 * (rr & 3));
       }
-    }
-  }
-  float s[4][4];
-#pragma unroll
-  for (int b = 0; b < 4; ++b)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int slot = 16 * b + 4 * g + i;
-      s[b][i] = ((valid_bits >> slot) & 1ull) ? S[b][i] * a.sl2 : NEG_INF;
-    }
-  half4_t phi[4], plo[4];
-  softmax_step(st, s, phi, plo);
-
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    uint4 vr[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int slot = 16 * b + 4 * g + r;
-      const int64_t row = min((int64_t)slot, last);
-      vr[r] = *reinterpret_cast<const uint4*>(v_h + row * D + 8 * c);
-      if (!((valid_bits >> slot) & 1ull)) vr[r] = uint4{0, 0, 0, 0};
+      keep = u32x2{m[0], m[1]};
     }
 #pragma unroll
     for (int cb = 0; cb < 8; ++cb) {
-      const uint32_t sel = (cb & 1) ? 0x07060302u : 0x05040100u;
-      const int wi = cb >> 1;
-      const uint32_t w0 = wi == 0 ? vr[0].x : wi == 1 ? vr[0].y : wi == 2 ? vr[0].z : vr[0].w;
-      const uint32_t w1 = wi == 0 ? vr[1].x : wi == 1 ? vr[1].y : wi == 2 ? vr[1].z : vr[1].w;
-      const uint32_t w2 = wi == 0 ? vr[2].x : wi == 1 ? vr[2].y : wi == 2 ? vr[2].z : vr[2].w;
-      const uint32_t w3 = wi == 0 ? vr[3].x : wi == 1 ? vr[3].y : wi == 2 ? vr[3].z : vr[3].w;
-      const half2_t v01 = as_h2(perm(w1, w0, sel)), v23 = as_h2(perm(w3, w2, sel));
-      const half4_t vb = half4_t{v01.x, v01.y, v23.x, v23.y};
-      st.acc[cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi[b], vb, st.acc[cb], 0, 0, 0);
-      st.acc[cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo[b], vb, st.acc[cb], 0, 0, 0);
+      const u32x2 vw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                           (lds_v2i_t*)(const lds_void_t*)(rowp + ((cb ^ key) << 4)))) & keep;
+      const half8_t vb = dq8_splat(vw.x, vw.y, vsp[cb], vmp[cb]);
+      st.acc[cb] = mfma32(phi[B], vb, st.acc[cb]);
+      st.acc[cb] = mfma32(plo[B], vb, st.acc[cb]);
     }
   }
 }
 
-// Requantize the ring of one tensor (K or V) of head h into ruler group `gcur`, after
-// writing the new token into slot `slot`. One wave: lanes (l & 15) own 8 channels,
-// lanes (l >> 4) own rows (l >> 4) + 4i. Same arithmetic as the bulk quantizer.
-__device__ __forceinline__ void append_ring_tensor(uint16_t* ring_h, const uint16_t* new_h,
-                                                   uint8_t* codes_h, uint16_t* mn_g, uint16_t* st_g,
-                                                   int slot, int64_t gcur, int64_t capacity) {
-  const int lane = threadIdx.x & 63, cl = lane & 15, rl = lane >> 4;
-  uint4 rows[16];
+// Online-softmax update with the 4 masked scores s[i] (token 4g + i of a 16-token block,
+// head c); returns P as the A operand of v_mfma_f32_16x16x16_f16 (hi/lo halves).
+__device__ __forceinline__ void softmax_step4(WaveState& st, const float (&s)[4], half4_t& phi, half4_t& plo, int gq) {
+  const int lane = threadIdx.x & 63, g = lane >> 4;
+  const float mloc = max4rows(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+  const float m_new = fmaxf(st.m, mloc);
+  const float m_use = m_new == NEG_INF ? 0.0f : m_new;
+  const float alpha = __builtin_amdgcn_exp2f(st.m - m_use);
+  float q[4], lsum = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int r = rl + 4 * i;
-    if (r == slot) {
-      rows[i] = *reinterpret_cast<const uint4*>(new_h + 8 * cl);
-      *reinterpret_cast<uint4*>(ring_h + r * D + 8 * cl) = rows[i];
-    } else {
-      rows[i] = *reinterpret_cast<const uint4*>(ring_h + r * D + 8 * cl);
-    }
+  for (int i = 0; i < 4; ++i) {
+    const float p = __builtin_amdgcn_exp2f(s[i] - m_use);
+    lsum += p;
+    q[i] = p * P_SCALE;
   }
+  const half2_t h01 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(q[0], q[1]));
+  const half2_t h23 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(q[2], q[3]));
+  const half2_t l01 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(q[0] - (float)h01.x, q[1] - (float)h01.y));
+  const half2_t l23 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(q[2] - (float)h23.x, q[3] - (float)h23.y));
+  phi = half4_t{h01.x, h01.y, h23.x, h23.y};
+  plo = half4_t{l01.x, l01.y, l23.x, l23.y};
+  st.l = st.l * alpha + sum4rows(lsum);
+  st.m = m_new;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float ai = gq <= 4 ? __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(alpha), i)) : shfl(alpha, 4 * g + i);
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb) st.acc[cb][i] *= ai;
+  }
+}
+
+// Ring tokens 16 * blk .. 16 * blk + 15 of one head, resident in LDS (K at `rk`, V at `rv`,
+// layout of ring_chunk_pos), slot validity from `valid_bits`. QK^T on 16x16x32 MFMA with
+// the same Q operand as the prefix; PV on 16x16x16 (16 tokens), whose P operand is the
+// S^T output layout of the block.
+__device__ __forceinline__ void attend_ring16(const AttnArgs& a, WaveState& st, const half8_t (&qb)[4],
+                                              const uint8_t* rk, const uint8_t* rv, int blk, uint64_t valid_bits) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  float4_t S = {0.f, 0.f, 0.f, 0.f};
+  const int row = 16 * blk + c;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int chunk = 2 * g + 8 * (k >> 1) + (k & 1);
+    const uint4 kw = *reinterpret_cast<const uint4*>(rk + row * (2 * D) + (ring_chunk_pos(row, chunk) << 4));
+    S = mfma32(as_h8(kw), qb[k], S);
+  }
+  float sc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int slot = 16 * blk + 4 * g + i;
+    sc[i] = ((valid_bits >> slot) & 1ull) ? S[i] * a.sl2 : NEG_INF;
+  }
+  half4_t phi, plo;
+  softmax_step4(st, sc, phi, plo, a.gq);
+  // V as the B operand: lane (c, g) holds tokens 16 blk + 4g + [0..3] of dim 16 cb + c
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb) {
+    _Float16 v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int slot = 16 * blk + 4 * g + r;
+      const int chunk = 2 * cb + (c >> 3);
+      const uint16_t bits = *reinterpret_cast<const uint16_t*>(rv + slot * (2 * D) + (ring_chunk_pos(slot, chunk) << 4) + 2 * (c & 7));
+      v[r] = ((valid_bits >> slot) & 1ull) ? __builtin_bit_cast(_Float16, bits) : (_Float16)0.0f;
+    }
+    const half4_t vb = half4_t{v[0], v[1], v[2], v[3]};
+    st.acc[cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, vb, st.acc[cb], 0, 0, 0);
+    st.acc[cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, vb, st.acc[cb], 0, 0, 0);
+  }
+}
+
+// ---------------------------------------------------------------- ring append
+
+__device__ __forceinline__ float min4rows(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fminf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fminf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// One quarter (16 rows) of one ring tensor as one wave holds it: lanes (l & 15) own 8
+// channels, lanes (l >> 4) own rows 16 qtr + (l >> 4) + 4i, i < 4; plus the new token's 8
+// channels. Rows at or beyond `slots` repeat the last one (never attended).
+struct RingQuarter {
+  uint4 rows[4];
+  uint4 fresh;
+};
+
+__device__ __forceinline__ void ring_load_quarter(const uint16_t* ring_h, const uint16_t* fresh_h, int slots, int qtr,
+                                                  RingQuarter& rq) {
+  const int lane = threadIdx.x & 63, cl = lane & 15, rl = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    rq.rows[i] = *reinterpret_cast<const uint4*>(ring_h + min(16 * qtr + rl + 4 * i, slots - 1) * D + 8 * cl);
+  rq.fresh = fresh_h ? *reinterpret_cast<const uint4*>(fresh_h + 8 * cl) : uint4{0, 0, 0, 0};
+}
+
+// The quarter's rows as the ring attention reads them: into the LDS ring buffer.
+__device__ __forceinline__ void ring_quarter_to_lds(const uint4 (&rows)[4], int qtr, uint8_t* ring_lds) {
+  const int lane = threadIdx.x & 63, cl = lane & 15, rl = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 16 * qtr + rl + 4 * i;
+    *reinterpret_cast<uint4*>(ring_lds + r * (2 * D) + (ring_chunk_pos(r, cl) << 4)) = rows[i];
+  }
+}
+
+// Append of one decode token, one tensor (K or V) of head h, by the 4 waves that hold its
+// quarters: the token goes into ring slot `slot`, the whole ring is requantized into ruler
+// group `gcur` (same arithmetic as the bulk quantizer; per-channel min/max combined over the
+// quarters through `xch`, [4 quarters][min, max][D] floats) and, for the ring attention,
+// the LDS ring buffer gets the fp16 ring — or, when the token completes the group, the
+// group's dequantized values fp16(code * step16 + min16), exactly as the prefix kernel
+// dequantizes. Contains one workgroup barrier: every wave of the workgroup must call it.
+__device__ __forceinline__ void ring_append_quarter(RingQuarter& rq, uint16_t* ring_h, uint8_t* codes_h,
+                                                    uint16_t* mn_g, uint16_t* st_g, int slot, int64_t gcur,
+                                                    int64_t capacity, bool completes, int qtr, float* xch,
+                                                    uint8_t* ring_lds) {
+  const int lane = threadIdx.x & 63, cl = lane & 15, rl = lane >> 4;
   float mn[8], mx[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) { mn[j] = __builtin_huge_valf(); mx[j] = -__builtin_huge_valf(); }
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const uint32_t w[4] = {rows[i].x, rows[i].y, rows[i].z, rows[i].w};
+  for (int i = 0; i < 4; ++i) {
+    const int r = 16 * qtr + rl + 4 * i;
+    if (r == slot) {
+      rq.rows[i] = rq.fresh;
+      *reinterpret_cast<uint4*>(ring_h + slot * D + 8 * cl) = rq.fresh;
+    }
+    const uint32_t w[4] = {rq.rows[i].x, rq.rows[i].y, rq.rows[i].z, rq.rows[i].w};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float v = h2f((uint16_t)(w[j >> 1] >> (16 * (j & 1))));
@@ -361,55 +524,72 @@ __device__ __forceinline__ void append_ring_tensor(uint16_t* ring_h, const uint1
     }
   }
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    mn[j] = fminf(mn[j], shfl_xor(mn[j], 16));
-    mn[j] = fminf(mn[j], shfl_xor(mn[j], 32));
-    mx[j] = fmaxf(mx[j], shfl_xor(mx[j], 16));
-    mx[j] = fmaxf(mx[j], shfl_xor(mx[j], 32));
-  }
-  float stp[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) stp[j] = ruler_step(mn[j], mx[j]);
+  for (int j = 0; j < 8; ++j) { mn[j] = min4rows(mn[j]); mx[j] = max4rows(mx[j]); }
   if (rl == 0) {
-    uint4 m4, s4;
-    m4.x = (uint32_t)f2h(mn[0]) | ((uint32_t)f2h(mn[1]) << 16);
-    m4.y = (uint32_t)f2h(mn[2]) | ((uint32_t)f2h(mn[3]) << 16);
-    m4.z = (uint32_t)f2h(mn[4]) | ((uint32_t)f2h(mn[5]) << 16);
-    m4.w = (uint32_t)f2h(mn[6]) | ((uint32_t)f2h(mn[7]) << 16);
-    s4.x = (uint32_t)f2h(stp[0]) | ((uint32_t)f2h(stp[1]) << 16);
-    s4.y = (uint32_t)f2h(stp[2]) | ((uint32_t)f2h(stp[3]) << 16);
-    s4.z = (uint32_t)f2h(stp[4]) | ((uint32_t)f2h(stp[5]) << 16);
-    s4.w = (uint32_t)f2h(stp[6]) | ((uint32_t)f2h(stp[7]) << 16);
-    *reinterpret_cast<uint4*>(mn_g + 8 * cl) = m4;
-    *reinterpret_cast<uint4*>(st_g + 8 * cl) = s4;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { xch[(2 * qtr) * D + 8 * cl + j] = mn[j]; xch[(2 * qtr + 1) * D + 8 * cl + j] = mx[j]; }
+  }
+  __syncthreads();
+  float stp[8], inv[8];
+  uint32_t s16[4], m16[4];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float a0 = xch[8 * cl + j], b0 = xch[D + 8 * cl + j];
+#pragma unroll
+    for (int k = 1; k < 4; ++k) { a0 = fminf(a0, xch[2 * k * D + 8 * cl + j]); b0 = fmaxf(b0, xch[(2 * k + 1) * D + 8 * cl + j]); }
+    mn[j] = a0;
+    stp[j] = ruler_step(a0, b0);
+    inv[j] = ruler_inv(stp[j]);
   }
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int r = rl + 4 * i;
+  for (int j = 0; j < 4; ++j) {
+    s16[j] = (uint32_t)f2h(stp[2 * j]) | ((uint32_t)f2h(stp[2 * j + 1]) << 16);
+    m16[j] = (uint32_t)f2h(mn[2 * j]) | ((uint32_t)f2h(mn[2 * j + 1]) << 16);
+  }
+  if (qtr == 0 && rl == 0) {
+    *reinterpret_cast<uint4*>(mn_g + 8 * cl) = uint4{m16[0], m16[1], m16[2], m16[3]};
+    *reinterpret_cast<uint4*>(st_g + 8 * cl) = uint4{s16[0], s16[1], s16[2], s16[3]};
+  }
+  uint4 vals[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 16 * qtr + rl + 4 * i;
+    const uint32_t w[4] = {rq.rows[i].x, rq.rows[i].y, rq.rows[i].z, rq.rows[i].w};
+    uint32_t cc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cc[j] = ruler_code_rcp(h2f((uint16_t)(w[j >> 1] >> (16 * (j & 1)))), mn[j], stp[j], inv[j]);
+    const uint32_t o0 = cc[0] | (cc[1] << 8) | (cc[2] << 16) | (cc[3] << 24);
+    const uint32_t o1 = cc[4] | (cc[5] << 8) | (cc[6] << 16) | (cc[7] << 24);
     const int64_t t = gcur * GT + r;
-    if (t < capacity) {
-      const uint32_t w[4] = {rows[i].x, rows[i].y, rows[i].z, rows[i].w};
-      uint32_t cc[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) cc[j] = ruler_code(h2f((uint16_t)(w[j >> 1] >> (16 * (j & 1)))), mn[j], stp[j]);
-      uint2 o;
-      o.x = cc[0] | (cc[1] << 8) | (cc[2] << 16) | (cc[3] << 24);
-      o.y = cc[4] | (cc[5] << 8) | (cc[6] << 16) | (cc[7] << 24);
-      *reinterpret_cast<uint2*>(codes_h + t * D + 8 * cl) = o;
-    }
+    if (t < capacity) *reinterpret_cast<uint2*>(codes_h + t * D + 8 * cl) = uint2{o0, o1};
+    vals[i] = completes ? __builtin_bit_cast(uint4, dq8(o0, o1, uint4{s16[0], s16[1], s16[2], s16[3]},
+                                                        uint4{m16[0], m16[1], m16[2], m16[3]}))
+                        : rq.rows[i];
   }
+  ring_quarter_to_lds(vals, qtr, ring_lds);
 }
 
-__device__ __forceinline__ void append_head(const AttnArgs& a, int h, int which, int64_t pos) {
+__device__ __forceinline__ const uint16_t* ring_of(const AttnArgs& a, int h, int which) {
+  return (which == 0 ? a.tail_k : a.tail_v) + (int64_t)h * a.tail_slots * D;
+}
+__device__ __forceinline__ const uint16_t* fresh_of(const AttnArgs& a, int h, int which) {
+  return (which == 0 ? a.k_new : a.v_new) + h * a.kv_hs;
+}
+
+// The append of head h by the 8 waves of a workgroup: waves 0-3 take the quarters of K,
+// waves 4-7 those of V.
+__device__ __forceinline__ void append_head8(const AttnArgs& a, int h, int wave, int64_t pos, RingQuarter& rq,
+                                             bool completes, float* xch, uint8_t* ring_k, uint8_t* ring_v) {
+  const int which = wave >> 2, qtr = wave & 3;
   const int slot = (int)(pos % GT);
   const int64_t gcur = pos / GT;
   const int64_t ro = ((int64_t)h * a.ngroups_cap + gcur) * D;
-  if (which == 0)
-    append_ring_tensor(a.tail_k + (int64_t)h * GT * D, a.k_new + h * a.kv_hs, a.kq + (int64_t)h * a.capacity * D,
-                       a.kmn + ro, a.kst + ro, slot, gcur, a.capacity);
-  else
-    append_ring_tensor(a.tail_v + (int64_t)h * GT * D, a.v_new + h * a.kv_hs, a.vq + (int64_t)h * a.capacity * D,
-                       a.vmn + ro, a.vst + ro, slot, gcur, a.capacity);
+  uint16_t* ring = (which == 0 ? a.tail_k : a.tail_v) + (int64_t)h * GT * D;
+  uint8_t* codes = (which == 0 ? a.kq : a.vq) + (int64_t)h * a.capacity * D;
+  uint16_t* mn = (which == 0 ? a.kmn : a.vmn) + ro;
+  uint16_t* st = (which == 0 ? a.kst : a.vst) + ro;
+  ring_append_quarter(rq, ring, codes, mn, st, slot, gcur, a.capacity, completes, qtr, xch + which * 8 * D,
+                      which == 0 ? ring_k : ring_v);
 }
 
 __device__ __forceinline__ void write_scalars(const AttnArgs& a, int64_t pos) {
@@ -433,154 +613,249 @@ __device__ __forceinline__ uint64_t ring_bits(int64_t written, int64_t qlen, int
   return bits;
 }
 
-// ---------------------------------------------------------------- the kernel
+// ---------------------------------------------------------------- partials
 
-__global__ __launch_bounds__(THREADS, 2) void attn_decode_kernel(AttnArgs a) {
-  extern __shared__ float lds[];
-  __shared__ int s_last;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int h = blockIdx.x % a.hkv;
-  const int part = blockIdx.x / a.hkv;
-  const bool is_tail = part == a.n_parts;
+// Floats of one partial: [acc: gq * D][m: gq][l: gq], rounded up to 4 floats so that every
+// partial starts 16-byte aligned. acc is scaled by 2^15, m is in the log2 domain.
+__host__ __device__ __forceinline__ int part_stride(int gq) { return gq * D + ((2 * gq + 3) & ~3); }
 
-  WaveState st;
-  state_init(st);
-  half4_t qb[8];
-  load_q(a, h, qb);
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+  return v;
+}
 
-  // token limit of the int8 prefix and where the ring stands
+// Write one wave's online-softmax state as a partial at `dst` (LDS or memory): lane (c, g)
+// holds m, l of head c (replicated over g) and acc of heads 4g + i, dims 16cb + c.
+__device__ __forceinline__ void store_wave_partial(const WaveState& st, int gq, float* dst) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  if (g == 0 && c < gq) { dst[gq * D + c] = st.m; dst[gq * D + gq + c] = st.l; }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int head = 4 * g + i;
+    if (head < gq)
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb) dst[head * D + 16 * cb + c] = st.acc[cb][i];
+  }
+}
+
+// Token limit of the int8 prefix for this launch: whole groups before the ring's group in
+// the fused step (from the write position), else min(used, 64 * prefix_groups).
+__device__ __forceinline__ int64_t prefix_limit(const AttnArgs& a, int64_t& pos, bool& pos_ok) {
   int64_t U;
-  int64_t pos = 0;
-  bool pos_ok = true;
+  pos = 0;
+  pos_ok = true;
   if (a.tail_mode == TAIL_FUSED) {
     pos = *a.pos_dev;
     pos_ok = pos >= 0 && pos < a.capacity;  // a position outside the cache appends nothing
-    U = pos_ok ? pos / GT * GT : 0;         // whole groups before the ring's group
+    U = pos_ok ? pos / GT * GT : 0;
   } else {
     const int64_t used = a.used_dev ? *a.used_dev : a.used;
     const int64_t pgv = a.pg_dev ? *a.pg_dev : a.pg;
     U = min(used, pgv * GT);
   }
-  U = max<int64_t>(0, min(U, a.ngroups_cap * GT));
-
-  if (!is_tail) {
-    const int64_t W = (U + GT - 1) / GT;
-    const int64_t gs = (int64_t)part * W / a.n_parts;
-    const int64_t ge = (int64_t)(part + 1) * W / a.n_parts;
-    for (int64_t grp = gs + wave; grp < ge; grp += WAVES) {
-      const int nvalid = (int)min<int64_t>(GT, U - grp * GT);
-      attend_group_int8(a, st, qb, h, grp, nvalid);
-    }
-  } else {
-    if (a.tail_mode == TAIL_FUSED && pos_ok) {
-      if (wave < 2) append_head(a, h, wave, pos);
-      if (h == 0 && tid == 0) write_scalars(a, pos);
-      __threadfence_block();
-      __syncthreads();
-      if (wave == 0) {
-        const int64_t written = pos + 1;
-        const int64_t qlen = written / GT * GT;
-        if (qlen > U) {
-          attend_group_int8(a, st, qb, h, pos / GT, GT);  // the ring just completed its group
-        } else {
-          const int64_t first = a.first_dev ? *a.first_dev : 0;
-          attend_ring_f16(a, st, qb, h, ring_bits(written, qlen, first));
-        }
-      }
-    } else if (a.tail_mode != TAIL_FUSED && wave == 0) {
-      uint64_t bits;
-      if (a.tail_mode == TAIL_MASK) {
-        bits = 0;
-        for (int i = 0; i < a.tail_slots; ++i) bits |= (uint64_t)(a.tail_mask[i] != 0) << i;
-      } else {
-        const int64_t written = *a.written_dev;
-        const int64_t first = a.first_dev ? *a.first_dev : 0;
-        bits = ring_bits(written, U, first);
-      }
-      attend_ring_f16(a, st, qb, h, bits);
-    }
-  }
-
-  // ---- merge the waves through LDS: per wave [m: gq][l: gq][acc: gq * D]
-  const int gq = a.gq;
-  const int pw = gq * (D + 2);
-  float* lw = lds + wave * pw;
-  {
-    const int c = lane & 15, g = lane >> 4;
-    if (g == 0 && c < gq) { lw[c] = st.m; lw[gq + c] = st.l; }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int head = 4 * g + i;
-      if (head < gq)
-#pragma unroll
-        for (int cb = 0; cb < 8; ++cb) lw[2 * gq + head * D + 8 * c + cb] = st.acc[cb][i];
-    }
-  }
-  __syncthreads();
-  const int nslots = a.nslots;
-  float* part_ws = a.ws + ((int64_t)h * nslots + part) * pw;
-  for (int e = tid; e < gq * D; e += THREADS) {
-    const int head = e / D;
-    float m = NEG_INF;
-    for (int w = 0; w < WAVES; ++w) m = fmaxf(m, lds[w * pw + head]);
-    const float mu = m == NEG_INF ? 0.0f : m;
-    float acc = 0.0f, l = 0.0f;
-    for (int w = 0; w < WAVES; ++w) {
-      const float wt = __builtin_amdgcn_exp2f(lds[w * pw + head] - mu);
-      acc += lds[w * pw + 2 * gq + e] * wt;
-      l += lds[w * pw + gq + head] * wt;
-    }
-    part_ws[2 * gq + e] = acc;
-    if ((e % D) == 0) { part_ws[head] = m; part_ws[gq + head] = l; }
-  }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(a.counters + h, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == (uint32_t)(nslots - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  // ---- last workgroup of head h: merge all partials of the head
-  float* wts = lds;               // [nslots][gq] weights
-  float* mh = lds + nslots * gq;  // [gq] merged max
-  const float* head_ws = a.ws + (int64_t)h * nslots * pw;
-  if (tid < gq) {
-    float m = NEG_INF;
-    for (int s = 0; s < nslots; ++s) m = fmaxf(m, __builtin_nontemporal_load(head_ws + (int64_t)s * pw + tid));
-    mh[tid] = m;
-  }
-  __syncthreads();
-  for (int e = tid; e < nslots * gq; e += THREADS) {
-    const int s = e / gq, head = e % gq;
-    const float m = mh[head];
-    const float ms = __builtin_nontemporal_load(head_ws + (int64_t)s * pw + head);
-    wts[e] = ms == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(ms - m);
-  }
-  __syncthreads();
-  for (int e = tid; e < gq * D; e += THREADS) {
-    const int head = e / D;
-    float acc = 0.0f, l = 0.0f;
-    for (int s = 0; s < nslots; ++s) {
-      const float wt = wts[s * gq + head];
-      acc += __builtin_nontemporal_load(head_ws + (int64_t)s * pw + 2 * gq + e) * wt;
-      l += __builtin_nontemporal_load(head_ws + (int64_t)s * pw + gq + head) * wt;
-    }
-    const int qh = h * gq + head;
-    a.out[(int64_t)qh * D + (e % D)] = f2h(l > 0.0f ? acc / l * INV_P_SCALE : 0.0f);
-    if (a.lse && (e % D) == 0) a.lse[qh] = l > 0.0f ? (mh[head] + __log2f(l)) * LN2 : NEG_INF;
-  }
-  if (tid == 0) __hip_atomic_store(a.counters + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return max<int64_t>(0, min(U, a.ngroups_cap * GT));
 }
 
-// Standalone append (two waves per KV head: K and V).
-__global__ __launch_bounds__(128) void append_kernel(AttnArgs a) {
+// ---------------------------------------------------------------- kernel A: the prefix
+
+// Workgroup (h, part) streams the 64-token groups [gs, ge) of KV head h's int8 prefix and
+// writes one partial to ws[h][part]. Plain stores: the tail kernel that reads them runs
+// after this launch completes.
+__global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds_raw[LDS_BYTES];
+  float* lds = reinterpret_cast<float*>(lds_raw);
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = blockIdx.x % a.hkv;
+  const int part = blockIdx.x / a.hkv;
+  uint8_t* my_stages = lds_raw + wave * STAGES * STAGE_BYTES;
+  const uint32_t my_lds = __builtin_amdgcn_readfirstlane(lds_addr(my_stages));
+
+  WaveState st;
+  state_init(st);
+  half8_t qb[4];
+  load_q(a, h, qb);
+  int64_t pos;
+  bool pos_ok;
+  const int64_t U = prefix_limit(a, pos, pos_ok);
+
+  const int64_t W = (U + GT - 1) / GT;
+  const int64_t gs = (int64_t)part * W / a.n_parts;
+  const int64_t ge = (int64_t)(part + 1) * W / a.n_parts;
+  const int n = ge - gs > wave ? (int)((ge - gs - wave + WAVES - 1) / WAVES) : 0;
+#pragma unroll
+  for (int s0 = 0; s0 < STAGES; ++s0)
+    if (s0 < n) issue_group(a, h, gs + wave + (int64_t)s0 * WAVES, my_lds + s0 * STAGE_BYTES);
+  for (int i = 0; i < n; ++i) {
+    if (STAGES > 1 && i + 1 < n) wait_groups_all_but_one();
+    else wait_groups_all();
+    const int64_t grp = gs + wave + (int64_t)i * WAVES;
+    const int nvalid = (int)min<int64_t>(GT, U - grp * GT);
+    const int sidx = STAGES > 1 ? (i & 1) : 0;
+    attend_stage(a, st, qb, my_stages + sidx * STAGE_BYTES, nvalid);
+    if (i + STAGES < n) issue_group(a, h, grp + STAGES * WAVES, my_lds + sidx * STAGE_BYTES);
+  }
+
+  // ---- merge the waves through LDS (the stages are dead once every wave is here)
+  __syncthreads();
+  const int gq = a.gq, pw = part_stride(gq);
+  store_wave_partial(st, gq, lds + wave * pw);
+  __syncthreads();
+  float* dst = a.ws + ((int64_t)h * a.n_parts + part) * pw;
+  for (int e = tid; e < gq * D + 2 * gq; e += THREADS) {
+    const int head = e < gq * D ? e / D : (e - gq * D) % gq;
+    float m = NEG_INF;
+    for (int w = 0; w < WAVES; ++w) m = fmaxf(m, lds[w * pw + gq * D + head]);
+    const float mu = m == NEG_INF ? 0.0f : m;
+    float sum = 0.0f;
+    const int src = e < gq * D ? e : gq * D + gq + head;  // acc element, or l for both m and l slots
+    for (int w = 0; w < WAVES; ++w) sum += lds[w * pw + src] * __builtin_amdgcn_exp2f(lds[w * pw + gq * D + head] - mu);
+    dst[e] = e < gq * D ? sum : (e < gq * D + gq ? m : sum);
+  }
+}
+
+// ---------------------------------------------------------------- kernel B: ring + merge
+
+constexpr int TB_WAVES = 8;
+constexpr int TB_THREADS = 64 * TB_WAVES;
+constexpr int MERGE_CHUNK = 32;  // partial slots per column loaded up front
+constexpr int RING_PARTS = 4;    // the ring's 64 tokens as 4 partials of 16
+
+// One workgroup per KV head, after kernel A: appends the new token (fused step), attends
+// over the ring (or the group the token completed), then merges the prefix partials of
+// kernel A and the ring's partials by log-sum-exp and writes out / lse. Every phase is
+// spread over the 8 waves (a wave's dependent instruction chain is what bounds this
+// kernel), and every load it needs is issued at its start.
+__global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring_lds[2 * RING_BYTES];          // K | V values
+  __shared__ __attribute__((aligned(16))) float ring_part[RING_PARTS][16 * D + 32];  // the ring's partials
+  __shared__ __attribute__((aligned(16))) float xch[2 * 8 * D];                      // append min / max
+  __shared__ float wts[(256 + RING_PARTS) * 16], lsv[(256 + RING_PARTS) * 16];
+  __shared__ float mh[16], lh[16];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = blockIdx.x;
+  const int gq = a.gq, pw = part_stride(gq), P = a.n_parts, cols = gq * D;
+  const bool fused = a.tail_mode == TAIL_FUSED;
+
+  int64_t pos;
+  bool pos_ok;
+  const int64_t U = prefix_limit(a, pos, pos_ok);
+  const bool ring = a.tail_mode != TAIL_NONE && (!fused || pos_ok);
+
+  // ---- every load up front: ring quarters, `first`, q, m / l and a column of the partials
+  RingQuarter rq;
+  if (ring) ring_load_quarter(ring_of(a, h, wave >> 2), fused ? fresh_of(a, h, wave >> 2) : nullptr,
+                              (int)a.tail_slots, wave & 3, rq);
+  const int64_t first = (ring && a.first_dev) ? *a.first_dev : 0;
+  half8_t qb[4];
+  if (ring && wave < RING_PARTS) load_q(a, h, qb);
+  const float* hws = a.ws + (int64_t)h * P * pw;
+  float ml[2] = {NEG_INF, 0.0f};  // m / l of partial (tid / gq, head tid % gq); more in the merge
+  if (tid < P * gq) {
+    const int s = tid / gq, head = tid - s * gq;
+    ml[0] = hws[(int64_t)s * pw + gq * D + head];
+    ml[1] = hws[(int64_t)s * pw + gq * D + gq + head];
+  }
+  float v[MERGE_CHUNK];
+#pragma unroll
+  for (int u = 0; u < MERGE_CHUNK; ++u) v[u] = (u < P && tid < cols) ? hws[(int64_t)u * pw + tid] : 0.0f;
+
+  // ---- the ring: append (fused) into the LDS ring, then 4 waves x 16 tokens
+  uint8_t* ring_k = ring_lds;
+  uint8_t* ring_v = ring_lds + RING_BYTES;
+  if (ring) {
+    const int64_t written = fused ? pos + 1 : (a.tail_mode == TAIL_SCALARS ? *a.written_dev : 0);
+    const int64_t qlen = fused ? written / GT * GT : U;
+    const bool completes = fused && qlen > U;  // this token completes the ring's group
+    if (fused) append_head8(a, h, wave, pos, rq, completes, xch, ring_k, ring_v);
+    else ring_quarter_to_lds(rq.rows, wave & 3, (wave >> 2) == 0 ? ring_k : ring_v);
+    if (fused && h == 0 && tid == 0) write_scalars(a, pos);
+    __syncthreads();
+    if (wave < RING_PARTS) {
+      uint64_t bits = 0;
+      if (completes) {
+        bits = ~0ull;  // the completed group, through its int8 values
+      } else if (a.tail_mode == TAIL_MASK) {
+        for (int i = 0; i < a.tail_slots; ++i) bits |= (uint64_t)(a.tail_mask[i] != 0) << i;
+      } else {
+        bits = ring_bits(written, qlen, first);
+      }
+      WaveState st;
+      state_init(st);
+      attend_ring16(a, st, qb, ring_k, ring_v, wave, bits);
+      store_wave_partial(st, gq, ring_part[wave]);
+    }
+  }
+
+  // ---- merge: P prefix partials + RING_PARTS ring partials
+  if (tid < P * gq) { wts[tid] = ml[0]; lsv[tid] = ml[1]; }
+  for (int i = tid + TB_THREADS; i < P * gq; i += TB_THREADS) {
+    const int s = i / gq, head = i - s * gq;
+    wts[i] = hws[(int64_t)s * pw + gq * D + head];
+    lsv[i] = hws[(int64_t)s * pw + gq * D + gq + head];
+  }
+  __syncthreads();
+  if (tid < RING_PARTS * gq) {
+    const int r = tid / gq, head = tid - r * gq;
+    wts[(P + r) * gq + head] = ring ? ring_part[r][gq * D + head] : NEG_INF;
+    lsv[(P + r) * gq + head] = ring ? ring_part[r][gq * D + gq + head] : 0.0f;
+  }
+  __syncthreads();
+  const int ns = P + RING_PARTS;
+  for (int head = wave; head < gq; head += TB_WAVES) {
+    float m = NEG_INF;
+    for (int s = lane; s < ns; s += 64) m = fmaxf(m, wts[s * gq + head]);
+    m = wave_max(m);
+    float l = 0.0f;
+    for (int s = lane; s < ns; s += 64) {
+      const float ms = wts[s * gq + head];
+      const float w = ms == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(ms - m);
+      wts[s * gq + head] = w;
+      l += lsv[s * gq + head] * w;
+    }
+    l = wave_sum(l);
+    if (lane == 0) { mh[head] = m; lh[head] = l; }
+  }
+  __syncthreads();
+#pragma unroll 1
+  for (int col = tid; col < cols; col += TB_THREADS) {
+    const int head = col / D;
+    float acc = 0.0f;
+    if (ring) {
+#pragma unroll
+      for (int r = 0; r < RING_PARTS; ++r) acc += ring_part[r][col] * wts[(P + r) * gq + head];
+    }
+    if (col == tid) {
+#pragma unroll
+      for (int u = 0; u < MERGE_CHUNK; ++u) if (u < P) acc += v[u] * wts[u * gq + head];
+    } else {
+      for (int s = 0; s < min(P, MERGE_CHUNK); ++s) acc += hws[(int64_t)s * pw + col] * wts[s * gq + head];
+    }
+#pragma unroll 4
+    for (int s = MERGE_CHUNK; s < P; ++s) acc += hws[(int64_t)s * pw + col] * wts[s * gq + head];
+    const float l = lh[head];
+    const int qh = h * gq + head, d = col % D;
+    a.out[(int64_t)qh * D + d] = f2h(l > 0.0f ? acc * (INV_P_SCALE / l) : 0.0f);
+    if (a.lse && d == 0) a.lse[qh] = l > 0.0f ? (mh[head] + __log2f(l)) * LN2 : NEG_INF;
+  }
+}
+
+// Standalone append: one workgroup of 8 waves per KV head (4 per tensor).
+__global__ __launch_bounds__(512) void append_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring[2 * RING_BYTES];
+  __shared__ __attribute__((aligned(16))) float xch[2 * 8 * D];
+  const int h = blockIdx.x, wave = threadIdx.x >> 6;
   const int64_t pos = *a.pos_dev;
   if (pos < 0 || pos >= a.capacity) return;  // a position outside the cache appends nothing
-  append_head(a, h, threadIdx.x >> 6, pos);
+  RingQuarter rq;
+  ring_load_quarter(ring_of(a, h, wave >> 2), fresh_of(a, h, wave >> 2), GT, wave & 3, rq);
+  append_head8(a, h, wave, pos, rq, false, xch, ring, ring + RING_BYTES);
   if (h == 0 && threadIdx.x == 0) write_scalars(a, pos);
 }
 
@@ -597,21 +872,14 @@ __global__ void ring_mask_kernel(const int64_t* written, const int64_t* qlen, co
 
 // ---------------------------------------------------------------- host side
 
+// Prefix work units per KV head: at least 8 groups (one per wave) per workgroup, and at
+// most one workgroup per CU (256 CUs).
 static int64_t default_parts(int64_t hkv, int64_t groups) {
-  // about 2 workgroups per CU over the 256 CUs of an MI355X, at least 2 groups per part
-  const int64_t target_wgs = 512;
-  int64_t parts = std::max<int64_t>(1, target_wgs / std::max<int64_t>(1, hkv));
-  parts = std::min<int64_t>(parts, std::max<int64_t>(1, groups / 2));
-  return parts;
+  const int64_t max_parts = std::max<int64_t>(1, 256 / std::max<int64_t>(1, hkv));
+  return std::min<int64_t>(max_parts, std::max<int64_t>(1, cdiv(groups, 8)));
 }
 
-static int64_t part_floats(int64_t hq, int64_t hkv) { return (hq / hkv) * (D + 2); }
-
-static size_t lds_bytes(int gq, int nslots) {
-  const size_t merge = (size_t)WAVES * gq * (D + 2) * sizeof(float);
-  const size_t final_ = ((size_t)nslots * gq + gq) * sizeof(float);
-  return std::max(merge, final_);
-}
+static int64_t part_floats(int64_t hq, int64_t hkv) { return part_stride((int)(hq / hkv)); }
 
 static int check_heads(int64_t hq, int64_t hkv, int64_t head_dim) {
   if (hkv <= 0 || hq <= 0 || hq % hkv) return fail(NKV_ERR_INVALID, "Q heads %lld not divisible by KV heads %lld", (long long)hq, (long long)hkv);
@@ -620,14 +888,19 @@ static int check_heads(int64_t hq, int64_t hkv, int64_t head_dim) {
   return NKV_OK;
 }
 
+// Kernel A over n_parts prefix parts (none when n_parts == 0), then kernel B.
 static int launch_attn(AttnArgs& a, int64_t n_parts, int64_t workspace_bytes, hipStream_t s, const char* what) {
+  if (n_parts < 0) return fail(NKV_ERR_INVALID, "%s: n_parts %lld is negative", what, (long long)n_parts);
   a.n_parts = (int)n_parts;
-  a.nslots = (int)(n_parts + (a.tail_mode != TAIL_NONE ? 1 : 0));
-  const int64_t need = (int64_t)a.hkv * a.nslots * part_floats(a.hq, a.hkv) * (int64_t)sizeof(float);
-  if (workspace_bytes < need) return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
-  const size_t shm = lds_bytes(a.gq, a.nslots);
-  if (shm > 64 * 1024) return fail(NKV_ERR_UNSUPPORTED, "%s: n_parts %lld needs too much LDS", what, (long long)n_parts);
-  hipLaunchKernelGGL(attn_decode_kernel, dim3((unsigned)(a.hkv * a.nslots)), dim3(THREADS), shm, s, a);
+  const int64_t need = (int64_t)a.hkv * std::max<int64_t>(1, n_parts) * part_floats(a.hq, a.hkv) * (int64_t)sizeof(float);
+  if (n_parts > 0 && workspace_bytes < need)
+    return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
+  if (n_parts > 256) return fail(NKV_ERR_UNSUPPORTED, "%s: n_parts %lld exceeds the 256 partials the merge holds", what, (long long)n_parts);
+  if (n_parts > 0) {
+    hipLaunchKernelGGL(attn_prefix_kernel, dim3((unsigned)(a.hkv * n_parts)), dim3(THREADS), 0, s, a);
+    if (int rc = check_launch(what)) return rc;
+  }
+  hipLaunchKernelGGL(attn_tail_kernel, dim3((unsigned)a.hkv), dim3(TB_THREADS), 0, s, a);
   return check_launch(what);
 }
 
@@ -638,8 +911,8 @@ static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) 
 using namespace nkv;
 
 extern "C" int64_t nkv_attn_workspace_bytes(int64_t hkv, int64_t hq, int64_t n_parts) {
-  if (hkv <= 0 || hq <= 0 || n_parts < 0) return 0;
-  return hkv * (n_parts + 1) * part_floats(hq, hkv) * (int64_t)sizeof(float);
+  if (hkv <= 0 || hq <= 0 || n_parts < 0 || hq % hkv) return 0;
+  return hkv * std::max<int64_t>(1, n_parts) * part_floats(hq, hkv) * (int64_t)sizeof(float);
 }
 
 extern "C" int64_t nkv_attn_default_parts(int64_t hkv, int64_t groups) { return default_parts(hkv, groups); }
@@ -652,17 +925,17 @@ extern "C" int nkv_attn_decode_t64(const uint16_t* q, const uint8_t* kq, const u
                                    const uint16_t* tail_k, const uint16_t* tail_v,
                                    const int64_t* written_dev, const int64_t* first_dev,
                                    uint16_t* out, float* lse_out, void* workspace,
-                                   int64_t workspace_bytes, uint32_t* counters, int64_t n_parts,
-                                   void* stream) {
+                                   int64_t workspace_bytes, int64_t n_parts, void* stream) {
   set_error("");
   if (int rc = check_heads(hq, hkv, head_dim)) return rc;
   if (capacity <= 0) return fail(NKV_ERR_INVALID, "capacity must be positive");
-  if (!q || !kq || !kmn || !kst || !vq || !vmn || !vst || !out || !workspace || !counters)
+  if (!q || !kq || !kmn || !kst || !vq || !vmn || !vst || !out || !workspace)
     return fail(NKV_ERR_INVALID, "attn_decode: null pointer argument");
-  if (!al16(q) || !al16(kq) || !al16(vq) || !al16(kmn) || !al16(kst) || !al16(vmn) || !al16(vst))
+  if (!al16(q) || !al16(kq) || !al16(vq) || !al16(kmn) || !al16(kst) || !al16(vmn) || !al16(vst) || !al16(workspace))
     return fail(NKV_ERR_UNSUPPORTED, "attn_decode: buffers must be 16-byte aligned");
   if ((tail_k == nullptr) != (tail_v == nullptr)) return fail(NKV_ERR_INVALID, "tail_k and tail_v go together");
   if (tail_k && !written_dev) return fail(NKV_ERR_INVALID, "the ring needs written_dev");
+  if (tail_k && (!al16(tail_k) || !al16(tail_v))) return fail(NKV_ERR_UNSUPPORTED, "attn_decode: the ring must be 16-byte aligned");
   if (!used_dev && (used < 0 || used > capacity)) return fail(NKV_ERR_INVALID, "used=%lld outside [0, %lld]", (long long)used, (long long)capacity);
   const int64_t ngroups = cdiv(capacity, GT);
   if ((used_dev == nullptr) != (prefix_groups_dev == nullptr))
@@ -682,7 +955,7 @@ extern "C" int nkv_attn_decode_t64(const uint16_t* q, const uint8_t* kq, const u
   a.hq = (int)hq; a.hkv = (int)hkv; a.gq = (int)(hq / hkv);
   a.tail_mode = tail_k ? TAIL_SCALARS : TAIL_NONE;
   a.sl2 = LOG2E / sqrtf((float)head_dim);
-  a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace); a.counters = counters;
+  a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace);
   return launch_attn(a, n_parts, workspace_bytes, static_cast<hipStream_t>(stream), "attn_decode_t64");
 }
 
@@ -697,15 +970,16 @@ extern "C" int nkv_append_t64(const uint16_t* k_new, const uint16_t* v_new, int6
   if (!k_new || !v_new || !kq || !kmn || !kst || !vq || !vmn || !vst || !tail_k || !tail_v || !pos_dev ||
       !written_dev || !qlen_dev || !pg_dev)
     return fail(NKV_ERR_INVALID, "append: null pointer argument");
-  if (!al16(k_new) || !al16(v_new) || kv_head_stride % 8 || !al16(tail_k) || !al16(tail_v) || !al16(kq) || !al16(vq))
+  if (!al16(k_new) || !al16(v_new) || kv_head_stride % 8 || !al16(tail_k) || !al16(tail_v) || !al16(kq) || !al16(vq) ||
+      !al16(kmn) || !al16(kst) || !al16(vmn) || !al16(vst))
     return fail(NKV_ERR_UNSUPPORTED, "append: buffers must be 16-byte aligned");
   AttnArgs a{};
   a.k_new = k_new; a.v_new = v_new; a.kv_hs = kv_head_stride;
   a.kq = kq; a.kmn = kmn; a.kst = kst; a.vq = vq; a.vmn = vmn; a.vst = vst;
   a.tail_k = tail_k; a.tail_v = tail_v; a.pos_dev = pos_dev;
   a.written_out = written_dev; a.qlen_out = qlen_dev; a.pg_out = pg_dev;
-  a.capacity = capacity; a.ngroups_cap = cdiv(capacity, GT); a.hkv = (int)hkv;
-  hipLaunchKernelGGL(append_kernel, dim3((unsigned)hkv), dim3(128), 0, static_cast<hipStream_t>(stream), a);
+  a.capacity = capacity; a.ngroups_cap = cdiv(capacity, GT); a.hkv = (int)hkv; a.tail_slots = GT;
+  hipLaunchKernelGGL(append_kernel, dim3((unsigned)hkv), dim3(512), 0, static_cast<hipStream_t>(stream), a);
   return check_launch("append_t64");
 }
 
@@ -716,15 +990,15 @@ extern "C" int nkv_decode_step_t64(const uint16_t* q, const uint16_t* k_new, con
                                    int64_t* written_dev, int64_t* qlen_dev, int64_t* pg_dev, int64_t hq,
                                    int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out,
                                    float* lse_out, void* workspace, int64_t workspace_bytes,
-                                   uint32_t* counters, int64_t n_parts, void* stream) {
+                                   int64_t n_parts, void* stream) {
   set_error("");
   if (int rc = check_heads(hq, hkv, head_dim)) return rc;
   if (capacity <= 0) return fail(NKV_ERR_INVALID, "capacity must be positive");
   if (!q || !k_new || !v_new || !kq || !kmn || !kst || !vq || !vmn || !vst || !tail_k || !tail_v ||
-      !pos_dev || !written_dev || !qlen_dev || !pg_dev || !out || !workspace || !counters)
+      !pos_dev || !written_dev || !qlen_dev || !pg_dev || !out || !workspace)
     return fail(NKV_ERR_INVALID, "decode_step: null pointer argument");
   if (!al16(q) || !al16(k_new) || !al16(v_new) || kv_head_stride % 8 || !al16(tail_k) || !al16(tail_v) ||
-      !al16(kq) || !al16(vq) || !al16(kmn) || !al16(kst) || !al16(vmn) || !al16(vst))
+      !al16(kq) || !al16(vq) || !al16(kmn) || !al16(kst) || !al16(vmn) || !al16(vst) || !al16(workspace))
     return fail(NKV_ERR_UNSUPPORTED, "decode_step: buffers must be 16-byte aligned");
   const int64_t ngroups = cdiv(capacity, GT);
   if (n_parts <= 0) n_parts = default_parts(hkv, ngroups);
@@ -737,18 +1011,17 @@ extern "C" int nkv_decode_step_t64(const uint16_t* q, const uint16_t* k_new, con
   a.hq = (int)hq; a.hkv = (int)hkv; a.gq = (int)(hq / hkv);
   a.tail_mode = TAIL_FUSED;
   a.sl2 = LOG2E / sqrtf((float)head_dim);
-  a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace); a.counters = counters;
+  a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace);
   return launch_attn(a, n_parts, workspace_bytes, static_cast<hipStream_t>(stream), "decode_step_t64");
 }
 
 extern "C" int nkv_tail_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                const uint8_t* mask, int64_t hq, int64_t hkv, int64_t head_dim,
-                               int64_t slots, uint16_t* out, float* lse, void* workspace,
-                               int64_t workspace_bytes, uint32_t* counters, void* stream) {
+                               int64_t slots, uint16_t* out, float* lse, void* stream) {
   set_error("");
   if (int rc = check_heads(hq, hkv, head_dim)) return rc;
   if (slots <= 0 || slots > GT) return fail(NKV_ERR_UNSUPPORTED, "tail_attend: %lld slots (1..64 supported)", (long long)slots);
-  if (!q || !k || !v || !mask || !out || !workspace || !counters) return fail(NKV_ERR_INVALID, "tail_attend: null pointer argument");
+  if (!q || !k || !v || !mask || !out || !lse) return fail(NKV_ERR_INVALID, "tail_attend: null pointer argument");
   if (!al16(q) || !al16(k) || !al16(v)) return fail(NKV_ERR_UNSUPPORTED, "tail_attend: buffers must be 16-byte aligned");
   AttnArgs a{};
   a.q = q; a.tail_k = const_cast<uint16_t*>(k); a.tail_v = const_cast<uint16_t*>(v); a.tail_mask = mask;
@@ -756,8 +1029,8 @@ extern "C" int nkv_tail_attend(const uint16_t* q, const uint16_t* k, const uint1
   a.hq = (int)hq; a.hkv = (int)hkv; a.gq = (int)(hq / hkv);
   a.tail_mode = TAIL_MASK;
   a.sl2 = LOG2E / sqrtf((float)head_dim);
-  a.out = out; a.lse = lse; a.ws = static_cast<float*>(workspace); a.counters = counters;
-  return launch_attn(a, 0, workspace_bytes, static_cast<hipStream_t>(stream), "tail_attend");
+  a.out = out; a.lse = lse;
+  return launch_attn(a, 0, 0, static_cast<hipStream_t>(stream), "tail_attend");
 }
 
 extern "C" int nkv_ring_mask(const int64_t* written_dev, const int64_t* qlen_dev, const int64_t* first_dev,

@@ -71,6 +71,20 @@ __device__ __forceinline__ uint32_t ruler_code(float x, float mn, float step) {
   return (uint32_t)r;
 }
 
+// The same code with the quotient taken as (x - mn) * inv, inv = rcp(step) (<= 1 ulp).
+// For quotients in [0, 256] that product is within 2^-14 of the exact quotient, and the
+// correctly rounded quotient within 2^-16 of it, so both round to the same integer unless
+// the product lies within 2^-12 of a half-integer; there the IEEE division decides. The
+// result is identical to ruler_code for every input.
+__device__ __forceinline__ uint32_t ruler_code_rcp(float x, float mn, float step, float inv) {
+  const float d = __fsub_rn(x, mn);
+  float q = __fmul_rn(d, inv);
+  if (__builtin_fabsf((q - __builtin_floorf(q)) - 0.5f) < 0x1p-12f) q = __fdiv_rn(d, step);
+  const float r = fminf(fmaxf(__builtin_rintf(q), 0.0f), 255.0f);
+  return (uint32_t)r;
+}
+__device__ __forceinline__ float ruler_inv(float step) { return __builtin_amdgcn_rcpf(step); }
+
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace nkv

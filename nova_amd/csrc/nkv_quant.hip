@@ -83,10 +83,10 @@ struct Elem8<NKV_F32> {
 };
 
 __device__ __forceinline__ uint2 pack_codes8(const float (&x)[8], const float (&mn)[8],
-                                             const float (&st)[8]) {
+                                             const float (&st)[8], const float (&inv)[8]) {
   uint32_t c[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) c[i] = ruler_code(x[i], mn[i], st[i]);
+  for (int i = 0; i < 8; ++i) c[i] = ruler_code_rcp(x[i], mn[i], st[i], inv[i]);
   uint2 r;
   r.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
   r.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
@@ -167,9 +167,9 @@ __global__ __launch_bounds__(64 * kQuantWaves) void quant_token_kernel(QuantTokA
     mx[j] = fmaxf(mx[j], shfl_xor(mx[j], 32));
   }
   if (!active) return;
-  float st[8];
+  float st[8], inv[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) st[j] = ruler_step(mn[j], mx[j]);
+  for (int j = 0; j < 8; ++j) { st[j] = ruler_step(mn[j], mx[j]); inv[j] = ruler_inv(st[j]); }
   if (rl == 0) {
     const int64_t so = r * a.s_rs + gi * a.dim + ch;
     *reinterpret_cast<uint4*>(a.mins + so) = pack_h8(mn);
@@ -180,14 +180,14 @@ __global__ __launch_bounds__(64 * kQuantWaves) void quant_token_kernel(QuantTokA
 #pragma unroll
     for (int i = 0; i < kCacheRows; ++i) {
       const int64_t t = rl + 4 * i;
-      if (t < nr) *reinterpret_cast<uint2*>(a.codes + cbase + (t0 + t) * a.dim) = pack_codes8(cache[i], mn, st);
+      if (t < nr) *reinterpret_cast<uint2*>(a.codes + cbase + (t0 + t) * a.dim) = pack_codes8(cache[i], mn, st, inv);
     }
   } else {
     const int64_t base = r * a.x_rs + ch;
     for (int64_t t = rl; t < nr; t += 4) {
       float v[8];
       Elem8<DT>::load(a.x, base + (t0 + t) * a.dim, v);
-      *reinterpret_cast<uint2*>(a.codes + cbase + (t0 + t) * a.dim) = pack_codes8(v, mn, st);
+      *reinterpret_cast<uint2*>(a.codes + cbase + (t0 + t) * a.dim) = pack_codes8(v, mn, st, inv);
     }
   }
 }
@@ -228,8 +228,9 @@ __global__ __launch_bounds__(256) void quant_channel_kernel(QuantChanArgs a) {
     mx = fmaxf(mx, v);
   }
   const float st = ruler_step(mn, mx);
+  const float inv = ruler_inv(st);
   const int64_t co = r * a.c_rs + t * a.dim + g * a.gc;
-  for (int64_t j = 0; j < a.gc; ++j) a.codes[co + j] = (uint8_t)ruler_code(load1<DT>(a.x, xo + j), mn, st);
+  for (int64_t j = 0; j < a.gc; ++j) a.codes[co + j] = (uint8_t)ruler_code_rcp(load1<DT>(a.x, xo + j), mn, st, inv);
   const int64_t so = r * a.s_rs + t * a.ngc + g;
   a.mins[so] = f2h(mn);
   a.steps[so] = f2h(st);
@@ -300,6 +301,28 @@ __global__ __launch_bounds__(256) void copy16_kernel(const uint4* __restrict__ s
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (; i < n16; i += stride) dst[i] = src[i];
+}
+
+// Read-only streaming probe: every lane reads 16-byte words with a grid stride and folds
+// them into one XOR checksum per workgroup (written so the loads cannot be elided).
+__global__ __launch_bounds__(256) void read_bw_kernel(const uint4* __restrict__ src, int64_t n16,
+                                                      uint32_t* __restrict__ sink) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  uint32_t x = 0;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+    x ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+  }
+  for (; i < n16; i += stride) {
+    const uint4 a = src[i];
+    x ^= a.x ^ a.y ^ a.z ^ a.w;
+  }
+  for (int m = 32; m >= 1; m >>= 1) x ^= (uint32_t)__shfl_xor((int)x, m, 64);
+  __shared__ uint32_t part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) sink[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -399,4 +422,14 @@ extern "C" int nkv_copy_bytes(const void* src, void* dst, int64_t nbytes, void* 
   hipLaunchKernelGGL(copy16_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint4*>(src), static_cast<uint4*>(dst), n16);
   return check_launch("copy_bytes");
+}
+
+extern "C" int nkv_read_bw(const void* src, int64_t nbytes, uint32_t* sink, int64_t blocks, void* stream) {
+  g_err.clear();
+  if (!src || !sink || nbytes <= 0 || nbytes % 16 || !aligned16(src))
+    return fail(NKV_ERR_INVALID, "read_bw: nbytes must be a positive multiple of 16 and src 16-byte aligned");
+  if (blocks <= 0 || blocks > (1 << 20)) return fail(NKV_ERR_INVALID, "read_bw: blocks must be in [1, 2^20]");
+  hipLaunchKernelGGL(read_bw_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint4*>(src), nbytes / 16, sink);
+  return check_launch("read_bw");
 }

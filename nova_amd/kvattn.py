@@ -51,8 +51,8 @@ def _is_capturing() -> bool:
 def _pick_parts(hkv: int, hq: int, groups: int, ws_bytes: int | None) -> int:
     parts = int(_lib.load().nkv_attn_default_parts(hkv, groups))
     if ws_bytes is not None:
-        per_part = hkv * (hq // hkv) * (D_SUPPORTED + 2) * 4
-        fit = ws_bytes // per_part - 1  # one slot stays free for the ring worker
+        per_part = int(_lib.load().nkv_attn_workspace_bytes(hkv, hq, 1))  # one partial per KV head
+        fit = ws_bytes // per_part
         if fit < 1:
             raise ValueError(f"scratch too small: {ws_bytes} bytes")
         parts = max(1, min(parts, fit))
@@ -188,12 +188,11 @@ def int8_attn_decode(
                                 or _lib._WORKSPACES[str(q.device)].numel() < ws_bytes):
             raise ValueError("under graph capture pass scratch=(pm, pl, pa) (no workspace is allocated there)")
         ws = _lib.workspace(q.device, ws_bytes)
-    ctr = _lib.counters(q.device, h_kv)
     _lib.call(
         "nkv_attn_decode_t64", q.data_ptr(), kq.data_ptr(), kmn.data_ptr(), kst.data_ptr(), vq.data_ptr(),
         vmn.data_ptr(), vst.data_ptr(), hq, h_kv, d, length, used, prefix_groups,
         _lib.ptr(used_t), _lib.ptr(prefix_groups_t), None, None, None, None,
-        out.data_ptr(), _lib.ptr(lse_out), ws.data_ptr(), ws_bytes, ctr.data_ptr(), n_parts,
+        out.data_ptr(), _lib.ptr(lse_out), ws.data_ptr(), ws_bytes, n_parts,
         _lib.stream_ptr(q.device))
     return out
 
@@ -229,12 +228,8 @@ def tail_attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tail_mask: to
     mask = mask.to(torch.uint8) if mask.dtype != torch.uint8 else mask.contiguous()
     out = torch.empty((1, hq, 1, d), dtype=torch.float16, device=q.device)
     lse = torch.empty((1, hq), dtype=torch.float32, device=q.device)
-    ws_bytes = int(_lib.load().nkv_attn_workspace_bytes(h_kv, hq, 0))
-    ws = _lib.workspace(q.device, ws_bytes)
-    ctr = _lib.counters(q.device, h_kv)
     _lib.call("nkv_tail_attend", qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), mask.data_ptr(),
-              hq, h_kv, d, slots, out.data_ptr(), lse.data_ptr(), ws.data_ptr(), ws_bytes, ctr.data_ptr(),
-              _lib.stream_ptr(q.device))
+              hq, h_kv, d, slots, out.data_ptr(), lse.data_ptr(), _lib.stream_ptr(q.device))
     return out, lse
 
 
@@ -338,7 +333,6 @@ class KVInt8Cache:
         self.merged = torch.zeros((batch, self.num_q_heads, 1, self.head_dim), dtype=dtype, device=device)
         self._n_parts = _pick_parts(self.num_kv_heads, self.num_q_heads, n_groups, self.pa.numel() * 4)
         self._ws_bytes = self.pa.numel() * 4
-        self._ctr = torch.zeros(max(64, self.num_kv_heads), dtype=torch.int32, device=device)
 
         self.staging: Any = None
 
@@ -512,7 +506,7 @@ class KVInt8Cache:
             0, 0, self._qlen.data_ptr(), self._pg.data_ptr(), self.tail_k[layer_idx].data_ptr(),
             self.tail_v[layer_idx].data_ptr(), self._written.data_ptr(), self.first.data_ptr(),
             self.merged.data_ptr(), self.lse.data_ptr(), self.pa.data_ptr(), self._ws_bytes,
-            self._ctr.data_ptr(), self._n_parts, _lib.stream_ptr(self.pos.device))
+            self._n_parts, _lib.stream_ptr(self.pos.device))
         return self.merged
 
     def update_attend(self, key: torch.Tensor, value: torch.Tensor, query: torch.Tensor,
@@ -537,7 +531,7 @@ class KVInt8Cache:
             self.tail_k[layer_idx].data_ptr(), self.tail_v[layer_idx].data_ptr(), self.pos.data_ptr(),
             self.first.data_ptr(), self._written.data_ptr(), self._qlen.data_ptr(), self._pg.data_ptr(),
             self.num_q_heads, self.num_kv_heads, self.head_dim, self.max_len, self.merged.data_ptr(),
-            self.lse.data_ptr(), self.pa.data_ptr(), self._ws_bytes, self._ctr.data_ptr(), self._n_parts,
+            self.lse.data_ptr(), self.pa.data_ptr(), self._ws_bytes, self._n_parts,
             _lib.stream_ptr(self.pos.device))
         return self.merged
 

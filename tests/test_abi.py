@@ -52,11 +52,16 @@ def test_abi_version_and_host_helpers(lib):
     from nova_amd import _lib
 
     assert lib.nkv_abi_version() == _lib.ABI_VERSION
-    # 32K tokens = 512 rulers per head: 64 parts per head over 8 heads
-    assert lib.nkv_attn_default_parts(8, 512) == 64
+    # at least 8 rulers per workgroup (one per wave) and at most 256 workgroups (one per
+    # CU): 32K tokens = 512 rulers per head over 8 heads -> 32 parts
+    assert lib.nkv_attn_default_parts(8, 512) == 32
+    assert lib.nkv_attn_default_parts(8, 64) == 8
     assert lib.nkv_attn_default_parts(8, 1) == 1
-    per_part = 8 * 4 * 130 * 4
-    assert lib.nkv_attn_workspace_bytes(8, 32, 64) == 65 * per_part
+    assert lib.nkv_attn_default_parts(2, 4096) == 128
+    # one partial = [acc: 4 heads x 128][m: 4][l: 4] floats, 16-byte aligned
+    per_part = 8 * (4 * 128 + 8) * 4
+    assert lib.nkv_attn_workspace_bytes(8, 32, 64) == 64 * per_part
+    assert lib.nkv_attn_workspace_bytes(8, 32, 0) == per_part
 
 
 def test_only_one_hip_runtime_is_mapped(lib):
@@ -77,7 +82,7 @@ def test_validation_errors_return_before_launch(lib):
     assert rc == _lib.NKV_ERR_INVALID and b"axis" in lib.nkv_last_error()
     # Q heads not divisible by KV heads, head_dim other than 128
     args = [None] * 7 + [30, 8, 128, 64, 64, 1, None, None, None, None, None, None, None, None, None, 1 << 20,
-                         None, 0, None]
+                         0, None]
     assert lib.nkv_attn_decode_t64(*args) == _lib.NKV_ERR_INVALID
     assert b"divisible" in lib.nkv_last_error()
     args[7], args[9] = 32, 64
