@@ -1,19 +1,22 @@
 // Split-K int8 decode attention, ring append and the fused decode step (gfx950, wave64).
 //
-// Work decomposition. One launch covers one layer. Workgroup `bid` serves KV head
-// `bid % hkv` and part `bid / hkv`: with 8 KV heads, consecutive workgroups land on the
-// 8 XCDs round-robin, so every workgroup of a head runs on one XCD and its partials
-// stay in that XCD's L2. Parts 0..n_parts-1 split the whole 64-token groups of the
-// int8 prefix evenly; part n_parts (when present) is the ring worker: it appends the
-// new token and requantizes the ring (fused step), then attends over the ring or over
-// the group the ring just completed.
+// Work decomposition. One layer is two launches on one stream.
+//   Prefix kernel: workgroup `bid` serves KV head `bid % hkv` and part `bid / hkv` and
+//     streams its share of the whole 64-token groups of the int8 prefix into one
+//     partial (m, l, acc per query head). With 8 KV heads, consecutive workgroups land
+//     on the 8 XCDs round-robin, so every workgroup of a head runs on one XCD. In the
+//     fused step, the new token's append (ring slot, requantization of the ring into
+//     the current group: 4 units of 64 channels of K or V per head) runs in parts 0..3
+//     ahead of their streams; the prefix never reads the group it writes.
+//   Tail kernel: one workgroup per KV head attends over the fp16 ring (or over the group
+//     the new token completed) and merges all partials by log-sum-exp into out / lse.
+//     The launch boundary orders the partials and the append before it.
 //
-// Streaming. Each of the 4 waves of a workgroup owns every 4th group of the
-// workgroup's range and a private two-stage ring of LDS buffers. A group is moved
-// HBM -> LDS by 20 asynchronous `global_load_lds_dwordx4` (K codes 8 x 1 KiB, V codes
-// 8 x 1 KiB, the four fp16 rulers 4 x 256 B); while a wave computes one group the next one is
-// in flight. Those loads are issued from inline assembly, and the wave waits for
-// them with an explicit `s_waitcnt vmcnt(n)`: left to the compiler, a wait for all
+// Streaming. Each of the 8 waves of a prefix workgroup owns every 8th group of the
+// workgroup's range and a private LDS stage. A group is moved HBM -> LDS by 20
+// asynchronous `global_load_lds_dwordx4` (K codes 8 x 1 KiB, V codes 8 x 1 KiB, the four
+// fp16 rulers 4 x 256 B). Those loads are issued from inline assembly, and the wave waits
+// for them with an explicit `s_waitcnt vmcnt(n)`: left to the compiler, a wait for all
 // outstanding loads would be placed before every LDS read and serialize the stream.
 // Rows are stored with their 16-byte chunks XOR-swizzled by `swz(row)`, which makes
 // both LDS read patterns below free of bank conflicts.
@@ -234,6 +237,26 @@ __device__ __forceinline__ void issue_group(const AttnArgs& a, int h, int64_t gr
   if (which == 1) dma16(uniform_ptr(a.kmn + ro), roff, st + 2 * CODE_BYTES);
   if (which == 2) dma16(uniform_ptr(a.vst + ro), roff, st + 2 * CODE_BYTES);
   if (which == 3) dma16(uniform_ptr(a.vmn + ro), roff, st + 2 * CODE_BYTES);
+}
+
+// Q of KV head h (gq rows of 256 bytes) into LDS at `dst`, by one wave.
+__device__ __forceinline__ void issue_q(const AttnArgs& a, int h, uint32_t dst) {
+  const int lane = threadIdx.x & 63;
+  const int bytes = a.gq * D * 2;
+  const void* qg = uniform_ptr(a.q + (int64_t)h * a.gq * D);
+  for (int k = 0; k < bytes; k += 1024)
+    if (k + 16 * lane < bytes) dma16(qg, (uint32_t)(k + 16 * lane), dst + k);
+}
+
+// The B operand of load_q, from Q rows in LDS.
+__device__ __forceinline__ void load_q_lds(const uint16_t* q_lds, int gq, half8_t (&qb)[4]) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint4 w = {0, 0, 0, 0};
+    if (c < gq) w = *reinterpret_cast<const uint4*>(q_lds + c * D + 16 * g + 64 * (k >> 1) + 8 * (k & 1));
+    qb[k] = as_h8(w);
+  }
 }
 
 __device__ __forceinline__ void wait_groups_all_but_one() { asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); }
@@ -467,20 +490,17 @@ __device__ __forceinline__ float min4rows(float v) {
 }
 
 // One quarter (16 rows) of one ring tensor as one wave holds it: lanes (l & 15) own 8
-// channels, lanes (l >> 4) own rows 16 qtr + (l >> 4) + 4i, i < 4; plus the new token's 8
-// channels. Rows at or beyond `slots` repeat the last one (never attended).
+// channels, lanes (l >> 4) own rows 16 qtr + (l >> 4) + 4i, i < 4. Rows at or beyond
+// `slots` repeat the last one (never attended).
 struct RingQuarter {
   uint4 rows[4];
-  uint4 fresh;
 };
 
-__device__ __forceinline__ void ring_load_quarter(const uint16_t* ring_h, const uint16_t* fresh_h, int slots, int qtr,
-                                                  RingQuarter& rq) {
+__device__ __forceinline__ void ring_load_quarter(const uint16_t* ring_h, int slots, int qtr, RingQuarter& rq) {
   const int lane = threadIdx.x & 63, cl = lane & 15, rl = lane >> 4;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     rq.rows[i] = *reinterpret_cast<const uint4*>(ring_h + min(16 * qtr + rl + 4 * i, slots - 1) * D + 8 * cl);
-  rq.fresh = fresh_h ? *reinterpret_cast<const uint4*>(fresh_h + 8 * cl) : uint4{0, 0, 0, 0};
 }
 
 // The quarter's rows as the ring attention reads them: into the LDS ring buffer.
@@ -493,103 +513,11 @@ __device__ __forceinline__ void ring_quarter_to_lds(const uint4 (&rows)[4], int 
   }
 }
 
-// Append of one decode token, one tensor (K or V) of head h, by the 4 waves that hold its
-// quarters: the token goes into ring slot `slot`, the whole ring is requantized into ruler
-// group `gcur` (same arithmetic as the bulk quantizer; per-channel min/max combined over the
-// quarters through `xch`, [4 quarters][min, max][D] floats) and, for the ring attention,
-// the LDS ring buffer gets the fp16 ring — or, when the token completes the group, the
-// group's dequantized values fp16(code * step16 + min16), exactly as the prefix kernel
-// dequantizes. Contains one workgroup barrier: every wave of the workgroup must call it.
-__device__ __forceinline__ void ring_append_quarter(RingQuarter& rq, uint16_t* ring_h, uint8_t* codes_h,
-                                                    uint16_t* mn_g, uint16_t* st_g, int slot, int64_t gcur,
-                                                    int64_t capacity, bool completes, int qtr, float* xch,
-                                                    uint8_t* ring_lds) {
-  const int lane = threadIdx.x & 63, cl = lane & 15, rl = lane >> 4;
-  float mn[8], mx[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) { mn[j] = __builtin_huge_valf(); mx[j] = -__builtin_huge_valf(); }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 16 * qtr + rl + 4 * i;
-    if (r == slot) {
-      rq.rows[i] = rq.fresh;
-      *reinterpret_cast<uint4*>(ring_h + slot * D + 8 * cl) = rq.fresh;
-    }
-    const uint32_t w[4] = {rq.rows[i].x, rq.rows[i].y, rq.rows[i].z, rq.rows[i].w};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float v = h2f((uint16_t)(w[j >> 1] >> (16 * (j & 1))));
-      mn[j] = fminf(mn[j], v);
-      mx[j] = fmaxf(mx[j], v);
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) { mn[j] = min4rows(mn[j]); mx[j] = max4rows(mx[j]); }
-  if (rl == 0) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) { xch[(2 * qtr) * D + 8 * cl + j] = mn[j]; xch[(2 * qtr + 1) * D + 8 * cl + j] = mx[j]; }
-  }
-  __syncthreads();
-  float stp[8], inv[8];
-  uint32_t s16[4], m16[4];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    float a0 = xch[8 * cl + j], b0 = xch[D + 8 * cl + j];
-#pragma unroll
-    for (int k = 1; k < 4; ++k) { a0 = fminf(a0, xch[2 * k * D + 8 * cl + j]); b0 = fmaxf(b0, xch[(2 * k + 1) * D + 8 * cl + j]); }
-    mn[j] = a0;
-    stp[j] = ruler_step(a0, b0);
-    inv[j] = ruler_inv(stp[j]);
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    s16[j] = (uint32_t)f2h(stp[2 * j]) | ((uint32_t)f2h(stp[2 * j + 1]) << 16);
-    m16[j] = (uint32_t)f2h(mn[2 * j]) | ((uint32_t)f2h(mn[2 * j + 1]) << 16);
-  }
-  if (qtr == 0 && rl == 0) {
-    *reinterpret_cast<uint4*>(mn_g + 8 * cl) = uint4{m16[0], m16[1], m16[2], m16[3]};
-    *reinterpret_cast<uint4*>(st_g + 8 * cl) = uint4{s16[0], s16[1], s16[2], s16[3]};
-  }
-  uint4 vals[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 16 * qtr + rl + 4 * i;
-    const uint32_t w[4] = {rq.rows[i].x, rq.rows[i].y, rq.rows[i].z, rq.rows[i].w};
-    uint32_t cc[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) cc[j] = ruler_code_rcp(h2f((uint16_t)(w[j >> 1] >> (16 * (j & 1)))), mn[j], stp[j], inv[j]);
-    const uint32_t o0 = cc[0] | (cc[1] << 8) | (cc[2] << 16) | (cc[3] << 24);
-    const uint32_t o1 = cc[4] | (cc[5] << 8) | (cc[6] << 16) | (cc[7] << 24);
-    const int64_t t = gcur * GT + r;
-    if (t < capacity) *reinterpret_cast<uint2*>(codes_h + t * D + 8 * cl) = uint2{o0, o1};
-    vals[i] = completes ? __builtin_bit_cast(uint4, dq8(o0, o1, uint4{s16[0], s16[1], s16[2], s16[3]},
-                                                        uint4{m16[0], m16[1], m16[2], m16[3]}))
-                        : rq.rows[i];
-  }
-  ring_quarter_to_lds(vals, qtr, ring_lds);
-}
-
 __device__ __forceinline__ const uint16_t* ring_of(const AttnArgs& a, int h, int which) {
   return (which == 0 ? a.tail_k : a.tail_v) + (int64_t)h * a.tail_slots * D;
 }
 __device__ __forceinline__ const uint16_t* fresh_of(const AttnArgs& a, int h, int which) {
   return (which == 0 ? a.k_new : a.v_new) + h * a.kv_hs;
-}
-
-// The append of head h by the 8 waves of a workgroup: waves 0-3 take the quarters of K,
-// waves 4-7 those of V.
-__device__ __forceinline__ void append_head8(const AttnArgs& a, int h, int wave, int64_t pos, RingQuarter& rq,
-                                             bool completes, float* xch, uint8_t* ring_k, uint8_t* ring_v) {
-  const int which = wave >> 2, qtr = wave & 3;
-  const int slot = (int)(pos % GT);
-  const int64_t gcur = pos / GT;
-  const int64_t ro = ((int64_t)h * a.ngroups_cap + gcur) * D;
-  uint16_t* ring = (which == 0 ? a.tail_k : a.tail_v) + (int64_t)h * GT * D;
-  uint8_t* codes = (which == 0 ? a.kq : a.vq) + (int64_t)h * a.capacity * D;
-  uint16_t* mn = (which == 0 ? a.kmn : a.vmn) + ro;
-  uint16_t* st = (which == 0 ? a.kst : a.vst) + ro;
-  ring_append_quarter(rq, ring, codes, mn, st, slot, gcur, a.capacity, completes, qtr, xch + which * 8 * D,
-                      which == 0 ? ring_k : ring_v);
 }
 
 __device__ __forceinline__ void write_scalars(const AttnArgs& a, int64_t pos) {
@@ -600,17 +528,69 @@ __device__ __forceinline__ void write_scalars(const AttnArgs& a, int64_t pos) {
   *a.pg_out = qlen / GT;
 }
 
-// Slot validity of the ring: slot i holds p = u - ((u - i) mod 64), valid iff qlen <= p <= u, p >= first.
+// Slot validity of the ring: slot i holds p = u - ((u - i) mod 64), valid iff qlen <= p <= u,
+// p >= first (u = written - 1). Lane i decides slot i; the wave's ballot is the mask.
 __device__ __forceinline__ uint64_t ring_bits(int64_t written, int64_t qlen, int64_t first) {
+  const int i = threadIdx.x & 63;
   const int64_t u = written - 1;
-  uint64_t bits = 0;
-  for (int i = 0; i < GT; ++i) {
-    int64_t d = (u - i) % GT;
-    if (d < 0) d += GT;
-    const int64_t p = u - d;
-    if (p >= qlen && p <= u && p >= first) bits |= 1ull << i;
+  const int64_t p = u - ((u - i) & (GT - 1));
+  return __builtin_amdgcn_ballot_w64(p >= qlen && p <= u && p >= first);
+}
+
+// ---------------------------------------------------------------- append units
+
+// The fused step's append is split into APPEND_UNITS units per KV head (8 channels of K or
+// V each), one per prefix workgroup, run ahead of its stream. A unit's source rows (the
+// 64 ring rows and the new token, 16 bytes each) come into LDS through one HBM -> LDS load
+// of wave 0, issued with the groups.
+constexpr int UNIT_CH = 8;
+constexpr int APPEND_UNITS = 2 * D / UNIT_CH;
+constexpr int UNIT_SRC_BYTES = (GT + 1) * UNIT_CH * 2;
+
+__device__ __forceinline__ void issue_unit_rows(const AttnArgs& a, int h, int unit, uint32_t src) {
+  const int lane = threadIdx.x & 63, which = unit / (D / UNIT_CH), ch0 = unit % (D / UNIT_CH) * UNIT_CH;
+  dma16(uniform_ptr(ring_of(a, h, which) + ch0), (uint32_t)(lane * D * 2), src);
+  if (lane == 0) dma16(uniform_ptr(fresh_of(a, h, which) + ch0), 0u, src + GT * UNIT_CH * 2);
+}
+
+__device__ __forceinline__ float ror8(float v) {  // lane l <- lane l ^ 8 within each 16-lane row
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
+}
+
+// Requantization of append unit `unit` of head h for the token at `pos`, once its source
+// rows are in `src` (LDS, visible to the workgroup): the ring with the new token in slot
+// pos % 64 is ruled per channel over all 64 slots into group pos / 64 exactly as the bulk
+// quantizer rules a group, and the group's codes and rulers and the new ring slot are
+// stored. Thread t takes ring row t >> 3, channel t & 7 of the unit. Needs 512 threads;
+// `xch` is 8 x 16 floats of LDS; one workgroup barrier inside.
+__device__ __forceinline__ void append_unit(const AttnArgs& a, int h, int unit, int64_t pos, const uint16_t* src,
+                                            float* xch) {
+  static_assert(THREADS == UNIT_CH * GT, "one thread per value of a unit");
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, r = t >> 3, c = t & 7;
+  const int which = unit / (D / UNIT_CH), ch = unit % (D / UNIT_CH) * UNIT_CH + c;
+  const int slot = (int)(pos % GT);
+  const int64_t gcur = pos / GT;
+  const uint16_t bits = src[(r == slot ? GT : r) * UNIT_CH + c];
+  const float v = h2f(bits);
+  // extremes over the wave's rows (lane >> 3): lane ^ 8 within each 16-lane row, then across rows
+  const float mn = min4rows(fminf(v, ror8(v)));
+  const float mx = max4rows(fmaxf(v, ror8(v)));
+  if (lane < UNIT_CH) { xch[c * 16 + wave] = mn; xch[c * 16 + 8 + wave] = mx; }
+  __syncthreads();
+  const float4* x4 = reinterpret_cast<const float4*>(xch + 16 * c);
+  const float4 m0 = x4[0], m1 = x4[1], M0 = x4[2], M1 = x4[3];
+  const float lo = fminf(fminf(fminf(m0.x, m0.y), fminf(m0.z, m0.w)), fminf(fminf(m1.x, m1.y), fminf(m1.z, m1.w)));
+  const float hi = fmaxf(fmaxf(fmaxf(M0.x, M0.y), fmaxf(M0.z, M0.w)), fmaxf(fmaxf(M1.x, M1.y), fmaxf(M1.z, M1.w)));
+  const float step = ruler_step(lo, hi);
+  const int64_t ro = ((int64_t)h * a.ngroups_cap + gcur) * D + ch;
+  if (r == 0) {
+    (which == 0 ? a.kmn : a.vmn)[ro] = f2h(lo);
+    (which == 0 ? a.kst : a.vst)[ro] = f2h(step);
   }
-  return bits;
+  const int64_t tok = gcur * GT + r;
+  if (tok < a.capacity)
+    (which == 0 ? a.kq : a.vq)[((int64_t)h * a.capacity + tok) * D + ch] = (uint8_t)ruler_code_rcp(v, lo, step, ruler_inv(step));
+  if (r == slot) (which == 0 ? a.tail_k : a.tail_v)[((int64_t)h * GT + slot) * D + ch] = bits;
 }
 
 // ---------------------------------------------------------------- partials
@@ -619,15 +599,25 @@ __device__ __forceinline__ uint64_t ring_bits(int64_t written, int64_t qlen, int
 // partial starts 16-byte aligned. acc is scaled by 2^15, m is in the log2 domain.
 __host__ __device__ __forceinline__ int part_stride(int gq) { return gq * D + ((2 * gq + 3) & ~3); }
 
+// Whole-wave reductions on VALU data movement only: DPP within each 16-lane row (lane ^ 1,
+// lane ^ 2, then rotations by 4 and 8), then the permlane swaps across rows.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
-  return v;
+  v = fmaxf(v, dpp<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = fmaxf(v, dpp<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = fmaxf(v, dpp<0x124>(v));  // row_ror 4
+  v = fmaxf(v, dpp<0x128>(v));  // row_ror 8
+  return max4rows(v);
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
-  return v;
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x124>(v);
+  v += dpp<0x128>(v);
+  return sum4rows(v);
 }
 
 // Write one wave's online-softmax state as a partial at `dst` (LDS or memory): lane (c, g)
@@ -666,9 +656,14 @@ __device__ __forceinline__ int64_t prefix_limit(const AttnArgs& a, int64_t& pos,
 
 // Workgroup (h, part) streams the 64-token groups [gs, ge) of KV head h's int8 prefix and
 // writes one partial to ws[h][part]. Plain stores: the tail kernel that reads them runs
-// after this launch completes.
+// after this launch completes. In the fused step, workgroup part < APPEND_UNITS first runs
+// append unit `part` of head h (the prefix never reads the group it writes), and the grid
+// has max(n_parts, APPEND_UNITS) parts per head; parts >= n_parts only append.
 __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_raw[LDS_BYTES];
+  __shared__ __attribute__((aligned(16))) uint16_t unit_src[UNIT_SRC_BYTES / 2];
+  __shared__ __attribute__((aligned(16))) uint16_t q_lds[16 * D];
+  __shared__ __attribute__((aligned(16))) float xch[UNIT_CH * 16];
   float* lds = reinterpret_cast<float*>(lds_raw);
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -676,22 +671,41 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   const int part = blockIdx.x / a.hkv;
   uint8_t* my_stages = lds_raw + wave * STAGES * STAGE_BYTES;
   const uint32_t my_lds = __builtin_amdgcn_readfirstlane(lds_addr(my_stages));
+  const uint32_t src_lds = __builtin_amdgcn_readfirstlane(lds_addr(unit_src));
 
-  WaveState st;
-  state_init(st);
-  half8_t qb[4];
-  load_q(a, h, qb);
   int64_t pos;
   bool pos_ok;
   const int64_t U = prefix_limit(a, pos, pos_ok);
+  const bool append = a.tail_mode == TAIL_FUSED && pos_ok && part < APPEND_UNITS;
+  const bool prefix = part < a.n_parts;  // the fused step's grid has at least APPEND_UNITS parts
 
   const int64_t W = (U + GT - 1) / GT;
-  const int64_t gs = (int64_t)part * W / a.n_parts;
-  const int64_t ge = (int64_t)(part + 1) * W / a.n_parts;
+  const int64_t gs = prefix ? (int64_t)part * W / a.n_parts : 0;
+  const int64_t ge = prefix ? (int64_t)(part + 1) * W / a.n_parts : 0;
   const int n = ge - gs > wave ? (int)((ge - gs - wave + WAVES - 1) / WAVES) : 0;
+  // Q and the append unit's rows are loaded ahead of the groups, so that waiting for them
+  // leaves the groups in flight
+  if (wave == 0 && prefix) issue_q(a, h, __builtin_amdgcn_readfirstlane(lds_addr(q_lds)));
+  if (wave == 0 && append) issue_unit_rows(a, h, part, src_lds);
 #pragma unroll
   for (int s0 = 0; s0 < STAGES; ++s0)
     if (s0 < n) issue_group(a, h, gs + wave + (int64_t)s0 * WAVES, my_lds + s0 * STAGE_BYTES);
+  const int in_flight = min(n, STAGES);
+  if (in_flight == 0) wait_groups_all();
+  else if (in_flight == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_PER_GROUP) : "memory");
+  else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_PER_GROUP) : "memory");
+  __syncthreads();
+
+  if (append) {
+    append_unit(a, h, part, pos, unit_src, xch);
+    if (blockIdx.x == 0 && tid == 0) write_scalars(a, pos);
+  }
+  if (!prefix) return;
+  WaveState st;
+  state_init(st);
+  half8_t qb[4];
+  load_q_lds(q_lds, a.gq, qb);
+
   for (int i = 0; i < n; ++i) {
     if (STAGES > 1 && i + 1 < n) wait_groups_all_but_one();
     else wait_groups_all();
@@ -726,17 +740,19 @@ constexpr int TB_WAVES = 8;
 constexpr int TB_THREADS = 64 * TB_WAVES;
 constexpr int MERGE_CHUNK = 32;  // partial slots per column loaded up front
 constexpr int RING_PARTS = 4;    // the ring's 64 tokens as 4 partials of 16
+constexpr int WT_STRIDE = 256 + RING_PARTS + 4;
+static_assert(MERGE_CHUNK + RING_PARTS <= WT_STRIDE && WT_STRIDE % 4 == 0, "merge weight rows");
 
-// One workgroup per KV head, after kernel A: appends the new token (fused step), attends
-// over the ring (or the group the token completed), then merges the prefix partials of
-// kernel A and the ring's partials by log-sum-exp and writes out / lse. Every phase is
-// spread over the 8 waves (a wave's dependent instruction chain is what bounds this
-// kernel), and every load it needs is issued at its start.
+// One workgroup per KV head, after the prefix kernel: attends over the ring (or the group
+// the token completed), then merges the prefix partials and the ring's partials by
+// log-sum-exp and writes out / lse. Every phase is spread over the 8 waves (a wave's
+// dependent instruction chain is what bounds this kernel), and every load it needs is
+// issued at its start.
 __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t ring_lds[2 * RING_BYTES];          // K | V values
   __shared__ __attribute__((aligned(16))) float ring_part[RING_PARTS][16 * D + 32];  // the ring's partials
-  __shared__ __attribute__((aligned(16))) float xch[2 * 8 * D];                      // append min / max
   __shared__ float wts[(256 + RING_PARTS) * 16], lsv[(256 + RING_PARTS) * 16];
+  __shared__ __attribute__((aligned(16))) float wT[16][WT_STRIDE];  // merge weights [head][partial], 0-padded
   __shared__ float mh[16], lh[16];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = blockIdx.x;
@@ -748,11 +764,24 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
   const int64_t U = prefix_limit(a, pos, pos_ok);
   const bool ring = a.tail_mode != TAIL_NONE && (!fused || pos_ok);
 
-  // ---- every load up front: ring quarters, `first`, q, m / l and a column of the partials
+  // ---- every load up front: ring quarters (or the completed group), `first`, the mask, q,
+  // m / l and a column of the partials
+  const int which = wave >> 2, qtr = wave & 3;
+  const bool completes = fused && pos_ok && (pos + 1) % GT == 0;  // the token completed its group
   RingQuarter rq;
-  if (ring) ring_load_quarter(ring_of(a, h, wave >> 2), fused ? fresh_of(a, h, wave >> 2) : nullptr,
-                              (int)a.tail_slots, wave & 3, rq);
+  if (ring && !completes) ring_load_quarter(ring_of(a, h, which), (int)a.tail_slots, qtr, rq);
+  uint2 cw[4];
+  uint4 cst, cmn;
+  if (completes) {
+    const int64_t gcur = pos / GT, ro = ((int64_t)h * a.ngroups_cap + gcur) * D + 8 * (lane & 15);
+    const uint8_t* codes = (which == 0 ? a.kq : a.vq) + ((int64_t)h * a.capacity + gcur * GT) * D + 8 * (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cw[i] = *reinterpret_cast<const uint2*>(codes + (16 * qtr + (lane >> 4) + 4 * i) * D);
+    cst = *reinterpret_cast<const uint4*>((which == 0 ? a.kst : a.vst) + ro);
+    cmn = *reinterpret_cast<const uint4*>((which == 0 ? a.kmn : a.vmn) + ro);
+  }
   const int64_t first = (ring && a.first_dev) ? *a.first_dev : 0;
+  const bool mask_on = ring && a.tail_mode == TAIL_MASK && lane < a.tail_slots && a.tail_mask[lane] != 0;
   half8_t qb[4];
   if (ring && wave < RING_PARTS) load_q(a, h, qb);
   const float* hws = a.ws + (int64_t)h * P * pw;
@@ -766,26 +795,25 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
 #pragma unroll
   for (int u = 0; u < MERGE_CHUNK; ++u) v[u] = (u < P && tid < cols) ? hws[(int64_t)u * pw + tid] : 0.0f;
 
-  // ---- the ring: append (fused) into the LDS ring, then 4 waves x 16 tokens
+  // ---- the ring (the prefix kernel did the fused step's append) into LDS, then 4 waves x
+  // 16 tokens. A token that completes its group is attended through the group's int8
+  // values, dequantized as the prefix dequantizes them.
   uint8_t* ring_k = ring_lds;
   uint8_t* ring_v = ring_lds + RING_BYTES;
   if (ring) {
     const int64_t written = fused ? pos + 1 : (a.tail_mode == TAIL_SCALARS ? *a.written_dev : 0);
-    const int64_t qlen = fused ? written / GT * GT : U;
-    const bool completes = fused && qlen > U;  // this token completes the ring's group
-    if (fused) append_head8(a, h, wave, pos, rq, completes, xch, ring_k, ring_v);
-    else ring_quarter_to_lds(rq.rows, wave & 3, (wave >> 2) == 0 ? ring_k : ring_v);
-    if (fused && h == 0 && tid == 0) write_scalars(a, pos);
+    const int64_t qlen = U;
+    if (completes) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rq.rows[i] = __builtin_bit_cast(uint4, dq8(cw[i].x, cw[i].y, cst, cmn));
+    }
+    ring_quarter_to_lds(rq.rows, qtr, which == 0 ? ring_k : ring_v);
     __syncthreads();
     if (wave < RING_PARTS) {
-      uint64_t bits = 0;
-      if (completes) {
-        bits = ~0ull;  // the completed group, through its int8 values
-      } else if (a.tail_mode == TAIL_MASK) {
-        for (int i = 0; i < a.tail_slots; ++i) bits |= (uint64_t)(a.tail_mask[i] != 0) << i;
-      } else {
-        bits = ring_bits(written, qlen, first);
-      }
+      uint64_t bits;
+      if (completes) bits = ~0ull;
+      else if (a.tail_mode == TAIL_MASK) bits = __builtin_amdgcn_ballot_w64(mask_on);
+      else bits = ring_bits(written, qlen, first);
       WaveState st;
       state_init(st);
       attend_ring16(a, st, qb, ring_k, ring_v, wave, bits);
@@ -813,11 +841,11 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
     for (int s = lane; s < ns; s += 64) m = fmaxf(m, wts[s * gq + head]);
     m = wave_max(m);
     float l = 0.0f;
-    for (int s = lane; s < ns; s += 64) {
-      const float ms = wts[s * gq + head];
+    for (int s = lane; s < WT_STRIDE; s += 64) {  // weights of every partial, 0 past the last
+      const float ms = s < ns ? wts[s * gq + head] : NEG_INF;
       const float w = ms == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(ms - m);
-      wts[s * gq + head] = w;
-      l += lsv[s * gq + head] * w;
+      wT[head][s] = w;
+      if (s < ns) l += lsv[s * gq + head] * w;
     }
     l = wave_sum(l);
     if (lane == 0) { mh[head] = m; lh[head] = l; }
@@ -826,19 +854,24 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
 #pragma unroll 1
   for (int col = tid; col < cols; col += TB_THREADS) {
     const int head = col / D;
+    const float* w = wT[head];
     float acc = 0.0f;
     if (ring) {
 #pragma unroll
-      for (int r = 0; r < RING_PARTS; ++r) acc += ring_part[r][col] * wts[(P + r) * gq + head];
+      for (int r = 0; r < RING_PARTS; ++r) acc += ring_part[r][col] * w[P + r];
     }
     if (col == tid) {
+      // v[u] is 0 for u >= P, where w holds ring weights or 0
 #pragma unroll
-      for (int u = 0; u < MERGE_CHUNK; ++u) if (u < P) acc += v[u] * wts[u * gq + head];
+      for (int u = 0; u < MERGE_CHUNK; u += 4) {
+        const float4 w4 = *reinterpret_cast<const float4*>(w + u);
+        acc += v[u] * w4.x + v[u + 1] * w4.y + v[u + 2] * w4.z + v[u + 3] * w4.w;
+      }
     } else {
-      for (int s = 0; s < min(P, MERGE_CHUNK); ++s) acc += hws[(int64_t)s * pw + col] * wts[s * gq + head];
+      for (int s = 0; s < min(P, MERGE_CHUNK); ++s) acc += hws[(int64_t)s * pw + col] * w[s];
     }
 #pragma unroll 4
-    for (int s = MERGE_CHUNK; s < P; ++s) acc += hws[(int64_t)s * pw + col] * wts[s * gq + head];
+    for (int s = MERGE_CHUNK; s < P; ++s) acc += hws[(int64_t)s * pw + col] * w[s];
     const float l = lh[head];
     const int qh = h * gq + head, d = col % D;
     a.out[(int64_t)qh * D + d] = f2h(l > 0.0f ? acc * (INV_P_SCALE / l) : 0.0f);
@@ -846,17 +879,18 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
   }
 }
 
-// Standalone append: one workgroup of 8 waves per KV head (4 per tensor).
-__global__ __launch_bounds__(512) void append_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t ring[2 * RING_BYTES];
-  __shared__ __attribute__((aligned(16))) float xch[2 * 8 * D];
-  const int h = blockIdx.x, wave = threadIdx.x >> 6;
+// Standalone append: one workgroup per append unit (APPEND_UNITS per KV head).
+__global__ __launch_bounds__(THREADS) void append_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t unit_src[UNIT_SRC_BYTES / 2];
+  __shared__ __attribute__((aligned(16))) float xch[UNIT_CH * 16];
+  const int h = blockIdx.x / APPEND_UNITS, unit = blockIdx.x % APPEND_UNITS;
   const int64_t pos = *a.pos_dev;
   if (pos < 0 || pos >= a.capacity) return;  // a position outside the cache appends nothing
-  RingQuarter rq;
-  ring_load_quarter(ring_of(a, h, wave >> 2), fresh_of(a, h, wave >> 2), GT, wave & 3, rq);
-  append_head8(a, h, wave, pos, rq, false, xch, ring, ring + RING_BYTES);
-  if (h == 0 && threadIdx.x == 0) write_scalars(a, pos);
+  if (threadIdx.x < 64) issue_unit_rows(a, h, unit, __builtin_amdgcn_readfirstlane(lds_addr(unit_src)));
+  wait_groups_all();
+  __syncthreads();
+  append_unit(a, h, unit, pos, unit_src, xch);
+  if (blockIdx.x == 0 && threadIdx.x == 0) write_scalars(a, pos);
 }
 
 __global__ void ring_mask_kernel(const int64_t* written, const int64_t* qlen, const int64_t* first,
@@ -897,7 +931,8 @@ static int launch_attn(AttnArgs& a, int64_t n_parts, int64_t workspace_bytes, hi
     return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
   if (n_parts > 256) return fail(NKV_ERR_UNSUPPORTED, "%s: n_parts %lld exceeds the 256 partials the merge holds", what, (long long)n_parts);
   if (n_parts > 0) {
-    hipLaunchKernelGGL(attn_prefix_kernel, dim3((unsigned)(a.hkv * n_parts)), dim3(THREADS), 0, s, a);
+    const int64_t parts = a.tail_mode == TAIL_FUSED ? std::max<int64_t>(n_parts, APPEND_UNITS) : n_parts;
+    hipLaunchKernelGGL(attn_prefix_kernel, dim3((unsigned)(a.hkv * parts)), dim3(THREADS), 0, s, a);
     if (int rc = check_launch(what)) return rc;
   }
   hipLaunchKernelGGL(attn_tail_kernel, dim3((unsigned)a.hkv), dim3(TB_THREADS), 0, s, a);
@@ -979,7 +1014,7 @@ extern "C" int nkv_append_t64(const uint16_t* k_new, const uint16_t* v_new, int6
   a.tail_k = tail_k; a.tail_v = tail_v; a.pos_dev = pos_dev;
   a.written_out = written_dev; a.qlen_out = qlen_dev; a.pg_out = pg_dev;
   a.capacity = capacity; a.ngroups_cap = cdiv(capacity, GT); a.hkv = (int)hkv; a.tail_slots = GT;
-  hipLaunchKernelGGL(append_kernel, dim3((unsigned)hkv), dim3(512), 0, static_cast<hipStream_t>(stream), a);
+  hipLaunchKernelGGL(append_kernel, dim3((unsigned)(hkv * APPEND_UNITS)), dim3(THREADS), 0, static_cast<hipStream_t>(stream), a);
   return check_launch("append_t64");
 }
 
