@@ -8,13 +8,22 @@ synthetic q/k/v, then ``pos += 1``; the step is captured once as a hipGraph and
 replayed (one replay per token). W untimed replays, then K timed replays bracketed by
 ``torch.cuda.synchronize()`` and HIP events on the replay stream.
 
+Each layer's step is two launches: the prefix kernel (the append and the split-K
+partials over the int8 prefix) and the tail kernel (ring attention and the combine).
+
 Prints one JSON line (the driver's contract). ``value`` = decode tokens/s of the whole
-job. ``roofline`` refers to the dominant kernel (the fused decode-step kernel):
-algorithmic bytes per launch / average launch duration over the timed region.
-``cpu_baseline`` times the numpy oracle (dequantize + softmax attention, 8 threads over
-KV heads) on one layer for ~10-30 s and scales to the 36-layer step.
+job. ``roofline`` refers to the dominant kernel, the prefix kernel: its algorithmic bytes
+per launch / its average launch duration, timed with HIP events over K replays of a
+graph holding only its 36 launches per step (``nkv_decode_step_partials_t64``, the same
+kernel and arguments as in the full step); the tail kernel is timed the same way and
+reported beside it. ``traffic`` comes from the committed rocprofv3 --pmc summary
+(FETCH_SIZE + WRITE_SIZE per dispatch of the prefix kernel, scaled by what the same
+counters read for the library's plain copy kernel of known size). ``cpu_baseline`` times
+the numpy oracle (dequantize + softmax attention, threads over KV heads) on one layer for
+~10-30 s and scales to the 36-layer step.
 
     python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu-baseline]
+    python bench.py --traffic-from FETCH_DIR WRITE_DIR   # summarize two rocprofv3 --pmc runs
 """
 
 from __future__ import annotations
@@ -33,8 +42,13 @@ sys.path.insert(0, str(ROOT))
 
 LAYERS, HQ, HKV, D, CTX = 36, 32, 8, 128, 32768
 HBM_PEAK_GBS = 8000.0
-APPEND_BYTES = 64 * 128 * 2 * 2 * HKV + 64 * 128 * 2 * HKV + 4 * 128 * 2 * HKV + 2 * 2 * 128 * 2 * HKV
-TRAFFIC_FILE = ROOT / "profiles" / "decode_step_32k_traffic.txt"
+# the fused step's append per layer: K and V ring read (64 x 128 fp16 each per KV head),
+# new token read and written into the ring, 64 code rows and 4 ruler rows written
+APPEND_BYTES = 64 * 128 * 2 * 2 * HKV + 2 * 2 * 128 * 2 * HKV + 64 * 128 * 2 * HKV + 4 * 128 * 2 * HKV
+Q_BYTES = HQ * D * 2
+PREFIX_KERNEL = "attn_prefix_kernel"
+COPY_KERNEL = "copy16_kernel"
+TRAFFIC_FILE = ROOT / "profiles" / "attn_prefix_kernel_32k_traffic.txt"
 
 
 def attn_bytes(u: int) -> int:
@@ -45,10 +59,12 @@ def attn_bytes(u: int) -> int:
     return 2176 * q + 4096 * (u - q) + 16384
 
 
-def step_launch_bytes(u: int) -> int:
-    """One fused launch: attention plus the ring append (new token in, whole-ring
-    requantize: ring read, 64 code rows and two rulers written)."""
-    return attn_bytes(u) + APPEND_BYTES
+def prefix_launch_bytes(u: int) -> int:
+    """Algorithmic bytes of one prefix-kernel launch with ``u`` tokens written: int8 codes
+    + fp16 rulers of the whole groups before the ring's group (2176 B per token over 8 KV
+    heads), q, and the append."""
+    prefix = max(u - 1, 0) // 64 * 64
+    return 2176 * prefix + Q_BYTES + APPEND_BYTES
 
 
 def parse_args():
@@ -61,12 +77,66 @@ def parse_args():
     ap.add_argument("--parts", type=int, default=0, help="work units per KV head (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarize two rocprofv3 --pmc runs of this script into the traffic file")
     return ap.parse_args()
 
 
+def _pmc_means(run_dir: str, counter: str) -> dict:
+    """Mean per-dispatch value of ``counter`` for each kernel in a rocprofv3 --pmc CSV run."""
+    import csv
+
+    files = sorted(Path(run_dir).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {run_dir}")
+    acc: dict = {}
+    for f in files:
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") != counter:
+                    continue
+                name = row["Kernel_Name"]
+                for key in (PREFIX_KERNEL, "attn_tail_kernel", COPY_KERNEL):
+                    if key in name:
+                        acc.setdefault(key, []).append(float(row["Counter_Value"]))
+    return {k: sum(v) / len(v) for k, v in acc.items()}
+
+
+def write_traffic(fetch_dir: str, write_dir: str) -> None:
+    """Traffic of the prefix kernel from FETCH_SIZE and WRITE_SIZE (KiB per dispatch),
+    each scaled by the factor that makes the same counter read the copy kernel's known
+    byte count (COPY_BYTES read and written)."""
+    fetch, write = _pmc_means(fetch_dir, "FETCH_SIZE"), _pmc_means(write_dir, "WRITE_SIZE")
+    f_scale = COPY_BYTES / (fetch[COPY_KERNEL] * 1024)
+    w_scale = COPY_BYTES / (write[COPY_KERNEL] * 1024)
+    f_bytes = fetch[PREFIX_KERNEL] * 1024 * f_scale
+    w_bytes = write[PREFIX_KERNEL] * 1024 * w_scale
+    alg = prefix_launch_bytes(CTX + 1)
+    lines = [
+        "# HBM traffic of nkv::attn_prefix_kernel, 32k-context decode step (36 layers, 32 q / 8 kv heads)",
+        "# made by (rocprofv3 --pmc runs of bench.py, then this summary):",
+        "#   rocprofv3 --pmc FETCH_SIZE -d FETCH_DIR -o run --output-format csv -- python3 bench.py --steps 4 --warmup 1 --no-cpu-baseline",
+        "#   rocprofv3 --pmc WRITE_SIZE -d WRITE_DIR -o run --output-format csv -- python3 bench.py --steps 4 --warmup 1 --no-cpu-baseline",
+        "#   python3 bench.py --traffic-from FETCH_DIR WRITE_DIR",
+        f"copy_kernel_bytes: {COPY_BYTES}  (read, and again written, by nkv_copy_bytes)",
+        f"copy_kernel_FETCH_SIZE_KiB: {fetch[COPY_KERNEL]:.1f}  -> fetch scale {f_scale:.4f}",
+        f"copy_kernel_WRITE_SIZE_KiB: {write[COPY_KERNEL]:.1f}  -> write scale {w_scale:.4f}",
+        f"prefix_kernel_FETCH_SIZE_KiB: {fetch[PREFIX_KERNEL]:.1f}  -> {f_bytes:.0f} B",
+        f"prefix_kernel_WRITE_SIZE_KiB: {write[PREFIX_KERNEL]:.1f}  -> {w_bytes:.0f} B",
+        f"algorithmic_bytes_per_launch: {alg}",
+        f"traffic_bytes_per_launch: {f_bytes + w_bytes:.0f}",
+        f"traffic_over_algorithmic: {(f_bytes + w_bytes) / alg:.4f}",
+    ]
+    if "attn_tail_kernel" in fetch and "attn_tail_kernel" in write:
+        lines.append(f"tail_kernel_traffic_bytes_per_launch: "
+                     f"{fetch['attn_tail_kernel'] * 1024 * f_scale + write['attn_tail_kernel'] * 1024 * w_scale:.0f}")
+    TRAFFIC_FILE.write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def read_traffic():
-    """HBM bytes per launch of the decode-step kernel from the committed rocprofv3 --pmc
-    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), or None."""
+    """HBM bytes per launch of the prefix kernel from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), or None."""
     if not TRAFFIC_FILE.exists():
         return None
     m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", TRAFFIC_FILE.read_text(), re.M)
@@ -118,8 +188,14 @@ def cpu_baseline(budget_s: float) -> dict:
             "seconds_per_step": per_step}
 
 
+COPY_BYTES = 64 << 20
+
+
 def main() -> int:
     args = parse_args()
+    if args.traffic_from:
+        write_traffic(*args.traffic_from)
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported on this path "
               "(the decode attention shards by KV head across GPUs; see the design notes)", file=sys.stderr)
@@ -134,7 +210,7 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     L, ctx, W, K = args.layers, args.ctx, args.warmup, args.steps
-    max_len = -(-(ctx + W + K + 1) // 64) * 64
+    max_len = -(-(ctx + 3 * (W + K) + 1) // 64) * 64
 
     # ---- prefill: seeded N(0,1) K/V, 4 random K channels per head x8, quantized by the
     # bulk HIP quantizer into the cache (staging area -> finish_prefill)
@@ -187,8 +263,39 @@ def main() -> int:
     assert int(cache.pos.item()) == pos0 + K
     assert torch.isfinite(cache.merged).all()
 
+    # ---- each of the step's two kernels alone: a graph of its 36 launches per step (the
+    # same kernel and arguments as above), K replays timed with HIP events
+    def kernel_graph(entry: str, advance: bool):
+        args_per_layer = [cache.step_args(ks[layer], vs[layer], qs[layer], layer) for layer in range(L)]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for a in args_per_layer:
+                _lib.call(entry, *a[:-1], _lib.stream_ptr(dev))
+            if advance:
+                cache.pos.add_(1)
+        return g, args_per_layer
+
+    def time_graph(g) -> float:
+        for _ in range(W):
+            g.replay()
+        torch.cuda.synchronize()
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record(stream)
+        for _ in range(K):
+            g.replay()
+        s1.record(stream)
+        torch.cuda.synchronize()
+        return s0.elapsed_time(s1)
+
+    g_prefix, keep = kernel_graph("nkv_decode_step_partials_t64", True)
+    pos_a = int(cache.pos.item()) + W
+    ms_prefix = time_graph(g_prefix)
+    g_tail, keep2 = kernel_graph("nkv_decode_step_combine_t64", False)
+    ms_tail = time_graph(g_tail)
+    del keep, keep2
+
     # ---- traffic calibration copy (known byte count; read by the --pmc runs)
-    cal = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    cal = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)
     cal2 = torch.empty_like(cal)
     _lib.call("nkv_copy_bytes", cal.data_ptr(), cal2.data_ptr(), cal.numel(), _lib.stream_ptr(dev))
     torch.cuda.synchronize()
@@ -196,9 +303,10 @@ def main() -> int:
     ms_step = ms / K
     tok_s = K / (ms / 1e3)
     us = [pos0 + i + 1 for i in range(K)]  # tokens written when each timed step attends
-    launch_bytes = sum(step_launch_bytes(u) for u in us) / K
-    step_bytes = launch_bytes * L
-    per_launch_s = ms / 1e3 / (K * L)
+    step_bytes = sum(attn_bytes(u) + APPEND_BYTES for u in us) / K * L
+    ua = [pos_a + i + 1 for i in range(K)]  # the same for the prefix-kernel graph's replays
+    launch_bytes = sum(prefix_launch_bytes(u) for u in ua) / K
+    per_launch_s = ms_prefix / 1e3 / (K * L)
     achieved = launch_bytes / per_launch_s / 1e9
     traffic = read_traffic()
     out = {
@@ -231,9 +339,13 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "nkv::attn_decode_kernel (fused append + attention, one launch per layer)",
+            "kernel": "nkv::attn_prefix_kernel (append + split-K partials over the int8 prefix)",
             "algorithmic_bytes_per_launch": round(launch_bytes),
             "avg_launch_us": round(per_launch_s * 1e6, 3),
+        },
+        "tail_kernel": {
+            "kernel": "nkv::attn_tail_kernel (ring attention + log-sum-exp combine)",
+            "avg_launch_us": round(ms_tail / (K * L) * 1e3, 3),
         },
     }
     if not args.no_cpu_baseline:

@@ -141,8 +141,8 @@ int nkv_append_t64(const uint16_t* k_new, const uint16_t* v_new, int64_t kv_head
  * One decode step of one layer: nkv_append_t64 followed by nkv_attn_decode_t64
  * over the int8 prefix and the ring, with the same cache state and scalars as the
  * two-call sequence and the same output up to float summation order. Two launches:
- * the prefix kernel, then the tail kernel, which also performs the append (its
- * group is not read by the prefix kernel). Replaces the `KVInt8Cache.update` +
+ * the prefix kernel, which also performs the append (the prefix never reads the group
+ * it writes), then the tail kernel (ring attention and the combine). Replaces the `KVInt8Cache.update` +
  * `KVInt8Cache.attend` pair that `LeanAttention.forward` issues per layer
  * (src/nova/layers.py:132-136).
  */
@@ -154,6 +154,33 @@ int nkv_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t
                         int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out,
                         float* lse_out, void* workspace, int64_t workspace_bytes,
                         int64_t n_parts, void* stream);
+
+/*
+ * The two launches of nkv_decode_step_t64 as separate calls, with the same arguments:
+ * _partials (the prefix kernel: the append and one partial per workgroup into
+ * `workspace`; `out` / `lse_out` are not written) followed by _combine (the tail kernel:
+ * ring attention and the log-sum-exp combine into out / lse) on one stream equals one
+ * nkv_decode_step_t64 call. They replace the reference's split of the decode attention
+ * into `_int8_attn_partial_kernel` and `_int8_attn_combine_kernel`
+ * (src/nova/kvattn.py:110-253), and let a caller time or schedule the two separately.
+ * Between the two calls, `workspace` and the cache must not be touched.
+ */
+int nkv_decode_step_partials_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                                 int64_t kv_head_stride, uint8_t* kq, uint16_t* kmn, uint16_t* kst,
+                                 uint8_t* vq, uint16_t* vmn, uint16_t* vst, uint16_t* tail_k,
+                                 uint16_t* tail_v, const int64_t* pos_dev, const int64_t* first_dev,
+                                 int64_t* written_dev, int64_t* qlen_dev, int64_t* pg_dev, int64_t hq,
+                                 int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out,
+                                 float* lse_out, void* workspace, int64_t workspace_bytes,
+                                 int64_t n_parts, void* stream);
+int nkv_decode_step_combine_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                                int64_t kv_head_stride, uint8_t* kq, uint16_t* kmn, uint16_t* kst,
+                                uint8_t* vq, uint16_t* vmn, uint16_t* vst, uint16_t* tail_k,
+                                uint16_t* tail_v, const int64_t* pos_dev, const int64_t* first_dev,
+                                int64_t* written_dev, int64_t* qlen_dev, int64_t* pg_dev, int64_t hq,
+                                int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out,
+                                float* lse_out, void* workspace, int64_t workspace_bytes,
+                                int64_t n_parts, void* stream);
 
 /*
  * fp16 ring attention with a boolean slot mask and its log-sum-exp.

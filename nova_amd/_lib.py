@@ -31,6 +31,10 @@ P = c_void_p
 I64 = c_int64
 
 # name -> (restype, argtypes); must match include/nova_kv.h
+# q, k_new, v_new, kv_head_stride, kq, kmn, kst, vq, vmn, vst, tail_k, tail_v, pos, first, written,
+# qlen, pg, hq, hkv, head_dim, capacity, out, lse, workspace, workspace_bytes, n_parts, stream
+_STEP = [P, P, P, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, P, P, P, I64, I64, P]
+
 SIGNATURES = {
     "nkv_abi_version": (c_int, []),
     "nkv_last_error": (ctypes.c_char_p, []),
@@ -41,8 +45,9 @@ SIGNATURES = {
     "nkv_attn_workspace_bytes": (I64, [I64, I64, I64]),
     "nkv_attn_default_parts": (I64, [I64, I64]),
     "nkv_append_t64": (c_int, [P, P, I64, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, P]),
-    "nkv_decode_step_t64": (c_int, [P, P, P, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64,
-                                    P, P, P, I64, I64, P]),
+    "nkv_decode_step_t64": (c_int, _STEP),
+    "nkv_decode_step_partials_t64": (c_int, _STEP),
+    "nkv_decode_step_combine_t64": (c_int, _STEP),
     "nkv_tail_attend": (c_int, [P, P, P, P, I64, I64, I64, I64, P, P, P]),
     "nkv_ring_mask": (c_int, [P, P, P, I64, P, P]),
     "nkv_copy_bytes": (c_int, [P, P, I64, P]),

@@ -561,36 +561,53 @@ __device__ __forceinline__ float ror8(float v) {  // lane l <- lane l ^ 8 within
 // rows are in `src` (LDS, visible to the workgroup): the ring with the new token in slot
 // pos % 64 is ruled per channel over all 64 slots into group pos / 64 exactly as the bulk
 // quantizer rules a group, and the group's codes and rulers and the new ring slot are
-// stored. Thread t takes ring row t >> 3, channel t & 7 of the unit. Needs 512 threads;
-// `xch` is 8 x 16 floats of LDS; one workgroup barrier inside.
+// stored. Thread t takes channel t & 7 of the unit and ring rows (t >> 3) + 8 WAVES i.
+// `xch` is 8 x 2 WAVES floats of LDS; one workgroup barrier inside.
 __device__ __forceinline__ void append_unit(const AttnArgs& a, int h, int unit, int64_t pos, const uint16_t* src,
                                             float* xch) {
-  static_assert(THREADS == UNIT_CH * GT, "one thread per value of a unit");
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, r = t >> 3, c = t & 7;
+  constexpr int RPT = GT / (8 * WAVES);  // ring rows per thread
+  static_assert(RPT * 8 * WAVES == GT, "8 WAVES must divide the 64 ring rows");
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, r0 = t >> 3, c = t & 7;
   const int which = unit / (D / UNIT_CH), ch = unit % (D / UNIT_CH) * UNIT_CH + c;
   const int slot = (int)(pos % GT);
   const int64_t gcur = pos / GT;
-  const uint16_t bits = src[(r == slot ? GT : r) * UNIT_CH + c];
-  const float v = h2f(bits);
+  uint16_t bits[RPT];
+  float v[RPT];
+  float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int r = r0 + 8 * WAVES * i;
+    bits[i] = src[(r == slot ? GT : r) * UNIT_CH + c];
+    v[i] = h2f(bits[i]);
+    mn = fminf(mn, v[i]);
+    mx = fmaxf(mx, v[i]);
+  }
   // extremes over the wave's rows (lane >> 3): lane ^ 8 within each 16-lane row, then across rows
-  const float mn = min4rows(fminf(v, ror8(v)));
-  const float mx = max4rows(fmaxf(v, ror8(v)));
-  if (lane < UNIT_CH) { xch[c * 16 + wave] = mn; xch[c * 16 + 8 + wave] = mx; }
+  mn = min4rows(fminf(mn, ror8(mn)));
+  mx = max4rows(fmaxf(mx, ror8(mx)));
+  if (lane < UNIT_CH) { xch[c * 2 * WAVES + wave] = mn; xch[c * 2 * WAVES + WAVES + wave] = mx; }
   __syncthreads();
-  const float4* x4 = reinterpret_cast<const float4*>(xch + 16 * c);
-  const float4 m0 = x4[0], m1 = x4[1], M0 = x4[2], M1 = x4[3];
-  const float lo = fminf(fminf(fminf(m0.x, m0.y), fminf(m0.z, m0.w)), fminf(fminf(m1.x, m1.y), fminf(m1.z, m1.w)));
-  const float hi = fmaxf(fmaxf(fmaxf(M0.x, M0.y), fmaxf(M0.z, M0.w)), fmaxf(fmaxf(M1.x, M1.y), fmaxf(M1.z, M1.w)));
-  const float step = ruler_step(lo, hi);
+  float lo = xch[c * 2 * WAVES], hi = xch[c * 2 * WAVES + WAVES];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) {
+    lo = fminf(lo, xch[c * 2 * WAVES + w]);
+    hi = fmaxf(hi, xch[c * 2 * WAVES + WAVES + w]);
+  }
+  const float step = ruler_step(lo, hi), inv = ruler_inv(step);
   const int64_t ro = ((int64_t)h * a.ngroups_cap + gcur) * D + ch;
-  if (r == 0) {
+  if (r0 == 0) {
     (which == 0 ? a.kmn : a.vmn)[ro] = f2h(lo);
     (which == 0 ? a.kst : a.vst)[ro] = f2h(step);
   }
-  const int64_t tok = gcur * GT + r;
-  if (tok < a.capacity)
-    (which == 0 ? a.kq : a.vq)[((int64_t)h * a.capacity + tok) * D + ch] = (uint8_t)ruler_code_rcp(v, lo, step, ruler_inv(step));
-  if (r == slot) (which == 0 ? a.tail_k : a.tail_v)[((int64_t)h * GT + slot) * D + ch] = bits;
+  uint8_t* codes = (which == 0 ? a.kq : a.vq) + (int64_t)h * a.capacity * D + ch;
+  uint16_t* ring = (which == 0 ? a.tail_k : a.tail_v) + (int64_t)h * GT * D + ch;
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int r = r0 + 8 * WAVES * i;
+    const int64_t tok = gcur * GT + r;
+    if (tok < a.capacity) codes[tok * D] = (uint8_t)ruler_code_rcp(v[i], lo, step, inv);
+    if (r == slot) ring[slot * D] = bits[i];
+  }
 }
 
 // ---------------------------------------------------------------- partials
@@ -663,7 +680,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_raw[LDS_BYTES];
   __shared__ __attribute__((aligned(16))) uint16_t unit_src[UNIT_SRC_BYTES / 2];
   __shared__ __attribute__((aligned(16))) uint16_t q_lds[16 * D];
-  __shared__ __attribute__((aligned(16))) float xch[UNIT_CH * 16];
+  __shared__ __attribute__((aligned(16))) float xch[UNIT_CH * 2 * WAVES];
   float* lds = reinterpret_cast<float*>(lds_raw);
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -882,7 +899,7 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
 // Standalone append: one workgroup per append unit (APPEND_UNITS per KV head).
 __global__ __launch_bounds__(THREADS) void append_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t unit_src[UNIT_SRC_BYTES / 2];
-  __shared__ __attribute__((aligned(16))) float xch[UNIT_CH * 16];
+  __shared__ __attribute__((aligned(16))) float xch[UNIT_CH * 2 * WAVES];
   const int h = blockIdx.x / APPEND_UNITS, unit = blockIdx.x % APPEND_UNITS;
   const int64_t pos = *a.pos_dev;
   if (pos < 0 || pos >= a.capacity) return;  // a position outside the cache appends nothing
@@ -923,18 +940,22 @@ static int check_heads(int64_t hq, int64_t hkv, int64_t head_dim) {
 }
 
 // Kernel A over n_parts prefix parts (none when n_parts == 0), then kernel B.
-static int launch_attn(AttnArgs& a, int64_t n_parts, int64_t workspace_bytes, hipStream_t s, const char* what) {
+constexpr int LAUNCH_PREFIX = 1, LAUNCH_TAIL = 2;
+
+static int launch_attn(AttnArgs& a, int64_t n_parts, int64_t workspace_bytes, hipStream_t s, const char* what,
+                       int launches = LAUNCH_PREFIX | LAUNCH_TAIL) {
   if (n_parts < 0) return fail(NKV_ERR_INVALID, "%s: n_parts %lld is negative", what, (long long)n_parts);
   a.n_parts = (int)n_parts;
   const int64_t need = (int64_t)a.hkv * std::max<int64_t>(1, n_parts) * part_floats(a.hq, a.hkv) * (int64_t)sizeof(float);
   if (n_parts > 0 && workspace_bytes < need)
     return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
   if (n_parts > 256) return fail(NKV_ERR_UNSUPPORTED, "%s: n_parts %lld exceeds the 256 partials the merge holds", what, (long long)n_parts);
-  if (n_parts > 0) {
+  if (n_parts > 0 && (launches & LAUNCH_PREFIX)) {
     const int64_t parts = a.tail_mode == TAIL_FUSED ? std::max<int64_t>(n_parts, APPEND_UNITS) : n_parts;
     hipLaunchKernelGGL(attn_prefix_kernel, dim3((unsigned)(a.hkv * parts)), dim3(THREADS), 0, s, a);
     if (int rc = check_launch(what)) return rc;
   }
+  if (!(launches & LAUNCH_TAIL)) return NKV_OK;
   hipLaunchKernelGGL(attn_tail_kernel, dim3((unsigned)a.hkv), dim3(TB_THREADS), 0, s, a);
   return check_launch(what);
 }
@@ -1018,7 +1039,7 @@ extern "C" int nkv_append_t64(const uint16_t* k_new, const uint16_t* v_new, int6
   return check_launch("append_t64");
 }
 
-extern "C" int nkv_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+static int decode_step(const char* what, int launches, const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                                    int64_t kv_head_stride, uint8_t* kq, uint16_t* kmn, uint16_t* kst,
                                    uint8_t* vq, uint16_t* vmn, uint16_t* vst, uint16_t* tail_k,
                                    uint16_t* tail_v, const int64_t* pos_dev, const int64_t* first_dev,
@@ -1031,10 +1052,10 @@ extern "C" int nkv_decode_step_t64(const uint16_t* q, const uint16_t* k_new, con
   if (capacity <= 0) return fail(NKV_ERR_INVALID, "capacity must be positive");
   if (!q || !k_new || !v_new || !kq || !kmn || !kst || !vq || !vmn || !vst || !tail_k || !tail_v ||
       !pos_dev || !written_dev || !qlen_dev || !pg_dev || !out || !workspace)
-    return fail(NKV_ERR_INVALID, "decode_step: null pointer argument");
+    return fail(NKV_ERR_INVALID, "%s: null pointer argument", what);
   if (!al16(q) || !al16(k_new) || !al16(v_new) || kv_head_stride % 8 || !al16(tail_k) || !al16(tail_v) ||
       !al16(kq) || !al16(vq) || !al16(kmn) || !al16(kst) || !al16(vmn) || !al16(vst) || !al16(workspace))
-    return fail(NKV_ERR_UNSUPPORTED, "decode_step: buffers must be 16-byte aligned");
+    return fail(NKV_ERR_UNSUPPORTED, "%s: buffers must be 16-byte aligned", what);
   const int64_t ngroups = cdiv(capacity, GT);
   if (n_parts <= 0) n_parts = default_parts(hkv, ngroups);
   AttnArgs a{};
@@ -1047,7 +1068,46 @@ extern "C" int nkv_decode_step_t64(const uint16_t* q, const uint16_t* k_new, con
   a.tail_mode = TAIL_FUSED;
   a.sl2 = LOG2E / sqrtf((float)head_dim);
   a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace);
-  return launch_attn(a, n_parts, workspace_bytes, static_cast<hipStream_t>(stream), "decode_step_t64");
+  return launch_attn(a, n_parts, workspace_bytes, static_cast<hipStream_t>(stream), what, launches);
+}
+
+extern "C" int nkv_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                                   int64_t kv_head_stride, uint8_t* kq, uint16_t* kmn, uint16_t* kst,
+                                   uint8_t* vq, uint16_t* vmn, uint16_t* vst, uint16_t* tail_k,
+                                   uint16_t* tail_v, const int64_t* pos_dev, const int64_t* first_dev,
+                                   int64_t* written_dev, int64_t* qlen_dev, int64_t* pg_dev, int64_t hq,
+                                   int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out,
+                                   float* lse_out, void* workspace, int64_t workspace_bytes,
+                                   int64_t n_parts, void* stream) {
+  return decode_step("decode_step_t64", LAUNCH_PREFIX | LAUNCH_TAIL, q, k_new, v_new, kv_head_stride, kq, kmn, kst, vq, vmn, vst, tail_k, tail_v, pos_dev, first_dev,
+                     written_dev, qlen_dev, pg_dev, hq, hkv, head_dim, capacity, out, lse_out, workspace,
+                     workspace_bytes, n_parts, stream);
+}
+
+extern "C" int nkv_decode_step_partials_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                                   int64_t kv_head_stride, uint8_t* kq, uint16_t* kmn, uint16_t* kst,
+                                   uint8_t* vq, uint16_t* vmn, uint16_t* vst, uint16_t* tail_k,
+                                   uint16_t* tail_v, const int64_t* pos_dev, const int64_t* first_dev,
+                                   int64_t* written_dev, int64_t* qlen_dev, int64_t* pg_dev, int64_t hq,
+                                   int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out,
+                                   float* lse_out, void* workspace, int64_t workspace_bytes,
+                                   int64_t n_parts, void* stream) {
+  return decode_step("decode_step_partials_t64", LAUNCH_PREFIX, q, k_new, v_new, kv_head_stride, kq, kmn, kst, vq, vmn, vst, tail_k, tail_v, pos_dev, first_dev,
+                     written_dev, qlen_dev, pg_dev, hq, hkv, head_dim, capacity, out, lse_out, workspace,
+                     workspace_bytes, n_parts, stream);
+}
+
+extern "C" int nkv_decode_step_combine_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                                   int64_t kv_head_stride, uint8_t* kq, uint16_t* kmn, uint16_t* kst,
+                                   uint8_t* vq, uint16_t* vmn, uint16_t* vst, uint16_t* tail_k,
+                                   uint16_t* tail_v, const int64_t* pos_dev, const int64_t* first_dev,
+                                   int64_t* written_dev, int64_t* qlen_dev, int64_t* pg_dev, int64_t hq,
+                                   int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out,
+                                   float* lse_out, void* workspace, int64_t workspace_bytes,
+                                   int64_t n_parts, void* stream) {
+  return decode_step("decode_step_combine_t64", LAUNCH_TAIL, q, k_new, v_new, kv_head_stride, kq, kmn, kst, vq, vmn, vst, tail_k, tail_v, pos_dev, first_dev,
+                     written_dev, qlen_dev, pg_dev, hq, hkv, head_dim, capacity, out, lse_out, workspace,
+                     workspace_bytes, n_parts, stream);
 }
 
 extern "C" int nkv_tail_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v,

@@ -520,20 +520,25 @@ class KVInt8Cache:
         if self.staging is not None:
             self.update(key, value, layer_idx)
             return self.attend_prefill(query, layer_idx)
+        _lib.call("nkv_decode_step_t64", *self.step_args(key, value, query, layer_idx))
+        return self.merged
+
+    def step_args(self, key: torch.Tensor, value: torch.Tensor, query: torch.Tensor, layer_idx: int) -> tuple:
+        """Arguments of the decode-step entry points (``nkv_decode_step_t64`` and its two
+        halves ``_partials`` / ``_combine``) for one decode token of layer ``layer_idx``
+        on the current stream. The tensors must stay alive until the launch completes."""
         if key.shape[2] != 1:
             raise RuntimeError("没有暂存区时只支持解码一步（n == 1）；prefill 请先 `begin_prefill()`")
         k, v = self._token(key, "key"), self._token(value, "value")
         q = self._q(query)
-        _lib.call(
-            "nkv_decode_step_t64", q.data_ptr(), k.data_ptr(), v.data_ptr(), k.stride(1),
-            self.kq[layer_idx].data_ptr(), self.kmn[layer_idx].data_ptr(), self.kst[layer_idx].data_ptr(),
-            self.vq[layer_idx].data_ptr(), self.vmn[layer_idx].data_ptr(), self.vst[layer_idx].data_ptr(),
-            self.tail_k[layer_idx].data_ptr(), self.tail_v[layer_idx].data_ptr(), self.pos.data_ptr(),
-            self.first.data_ptr(), self._written.data_ptr(), self._qlen.data_ptr(), self._pg.data_ptr(),
-            self.num_q_heads, self.num_kv_heads, self.head_dim, self.max_len, self.merged.data_ptr(),
-            self.lse.data_ptr(), self.pa.data_ptr(), self._ws_bytes, self._n_parts,
-            _lib.stream_ptr(self.pos.device))
-        return self.merged
+        return (q.data_ptr(), k.data_ptr(), v.data_ptr(), k.stride(1),
+                self.kq[layer_idx].data_ptr(), self.kmn[layer_idx].data_ptr(), self.kst[layer_idx].data_ptr(),
+                self.vq[layer_idx].data_ptr(), self.vmn[layer_idx].data_ptr(), self.vst[layer_idx].data_ptr(),
+                self.tail_k[layer_idx].data_ptr(), self.tail_v[layer_idx].data_ptr(), self.pos.data_ptr(),
+                self.first.data_ptr(), self._written.data_ptr(), self._qlen.data_ptr(), self._pg.data_ptr(),
+                self.num_q_heads, self.num_kv_heads, self.head_dim, self.max_len, self.merged.data_ptr(),
+                self.lse.data_ptr(), self.pa.data_ptr(), self._ws_bytes, self._n_parts,
+                _lib.stream_ptr(self.pos.device))
 
     # ---- memory accounting
 

@@ -267,6 +267,38 @@ def test_fused_equals_two_calls():
         assert_ulp_or_abs(npy(ob)[0, :, 0], npy(oa)[0, :, 0].astype(np.float64), MAX_ULP, ABS_TOL, f"p={p}")
 
 
+def test_partials_then_combine_equals_fused_step():
+    """The decode step's two launches called one by one (``nkv_decode_step_partials_t64``
+    then ``nkv_decode_step_combine_t64``) give the fused call's state and output bit for
+    bit, across a group boundary and with more parts than groups."""
+    from nova_amd import _lib
+
+    used0 = 190
+    _, k, v = make(used0 + 70, seed=37)
+    q = randn((1, HQ, 1, D), 38).cuda()
+    k, v = k.cuda(), v.cuda()
+    a, b = _cache(max_len=320), _cache(max_len=320)
+    for c in (a, b):
+        c.begin_prefill(used0)
+        c.set_prefill_pos(0)
+        c.update(k[:, :, :used0], v[:, :, :used0], 0)
+        c.finish_prefill(used0)
+    for p in range(used0, used0 + 70):
+        a.pos.fill_(p)
+        b.pos.fill_(p)
+        oa = a.update_attend(k[:, :, p:p + 1], v[:, :, p:p + 1], q, 0).clone()
+        args = b.step_args(k[:, :, p:p + 1], v[:, :, p:p + 1], q, 0)
+        _lib.call("nkv_decode_step_partials_t64", *args)
+        _lib.call("nkv_decode_step_combine_t64", *args)
+        ob = b.merged.clone()
+        for nm in ("kq", "vq", "kmn", "kst", "vmn", "vst", "tail_k", "tail_v"):
+            assert torch.equal(getattr(a, nm)[0], getattr(b, nm)[0]), (p, nm)
+        for nm in ("_written", "_qlen", "_pg"):
+            assert torch.equal(getattr(a, nm), getattr(b, nm)), (p, nm)
+        assert torch.equal(oa, ob), p
+        assert torch.equal(a.lse, b.lse), p
+
+
 def test_streaming_decode_4096_steps_against_oracle():
     """One layer: prefill 512, then 4096 fused append+attend steps (q ~ N(0,1)/sqrt(128)).
     The cache state equals the oracle's bit for bit at the end; outputs are checked
