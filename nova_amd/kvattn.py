@@ -2,8 +2,9 @@
 
 Public surface and error behaviour follow src/nova/kvattn.py: ``GROUP_T``, ``CHUNK``,
 ``PAD_M``, ``int8_attn_decode``, ``pack_int8_kv``, ``tail_attend`` and ``KVInt8Cache``.
-Every computation runs in the HIP kernels of ``libnova_kv.so`` (one launch per call;
-one launch per layer for the fused ``KVInt8Cache.update_attend``). ValueError messages
+Every computation runs in the HIP kernels of ``libnova_kv.so``: decode attention is two
+launches (the split-K prefix kernel, then the tail kernel with the ring and the combine),
+and the fused ``KVInt8Cache.update_attend`` runs the append inside the first of them. ValueError messages
 keep the reference's key terms (解码一步, chunk, group, used, 尺子) so callers that
 match on them keep working.
 
@@ -496,7 +497,7 @@ class KVInt8Cache:
 
     def attend(self, query: torch.Tensor, layer_idx: int) -> torch.Tensor:
         """Decode-step attention over the int8 prefix and the valid ring slots, one
-        softmax, one HIP launch; writes and returns ``merged`` (``lse`` holds the
+        softmax (one ``nkv_attn_decode_t64`` call); writes and returns ``merged`` (``lse`` holds the
         log-sum-exp). No host sync — lengths come from ``_qlen`` / ``_pg`` / ``_written``."""
         q = self._q(query)
         _lib.call(
@@ -511,7 +512,7 @@ class KVInt8Cache:
 
     def update_attend(self, key: torch.Tensor, value: torch.Tensor, query: torch.Tensor,
                       layer_idx: int) -> torch.Tensor:
-        """``update()`` + ``attend()`` of one decode token in a single HIP launch.
+        """``update()`` + ``attend()`` of one decode token in one ``nkv_decode_step_t64`` call.
 
         Same cache state and scalars as the two calls; the output equals ``attend()``'s up
         to float summation order. During prefill (staging present) it falls back to the
