@@ -4,7 +4,7 @@ Mirrors ``GraphDecoder`` (src/nova/decode.py:87-526) for the KV paths this packa
 builds: one hipGraph replay per generated token, the whole step (embed -> layers ->
 lm_head -> argmax written back into ``input_ids`` -> ``pos += 1``) inside the graph,
 no host sync inside. With ``quant="int8"`` the cache is :class:`KVInt8Cache` and every
-layer's attention is one HIP launch. Capacity buckets and the O(max_len) mask row
+layer's attention is one ``update_attend`` call (two HIP launches). Capacity buckets and the O(max_len) mask row
 follow ``decode.py:39-48,200-205``. Sliding-window layers and memory injection are
 not part of this path.
 """

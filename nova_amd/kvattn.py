@@ -246,9 +246,10 @@ class KVInt8Cache:
     1. ``update()``: one HIP launch writes K/V into ring slot ``pos % 64``, requantizes
        the whole ring into ruler group ``pos // 64`` and sets ``_written = pos + 1``,
        ``_qlen = 64 * floor(_written / 64)``, ``_pg = _qlen / 64``;
-    2. ``attend()``: one HIP launch attends over the int8 prefix ``[0, _qlen)`` and the
-       valid ring slots in a single softmax.
-    ``update_attend()`` does both in one launch (what the decode loop uses).
+    2. ``attend()``: two HIP launches (split-K partials, then ring + combine) attend over
+       the int8 prefix ``[0, _qlen)`` and the valid ring slots in a single softmax.
+    ``update_attend()`` does both in those two launches, the append running inside the
+    first (what the decode loop uses).
 
     Prefill goes through an fp16 staging area sized to the prompt (``begin_prefill``),
     then ``finish_prefill`` quantizes whole groups with the bulk HIP quantizer, fills the
