@@ -43,6 +43,9 @@ namespace nkv {
 #ifndef NKV_STAGES
 #define NKV_STAGES 1
 #endif
+#ifndef NKV_HALF
+#define NKV_HALF 1  // stream half groups (32 tokens) through two LDS slots per wave
+#endif
 
 constexpr int D = 128;
 constexpr int GT = 64;              // tokens per ruler group == ring slots
@@ -52,7 +55,13 @@ constexpr int STAGES = NKV_STAGES;  // LDS buffers per wave
 constexpr int CODE_BYTES = GT * D;                        // one tensor's codes of one group
 constexpr int RULER_BYTES = 4 * D * 2;                    // kst, kmn, vst, vmn of one group
 constexpr int STAGE_BYTES = 2 * CODE_BYTES + RULER_BYTES;  // 17 KiB
-constexpr int LDS_BYTES = WAVES * STAGES * STAGE_BYTES;   // 136 KiB
+constexpr int HALF_CODE = 32 * D;                          // one tensor's codes of a half group
+constexpr int HALF_SLOT = 2 * HALF_CODE;                   // K | V codes of a half group
+constexpr int WAVE_HALF_BYTES = 2 * HALF_SLOT + 2 * RULER_BYTES;  // two slots + two ruler sets
+constexpr int WAVE_LDS = NKV_HALF ? WAVE_HALF_BYTES : STAGES * STAGE_BYTES;
+constexpr int LDS_BYTES = WAVES * WAVE_LDS;                // 144 KiB (half groups) / 136 KiB
+constexpr int DMA_FIRST_HALF = 2 * (HALF_CODE / 1024) + 4; // with the group's rulers
+constexpr int DMA_SECOND_HALF = 2 * (HALF_CODE / 1024);
 constexpr int RING_BYTES = GT * D * 2;                    // one fp16 ring tensor of one head
 constexpr int DMA_PER_GROUP = 2 * (CODE_BYTES / 1024) + 4;
 constexpr float P_SCALE = 32768.0f;       // 2^15
@@ -239,6 +248,41 @@ __device__ __forceinline__ void issue_group(const AttnArgs& a, int h, int64_t gr
   if (which == 3) dma16(uniform_ptr(a.vmn + ro), roff, st + 2 * CODE_BYTES);
 }
 
+// Issue the loads of half `hf` (tokens 32 hf .. 32 hf + 31) of group `grp` of head h: 32
+// K and 32 V code rows (4 + 4 loads) into the slot at `slot` (K codes, then V codes), and
+// for hf == 0 the group's rulers (4 loads) into `rs`. Rows are swizzled as in a full
+// stage; token rows at or beyond the capacity are never read (the last row is repeated).
+__device__ __forceinline__ void issue_half(const AttnArgs& a, int h, int64_t grp, int hf, uint32_t slot, uint32_t rs) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t0 = grp * GT + 32 * hf;
+  const void* kb = uniform_ptr(a.kq + (int64_t)h * a.capacity * D);
+  const void* vb = uniform_ptr(a.vq + (int64_t)h * a.capacity * D);
+  slot = __builtin_amdgcn_readfirstlane(slot);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // earlier reads of this slot are done
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    const uint32_t off = (uint32_t)(min<int64_t>(t0 + row, a.capacity - 1) * D) + (((lane & 7) ^ swz(row)) << 4);
+    dma16(kb, off, slot + 1024 * j);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    const uint32_t off = (uint32_t)(min<int64_t>(t0 + row, a.capacity - 1) * D) + (((lane & 7) ^ swz(row)) << 4);
+    dma16(vb, off, slot + HALF_CODE + 1024 * j);
+  }
+  if (hf == 0) {
+    rs = __builtin_amdgcn_readfirstlane(rs);
+    const int64_t ro = ((int64_t)h * a.ngroups_cap + grp) * D;
+    const uint32_t roff = (uint32_t)(8 * (lane & 15)) * 2;
+    const int which = lane >> 4;
+    if (which == 0) dma16(uniform_ptr(a.kst + ro), roff, rs);
+    if (which == 1) dma16(uniform_ptr(a.kmn + ro), roff, rs);
+    if (which == 2) dma16(uniform_ptr(a.vst + ro), roff, rs);
+    if (which == 3) dma16(uniform_ptr(a.vmn + ro), roff, rs);
+  }
+}
+
 // Q of KV head h (gq rows of 256 bytes) into LDS at `dst`, by one wave.
 __device__ __forceinline__ void issue_q(const AttnArgs& a, int h, uint32_t dst) {
   const int lane = threadIdx.x & 63;
@@ -267,12 +311,13 @@ __device__ __forceinline__ void wait_groups_all() { asm volatile("s_waitcnt vmcn
 // Online-softmax update with the 16 masked scores s[b][i] (token 16b + 4g + i, head c);
 // returns P of token blocks (0,1) and (2,3) split into hi/lo fp16 A operands and
 // rescales the accumulator when a running maximum moved.
-__device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[4][4], half8_t (&phi)[2],
-                                             half8_t (&plo)[2], int gq) {
+template <int NB>
+__device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[2 * NB][4], half8_t (&phi)[NB],
+                                             half8_t (&plo)[NB], int gq) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
   float mloc = NEG_INF;
 #pragma unroll
-  for (int b = 0; b < 4; ++b)
+  for (int b = 0; b < 2 * NB; ++b)
 #pragma unroll
     for (int i = 0; i < 4; ++i) mloc = fmaxf(mloc, s[b][i]);
   mloc = max4rows(mloc);
@@ -280,9 +325,9 @@ __device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[4][4], ha
   const float m_use = m_new == NEG_INF ? 0.0f : m_new;
   const float alpha = __builtin_amdgcn_exp2f(st.m - m_use);
   float lsum = 0.0f;
-  _Float16 hi[2][8], lo[2][8];
+  _Float16 hi[NB][8], lo[NB][8];
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
+  for (int b = 0; b < 2 * NB; ++b) {
     float q[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -301,7 +346,7 @@ __device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[4][4], ha
     }
   }
 #pragma unroll
-  for (int B = 0; B < 2; ++B) {
+  for (int B = 0; B < NB; ++B) {
     phi[B] = half8_t{hi[B][0], hi[B][1], hi[B][2], hi[B][3], hi[B][4], hi[B][5], hi[B][6], hi[B][7]};
     plo[B] = half8_t{lo[B][0], lo[B][1], lo[B][2], lo[B][3], lo[B][4], lo[B][5], lo[B][6], lo[B][7]};
   }
@@ -330,11 +375,14 @@ __device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[4][4], ha
   }
 }
 
-// One 64-token int8 group resident in an LDS stage, `nvalid` of its tokens valid.
-__device__ __forceinline__ void attend_stage(const AttnArgs& a, WaveState& st, const half8_t (&qb)[4],
-                                             const uint8_t* stage, int nvalid) {
+// 32 NB tokens of one int8 group resident in LDS: K codes at `kc`, V codes at `vc` (rows of
+// 128 bytes, chunks swizzled by swz(row)), the group's rulers at `rul` (kst | kmn | vst |
+// vmn, 128 fp16 each); `nvalid` of the tokens are valid.
+template <int NB>
+__device__ __forceinline__ void attend_block(const AttnArgs& a, WaveState& st, const half8_t (&qb)[4],
+                                             const uint8_t* kc, const uint8_t* vc, const uint8_t* rul, int nvalid) {
   const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-  const uint16_t* rks = reinterpret_cast<const uint16_t*>(stage + 2 * CODE_BYTES);
+  const uint16_t* rks = reinterpret_cast<const uint16_t*>(rul);
   const uint16_t* rkm = rks + D;
   const uint16_t* rvs = rks + 2 * D;
   const uint16_t* rvm = rks + 3 * D;
@@ -348,27 +396,27 @@ __device__ __forceinline__ void attend_stage(const AttnArgs& a, WaveState& st, c
       kst4[hh][e] = *reinterpret_cast<const uint4*>(rks + 16 * g + 64 * hh + 8 * e);
       kmn4[hh][e] = *reinterpret_cast<const uint4*>(rkm + 16 * g + 64 * hh + 8 * e);
     }
-  float4_t S[4];
+  float4_t S[2 * NB];
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
+  for (int b = 0; b < 2 * NB; ++b) {
     S[b] = float4_t{0.f, 0.f, 0.f, 0.f};
     const int row = 16 * b + c;
     const int key = swz(row);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
-      const uint4 kw = *reinterpret_cast<const uint4*>(stage + row * D + (((g + 4 * hh) ^ key) << 4));
+      const uint4 kw = *reinterpret_cast<const uint4*>(kc + row * D + (((g + 4 * hh) ^ key) << 4));
       S[b] = mfma32(dq8(kw.x, kw.y, kst4[hh][0], kmn4[hh][0]), qb[2 * hh], S[b]);
       S[b] = mfma32(dq8(kw.z, kw.w, kst4[hh][1], kmn4[hh][1]), qb[2 * hh + 1], S[b]);
     }
   }
-  float s[4][4];
+  float s[2 * NB][4];
 #pragma unroll
-  for (int b = 0; b < 4; ++b)
+  for (int b = 0; b < 2 * NB; ++b)
 #pragma unroll
     for (int i = 0; i < 4; ++i) s[b][i] = (16 * b + 4 * g + i) < nvalid ? S[b][i] * a.sl2 : NEG_INF;
 
-  half8_t phi[2], plo[2];
-  softmax_step(st, s, phi, plo, a.gq);
+  half8_t phi[NB], plo[NB];
+  softmax_step<NB>(st, s, phi, plo, a.gq);
 
   // ---- O += P V. Lane (c, g) of a transpose read supplies row k(g, c >> 1) and half
   // (c & 1) of the 16-dim chunk; it receives dim 16cb + c of the 8 tokens k(g, 0..7),
@@ -383,13 +431,13 @@ __device__ __forceinline__ void attend_stage(const AttnArgs& a, WaveState& st, c
   }
   const int r = c >> 1;
 #pragma unroll
-  for (int B = 0; B < 2; ++B) {
+  for (int B = 0; B < NB; ++B) {
     const int row = 16 * (2 * B + (r >> 2)) + 4 * g + (r & 3);
     const int key = swz(row);
-    const uint8_t* rowp = stage + CODE_BYTES + row * D + 8 * (c & 1);
+    const uint8_t* rowp = vc + row * D + 8 * (c & 1);
     // invalid tokens of a partial group get code 0 (finite value, weight 0)
     u32x2 keep = {~0u, ~0u};
-    if (nvalid < GT) {
+    if (nvalid < 32 * NB) {
       uint32_t m[2] = {0u, 0u};
 #pragma unroll
       for (int rr = 0; rr < 8; ++rr) {
@@ -407,6 +455,12 @@ __device__ __forceinline__ void attend_stage(const AttnArgs& a, WaveState& st, c
       st.acc[cb] = mfma32(plo[B], vb, st.acc[cb]);
     }
   }
+}
+
+// One whole 64-token group resident in a full LDS stage (K codes, V codes, rulers).
+__device__ __forceinline__ void attend_stage(const AttnArgs& a, WaveState& st, const half8_t (&qb)[4],
+                                             const uint8_t* stage, int nvalid) {
+  attend_block<2>(a, st, qb, stage, stage + CODE_BYTES, stage + 2 * CODE_BYTES, nvalid);
 }
 
 // Online-softmax update with the 4 masked scores s[i] (token 4g + i of a 16-token block,
@@ -686,7 +740,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.x % a.hkv;
   const int part = blockIdx.x / a.hkv;
-  uint8_t* my_stages = lds_raw + wave * STAGES * STAGE_BYTES;
+  uint8_t* my_stages = lds_raw + wave * WAVE_LDS;
   const uint32_t my_lds = __builtin_amdgcn_readfirstlane(lds_addr(my_stages));
   const uint32_t src_lds = __builtin_amdgcn_readfirstlane(lds_addr(unit_src));
 
@@ -704,6 +758,18 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   // leaves the groups in flight
   if (wave == 0 && prefix) issue_q(a, h, __builtin_amdgcn_readfirstlane(lds_addr(q_lds)));
   if (wave == 0 && append) issue_unit_rows(a, h, part, src_lds);
+#if NKV_HALF
+  // this wave's half groups u = 0 .. 2n - 1: group gs + wave + 8 (u >> 1), half u & 1, in
+  // slot u & 1; rulers of its i-th group in ruler set i & 1
+  const uint32_t rul_lds = my_lds + 2 * HALF_SLOT;
+  if (n > 0) {
+    issue_half(a, h, gs + wave, 0, my_lds, rul_lds);
+    issue_half(a, h, gs + wave, 1, my_lds + HALF_SLOT, rul_lds);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF + DMA_SECOND_HALF) : "memory");
+  } else {
+    wait_groups_all();
+  }
+#else
 #pragma unroll
   for (int s0 = 0; s0 < STAGES; ++s0)
     if (s0 < n) issue_group(a, h, gs + wave + (int64_t)s0 * WAVES, my_lds + s0 * STAGE_BYTES);
@@ -711,6 +777,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   if (in_flight == 0) wait_groups_all();
   else if (in_flight == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_PER_GROUP) : "memory");
   else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_PER_GROUP) : "memory");
+#endif
   __syncthreads();
 
   if (append) {
@@ -723,6 +790,22 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   half8_t qb[4];
   load_q_lds(q_lds, a.gq, qb);
 
+#if NKV_HALF
+  for (int u = 0; u < 2 * n; ++u) {
+    const int hf = u & 1, i = u >> 1;
+    // wait for half u; half u + 1 (issued after it) may stay in flight
+    if (u + 1 == 2 * n) wait_groups_all();
+    else if (hf == 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_SECOND_HALF) : "memory");
+    else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF) : "memory");
+    const int64_t grp = gs + wave + (int64_t)i * WAVES;
+    const int nvalid = (int)min<int64_t>(32, U - grp * GT - 32 * hf);
+    const uint8_t* slot = my_stages + hf * HALF_SLOT;
+    if (nvalid > 0)
+      attend_block<1>(a, st, qb, slot, slot + HALF_CODE, my_stages + 2 * HALF_SLOT + (i & 1) * RULER_BYTES, nvalid);
+    if (u + 2 < 2 * n)
+      issue_half(a, h, grp + WAVES, hf, my_lds + hf * HALF_SLOT, rul_lds + ((i + 1) & 1) * RULER_BYTES);
+  }
+#else
   for (int i = 0; i < n; ++i) {
     if (STAGES > 1 && i + 1 < n) wait_groups_all_but_one();
     else wait_groups_all();
@@ -732,6 +815,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
     attend_stage(a, st, qb, my_stages + sidx * STAGE_BYTES, nvalid);
     if (i + STAGES < n) issue_group(a, h, grp + STAGES * WAVES, my_lds + sidx * STAGE_BYTES);
   }
+#endif
 
   // ---- merge the waves through LDS (the stages are dead once every wave is here)
   __syncthreads();
@@ -950,6 +1034,8 @@ static int launch_attn(AttnArgs& a, int64_t n_parts, int64_t workspace_bytes, hi
   if (n_parts > 0 && workspace_bytes < need)
     return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
   if (n_parts > 256) return fail(NKV_ERR_UNSUPPORTED, "%s: n_parts %lld exceeds the 256 partials the merge holds", what, (long long)n_parts);
+  if (a.capacity > (int64_t(1) << 24))  // code row offsets of one head stay 32-bit
+    return fail(NKV_ERR_UNSUPPORTED, "%s: capacity %lld exceeds 16M tokens", what, (long long)a.capacity);
   if (n_parts > 0 && (launches & LAUNCH_PREFIX)) {
     const int64_t parts = a.tail_mode == TAIL_FUSED ? std::max<int64_t>(n_parts, APPEND_UNITS) : n_parts;
     hipLaunchKernelGGL(attn_prefix_kernel, dim3((unsigned)(a.hkv * parts)), dim3(THREADS), 0, s, a);
