@@ -735,8 +735,9 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t unit_src[UNIT_SRC_BYTES / 2];
   __shared__ __attribute__((aligned(16))) uint16_t q_lds[16 * D];
   __shared__ __attribute__((aligned(16))) float xch[UNIT_CH * 2 * WAVES];
+  __shared__ int next_group;
   float* lds = reinterpret_cast<float*>(lds_raw);
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.x % a.hkv;
   const int part = blockIdx.x / a.hkv;
@@ -759,10 +760,14 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   if (wave == 0 && prefix) issue_q(a, h, __builtin_amdgcn_readfirstlane(lds_addr(q_lds)));
   if (wave == 0 && append) issue_unit_rows(a, h, part, src_lds);
 #if NKV_HALF
-  // this wave's half groups u = 0 .. 2n - 1: group gs + wave + 8 (u >> 1), half u & 1, in
-  // slot u & 1; rulers of its i-th group in ruler set i & 1
+  // Groups gs + gi, gi < ng, are handed out to the waves one at a time: wave w starts with
+  // gi = w, and a wave claims the next one from `next_group` once the first half of its
+  // current group is done, so waves whose loads arrive early take more groups. A group's
+  // halves go to slots 0 and 1, its rulers to the wave's ruler set (alternating).
+  const int ng = (int)(ge - gs);
   const uint32_t rul_lds = my_lds + 2 * HALF_SLOT;
-  if (n > 0) {
+  if (tid == 0) next_group = WAVES;
+  if (wave < ng) {
     issue_half(a, h, gs + wave, 0, my_lds, rul_lds);
     issue_half(a, h, gs + wave, 1, my_lds + HALF_SLOT, rul_lds);
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF + DMA_SECOND_HALF) : "memory");
@@ -791,19 +796,24 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   load_q_lds(q_lds, a.gq, qb);
 
 #if NKV_HALF
-  for (int u = 0; u < 2 * n; ++u) {
-    const int hf = u & 1, i = u >> 1;
-    // wait for half u; half u + 1 (issued after it) may stay in flight
-    if (u + 1 == 2 * n) wait_groups_all();
-    else if (hf == 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_SECOND_HALF) : "memory");
-    else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF) : "memory");
-    const int64_t grp = gs + wave + (int64_t)i * WAVES;
-    const int nvalid = (int)min<int64_t>(32, U - grp * GT - 32 * hf);
-    const uint8_t* slot = my_stages + hf * HALF_SLOT;
-    if (nvalid > 0)
-      attend_block<1>(a, st, qb, slot, slot + HALF_CODE, my_stages + 2 * HALF_SLOT + (i & 1) * RULER_BYTES, nvalid);
-    if (u + 2 < 2 * n)
-      issue_half(a, h, grp + WAVES, hf, my_lds + hf * HALF_SLOT, rul_lds + ((i + 1) & 1) * RULER_BYTES);
+  int gi = wave;
+  for (int rs = 0; gi < ng; rs ^= 1) {
+    const int64_t grp = gs + gi;
+    const uint8_t* rul = my_stages + 2 * HALF_SLOT + rs * RULER_BYTES;
+    // first half (slot 0); the second half, issued after it, may stay in flight
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_SECOND_HALF) : "memory");
+    attend_block<1>(a, st, qb, my_stages, my_stages + HALF_CODE, rul, (int)min<int64_t>(32, U - grp * GT));
+    int nx = 0;
+    if (lane == 0) nx = __hip_atomic_fetch_add(&next_group, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    nx = __builtin_amdgcn_readfirstlane(nx);
+    if (nx < ng) issue_half(a, h, gs + nx, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
+    // second half (slot 1)
+    if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF) : "memory");
+    else wait_groups_all();
+    const int nv2 = (int)min<int64_t>(32, U - grp * GT - 32);
+    if (nv2 > 0) attend_block<1>(a, st, qb, my_stages + HALF_SLOT, my_stages + HALF_SLOT + HALF_CODE, rul, nv2);
+    if (nx < ng) issue_half(a, h, gs + nx, 1, my_lds + HALF_SLOT, 0u);
+    gi = nx;
   }
 #else
   for (int i = 0; i < n; ++i) {
