@@ -851,8 +851,7 @@ constexpr int TB_WAVES = 8;
 constexpr int TB_THREADS = 64 * TB_WAVES;
 constexpr int MERGE_CHUNK = 32;  // partial slots per column loaded up front
 constexpr int RING_PARTS = 4;    // the ring's 64 tokens as 4 partials of 16
-constexpr int WT_STRIDE = 256 + RING_PARTS + 4;
-static_assert(MERGE_CHUNK + RING_PARTS <= WT_STRIDE && WT_STRIDE % 4 == 0, "merge weight rows");
+constexpr int WT_STRIDE = 256;  // partials one merge holds
 
 // One workgroup per KV head, after the prefix kernel: attends over the ring (or the group
 // the token completed), then merges the prefix partials and the ring's partials by
@@ -862,9 +861,9 @@ static_assert(MERGE_CHUNK + RING_PARTS <= WT_STRIDE && WT_STRIDE % 4 == 0, "merg
 __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t ring_lds[2 * RING_BYTES];          // K | V values
   __shared__ __attribute__((aligned(16))) float ring_part[RING_PARTS][16 * D + 32];  // the ring's partials
-  __shared__ float wts[(256 + RING_PARTS) * 16], lsv[(256 + RING_PARTS) * 16];
-  __shared__ __attribute__((aligned(16))) float wT[16][WT_STRIDE];  // merge weights [head][partial], 0-padded
-  __shared__ float mh[16], lh[16];
+  __shared__ __attribute__((aligned(16))) float pre_acc[16 * D];  // prefix: sum_s w_s acc_s per column
+  __shared__ float pre_m[16], pre_l[16];                           // prefix: max_s m_s, sum_s w_s l_s
+  __shared__ __attribute__((aligned(16))) float wbuf[TB_WAVES][WT_STRIDE];  // one head's w_s per wave
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = blockIdx.x;
   const int gq = a.gq, pw = part_stride(gq), P = a.n_parts, cols = gq * D;
@@ -874,9 +873,13 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
   bool pos_ok;
   const int64_t U = prefix_limit(a, pos, pos_ok);
   const bool ring = a.tail_mode != TAIL_NONE && (!fused || pos_ok);
+  // while waves 0..3 attend over the ring, the others merge the prefix partials
+  const int mbase = ring ? RING_PARTS : 0, nmw = TB_WAVES - mbase;
+  const bool merger = wave >= mbase;
 
-  // ---- every load up front: ring quarters (or the completed group), `first`, the mask, q,
-  // m / l and a column of the partials
+  // ---- every load up front: ring quarters (or the completed group), `first`, the mask, q;
+  // for a merging wave the m / l of its first head's partials (lane s) and its two columns
+  // (2 lane, 2 lane + 1) of the first MERGE_CHUNK partials
   const int which = wave >> 2, qtr = wave & 3;
   const bool completes = fused && pos_ok && (pos + 1) % GT == 0;  // the token completed its group
   RingQuarter rq;
@@ -896,97 +899,111 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
   half8_t qb[4];
   if (ring && wave < RING_PARTS) load_q(a, h, qb);
   const float* hws = a.ws + (int64_t)h * P * pw;
-  float ml[2] = {NEG_INF, 0.0f};  // m / l of partial (tid / gq, head tid % gq); more in the merge
-  if (tid < P * gq) {
-    const int s = tid / gq, head = tid - s * gq;
-    ml[0] = hws[(int64_t)s * pw + gq * D + head];
-    ml[1] = hws[(int64_t)s * pw + gq * D + gq + head];
-  }
-  float v[MERGE_CHUNK];
+  const int head0 = wave - mbase;
+  float m0 = NEG_INF, l0 = 0.0f;
+  float2 v0[MERGE_CHUNK];
+  if (merger && head0 < gq) {
+    if (lane < P) {
+      m0 = hws[(int64_t)lane * pw + gq * D + head0];
+      l0 = hws[(int64_t)lane * pw + gq * D + gq + head0];
+    }
 #pragma unroll
-  for (int u = 0; u < MERGE_CHUNK; ++u) v[u] = (u < P && tid < cols) ? hws[(int64_t)u * pw + tid] : 0.0f;
+    for (int u = 0; u < MERGE_CHUNK; ++u)
+      v0[u] = u < P ? *reinterpret_cast<const float2*>(hws + (int64_t)u * pw + head0 * D + 2 * lane) : float2{0.f, 0.f};
+  }
 
-  // ---- the ring (the prefix kernel did the fused step's append) into LDS, then 4 waves x
-  // 16 tokens. A token that completes its group is attended through the group's int8
-  // values, dequantized as the prefix dequantizes them.
+  // ---- the ring (the prefix kernel did the fused step's append) into LDS. A token that
+  // completes its group is attended through the group's int8 values, dequantized as the
+  // prefix dequantizes them.
   uint8_t* ring_k = ring_lds;
   uint8_t* ring_v = ring_lds + RING_BYTES;
   if (ring) {
-    const int64_t written = fused ? pos + 1 : (a.tail_mode == TAIL_SCALARS ? *a.written_dev : 0);
-    const int64_t qlen = U;
     if (completes) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) rq.rows[i] = __builtin_bit_cast(uint4, dq8(cw[i].x, cw[i].y, cst, cmn));
     }
     ring_quarter_to_lds(rq.rows, qtr, which == 0 ? ring_k : ring_v);
     __syncthreads();
-    if (wave < RING_PARTS) {
-      uint64_t bits;
-      if (completes) bits = ~0ull;
-      else if (a.tail_mode == TAIL_MASK) bits = __builtin_amdgcn_ballot_w64(mask_on);
-      else bits = ring_bits(written, qlen, first);
-      WaveState st;
-      state_init(st);
-      attend_ring16(a, st, qb, ring_k, ring_v, wave, bits);
-      store_wave_partial(st, gq, ring_part[wave]);
+  }
+  if (!merger) {
+    // ---- ring attention: 4 waves x 16 tokens, one partial each
+    const int64_t written = fused ? pos + 1 : (a.tail_mode == TAIL_SCALARS ? *a.written_dev : 0);
+    uint64_t bits;
+    if (completes) bits = ~0ull;
+    else if (a.tail_mode == TAIL_MASK) bits = __builtin_amdgcn_ballot_w64(mask_on);
+    else bits = ring_bits(written, U, first);
+    WaveState st;
+    state_init(st);
+    attend_ring16(a, st, qb, ring_k, ring_v, wave, bits);
+    store_wave_partial(st, gq, ring_part[wave]);
+  } else {
+    // ---- prefix merge, one head at a time: m_p = max_s m_s, w_s = 2^(m_s - m_p),
+    // l_p = sum_s w_s l_s, pre_acc = sum_s w_s acc_s (two columns per lane)
+    float* wb = wbuf[wave];
+    for (int head = head0; head < gq; head += nmw) {
+      const bool first_head = head == head0;
+      float m = first_head ? m0 : NEG_INF;
+      for (int s = first_head ? lane + 64 : lane; s < P; s += 64) m = fmaxf(m, hws[(int64_t)s * pw + gq * D + head]);
+      m = wave_max(m);
+      float l = 0.0f;
+      for (int s = lane; s < P; s += 64) {
+        const float ms = (first_head && s == lane) ? m0 : hws[(int64_t)s * pw + gq * D + head];
+        const float ls = (first_head && s == lane) ? l0 : hws[(int64_t)s * pw + gq * D + gq + head];
+        const float w = ms == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(ms - m);
+        wb[s] = w;
+        l += ls * w;
+      }
+      l = wave_sum(l);
+      float2 acc = {0.0f, 0.0f};
+      if (first_head) {
+#pragma unroll
+        for (int u = 0; u < MERGE_CHUNK; ++u) {
+          const float w = u < P ? wb[u] : 0.0f;
+          acc.x += v0[u].x * w;
+          acc.y += v0[u].y * w;
+        }
+      } else {
+        for (int s = 0; s < min(P, MERGE_CHUNK); ++s) {
+          const float2 vv = *reinterpret_cast<const float2*>(hws + (int64_t)s * pw + head * D + 2 * lane);
+          acc.x += vv.x * wb[s];
+          acc.y += vv.y * wb[s];
+        }
+      }
+      for (int s = MERGE_CHUNK; s < P; ++s) {
+        const float2 vv = *reinterpret_cast<const float2*>(hws + (int64_t)s * pw + head * D + 2 * lane);
+        acc.x += vv.x * wb[s];
+        acc.y += vv.y * wb[s];
+      }
+      *reinterpret_cast<float2*>(pre_acc + head * D + 2 * lane) = acc;
+      if (lane == 0) { pre_m[head] = m; pre_l[head] = l; }
     }
   }
+  __syncthreads();
 
-  // ---- merge: P prefix partials + RING_PARTS ring partials
-  if (tid < P * gq) { wts[tid] = ml[0]; lsv[tid] = ml[1]; }
-  for (int i = tid + TB_THREADS; i < P * gq; i += TB_THREADS) {
-    const int s = i / gq, head = i - s * gq;
-    wts[i] = hws[(int64_t)s * pw + gq * D + head];
-    lsv[i] = hws[(int64_t)s * pw + gq * D + gq + head];
-  }
-  __syncthreads();
-  if (tid < RING_PARTS * gq) {
-    const int r = tid / gq, head = tid - r * gq;
-    wts[(P + r) * gq + head] = ring ? ring_part[r][gq * D + head] : NEG_INF;
-    lsv[(P + r) * gq + head] = ring ? ring_part[r][gq * D + gq + head] : 0.0f;
-  }
-  __syncthreads();
-  const int ns = P + RING_PARTS;
-  for (int head = wave; head < gq; head += TB_WAVES) {
-    float m = NEG_INF;
-    for (int s = lane; s < ns; s += 64) m = fmaxf(m, wts[s * gq + head]);
-    m = wave_max(m);
-    float l = 0.0f;
-    for (int s = lane; s < WT_STRIDE; s += 64) {  // weights of every partial, 0 past the last
-      const float ms = s < ns ? wts[s * gq + head] : NEG_INF;
-      const float w = ms == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(ms - m);
-      wT[head][s] = w;
-      if (s < ns) l += lsv[s * gq + head] * w;
-    }
-    l = wave_sum(l);
-    if (lane == 0) { mh[head] = m; lh[head] = l; }
-  }
-  __syncthreads();
-#pragma unroll 1
+  // ---- combine: prefix (m_p, l_p, pre_acc) and the ring's partials, one column per thread
   for (int col = tid; col < cols; col += TB_THREADS) {
     const int head = col / D;
-    const float* w = wT[head];
-    float acc = 0.0f;
+    const float mp = pre_m[head];
+    float M = mp;
     if (ring) {
 #pragma unroll
-      for (int r = 0; r < RING_PARTS; ++r) acc += ring_part[r][col] * w[P + r];
+      for (int r = 0; r < RING_PARTS; ++r) M = fmaxf(M, ring_part[r][gq * D + head]);
     }
-    if (col == tid) {
-      // v[u] is 0 for u >= P, where w holds ring weights or 0
+    const float Mu = M == NEG_INF ? 0.0f : M;
+    const float alpha = mp == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mp - Mu);
+    float acc = alpha * pre_acc[col], l = alpha * pre_l[head];
+    if (ring) {
 #pragma unroll
-      for (int u = 0; u < MERGE_CHUNK; u += 4) {
-        const float4 w4 = *reinterpret_cast<const float4*>(w + u);
-        acc += v[u] * w4.x + v[u + 1] * w4.y + v[u + 2] * w4.z + v[u + 3] * w4.w;
+      for (int r = 0; r < RING_PARTS; ++r) {
+        const float mr = ring_part[r][gq * D + head];
+        const float beta = mr == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mr - Mu);
+        acc += beta * ring_part[r][col];
+        l += beta * ring_part[r][gq * D + gq + head];
       }
-    } else {
-      for (int s = 0; s < min(P, MERGE_CHUNK); ++s) acc += hws[(int64_t)s * pw + col] * w[s];
     }
-#pragma unroll 4
-    for (int s = MERGE_CHUNK; s < P; ++s) acc += hws[(int64_t)s * pw + col] * w[s];
-    const float l = lh[head];
     const int qh = h * gq + head, d = col % D;
     a.out[(int64_t)qh * D + d] = f2h(l > 0.0f ? acc * (INV_P_SCALE / l) : 0.0f);
-    if (a.lse && d == 0) a.lse[qh] = l > 0.0f ? (mh[head] + __log2f(l)) * LN2 : NEG_INF;
+    if (a.lse && d == 0) a.lse[qh] = l > 0.0f ? (M + __log2f(l)) * LN2 : NEG_INF;
   }
 }
 
