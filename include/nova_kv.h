@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 2
+#define NKV_ABI_VERSION 3
 
 #define NKV_OK 0
 #define NKV_ERR_INVALID 1     /* argument outside what the reference accepts */
@@ -200,6 +200,57 @@ int nkv_tail_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v,
  */
 int nkv_ring_mask(const int64_t* written_dev, const int64_t* qlen_dev, const int64_t* first_dev,
                   int64_t slots, uint8_t* mask, void* stream);
+
+/*
+ * ---- Per-token symmetric int8 format ("tok") ----
+ * An extension with no counterpart in the reference's storage formats: one symmetric
+ * absmax scale per (token, KV head) row of 128, the layout the decode-path specification
+ * asks for (int8 codes [H_kv, L, 128], fp16 scales [H_kv, L]). Rounding follows the
+ * conventions of kvquant.quantize_int8 (src/nova/kvquant.py:136-149): fp32 arithmetic,
+ * round half to even, a 1e-8 floor on the fp32 scale, the scale stored as fp16 and the
+ * codes computed with the fp32 scale:
+ *   scale = max(max|x| / 127, 1e-8), code = clamp(rint(x / scale), -127, 127),
+ *   dequantized value = fp16(code * scale16).
+ * A cache in this format keeps every token as int8 (no fp16 ring); its capacity is a
+ * multiple of 64.
+ */
+
+/* Quantize `rows` slabs of `[n, 128]` (token stride 128, slab stride x_row_stride
+ * elements; NKV_F16 / NKV_BF16 / NKV_F32) into codes (slab stride codes_row_stride) and
+ * scales (slab stride scale_row_stride). One wave reduces the absmax of 4 rows. */
+int nkv_quantize_tok(const void* x, int x_dtype, int64_t x_row_stride, int64_t rows, int64_t n,
+                     int64_t dim, int8_t* codes, int64_t codes_row_stride, uint16_t* scales,
+                     int64_t scale_row_stride, void* stream);
+
+/* Inverse: out = fp16/bf16/fp32 of code * scale16 (exact in fp32, rounded once). */
+int nkv_dequantize_tok(const int8_t* codes, int64_t codes_row_stride, const uint16_t* scales,
+                       int64_t scale_row_stride, int64_t rows, int64_t n, int64_t dim, void* out,
+                       int out_dtype, int64_t out_row_stride, void* stream);
+
+/* Split-K decode attention over tokens [0, used) of a tok cache (`used` from used_dev
+ * when non-NULL). Same launches, q / out / lse / workspace / n_parts contract as
+ * nkv_attn_decode_t64 (the counterpart of src/nova/kvattn.py:281-427 for this format). */
+int nkv_attn_decode_tok(const uint16_t* q, const int8_t* kq, const uint16_t* ksc, const int8_t* vq,
+                        const uint16_t* vsc, int64_t hq, int64_t hkv, int64_t head_dim,
+                        int64_t capacity, int64_t used, const int64_t* used_dev, uint16_t* out,
+                        float* lse_out, void* workspace, int64_t workspace_bytes, int64_t n_parts,
+                        void* stream);
+
+/* Append of one decode token: quantizes k_new / v_new ([hkv, 128], head stride
+ * kv_head_stride) into position *pos_dev and sets *written_dev = pos + 1. */
+int nkv_append_tok(const uint16_t* k_new, const uint16_t* v_new, int64_t kv_head_stride, int8_t* kq,
+                   uint16_t* ksc, int8_t* vq, uint16_t* vsc, const int64_t* pos_dev,
+                   int64_t* written_dev, int64_t hkv, int64_t head_dim, int64_t capacity,
+                   void* stream);
+
+/* One decode step: nkv_append_tok then attention over [0, pos]. Two launches: the prefix
+ * kernel over [0, pos) (which also performs the append), then the tail kernel (the new
+ * token and the combine). */
+int nkv_decode_step_tok(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                        int64_t kv_head_stride, int8_t* kq, uint16_t* ksc, int8_t* vq, uint16_t* vsc,
+                        const int64_t* pos_dev, int64_t* written_dev, int64_t hq, int64_t hkv,
+                        int64_t head_dim, int64_t capacity, uint16_t* out, float* lse_out,
+                        void* workspace, int64_t workspace_bytes, int64_t n_parts, void* stream);
 
 /*
  * Plain device copy (16-byte vector loads and stores). Used to calibrate the

@@ -50,11 +50,16 @@ SIGNATURES = {
     "nkv_decode_step_combine_t64": (c_int, _STEP),
     "nkv_tail_attend": (c_int, [P, P, P, P, I64, I64, I64, I64, P, P, P]),
     "nkv_ring_mask": (c_int, [P, P, P, I64, P, P]),
+    "nkv_quantize_tok": (c_int, [P, c_int, I64, I64, I64, I64, P, I64, P, I64, P]),
+    "nkv_dequantize_tok": (c_int, [P, I64, P, I64, I64, I64, I64, P, c_int, I64, P]),
+    "nkv_attn_decode_tok": (c_int, [P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P, P, I64, I64, P]),
+    "nkv_append_tok": (c_int, [P, P, I64, P, P, P, P, P, P, I64, I64, I64, P]),
+    "nkv_decode_step_tok": (c_int, [P, P, P, I64, P, P, P, P, P, P, I64, I64, I64, I64, P, P, P, I64, I64, P]),
     "nkv_copy_bytes": (c_int, [P, P, I64, P]),
     "nkv_read_bw": (c_int, [P, I64, P, I64, P]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 _lock = threading.Lock()

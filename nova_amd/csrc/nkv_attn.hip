@@ -40,39 +40,36 @@ namespace nkv {
 #ifndef NKV_WAVES
 #define NKV_WAVES 8
 #endif
-#ifndef NKV_STAGES
-#define NKV_STAGES 1
-#endif
-#ifndef NKV_HALF
-#define NKV_HALF 1  // stream half groups (32 tokens) through two LDS slots per wave
-#endif
+
 
 constexpr int D = 128;
 constexpr int GT = 64;              // tokens per ruler group == ring slots
 constexpr int WAVES = NKV_WAVES;    // waves per workgroup
 constexpr int THREADS = 64 * WAVES;
-constexpr int STAGES = NKV_STAGES;  // LDS buffers per wave
 constexpr int CODE_BYTES = GT * D;                        // one tensor's codes of one group
 constexpr int RULER_BYTES = 4 * D * 2;                    // kst, kmn, vst, vmn of one group
-constexpr int STAGE_BYTES = 2 * CODE_BYTES + RULER_BYTES;  // 17 KiB
 constexpr int HALF_CODE = 32 * D;                          // one tensor's codes of a half group
 constexpr int HALF_SLOT = 2 * HALF_CODE;                   // K | V codes of a half group
-constexpr int WAVE_HALF_BYTES = 2 * HALF_SLOT + 2 * RULER_BYTES;  // two slots + two ruler sets
-constexpr int WAVE_LDS = NKV_HALF ? WAVE_HALF_BYTES : STAGES * STAGE_BYTES;
-constexpr int LDS_BYTES = WAVES * WAVE_LDS;                // 144 KiB (half groups) / 136 KiB
+constexpr int WAVE_LDS = 2 * HALF_SLOT + 2 * RULER_BYTES;  // two slots + two ruler sets
+constexpr int LDS_BYTES = WAVES * WAVE_LDS;                // 144 KiB
 constexpr int DMA_FIRST_HALF = 2 * (HALF_CODE / 1024) + 4; // with the group's rulers
 constexpr int DMA_SECOND_HALF = 2 * (HALF_CODE / 1024);
+// the per-token symmetric format: a half-group slot holds K and V codes and the 32 K and
+// 32 V fp16 scales of its tokens
+constexpr int TOK_SCALE_BYTES = 32 * 2;
+constexpr int HALF_SLOT_TOK = 2 * HALF_CODE + 2 * TOK_SCALE_BYTES;
+constexpr int WAVE_LDS_TOK = 2 * HALF_SLOT_TOK;
+constexpr int LDS_BYTES_TOK = WAVES * WAVE_LDS_TOK;        // 130 KiB
+constexpr int DMA_HALF_TOK = 2 * (HALF_CODE / 1024) + 2;
 constexpr int RING_BYTES = GT * D * 2;                    // one fp16 ring tensor of one head
-constexpr int DMA_PER_GROUP = 2 * (CODE_BYTES / 1024) + 4;
 constexpr float P_SCALE = 32768.0f;       // 2^15
 constexpr float INV_P_SCALE = 1.0f / 32768.0f;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 constexpr float NEG_INF = -__builtin_huge_valf();
 
-static_assert(DMA_PER_GROUP == 20, "the vmcnt immediates below assume 20 loads per group");
-static_assert(STAGES == 1 || STAGES == 2, "one or two LDS stages per wave");
-static_assert(LDS_BYTES <= 160 * 1024, "LDS of one workgroup");
+static_assert(DMA_FIRST_HALF == 12 && DMA_SECOND_HALF == 8 && DMA_HALF_TOK == 10, "loads per half group");
+static_assert(LDS_BYTES <= 150 * 1024 && LDS_BYTES_TOK <= 150 * 1024, "LDS of one workgroup");
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -81,6 +78,7 @@ typedef int v2i_t __attribute__((vector_size(8)));
 typedef __attribute__((address_space(3))) v2i_t lds_v2i_t;
 
 enum TailMode : int { TAIL_NONE = 0, TAIL_MASK = 1, TAIL_SCALARS = 2, TAIL_FUSED = 3 };
+// TAIL_FUSED with `tok`: the new token itself is the tail (its codes written by the prefix kernel).
 
 struct AttnArgs {
   const uint16_t* q;
@@ -103,6 +101,9 @@ struct AttnArgs {
   int64_t* pg_out;
   const uint16_t* k_new;
   const uint16_t* v_new;
+  uint16_t* ksc;  // per-token symmetric format: fp16 scales [hkv, capacity]
+  uint16_t* vsc;
+  int tok;        // 1: per-token symmetric int8 codes and scales, 0: int8t64
   int64_t kv_hs;
   int64_t used, pg;  // host values when the device pointers are null
   int64_t capacity, ngroups_cap;
@@ -214,40 +215,6 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
 
-// Issue the 20 loads of group `grp` of head h into the LDS stage at byte address `st`.
-// LDS row r, chunk position p holds chunk p ^ swz(r) of token row r. Rows at or beyond
-// the cache capacity are never read (the last row is repeated).
-__device__ __forceinline__ void issue_group(const AttnArgs& a, int h, int64_t grp, uint32_t st) {
-  const int lane = threadIdx.x & 63;
-  const int64_t t0 = grp * GT;
-  const int rows = (int)min<int64_t>(GT, a.capacity - t0);
-  const void* kb = uniform_ptr(a.kq + ((int64_t)h * a.capacity + t0) * D);
-  const void* vb = uniform_ptr(a.vq + ((int64_t)h * a.capacity + t0) * D);
-  st = __builtin_amdgcn_readfirstlane(st);
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // earlier reads of this stage are done
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int row = 8 * j + (lane >> 3);
-    const uint32_t off = (uint32_t)(min(row, rows - 1) * D + (((lane & 7) ^ swz(row)) << 4));
-    dma16(kb, off, st + 1024 * j);
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int row = 8 * j + (lane >> 3);
-    const uint32_t off = (uint32_t)(min(row, rows - 1) * D + (((lane & 7) ^ swz(row)) << 4));
-    dma16(vb, off, st + CODE_BYTES + 1024 * j);
-  }
-  // rulers: one load per tensor, lanes 16w..16w+15 active for tensor w (kst, kmn, vst, vmn),
-  // so that every base address stays in scalar registers
-  const int64_t ro = ((int64_t)h * a.ngroups_cap + grp) * D;
-  const uint32_t roff = (uint32_t)(8 * (lane & 15)) * 2;
-  const int which = lane >> 4;
-  if (which == 0) dma16(uniform_ptr(a.kst + ro), roff, st + 2 * CODE_BYTES);
-  if (which == 1) dma16(uniform_ptr(a.kmn + ro), roff, st + 2 * CODE_BYTES);
-  if (which == 2) dma16(uniform_ptr(a.vst + ro), roff, st + 2 * CODE_BYTES);
-  if (which == 3) dma16(uniform_ptr(a.vmn + ro), roff, st + 2 * CODE_BYTES);
-}
-
 // Issue the loads of half `hf` (tokens 32 hf .. 32 hf + 31) of group `grp` of head h: 32
 // K and 32 V code rows (4 + 4 loads) into the slot at `slot` (K codes, then V codes), and
 // for hf == 0 the group's rulers (4 loads) into `rs`. Rows are swizzled as in a full
@@ -283,6 +250,30 @@ __device__ __forceinline__ void issue_half(const AttnArgs& a, int h, int64_t grp
   }
 }
 
+// The per-token symmetric format's half group: 32 K and 32 V code rows (4 + 4 loads) into
+// the slot, then the 32 K and 32 V scales of those tokens (one load each, 4 lanes).
+// Token rows stay below the capacity (a multiple of 64 in this format).
+__device__ __forceinline__ void issue_half_tok(const AttnArgs& a, int h, int64_t grp, int hf, uint32_t slot) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t0 = grp * GT + 32 * hf;
+  const void* kb = uniform_ptr(a.kq + (int64_t)h * a.capacity * D);
+  const void* vb = uniform_ptr(a.vq + (int64_t)h * a.capacity * D);
+  slot = __builtin_amdgcn_readfirstlane(slot);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // earlier reads of this slot are done
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    dma16(kb, (uint32_t)((t0 + row) * D) + (((lane & 7) ^ swz(row)) << 4), slot + 1024 * j);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    dma16(vb, (uint32_t)((t0 + row) * D) + (((lane & 7) ^ swz(row)) << 4), slot + HALF_CODE + 1024 * j);
+  }
+  if (lane < 4) dma16(uniform_ptr(a.ksc + (int64_t)h * a.capacity + t0), 16u * lane, slot + 2 * HALF_CODE);
+  if (lane < 4) dma16(uniform_ptr(a.vsc + (int64_t)h * a.capacity + t0), 16u * lane, slot + 2 * HALF_CODE + TOK_SCALE_BYTES);
+}
+
 // Q of KV head h (gq rows of 256 bytes) into LDS at `dst`, by one wave.
 __device__ __forceinline__ void issue_q(const AttnArgs& a, int h, uint32_t dst) {
   const int lane = threadIdx.x & 63;
@@ -303,7 +294,6 @@ __device__ __forceinline__ void load_q_lds(const uint16_t* q_lds, int gq, half8_
   }
 }
 
-__device__ __forceinline__ void wait_groups_all_but_one() { asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); }
 __device__ __forceinline__ void wait_groups_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ---------------------------------------------------------------- one group's attention
@@ -457,11 +447,87 @@ __device__ __forceinline__ void attend_block(const AttnArgs& a, WaveState& st, c
   }
 }
 
-// One whole 64-token group resident in a full LDS stage (K codes, V codes, rulers).
-__device__ __forceinline__ void attend_stage(const AttnArgs& a, WaveState& st, const half8_t (&qb)[4],
-                                             const uint8_t* stage, int nvalid) {
-  attend_block<2>(a, st, qb, stage, stage + CODE_BYTES, stage + 2 * CODE_BYTES, nvalid);
+// fp16(code * scale) for 8 signed codes sharing one fp16 scale, and for 8 codes with one
+// scale each: the product of an 8-bit integer and an fp16 is exact in fp32, so the packed
+// fp16 multiply rounds it once, as fp16(fp32(code) * fp32(scale)) does.
+__device__ __forceinline__ half8_t dq8_sym(uint32_t w0, uint32_t w1, half2_t s) {
+  const half2_t a = scodes_to_h2(w0, kSelB01) * s;
+  const half2_t b = scodes_to_h2(w0, kSelB23) * s;
+  const half2_t c = scodes_to_h2(w1, kSelB01) * s;
+  const half2_t d = scodes_to_h2(w1, kSelB23) * s;
+  return half8_t{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
 }
+__device__ __forceinline__ half8_t dq8_sym_v(uint32_t w0, uint32_t w1, uint4 s) {
+  const half2_t a = scodes_to_h2(w0, kSelB01) * as_h2(s.x);
+  const half2_t b = scodes_to_h2(w0, kSelB23) * as_h2(s.y);
+  const half2_t c = scodes_to_h2(w1, kSelB01) * as_h2(s.z);
+  const half2_t d = scodes_to_h2(w1, kSelB23) * as_h2(s.w);
+  return half8_t{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+// attend_block for 32 tokens of the per-token symmetric format: codes as in attend_block
+// (signed), the tokens' K scales at `ksc` and V scales at `vsc` (32 fp16 each).
+__device__ __forceinline__ void attend_block_tok(const AttnArgs& a, WaveState& st, const half8_t (&qb)[4],
+                                                 const uint8_t* kc, const uint8_t* vc, const uint16_t* ksc,
+                                                 const uint16_t* vsc, int nvalid) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  // ---- S^T = K Q^T; lane (c, g) holds token 16b + c, whose scale it splats
+  float4_t S[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    S[b] = float4_t{0.f, 0.f, 0.f, 0.f};
+    const int row = 16 * b + c;
+    const int key = swz(row);
+    const _Float16 ks = __builtin_bit_cast(_Float16, ksc[row]);
+    const half2_t ks2 = half2_t{ks, ks};
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const uint4 kw = *reinterpret_cast<const uint4*>(kc + row * D + (((g + 4 * hh) ^ key) << 4));
+      S[b] = mfma32(dq8_sym(kw.x, kw.y, ks2), qb[2 * hh], S[b]);
+      S[b] = mfma32(dq8_sym(kw.z, kw.w, ks2), qb[2 * hh + 1], S[b]);
+    }
+  }
+  float s[2][4];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[b][i] = (16 * b + 4 * g + i) < nvalid ? S[b][i] * a.sl2 : NEG_INF;
+  half8_t phi[1], plo[1];
+  softmax_step<1>(st, s, phi, plo, a.gq);
+
+  // ---- O += P V: lane (c, g) receives dim 16cb + c of tokens 4g + {0..3} and 16 + 4g +
+  // {0..3}; their 8 scales are the same for every cb. Invalid tokens get code 0 and scale 0.
+  const int r = c >> 1;
+  const int row = 16 * (r >> 2) + 4 * g + (r & 3);
+  const int key = swz(row);
+  const uint8_t* rowp = vc + row * D + 8 * (c & 1);
+  const uint2 s_lo = *reinterpret_cast<const uint2*>(vsc + 4 * g);
+  const uint2 s_hi = *reinterpret_cast<const uint2*>(vsc + 16 + 4 * g);
+  uint4 vs = uint4{s_lo.x, s_lo.y, s_hi.x, s_hi.y};
+  u32x2 keep = {~0u, ~0u};
+  if (nvalid < 32) {
+    uint32_t m[2] = {0u, 0u}, hm[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      const int tok = 16 * (rr >> 2) + 4 * g + (rr & 3);
+      if (tok < nvalid) {
+        m[rr >> 2] |= 0xffu << (8 * (rr & 3));
+        hm[rr >> 1] |= 0xffffu << (16 * (rr & 1));
+      }
+    }
+    keep = u32x2{m[0], m[1]};
+    vs = uint4{vs.x & hm[0], vs.y & hm[1], vs.z & hm[2], vs.w & hm[3]};
+  }
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb) {
+    const u32x2 vw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                         (lds_v2i_t*)(const lds_void_t*)(rowp + ((cb ^ key) << 4)))) & keep;
+    const half8_t vb = dq8_sym_v(vw.x, vw.y, vs);
+    st.acc[cb] = mfma32(phi[0], vb, st.acc[cb]);
+    st.acc[cb] = mfma32(plo[0], vb, st.acc[cb]);
+  }
+}
+
 
 // Online-softmax update with the 4 masked scores s[i] (token 4g + i of a 16-token block,
 // head c); returns P as the A operand of v_mfma_f32_16x16x16_f16 (hi/lo halves).
@@ -574,12 +640,30 @@ __device__ __forceinline__ const uint16_t* fresh_of(const AttnArgs& a, int h, in
   return (which == 0 ? a.k_new : a.v_new) + h * a.kv_hs;
 }
 
+// The per-token symmetric append of the token at `pos`: waves 0 and 1 of the calling
+// workgroup quantize K and V of KV head h (lanes 0..15, 8 values each) and store the codes
+// and the fp16 scale at position pos.
+__device__ __forceinline__ void append_tok_rows(const AttnArgs& a, int h, int64_t pos) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (wave > 1 || lane >= 16) return;
+  const uint4 w = *reinterpret_cast<const uint4*>(fresh_of(a, h, wave) + 8 * lane);
+  const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = h2f((uint16_t)(wv[j >> 1] >> (16 * (j & 1))));
+  float scale;
+  const uint2 cw = sym_quant8(v, scale);
+  const int64_t row = (int64_t)h * a.capacity + pos;
+  *reinterpret_cast<uint2*>((wave == 0 ? a.kq : a.vq) + row * D + 8 * lane) = cw;
+  if (lane == 0) (wave == 0 ? a.ksc : a.vsc)[row] = f2h(scale);
+}
+
 __device__ __forceinline__ void write_scalars(const AttnArgs& a, int64_t pos) {
   const int64_t written = pos + 1;
   const int64_t qlen = written / GT * GT;
   *a.written_out = written;
-  *a.qlen_out = qlen;
-  *a.pg_out = qlen / GT;
+  if (a.qlen_out) *a.qlen_out = qlen;
+  if (a.pg_out) *a.pg_out = qlen / GT;
 }
 
 // Slot validity of the ring: slot i holds p = u - ((u - i) mod 64), valid iff qlen <= p <= u,
@@ -714,7 +798,9 @@ __device__ __forceinline__ int64_t prefix_limit(const AttnArgs& a, int64_t& pos,
   if (a.tail_mode == TAIL_FUSED) {
     pos = *a.pos_dev;
     pos_ok = pos >= 0 && pos < a.capacity;  // a position outside the cache appends nothing
-    U = pos_ok ? pos / GT * GT : 0;
+    U = pos_ok ? (a.tok ? pos : pos / GT * GT) : 0;
+  } else if (a.tok) {
+    U = a.used_dev ? *a.used_dev : a.used;
   } else {
     const int64_t used = a.used_dev ? *a.used_dev : a.used;
     const int64_t pgv = a.pg_dev ? *a.pg_dev : a.pg;
@@ -730,9 +816,10 @@ __device__ __forceinline__ int64_t prefix_limit(const AttnArgs& a, int64_t& pos,
 // after this launch completes. In the fused step, workgroup part < APPEND_UNITS first runs
 // append unit `part` of head h (the prefix never reads the group it writes), and the grid
 // has max(n_parts, APPEND_UNITS) parts per head; parts >= n_parts only append.
+template <bool TOK>
 __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds_raw[LDS_BYTES];
-  __shared__ __attribute__((aligned(16))) uint16_t unit_src[UNIT_SRC_BYTES / 2];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_raw[TOK ? LDS_BYTES_TOK : LDS_BYTES];
+  __shared__ __attribute__((aligned(16))) uint16_t unit_src[TOK ? 8 : UNIT_SRC_BYTES / 2];
   __shared__ __attribute__((aligned(16))) uint16_t q_lds[16 * D];
   __shared__ __attribute__((aligned(16))) float xch[UNIT_CH * 2 * WAVES];
   __shared__ int next_group;
@@ -741,52 +828,53 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.x % a.hkv;
   const int part = blockIdx.x / a.hkv;
-  uint8_t* my_stages = lds_raw + wave * WAVE_LDS;
+  constexpr int wave_lds = TOK ? WAVE_LDS_TOK : WAVE_LDS;
+  constexpr int slot_bytes = TOK ? HALF_SLOT_TOK : HALF_SLOT;
+  uint8_t* my_stages = lds_raw + wave * wave_lds;
   const uint32_t my_lds = __builtin_amdgcn_readfirstlane(lds_addr(my_stages));
   const uint32_t src_lds = __builtin_amdgcn_readfirstlane(lds_addr(unit_src));
 
   int64_t pos;
   bool pos_ok;
   const int64_t U = prefix_limit(a, pos, pos_ok);
-  const bool append = a.tail_mode == TAIL_FUSED && pos_ok && part < APPEND_UNITS;
-  const bool prefix = part < a.n_parts;  // the fused step's grid has at least APPEND_UNITS parts
+  // the fused step's append: int8t64 units in parts < APPEND_UNITS (the grid has at least
+  // that many parts), the per-token symmetric token in part 0
+  const bool append = a.tail_mode == TAIL_FUSED && pos_ok && (TOK ? part == 0 : part < APPEND_UNITS);
+  const bool prefix = part < a.n_parts;
 
   const int64_t W = (U + GT - 1) / GT;
   const int64_t gs = prefix ? (int64_t)part * W / a.n_parts : 0;
   const int64_t ge = prefix ? (int64_t)(part + 1) * W / a.n_parts : 0;
-  const int n = ge - gs > wave ? (int)((ge - gs - wave + WAVES - 1) / WAVES) : 0;
-  // Q and the append unit's rows are loaded ahead of the groups, so that waiting for them
-  // leaves the groups in flight
-  if (wave == 0 && prefix) issue_q(a, h, __builtin_amdgcn_readfirstlane(lds_addr(q_lds)));
-  if (wave == 0 && append) issue_unit_rows(a, h, part, src_lds);
-#if NKV_HALF
   // Groups gs + gi, gi < ng, are handed out to the waves one at a time: wave w starts with
   // gi = w, and a wave claims the next one from `next_group` once the first half of its
   // current group is done, so waves whose loads arrive early take more groups. A group's
-  // halves go to slots 0 and 1, its rulers to the wave's ruler set (alternating).
+  // halves (32 tokens) go to slots 0 and 1 (int8t64: its rulers to the wave's ruler set,
+  // alternating).
   const int ng = (int)(ge - gs);
   const uint32_t rul_lds = my_lds + 2 * HALF_SLOT;
   if (tid == 0) next_group = WAVES;
+  // Q and the append unit's rows are loaded ahead of the groups, so that waiting for them
+  // leaves the groups in flight
+  if (wave == 0 && prefix) issue_q(a, h, __builtin_amdgcn_readfirstlane(lds_addr(q_lds)));
+  if (!TOK && wave == 0 && append) issue_unit_rows(a, h, part, src_lds);
   if (wave < ng) {
-    issue_half(a, h, gs + wave, 0, my_lds, rul_lds);
-    issue_half(a, h, gs + wave, 1, my_lds + HALF_SLOT, rul_lds);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF + DMA_SECOND_HALF) : "memory");
+    if constexpr (TOK) {
+      issue_half_tok(a, h, gs + wave, 0, my_lds);
+      issue_half_tok(a, h, gs + wave, 1, my_lds + HALF_SLOT_TOK);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_HALF_TOK) : "memory");
+    } else {
+      issue_half(a, h, gs + wave, 0, my_lds, rul_lds);
+      issue_half(a, h, gs + wave, 1, my_lds + HALF_SLOT, rul_lds);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF + DMA_SECOND_HALF) : "memory");
+    }
   } else {
     wait_groups_all();
   }
-#else
-#pragma unroll
-  for (int s0 = 0; s0 < STAGES; ++s0)
-    if (s0 < n) issue_group(a, h, gs + wave + (int64_t)s0 * WAVES, my_lds + s0 * STAGE_BYTES);
-  const int in_flight = min(n, STAGES);
-  if (in_flight == 0) wait_groups_all();
-  else if (in_flight == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_PER_GROUP) : "memory");
-  else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_PER_GROUP) : "memory");
-#endif
   __syncthreads();
 
   if (append) {
-    append_unit(a, h, part, pos, unit_src, xch);
+    if constexpr (TOK) append_tok_rows(a, h, pos);
+    else append_unit(a, h, part, pos, unit_src, xch);
     if (blockIdx.x == 0 && tid == 0) write_scalars(a, pos);
   }
   if (!prefix) return;
@@ -795,37 +883,44 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   half8_t qb[4];
   load_q_lds(q_lds, a.gq, qb);
 
-#if NKV_HALF
   int gi = wave;
   for (int rs = 0; gi < ng; rs ^= 1) {
     const int64_t grp = gs + gi;
     const uint8_t* rul = my_stages + 2 * HALF_SLOT + rs * RULER_BYTES;
+    const uint8_t* slot1 = my_stages + slot_bytes;
     // first half (slot 0); the second half, issued after it, may stay in flight
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_SECOND_HALF) : "memory");
-    attend_block<1>(a, st, qb, my_stages, my_stages + HALF_CODE, rul, (int)min<int64_t>(32, U - grp * GT));
+    if constexpr (TOK) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_HALF_TOK) : "memory");
+      attend_block_tok(a, st, qb, my_stages, my_stages + HALF_CODE,
+                       reinterpret_cast<const uint16_t*>(my_stages + 2 * HALF_CODE),
+                       reinterpret_cast<const uint16_t*>(my_stages + 2 * HALF_CODE + TOK_SCALE_BYTES),
+                       (int)min<int64_t>(32, U - grp * GT));
+    } else {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_SECOND_HALF) : "memory");
+      attend_block<1>(a, st, qb, my_stages, my_stages + HALF_CODE, rul, (int)min<int64_t>(32, U - grp * GT));
+    }
     int nx = 0;
     if (lane == 0) nx = __hip_atomic_fetch_add(&next_group, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     nx = __builtin_amdgcn_readfirstlane(nx);
-    if (nx < ng) issue_half(a, h, gs + nx, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
     // second half (slot 1)
-    if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF) : "memory");
-    else wait_groups_all();
     const int nv2 = (int)min<int64_t>(32, U - grp * GT - 32);
-    if (nv2 > 0) attend_block<1>(a, st, qb, my_stages + HALF_SLOT, my_stages + HALF_SLOT + HALF_CODE, rul, nv2);
-    if (nx < ng) issue_half(a, h, gs + nx, 1, my_lds + HALF_SLOT, 0u);
+    if constexpr (TOK) {
+      if (nx < ng) issue_half_tok(a, h, gs + nx, 0, my_lds);
+      if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_HALF_TOK) : "memory");
+      else wait_groups_all();
+      if (nv2 > 0)
+        attend_block_tok(a, st, qb, slot1, slot1 + HALF_CODE, reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE),
+                         reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE + TOK_SCALE_BYTES), nv2);
+      if (nx < ng) issue_half_tok(a, h, gs + nx, 1, my_lds + HALF_SLOT_TOK);
+    } else {
+      if (nx < ng) issue_half(a, h, gs + nx, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
+      if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF) : "memory");
+      else wait_groups_all();
+      if (nv2 > 0) attend_block<1>(a, st, qb, slot1, slot1 + HALF_CODE, rul, nv2);
+      if (nx < ng) issue_half(a, h, gs + nx, 1, my_lds + HALF_SLOT, 0u);
+    }
     gi = nx;
   }
-#else
-  for (int i = 0; i < n; ++i) {
-    if (STAGES > 1 && i + 1 < n) wait_groups_all_but_one();
-    else wait_groups_all();
-    const int64_t grp = gs + wave + (int64_t)i * WAVES;
-    const int nvalid = (int)min<int64_t>(GT, U - grp * GT);
-    const int sidx = STAGES > 1 ? (i & 1) : 0;
-    attend_stage(a, st, qb, my_stages + sidx * STAGE_BYTES, nvalid);
-    if (i + STAGES < n) issue_group(a, h, grp + STAGES * WAVES, my_lds + sidx * STAGE_BYTES);
-  }
-#endif
 
   // ---- merge the waves through LDS (the stages are dead once every wave is here)
   __syncthreads();
@@ -881,9 +976,17 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
   // for a merging wave the m / l of its first head's partials (lane s) and its two columns
   // (2 lane, 2 lane + 1) of the first MERGE_CHUNK partials
   const int which = wave >> 2, qtr = wave & 3;
-  const bool completes = fused && pos_ok && (pos + 1) % GT == 0;  // the token completed its group
+  const bool completes = fused && pos_ok && !a.tok && (pos + 1) % GT == 0;  // the token completed its group
+  const bool tok1 = ring && a.tok;  // per-token symmetric fused step: the tail is the new token
   RingQuarter rq;
-  if (ring && !completes) ring_load_quarter(ring_of(a, h, which), (int)a.tail_slots, qtr, rq);
+  if (ring && !completes && !tok1) ring_load_quarter(ring_of(a, h, which), (int)a.tail_slots, qtr, rq);
+  uint2 tw = {0u, 0u};
+  uint16_t tsc = 0;
+  if (tok1 && qtr == 0 && lane < 16) {
+    const int64_t row = (int64_t)h * a.capacity + pos;
+    tw = *reinterpret_cast<const uint2*>((which == 0 ? a.kq : a.vq) + row * D + 8 * lane);
+    tsc = (which == 0 ? a.ksc : a.vsc)[row];
+  }
   uint2 cw[4];
   uint4 cst, cmn;
   if (completes) {
@@ -922,7 +1025,15 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) rq.rows[i] = __builtin_bit_cast(uint4, dq8(cw[i].x, cw[i].y, cst, cmn));
     }
-    ring_quarter_to_lds(rq.rows, qtr, which == 0 ? ring_k : ring_v);
+    if (tok1) {
+      if (qtr == 0 && lane < 16) {
+        const _Float16 sc = __builtin_bit_cast(_Float16, tsc);
+        *reinterpret_cast<half8_t*>((which == 0 ? ring_k : ring_v) + (ring_chunk_pos(0, lane) << 4)) =
+            dq8_sym(tw.x, tw.y, half2_t{sc, sc});
+      }
+    } else {
+      ring_quarter_to_lds(rq.rows, qtr, which == 0 ? ring_k : ring_v);
+    }
     __syncthreads();
   }
   if (!merger) {
@@ -930,6 +1041,7 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
     const int64_t written = fused ? pos + 1 : (a.tail_mode == TAIL_SCALARS ? *a.written_dev : 0);
     uint64_t bits;
     if (completes) bits = ~0ull;
+    else if (tok1) bits = wave == 0 ? 1ull : 0ull;
     else if (a.tail_mode == TAIL_MASK) bits = __builtin_amdgcn_ballot_w64(mask_on);
     else bits = ring_bits(written, U, first);
     WaveState st;
@@ -1021,6 +1133,14 @@ __global__ __launch_bounds__(THREADS) void append_kernel(AttnArgs a) {
   if (blockIdx.x == 0 && threadIdx.x == 0) write_scalars(a, pos);
 }
 
+// Standalone per-token symmetric append: one workgroup of 2 waves (K, V) per KV head.
+__global__ __launch_bounds__(128) void append_tok_kernel(AttnArgs a) {
+  const int64_t pos = *a.pos_dev;
+  if (pos < 0 || pos >= a.capacity) return;  // a position outside the cache appends nothing
+  append_tok_rows(a, blockIdx.x, pos);
+  if (blockIdx.x == 0 && threadIdx.x == 0) write_scalars(a, pos);
+}
+
 __global__ void ring_mask_kernel(const int64_t* written, const int64_t* qlen, const int64_t* first,
                                  int64_t slots, uint8_t* mask) {
   const int i = threadIdx.x;
@@ -1064,8 +1184,9 @@ static int launch_attn(AttnArgs& a, int64_t n_parts, int64_t workspace_bytes, hi
   if (a.capacity > (int64_t(1) << 24))  // code row offsets of one head stay 32-bit
     return fail(NKV_ERR_UNSUPPORTED, "%s: capacity %lld exceeds 16M tokens", what, (long long)a.capacity);
   if (n_parts > 0 && (launches & LAUNCH_PREFIX)) {
-    const int64_t parts = a.tail_mode == TAIL_FUSED ? std::max<int64_t>(n_parts, APPEND_UNITS) : n_parts;
-    hipLaunchKernelGGL(attn_prefix_kernel, dim3((unsigned)(a.hkv * parts)), dim3(THREADS), 0, s, a);
+    const int64_t parts = a.tail_mode == TAIL_FUSED && !a.tok ? std::max<int64_t>(n_parts, APPEND_UNITS) : n_parts;
+    if (a.tok) hipLaunchKernelGGL(attn_prefix_kernel<true>, dim3((unsigned)(a.hkv * parts)), dim3(THREADS), 0, s, a);
+    else hipLaunchKernelGGL(attn_prefix_kernel<false>, dim3((unsigned)(a.hkv * parts)), dim3(THREADS), 0, s, a);
     if (int rc = check_launch(what)) return rc;
   }
   if (!(launches & LAUNCH_TAIL)) return NKV_OK;
@@ -1249,4 +1370,80 @@ extern "C" int nkv_ring_mask(const int64_t* written_dev, const int64_t* qlen_dev
   hipLaunchKernelGGL(ring_mask_kernel, dim3(1), dim3((unsigned)slots), 0, static_cast<hipStream_t>(stream),
                      written_dev, qlen_dev, first_dev, slots, mask);
   return check_launch("ring_mask");
+}
+
+// ---------------------------------------------------------------- per-token symmetric format
+
+static int check_tok_cache(const char* what, int64_t capacity, const void* kq, const void* ksc, const void* vq,
+                           const void* vsc) {
+  if (capacity <= 0 || capacity % GT) return fail(NKV_ERR_INVALID, "%s: capacity %lld must be a positive multiple of 64", what, (long long)capacity);
+  if (!kq || !ksc || !vq || !vsc) return fail(NKV_ERR_INVALID, "%s: null pointer argument", what);
+  if (!al16(kq) || !al16(vq) || !al16(ksc) || !al16(vsc)) return fail(NKV_ERR_UNSUPPORTED, "%s: buffers must be 16-byte aligned", what);
+  return NKV_OK;
+}
+
+extern "C" int nkv_attn_decode_tok(const uint16_t* q, const int8_t* kq, const uint16_t* ksc, const int8_t* vq,
+                                   const uint16_t* vsc, int64_t hq, int64_t hkv, int64_t head_dim, int64_t capacity,
+                                   int64_t used, const int64_t* used_dev, uint16_t* out, float* lse_out,
+                                   void* workspace, int64_t workspace_bytes, int64_t n_parts, void* stream) {
+  set_error("");
+  if (int rc = check_heads(hq, hkv, head_dim)) return rc;
+  if (int rc = check_tok_cache("attn_decode_tok", capacity, kq, ksc, vq, vsc)) return rc;
+  if (!q || !out || !workspace) return fail(NKV_ERR_INVALID, "attn_decode_tok: null pointer argument");
+  if (!al16(q) || !al16(workspace)) return fail(NKV_ERR_UNSUPPORTED, "attn_decode_tok: buffers must be 16-byte aligned");
+  if (!used_dev && (used < 0 || used > capacity)) return fail(NKV_ERR_INVALID, "used=%lld outside [0, %lld]", (long long)used, (long long)capacity);
+  const int64_t ngroups = capacity / GT;
+  if (n_parts <= 0) n_parts = default_parts(hkv, used_dev ? ngroups : cdiv(used, GT));
+  AttnArgs a{};
+  a.q = q; a.kq = reinterpret_cast<uint8_t*>(const_cast<int8_t*>(kq)); a.vq = reinterpret_cast<uint8_t*>(const_cast<int8_t*>(vq));
+  a.ksc = const_cast<uint16_t*>(ksc); a.vsc = const_cast<uint16_t*>(vsc); a.tok = 1;
+  a.used_dev = used_dev; a.used = used; a.capacity = capacity; a.ngroups_cap = ngroups;
+  a.hq = (int)hq; a.hkv = (int)hkv; a.gq = (int)(hq / hkv);
+  a.tail_mode = TAIL_NONE;
+  a.sl2 = LOG2E / sqrtf((float)head_dim);
+  a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace);
+  return launch_attn(a, n_parts, workspace_bytes, static_cast<hipStream_t>(stream), "attn_decode_tok");
+}
+
+extern "C" int nkv_append_tok(const uint16_t* k_new, const uint16_t* v_new, int64_t kv_head_stride, int8_t* kq,
+                              uint16_t* ksc, int8_t* vq, uint16_t* vsc, const int64_t* pos_dev, int64_t* written_dev,
+                              int64_t hkv, int64_t head_dim, int64_t capacity, void* stream) {
+  set_error("");
+  if (head_dim != D) return fail(NKV_ERR_UNSUPPORTED, "head_dim %lld: the HIP kernels are built for head_dim 128", (long long)head_dim);
+  if (hkv <= 0) return fail(NKV_ERR_INVALID, "append_tok: bad sizes");
+  if (int rc = check_tok_cache("append_tok", capacity, kq, ksc, vq, vsc)) return rc;
+  if (!k_new || !v_new || !pos_dev || !written_dev) return fail(NKV_ERR_INVALID, "append_tok: null pointer argument");
+  if (!al16(k_new) || !al16(v_new) || kv_head_stride % 8) return fail(NKV_ERR_UNSUPPORTED, "append_tok: buffers must be 16-byte aligned");
+  AttnArgs a{};
+  a.k_new = k_new; a.v_new = v_new; a.kv_hs = kv_head_stride;
+  a.kq = reinterpret_cast<uint8_t*>(kq); a.vq = reinterpret_cast<uint8_t*>(vq); a.ksc = ksc; a.vsc = vsc; a.tok = 1;
+  a.pos_dev = pos_dev; a.written_out = written_dev; a.capacity = capacity; a.hkv = (int)hkv;
+  hipLaunchKernelGGL(append_tok_kernel, dim3((unsigned)hkv), dim3(128), 0, static_cast<hipStream_t>(stream), a);
+  return check_launch("append_tok");
+}
+
+extern "C" int nkv_decode_step_tok(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                                   int64_t kv_head_stride, int8_t* kq, uint16_t* ksc, int8_t* vq, uint16_t* vsc,
+                                   const int64_t* pos_dev, int64_t* written_dev, int64_t hq, int64_t hkv,
+                                   int64_t head_dim, int64_t capacity, uint16_t* out, float* lse_out, void* workspace,
+                                   int64_t workspace_bytes, int64_t n_parts, void* stream) {
+  set_error("");
+  if (int rc = check_heads(hq, hkv, head_dim)) return rc;
+  if (int rc = check_tok_cache("decode_step_tok", capacity, kq, ksc, vq, vsc)) return rc;
+  if (!q || !k_new || !v_new || !pos_dev || !written_dev || !out || !workspace)
+    return fail(NKV_ERR_INVALID, "decode_step_tok: null pointer argument");
+  if (!al16(q) || !al16(k_new) || !al16(v_new) || kv_head_stride % 8 || !al16(workspace))
+    return fail(NKV_ERR_UNSUPPORTED, "decode_step_tok: buffers must be 16-byte aligned");
+  const int64_t ngroups = capacity / GT;
+  if (n_parts <= 0) n_parts = default_parts(hkv, ngroups);
+  AttnArgs a{};
+  a.q = q; a.k_new = k_new; a.v_new = v_new; a.kv_hs = kv_head_stride;
+  a.kq = reinterpret_cast<uint8_t*>(kq); a.vq = reinterpret_cast<uint8_t*>(vq); a.ksc = ksc; a.vsc = vsc; a.tok = 1;
+  a.pos_dev = pos_dev; a.written_out = written_dev;
+  a.capacity = capacity; a.ngroups_cap = ngroups; a.tail_slots = GT;
+  a.hq = (int)hq; a.hkv = (int)hkv; a.gq = (int)(hq / hkv);
+  a.tail_mode = TAIL_FUSED;
+  a.sl2 = LOG2E / sqrtf((float)head_dim);
+  a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace);
+  return launch_attn(a, n_parts, workspace_bytes, static_cast<hipStream_t>(stream), "decode_step_tok");
 }

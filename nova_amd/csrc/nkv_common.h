@@ -43,6 +43,13 @@ __device__ __forceinline__ half2_t codes_to_h2(uint32_t x, uint32_t sel) {
   return as_h2(perm(kBias1024, x, sel)) - k1024;  // exact: integers 0..255
 }
 
+// Signed int8 codes (two's-complement bytes) to fp16, exactly: flipping the sign bit gives
+// code + 128 in 0..255, converted as above, minus 1152.
+__device__ __forceinline__ half2_t scodes_to_h2(uint32_t x, uint32_t sel) {
+  const half2_t k1152 = {(_Float16)1152.0f, (_Float16)1152.0f};
+  return as_h2(perm(kBias1024, x ^ 0x80808080u, sel)) - k1152;
+}
+
 // fp16 <-> fp32 with explicit round-to-nearest-even.
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
@@ -84,6 +91,36 @@ __device__ __forceinline__ uint32_t ruler_code_rcp(float x, float mn, float step
   return (uint32_t)r;
 }
 __device__ __forceinline__ float ruler_inv(float step) { return __builtin_amdgcn_rcpf(step); }
+
+// The per-token symmetric ("tok") arithmetic: scale = max(absmax / 127, 1e-8) in fp32 (stored
+// as fp16), code = clamp(rint(x / scale), -127, 127) with the fp32 scale.
+__device__ __forceinline__ float sym_scale(float amax) { return fmaxf(__fdiv_rn(amax, 127.0f), 1e-8f); }
+__device__ __forceinline__ uint32_t sym_code(float x, float scale) {
+  const float r = fminf(fmaxf(__builtin_rintf(__fdiv_rn(x, scale)), -127.0f), 127.0f);
+  return (uint32_t)(int32_t)r & 0xffu;
+}
+
+// Max over the 16 lanes of each 16-lane row (DPP only).
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false)));
+  return v;
+}
+
+// One 128-value row quantized by the 16 lanes of a 16-lane row, 8 values per lane: returns
+// the lane's 8 packed codes and (in every lane) the fp32 scale.
+__device__ __forceinline__ uint2 sym_quant8(const float (&v)[8], float& scale) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) amax = fmaxf(amax, __builtin_fabsf(v[j]));
+  scale = sym_scale(row16_max(amax));
+  uint32_t c[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) c[j] = sym_code(v[j], scale);
+  return uint2{c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24), c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24)};
+}
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

@@ -294,6 +294,65 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
   store8<OT>(a.out, r * a.o_rs + t * a.dim + c8, v);
 }
 
+// ---------------------------------------------------------------- per-token symmetric ("tok")
+
+// One (slab, token) row of 128 values per 16-lane row: lane l & 15 quantizes values
+// 8 (l & 15) .. + 7 (16-byte loads, 8-byte code stores); a wave covers 4 tokens, a
+// 256-thread workgroup 16. The absmax is reduced with DPP within the 16-lane row.
+struct QuantSymArgs {
+  const void* x;
+  int64_t x_rs;
+  int64_t rows, n;
+  uint8_t* codes;
+  int64_t c_rs;
+  uint16_t* scales;
+  int64_t s_rs;
+  int64_t items;  // rows * n
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) void quant_sym_kernel(QuantSymArgs a) {
+  const int64_t item = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const bool on = item < a.items;  // whole 16-lane rows agree
+  const int c8 = (threadIdx.x & 15) * 8;
+  const int64_t r = on ? item / a.n : 0, t = on ? item % a.n : 0;
+  float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (on) Elem8<DT>::load(a.x, r * a.x_rs + t * 128 + c8, v);
+  float scale;
+  const uint2 cw = sym_quant8(v, scale);
+  if (!on) return;
+  *reinterpret_cast<uint2*>(a.codes + r * a.c_rs + t * 128 + c8) = cw;
+  if (c8 == 0) a.scales[r * a.s_rs + t] = f2h(scale);
+}
+
+struct DequantSymArgs {
+  const uint8_t* codes;
+  int64_t c_rs;
+  const uint16_t* scales;
+  int64_t s_rs;
+  int64_t rows, n;
+  void* out;
+  int64_t o_rs;
+  int64_t items;  // rows * n * 16
+};
+
+template <int OT>
+__global__ __launch_bounds__(256) void dequant_sym_kernel(DequantSymArgs a) {
+  const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= a.items) return;
+  const int c8 = (int)(item % 16) * 8;
+  const int64_t t = (item / 16) % a.n, r = item / (16 * a.n);
+  const uint2 cw = *reinterpret_cast<const uint2*>(a.codes + r * a.c_rs + t * 128 + c8);
+  const float sc = h2f(a.scales[r * a.s_rs + t]);
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int code = (int)(int8_t)(((j < 4 ? cw.x : cw.y) >> (8 * (j & 3))) & 0xffu);
+    v[j] = __fmul_rn((float)code, sc);  // exact in fp32; rounded once by the store
+  }
+  store8<OT>(a.out, r * a.o_rs + t * 128 + c8, v);
+}
+
 // ---------------------------------------------------------------- copy (traffic calibration)
 
 __global__ __launch_bounds__(256) void copy16_kernel(const uint4* __restrict__ src,
@@ -410,6 +469,54 @@ extern "C" int nkv_dequantize_int8(const uint8_t* codes, int64_t codes_row_strid
   else if (out_dtype == NKV_BF16) hipLaunchKernelGGL(dequant_kernel<NKV_BF16>, grid, block, 0, s, a);
   else hipLaunchKernelGGL(dequant_kernel<NKV_F32>, grid, block, 0, s, a);
   return check_launch("dequantize_int8");
+}
+
+extern "C" int nkv_quantize_tok(const void* x, int x_dtype, int64_t x_row_stride, int64_t rows, int64_t n,
+                                int64_t dim, int8_t* codes, int64_t codes_row_stride, uint16_t* scales,
+                                int64_t scale_row_stride, void* stream) {
+  g_err.clear();
+  if (x_dtype != NKV_F16 && x_dtype != NKV_BF16 && x_dtype != NKV_F32)
+    return fail(NKV_ERR_INVALID, "quantize_tok: unknown dtype %d", x_dtype);
+  if (rows < 0 || n < 0 || dim <= 0)
+    return fail(NKV_ERR_INVALID, "quantize_tok: bad sizes rows=%lld n=%lld dim=%lld", (long long)rows,
+                (long long)n, (long long)dim);
+  if (dim != 128) return fail(NKV_ERR_UNSUPPORTED, "quantize_tok: head_dim %lld (only 128 is built)", (long long)dim);
+  if (rows == 0 || n == 0) return NKV_OK;
+  const int esz = x_dtype == NKV_F32 ? 4 : 2;
+  if (!x || !codes || !scales || !aligned16(x) || (reinterpret_cast<uintptr_t>(codes) & 7u) ||
+      (reinterpret_cast<uintptr_t>(scales) & 1u) || (x_row_stride * esz) % 16 || codes_row_stride % 8)
+    return fail(NKV_ERR_UNSUPPORTED, "quantize_tok: buffers or row strides are not aligned");
+  QuantSymArgs a{x, x_row_stride, rows, n, reinterpret_cast<uint8_t*>(codes), codes_row_stride, scales,
+                 scale_row_stride, rows * n};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)cdiv(a.items, 16)), block(256);
+  if (x_dtype == NKV_F16) hipLaunchKernelGGL(quant_sym_kernel<NKV_F16>, grid, block, 0, s, a);
+  else if (x_dtype == NKV_BF16) hipLaunchKernelGGL(quant_sym_kernel<NKV_BF16>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(quant_sym_kernel<NKV_F32>, grid, block, 0, s, a);
+  return check_launch("quantize_tok");
+}
+
+extern "C" int nkv_dequantize_tok(const int8_t* codes, int64_t codes_row_stride, const uint16_t* scales,
+                                  int64_t scale_row_stride, int64_t rows, int64_t n, int64_t dim, void* out,
+                                  int out_dtype, int64_t out_row_stride, void* stream) {
+  g_err.clear();
+  if (out_dtype != NKV_F16 && out_dtype != NKV_BF16 && out_dtype != NKV_F32)
+    return fail(NKV_ERR_INVALID, "dequantize_tok: unknown dtype %d", out_dtype);
+  if (rows < 0 || n < 0 || dim <= 0) return fail(NKV_ERR_INVALID, "dequantize_tok: bad sizes");
+  if (dim != 128) return fail(NKV_ERR_UNSUPPORTED, "dequantize_tok: head_dim %lld (only 128 is built)", (long long)dim);
+  if (rows == 0 || n == 0) return NKV_OK;
+  const int esz = out_dtype == NKV_F32 ? 4 : 2;
+  if (!codes || !scales || !out || (reinterpret_cast<uintptr_t>(codes) & 7u) || codes_row_stride % 8 ||
+      !aligned16(out) || (out_row_stride * esz) % 16)
+    return fail(NKV_ERR_UNSUPPORTED, "dequantize_tok: buffers or row strides are not aligned");
+  DequantSymArgs a{reinterpret_cast<const uint8_t*>(codes), codes_row_stride, scales, scale_row_stride, rows, n,
+                   out, out_row_stride, rows * n * 16};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)cdiv(a.items, 256)), block(256);
+  if (out_dtype == NKV_F16) hipLaunchKernelGGL(dequant_sym_kernel<NKV_F16>, grid, block, 0, s, a);
+  else if (out_dtype == NKV_BF16) hipLaunchKernelGGL(dequant_sym_kernel<NKV_BF16>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(dequant_sym_kernel<NKV_F32>, grid, block, 0, s, a);
+  return check_launch("dequantize_tok");
 }
 
 extern "C" int nkv_copy_bytes(const void* src, void* dst, int64_t nbytes, void* stream) {
