@@ -22,7 +22,10 @@ counters read for the library's plain copy kernel of known size). ``cpu_baseline
 the numpy oracle (dequantize + softmax attention, threads over KV heads) on one layer for
 ~10-30 s and scales to the 36-layer step.
 
-    python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu-baseline] [--scheme t64|tok]
+
+``--scheme tok`` runs the same workload on the per-token symmetric int8 format
+(``KVInt8TokCache``: every token int8 with one fp16 scale per token and KV head).
     python bench.py --traffic-from FETCH_DIR WRITE_DIR   # summarize two rocprofv3 --pmc runs
 """
 
@@ -49,6 +52,9 @@ Q_BYTES = HQ * D * 2
 PREFIX_KERNEL = "attn_prefix_kernel"
 COPY_KERNEL = "copy16_kernel"
 TRAFFIC_FILE = ROOT / "profiles" / "attn_prefix_kernel_32k_traffic.txt"
+TRAFFIC_FILE_TOK = ROOT / "profiles" / "attn_prefix_kernel_tok_32k_traffic.txt"
+# per-token symmetric format: the new token read, its codes and scale written (8 KV heads)
+APPEND_BYTES_TOK = 2 * 128 * 2 * HKV + 2 * 128 * HKV + 2 * 2 * HKV
 
 
 def attn_bytes(u: int) -> int:
@@ -57,6 +63,19 @@ def attn_bytes(u: int) -> int:
     ring tokens (4096 B), q and out (16384 B)."""
     q = u // 64 * 64
     return 2176 * q + 4096 * (u - q) + 16384
+
+
+def attn_bytes_tok(u: int) -> int:
+    """Algorithmic bytes of one layer's decode attention over ``u`` tokens of the per-token
+    symmetric format: int8 codes + one fp16 scale per token, K and V, 8 KV heads (2080 B
+    per token), q and out (16384 B)."""
+    return 2080 * u + 16384
+
+
+def prefix_launch_bytes_tok(u: int) -> int:
+    """One prefix-kernel launch of the per-token symmetric step: the ``u - 1`` tokens before
+    the new one, q, and the append."""
+    return 2080 * max(u - 1, 0) + Q_BYTES + APPEND_BYTES_TOK
 
 
 def prefix_launch_bytes(u: int) -> int:
@@ -77,6 +96,8 @@ def parse_args():
     ap.add_argument("--parts", type=int, default=0, help="work units per KV head (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--scheme", choices=("t64", "tok"), default="t64",
+                    help="KV format: int8t64 (the reference's) or per-token symmetric")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarize two rocprofv3 --pmc runs of this script into the traffic file")
     return ap.parse_args()
@@ -102,7 +123,7 @@ def _pmc_means(run_dir: str, counter: str) -> dict:
     return {k: sum(v) / len(v) for k, v in acc.items()}
 
 
-def write_traffic(fetch_dir: str, write_dir: str) -> None:
+def write_traffic(fetch_dir: str, write_dir: str, scheme: str = "t64") -> None:
     """Traffic of the prefix kernel from FETCH_SIZE and WRITE_SIZE (KiB per dispatch),
     each scaled by the factor that makes the same counter read the copy kernel's known
     byte count (COPY_BYTES read and written)."""
@@ -111,13 +132,16 @@ def write_traffic(fetch_dir: str, write_dir: str) -> None:
     w_scale = COPY_BYTES / (write[COPY_KERNEL] * 1024)
     f_bytes = fetch[PREFIX_KERNEL] * 1024 * f_scale
     w_bytes = write[PREFIX_KERNEL] * 1024 * w_scale
-    alg = prefix_launch_bytes(CTX + 1)
+    tok = scheme == "tok"
+    alg = prefix_launch_bytes_tok(CTX + 1) if tok else prefix_launch_bytes(CTX + 1)
+    flag = " --scheme tok" if tok else ""
     lines = [
-        "# HBM traffic of nkv::attn_prefix_kernel, 32k-context decode step (36 layers, 32 q / 8 kv heads)",
+        f"# HBM traffic of nkv::attn_prefix_kernel ({'per-token symmetric' if tok else 'int8t64'} format), "
+        "32k-context decode step (36 layers, 32 q / 8 kv heads)",
         "# made by (rocprofv3 --pmc runs of bench.py, then this summary):",
-        "#   rocprofv3 --pmc FETCH_SIZE -d FETCH_DIR -o run --output-format csv -- python3 bench.py --steps 4 --warmup 1 --no-cpu-baseline",
-        "#   rocprofv3 --pmc WRITE_SIZE -d WRITE_DIR -o run --output-format csv -- python3 bench.py --steps 4 --warmup 1 --no-cpu-baseline",
-        "#   python3 bench.py --traffic-from FETCH_DIR WRITE_DIR",
+        f"#   rocprofv3 --pmc FETCH_SIZE -d FETCH_DIR -o run --output-format csv -- python3 bench.py --steps 4 --warmup 1 --no-cpu-baseline{flag}",
+        f"#   rocprofv3 --pmc WRITE_SIZE -d WRITE_DIR -o run --output-format csv -- python3 bench.py --steps 4 --warmup 1 --no-cpu-baseline{flag}",
+        f"#   python3 bench.py --traffic-from FETCH_DIR WRITE_DIR{flag}",
         f"copy_kernel_bytes: {COPY_BYTES}  (read, and again written, by nkv_copy_bytes)",
         f"copy_kernel_FETCH_SIZE_KiB: {fetch[COPY_KERNEL]:.1f}  -> fetch scale {f_scale:.4f}",
         f"copy_kernel_WRITE_SIZE_KiB: {write[COPY_KERNEL]:.1f}  -> write scale {w_scale:.4f}",
@@ -130,20 +154,20 @@ def write_traffic(fetch_dir: str, write_dir: str) -> None:
     if "attn_tail_kernel" in fetch and "attn_tail_kernel" in write:
         lines.append(f"tail_kernel_traffic_bytes_per_launch: "
                      f"{fetch['attn_tail_kernel'] * 1024 * f_scale + write['attn_tail_kernel'] * 1024 * w_scale:.0f}")
-    TRAFFIC_FILE.write_text("\n".join(lines) + "\n")
+    (TRAFFIC_FILE_TOK if tok else TRAFFIC_FILE).write_text("\n".join(lines) + "\n")
     print("\n".join(lines))
 
 
-def read_traffic():
+def read_traffic(path: Path = TRAFFIC_FILE):
     """HBM bytes per launch of the prefix kernel from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), or None."""
-    if not TRAFFIC_FILE.exists():
+    if not path.exists():
         return None
-    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", TRAFFIC_FILE.read_text(), re.M)
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text(), re.M)
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(budget_s: float) -> dict:
+def cpu_baseline(budget_s: float, scheme: str = "t64") -> dict:
     """Time the numpy oracle's decode step for one layer at 32k context: dequantize the
     int8 prefix with the stored rulers, softmax attention over prefix + ring. Threads run
     the 8 KV heads in parallel (numpy releases the GIL inside its kernels)."""
@@ -156,8 +180,13 @@ def cpu_baseline(budget_s: float) -> dict:
     n = CTX
     k = rng.standard_normal((HKV, n, D), dtype=np.float32).astype(np.float16)
     v = rng.standard_normal((HKV, n, D), dtype=np.float32).astype(np.float16)
-    kq, kmn, kst = okq.quantize_int8_token(k, 64)
-    vq, vmn, vst = okq.quantize_int8_token(v, 64)
+    tok = scheme == "tok"
+    if tok:
+        kq, ks = okq.quantize_tok(k)
+        vq, vs = okq.quantize_tok(v)
+    else:
+        kq, kmn, kst = okq.quantize_int8_token(k, 64)
+        vq, vmn, vst = okq.quantize_int8_token(v, 64)
     ring_k = k[:, -64:].copy()
     ring_v = v[:, -64:].copy()
     q = (rng.standard_normal((HQ, D)) / D ** 0.5).astype(np.float16)
@@ -165,8 +194,12 @@ def cpu_baseline(budget_s: float) -> dict:
     threads = min(HKV, os.cpu_count() or 1)
 
     def head(h):
-        k16 = okq.dequantize_int8_token(kq[h:h + 1], kmn[h:h + 1], kst[h:h + 1], 64)[0]
-        v16 = okq.dequantize_int8_token(vq[h:h + 1], vmn[h:h + 1], vst[h:h + 1], 64)[0]
+        if tok:
+            k16 = okq.dequantize_tok(kq[h], ks[h])
+            v16 = okq.dequantize_tok(vq[h], vs[h])
+        else:
+            k16 = okq.dequantize_int8_token(kq[h:h + 1], kmn[h:h + 1], kst[h:h + 1], 64)[0]
+            v16 = okq.dequantize_int8_token(vq[h:h + 1], vmn[h:h + 1], vst[h:h + 1], 64)[0]
         kk = np.concatenate([k16, ring_k[h, :1]], 0)
         vv = np.concatenate([v16, ring_v[h, :1]], 0)
         return oattn.attend_fp16_kv(q[h * gq:(h + 1) * gq], kk[None], vv[None])[0]
@@ -183,7 +216,7 @@ def cpu_baseline(budget_s: float) -> dict:
     per_layer = el / reps
     per_step = per_layer * LAYERS
     return {"value": 1.0 / per_step, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"numpy oracle, 1 layer x {reps} decode steps at {CTX} ctx ({el:.1f} s), "
+            "sample": f"numpy oracle ({scheme}), 1 layer x {reps} decode steps at {CTX} ctx ({el:.1f} s), "
                       f"scaled x{LAYERS} layers (extrapolated)",
             "seconds_per_step": per_step}
 
@@ -194,7 +227,7 @@ COPY_BYTES = 64 << 20
 def main() -> int:
     args = parse_args()
     if args.traffic_from:
-        write_traffic(*args.traffic_from)
+        write_traffic(*args.traffic_from, scheme=args.scheme)
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported on this path "
@@ -205,6 +238,7 @@ def main() -> int:
 
     from nova_amd import _lib
     from nova_amd.kvattn import KVInt8Cache
+    from nova_amd.kvtok import KVInt8TokCache
 
     _lib.load()
     dev = torch.device("cuda:0")
@@ -214,7 +248,9 @@ def main() -> int:
 
     # ---- prefill: seeded N(0,1) K/V, 4 random K channels per head x8, quantized by the
     # bulk HIP quantizer into the cache (staging area -> finish_prefill)
-    cache = KVInt8Cache(num_slots=L, num_kv_heads=HKV, head_dim=D, max_len=max_len, num_q_heads=HQ, device=dev)
+    tok = args.scheme == "tok"
+    cls = KVInt8TokCache if tok else KVInt8Cache
+    cache = cls(num_slots=L, num_kv_heads=HKV, head_dim=D, max_len=max_len, num_q_heads=HQ, device=dev)
     if args.parts:
         cache._n_parts = args.parts
     gen = torch.Generator(device=dev).manual_seed(2)
@@ -287,10 +323,11 @@ def main() -> int:
         torch.cuda.synchronize()
         return s0.elapsed_time(s1)
 
-    g_prefix, keep = kernel_graph("nkv_decode_step_partials_t64", True)
+    sfx = "tok" if tok else "t64"
+    g_prefix, keep = kernel_graph(f"nkv_decode_step_partials_{sfx}", True)
     pos_a = int(cache.pos.item()) + W
     ms_prefix = time_graph(g_prefix)
-    g_tail, keep2 = kernel_graph("nkv_decode_step_combine_t64", False)
+    g_tail, keep2 = kernel_graph(f"nkv_decode_step_combine_{sfx}", False)
     ms_tail = time_graph(g_tail)
     del keep, keep2
 
@@ -303,12 +340,15 @@ def main() -> int:
     ms_step = ms / K
     tok_s = K / (ms / 1e3)
     us = [pos0 + i + 1 for i in range(K)]  # tokens written when each timed step attends
-    step_bytes = sum(attn_bytes(u) + APPEND_BYTES for u in us) / K * L
+    if tok:
+        step_bytes = sum(attn_bytes_tok(u) + APPEND_BYTES_TOK for u in us) / K * L
+    else:
+        step_bytes = sum(attn_bytes(u) + APPEND_BYTES for u in us) / K * L
     ua = [pos_a + i + 1 for i in range(K)]  # the same for the prefix-kernel graph's replays
-    launch_bytes = sum(prefix_launch_bytes(u) for u in ua) / K
+    launch_bytes = sum((prefix_launch_bytes_tok if tok else prefix_launch_bytes)(u) for u in ua) / K
     per_launch_s = ms_prefix / 1e3 / (K * L)
     achieved = launch_bytes / per_launch_s / 1e9
-    traffic = read_traffic()
+    traffic = read_traffic(TRAFFIC_FILE_TOK if tok else TRAFFIC_FILE)
     out = {
         "metric": "int8-KV decode attention tokens/s + achieved HBM GB/s (% of peak) at 32k ctx",
         "value": round(tok_s, 2),
@@ -323,10 +363,12 @@ def main() -> int:
         "dtype": "fp16",
         "data": "synthetic",
         "config": {
-            "workload": f"int8t64 KV decode step, {L} layers x (32 q / 8 kv heads, head_dim 128), batch 1, "
+            "workload": f"{'per-token symmetric int8' if tok else 'int8t64'} KV decode step, {L} layers x "
+                        f"(32 q / 8 kv heads, head_dim 128), batch 1, "
                         f"{ctx}-token prefilled cache, {K} hipGraph-replayed steps",
             "layers": L, "context": ctx, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "batch": 1,
-            "kv_format": "int8t64 (uint8 codes, fp16 min/step per 64 tokens per channel)",
+            "kv_format": ("tok (int8 codes, one fp16 absmax scale per token and KV head)" if tok
+                          else "int8t64 (uint8 codes, fp16 min/step per 64 tokens per channel)"),
             "parts_per_head": cache._n_parts,
         },
         "step_gbs": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
@@ -339,7 +381,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "nkv::attn_prefix_kernel (append + split-K partials over the int8 prefix)",
+            "kernel": f"nkv::attn_prefix_kernel<{'true' if tok else 'false'}> (append + split-K partials over the int8 prefix)",
             "algorithmic_bytes_per_launch": round(launch_bytes),
             "avg_launch_us": round(per_launch_s * 1e6, 3),
         },
@@ -349,7 +391,7 @@ def main() -> int:
         },
     }
     if not args.no_cpu_baseline:
-        cb = cpu_baseline(args.cpu_seconds)
+        cb = cpu_baseline(args.cpu_seconds, args.scheme)
         cb.pop("seconds_per_step")
         out["cpu_baseline"] = cb
     else:

@@ -252,6 +252,21 @@ int nkv_decode_step_tok(const uint16_t* q, const uint16_t* k_new, const uint16_t
                         int64_t head_dim, int64_t capacity, uint16_t* out, float* lse_out,
                         void* workspace, int64_t workspace_bytes, int64_t n_parts, void* stream);
 
+/* The two launches of nkv_decode_step_tok as separate calls with the same arguments, as
+ * nkv_decode_step_partials_t64 / _combine_t64 are for the int8t64 step. */
+int nkv_decode_step_partials_tok(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                                 int64_t kv_head_stride, int8_t* kq, uint16_t* ksc, int8_t* vq,
+                                 uint16_t* vsc, const int64_t* pos_dev, int64_t* written_dev, int64_t hq,
+                                 int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out,
+                                 float* lse_out, void* workspace, int64_t workspace_bytes,
+                                 int64_t n_parts, void* stream);
+int nkv_decode_step_combine_tok(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                                int64_t kv_head_stride, int8_t* kq, uint16_t* ksc, int8_t* vq,
+                                uint16_t* vsc, const int64_t* pos_dev, int64_t* written_dev, int64_t hq,
+                                int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out,
+                                float* lse_out, void* workspace, int64_t workspace_bytes,
+                                int64_t n_parts, void* stream);
+
 /*
  * Plain device copy (16-byte vector loads and stores). Used to calibrate the
  * HBM traffic counters (FETCH_SIZE / WRITE_SIZE) against a known byte count;

@@ -34,6 +34,9 @@ I64 = c_int64
 # q, k_new, v_new, kv_head_stride, kq, kmn, kst, vq, vmn, vst, tail_k, tail_v, pos, first, written,
 # qlen, pg, hq, hkv, head_dim, capacity, out, lse, workspace, workspace_bytes, n_parts, stream
 _STEP = [P, P, P, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, P, P, P, I64, I64, P]
+# q, k_new, v_new, kv_head_stride, kq, ksc, vq, vsc, pos, written, hq, hkv, head_dim, capacity, out,
+# lse, workspace, workspace_bytes, n_parts, stream
+_STEP_TOK = [P, P, P, I64, P, P, P, P, P, P, I64, I64, I64, I64, P, P, P, I64, I64, P]
 
 SIGNATURES = {
     "nkv_abi_version": (c_int, []),
@@ -54,7 +57,9 @@ SIGNATURES = {
     "nkv_dequantize_tok": (c_int, [P, I64, P, I64, I64, I64, I64, P, c_int, I64, P]),
     "nkv_attn_decode_tok": (c_int, [P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P, P, I64, I64, P]),
     "nkv_append_tok": (c_int, [P, P, I64, P, P, P, P, P, P, I64, I64, I64, P]),
-    "nkv_decode_step_tok": (c_int, [P, P, P, I64, P, P, P, P, P, P, I64, I64, I64, I64, P, P, P, I64, I64, P]),
+    "nkv_decode_step_tok": (c_int, _STEP_TOK),
+    "nkv_decode_step_partials_tok": (c_int, _STEP_TOK),
+    "nkv_decode_step_combine_tok": (c_int, _STEP_TOK),
     "nkv_copy_bytes": (c_int, [P, P, I64, P]),
     "nkv_read_bw": (c_int, [P, I64, P, I64, P]),
 }

@@ -1422,11 +1422,11 @@ extern "C" int nkv_append_tok(const uint16_t* k_new, const uint16_t* v_new, int6
   return check_launch("append_tok");
 }
 
-extern "C" int nkv_decode_step_tok(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
-                                   int64_t kv_head_stride, int8_t* kq, uint16_t* ksc, int8_t* vq, uint16_t* vsc,
-                                   const int64_t* pos_dev, int64_t* written_dev, int64_t hq, int64_t hkv,
-                                   int64_t head_dim, int64_t capacity, uint16_t* out, float* lse_out, void* workspace,
-                                   int64_t workspace_bytes, int64_t n_parts, void* stream) {
+static int decode_step_tok(const char* what, int launches, const uint16_t* q, const uint16_t* k_new,
+                           const uint16_t* v_new, int64_t kv_head_stride, int8_t* kq, uint16_t* ksc, int8_t* vq,
+                           uint16_t* vsc, const int64_t* pos_dev, int64_t* written_dev, int64_t hq, int64_t hkv,
+                           int64_t head_dim, int64_t capacity, uint16_t* out, float* lse_out, void* workspace,
+                           int64_t workspace_bytes, int64_t n_parts, void* stream) {
   set_error("");
   if (int rc = check_heads(hq, hkv, head_dim)) return rc;
   if (int rc = check_tok_cache("decode_step_tok", capacity, kq, ksc, vq, vsc)) return rc;
@@ -1445,5 +1445,24 @@ extern "C" int nkv_decode_step_tok(const uint16_t* q, const uint16_t* k_new, con
   a.tail_mode = TAIL_FUSED;
   a.sl2 = LOG2E / sqrtf((float)head_dim);
   a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace);
-  return launch_attn(a, n_parts, workspace_bytes, static_cast<hipStream_t>(stream), "decode_step_tok");
+  return launch_attn(a, n_parts, workspace_bytes, static_cast<hipStream_t>(stream), what, launches);
+}
+
+#define NKV_STEP_TOK_PARAMS                                                                                      \
+  const uint16_t *q, const uint16_t *k_new, const uint16_t *v_new, int64_t kv_head_stride, int8_t *kq,          \
+      uint16_t *ksc, int8_t *vq, uint16_t *vsc, const int64_t *pos_dev, int64_t *written_dev, int64_t hq,        \
+      int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t *out, float *lse_out, void *workspace,          \
+      int64_t workspace_bytes, int64_t n_parts, void *stream
+#define NKV_STEP_TOK_ARGS                                                                                        \
+  q, k_new, v_new, kv_head_stride, kq, ksc, vq, vsc, pos_dev, written_dev, hq, hkv, head_dim, capacity, out,   \
+      lse_out, workspace, workspace_bytes, n_parts, stream
+
+extern "C" int nkv_decode_step_tok(NKV_STEP_TOK_PARAMS) {
+  return decode_step_tok("decode_step_tok", LAUNCH_PREFIX | LAUNCH_TAIL, NKV_STEP_TOK_ARGS);
+}
+extern "C" int nkv_decode_step_partials_tok(NKV_STEP_TOK_PARAMS) {
+  return decode_step_tok("decode_step_partials_tok", LAUNCH_PREFIX, NKV_STEP_TOK_ARGS);
+}
+extern "C" int nkv_decode_step_combine_tok(NKV_STEP_TOK_PARAMS) {
+  return decode_step_tok("decode_step_combine_tok", LAUNCH_TAIL, NKV_STEP_TOK_ARGS);
 }

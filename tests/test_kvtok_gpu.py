@@ -206,3 +206,30 @@ def test_tok_graph_replay_equals_eager():
         assert torch.equal(g.merged, want), p
     for nm in ("kq", "vq", "ksc", "vsc"):
         assert torch.equal(getattr(e, nm)[0], getattr(g, nm)[0]), nm
+
+
+def test_tok_partials_then_combine_equals_fused_step():
+    from nova_amd import _lib
+    from nova_amd.kvtok import KVInt8TokCache
+
+    n0 = 130
+    _, k, v = make(n0 + 5, seed=26)
+    q = randn((1, HQ, 1, D), 27).cuda()
+    k, v = k.cuda(), v.cuda()
+    a, b = KVInt8TokCache(1, H_KV, D, 192, HQ), KVInt8TokCache(1, H_KV, D, 192, HQ)
+    for c in (a, b):
+        c.begin_prefill(n0)
+        c.set_prefill_pos(0)
+        c.update(k[:, :, :n0], v[:, :, :n0], 0)
+        c.finish_prefill(n0)
+    for p in range(n0, n0 + 5):
+        a.pos.fill_(p)
+        b.pos.fill_(p)
+        oa = a.update_attend(k[:, :, p:p + 1], v[:, :, p:p + 1], q, 0).clone()
+        args = b.step_args(k[:, :, p:p + 1], v[:, :, p:p + 1], q, 0)
+        _lib.call("nkv_decode_step_partials_tok", *args)
+        _lib.call("nkv_decode_step_combine_tok", *args)
+        assert torch.equal(oa, b.merged), p
+        assert torch.equal(a.lse, b.lse), p
+        for nm in ("kq", "vq", "ksc", "vsc"):
+            assert torch.equal(getattr(a, nm)[0], getattr(b, nm)[0]), (p, nm)
