@@ -268,6 +268,52 @@ int nkv_decode_step_combine_tok(const uint16_t* q, const uint16_t* k_new, const 
                                 int64_t n_parts, void* stream);
 
 /*
+ * ---- Paged batch of ragged sequences (int8t64) ----
+ * No counterpart in the reference, which decodes one sequence and pads lengths to
+ * power-of-two buckets with an additive -inf mask (src/nova/decode.py:39-48, 200-205);
+ * here each sequence is attended over exactly its own tokens, which equals that masked
+ * computation without reading the padding. The per-sequence arithmetic is the int8t64
+ * step's (nkv_decode_step_t64).
+ * pages: uint8 [num_pages][hkv][17408], one page = one 64-token group of one KV head:
+ *   K codes [64][128], V codes [64][128], then fp16 kst[128], kmn[128], vst[128], vmn[128].
+ * page_table: int32 [nseq][table_stride], group g of sequence b lives in page
+ *   page_table[b * table_stride + g] (the same ids in every layer's pool).
+ * rings: fp16 [nseq][hkv][2][64][128] (K then V; slot = position mod 64).
+ * pos_dev: int64 [nseq], the position each sequence appends at this step.
+ * k_new / v_new: [nseq][hkv][128] fp16 with strides kv_seq_stride / kv_head_stride.
+ * Prefix work unit w (w < total_parts) serves sequence wg_map[w] >> 16, part
+ * wg_map[w] & 0xffff of its seq_parts[2b + 1] parts; seq_parts[2b] is its first unit.
+ * q / out: [nseq][hq][128] fp16; lse_out [nseq][hq] fp32 (may be NULL).
+ */
+int64_t nkv_paged_workspace_bytes(int64_t hkv, int64_t hq, int64_t total_parts);
+
+/* Append of one token per sequence: ring slot pos % 64, requantization of the ring into
+ * the sequence's page of group pos / 64 (which must be assigned). */
+int nkv_paged_append_t64(const uint16_t* k_new, const uint16_t* v_new, int64_t kv_seq_stride,
+                         int64_t kv_head_stride, uint8_t* pages, const int32_t* page_table,
+                         int64_t table_stride, uint16_t* rings, const int64_t* pos_dev, int64_t nseq,
+                         int64_t hkv, int64_t head_dim, void* stream);
+
+/* Decode attention of every sequence over its whole groups before pos and its ring
+ * (tokens up to and including pos). Two launches: the prefix kernel (total_parts * hkv
+ * workgroups), then the tail kernel (nseq * hkv workgroups). */
+int nkv_paged_attn_decode_t64(const uint16_t* q, const uint8_t* pages, const int32_t* page_table,
+                              int64_t table_stride, const uint16_t* rings, const int64_t* pos_dev,
+                              int64_t nseq, int64_t hq, int64_t hkv, int64_t head_dim,
+                              const int32_t* wg_map, const int32_t* seq_parts, int64_t total_parts,
+                              uint16_t* out, float* lse_out, void* workspace, int64_t workspace_bytes,
+                              void* stream);
+
+/* nkv_paged_append_t64 then nkv_paged_attn_decode_t64. */
+int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                              int64_t kv_seq_stride, int64_t kv_head_stride, uint8_t* pages,
+                              const int32_t* page_table, int64_t table_stride, uint16_t* rings,
+                              const int64_t* pos_dev, int64_t nseq, int64_t hq, int64_t hkv,
+                              int64_t head_dim, const int32_t* wg_map, const int32_t* seq_parts,
+                              int64_t total_parts, uint16_t* out, float* lse_out, void* workspace,
+                              int64_t workspace_bytes, void* stream);
+
+/*
  * Plain device copy (16-byte vector loads and stores). Used to calibrate the
  * HBM traffic counters (FETCH_SIZE / WRITE_SIZE) against a known byte count;
  * no counterpart in the reference. nbytes must be a multiple of 16.

@@ -60,6 +60,11 @@ SIGNATURES = {
     "nkv_decode_step_tok": (c_int, _STEP_TOK),
     "nkv_decode_step_partials_tok": (c_int, _STEP_TOK),
     "nkv_decode_step_combine_tok": (c_int, _STEP_TOK),
+    "nkv_paged_workspace_bytes": (I64, [I64, I64, I64]),
+    "nkv_paged_append_t64": (c_int, [P, P, I64, I64, P, P, I64, P, P, I64, I64, I64, P]),
+    "nkv_paged_attn_decode_t64": (c_int, [P, P, P, I64, P, P, I64, I64, I64, I64, P, P, I64, P, P, P, I64, P]),
+    "nkv_paged_decode_step_t64": (c_int, [P, P, P, I64, I64, P, P, I64, P, P, I64, I64, I64, I64, P, P, I64, P, P,
+                                          P, I64, P]),
     "nkv_copy_bytes": (c_int, [P, P, I64, P]),
     "nkv_read_bw": (c_int, [P, I64, P, I64, P]),
 }

@@ -62,6 +62,10 @@ constexpr int WAVE_LDS_TOK = 2 * HALF_SLOT_TOK;
 constexpr int LDS_BYTES_TOK = WAVES * WAVE_LDS_TOK;        // 130 KiB
 constexpr int DMA_HALF_TOK = 2 * (HALF_CODE / 1024) + 2;
 constexpr int RING_BYTES = GT * D * 2;                    // one fp16 ring tensor of one head
+// paged layout: one page = one 64-token group of one KV head, K codes | V codes | kst | kmn | vst | vmn
+constexpr int PAGE_BYTES = 2 * CODE_BYTES + RULER_BYTES;  // 17 KiB, a multiple of 128
+constexpr int DMA_FIRST_HALF_PAGED = 2 * (HALF_CODE / 1024) + 1;  // the rulers are one 1 KiB load
+enum Layout : int { CONTIG_T64 = 0, CONTIG_TOK = 1, PAGED_T64 = 2 };
 constexpr float P_SCALE = 32768.0f;       // 2^15
 constexpr float INV_P_SCALE = 1.0f / 32768.0f;
 constexpr float LOG2E = 1.4426950408889634f;
@@ -104,6 +108,17 @@ struct AttnArgs {
   uint16_t* ksc;  // per-token symmetric format: fp16 scales [hkv, capacity]
   uint16_t* vsc;
   int tok;        // 1: per-token symmetric int8 codes and scales, 0: int8t64
+  // paged batch (int8t64): pages [num_pages][hkv][PAGE_BYTES], page table [nseq][table_stride],
+  // rings [nseq][hkv][K, V][64][D], pos_dev [nseq]; prefix work unit w serves sequence
+  // wg_map[w] >> 16, part wg_map[w] & 0xffff of seq_parts[2b + 1] starting at unit seq_parts[2b]
+  uint8_t* pages;
+  const int32_t* table;
+  int64_t table_stride;
+  uint16_t* rings;
+  const int32_t* wg_map;
+  const int32_t* seq_parts;
+  int nseq, total_parts;
+  int64_t kv_ss;  // k_new / v_new sequence stride (elements)
   int64_t kv_hs;
   int64_t used, pg;  // host values when the device pointers are null
   int64_t capacity, ngroups_cap;
@@ -182,12 +197,12 @@ __device__ __forceinline__ half8_t dq8_splat(uint32_t w0, uint32_t w1, half2_t s
 
 // Q as the B operand of v_mfma_f32_16x16x32_f16: lane (c, g) holds head c's dims
 // 16g + 64hh + 8e + [0..7] for k-step 2hh + e (zeros for c >= gq).
-__device__ __forceinline__ void load_q(const AttnArgs& a, int h, half8_t (&qb)[4]) {
+__device__ __forceinline__ void load_q(const uint16_t* qh, int gq, half8_t (&qb)[4]) {
   const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     uint4 w = {0, 0, 0, 0};
-    if (c < a.gq) w = *reinterpret_cast<const uint4*>(a.q + (int64_t)(h * a.gq + c) * D + 16 * g + 64 * (k >> 1) + 8 * (k & 1));
+    if (c < gq) w = *reinterpret_cast<const uint4*>(qh + c * D + 16 * g + 64 * (k >> 1) + 8 * (k & 1));
     qb[k] = as_h8(w);
   }
   // Make the compiler complete these loads here, before the untracked LDS streams start:
@@ -274,11 +289,35 @@ __device__ __forceinline__ void issue_half_tok(const AttnArgs& a, int h, int64_t
   if (lane < 4) dma16(uniform_ptr(a.vsc + (int64_t)h * a.capacity + t0), 16u * lane, slot + 2 * HALF_CODE + TOK_SCALE_BYTES);
 }
 
-// Q of KV head h (gq rows of 256 bytes) into LDS at `dst`, by one wave.
-__device__ __forceinline__ void issue_q(const AttnArgs& a, int h, uint32_t dst) {
+// The paged layout's half group: the group's page holds K code rows, V code rows and the
+// four rulers contiguously; 4 + 4 loads of code rows and, with hf == 0, one 1 KiB load of
+// the rulers (kst | kmn | vst | vmn, the order of a ruler set in LDS).
+__device__ __forceinline__ void issue_half_paged(const AttnArgs& a, int b, int h, int64_t grp, int hf, uint32_t slot,
+                                                 uint32_t rs) {
   const int lane = threadIdx.x & 63;
-  const int bytes = a.gq * D * 2;
-  const void* qg = uniform_ptr(a.q + (int64_t)h * a.gq * D);
+  const int32_t page = a.table[(int64_t)b * a.table_stride + grp];
+  const uint8_t* base = a.pages + ((int64_t)page * a.hkv + h) * PAGE_BYTES;
+  const void* pb = uniform_ptr(base);
+  slot = __builtin_amdgcn_readfirstlane(slot);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // earlier reads of this slot are done
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    dma16(pb, (uint32_t)((32 * hf + row) * D + (((lane & 7) ^ swz(row)) << 4)), slot + 1024 * j);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    dma16(pb, (uint32_t)(CODE_BYTES + (32 * hf + row) * D + (((lane & 7) ^ swz(row)) << 4)), slot + HALF_CODE + 1024 * j);
+  }
+  if (hf == 0) dma16(pb, (uint32_t)(2 * CODE_BYTES + 16 * lane), __builtin_amdgcn_readfirstlane(rs));
+}
+
+// Q of KV head h (gq rows of 256 bytes) into LDS at `dst`, by one wave.
+__device__ __forceinline__ void issue_q(const uint16_t* qh, int gq, uint32_t dst) {
+  const int lane = threadIdx.x & 63;
+  const int bytes = gq * D * 2;
+  const void* qg = uniform_ptr(qh);
   for (int k = 0; k < bytes; k += 1024)
     if (k + 16 * lane < bytes) dma16(qg, (uint32_t)(k + 16 * lane), dst + k);
 }
@@ -685,30 +724,68 @@ constexpr int UNIT_CH = 8;
 constexpr int APPEND_UNITS = 2 * D / UNIT_CH;
 constexpr int UNIT_SRC_BYTES = (GT + 1) * UNIT_CH * 2;
 
-__device__ __forceinline__ void issue_unit_rows(const AttnArgs& a, int h, int unit, uint32_t src) {
-  const int lane = threadIdx.x & 63, which = unit / (D / UNIT_CH), ch0 = unit % (D / UNIT_CH) * UNIT_CH;
-  dma16(uniform_ptr(ring_of(a, h, which) + ch0), (uint32_t)(lane * D * 2), src);
-  if (lane == 0) dma16(uniform_ptr(fresh_of(a, h, which) + ch0), 0u, src + GT * UNIT_CH * 2);
+// Where one append unit reads and writes: the ring rows and the new token of one tensor of
+// one head, and the current group's code rows and ruler rows of that tensor.
+struct UnitIO {
+  const uint16_t* ring;   // [64][D] fp16, row stride D
+  const uint16_t* fresh;  // [D] fp16
+  uint8_t* codes;         // the group's row 0 (row stride D)
+  int code_rows;          // rows stored (the cache capacity can end inside the group)
+  uint16_t* mn;           // the group's [D] ruler rows
+  uint16_t* st;
+};
+
+// A unit of the contiguous layout: unit u covers channels 8 (u % 16) .. + 7 of tensor u / 16.
+__device__ __forceinline__ UnitIO unit_io(const AttnArgs& a, int h, int unit, int64_t pos) {
+  const int which = unit / (D / UNIT_CH);
+  const int64_t gcur = pos / GT, ro = ((int64_t)h * a.ngroups_cap + gcur) * D;
+  UnitIO io;
+  io.ring = ring_of(a, h, which);
+  io.fresh = fresh_of(a, h, which);
+  io.codes = (which == 0 ? a.kq : a.vq) + ((int64_t)h * a.capacity + gcur * GT) * D;
+  io.code_rows = (int)min<int64_t>(GT, a.capacity - gcur * GT);
+  io.mn = (which == 0 ? a.kmn : a.vmn) + ro;
+  io.st = (which == 0 ? a.kst : a.vst) + ro;
+  return io;
+}
+
+// A unit of the paged layout: sequence b's ring and page of the current group.
+__device__ __forceinline__ UnitIO unit_io_paged(const AttnArgs& a, int b, int h, int unit, int64_t pos) {
+  const int which = unit / (D / UNIT_CH);
+  const int32_t page = a.table[(int64_t)b * a.table_stride + pos / GT];
+  uint8_t* base = a.pages + ((int64_t)page * a.hkv + h) * PAGE_BYTES;
+  UnitIO io;
+  io.ring = a.rings + (((int64_t)b * a.hkv + h) * 2 + which) * GT * D;
+  io.fresh = (which == 0 ? a.k_new : a.v_new) + (int64_t)b * a.kv_ss + (int64_t)h * a.kv_hs;
+  io.codes = base + which * CODE_BYTES;
+  io.code_rows = GT;
+  io.st = reinterpret_cast<uint16_t*>(base + 2 * CODE_BYTES) + which * 2 * D;
+  io.mn = io.st + D;
+  return io;
+}
+
+__device__ __forceinline__ void issue_unit_rows(const UnitIO& io, int unit, uint32_t src) {
+  const int lane = threadIdx.x & 63, ch0 = unit % (D / UNIT_CH) * UNIT_CH;
+  dma16(uniform_ptr(io.ring + ch0), (uint32_t)(lane * D * 2), src);
+  if (lane == 0) dma16(uniform_ptr(io.fresh + ch0), 0u, src + GT * UNIT_CH * 2);
 }
 
 __device__ __forceinline__ float ror8(float v) {  // lane l <- lane l ^ 8 within each 16-lane row
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
 }
 
-// Requantization of append unit `unit` of head h for the token at `pos`, once its source
-// rows are in `src` (LDS, visible to the workgroup): the ring with the new token in slot
-// pos % 64 is ruled per channel over all 64 slots into group pos / 64 exactly as the bulk
-// quantizer rules a group, and the group's codes and rulers and the new ring slot are
-// stored. Thread t takes channel t & 7 of the unit and ring rows (t >> 3) + 8 WAVES i.
+// Requantization of append unit `unit` for the token at `pos`, once its source rows are in
+// `src` (LDS, visible to the workgroup): the ring with the new token in slot pos % 64 is
+// ruled per channel over all 64 slots into the current group exactly as the bulk quantizer
+// rules a group, and the group's codes and rulers and the new ring slot are stored through
+// `io`. Thread t takes channel t & 7 of the unit and ring rows (t >> 3) + 8 WAVES i.
 // `xch` is 8 x 2 WAVES floats of LDS; one workgroup barrier inside.
-__device__ __forceinline__ void append_unit(const AttnArgs& a, int h, int unit, int64_t pos, const uint16_t* src,
-                                            float* xch) {
+__device__ __forceinline__ void append_unit(const UnitIO& io, int unit, int64_t pos, const uint16_t* src, float* xch) {
   constexpr int RPT = GT / (8 * WAVES);  // ring rows per thread
   static_assert(RPT * 8 * WAVES == GT, "8 WAVES must divide the 64 ring rows");
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, r0 = t >> 3, c = t & 7;
-  const int which = unit / (D / UNIT_CH), ch = unit % (D / UNIT_CH) * UNIT_CH + c;
+  const int ch = unit % (D / UNIT_CH) * UNIT_CH + c;
   const int slot = (int)(pos % GT);
-  const int64_t gcur = pos / GT;
   uint16_t bits[RPT];
   float v[RPT];
   float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
@@ -732,18 +809,15 @@ __device__ __forceinline__ void append_unit(const AttnArgs& a, int h, int unit, 
     hi = fmaxf(hi, xch[c * 2 * WAVES + WAVES + w]);
   }
   const float step = ruler_step(lo, hi), inv = ruler_inv(step);
-  const int64_t ro = ((int64_t)h * a.ngroups_cap + gcur) * D + ch;
   if (r0 == 0) {
-    (which == 0 ? a.kmn : a.vmn)[ro] = f2h(lo);
-    (which == 0 ? a.kst : a.vst)[ro] = f2h(step);
+    io.mn[ch] = f2h(lo);
+    io.st[ch] = f2h(step);
   }
-  uint8_t* codes = (which == 0 ? a.kq : a.vq) + (int64_t)h * a.capacity * D + ch;
-  uint16_t* ring = (which == 0 ? a.tail_k : a.tail_v) + (int64_t)h * GT * D + ch;
+  uint16_t* ring = const_cast<uint16_t*>(io.ring) + ch;
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
     const int r = r0 + 8 * WAVES * i;
-    const int64_t tok = gcur * GT + r;
-    if (tok < a.capacity) codes[tok * D] = (uint8_t)ruler_code_rcp(v[i], lo, step, inv);
+    if (r < io.code_rows) io.codes[r * D + ch] = (uint8_t)ruler_code_rcp(v[i], lo, step, inv);
     if (r == slot) ring[slot * D] = bits[i];
   }
 }
@@ -816,8 +890,9 @@ __device__ __forceinline__ int64_t prefix_limit(const AttnArgs& a, int64_t& pos,
 // after this launch completes. In the fused step, workgroup part < APPEND_UNITS first runs
 // append unit `part` of head h (the prefix never reads the group it writes), and the grid
 // has max(n_parts, APPEND_UNITS) parts per head; parts >= n_parts only append.
-template <bool TOK>
+template <int LAYOUT>
 __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
+  constexpr bool TOK = LAYOUT == CONTIG_TOK, PAGED = LAYOUT == PAGED_T64;
   __shared__ __attribute__((aligned(16))) uint8_t lds_raw[TOK ? LDS_BYTES_TOK : LDS_BYTES];
   __shared__ __attribute__((aligned(16))) uint16_t unit_src[TOK ? 8 : UNIT_SRC_BYTES / 2];
   __shared__ __attribute__((aligned(16))) uint16_t q_lds[16 * D];
@@ -827,7 +902,15 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.x % a.hkv;
-  const int part = blockIdx.x / a.hkv;
+  // work unit -> (sequence, part of its prefix, parts of that sequence, partial slot)
+  int b = 0, part = blockIdx.x / a.hkv, nparts = a.n_parts;
+  const int pslot = part;
+  if constexpr (PAGED) {
+    const int m = a.wg_map[pslot];
+    b = m >> 16;
+    part = m & 0xffff;
+    nparts = a.seq_parts[2 * b + 1];
+  }
   constexpr int wave_lds = TOK ? WAVE_LDS_TOK : WAVE_LDS;
   constexpr int slot_bytes = TOK ? HALF_SLOT_TOK : HALF_SLOT;
   uint8_t* my_stages = lds_raw + wave * wave_lds;
@@ -836,15 +919,22 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
 
   int64_t pos;
   bool pos_ok;
-  const int64_t U = prefix_limit(a, pos, pos_ok);
+  int64_t U;
+  if constexpr (PAGED) {
+    pos = a.pos_dev[b];  // the ring holds the group of pos (appended before this launch)
+    pos_ok = pos >= 0 && pos / GT < a.table_stride;
+    U = pos_ok ? pos / GT * GT : 0;
+  } else {
+    U = prefix_limit(a, pos, pos_ok);
+  }
   // the fused step's append: int8t64 units in parts < APPEND_UNITS (the grid has at least
   // that many parts), the per-token symmetric token in part 0
-  const bool append = a.tail_mode == TAIL_FUSED && pos_ok && (TOK ? part == 0 : part < APPEND_UNITS);
-  const bool prefix = part < a.n_parts;
+  const bool append = !PAGED && a.tail_mode == TAIL_FUSED && pos_ok && (TOK ? part == 0 : part < APPEND_UNITS);
+  const bool prefix = part < nparts;
 
   const int64_t W = (U + GT - 1) / GT;
-  const int64_t gs = prefix ? (int64_t)part * W / a.n_parts : 0;
-  const int64_t ge = prefix ? (int64_t)(part + 1) * W / a.n_parts : 0;
+  const int64_t gs = prefix ? (int64_t)part * W / nparts : 0;
+  const int64_t ge = prefix ? (int64_t)(part + 1) * W / nparts : 0;
   // Groups gs + gi, gi < ng, are handed out to the waves one at a time: wave w starts with
   // gi = w, and a wave claims the next one from `next_group` once the first half of its
   // current group is done, so waves whose loads arrive early take more groups. A group's
@@ -855,13 +945,20 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   if (tid == 0) next_group = WAVES;
   // Q and the append unit's rows are loaded ahead of the groups, so that waiting for them
   // leaves the groups in flight
-  if (wave == 0 && prefix) issue_q(a, h, __builtin_amdgcn_readfirstlane(lds_addr(q_lds)));
-  if (!TOK && wave == 0 && append) issue_unit_rows(a, h, part, src_lds);
+  if (wave == 0 && prefix)
+    issue_q(a.q + ((int64_t)b * a.hq + h * a.gq) * D, a.gq, __builtin_amdgcn_readfirstlane(lds_addr(q_lds)));
+  UnitIO uio{};
+  if (!TOK && !PAGED && append) uio = unit_io(a, h, part, pos);
+  if (!TOK && wave == 0 && append) issue_unit_rows(uio, part, src_lds);
   if (wave < ng) {
     if constexpr (TOK) {
       issue_half_tok(a, h, gs + wave, 0, my_lds);
       issue_half_tok(a, h, gs + wave, 1, my_lds + HALF_SLOT_TOK);
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_HALF_TOK) : "memory");
+    } else if constexpr (PAGED) {
+      issue_half_paged(a, b, h, gs + wave, 0, my_lds, rul_lds);
+      issue_half_paged(a, b, h, gs + wave, 1, my_lds + HALF_SLOT, rul_lds);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF_PAGED + DMA_SECOND_HALF) : "memory");
     } else {
       issue_half(a, h, gs + wave, 0, my_lds, rul_lds);
       issue_half(a, h, gs + wave, 1, my_lds + HALF_SLOT, rul_lds);
@@ -874,7 +971,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
 
   if (append) {
     if constexpr (TOK) append_tok_rows(a, h, pos);
-    else append_unit(a, h, part, pos, unit_src, xch);
+    else append_unit(uio, part, pos, unit_src, xch);
     if (blockIdx.x == 0 && tid == 0) write_scalars(a, pos);
   }
   if (!prefix) return;
@@ -912,6 +1009,12 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
         attend_block_tok(a, st, qb, slot1, slot1 + HALF_CODE, reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE),
                          reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE + TOK_SCALE_BYTES), nv2);
       if (nx < ng) issue_half_tok(a, h, gs + nx, 1, my_lds + HALF_SLOT_TOK);
+    } else if constexpr (PAGED) {
+      if (nx < ng) issue_half_paged(a, b, h, gs + nx, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
+      if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF_PAGED) : "memory");
+      else wait_groups_all();
+      if (nv2 > 0) attend_block<1>(a, st, qb, slot1, slot1 + HALF_CODE, rul, nv2);
+      if (nx < ng) issue_half_paged(a, b, h, gs + nx, 1, my_lds + HALF_SLOT, 0u);
     } else {
       if (nx < ng) issue_half(a, h, gs + nx, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
       if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF) : "memory");
@@ -927,7 +1030,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   const int gq = a.gq, pw = part_stride(gq);
   store_wave_partial(st, gq, lds + wave * pw);
   __syncthreads();
-  float* dst = a.ws + ((int64_t)h * a.n_parts + part) * pw;
+  float* dst = a.ws + ((int64_t)h * (PAGED ? a.total_parts : a.n_parts) + pslot) * pw;
   for (int e = tid; e < gq * D + 2 * gq; e += THREADS) {
     const int head = e < gq * D ? e / D : (e - gq * D) % gq;
     float m = NEG_INF;
@@ -953,6 +1056,7 @@ constexpr int WT_STRIDE = 256;  // partials one merge holds
 // log-sum-exp and writes out / lse. Every phase is spread over the 8 waves (a wave's
 // dependent instruction chain is what bounds this kernel), and every load it needs is
 // issued at its start.
+template <bool PAGED>
 __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t ring_lds[2 * RING_BYTES];          // K | V values
   __shared__ __attribute__((aligned(16))) float ring_part[RING_PARTS][16 * D + 32];  // the ring's partials
@@ -960,14 +1064,25 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
   __shared__ float pre_m[16], pre_l[16];                           // prefix: max_s m_s, sum_s w_s l_s
   __shared__ __attribute__((aligned(16))) float wbuf[TB_WAVES][WT_STRIDE];  // one head's w_s per wave
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int h = blockIdx.x;
-  const int gq = a.gq, pw = part_stride(gq), P = a.n_parts, cols = gq * D;
-  const bool fused = a.tail_mode == TAIL_FUSED;
+  // paged: workgroup (b, h) serves KV head h of sequence b, whose partials are units
+  // seq_parts[2b] .. + seq_parts[2b + 1] - 1
+  const int h = PAGED ? blockIdx.x % a.hkv : blockIdx.x;
+  const int b = PAGED ? blockIdx.x / a.hkv : 0;
+  const int gq = a.gq, pw = part_stride(gq), cols = gq * D;
+  const int P = PAGED ? a.seq_parts[2 * b + 1] : a.n_parts;
+  const bool fused = PAGED || a.tail_mode == TAIL_FUSED;
 
   int64_t pos;
   bool pos_ok;
-  const int64_t U = prefix_limit(a, pos, pos_ok);
-  const bool ring = a.tail_mode != TAIL_NONE && (!fused || pos_ok);
+  int64_t U;
+  if constexpr (PAGED) {
+    pos = a.pos_dev[b];
+    pos_ok = pos >= 0 && pos / GT < a.table_stride;
+    U = pos_ok ? pos / GT * GT : 0;
+  } else {
+    U = prefix_limit(a, pos, pos_ok);
+  }
+  const bool ring = (PAGED || a.tail_mode != TAIL_NONE) && (!fused || pos_ok);
   // while waves 0..3 attend over the ring, the others merge the prefix partials
   const int mbase = ring ? RING_PARTS : 0, nmw = TB_WAVES - mbase;
   const bool merger = wave >= mbase;
@@ -977,9 +1092,10 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
   // (2 lane, 2 lane + 1) of the first MERGE_CHUNK partials
   const int which = wave >> 2, qtr = wave & 3;
   const bool completes = fused && pos_ok && !a.tok && (pos + 1) % GT == 0;  // the token completed its group
-  const bool tok1 = ring && a.tok;  // per-token symmetric fused step: the tail is the new token
+  const bool tok1 = !PAGED && ring && a.tok;  // per-token symmetric fused step: the tail is the new token
+  const uint16_t* ring_h = PAGED ? a.rings + (((int64_t)b * a.hkv + h) * 2 + which) * GT * D : ring_of(a, h, which);
   RingQuarter rq;
-  if (ring && !completes && !tok1) ring_load_quarter(ring_of(a, h, which), (int)a.tail_slots, qtr, rq);
+  if (ring && !completes && !tok1) ring_load_quarter(ring_h, PAGED ? GT : (int)a.tail_slots, qtr, rq);
   uint2 tw = {0u, 0u};
   uint16_t tsc = 0;
   if (tok1 && qtr == 0 && lane < 16) {
@@ -990,18 +1106,32 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
   uint2 cw[4];
   uint4 cst, cmn;
   if (completes) {
-    const int64_t gcur = pos / GT, ro = ((int64_t)h * a.ngroups_cap + gcur) * D + 8 * (lane & 15);
-    const uint8_t* codes = (which == 0 ? a.kq : a.vq) + ((int64_t)h * a.capacity + gcur * GT) * D + 8 * (lane & 15);
+    const int64_t gcur = pos / GT;
+    const uint8_t* codes;
+    const uint16_t *gst, *gmn;
+    if constexpr (PAGED) {
+      const uint8_t* base = a.pages + ((int64_t)a.table[(int64_t)b * a.table_stride + gcur] * a.hkv + h) * PAGE_BYTES;
+      codes = base + which * CODE_BYTES;
+      gst = reinterpret_cast<const uint16_t*>(base + 2 * CODE_BYTES) + which * 2 * D;
+      gmn = gst + D;
+    } else {
+      const int64_t ro = ((int64_t)h * a.ngroups_cap + gcur) * D;
+      codes = (which == 0 ? a.kq : a.vq) + ((int64_t)h * a.capacity + gcur * GT) * D;
+      gst = (which == 0 ? a.kst : a.vst) + ro;
+      gmn = (which == 0 ? a.kmn : a.vmn) + ro;
+    }
+    codes += 8 * (lane & 15);
 #pragma unroll
     for (int i = 0; i < 4; ++i) cw[i] = *reinterpret_cast<const uint2*>(codes + (16 * qtr + (lane >> 4) + 4 * i) * D);
-    cst = *reinterpret_cast<const uint4*>((which == 0 ? a.kst : a.vst) + ro);
-    cmn = *reinterpret_cast<const uint4*>((which == 0 ? a.kmn : a.vmn) + ro);
+    cst = *reinterpret_cast<const uint4*>(gst + 8 * (lane & 15));
+    cmn = *reinterpret_cast<const uint4*>(gmn + 8 * (lane & 15));
   }
-  const int64_t first = (ring && a.first_dev) ? *a.first_dev : 0;
+  const int64_t first = (!PAGED && ring && a.first_dev) ? *a.first_dev : 0;
   const bool mask_on = ring && a.tail_mode == TAIL_MASK && lane < a.tail_slots && a.tail_mask[lane] != 0;
   half8_t qb[4];
-  if (ring && wave < RING_PARTS) load_q(a, h, qb);
-  const float* hws = a.ws + (int64_t)h * P * pw;
+  const int64_t qh0 = (int64_t)b * a.hq + h * gq;  // first query head of this workgroup
+  if (ring && wave < RING_PARTS) load_q(a.q + qh0 * D, gq, qb);
+  const float* hws = PAGED ? a.ws + ((int64_t)h * a.total_parts + a.seq_parts[2 * b]) * pw : a.ws + (int64_t)h * P * pw;
   const int head0 = wave - mbase;
   float m0 = NEG_INF, l0 = 0.0f;
   float2 v0[MERGE_CHUNK];
@@ -1113,7 +1243,8 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
         l += beta * ring_part[r][gq * D + gq + head];
       }
     }
-    const int qh = h * gq + head, d = col % D;
+    const int64_t qh = qh0 + head;
+    const int d = col % D;
     a.out[(int64_t)qh * D + d] = f2h(l > 0.0f ? acc * (INV_P_SCALE / l) : 0.0f);
     if (a.lse && d == 0) a.lse[qh] = l > 0.0f ? (M + __log2f(l)) * LN2 : NEG_INF;
   }
@@ -1126,11 +1257,27 @@ __global__ __launch_bounds__(THREADS) void append_kernel(AttnArgs a) {
   const int h = blockIdx.x / APPEND_UNITS, unit = blockIdx.x % APPEND_UNITS;
   const int64_t pos = *a.pos_dev;
   if (pos < 0 || pos >= a.capacity) return;  // a position outside the cache appends nothing
-  if (threadIdx.x < 64) issue_unit_rows(a, h, unit, __builtin_amdgcn_readfirstlane(lds_addr(unit_src)));
+  const UnitIO io = unit_io(a, h, unit, pos);
+  if (threadIdx.x < 64) issue_unit_rows(io, unit, __builtin_amdgcn_readfirstlane(lds_addr(unit_src)));
   wait_groups_all();
   __syncthreads();
-  append_unit(a, h, unit, pos, unit_src, xch);
+  append_unit(io, unit, pos, unit_src, xch);
   if (blockIdx.x == 0 && threadIdx.x == 0) write_scalars(a, pos);
+}
+
+// Paged batch append: one workgroup per (sequence, KV head, append unit).
+__global__ __launch_bounds__(THREADS) void append_paged_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t unit_src[UNIT_SRC_BYTES / 2];
+  __shared__ __attribute__((aligned(16))) float xch[UNIT_CH * 2 * WAVES];
+  const int unit = blockIdx.x % APPEND_UNITS, h = (blockIdx.x / APPEND_UNITS) % a.hkv;
+  const int b = blockIdx.x / (APPEND_UNITS * a.hkv);
+  const int64_t pos = a.pos_dev[b];
+  if (pos < 0 || pos / GT >= a.table_stride) return;  // a position without a page appends nothing
+  const UnitIO io = unit_io_paged(a, b, h, unit, pos);
+  if (threadIdx.x < 64) issue_unit_rows(io, unit, __builtin_amdgcn_readfirstlane(lds_addr(unit_src)));
+  wait_groups_all();
+  __syncthreads();
+  append_unit(io, unit, pos, unit_src, xch);
 }
 
 // Standalone per-token symmetric append: one workgroup of 2 waves (K, V) per KV head.
@@ -1185,12 +1332,12 @@ static int launch_attn(AttnArgs& a, int64_t n_parts, int64_t workspace_bytes, hi
     return fail(NKV_ERR_UNSUPPORTED, "%s: capacity %lld exceeds 16M tokens", what, (long long)a.capacity);
   if (n_parts > 0 && (launches & LAUNCH_PREFIX)) {
     const int64_t parts = a.tail_mode == TAIL_FUSED && !a.tok ? std::max<int64_t>(n_parts, APPEND_UNITS) : n_parts;
-    if (a.tok) hipLaunchKernelGGL(attn_prefix_kernel<true>, dim3((unsigned)(a.hkv * parts)), dim3(THREADS), 0, s, a);
-    else hipLaunchKernelGGL(attn_prefix_kernel<false>, dim3((unsigned)(a.hkv * parts)), dim3(THREADS), 0, s, a);
+    if (a.tok) hipLaunchKernelGGL(attn_prefix_kernel<CONTIG_TOK>, dim3((unsigned)(a.hkv * parts)), dim3(THREADS), 0, s, a);
+    else hipLaunchKernelGGL(attn_prefix_kernel<CONTIG_T64>, dim3((unsigned)(a.hkv * parts)), dim3(THREADS), 0, s, a);
     if (int rc = check_launch(what)) return rc;
   }
   if (!(launches & LAUNCH_TAIL)) return NKV_OK;
-  hipLaunchKernelGGL(attn_tail_kernel, dim3((unsigned)a.hkv), dim3(TB_THREADS), 0, s, a);
+  hipLaunchKernelGGL(attn_tail_kernel<false>, dim3((unsigned)a.hkv), dim3(TB_THREADS), 0, s, a);
   return check_launch(what);
 }
 
@@ -1465,4 +1612,91 @@ extern "C" int nkv_decode_step_partials_tok(NKV_STEP_TOK_PARAMS) {
 }
 extern "C" int nkv_decode_step_combine_tok(NKV_STEP_TOK_PARAMS) {
   return decode_step_tok("decode_step_combine_tok", LAUNCH_TAIL, NKV_STEP_TOK_ARGS);
+}
+
+// ---------------------------------------------------------------- paged batch (int8t64)
+
+extern "C" int64_t nkv_paged_workspace_bytes(int64_t hkv, int64_t hq, int64_t total_parts) {
+  if (hkv <= 0 || hq <= 0 || total_parts <= 0 || hq % hkv) return 0;
+  return hkv * total_parts * part_floats(hq, hkv) * (int64_t)sizeof(float);
+}
+
+static int paged_args(const char* what, AttnArgs& a, const uint8_t* pages, const int32_t* page_table,
+                      int64_t table_stride, const uint16_t* rings, const int64_t* pos_dev, int64_t nseq, int64_t hkv,
+                      int64_t head_dim) {
+  if (head_dim != D) return fail(NKV_ERR_UNSUPPORTED, "head_dim %lld: the HIP kernels are built for head_dim 128", (long long)head_dim);
+  if (nseq <= 0 || nseq > 32767 || hkv <= 0 || table_stride <= 0)
+    return fail(NKV_ERR_INVALID, "%s: bad sizes nseq=%lld hkv=%lld table_stride=%lld", what, (long long)nseq,
+                (long long)hkv, (long long)table_stride);
+  if (!pages || !page_table || !rings || !pos_dev) return fail(NKV_ERR_INVALID, "%s: null pointer argument", what);
+  if (!al16(pages) || !al16(rings)) return fail(NKV_ERR_UNSUPPORTED, "%s: buffers must be 16-byte aligned", what);
+  a.pages = const_cast<uint8_t*>(pages);
+  a.table = page_table;
+  a.table_stride = table_stride;
+  a.rings = const_cast<uint16_t*>(rings);
+  a.pos_dev = pos_dev;
+  a.nseq = (int)nseq;
+  a.hkv = (int)hkv;
+  a.tail_mode = TAIL_FUSED;
+  a.tail_slots = GT;
+  return NKV_OK;
+}
+
+extern "C" int nkv_paged_append_t64(const uint16_t* k_new, const uint16_t* v_new, int64_t kv_seq_stride,
+                                    int64_t kv_head_stride, uint8_t* pages, const int32_t* page_table,
+                                    int64_t table_stride, uint16_t* rings, const int64_t* pos_dev, int64_t nseq,
+                                    int64_t hkv, int64_t head_dim, void* stream) {
+  set_error("");
+  AttnArgs a{};
+  if (int rc = paged_args("paged_append_t64", a, pages, page_table, table_stride, rings, pos_dev, nseq, hkv, head_dim)) return rc;
+  if (!k_new || !v_new) return fail(NKV_ERR_INVALID, "paged_append_t64: null pointer argument");
+  if (!al16(k_new) || !al16(v_new) || kv_head_stride % 8 || kv_seq_stride % 8)
+    return fail(NKV_ERR_UNSUPPORTED, "paged_append_t64: k_new / v_new must be 16-byte aligned");
+  a.k_new = k_new; a.v_new = v_new; a.kv_hs = kv_head_stride; a.kv_ss = kv_seq_stride;
+  hipLaunchKernelGGL(append_paged_kernel, dim3((unsigned)(nseq * hkv * APPEND_UNITS)), dim3(THREADS), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("paged_append_t64");
+}
+
+extern "C" int nkv_paged_attn_decode_t64(const uint16_t* q, const uint8_t* pages, const int32_t* page_table,
+                                         int64_t table_stride, const uint16_t* rings, const int64_t* pos_dev,
+                                         int64_t nseq, int64_t hq, int64_t hkv, int64_t head_dim,
+                                         const int32_t* wg_map, const int32_t* seq_parts, int64_t total_parts,
+                                         uint16_t* out, float* lse_out, void* workspace, int64_t workspace_bytes,
+                                         void* stream) {
+  set_error("");
+  if (int rc = check_heads(hq, hkv, head_dim)) return rc;
+  AttnArgs a{};
+  if (int rc = paged_args("paged_attn_decode_t64", a, pages, page_table, table_stride, rings, pos_dev, nseq, hkv, head_dim)) return rc;
+  if (!q || !wg_map || !seq_parts || !out || !workspace)
+    return fail(NKV_ERR_INVALID, "paged_attn_decode_t64: null pointer argument");
+  if (!al16(q) || !al16(workspace)) return fail(NKV_ERR_UNSUPPORTED, "paged_attn_decode_t64: buffers must be 16-byte aligned");
+  if (total_parts < nseq || total_parts > 65535)
+    return fail(NKV_ERR_INVALID, "paged_attn_decode_t64: total_parts %lld outside [nseq, 65535]", (long long)total_parts);
+  const int64_t need = nkv_paged_workspace_bytes(hkv, hq, total_parts);
+  if (workspace_bytes < need)
+    return fail(NKV_ERR_INVALID, "paged_attn_decode_t64: workspace of %lld bytes, need %lld", (long long)workspace_bytes, (long long)need);
+  a.q = q; a.hq = (int)hq; a.gq = (int)(hq / hkv);
+  a.wg_map = wg_map; a.seq_parts = seq_parts; a.total_parts = (int)total_parts;
+  a.sl2 = LOG2E / sqrtf((float)head_dim);
+  a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(attn_prefix_kernel<PAGED_T64>, dim3((unsigned)(hkv * total_parts)), dim3(THREADS), 0, s, a);
+  if (int rc = check_launch("paged_attn_decode_t64")) return rc;
+  hipLaunchKernelGGL(attn_tail_kernel<true>, dim3((unsigned)(nseq * hkv)), dim3(TB_THREADS), 0, s, a);
+  return check_launch("paged_attn_decode_t64");
+}
+
+extern "C" int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                                         int64_t kv_seq_stride, int64_t kv_head_stride, uint8_t* pages,
+                                         const int32_t* page_table, int64_t table_stride, uint16_t* rings,
+                                         const int64_t* pos_dev, int64_t nseq, int64_t hq, int64_t hkv,
+                                         int64_t head_dim, const int32_t* wg_map, const int32_t* seq_parts,
+                                         int64_t total_parts, uint16_t* out, float* lse_out, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+  if (int rc = nkv_paged_append_t64(k_new, v_new, kv_seq_stride, kv_head_stride, pages, page_table, table_stride,
+                                    rings, pos_dev, nseq, hkv, head_dim, stream))
+    return rc;
+  return nkv_paged_attn_decode_t64(q, pages, page_table, table_stride, rings, pos_dev, nseq, hq, hkv, head_dim,
+                                   wg_map, seq_parts, total_parts, out, lse_out, workspace, workspace_bytes, stream);
 }
