@@ -304,7 +304,7 @@ int nkv_paged_attn_decode_t64(const uint16_t* q, const uint8_t* pages, const int
                               uint16_t* out, float* lse_out, void* workspace, int64_t workspace_bytes,
                               void* stream);
 
-/* nkv_paged_append_t64 then nkv_paged_attn_decode_t64. */
+/* nkv_paged_append_t64 then nkv_paged_attn_decode_t64 (three launches). */
 int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                               int64_t kv_seq_stride, int64_t kv_head_stride, uint8_t* pages,
                               const int32_t* page_table, int64_t table_stride, uint16_t* rings,

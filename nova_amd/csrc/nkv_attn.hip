@@ -822,6 +822,65 @@ __device__ __forceinline__ void append_unit(const UnitIO& io, int unit, int64_t 
   }
 }
 
+// A wide unit: 64 channels of one tensor of one head, for the standalone paged append
+// (few, larger workgroups). Each wave loads 8 of the 64 ring rows (128 bytes of each), wave 0
+// also the new token's 128 bytes; thread t takes ring row t >> 3 and channels 8 (t & 7) + [0..7].
+constexpr int WIDE_CH = 64;
+constexpr int WIDE_UNITS = 2 * D / WIDE_CH;
+constexpr int WIDE_SRC_BYTES = (GT + 1) * WIDE_CH * 2;
+
+__device__ __forceinline__ void issue_wide_rows(const UnitIO& io, int ch0, uint32_t src) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = 8 * wave + (lane >> 3);
+  dma16(uniform_ptr(io.ring + ch0), (uint32_t)(row * D * 2 + (lane & 7) * 16), __builtin_amdgcn_readfirstlane(src + 1024 * wave));
+  if (wave == 0 && lane < 8)
+    dma16(uniform_ptr(io.fresh + ch0), (uint32_t)(lane * 16), __builtin_amdgcn_readfirstlane(src + GT * WIDE_CH * 2));
+}
+
+// append_unit for a wide unit (channels ch0 .. ch0 + 63); `xch` 64 x 16 floats and `rul` 64
+// float4 of LDS; two workgroup barriers inside.
+__device__ __forceinline__ void append_wide(const UnitIO& io, int ch0, int64_t pos, const uint8_t* src, float* xch,
+                                            float4* rul) {
+  static_assert(THREADS == 8 * GT, "one thread per 8 channels of a ring row");
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, r = t >> 3, c8 = t & 7;
+  const int slot = (int)(pos % GT);
+  const uint4 w = *reinterpret_cast<const uint4*>(src + (r == slot ? GT : r) * (WIDE_CH * 2) + 16 * c8);
+  const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    v[j] = h2f((uint16_t)(wv[j >> 1] >> (16 * (j & 1))));
+    const float mn = min4rows(fminf(v[j], ror8(v[j])));
+    const float mx = max4rows(fmaxf(v[j], ror8(v[j])));
+    if (lane < 8) {
+      xch[(8 * c8 + j) * 16 + wave] = mn;
+      xch[(8 * c8 + j) * 16 + 8 + wave] = mx;
+    }
+  }
+  __syncthreads();
+  if (t < WIDE_CH) {
+    const float4* x4 = reinterpret_cast<const float4*>(xch + 16 * t);
+    const float4 m0 = x4[0], m1 = x4[1], M0 = x4[2], M1 = x4[3];
+    const float lo = fminf(fminf(fminf(m0.x, m0.y), fminf(m0.z, m0.w)), fminf(fminf(m1.x, m1.y), fminf(m1.z, m1.w)));
+    const float hi = fmaxf(fmaxf(fmaxf(M0.x, M0.y), fmaxf(M0.z, M0.w)), fmaxf(fmaxf(M1.x, M1.y), fmaxf(M1.z, M1.w)));
+    const float step = ruler_step(lo, hi);
+    rul[t] = float4{lo, step, ruler_inv(step), 0.0f};
+    io.mn[ch0 + t] = f2h(lo);
+    io.st[ch0 + t] = f2h(step);
+  }
+  __syncthreads();
+  uint32_t cc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float4 rj = rul[8 * c8 + j];
+    cc[j] = ruler_code_rcp(v[j], rj.x, rj.y, rj.z);
+  }
+  if (r < io.code_rows)
+    *reinterpret_cast<uint2*>(io.codes + r * D + ch0 + 8 * c8) =
+        uint2{cc[0] | (cc[1] << 8) | (cc[2] << 16) | (cc[3] << 24), cc[4] | (cc[5] << 8) | (cc[6] << 16) | (cc[7] << 24)};
+  if (r == slot) *reinterpret_cast<uint4*>(const_cast<uint16_t*>(io.ring) + slot * D + ch0 + 8 * c8) = w;
+}
+
 // ---------------------------------------------------------------- partials
 
 // Floats of one partial: [acc: gq * D][m: gq][l: gq], rounded up to 4 floats so that every
@@ -894,7 +953,7 @@ template <int LAYOUT>
 __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   constexpr bool TOK = LAYOUT == CONTIG_TOK, PAGED = LAYOUT == PAGED_T64;
   __shared__ __attribute__((aligned(16))) uint8_t lds_raw[TOK ? LDS_BYTES_TOK : LDS_BYTES];
-  __shared__ __attribute__((aligned(16))) uint16_t unit_src[TOK ? 8 : UNIT_SRC_BYTES / 2];
+  __shared__ __attribute__((aligned(16))) uint16_t unit_src[TOK || PAGED ? 8 : UNIT_SRC_BYTES / 2];
   __shared__ __attribute__((aligned(16))) uint16_t q_lds[16 * D];
   __shared__ __attribute__((aligned(16))) float xch[UNIT_CH * 2 * WAVES];
   __shared__ int next_group;
@@ -950,6 +1009,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   UnitIO uio{};
   if (!TOK && !PAGED && append) uio = unit_io(a, h, part, pos);
   if (!TOK && wave == 0 && append) issue_unit_rows(uio, part, src_lds);
+
   if (wave < ng) {
     if constexpr (TOK) {
       issue_half_tok(a, h, gs + wave, 0, my_lds);
@@ -974,6 +1034,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
     else append_unit(uio, part, pos, unit_src, xch);
     if (blockIdx.x == 0 && tid == 0) write_scalars(a, pos);
   }
+
   if (!prefix) return;
   WaveState st;
   state_init(st);
@@ -1265,19 +1326,21 @@ __global__ __launch_bounds__(THREADS) void append_kernel(AttnArgs a) {
   if (blockIdx.x == 0 && threadIdx.x == 0) write_scalars(a, pos);
 }
 
-// Paged batch append: one workgroup per (sequence, KV head, append unit).
+// Paged batch append: one workgroup per (sequence, KV head, wide unit of 64 channels).
 __global__ __launch_bounds__(THREADS) void append_paged_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t unit_src[UNIT_SRC_BYTES / 2];
-  __shared__ __attribute__((aligned(16))) float xch[UNIT_CH * 2 * WAVES];
-  const int unit = blockIdx.x % APPEND_UNITS, h = (blockIdx.x / APPEND_UNITS) % a.hkv;
-  const int b = blockIdx.x / (APPEND_UNITS * a.hkv);
+  __shared__ __attribute__((aligned(16))) uint8_t src[WIDE_SRC_BYTES];
+  __shared__ __attribute__((aligned(16))) float xch[WIDE_CH * 16];
+  __shared__ float4 rul[WIDE_CH];
+  const int w = blockIdx.x % WIDE_UNITS, h = (blockIdx.x / WIDE_UNITS) % a.hkv;
+  const int b = blockIdx.x / (WIDE_UNITS * a.hkv);
   const int64_t pos = a.pos_dev[b];
   if (pos < 0 || pos / GT >= a.table_stride) return;  // a position without a page appends nothing
-  const UnitIO io = unit_io_paged(a, b, h, unit, pos);
-  if (threadIdx.x < 64) issue_unit_rows(io, unit, __builtin_amdgcn_readfirstlane(lds_addr(unit_src)));
+  const int which = w / (D / WIDE_CH), ch0 = (w % (D / WIDE_CH)) * WIDE_CH;
+  const UnitIO io = unit_io_paged(a, b, h, which * (D / UNIT_CH), pos);
+  issue_wide_rows(io, ch0, lds_addr(src));
   wait_groups_all();
   __syncthreads();
-  append_unit(io, unit, pos, unit_src, xch);
+  append_wide(io, ch0, pos, src, xch, rul);
 }
 
 // Standalone per-token symmetric append: one workgroup of 2 waves (K, V) per KV head.
@@ -1653,9 +1716,38 @@ extern "C" int nkv_paged_append_t64(const uint16_t* k_new, const uint16_t* v_new
   if (!al16(k_new) || !al16(v_new) || kv_head_stride % 8 || kv_seq_stride % 8)
     return fail(NKV_ERR_UNSUPPORTED, "paged_append_t64: k_new / v_new must be 16-byte aligned");
   a.k_new = k_new; a.v_new = v_new; a.kv_hs = kv_head_stride; a.kv_ss = kv_seq_stride;
-  hipLaunchKernelGGL(append_paged_kernel, dim3((unsigned)(nseq * hkv * APPEND_UNITS)), dim3(THREADS), 0,
+  hipLaunchKernelGGL(append_paged_kernel, dim3((unsigned)(nseq * hkv * WIDE_UNITS)), dim3(THREADS), 0,
                      static_cast<hipStream_t>(stream), a);
   return check_launch("paged_append_t64");
+}
+
+static int paged_attn(const char* what, const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                      int64_t kv_seq_stride, int64_t kv_head_stride, const uint8_t* pages, const int32_t* page_table,
+                      int64_t table_stride, const uint16_t* rings, const int64_t* pos_dev, int64_t nseq, int64_t hq,
+                      int64_t hkv, int64_t head_dim, const int32_t* wg_map, const int32_t* seq_parts,
+                      int64_t total_parts, uint16_t* out, float* lse_out, void* workspace, int64_t workspace_bytes,
+                      void* stream) {
+  set_error("");
+  if (int rc = check_heads(hq, hkv, head_dim)) return rc;
+  AttnArgs a{};
+  if (int rc = paged_args(what, a, pages, page_table, table_stride, rings, pos_dev, nseq, hkv, head_dim)) return rc;
+  if (!q || !wg_map || !seq_parts || !out || !workspace) return fail(NKV_ERR_INVALID, "%s: null pointer argument", what);
+  if (!al16(q) || !al16(workspace)) return fail(NKV_ERR_UNSUPPORTED, "%s: buffers must be 16-byte aligned", what);
+  if (total_parts < nseq || total_parts > 65535)
+    return fail(NKV_ERR_INVALID, "%s: total_parts %lld outside [nseq, 65535]", what, (long long)total_parts);
+  const int64_t need = nkv_paged_workspace_bytes(hkv, hq, total_parts);
+  if (workspace_bytes < need)
+    return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
+  a.q = q; a.hq = (int)hq; a.gq = (int)(hq / hkv);
+  a.wg_map = wg_map; a.seq_parts = seq_parts; a.total_parts = (int)total_parts;
+  (void)k_new; (void)v_new; (void)kv_seq_stride; (void)kv_head_stride;
+  a.sl2 = LOG2E / sqrtf((float)head_dim);
+  a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(attn_prefix_kernel<PAGED_T64>, dim3((unsigned)(hkv * total_parts)), dim3(THREADS), 0, s, a);
+  if (int rc = check_launch(what)) return rc;
+  hipLaunchKernelGGL(attn_tail_kernel<true>, dim3((unsigned)(nseq * hkv)), dim3(TB_THREADS), 0, s, a);
+  return check_launch(what);
 }
 
 extern "C" int nkv_paged_attn_decode_t64(const uint16_t* q, const uint8_t* pages, const int32_t* page_table,
@@ -1664,27 +1756,9 @@ extern "C" int nkv_paged_attn_decode_t64(const uint16_t* q, const uint8_t* pages
                                          const int32_t* wg_map, const int32_t* seq_parts, int64_t total_parts,
                                          uint16_t* out, float* lse_out, void* workspace, int64_t workspace_bytes,
                                          void* stream) {
-  set_error("");
-  if (int rc = check_heads(hq, hkv, head_dim)) return rc;
-  AttnArgs a{};
-  if (int rc = paged_args("paged_attn_decode_t64", a, pages, page_table, table_stride, rings, pos_dev, nseq, hkv, head_dim)) return rc;
-  if (!q || !wg_map || !seq_parts || !out || !workspace)
-    return fail(NKV_ERR_INVALID, "paged_attn_decode_t64: null pointer argument");
-  if (!al16(q) || !al16(workspace)) return fail(NKV_ERR_UNSUPPORTED, "paged_attn_decode_t64: buffers must be 16-byte aligned");
-  if (total_parts < nseq || total_parts > 65535)
-    return fail(NKV_ERR_INVALID, "paged_attn_decode_t64: total_parts %lld outside [nseq, 65535]", (long long)total_parts);
-  const int64_t need = nkv_paged_workspace_bytes(hkv, hq, total_parts);
-  if (workspace_bytes < need)
-    return fail(NKV_ERR_INVALID, "paged_attn_decode_t64: workspace of %lld bytes, need %lld", (long long)workspace_bytes, (long long)need);
-  a.q = q; a.hq = (int)hq; a.gq = (int)(hq / hkv);
-  a.wg_map = wg_map; a.seq_parts = seq_parts; a.total_parts = (int)total_parts;
-  a.sl2 = LOG2E / sqrtf((float)head_dim);
-  a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(attn_prefix_kernel<PAGED_T64>, dim3((unsigned)(hkv * total_parts)), dim3(THREADS), 0, s, a);
-  if (int rc = check_launch("paged_attn_decode_t64")) return rc;
-  hipLaunchKernelGGL(attn_tail_kernel<true>, dim3((unsigned)(nseq * hkv)), dim3(TB_THREADS), 0, s, a);
-  return check_launch("paged_attn_decode_t64");
+  return paged_attn("paged_attn_decode_t64", q, nullptr, nullptr, 0, 0, pages, page_table, table_stride, rings,
+                    pos_dev, nseq, hq, hkv, head_dim, wg_map, seq_parts, total_parts, out, lse_out, workspace,
+                    workspace_bytes, stream);
 }
 
 extern "C" int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
@@ -1697,6 +1771,7 @@ extern "C" int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_ne
   if (int rc = nkv_paged_append_t64(k_new, v_new, kv_seq_stride, kv_head_stride, pages, page_table, table_stride,
                                     rings, pos_dev, nseq, hkv, head_dim, stream))
     return rc;
-  return nkv_paged_attn_decode_t64(q, pages, page_table, table_stride, rings, pos_dev, nseq, hq, hkv, head_dim,
-                                   wg_map, seq_parts, total_parts, out, lse_out, workspace, workspace_bytes, stream);
+  return paged_attn("paged_decode_step_t64", q, k_new, v_new, kv_seq_stride, kv_head_stride, pages, page_table,
+                    table_stride, rings, pos_dev, nseq, hq, hkv, head_dim, wg_map, seq_parts, total_parts, out,
+                    lse_out, workspace, workspace_bytes, stream);
 }
