@@ -227,6 +227,7 @@ __device__ __forceinline__ const void* uniform_ptr(const void* p) {
 // One `global_load_lds_dwordx4`: lane L's 16 bytes at sbase + voff land at LDS byte
 // address lds + 16 * L (sbase and lds are wave-uniform).
 __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds) {
+  lds = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
 
@@ -1362,6 +1363,301 @@ __global__ void ring_mask_kernel(const int64_t* written, const int64_t* qlen, co
   mask[i] = (p >= *qlen && p <= u && p >= (first ? *first : 0)) ? 1 : 0;
 }
 
+// ---------------------------------------------------------------- chunked prefill (MFMA)
+//
+// Causal attention of a chunk of M query tokens (positions U .. U + M - 1) over the int8t64
+// cache [0, U) (U a multiple of 64) and over the chunk's own fp16 K/V. Query rows of KV head
+// h: row r = (token r / gq, q head h gq + r % gq), M gq rows per head. Workgroup (h, tile,
+// split) takes rows 128 tile .. + 127 (4 waves x 2 MFMA row blocks of 16) and the split's
+// share of the 64-token groups: cache groups [split G / S, (split + 1) G / S) and chunk
+// groups j = split (mod S) up to its last query token. Per group, the 4 waves dequantize
+// the int8 codes once into fp16 LDS tiles (K row-major, V transposed, both padded against
+// bank conflicts), then every wave runs QK^T and PV on v_mfma_f32_16x16x32_f16 for its 32
+// rows. P is a single fp16 operand (scaled by 2^15), as a fused fp16 attention kernel
+// computes it. Each workgroup writes one partial per row; a combine kernel merges the splits.
+constexpr int PF_WAVES = 4;
+constexpr int PF_THREADS = 64 * PF_WAVES;
+constexpr int PF_RB = 2;                             // MFMA row blocks per wave
+constexpr int PF_ROWS = PF_WAVES * PF_RB * 16;       // 128 query rows per workgroup
+constexpr int PF_KROW = D + 8;                       // fp16 K tile row stride (halves)
+constexpr int PF_VROW = GT + 8;                      // fp16 V^T tile row stride (halves, 16-byte rows)
+constexpr int PF_PART = D + 4;                       // floats per row partial: acc[128], m, l, pad
+
+// token slot of the V^T tile: P's k-slot order (slot 8g + r of a 32-token block <-> token
+// 16 (r >> 2) + 4g + (r & 3))
+__device__ __forceinline__ int pf_vslot(int t) {
+  const int u = t & 31;
+  return (t & 32) + 8 * ((u >> 2) & 3) + 4 * (u >> 4) + (u & 3);
+}
+
+struct PrefillArgs {
+  const uint16_t* q;   // [hq][M][D]
+  const uint16_t* kc;  // chunk K [hkv][M][D]
+  const uint16_t* vc;  // chunk V [hkv][M][D]
+  const uint8_t* kq;
+  const uint16_t* kmn;
+  const uint16_t* kst;
+  const uint8_t* vq;
+  const uint16_t* vmn;
+  const uint16_t* vst;
+  int64_t capacity, ngroups_cap, U;
+  int M, hq, hkv, gq, splits, tiles;
+  float sl2;
+  float* ws;       // [splits][hkv * M * gq][PF_PART]
+  uint16_t* out;   // [hq][M][D]
+};
+
+// Online softmax of one 16-row block over 64 tokens (s[b][i]: token 16b + 4g + i, row c),
+// returning P (scaled by 2^15) as two fp16 A operands (tokens of blocks 0,1 and 2,3).
+__device__ __forceinline__ void pf_softmax(WaveState& st, float (&s)[4][4], half8_t (&ph)[2]) {
+  const int lane = threadIdx.x & 63, g = lane >> 4;
+  float mloc = NEG_INF;
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mloc = fmaxf(mloc, s[b][i]);
+  mloc = max4rows(mloc);
+  const float m_new = fmaxf(st.m, mloc);
+  const float m_use = m_new == NEG_INF ? 0.0f : m_new;
+  const float alpha = __builtin_amdgcn_exp2f(st.m - m_use);
+  float lsum = 0.0f;
+  _Float16 p16[2][8];
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = __builtin_amdgcn_exp2f(s[b][i] - m_use);
+      lsum += p;
+      p16[b >> 1][4 * (b & 1) + i] = (_Float16)(p * P_SCALE);
+    }
+#pragma unroll
+  for (int B = 0; B < 2; ++B)
+    ph[B] = half8_t{p16[B][0], p16[B][1], p16[B][2], p16[B][3], p16[B][4], p16[B][5], p16[B][6], p16[B][7]};
+  st.l = st.l * alpha + sum4rows(lsum);
+  const bool moved = st.m != m_new;
+  st.m = m_new;
+  if (__builtin_amdgcn_ballot_w64(moved) == 0) return;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float ai = shfl(alpha, 4 * g + i);
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb) st.acc[cb][i] *= ai;
+  }
+}
+
+__global__ __launch_bounds__(PF_THREADS, 2) void prefill_chunk_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t stage[2][2 * CODE_BYTES + RULER_BYTES];
+  __shared__ __attribute__((aligned(16))) uint16_t ktile[GT * PF_KROW];
+  __shared__ __attribute__((aligned(16))) uint16_t vtile[D * PF_VROW];
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = blockIdx.x % a.hkv, tile = (blockIdx.x / a.hkv) % a.tiles, split = blockIdx.x / (a.hkv * a.tiles);
+  const int rows_h = a.M * a.gq;
+  const int row0 = tile * PF_ROWS + wave * PF_RB * 16;  // first row of this wave
+
+  // ---- Q operands (B of S^T = K Q^T): lane (c, g) holds row 16 rb + c, dims of k-step k
+  half8_t qb[PF_RB][4];
+#pragma unroll
+  for (int rb = 0; rb < PF_RB; ++rb) {
+    const int r = row0 + 16 * rb + c;
+    const bool ok = r < rows_h;
+    const int tk = ok ? r / a.gq : 0, hd = h * a.gq + (ok ? r % a.gq : 0);
+    const uint16_t* qr = a.q + ((int64_t)hd * a.M + tk) * D;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint4 w = {0, 0, 0, 0};
+      if (ok) w = *reinterpret_cast<const uint4*>(qr + 16 * g + 64 * (k >> 1) + 8 * (k & 1));
+      qb[rb][k] = as_h8(w);
+    }
+  }
+  asm volatile("" ::"v"(qb[0][0]), "v"(qb[0][1]), "v"(qb[0][2]), "v"(qb[0][3]), "v"(qb[PF_RB - 1][0]),
+               "v"(qb[PF_RB - 1][1]), "v"(qb[PF_RB - 1][2]), "v"(qb[PF_RB - 1][3]));
+  WaveState st[PF_RB];
+#pragma unroll
+  for (int rb = 0; rb < PF_RB; ++rb) state_init(st[rb]);
+
+  const int64_t G = a.U / GT;
+  const int64_t cs = (int64_t)split * G / a.splits, ce = (int64_t)(split + 1) * G / a.splits;
+  const int last_tok = min(rows_h - 1, (tile + 1) * PF_ROWS - 1) / a.gq;  // last query token of the tile
+  const int nchunk = min((a.M + GT - 1) / GT, last_tok / GT + 1);
+
+  // cache group loads: wave w issues K and V code rows 16w .. 16w + 15 and ruler w
+  auto issue = [&](int64_t grp, int sb) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(stage[sb]));
+    const void* kb = uniform_ptr(a.kq + ((int64_t)h * a.capacity + grp * GT) * D);
+    const void* vb = uniform_ptr(a.vq + ((int64_t)h * a.capacity + grp * GT) * D);
+#pragma unroll
+    for (int j = 2 * wave; j < 2 * wave + 2; ++j) {
+      const int row = 8 * j + (lane >> 3);
+      const uint32_t off = (uint32_t)(row * D + (((lane & 7) ^ swz(row)) << 4));
+      dma16(kb, off, base + 1024 * j);
+      dma16(vb, off, base + CODE_BYTES + 1024 * j);
+    }
+    const int64_t ro = ((int64_t)h * a.ngroups_cap + grp) * D;
+    const uint16_t* rsrc = wave == 0 ? a.kst : wave == 1 ? a.kmn : wave == 2 ? a.vst : a.vmn;
+    if (lane < 16) dma16(uniform_ptr(rsrc + ro), (uint32_t)(16 * lane), base + 2 * CODE_BYTES + 256 * wave);
+  };
+  constexpr int DMA_PF = 5;  // loads per wave and group
+
+  // ---- MFMA phase over the tiles in LDS; `mask_base` >= 0: chunk tokens from that index (causal)
+  auto attend_tiles = [&](int mask_base) {
+    float4_t S[PF_RB][4];
+#pragma unroll
+    for (int rb = 0; rb < PF_RB; ++rb)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) S[rb][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const half8_t ka = *reinterpret_cast<const half8_t*>(ktile + (16 * b + c) * PF_KROW + 16 * g + 64 * (k >> 1) + 8 * (k & 1));
+#pragma unroll
+        for (int rb = 0; rb < PF_RB; ++rb) S[rb][b] = mfma32(ka, qb[rb][k], S[rb][b]);
+      }
+    half8_t ph[PF_RB][2];
+#pragma unroll
+    for (int rb = 0; rb < PF_RB; ++rb) {
+      float sc[4][4];
+      const int tq = (row0 + 16 * rb + c) / a.gq;  // query token of row c (score column)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kt = mask_base + 16 * b + 4 * g + i;
+          sc[b][i] = (mask_base < 0 || kt <= tq) ? S[rb][b][i] * a.sl2 : NEG_INF;
+        }
+      // rows of the S^T layout are q rows c; the causal test above needs the row of column
+      // c, which is lane-independent of g: scores of lane (c, g) all belong to row c
+      pf_softmax(st[rb], sc, ph[rb]);
+    }
+#pragma unroll
+    for (int B = 0; B < 2; ++B)
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb) {
+        const half8_t vb = *reinterpret_cast<const half8_t*>(vtile + (16 * cb + c) * PF_VROW + 32 * B + 8 * g);
+#pragma unroll
+        for (int rb = 0; rb < PF_RB; ++rb) st[rb].acc[cb] = mfma32(ph[rb][B], vb, st[rb].acc[cb]);
+      }
+  };
+
+  // ---- cache groups: double-buffered LDS stages, dequantized once into the fp16 tiles
+  if (cs < ce) issue(cs, 0);
+  for (int64_t grp = cs; grp < ce; ++grp) {
+    const int sb = (int)((grp - cs) & 1);
+    if (grp + 1 < ce) {
+      issue(grp + 1, sb ^ 1);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_PF) : "memory");
+    } else {
+      wait_groups_all();
+    }
+    __syncthreads();  // stage sb is complete; every wave is done with the tiles
+    {
+      const uint8_t* sg = stage[sb];
+      const uint16_t* rks = reinterpret_cast<const uint16_t*>(sg + 2 * CODE_BYTES);
+      // K: thread t dequantizes row t >> 2, dims 32 (t & 3) .. + 31
+      const int row = tid >> 2, cp = tid & 3, key = swz(row);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int ch = 2 * cp + e;  // 16-dim chunk
+        const uint4 kw = *reinterpret_cast<const uint4*>(sg + row * D + ((ch ^ key) << 4));
+        const uint4 s0 = *reinterpret_cast<const uint4*>(rks + 16 * ch), s1 = *reinterpret_cast<const uint4*>(rks + 16 * ch + 8);
+        const uint4 m0 = *reinterpret_cast<const uint4*>(rks + D + 16 * ch), m1 = *reinterpret_cast<const uint4*>(rks + D + 16 * ch + 8);
+        *reinterpret_cast<half8_t*>(ktile + row * PF_KROW + 16 * ch) = dq8(kw.x, kw.y, s0, m0);
+        *reinterpret_cast<half8_t*>(ktile + row * PF_KROW + 16 * ch + 8) = dq8(kw.z, kw.w, s1, m1);
+      }
+      // V: transposed reads; wave w covers dim blocks 2w, 2w + 1 of both 32-token blocks
+      const int r = c >> 1;
+#pragma unroll
+      for (int B = 0; B < 2; ++B)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int cb = 2 * wave + e;
+          const int vrow = 16 * (2 * B + (r >> 2)) + 4 * g + (r & 3);
+          const u32x2 vw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+              (lds_v2i_t*)(const lds_void_t*)(sg + CODE_BYTES + vrow * D + 8 * (c & 1) + ((cb ^ swz(vrow)) << 4))));
+          const _Float16 vs = __builtin_bit_cast(_Float16, rks[2 * D + 16 * cb + c]);
+          const _Float16 vm = __builtin_bit_cast(_Float16, rks[3 * D + 16 * cb + c]);
+          *reinterpret_cast<half8_t*>(vtile + (16 * cb + c) * PF_VROW + 32 * B + 8 * g) =
+              dq8_splat(vw.x, vw.y, half2_t{vs, vs}, half2_t{vm, vm});
+        }
+    }
+    __syncthreads();  // tiles complete
+    attend_tiles(-1);
+  }
+
+  // ---- chunk groups (fp16, causal): j = split, split + S, ...
+  for (int j = split; j < nchunk; j += a.splits) {
+    __syncthreads();  // every wave is done with the tiles
+    {
+      const int row = tid >> 2, cp = tid & 3, t = GT * j + row;
+      const bool ok = t < a.M;
+      const uint16_t* kr = a.kc + ((int64_t)h * a.M + (ok ? t : 0)) * D + 32 * cp;
+      const uint16_t* vr = a.vc + ((int64_t)h * a.M + (ok ? t : 0)) * D + 32 * cp;
+      const int vs = pf_vslot(row);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint4 kw = ok ? *reinterpret_cast<const uint4*>(kr + 8 * e) : uint4{0, 0, 0, 0};
+        const uint4 vw = ok ? *reinterpret_cast<const uint4*>(vr + 8 * e) : uint4{0, 0, 0, 0};
+        *reinterpret_cast<uint4*>(ktile + row * PF_KROW + 32 * cp + 8 * e) = kw;
+        const uint32_t wv[4] = {vw.x, vw.y, vw.z, vw.w};
+#pragma unroll
+        for (int q2 = 0; q2 < 8; ++q2)
+          vtile[(32 * cp + 8 * e + q2) * PF_VROW + vs] = (uint16_t)(wv[q2 >> 1] >> (16 * (q2 & 1)));
+      }
+    }
+    __syncthreads();
+    attend_tiles(GT * j);
+  }
+
+  // ---- one partial per row: acc[128] (x 2^15), m (log2 domain), l
+  const int64_t total_rows = (int64_t)a.hkv * rows_h;
+#pragma unroll
+  for (int rb = 0; rb < PF_RB; ++rb) {
+    const int rbase = row0 + 16 * rb;
+    float* dst = a.ws + ((int64_t)split * total_rows + (int64_t)h * rows_h) * PF_PART;
+    if (g == 0 && rbase + c < rows_h) {
+      dst[(int64_t)(rbase + c) * PF_PART + D] = st[rb].m;
+      dst[(int64_t)(rbase + c) * PF_PART + D + 1] = st[rb].l;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = rbase + 4 * g + i;
+      if (r < rows_h)
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb) dst[(int64_t)r * PF_PART + 16 * cb + c] = st[rb].acc[cb][i];
+    }
+  }
+}
+
+// Merge of the splits' partials: one thread per (row, 4 dims).
+__global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
+  const int rows_h = a.M * a.gq;
+  const int64_t total_rows = (int64_t)a.hkv * rows_h;
+  const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (item >= total_rows * (D / 4)) return;
+  const int64_t row = item / (D / 4);
+  const int d4 = (int)(item % (D / 4)) * 4;
+  float m = NEG_INF;
+  for (int s = 0; s < a.splits; ++s) m = fmaxf(m, a.ws[((int64_t)s * total_rows + row) * PF_PART + D]);
+  const float mu = m == NEG_INF ? 0.0f : m;
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+  float l = 0.0f;
+  for (int s = 0; s < a.splits; ++s) {
+    const float* p = a.ws + ((int64_t)s * total_rows + row) * PF_PART;
+    const float ms = p[D];
+    const float w = ms == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(ms - mu);
+    const float4 v = *reinterpret_cast<const float4*>(p + d4);
+    acc.x += v.x * w; acc.y += v.y * w; acc.z += v.z * w; acc.w += v.w * w;
+    l += p[D + 1] * w;
+  }
+  const int h = (int)(row / rows_h), r = (int)(row % rows_h);
+  const int tk = r / a.gq, hd = h * a.gq + r % a.gq;
+  const float inv = l > 0.0f ? INV_P_SCALE / l : 0.0f;
+  uint16_t* o = a.out + ((int64_t)hd * a.M + tk) * D + d4;
+  *reinterpret_cast<uint2*>(o) = uint2{(uint32_t)f2h(acc.x * inv) | ((uint32_t)f2h(acc.y * inv) << 16),
+                                       (uint32_t)f2h(acc.z * inv) | ((uint32_t)f2h(acc.w * inv) << 16)};
+}
+
 // ---------------------------------------------------------------- host side
 
 // Prefix work units per KV head: at least 8 groups (one per wave) per workgroup, and at
@@ -1774,4 +2070,47 @@ extern "C" int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_ne
   return paged_attn("paged_decode_step_t64", q, k_new, v_new, kv_seq_stride, kv_head_stride, pages, page_table,
                     table_stride, rings, pos_dev, nseq, hq, hkv, head_dim, wg_map, seq_parts, total_parts, out,
                     lse_out, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------- chunked prefill
+
+extern "C" int64_t nkv_prefill_workspace_bytes(int64_t hkv, int64_t hq, int64_t m, int64_t splits) {
+  if (hkv <= 0 || hq <= 0 || m <= 0 || splits <= 0 || hq % hkv) return 0;
+  return splits * hq * m * PF_PART * (int64_t)sizeof(float);
+}
+
+extern "C" int nkv_prefill_attn_t64(const uint16_t* q, const uint16_t* k_chunk, const uint16_t* v_chunk, int64_t m,
+                                    const uint8_t* kq, const uint16_t* kmn, const uint16_t* kst, const uint8_t* vq,
+                                    const uint16_t* vmn, const uint16_t* vst, int64_t capacity, int64_t used,
+                                    int64_t hq, int64_t hkv, int64_t head_dim, uint16_t* out, void* workspace,
+                                    int64_t workspace_bytes, int64_t splits, void* stream) {
+  set_error("");
+  if (int rc = check_heads(hq, hkv, head_dim)) return rc;
+  if (m <= 0 || m > (1 << 20)) return fail(NKV_ERR_INVALID, "prefill_attn: chunk length %lld", (long long)m);
+  if (used < 0 || used % GT || used > capacity)
+    return fail(NKV_ERR_INVALID, "prefill_attn: used=%lld must be a multiple of 64 within the capacity %lld",
+                (long long)used, (long long)capacity);
+  if (!q || !k_chunk || !v_chunk || !out || !workspace || (used > 0 && (!kq || !kmn || !kst || !vq || !vmn || !vst)))
+    return fail(NKV_ERR_INVALID, "prefill_attn: null pointer argument");
+  if (!al16(q) || !al16(k_chunk) || !al16(v_chunk) || !al16(out) || !al16(workspace) ||
+      (used > 0 && (!al16(kq) || !al16(vq) || !al16(kmn) || !al16(kst) || !al16(vmn) || !al16(vst))))
+    return fail(NKV_ERR_UNSUPPORTED, "prefill_attn: buffers must be 16-byte aligned");
+  const int64_t gq = hq / hkv, rows_h = m * gq, tiles = cdiv(rows_h, PF_ROWS);
+  if (splits <= 0) splits = std::max<int64_t>(1, std::min<int64_t>(cdiv(256, hkv * tiles), std::max<int64_t>(1, used / GT)));
+  if (workspace_bytes < nkv_prefill_workspace_bytes(hkv, hq, m, splits))
+    return fail(NKV_ERR_INVALID, "prefill_attn: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
+                (long long)nkv_prefill_workspace_bytes(hkv, hq, m, splits));
+  PrefillArgs a{};
+  a.q = q; a.kc = k_chunk; a.vc = v_chunk;
+  a.kq = kq; a.kmn = kmn; a.kst = kst; a.vq = vq; a.vmn = vmn; a.vst = vst;
+  a.capacity = capacity; a.ngroups_cap = cdiv(capacity, GT); a.U = used;
+  a.M = (int)m; a.hq = (int)hq; a.hkv = (int)hkv; a.gq = (int)gq; a.splits = (int)splits; a.tiles = (int)tiles;
+  a.sl2 = LOG2E / sqrtf((float)head_dim);
+  a.ws = static_cast<float*>(workspace); a.out = out;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(prefill_chunk_kernel, dim3((unsigned)(hkv * tiles * splits)), dim3(PF_THREADS), 0, s, a);
+  if (int rc = check_launch("prefill_attn_t64")) return rc;
+  const int64_t items = hq * m * (D / 4);
+  hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)cdiv(items, 256)), dim3(256), 0, s, a);
+  return check_launch("prefill_attn_t64");
 }

@@ -198,6 +198,47 @@ def int8_attn_decode(
     return out
 
 
+def int8_prefill_attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, kq: torch.Tensor,
+                        kmn: torch.Tensor, kst: torch.Tensor, vq: torch.Tensor, vmn: torch.Tensor,
+                        vst: torch.Tensor, used: int, out: torch.Tensor | None = None,
+                        scratch: torch.Tensor | None = None, splits: int = 0) -> torch.Tensor:
+    """Causal attention of a prefill chunk over an int8t64 cache and itself (MFMA kernels).
+
+    The chunk's ``query`` ``[1, Hq, n, 128]`` (positions ``used .. used + n - 1``) attends to
+    the cache's first ``used`` tokens (a multiple of 64: ``kq``/``vq`` ``[1, Hkv, L, 128]``
+    uint8, rulers ``[1, Hkv, ceil(L/64), 128]``) and causally to its own fp16 ``key`` /
+    ``value`` ``[1, Hkv, n, 128]``. It computes what ``KVInt8Cache.attend_prefill`` does
+    over fp16 staging (src/nova/kvattn.py:791-815) with the cached part read as int8.
+    Returns ``out`` ``[1, Hq, n, 128]`` fp16.
+    """
+    for t, nm in ((query, "query"), (key, "key"), (value, "value")):
+        _check(t, nm, torch.float16)
+    for t, nm in ((kq, "kq"), (vq, "vq")):
+        _check(t, nm, torch.uint8)
+    for t, nm in ((kmn, "kmn"), (kst, "kst"), (vmn, "vmn"), (vst, "vst")):
+        _check(t, nm, torch.float16)
+    _, hq, n, d = query.shape
+    _, hkv, cap, _ = kq.shape
+    if key.shape != (1, hkv, n, d) or value.shape != key.shape:
+        raise ValueError(f"key / value must be [1, {hkv}, {n}, {d}]")
+    if used % GROUP_T or not 0 <= used <= cap:
+        raise ValueError(f"used={used} must be a multiple of {GROUP_T} in [0, {cap}]")
+    if out is None:
+        out = torch.empty_like(query)
+    lib = _lib.load()
+    if splits <= 0:
+        tiles = -(-(n * hq // hkv) // 128)
+        splits = max(1, min(-(-256 // (hkv * tiles)), max(1, used // GROUP_T)))
+    need = int(lib.nkv_prefill_workspace_bytes(hkv, hq, n, splits))
+    if scratch is None or scratch.numel() * scratch.element_size() < need:
+        scratch = _lib.workspace(query.device, need)
+    _lib.call("nkv_prefill_attn_t64", query.data_ptr(), key.data_ptr(), value.data_ptr(), n, kq.data_ptr(),
+              kmn.data_ptr(), kst.data_ptr(), vq.data_ptr(), vmn.data_ptr(), vst.data_ptr(), cap, used, hq, hkv,
+              d, out.data_ptr(), scratch.data_ptr(), scratch.numel() * scratch.element_size(), splits,
+              _lib.stream_ptr(query.device))
+    return out
+
+
 def pack_int8_kv(k: torch.Tensor, v: torch.Tensor, group: int = GROUP_T):
     """fp16 K/V -> ``(kq, kmn, kst, vq, vmn, vst)`` with the token-axis quantizer
     (``src/nova/kvattn.py:430-441``)."""

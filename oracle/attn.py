@@ -107,3 +107,43 @@ def tok_attn_decode(q, kq, ks, vq, vs, used: int):
     v16 = okq.dequantize_tok(vq[:, :used], vs[:, :used])
     out, lse = attend_fp16_kv(q, k16, v16)
     return out.astype(np.float16), lse.astype(np.float32)
+
+
+# ---------------------------------------------------------------- chunked prefill
+
+
+def chunk_prefill_attend(q, kq, kmn, kst, vq, vmn, vst, used: int, k_chunk, v_chunk, heads=None):
+    """Causal attention of a prefill chunk over the int8t64 cache and itself.
+
+    ``q`` [Hq, M, D] fp16 (query token i at position ``used + i``); ``kq``/``vq`` [Hkv, L, D]
+    uint8 with rulers [Hkv, ceil(L/64), D] (``used`` a multiple of 64); ``k_chunk``/``v_chunk``
+    [Hkv, M, D] fp16. Token i attends to the cache tokens [0, used), dequantized as
+    ``dequantize_int8_token`` does, and to chunk tokens [0, i] — the reference's
+    ``attend_prefill`` (``src/nova/kvattn.py:791-815``: causal SDPA over the positions
+    before and including each query) with the cache part read from int8. Returns fp64
+    ``[Hq, M, D]`` (only the KV heads in ``heads`` when given; other rows are 0).
+    """
+    q = np.asarray(q)
+    hq, m, d = q.shape
+    hkv = k_chunk.shape[0]
+    gq = hq // hkv
+    n_g = used // 64
+    out = np.zeros((hq, m, d))
+    for h in (range(hkv) if heads is None else heads):
+        if used:
+            kc = okq.dequantize_int8_token(kq[h:h + 1, :used], kmn[h:h + 1, :n_g], kst[h:h + 1, :n_g], 64)[0]
+            vc = okq.dequantize_int8_token(vq[h:h + 1, :used], vmn[h:h + 1, :n_g], vst[h:h + 1, :n_g], 64)[0]
+            k = np.concatenate([kc, k_chunk[h]], 0).astype(np.float64)
+            v = np.concatenate([vc, v_chunk[h]], 0).astype(np.float64)
+        else:
+            k = k_chunk[h].astype(np.float64)
+            v = v_chunk[h].astype(np.float64)
+        keypos = np.arange(used + m)
+        mask = keypos[None, :] > (used + np.arange(m))[:, None]  # [M, used + M]
+        for j in range(gq):
+            s = (q[h * gq + j].astype(np.float64) @ k.T) * d ** -0.5
+            s[mask] = -np.inf
+            s -= s.max(axis=1, keepdims=True)
+            p = np.exp(s)
+            out[h * gq + j] = (p @ v) / p.sum(axis=1, keepdims=True)
+    return out

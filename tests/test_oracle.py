@@ -318,3 +318,41 @@ def test_mask_row_matches_table():
     table = np.where(idx[None, :] <= idx[:, None], np.float16(0), np.float16(neg))
     for pos in (0, 1, 7, 63):
         np.testing.assert_array_equal(odec.mask_row(pos, max_len), table[pos])
+
+
+def test_chunk_prefill_oracle_pinned():
+    """The chunked-prefill oracle against independent routes: the last query token sees
+    every key (== ``attend_fp16_kv`` over the whole dequantized cache + chunk), the first
+    sees only the cache and itself, torch's math SDPA with an explicit causal mask agrees
+    on every row, and a constant V comes back (to fp64 rounding)."""
+    import torch
+
+    rng = np.random.default_rng(7)
+    hkv, gq, d, used, m = 2, 4, 128, 128, 40
+    hq = hkv * gq
+    kc = (rng.standard_normal((hkv, used, d)) * 0.7).astype(np.float16)
+    vc = (rng.standard_normal((hkv, used, d)) * 0.7).astype(np.float16)
+    kq, kmn, kst = okq.quantize_int8_token(kc, 64)
+    vq, vmn, vst = okq.quantize_int8_token(vc, 64)
+    k_ch = (rng.standard_normal((hkv, m, d)) * 0.7).astype(np.float16)
+    v_ch = (rng.standard_normal((hkv, m, d)) * 0.7).astype(np.float16)
+    q = (rng.standard_normal((hq, m, d)) * 0.7).astype(np.float16)
+    got = oattn.chunk_prefill_attend(q, kq, kmn, kst, vq, vmn, vst, used, k_ch, v_ch)
+    k16 = okq.dequantize_int8_token(kq, kmn, kst, 64)
+    v16 = okq.dequantize_int8_token(vq, vmn, vst, 64)
+    kall = np.concatenate([k16, k_ch], 1)
+    vall = np.concatenate([v16, v_ch], 1)
+    last, _ = oattn.attend_fp16_kv(q[:, m - 1], kall, vall)
+    np.testing.assert_allclose(got[:, m - 1], last, rtol=0, atol=1e-12)
+    first, _ = oattn.attend_fp16_kv(q[:, 0], kall[:, :used + 1], vall[:, :used + 1])
+    np.testing.assert_allclose(got[:, 0], first, rtol=0, atol=1e-12)
+    qt = torch.from_numpy(q.astype(np.float64))
+    kt = torch.from_numpy(kall.astype(np.float64)).repeat_interleave(gq, 0)
+    vt = torch.from_numpy(vall.astype(np.float64)).repeat_interleave(gq, 0)
+    mask = torch.arange(used + m)[None, :] <= (used + torch.arange(m))[:, None]
+    sd = torch.nn.functional.scaled_dot_product_attention(qt[None], kt[None], vt[None], attn_mask=mask)[0]
+    np.testing.assert_allclose(got, sd.numpy(), rtol=0, atol=1e-10)
+    vconst = np.full_like(v_ch, 0.375)
+    vqc, vmc, vsc = okq.quantize_int8_token(np.full_like(vc, 0.375), 64)
+    const = oattn.chunk_prefill_attend(q, kq, kmn, kst, vqc, vmc, vsc, used, k_ch, vconst)
+    np.testing.assert_allclose(const, np.full_like(const, 0.375), rtol=0, atol=1e-12)

@@ -1,0 +1,84 @@
+"""GPU parity of the MFMA chunked-prefill attention over the int8t64 cache.
+
+Oracle: ``oracle.attn.chunk_prefill_attend`` (fp64; pinned in ``tests/test_oracle.py``).
+The kernel rounds the softmax weights to one fp16 operand (scaled by 2^15), as a fused
+fp16 attention does, so the bar is the path's output criterion: max-abs <= 2e-3 against
+the oracle, plus a tight mean error that a wrong row or mask would break.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attn as oattn
+from tests.helpers import D, npy, randn
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(hq, hkv, used, m, seed, cap_extra=64):
+    from nova_amd.kvattn import pack_int8_kv
+
+    k = randn((1, hkv, used + cap_extra, D), seed, 1.0)
+    v = randn((1, hkv, used + cap_extra, D), seed + 1, 1.0)
+    packed = [t.contiguous() for t in pack_int8_kv(k.cuda(), v.cuda())]
+    kch = randn((1, hkv, m, D), seed + 2, 1.0).cuda()
+    vch = randn((1, hkv, m, D), seed + 3, 1.0).cuda()
+    q = randn((1, hq, m, D), seed + 4, 1.0).cuda()
+    return q, kch, vch, packed
+
+
+def _check(got, q, kch, vch, packed, used, heads=None, tag=""):
+    kq, kmn, kst, vq, vmn, vst = (npy(t)[0] for t in packed)
+    want = oattn.chunk_prefill_attend(npy(q)[0], kq, kmn, kst, vq, vmn, vst, used, npy(kch)[0], npy(vch)[0], heads)
+    g = npy(got)[0].astype(np.float64)
+    if heads is not None:
+        gq = q.shape[1] // kch.shape[1]
+        rows = [h * gq + j for h in heads for j in range(gq)]
+        g, want = g[rows], want[rows]
+    err = np.abs(g - want)
+    assert err.max() <= 2e-3, f"{tag}: max abs {err.max():.2e}"
+    assert err.mean() <= 1.5e-4, f"{tag}: mean abs {err.mean():.2e}"
+    return err
+
+
+@pytest.mark.parametrize("used,m", [(0, 1), (0, 70), (64, 1), (64, 65), (512, 17), (512, 130), (2048, 256)])
+def test_prefill_against_oracle(used, m):
+    from nova_amd.kvattn import int8_prefill_attend
+
+    print(f"case used={used} m={m}", flush=True)
+    q, kch, vch, packed = _case(32, 8, used, m, seed=60 + m)
+    got = int8_prefill_attend(q, kch, vch, *packed, used=used)
+    _check(got, q, kch, vch, packed, used, tag=f"used={used} m={m}")
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 2)])
+def test_prefill_gqa_ratios(hq, hkv):
+    from nova_amd.kvattn import int8_prefill_attend
+
+    q, kch, vch, packed = _case(hq, hkv, 256, 90, seed=70 + hq)
+    got = int8_prefill_attend(q, kch, vch, *packed, used=256)
+    _check(got, q, kch, vch, packed, 256, tag=f"hq={hq} hkv={hkv}")
+
+
+def test_prefill_split_settings_agree():
+    from nova_amd.kvattn import int8_prefill_attend
+
+    q, kch, vch, packed = _case(32, 8, 1024, 100, seed=80)
+    outs = [int8_prefill_attend(q, kch, vch, *packed, used=1024, splits=s).clone() for s in (1, 2, 5)]
+    for o in outs:
+        _check(o, q, kch, vch, packed, 1024, tag="splits")
+    assert (outs[0].float() - outs[1].float()).abs().max().item() <= 1e-3
+
+
+def test_prefill_chunk_512_over_16k():
+    """The chunked-prefill workload: a 512-token chunk over a 16384-token int8 cache, 32 q /
+    8 KV heads; checked on KV heads 0 and 7 (the fp64 oracle over all heads is slow)."""
+    from nova_amd.kvattn import int8_prefill_attend
+
+    q, kch, vch, packed = _case(32, 8, 16384, 512, seed=90, cap_extra=0)
+    got = int8_prefill_attend(q, kch, vch, *packed, used=16384)
+    assert torch.isfinite(got).all()
+    _check(got, q, kch, vch, packed, 16384, heads=[0, 7], tag="16k")
