@@ -96,8 +96,9 @@ def parse_args():
     ap.add_argument("--parts", type=int, default=0, help="work units per KV head (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=("decode", "paged"), default="decode",
-                    help="decode: one 32k sequence (the headline); paged: 8 ragged sequences in a paged cache")
+    ap.add_argument("--workload", choices=("decode", "paged", "prefill"), default="decode",
+                    help="decode: one 32k sequence (the headline); paged: 8 ragged sequences in a paged cache; "
+                         "prefill: a 512-token chunk over a 16384-token int8 cache (MFMA)")
     ap.add_argument("--scheme", choices=("t64", "tok"), default="t64",
                     help="KV format: int8t64 (the reference's) or per-token symmetric")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -226,6 +227,73 @@ def cpu_baseline(budget_s: float, scheme: str = "t64") -> dict:
 COPY_BYTES = 64 << 20
 
 
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+
+
+def bench_prefill(args) -> int:
+    """Chunked prefill over int8 KV: a 512-token fp16 query chunk attending causally to a
+    16384-token int8t64 cache plus itself, 32 q / 8 KV heads, head_dim 128 (seed 4). Timed
+    with HIP events over K graph replays of the two launches. Prints one JSON line: chunks/s,
+    achieved TFLOP/s and MFMA utilisation (against the dense fp16 peak), GB/s."""
+    import torch
+
+    from nova_amd import _lib
+    from nova_amd.kvattn import int8_prefill_attend, pack_int8_kv
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    M, U = 512, 16384
+    K = args.steps if args.steps != 256 else 64
+    W = args.warmup
+    g = torch.Generator(device=dev).manual_seed(4)
+    k = torch.randn(1, HKV, U, D, generator=g, device=dev).half()
+    v = torch.randn(1, HKV, U, D, generator=g, device=dev).half()
+    packed = [t.contiguous() for t in pack_int8_kv(k, v)]
+    del k, v
+    q = torch.randn(1, HQ, M, D, generator=g, device=dev).half()
+    kc = torch.randn(1, HKV, M, D, generator=g, device=dev).half()
+    vc = torch.randn(1, HKV, M, D, generator=g, device=dev).half()
+    out = torch.empty_like(q)
+    tiles = -(-(M * HQ // HKV) // 128)
+    splits = max(1, min(-(-256 // (HKV * tiles)), U // 64))
+    scratch = torch.empty(int(_lib.load().nkv_prefill_workspace_bytes(HKV, HQ, M, splits)), dtype=torch.uint8, device=dev)
+    int8_prefill_attend(q, kc, vc, *packed, used=U, out=out, scratch=scratch, splits=splits)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        int8_prefill_attend(q, kc, vc, *packed, used=U, out=out, scratch=scratch, splits=splits)
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(W):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(K):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / K
+    assert torch.isfinite(out).all()
+    flop = 2 * 2 * D * HQ * (M * U + M * (M + 1) // 2)
+    nbytes = U * 2176 + 2 * M * HQ * D * 2 + 2 * M * HKV * D * 2  # codes + rulers, q + out, chunk K/V
+    tflops = flop / (ms / 1e3) / 1e12
+    res = {
+        "metric": "chunked-prefill attention over int8 KV: chunks/s, TFLOP/s, MFMA utilisation, GB/s",
+        "value": round(1e3 / ms, 2), "unit": "chunks/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": f"{M}-token fp16 chunk causally over a {U}-token int8t64 cache plus itself, "
+                               "32 q / 8 kv heads, head_dim 128", "chunk": M, "cache_tokens": U, "splits": splits},
+        "flop_per_step": flop,
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": None},
+        "gbs": round(nbytes / (ms / 1e3) / 1e9, 1),
+    }
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def bench_paged(args) -> int:
     """Batched ragged decode: 8 sequences with seeded uniform lengths in [1024, 16384]
     (seed 3), 36 layers, int8t64 pages of 64 tokens; one step = every layer's
@@ -306,6 +374,8 @@ def main() -> int:
         return 0
     if args.workload == "paged" and args.gpus == 1:
         return bench_paged(args)
+    if args.workload == "prefill" and args.gpus == 1:
+        return bench_prefill(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported on this path "
               "(the decode attention shards by KV head across GPUs; see the design notes)", file=sys.stderr)
