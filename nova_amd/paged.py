@@ -140,7 +140,7 @@ class PagedKVInt8Cache:
     def _step_args(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer: int):
         n = self.nseq
         if q.shape != (n, self.num_q_heads, 1, D) or k.shape != (n, self.num_kv_heads, 1, D) or k.shape != v.shape:
-            raise ValueError("q [B, Hq, 1, 128], k / v [B, Hkv, 1, 128] fp16, B = the planned sequences (解码一步)")
+            raise ValueError("q [B, Hq, 1, 128], k / v [B, Hkv, 1, 128] fp16, B = the planned sequences")
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
         return q, k, v
 
