@@ -97,9 +97,15 @@ class GraphDecoder:
     # ---- eager prefill
 
     @torch.inference_mode()
-    def prefill(self, input_ids: torch.Tensor, offset: int | None = None, reset: bool = True) -> torch.Tensor:
+    def prefill(self, input_ids: torch.Tensor, offset: int | None = None, reset: bool = True,
+                chunk: int = 0) -> torch.Tensor:
         """Eager prefill of the prompt (``decode.py:224-297``): the int8 cache stages fp16
-        K/V, attends causally, then quantizes whole groups in ``finish_prefill``."""
+        K/V, attends causally, then quantizes whole groups in ``finish_prefill``.
+
+        ``chunk`` (int8 cache only, a multiple of 64): feed the prompt in chunks of that many
+        tokens as a streamed prefill. Each chunk is quantized as it lands, so the fp16
+        staging holds one chunk instead of the prompt, and each chunk attends the int8
+        history on MFMA. ``offset`` must then be a multiple of 64."""
         if reset:
             self.cache.reset()
         if offset is None:
@@ -108,19 +114,29 @@ class GraphDecoder:
         n = input_ids.shape[1]
         if n + offset > self.max_len:
             raise ValueError(f"prompt 长度 {n} + 起点 {offset} 超过 max_len {self.max_len}")
+        chunk = int(chunk)
+        if chunk and not isinstance(self.cache, KVInt8Cache):
+            raise ValueError("chunk= streams the prefill of the int8 cache (quant='int8')")
+        if chunk and offset % 64:
+            raise ValueError(f"流式 prefill 的起点 {offset} 必须是 64 的整数倍")
         if hasattr(self.cache, "begin_prefill"):
-            self.cache.begin_prefill(offset + n)
-        self.cache.pos.fill_(offset)
-        if hasattr(self.cache, "set_prefill_pos"):
-            self.cache.set_prefill_pos(offset)
-        if offset:
-            rows = torch.arange(offset, offset + n, device=self.cache.pos.device)
-            keep = self._arange.view(1, 1, 1, -1) <= rows.view(1, 1, n, 1)
-            mask = torch.where(keep, self._zero, self._ninf)
-        else:
-            mask = None
-        out = self.model(input_ids=input_ids, past_key_values=self.cache, attention_mask=mask,
-                         cross_mode="off", logits_to_keep=1)
+            self.cache.begin_prefill(offset + n, stream_chunk=chunk) if chunk else self.cache.begin_prefill(offset + n)
+        step = chunk or n
+        out = None
+        for c0 in range(0, n, step):
+            nc = min(step, n - c0)
+            off = offset + c0
+            self.cache.pos.fill_(off)
+            if hasattr(self.cache, "set_prefill_pos"):
+                self.cache.set_prefill_pos(off)
+            if off:
+                rows = torch.arange(off, off + nc, device=self.cache.pos.device)
+                keep = self._arange.view(1, 1, 1, -1) <= rows.view(1, 1, nc, 1)
+                mask = torch.where(keep, self._zero, self._ninf)
+            else:
+                mask = None
+            out = self.model(input_ids=input_ids[:, c0:c0 + nc], past_key_values=self.cache, attention_mask=mask,
+                             cross_mode="off", logits_to_keep=1)
         if hasattr(self.cache, "finish_prefill"):
             self.cache.finish_prefill(offset + n)
         self.input_ids.copy_(out[:, -1].argmax(-1).view(self.batch, 1))

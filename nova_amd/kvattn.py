@@ -295,6 +295,14 @@ class KVInt8Cache:
     Prefill goes through an fp16 staging area sized to the prompt (``begin_prefill``),
     then ``finish_prefill`` quantizes whole groups with the bulk HIP quantizer, fills the
     ring and frees the staging area.
+
+    Streamed prefill (``begin_prefill(total, stream_chunk=c)``, ``c`` a multiple of 64) keeps
+    only the current chunk in fp16: each chunk starts on a group boundary, ``update``
+    quantizes its whole groups straight into the int8 cache and writes its newest tokens to
+    the ring, and ``attend_prefill`` attends the int8 history plus the fp16 chunk on MFMA
+    (the 64-multiple chunking of ``reports/kv-int8-streaming-cache.md:126-131``). Every
+    group is quantized from the same 64 fp16 tokens as in the staged path, so the final
+    cache state is identical; only the chunk attention reads the history as int8.
     """
 
     def __init__(
@@ -378,6 +386,12 @@ class KVInt8Cache:
         self._ws_bytes = self.pa.numel() * 4
 
         self.staging: Any = None
+        self.stream_chunk = 0
+        self._chunk_k: list[torch.Tensor] = []
+        self._chunk_v: list[torch.Tensor] = []
+        self._chunk_n = [0] * self.num_slots
+        self._chunk_off = 0
+        self._stream_end: int | None = 0
 
     # ---- StaticKVCache-compatible surface
 
@@ -392,16 +406,35 @@ class KVInt8Cache:
         self._pg.zero_()
         if self.staging is not None:
             self.staging.reset()
+        self._stream_end, self._chunk_off = 0, 0
 
     # ---- prefill: fp16 staging area
 
-    def begin_prefill(self, total_len: int) -> None:
-        """Allocate the fp16 staging area for the tokens the prefill will write."""
+    def begin_prefill(self, total_len: int, stream_chunk: int = 0) -> None:
+        """Allocate the fp16 staging area for the tokens the prefill will write.
+
+        With ``stream_chunk`` (a multiple of 64) the staging area holds one chunk per layer
+        instead of the whole prompt, and every chunk is quantized as it lands."""
         from .cache import StaticKVCache
 
         total_len = int(total_len)
         if total_len <= 0 or total_len > self.max_len:
             raise ValueError(f"prefill 长度 {total_len} 超出 (0, {self.max_len}]")
+        stream_chunk = int(stream_chunk)
+        if stream_chunk:
+            if stream_chunk < 0 or stream_chunk % self.group:
+                raise ValueError(f"块大小 {stream_chunk} 必须是 {self.group} 的整数倍")
+            shape = (self.batch, self.num_kv_heads, stream_chunk, self.head_dim)
+            if not self._chunk_k or self._chunk_k[0].shape != shape:
+                self._chunk_k = [torch.empty(shape, dtype=self.dtype, device=self.device)
+                                 for _ in range(self.num_slots)]
+                self._chunk_v = [torch.empty_like(t) for t in self._chunk_k]
+            self.stream_chunk = stream_chunk
+            self._chunk_n = [0] * self.num_slots
+            self._chunk_off, self._stream_end = int(self.pos.item()), None
+            self.staging = None
+            return
+        self.stream_chunk = 0
         self.staging = StaticKVCache(
             num_slots=self.num_slots, num_kv_heads=self.num_kv_heads, head_dim=self.head_dim,
             max_len=total_len, batch=self.batch, dtype=self.dtype, device=self.device,
@@ -409,6 +442,13 @@ class KVInt8Cache:
 
     def set_prefill_pos(self, off: int) -> None:
         self.pos.fill_(int(off))
+        if self.stream_chunk:
+            off = int(off)
+            if self._stream_end is not None and off != self._stream_end:
+                raise ValueError(f"流式 prefill 的块必须首尾相接：上一块止于 {self._stream_end}，收到起点 {off}")
+            self._chunk_off = off
+            self._chunk_n = [0] * self.num_slots
+            return
         self._ensure_staging()
         self.staging.pos.fill_(int(off))
 
@@ -418,6 +458,9 @@ class KVInt8Cache:
         With a staging area (prefill) the fp16 staging cache is written; otherwise one
         decode token is appended to the ring and the ring is requantized (HIP launch).
         """
+        if self.stream_chunk:
+            self._stream_update(key, value, layer_idx)
+            return None, None
         if self.staging is not None:
             if key.shape[2] != 1:
                 self.staging.append_prefill(key, value, layer_idx)
@@ -438,6 +481,43 @@ class KVInt8Cache:
 
     append_prefill = update
 
+    def _chunk_view(self, bufs: list[torch.Tensor], layer_idx: int, n: int) -> torch.Tensor:
+        """The first ``n`` tokens of a chunk buffer as a contiguous ``[1, H_kv, n, D]``."""
+        return bufs[layer_idx].view(-1)[:self.num_kv_heads * n * self.head_dim].view(
+            1, self.num_kv_heads, n, self.head_dim)
+
+    def _stream_update(self, key: torch.Tensor, value: torch.Tensor, layer_idx: int) -> None:
+        """One chunk of a streamed prefill: keep it in fp16 for its own attention, quantize
+        its whole groups into ``[off, off + 64*floor(n/64))`` and put its newest
+        ``min(n, 64)`` tokens into the ring (slot = position mod 64)."""
+        n, off = key.shape[2], self._chunk_off
+        shape = (1, self.num_kv_heads, n, self.head_dim)
+        if key.shape != shape or value.shape != shape:
+            raise ValueError(f"key / value must be [1, {self.num_kv_heads}, n, {self.head_dim}]")
+        if key.dtype != self.dtype or value.dtype != self.dtype:
+            raise ValueError(f"key / value 必须是 {self.dtype}")
+        if n > self.stream_chunk:
+            raise ValueError(f"块长 {n} 超过 stream_chunk {self.stream_chunk}")
+        if off % self.group:
+            raise ValueError(f"流式 prefill 的块起点 {off} 必须是 {self.group} 的整数倍（只有最后一块可以不满）")
+        if off + n > self.max_len:
+            raise ValueError(f"prefill 写到 {off + n}，超过 max_len {self.max_len}")
+        self._chunk_view(self._chunk_k, layer_idx, n).copy_(key)
+        self._chunk_view(self._chunk_v, layer_idx, n).copy_(value)
+        self._chunk_n[layer_idx] = n
+        q = n // self.group * self.group
+        if q:
+            g0, g1 = off // self.group, (off + q) // self.group
+            for bufs, dq, dmn, dst in ((self._chunk_k, self.kq, self.kmn, self.kst),
+                                       (self._chunk_v, self.vq, self.vmn, self.vst)):
+                quantize_int8_into(self._chunk_view(bufs, layer_idx, n)[:, :, :q], self.group, dq[layer_idx][:, :, off:off + q],
+                                   dmn[layer_idx][:, :, g0:g1], dst[layer_idx][:, :, g0:g1])
+        take = min(n, self.group)
+        slots = torch.remainder(torch.arange(off + n - take, off + n, device=self.pos.device), self.group)
+        self.tail_k[layer_idx].index_copy_(2, slots, key[:, :, n - take:n])
+        self.tail_v[layer_idx].index_copy_(2, slots, value[:, :, n - take:n])
+        self._stream_end = off + n
+
     def _token(self, x: torch.Tensor, name: str) -> torch.Tensor:
         if x.shape != (1, self.num_kv_heads, 1, self.head_dim):
             raise ValueError(f"{name} must be [1, {self.num_kv_heads}, 1, {self.head_dim}], got {tuple(x.shape)}")
@@ -446,6 +526,11 @@ class KVInt8Cache:
         if x.stride(3) != 1 or x.stride(1) % 8 or x.data_ptr() % 16:
             x = x.contiguous()
         return x
+
+    @property
+    def prefilling(self) -> bool:
+        """True between ``begin_prefill`` and ``finish_prefill`` (staged or streamed)."""
+        return self.staging is not None or bool(self.stream_chunk)
 
     def _ensure_staging(self) -> None:
         if self.staging is None:
@@ -470,10 +555,20 @@ class KVInt8Cache:
         """Quantize whole groups of the staging area (one bulk HIP launch per layer and
         tensor, written straight into the cache), fill the ring with the newest <= 64
         tokens, set the scalars and free the staging area (``kvattn.py:745-783``)."""
-        self._ensure_staging()
         total = int(total)
         q = total // self.group * self.group
         n_groups = q // self.group
+        if self.stream_chunk:
+            if total != self._stream_end:
+                raise ValueError(f"流式 prefill 写到 {self._stream_end}，finish_prefill 收到 {total}")
+            self.pos.fill_(total)
+            self.first.fill_(0)
+            self._written.fill_(total)
+            self._qlen.fill_(q)
+            self._pg.fill_(n_groups)
+            self.stream_chunk = 0
+            return
+        self._ensure_staging()
         for layer in range(self.num_slots):
             src_k = self.staging.key_cache[layer]
             src_v = self.staging.value_cache[layer]
@@ -496,12 +591,26 @@ class KVInt8Cache:
 
     def release_staging(self) -> None:
         self.staging = None
+        self.stream_chunk = 0
+        self._chunk_k, self._chunk_v = [], []
 
     # ---- prefill attention (fp16 staging + causal mask, as the reference)
 
     def attend_prefill(self, query: torch.Tensor, layer_idx: int) -> torch.Tensor:
         """Attention of one prefill chunk over ``[0, off+n)`` of the fp16 staging area
-        with a causal mask (``kvattn.py:791-815``)."""
+        with a causal mask (``kvattn.py:791-815``).
+
+        In a streamed prefill the history ``[0, off)`` is read from the int8 cache and the
+        chunk from its fp16 copy (one MFMA launch pair, :func:`int8_prefill_attend`)."""
+        if self.stream_chunk:
+            n, off = query.shape[2], self._chunk_off
+            if n != self._chunk_n[layer_idx]:
+                raise RuntimeError(f"layer {layer_idx}: attend_prefill 的块长 {n} 与 update 写入的 "
+                                   f"{self._chunk_n[layer_idx]} 不符")
+            return int8_prefill_attend(query.contiguous(), self._chunk_view(self._chunk_k, layer_idx, n),
+                                       self._chunk_view(self._chunk_v, layer_idx, n), self.kq[layer_idx], self.kmn[layer_idx],
+                                       self.kst[layer_idx], self.vq[layer_idx], self.vmn[layer_idx],
+                                       self.vst[layer_idx], off)
         self._ensure_staging()
         n = query.shape[2]
         off = int(self.staging.pos.item())
@@ -540,7 +649,10 @@ class KVInt8Cache:
     def attend(self, query: torch.Tensor, layer_idx: int) -> torch.Tensor:
         """Decode-step attention over the int8 prefix and the valid ring slots, one
         softmax (one ``nkv_attn_decode_t64`` call); writes and returns ``merged`` (``lse`` holds the
-        log-sum-exp). No host sync — lengths come from ``_qlen`` / ``_pg`` / ``_written``."""
+        log-sum-exp). No host sync — lengths come from ``_qlen`` / ``_pg`` / ``_written``.
+        A one-token chunk of a streamed prefill is attended as a chunk."""
+        if self.stream_chunk:
+            return self.attend_prefill(query, layer_idx)
         q = self._q(query)
         _lib.call(
             "nkv_attn_decode_t64", q.data_ptr(), self.kq[layer_idx].data_ptr(), self.kmn[layer_idx].data_ptr(),
@@ -560,7 +672,7 @@ class KVInt8Cache:
         to float summation order. During prefill (staging present) it falls back to the
         two-call sequence's staging semantics via ``update`` + ``attend_prefill``.
         """
-        if self.staging is not None:
+        if self.prefilling:
             self.update(key, value, layer_idx)
             return self.attend_prefill(query, layer_idx)
         _lib.call("nkv_decode_step_t64", *self.step_args(key, value, query, layer_idx))

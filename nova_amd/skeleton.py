@@ -77,7 +77,7 @@ class SkeletonAttention(nn.Module):
         k = k * cos + _rotate_half(k) * sin
         if hasattr(cache, "attend"):
             # the int8 cache's caller contract (src/nova/layers.py:127-137)
-            if n == 1 and getattr(cache, "staging", None) is None and hasattr(cache, "update_attend"):
+            if n == 1 and not getattr(cache, "prefilling", False) and hasattr(cache, "update_attend"):
                 out = cache.update_attend(k, v, q, self.layer_idx)
             else:
                 cache.update(k, v, self.layer_idx)
