@@ -102,7 +102,7 @@ int nkv_dequantize_int8(const uint8_t* codes, int64_t codes_row_stride, const ui
  * lse_out [hq] fp32 (may be NULL) = log-sum-exp of the scaled scores; an empty
  *   key set gives out 0 and lse -inf (kvattn.py:244-253).
  * workspace: >= nkv_attn_workspace_bytes(hkv, hq, n_parts) bytes of device memory,
- *   16-byte aligned.
+ *   16-byte aligned (any contents).
  * n_parts: prefix work units per KV head (fixed for a captured graph); 0 picks one
  *   from `capacity` (or from `used` when no device scalar is given).
  * Calls that overlap on one GPU must not share `workspace`.
@@ -140,9 +140,13 @@ int nkv_append_t64(const uint16_t* k_new, const uint16_t* v_new, int64_t kv_head
 /*
  * One decode step of one layer: nkv_append_t64 followed by nkv_attn_decode_t64
  * over the int8 prefix and the ring, with the same cache state and scalars as the
- * two-call sequence and the same output up to float summation order. Two launches:
- * the prefix kernel, which also performs the append (the prefix never reads the group
- * it writes), then the tail kernel (ring attention and the combine). Replaces the `KVInt8Cache.update` +
+ * two-call sequence and the same output up to float summation order. One launch: the
+ * prefix kernel also performs the append (the prefix never reads the group it writes),
+ * and the last of each head's workgroups to finish runs the tail (ring attention and the
+ * combine; the new token's ring slot is read from k_new / v_new). Its ticket comes from
+ * a completion counter per head kept in the last bytes of `workspace`: the workspace must
+ * be zero-filled before its first use and serve only the decode-step entry points of one
+ * configuration; every call leaves the counters at zero. Replaces the `KVInt8Cache.update` +
  * `KVInt8Cache.attend` pair that `LeanAttention.forward` issues per layer
  * (src/nova/layers.py:132-136).
  */
@@ -156,7 +160,7 @@ int nkv_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t
                         int64_t n_parts, void* stream);
 
 /*
- * The two launches of nkv_decode_step_t64 as separate calls, with the same arguments:
+ * nkv_decode_step_t64 as two launches in two calls, with the same arguments:
  * _partials (the prefix kernel: the append and one partial per workgroup into
  * `workspace`; `out` / `lse_out` are not written) followed by _combine (the tail kernel:
  * ring attention and the log-sum-exp combine into out / lse) on one stream equals one
@@ -243,16 +247,16 @@ int nkv_append_tok(const uint16_t* k_new, const uint16_t* v_new, int64_t kv_head
                    int64_t* written_dev, int64_t hkv, int64_t head_dim, int64_t capacity,
                    void* stream);
 
-/* One decode step: nkv_append_tok then attention over [0, pos]. Two launches: the prefix
- * kernel over [0, pos) (which also performs the append), then the tail kernel (the new
- * token and the combine). */
+/* One decode step: nkv_append_tok then attention over [0, pos]. One launch: the prefix
+ * kernel over [0, pos) (which also performs the append); the last of each head's
+ * workgroups runs the tail (the new token and the combine). */
 int nkv_decode_step_tok(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                         int64_t kv_head_stride, int8_t* kq, uint16_t* ksc, int8_t* vq, uint16_t* vsc,
                         const int64_t* pos_dev, int64_t* written_dev, int64_t hq, int64_t hkv,
                         int64_t head_dim, int64_t capacity, uint16_t* out, float* lse_out,
                         void* workspace, int64_t workspace_bytes, int64_t n_parts, void* stream);
 
-/* The two launches of nkv_decode_step_tok as separate calls with the same arguments, as
+/* nkv_decode_step_tok as two launches in two calls with the same arguments, as
  * nkv_decode_step_partials_t64 / _combine_t64 are for the int8t64 step. */
 int nkv_decode_step_partials_tok(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                                  int64_t kv_head_stride, int8_t* kq, uint16_t* ksc, int8_t* vq,
@@ -295,8 +299,10 @@ int nkv_paged_append_t64(const uint16_t* k_new, const uint16_t* v_new, int64_t k
                          int64_t hkv, int64_t head_dim, void* stream);
 
 /* Decode attention of every sequence over its whole groups before pos and its ring
- * (tokens up to and including pos). Two launches: the prefix kernel (total_parts * hkv
- * workgroups), then the tail kernel (nseq * hkv workgroups). */
+ * (tokens up to and including pos). One launch of the prefix kernel (total_parts * hkv
+ * workgroups); the last workgroup of each (sequence, KV head) runs its tail. workspace:
+ * zero-filled before its first use, >= nkv_paged_workspace_bytes bytes, its last bytes
+ * hold the completion counters (left at zero by every call). */
 int nkv_paged_attn_decode_t64(const uint16_t* q, const uint8_t* pages, const int32_t* page_table,
                               int64_t table_stride, const uint16_t* rings, const int64_t* pos_dev,
                               int64_t nseq, int64_t hq, int64_t hkv, int64_t head_dim,
@@ -304,7 +310,7 @@ int nkv_paged_attn_decode_t64(const uint16_t* q, const uint8_t* pages, const int
                               uint16_t* out, float* lse_out, void* workspace, int64_t workspace_bytes,
                               void* stream);
 
-/* nkv_paged_append_t64 then nkv_paged_attn_decode_t64 (three launches). */
+/* nkv_paged_append_t64 then nkv_paged_attn_decode_t64 (two launches). */
 int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                               int64_t kv_seq_stride, int64_t kv_head_stride, uint8_t* pages,
                               const int32_t* page_table, int64_t table_stride, uint16_t* rings,

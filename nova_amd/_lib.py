@@ -133,11 +133,14 @@ def ptr(t: torch.Tensor | None) -> int | None:
 _WORKSPACES: dict[str, torch.Tensor] = {}
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A cached per-device byte workspace of at least ``nbytes`` (grown eagerly, never inside capture)."""
-    key = str(device)
+def workspace(device: torch.device, nbytes: int, kind: str = "scratch") -> torch.Tensor:
+    """A cached per-device, zero-filled byte workspace of at least ``nbytes`` (grown eagerly,
+    never inside capture). ``kind="decode"`` is the decode attention's own buffer: its last
+    bytes hold completion counters that every launch leaves at zero, so no other kernel may
+    write there; callers pass the whole buffer (``numel()`` bytes)."""
+    key = f"{device}/{kind}"
     w = _WORKSPACES.get(key)
     if w is None or w.numel() < nbytes:
-        w = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        w = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = w
     return w

@@ -130,6 +130,11 @@ struct AttnArgs {
   uint16_t* out;
   float* lse;
   float* ws;
+  // fused tail: the last prefix workgroup of each head runs the tail. Its ticket comes from
+  // counter i = head (paged: sequence * hkv + head) at tail_ctr_end[-1 - i], the workspace's
+  // last bytes; the counters start at zero and every launch leaves them at zero.
+  int inline_tail;
+  int* tail_ctr_end;
 };
 
 // XOR key of the 16-byte chunk positions of LDS row `row` (a token within its group).
@@ -694,8 +699,11 @@ __device__ __forceinline__ void append_tok_rows(const AttnArgs& a, int h, int64_
   float scale;
   const uint2 cw = sym_quant8(v, scale);
   const int64_t row = (int64_t)h * a.capacity + pos;
-  *reinterpret_cast<uint2*>((wave == 0 ? a.kq : a.vq) + row * D + 8 * lane) = cw;
-  if (lane == 0) (wave == 0 ? a.ksc : a.vsc)[row] = f2h(scale);
+  // agent-scope stores: the fused tail of this launch reads the token
+  __hip_atomic_store(reinterpret_cast<uint64_t*>((wave == 0 ? a.kq : a.vq) + row * D + 8 * lane),
+                     __builtin_bit_cast(uint64_t, cw), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0)
+    __hip_atomic_store((wave == 0 ? a.ksc : a.vsc) + row, f2h(scale), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void write_scalars(const AttnArgs& a, int64_t pos) {
@@ -811,14 +819,17 @@ __device__ __forceinline__ void append_unit(const UnitIO& io, int unit, int64_t 
   }
   const float step = ruler_step(lo, hi), inv = ruler_inv(step);
   if (r0 == 0) {
-    io.mn[ch] = f2h(lo);
-    io.st[ch] = f2h(step);
+    // agent-scope stores: the fused tail of this launch may read the group (it completes)
+    __hip_atomic_store(io.mn + ch, f2h(lo), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(io.st + ch, f2h(step), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   uint16_t* ring = const_cast<uint16_t*>(io.ring) + ch;
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
     const int r = r0 + 8 * WAVES * i;
-    if (r < io.code_rows) io.codes[r * D + ch] = (uint8_t)ruler_code_rcp(v[i], lo, step, inv);
+    if (r < io.code_rows)
+      __hip_atomic_store(io.codes + r * D + ch, (uint8_t)ruler_code_rcp(v[i], lo, step, inv), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     if (r == slot) ring[slot * D] = bits[i];
   }
 }
@@ -950,6 +961,257 @@ __device__ __forceinline__ int64_t prefix_limit(const AttnArgs& a, int64_t& pos,
 // after this launch completes. In the fused step, workgroup part < APPEND_UNITS first runs
 // append unit `part` of head h (the prefix never reads the group it writes), and the grid
 // has max(n_parts, APPEND_UNITS) parts per head; parts >= n_parts only append.
+// ---------------------------------------------------------------- the tail (ring + merge)
+
+constexpr int TB_WAVES = 8;
+constexpr int TB_THREADS = 64 * TB_WAVES;
+constexpr int MERGE_CHUNK = 32;  // partial slots per column loaded up front
+constexpr int RING_PARTS = 4;    // the ring's 64 tokens as 4 partials of 16
+constexpr int WT_STRIDE = 256;  // partials one merge holds
+static_assert(TB_WAVES == WAVES, "the prefix kernel's last workgroup runs the tail with its own waves");
+
+struct TailSmem {
+  uint8_t ring_lds[2 * RING_BYTES];          // K | V values
+  float ring_part[RING_PARTS][16 * D + 32];  // the ring's partials
+  float pre_acc[16 * D];                     // prefix: sum_s w_s acc_s per column
+  float pre_m[16], pre_l[16];                // prefix: max_s m_s, sum_s w_s l_s
+  float wbuf[TB_WAVES][WT_STRIDE];           // one head's w_s per wave
+};
+static_assert(sizeof(TailSmem) <= LDS_BYTES && sizeof(TailSmem) <= LDS_BYTES_TOK,
+              "the tail's LDS fits in the prefix kernel's stages");
+
+// Loads of data other workgroups of the same launch wrote with agent-scope stores: coherent
+// at agent scope (they bypass the XCD-local L2) when `co`, plain loads otherwise.
+__device__ __forceinline__ float ld_f(const float* p, bool co) {
+  return co ? __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *p;
+}
+__device__ __forceinline__ float2 ld_f2(const float* p, bool co) {
+  if (!co) return *reinterpret_cast<const float2*>(p);
+  return __builtin_bit_cast(float2, __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ uint2 ld_u2(const uint8_t* p, bool co) {
+  if (!co) return *reinterpret_cast<const uint2*>(p);
+  return __builtin_bit_cast(uint2, __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ uint4 ld_u4(const uint16_t* p, bool co) {
+  if (!co) return *reinterpret_cast<const uint4*>(p);
+  const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+  const uint64_t x = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t y = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return uint4{(uint32_t)x, (uint32_t)(x >> 32), (uint32_t)y, (uint32_t)(y >> 32)};
+}
+__device__ __forceinline__ uint16_t ld_u16(const uint16_t* p, bool co) {
+  return co ? __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *p;
+}
+
+// The tail of one decode step for KV head h (of sequence b when paged), by the 8 waves of the
+// calling workgroup: attends over the ring (or the group the token completed), merges the
+// prefix partials and the ring's partials by log-sum-exp and writes out / lse. Every phase is
+// spread over the waves (a wave's dependent instruction chain is what bounds it), and every
+// load it needs is issued at its start.
+//
+// `inl`: run by the last prefix workgroup of the head inside the fused launch. The partials,
+// the codes of a completed group and a new per-token symmetric token were then written in
+// this launch by other workgroups with agent-scope stores and are read with agent-scope
+// loads; the ring slot of the new token is taken from k_new / v_new (this launch's append
+// writes it concurrently), every other slot was written by earlier launches.
+template <bool PAGED>
+__device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailSmem& sm, bool inl) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int gq = a.gq, pw = part_stride(gq), cols = gq * D;
+  const int P = PAGED ? a.seq_parts[2 * b + 1] : a.n_parts;
+  const bool fused = PAGED || a.tail_mode == TAIL_FUSED;
+
+  int64_t pos;
+  bool pos_ok;
+  int64_t U;
+  if constexpr (PAGED) {
+    pos = a.pos_dev[b];
+    pos_ok = pos >= 0 && pos / GT < a.table_stride;
+    U = pos_ok ? pos / GT * GT : 0;
+  } else {
+    U = prefix_limit(a, pos, pos_ok);
+  }
+  const bool ring = (PAGED || a.tail_mode != TAIL_NONE) && (!fused || pos_ok);
+  // while waves 0..3 attend over the ring, the others merge the prefix partials
+  const int mbase = ring ? RING_PARTS : 0, nmw = TB_WAVES - mbase;
+  const bool merger = wave >= mbase;
+
+  // ---- every load up front: ring quarters (or the completed group), `first`, the mask, q;
+  // for a merging wave the m / l of its first head's partials (lane s) and its two columns
+  // (2 lane, 2 lane + 1) of the first MERGE_CHUNK partials
+  const int which = wave >> 2, qtr = wave & 3;
+  const bool completes = fused && pos_ok && !a.tok && (pos + 1) % GT == 0;  // the token completed its group
+  const bool tok1 = !PAGED && ring && a.tok;  // per-token symmetric fused step: the tail is the new token
+  const uint16_t* ring_h = PAGED ? a.rings + (((int64_t)b * a.hkv + h) * 2 + which) * GT * D : ring_of(a, h, which);
+  RingQuarter rq;
+  if (ring && !completes && !tok1) {
+    ring_load_quarter(ring_h, PAGED ? GT : (int)a.tail_slots, qtr, rq);
+    if (inl && !PAGED && a.tail_mode == TAIL_FUSED) {
+      // the new token's slot: from the step's input, not the ring this launch writes
+      const int slot = (int)(pos % GT), rl = lane >> 4, cl = lane & 15;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (16 * qtr + rl + 4 * i == slot)
+          rq.rows[i] = *reinterpret_cast<const uint4*>(fresh_of(a, h, which) + 8 * cl);
+    }
+  }
+  uint2 tw = {0u, 0u};
+  uint16_t tsc = 0;
+  if (tok1 && qtr == 0 && lane < 16) {
+    const int64_t row = (int64_t)h * a.capacity + pos;
+    tw = ld_u2((which == 0 ? a.kq : a.vq) + row * D + 8 * lane, inl);
+    tsc = ld_u16((which == 0 ? a.ksc : a.vsc) + row, inl);
+  }
+  uint2 cw[4];
+  uint4 cst, cmn;
+  if (completes) {
+    const int64_t gcur = pos / GT;
+    const uint8_t* codes;
+    const uint16_t *gst, *gmn;
+    if constexpr (PAGED) {
+      const uint8_t* base = a.pages + ((int64_t)a.table[(int64_t)b * a.table_stride + gcur] * a.hkv + h) * PAGE_BYTES;
+      codes = base + which * CODE_BYTES;
+      gst = reinterpret_cast<const uint16_t*>(base + 2 * CODE_BYTES) + which * 2 * D;
+      gmn = gst + D;
+    } else {
+      const int64_t ro = ((int64_t)h * a.ngroups_cap + gcur) * D;
+      codes = (which == 0 ? a.kq : a.vq) + ((int64_t)h * a.capacity + gcur * GT) * D;
+      gst = (which == 0 ? a.kst : a.vst) + ro;
+      gmn = (which == 0 ? a.kmn : a.vmn) + ro;
+    }
+    const bool co = inl && !PAGED;
+    codes += 8 * (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cw[i] = ld_u2(codes + (16 * qtr + (lane >> 4) + 4 * i) * D, co);
+    cst = ld_u4(gst + 8 * (lane & 15), co);
+    cmn = ld_u4(gmn + 8 * (lane & 15), co);
+  }
+  const int64_t first = (!PAGED && ring && a.first_dev) ? *a.first_dev : 0;
+  const bool mask_on = ring && a.tail_mode == TAIL_MASK && lane < a.tail_slots && a.tail_mask[lane] != 0;
+  half8_t qb[4];
+  const int64_t qh0 = (int64_t)b * a.hq + h * gq;  // first query head of this workgroup
+  if (ring && wave < RING_PARTS) load_q(a.q + qh0 * D, gq, qb);
+  const float* hws = PAGED ? a.ws + ((int64_t)h * a.total_parts + a.seq_parts[2 * b]) * pw : a.ws + (int64_t)h * P * pw;
+  const int head0 = wave - mbase;
+  float m0 = NEG_INF, l0 = 0.0f;
+  float2 v0[MERGE_CHUNK];
+  if (merger && head0 < gq) {
+    if (lane < P) {
+      m0 = ld_f(hws + (int64_t)lane * pw + gq * D + head0, inl);
+      l0 = ld_f(hws + (int64_t)lane * pw + gq * D + gq + head0, inl);
+    }
+#pragma unroll
+    for (int u = 0; u < MERGE_CHUNK; ++u)
+      v0[u] = u < P ? ld_f2(hws + (int64_t)u * pw + head0 * D + 2 * lane, inl) : float2{0.f, 0.f};
+  }
+
+  // ---- the ring into LDS. A token that completes its group is attended through the group's
+  // int8 values, dequantized as the prefix dequantizes them.
+  uint8_t* ring_k = sm.ring_lds;
+  uint8_t* ring_v = sm.ring_lds + RING_BYTES;
+  if (ring) {
+    if (completes) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rq.rows[i] = __builtin_bit_cast(uint4, dq8(cw[i].x, cw[i].y, cst, cmn));
+    }
+    if (tok1) {
+      if (qtr == 0 && lane < 16) {
+        const _Float16 sc = __builtin_bit_cast(_Float16, tsc);
+        *reinterpret_cast<half8_t*>((which == 0 ? ring_k : ring_v) + (ring_chunk_pos(0, lane) << 4)) =
+            dq8_sym(tw.x, tw.y, half2_t{sc, sc});
+      }
+    } else {
+      ring_quarter_to_lds(rq.rows, qtr, which == 0 ? ring_k : ring_v);
+    }
+    __syncthreads();
+  }
+  if (!merger) {
+    // ---- ring attention: 4 waves x 16 tokens, one partial each
+    const int64_t written = fused ? pos + 1 : (a.tail_mode == TAIL_SCALARS ? *a.written_dev : 0);
+    uint64_t bits;
+    if (completes) bits = ~0ull;
+    else if (tok1) bits = wave == 0 ? 1ull : 0ull;
+    else if (a.tail_mode == TAIL_MASK) bits = __builtin_amdgcn_ballot_w64(mask_on);
+    else bits = ring_bits(written, U, first);
+    WaveState st;
+    state_init(st);
+    attend_ring16(a, st, qb, ring_k, ring_v, wave, bits);
+    store_wave_partial(st, gq, sm.ring_part[wave]);
+  } else {
+    // ---- prefix merge, one head at a time: m_p = max_s m_s, w_s = 2^(m_s - m_p),
+    // l_p = sum_s w_s l_s, pre_acc = sum_s w_s acc_s (two columns per lane)
+    float* wb = sm.wbuf[wave];
+    for (int head = head0; head < gq; head += nmw) {
+      const bool first_head = head == head0;
+      float m = first_head ? m0 : NEG_INF;
+      for (int s = first_head ? lane + 64 : lane; s < P; s += 64) m = fmaxf(m, ld_f(hws + (int64_t)s * pw + gq * D + head, inl));
+      m = wave_max(m);
+      float l = 0.0f;
+      for (int s = lane; s < P; s += 64) {
+        const float ms = (first_head && s == lane) ? m0 : ld_f(hws + (int64_t)s * pw + gq * D + head, inl);
+        const float ls = (first_head && s == lane) ? l0 : ld_f(hws + (int64_t)s * pw + gq * D + gq + head, inl);
+        const float w = ms == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(ms - m);
+        wb[s] = w;
+        l += ls * w;
+      }
+      l = wave_sum(l);
+      float2 acc = {0.0f, 0.0f};
+      if (first_head) {
+#pragma unroll
+        for (int u = 0; u < MERGE_CHUNK; ++u) {
+          const float w = u < P ? wb[u] : 0.0f;
+          acc.x += v0[u].x * w;
+          acc.y += v0[u].y * w;
+        }
+      } else {
+        for (int s = 0; s < min(P, MERGE_CHUNK); ++s) {
+          const float2 vv = ld_f2(hws + (int64_t)s * pw + head * D + 2 * lane, inl);
+          acc.x += vv.x * wb[s];
+          acc.y += vv.y * wb[s];
+        }
+      }
+      for (int s = MERGE_CHUNK; s < P; ++s) {
+        const float2 vv = ld_f2(hws + (int64_t)s * pw + head * D + 2 * lane, inl);
+        acc.x += vv.x * wb[s];
+        acc.y += vv.y * wb[s];
+      }
+      *reinterpret_cast<float2*>(sm.pre_acc + head * D + 2 * lane) = acc;
+      if (lane == 0) { sm.pre_m[head] = m; sm.pre_l[head] = l; }
+    }
+  }
+  __syncthreads();
+
+  // ---- combine: prefix (m_p, l_p, pre_acc) and the ring's partials, one column per thread
+  for (int col = tid; col < cols; col += TB_THREADS) {
+    const int head = col / D;
+    const float mp = sm.pre_m[head];
+    float M = mp;
+    if (ring) {
+#pragma unroll
+      for (int r = 0; r < RING_PARTS; ++r) M = fmaxf(M, sm.ring_part[r][gq * D + head]);
+    }
+    const float Mu = M == NEG_INF ? 0.0f : M;
+    const float alpha = mp == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mp - Mu);
+    float acc = alpha * sm.pre_acc[col], l = alpha * sm.pre_l[head];
+    if (ring) {
+#pragma unroll
+      for (int r = 0; r < RING_PARTS; ++r) {
+        const float mr = sm.ring_part[r][gq * D + head];
+        const float beta = mr == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mr - Mu);
+        acc += beta * sm.ring_part[r][col];
+        l += beta * sm.ring_part[r][gq * D + gq + head];
+      }
+    }
+    const int64_t qh = qh0 + head;
+    const int d = col % D;
+    a.out[(int64_t)qh * D + d] = f2h(l > 0.0f ? acc * (INV_P_SCALE / l) : 0.0f);
+    if (a.lse && d == 0) a.lse[qh] = l > 0.0f ? (M + __log2f(l)) * LN2 : NEG_INF;
+  }
+}
+
 template <int LAYOUT>
 __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   constexpr bool TOK = LAYOUT == CONTIG_TOK, PAGED = LAYOUT == PAGED_T64;
@@ -1036,280 +1298,102 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
     if (blockIdx.x == 0 && tid == 0) write_scalars(a, pos);
   }
 
-  if (!prefix) return;
-  WaveState st;
-  state_init(st);
-  half8_t qb[4];
-  load_q_lds(q_lds, a.gq, qb);
+  if (prefix) {
+    WaveState st;
+    state_init(st);
+    half8_t qb[4];
+    load_q_lds(q_lds, a.gq, qb);
 
-  int gi = wave;
-  for (int rs = 0; gi < ng; rs ^= 1) {
-    const int64_t grp = gs + gi;
-    const uint8_t* rul = my_stages + 2 * HALF_SLOT + rs * RULER_BYTES;
-    const uint8_t* slot1 = my_stages + slot_bytes;
-    // first half (slot 0); the second half, issued after it, may stay in flight
-    if constexpr (TOK) {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_HALF_TOK) : "memory");
-      attend_block_tok(a, st, qb, my_stages, my_stages + HALF_CODE,
-                       reinterpret_cast<const uint16_t*>(my_stages + 2 * HALF_CODE),
-                       reinterpret_cast<const uint16_t*>(my_stages + 2 * HALF_CODE + TOK_SCALE_BYTES),
-                       (int)min<int64_t>(32, U - grp * GT));
-    } else {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_SECOND_HALF) : "memory");
-      attend_block<1>(a, st, qb, my_stages, my_stages + HALF_CODE, rul, (int)min<int64_t>(32, U - grp * GT));
+    int gi = wave;
+    for (int rs = 0; gi < ng; rs ^= 1) {
+      const int64_t grp = gs + gi;
+      const uint8_t* rul = my_stages + 2 * HALF_SLOT + rs * RULER_BYTES;
+      const uint8_t* slot1 = my_stages + slot_bytes;
+      // first half (slot 0); the second half, issued after it, may stay in flight
+      if constexpr (TOK) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_HALF_TOK) : "memory");
+        attend_block_tok(a, st, qb, my_stages, my_stages + HALF_CODE,
+                         reinterpret_cast<const uint16_t*>(my_stages + 2 * HALF_CODE),
+                         reinterpret_cast<const uint16_t*>(my_stages + 2 * HALF_CODE + TOK_SCALE_BYTES),
+                         (int)min<int64_t>(32, U - grp * GT));
+      } else {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_SECOND_HALF) : "memory");
+        attend_block<1>(a, st, qb, my_stages, my_stages + HALF_CODE, rul, (int)min<int64_t>(32, U - grp * GT));
+      }
+      int nx = 0;
+      if (lane == 0) nx = __hip_atomic_fetch_add(&next_group, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      nx = __builtin_amdgcn_readfirstlane(nx);
+      // second half (slot 1)
+      const int nv2 = (int)min<int64_t>(32, U - grp * GT - 32);
+      if constexpr (TOK) {
+        if (nx < ng) issue_half_tok(a, h, gs + nx, 0, my_lds);
+        if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_HALF_TOK) : "memory");
+        else wait_groups_all();
+        if (nv2 > 0)
+          attend_block_tok(a, st, qb, slot1, slot1 + HALF_CODE, reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE),
+                           reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE + TOK_SCALE_BYTES), nv2);
+        if (nx < ng) issue_half_tok(a, h, gs + nx, 1, my_lds + HALF_SLOT_TOK);
+      } else if constexpr (PAGED) {
+        if (nx < ng) issue_half_paged(a, b, h, gs + nx, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
+        if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF_PAGED) : "memory");
+        else wait_groups_all();
+        if (nv2 > 0) attend_block<1>(a, st, qb, slot1, slot1 + HALF_CODE, rul, nv2);
+        if (nx < ng) issue_half_paged(a, b, h, gs + nx, 1, my_lds + HALF_SLOT, 0u);
+      } else {
+        if (nx < ng) issue_half(a, h, gs + nx, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
+        if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF) : "memory");
+        else wait_groups_all();
+        if (nv2 > 0) attend_block<1>(a, st, qb, slot1, slot1 + HALF_CODE, rul, nv2);
+        if (nx < ng) issue_half(a, h, gs + nx, 1, my_lds + HALF_SLOT, 0u);
+      }
+      gi = nx;
     }
-    int nx = 0;
-    if (lane == 0) nx = __hip_atomic_fetch_add(&next_group, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    nx = __builtin_amdgcn_readfirstlane(nx);
-    // second half (slot 1)
-    const int nv2 = (int)min<int64_t>(32, U - grp * GT - 32);
-    if constexpr (TOK) {
-      if (nx < ng) issue_half_tok(a, h, gs + nx, 0, my_lds);
-      if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_HALF_TOK) : "memory");
-      else wait_groups_all();
-      if (nv2 > 0)
-        attend_block_tok(a, st, qb, slot1, slot1 + HALF_CODE, reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE),
-                         reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE + TOK_SCALE_BYTES), nv2);
-      if (nx < ng) issue_half_tok(a, h, gs + nx, 1, my_lds + HALF_SLOT_TOK);
-    } else if constexpr (PAGED) {
-      if (nx < ng) issue_half_paged(a, b, h, gs + nx, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
-      if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF_PAGED) : "memory");
-      else wait_groups_all();
-      if (nv2 > 0) attend_block<1>(a, st, qb, slot1, slot1 + HALF_CODE, rul, nv2);
-      if (nx < ng) issue_half_paged(a, b, h, gs + nx, 1, my_lds + HALF_SLOT, 0u);
-    } else {
-      if (nx < ng) issue_half(a, h, gs + nx, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
-      if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF) : "memory");
-      else wait_groups_all();
-      if (nv2 > 0) attend_block<1>(a, st, qb, slot1, slot1 + HALF_CODE, rul, nv2);
-      if (nx < ng) issue_half(a, h, gs + nx, 1, my_lds + HALF_SLOT, 0u);
-    }
-    gi = nx;
-  }
 
-  // ---- merge the waves through LDS (the stages are dead once every wave is here)
+    // ---- merge the waves through LDS (the stages are dead once every wave is here)
+    __syncthreads();
+    const int gq = a.gq, pw = part_stride(gq);
+    store_wave_partial(st, gq, lds + wave * pw);
+    __syncthreads();
+    float* dst = a.ws + ((int64_t)h * (PAGED ? a.total_parts : a.n_parts) + pslot) * pw;
+    for (int e = tid; e < gq * D + 2 * gq; e += THREADS) {
+      const int head = e < gq * D ? e / D : (e - gq * D) % gq;
+      float m = NEG_INF;
+      for (int w = 0; w < WAVES; ++w) m = fmaxf(m, lds[w * pw + gq * D + head]);
+      const float mu = m == NEG_INF ? 0.0f : m;
+      float sum = 0.0f;
+      const int src = e < gq * D ? e : gq * D + gq + head;  // acc element, or l for both m and l slots
+      for (int w = 0; w < WAVES; ++w) sum += lds[w * pw + src] * __builtin_amdgcn_exp2f(lds[w * pw + gq * D + head] - mu);
+      const float v = e < gq * D ? sum : (e < gq * D + gq ? m : sum);
+      if (a.inline_tail) __hip_atomic_store(dst + e, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else dst[e] = v;
+    }
+  }  // prefix
+
+  // ---- fused tail: once every store of this workgroup (partial, append) is done, take a
+  // ticket; the head's last workgroup resets the counter and runs the tail
+  if (!a.inline_tail) return;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  const int gq = a.gq, pw = part_stride(gq);
-  store_wave_partial(st, gq, lds + wave * pw);
-  __syncthreads();
-  float* dst = a.ws + ((int64_t)h * (PAGED ? a.total_parts : a.n_parts) + pslot) * pw;
-  for (int e = tid; e < gq * D + 2 * gq; e += THREADS) {
-    const int head = e < gq * D ? e / D : (e - gq * D) % gq;
-    float m = NEG_INF;
-    for (int w = 0; w < WAVES; ++w) m = fmaxf(m, lds[w * pw + gq * D + head]);
-    const float mu = m == NEG_INF ? 0.0f : m;
-    float sum = 0.0f;
-    const int src = e < gq * D ? e : gq * D + gq + head;  // acc element, or l for both m and l slots
-    for (int w = 0; w < WAVES; ++w) sum += lds[w * pw + src] * __builtin_amdgcn_exp2f(lds[w * pw + gq * D + head] - mu);
-    dst[e] = e < gq * D ? sum : (e < gq * D + gq ? m : sum);
+  const int last = (PAGED ? nparts : (int)(gridDim.x / a.hkv)) - 1;
+  int* ctr = a.tail_ctr_end - 1 - (PAGED ? b * a.hkv + h : h);
+  if (tid == 0) {
+    const int t = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t == last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    next_group = t;
   }
+  __syncthreads();
+  if (next_group == last) tail_body<PAGED>(a, h, b, *reinterpret_cast<TailSmem*>(lds_raw), true);
 }
 
 // ---------------------------------------------------------------- kernel B: ring + merge
 
-constexpr int TB_WAVES = 8;
-constexpr int TB_THREADS = 64 * TB_WAVES;
-constexpr int MERGE_CHUNK = 32;  // partial slots per column loaded up front
-constexpr int RING_PARTS = 4;    // the ring's 64 tokens as 4 partials of 16
-constexpr int WT_STRIDE = 256;  // partials one merge holds
-
-// One workgroup per KV head, after the prefix kernel: attends over the ring (or the group
-// the token completed), then merges the prefix partials and the ring's partials by
-// log-sum-exp and writes out / lse. Every phase is spread over the 8 waves (a wave's
-// dependent instruction chain is what bounds this kernel), and every load it needs is
-// issued at its start.
+// One workgroup per KV head (per sequence and KV head when paged), after the prefix kernel.
 template <bool PAGED>
 __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t ring_lds[2 * RING_BYTES];          // K | V values
-  __shared__ __attribute__((aligned(16))) float ring_part[RING_PARTS][16 * D + 32];  // the ring's partials
-  __shared__ __attribute__((aligned(16))) float pre_acc[16 * D];  // prefix: sum_s w_s acc_s per column
-  __shared__ float pre_m[16], pre_l[16];                           // prefix: max_s m_s, sum_s w_s l_s
-  __shared__ __attribute__((aligned(16))) float wbuf[TB_WAVES][WT_STRIDE];  // one head's w_s per wave
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  // paged: workgroup (b, h) serves KV head h of sequence b, whose partials are units
-  // seq_parts[2b] .. + seq_parts[2b + 1] - 1
+  __shared__ __attribute__((aligned(16))) TailSmem sm;
   const int h = PAGED ? blockIdx.x % a.hkv : blockIdx.x;
   const int b = PAGED ? blockIdx.x / a.hkv : 0;
-  const int gq = a.gq, pw = part_stride(gq), cols = gq * D;
-  const int P = PAGED ? a.seq_parts[2 * b + 1] : a.n_parts;
-  const bool fused = PAGED || a.tail_mode == TAIL_FUSED;
-
-  int64_t pos;
-  bool pos_ok;
-  int64_t U;
-  if constexpr (PAGED) {
-    pos = a.pos_dev[b];
-    pos_ok = pos >= 0 && pos / GT < a.table_stride;
-    U = pos_ok ? pos / GT * GT : 0;
-  } else {
-    U = prefix_limit(a, pos, pos_ok);
-  }
-  const bool ring = (PAGED || a.tail_mode != TAIL_NONE) && (!fused || pos_ok);
-  // while waves 0..3 attend over the ring, the others merge the prefix partials
-  const int mbase = ring ? RING_PARTS : 0, nmw = TB_WAVES - mbase;
-  const bool merger = wave >= mbase;
-
-  // ---- every load up front: ring quarters (or the completed group), `first`, the mask, q;
-  // for a merging wave the m / l of its first head's partials (lane s) and its two columns
-  // (2 lane, 2 lane + 1) of the first MERGE_CHUNK partials
-  const int which = wave >> 2, qtr = wave & 3;
-  const bool completes = fused && pos_ok && !a.tok && (pos + 1) % GT == 0;  // the token completed its group
-  const bool tok1 = !PAGED && ring && a.tok;  // per-token symmetric fused step: the tail is the new token
-  const uint16_t* ring_h = PAGED ? a.rings + (((int64_t)b * a.hkv + h) * 2 + which) * GT * D : ring_of(a, h, which);
-  RingQuarter rq;
-  if (ring && !completes && !tok1) ring_load_quarter(ring_h, PAGED ? GT : (int)a.tail_slots, qtr, rq);
-  uint2 tw = {0u, 0u};
-  uint16_t tsc = 0;
-  if (tok1 && qtr == 0 && lane < 16) {
-    const int64_t row = (int64_t)h * a.capacity + pos;
-    tw = *reinterpret_cast<const uint2*>((which == 0 ? a.kq : a.vq) + row * D + 8 * lane);
-    tsc = (which == 0 ? a.ksc : a.vsc)[row];
-  }
-  uint2 cw[4];
-  uint4 cst, cmn;
-  if (completes) {
-    const int64_t gcur = pos / GT;
-    const uint8_t* codes;
-    const uint16_t *gst, *gmn;
-    if constexpr (PAGED) {
-      const uint8_t* base = a.pages + ((int64_t)a.table[(int64_t)b * a.table_stride + gcur] * a.hkv + h) * PAGE_BYTES;
-      codes = base + which * CODE_BYTES;
-      gst = reinterpret_cast<const uint16_t*>(base + 2 * CODE_BYTES) + which * 2 * D;
-      gmn = gst + D;
-    } else {
-      const int64_t ro = ((int64_t)h * a.ngroups_cap + gcur) * D;
-      codes = (which == 0 ? a.kq : a.vq) + ((int64_t)h * a.capacity + gcur * GT) * D;
-      gst = (which == 0 ? a.kst : a.vst) + ro;
-      gmn = (which == 0 ? a.kmn : a.vmn) + ro;
-    }
-    codes += 8 * (lane & 15);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) cw[i] = *reinterpret_cast<const uint2*>(codes + (16 * qtr + (lane >> 4) + 4 * i) * D);
-    cst = *reinterpret_cast<const uint4*>(gst + 8 * (lane & 15));
-    cmn = *reinterpret_cast<const uint4*>(gmn + 8 * (lane & 15));
-  }
-  const int64_t first = (!PAGED && ring && a.first_dev) ? *a.first_dev : 0;
-  const bool mask_on = ring && a.tail_mode == TAIL_MASK && lane < a.tail_slots && a.tail_mask[lane] != 0;
-  half8_t qb[4];
-  const int64_t qh0 = (int64_t)b * a.hq + h * gq;  // first query head of this workgroup
-  if (ring && wave < RING_PARTS) load_q(a.q + qh0 * D, gq, qb);
-  const float* hws = PAGED ? a.ws + ((int64_t)h * a.total_parts + a.seq_parts[2 * b]) * pw : a.ws + (int64_t)h * P * pw;
-  const int head0 = wave - mbase;
-  float m0 = NEG_INF, l0 = 0.0f;
-  float2 v0[MERGE_CHUNK];
-  if (merger && head0 < gq) {
-    if (lane < P) {
-      m0 = hws[(int64_t)lane * pw + gq * D + head0];
-      l0 = hws[(int64_t)lane * pw + gq * D + gq + head0];
-    }
-#pragma unroll
-    for (int u = 0; u < MERGE_CHUNK; ++u)
-      v0[u] = u < P ? *reinterpret_cast<const float2*>(hws + (int64_t)u * pw + head0 * D + 2 * lane) : float2{0.f, 0.f};
-  }
-
-  // ---- the ring (the prefix kernel did the fused step's append) into LDS. A token that
-  // completes its group is attended through the group's int8 values, dequantized as the
-  // prefix dequantizes them.
-  uint8_t* ring_k = ring_lds;
-  uint8_t* ring_v = ring_lds + RING_BYTES;
-  if (ring) {
-    if (completes) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) rq.rows[i] = __builtin_bit_cast(uint4, dq8(cw[i].x, cw[i].y, cst, cmn));
-    }
-    if (tok1) {
-      if (qtr == 0 && lane < 16) {
-        const _Float16 sc = __builtin_bit_cast(_Float16, tsc);
-        *reinterpret_cast<half8_t*>((which == 0 ? ring_k : ring_v) + (ring_chunk_pos(0, lane) << 4)) =
-            dq8_sym(tw.x, tw.y, half2_t{sc, sc});
-      }
-    } else {
-      ring_quarter_to_lds(rq.rows, qtr, which == 0 ? ring_k : ring_v);
-    }
-    __syncthreads();
-  }
-  if (!merger) {
-    // ---- ring attention: 4 waves x 16 tokens, one partial each
-    const int64_t written = fused ? pos + 1 : (a.tail_mode == TAIL_SCALARS ? *a.written_dev : 0);
-    uint64_t bits;
-    if (completes) bits = ~0ull;
-    else if (tok1) bits = wave == 0 ? 1ull : 0ull;
-    else if (a.tail_mode == TAIL_MASK) bits = __builtin_amdgcn_ballot_w64(mask_on);
-    else bits = ring_bits(written, U, first);
-    WaveState st;
-    state_init(st);
-    attend_ring16(a, st, qb, ring_k, ring_v, wave, bits);
-    store_wave_partial(st, gq, ring_part[wave]);
-  } else {
-    // ---- prefix merge, one head at a time: m_p = max_s m_s, w_s = 2^(m_s - m_p),
-    // l_p = sum_s w_s l_s, pre_acc = sum_s w_s acc_s (two columns per lane)
-    float* wb = wbuf[wave];
-    for (int head = head0; head < gq; head += nmw) {
-      const bool first_head = head == head0;
-      float m = first_head ? m0 : NEG_INF;
-      for (int s = first_head ? lane + 64 : lane; s < P; s += 64) m = fmaxf(m, hws[(int64_t)s * pw + gq * D + head]);
-      m = wave_max(m);
-      float l = 0.0f;
-      for (int s = lane; s < P; s += 64) {
-        const float ms = (first_head && s == lane) ? m0 : hws[(int64_t)s * pw + gq * D + head];
-        const float ls = (first_head && s == lane) ? l0 : hws[(int64_t)s * pw + gq * D + gq + head];
-        const float w = ms == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(ms - m);
-        wb[s] = w;
-        l += ls * w;
-      }
-      l = wave_sum(l);
-      float2 acc = {0.0f, 0.0f};
-      if (first_head) {
-#pragma unroll
-        for (int u = 0; u < MERGE_CHUNK; ++u) {
-          const float w = u < P ? wb[u] : 0.0f;
-          acc.x += v0[u].x * w;
-          acc.y += v0[u].y * w;
-        }
-      } else {
-        for (int s = 0; s < min(P, MERGE_CHUNK); ++s) {
-          const float2 vv = *reinterpret_cast<const float2*>(hws + (int64_t)s * pw + head * D + 2 * lane);
-          acc.x += vv.x * wb[s];
-          acc.y += vv.y * wb[s];
-        }
-      }
-      for (int s = MERGE_CHUNK; s < P; ++s) {
-        const float2 vv = *reinterpret_cast<const float2*>(hws + (int64_t)s * pw + head * D + 2 * lane);
-        acc.x += vv.x * wb[s];
-        acc.y += vv.y * wb[s];
-      }
-      *reinterpret_cast<float2*>(pre_acc + head * D + 2 * lane) = acc;
-      if (lane == 0) { pre_m[head] = m; pre_l[head] = l; }
-    }
-  }
-  __syncthreads();
-
-  // ---- combine: prefix (m_p, l_p, pre_acc) and the ring's partials, one column per thread
-  for (int col = tid; col < cols; col += TB_THREADS) {
-    const int head = col / D;
-    const float mp = pre_m[head];
-    float M = mp;
-    if (ring) {
-#pragma unroll
-      for (int r = 0; r < RING_PARTS; ++r) M = fmaxf(M, ring_part[r][gq * D + head]);
-    }
-    const float Mu = M == NEG_INF ? 0.0f : M;
-    const float alpha = mp == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mp - Mu);
-    float acc = alpha * pre_acc[col], l = alpha * pre_l[head];
-    if (ring) {
-#pragma unroll
-      for (int r = 0; r < RING_PARTS; ++r) {
-        const float mr = ring_part[r][gq * D + head];
-        const float beta = mr == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mr - Mu);
-        acc += beta * ring_part[r][col];
-        l += beta * ring_part[r][gq * D + gq + head];
-      }
-    }
-    const int64_t qh = qh0 + head;
-    const int d = col % D;
-    a.out[(int64_t)qh * D + d] = f2h(l > 0.0f ? acc * (INV_P_SCALE / l) : 0.0f);
-    if (a.lse && d == 0) a.lse[qh] = l > 0.0f ? (M + __log2f(l)) * LN2 : NEG_INF;
-  }
+  tail_body<PAGED>(a, h, b, sm, false);
 }
 
 // Standalone append: one workgroup per append unit (APPEND_UNITS per KV head).
@@ -1668,6 +1752,8 @@ static int64_t default_parts(int64_t hkv, int64_t groups) {
 }
 
 static int64_t part_floats(int64_t hq, int64_t hkv) { return part_stride((int)(hq / hkv)); }
+// Bytes of the fused tail's completion counters (one int per head, or per sequence and head).
+static int64_t ctr_bytes(int64_t n) { return (n * (int64_t)sizeof(int) + 255) / 256 * 256; }
 
 static int check_heads(int64_t hq, int64_t hkv, int64_t head_dim) {
   if (hkv <= 0 || hq <= 0 || hq % hkv) return fail(NKV_ERR_INVALID, "Q heads %lld not divisible by KV heads %lld", (long long)hq, (long long)hkv);
@@ -1679,23 +1765,30 @@ static int check_heads(int64_t hq, int64_t hkv, int64_t head_dim) {
 // Kernel A over n_parts prefix parts (none when n_parts == 0), then kernel B.
 constexpr int LAUNCH_PREFIX = 1, LAUNCH_TAIL = 2;
 
+// `fusable`: the workspace is one the caller keeps zero-filled for these entry points (the
+// decode-step family), so both launches may become one with the last-workgroup tail.
 static int launch_attn(AttnArgs& a, int64_t n_parts, int64_t workspace_bytes, hipStream_t s, const char* what,
-                       int launches = LAUNCH_PREFIX | LAUNCH_TAIL) {
+                       int launches = LAUNCH_PREFIX | LAUNCH_TAIL, bool fusable = false) {
   if (n_parts < 0) return fail(NKV_ERR_INVALID, "%s: n_parts %lld is negative", what, (long long)n_parts);
   a.n_parts = (int)n_parts;
-  const int64_t need = (int64_t)a.hkv * std::max<int64_t>(1, n_parts) * part_floats(a.hq, a.hkv) * (int64_t)sizeof(float);
+  const int64_t part_bytes = (int64_t)a.hkv * std::max<int64_t>(1, n_parts) * part_floats(a.hq, a.hkv) * (int64_t)sizeof(float);
+  // both launches in one call: the prefix kernel's last workgroup per head runs the tail
+  const bool fuse = fusable && n_parts > 0 && launches == (LAUNCH_PREFIX | LAUNCH_TAIL);
+  const int64_t need = part_bytes + ctr_bytes(a.hkv);  // the counters' bytes stay reserved in every mode
   if (n_parts > 0 && workspace_bytes < need)
     return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
   if (n_parts > 256) return fail(NKV_ERR_UNSUPPORTED, "%s: n_parts %lld exceeds the 256 partials the merge holds", what, (long long)n_parts);
   if (a.capacity > (int64_t(1) << 24))  // code row offsets of one head stay 32-bit
     return fail(NKV_ERR_UNSUPPORTED, "%s: capacity %lld exceeds 16M tokens", what, (long long)a.capacity);
+  a.inline_tail = fuse ? 1 : 0;
+  a.tail_ctr_end = reinterpret_cast<int*>(reinterpret_cast<char*>(a.ws) + (workspace_bytes & ~int64_t(3)));
   if (n_parts > 0 && (launches & LAUNCH_PREFIX)) {
     const int64_t parts = a.tail_mode == TAIL_FUSED && !a.tok ? std::max<int64_t>(n_parts, APPEND_UNITS) : n_parts;
     if (a.tok) hipLaunchKernelGGL(attn_prefix_kernel<CONTIG_TOK>, dim3((unsigned)(a.hkv * parts)), dim3(THREADS), 0, s, a);
     else hipLaunchKernelGGL(attn_prefix_kernel<CONTIG_T64>, dim3((unsigned)(a.hkv * parts)), dim3(THREADS), 0, s, a);
     if (int rc = check_launch(what)) return rc;
   }
-  if (!(launches & LAUNCH_TAIL)) return NKV_OK;
+  if (!(launches & LAUNCH_TAIL) || fuse) return NKV_OK;
   hipLaunchKernelGGL(attn_tail_kernel<false>, dim3((unsigned)a.hkv), dim3(TB_THREADS), 0, s, a);
   return check_launch(what);
 }
@@ -1708,7 +1801,7 @@ using namespace nkv;
 
 extern "C" int64_t nkv_attn_workspace_bytes(int64_t hkv, int64_t hq, int64_t n_parts) {
   if (hkv <= 0 || hq <= 0 || n_parts < 0 || hq % hkv) return 0;
-  return hkv * std::max<int64_t>(1, n_parts) * part_floats(hq, hkv) * (int64_t)sizeof(float);
+  return hkv * std::max<int64_t>(1, n_parts) * part_floats(hq, hkv) * (int64_t)sizeof(float) + ctr_bytes(hkv);
 }
 
 extern "C" int64_t nkv_attn_default_parts(int64_t hkv, int64_t groups) { return default_parts(hkv, groups); }
@@ -1808,7 +1901,7 @@ static int decode_step(const char* what, int launches, const uint16_t* q, const 
   a.tail_mode = TAIL_FUSED;
   a.sl2 = LOG2E / sqrtf((float)head_dim);
   a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace);
-  return launch_attn(a, n_parts, workspace_bytes, static_cast<hipStream_t>(stream), what, launches);
+  return launch_attn(a, n_parts, workspace_bytes, static_cast<hipStream_t>(stream), what, launches, true);
 }
 
 extern "C" int nkv_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
@@ -1951,7 +2044,7 @@ static int decode_step_tok(const char* what, int launches, const uint16_t* q, co
   a.tail_mode = TAIL_FUSED;
   a.sl2 = LOG2E / sqrtf((float)head_dim);
   a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace);
-  return launch_attn(a, n_parts, workspace_bytes, static_cast<hipStream_t>(stream), what, launches);
+  return launch_attn(a, n_parts, workspace_bytes, static_cast<hipStream_t>(stream), what, launches, true);
 }
 
 #define NKV_STEP_TOK_PARAMS                                                                                      \
@@ -1977,7 +2070,7 @@ extern "C" int nkv_decode_step_combine_tok(NKV_STEP_TOK_PARAMS) {
 
 extern "C" int64_t nkv_paged_workspace_bytes(int64_t hkv, int64_t hq, int64_t total_parts) {
   if (hkv <= 0 || hq <= 0 || total_parts <= 0 || hq % hkv) return 0;
-  return hkv * total_parts * part_floats(hq, hkv) * (int64_t)sizeof(float);
+  return hkv * total_parts * part_floats(hq, hkv) * (int64_t)sizeof(float) + ctr_bytes(hkv * total_parts);
 }
 
 static int paged_args(const char* what, AttnArgs& a, const uint8_t* pages, const int32_t* page_table,
@@ -2039,10 +2132,11 @@ static int paged_attn(const char* what, const uint16_t* q, const uint16_t* k_new
   (void)k_new; (void)v_new; (void)kv_seq_stride; (void)kv_head_stride;
   a.sl2 = LOG2E / sqrtf((float)head_dim);
   a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace);
+  // one launch: the last prefix workgroup of each (sequence, KV head) runs its tail
+  a.inline_tail = 1;
+  a.tail_ctr_end = reinterpret_cast<int*>(static_cast<char*>(workspace) + (workspace_bytes & ~int64_t(3)));
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(attn_prefix_kernel<PAGED_T64>, dim3((unsigned)(hkv * total_parts)), dim3(THREADS), 0, s, a);
-  if (int rc = check_launch(what)) return rc;
-  hipLaunchKernelGGL(attn_tail_kernel<true>, dim3((unsigned)(nseq * hkv)), dim3(TB_THREADS), 0, s, a);
   return check_launch(what);
 }
 

@@ -185,10 +185,11 @@ def int8_attn_decode(
     else:
         n_parts = _pick_parts(h_kv, hq, groups, None)
         ws_bytes = int(_lib.load().nkv_attn_workspace_bytes(h_kv, hq, n_parts))
-        if _is_capturing() and (_lib._WORKSPACES.get(str(q.device)) is None
-                                or _lib._WORKSPACES[str(q.device)].numel() < ws_bytes):
+        cached = _lib._WORKSPACES.get(f"{q.device}/decode")
+        if _is_capturing() and (cached is None or cached.numel() < ws_bytes):
             raise ValueError("under graph capture pass scratch=(pm, pl, pa) (no workspace is allocated there)")
-        ws = _lib.workspace(q.device, ws_bytes)
+        ws = _lib.workspace(q.device, ws_bytes, "decode")
+        ws_bytes = ws.numel()
     _lib.call(
         "nkv_attn_decode_t64", q.data_ptr(), kq.data_ptr(), kmn.data_ptr(), kst.data_ptr(), vq.data_ptr(),
         vmn.data_ptr(), vst.data_ptr(), hq, h_kv, d, length, used, prefix_groups,
@@ -383,6 +384,8 @@ class KVInt8Cache:
         self.lse = torch.zeros((batch, self.num_q_heads), dtype=torch.float32, device=device)
         self.merged = torch.zeros((batch, self.num_q_heads, 1, self.head_dim), dtype=dtype, device=device)
         self._n_parts = _pick_parts(self.num_kv_heads, self.num_q_heads, n_groups, self.pa.numel() * 4)
+        # zero-filled and used by this cache's decode launches only: the fused step keeps its
+        # per-head completion counters in the last bytes (every launch leaves them at zero)
         self._ws_bytes = self.pa.numel() * 4
 
         self.staging: Any = None

@@ -110,7 +110,7 @@ def int8_tok_attn_decode(q: torch.Tensor, kq: torch.Tensor, ksc: torch.Tensor, v
     groups = cap // GROUP
     if scratch is None:
         parts = int(n_splits) if n_splits else int(_lib.load().nkv_attn_default_parts(hkv, groups))
-        scratch = _lib.workspace(q.device, int(_lib.load().nkv_attn_workspace_bytes(hkv, hq, parts)))
+        scratch = _lib.workspace(q.device, int(_lib.load().nkv_attn_workspace_bytes(hkv, hq, parts)), "decode")
     else:
         parts = int(n_splits) if n_splits else _parts(hkv, hq, groups, scratch.numel() * scratch.element_size())
     _lib.call("nkv_attn_decode_tok", q.data_ptr(), kq.data_ptr(), ksc.data_ptr(), vq.data_ptr(), vsc.data_ptr(),

@@ -299,6 +299,51 @@ def test_partials_then_combine_equals_fused_step():
         assert torch.equal(a.lse, b.lse), p
 
 
+def test_fused_tail_counters_return_to_zero_and_layers_interleave():
+    """The fused step's last-workgroup tail keeps one completion counter per head at the
+    end of the workspace: after every call they read zero. Two caches of different
+    lengths and several layers interleave on one stream, each call checked against the
+    two-launch split (partials, then the tail kernel), bit for bit."""
+    from nova_amd import _lib
+    from nova_amd.kvattn import KVInt8Cache
+
+    layers, used0 = 3, (130, 700)
+    caches, ref = [], []
+    data = []
+    for i, n in enumerate(used0):
+        _, k, v = make(n + 40, seed=60 + i)
+        data.append((k.cuda(), v.cuda()))
+        pair = []
+        for _ in range(2):
+            c = KVInt8Cache(num_slots=layers, num_kv_heads=H_KV, head_dim=D, max_len=n + 128, num_q_heads=HQ)
+            c.begin_prefill(n)
+            c.set_prefill_pos(0)
+            for layer in range(layers):
+                c.update(data[i][0][:, :, :n], data[i][1][:, :, :n], layer)
+            c.finish_prefill(n)
+            pair.append(c)
+        caches.append(pair[0])
+        ref.append(pair[1])
+    for step in range(40):
+        q = randn((1, HQ, 1, D), 900 + step).cuda()
+        for layer in range(layers):
+            for i, n in enumerate(used0):
+                k, v = data[i]
+                p = n + step
+                a, b = caches[i], ref[i]
+                a.pos.fill_(p)
+                b.pos.fill_(p)
+                oa = a.update_attend(k[:, :, p:p + 1], v[:, :, p:p + 1], q, layer).clone()
+                args = b.step_args(k[:, :, p:p + 1], v[:, :, p:p + 1], q, layer)
+                _lib.call("nkv_decode_step_partials_t64", *args)
+                _lib.call("nkv_decode_step_combine_t64", *args)
+                assert torch.equal(oa, b.merged), (step, layer, i)
+                assert torch.equal(a.lse, b.lse), (step, layer, i)
+        for c in caches:
+            tail = c.pa.reshape(-1).view(torch.int32)[-64:]
+            assert int(tail.abs().sum()) == 0, step
+
+
 def test_streaming_decode_4096_steps_against_oracle():
     """One layer: prefill 512, then 4096 fused append+attend steps (q ~ N(0,1)/sqrt(128)).
     The cache state equals the oracle's bit for bit at the end; outputs are checked
