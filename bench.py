@@ -399,7 +399,7 @@ def main() -> int:
     cls = KVInt8TokCache if tok else KVInt8Cache
     cache = cls(num_slots=L, num_kv_heads=HKV, head_dim=D, max_len=max_len, num_q_heads=HQ, device=dev)
     if args.parts:
-        cache._n_parts = args.parts
+        cache.set_parts(args.parts)
     gen = torch.Generator(device=dev).manual_seed(2)
     cpu_gen = torch.Generator().manual_seed(3)
     cache.begin_prefill(ctx)

@@ -965,17 +965,17 @@ __device__ __forceinline__ int64_t prefix_limit(const AttnArgs& a, int64_t& pos,
 
 constexpr int TB_WAVES = 8;
 constexpr int TB_THREADS = 64 * TB_WAVES;
-constexpr int MERGE_CHUNK = 32;  // partial slots per column loaded up front
-constexpr int RING_PARTS = 4;    // the ring's 64 tokens as 4 partials of 16
-constexpr int WT_STRIDE = 256;  // partials one merge holds
+constexpr int RING_PARTS = 4;  // the ring's 64 tokens as 4 partials of 16
+constexpr int MERGE_PRE = 32;  // partials per column pair loaded up front
+constexpr int WTS = 256;       // weights one merging wave holds: up to 256 prefix partials
 static_assert(TB_WAVES == WAVES, "the prefix kernel's last workgroup runs the tail with its own waves");
 
 struct TailSmem {
   uint8_t ring_lds[2 * RING_BYTES];          // K | V values
   float ring_part[RING_PARTS][16 * D + 32];  // the ring's partials
+  float wts[TB_WAVES * WTS];                 // prefix merge weights, per merging wave
   float pre_acc[16 * D];                     // prefix: sum_s w_s acc_s per column
-  float pre_m[16], pre_l[16];                // prefix: max_s m_s, sum_s w_s l_s
-  float wbuf[TB_WAVES][WT_STRIDE];           // one head's w_s per wave
+  float pre_m[16], pre_l[16];                // per head: m_p, l_p
 };
 static_assert(sizeof(TailSmem) <= LDS_BYTES && sizeof(TailSmem) <= LDS_BYTES_TOK,
               "the tail's LDS fits in the prefix kernel's stages");
@@ -1007,10 +1007,12 @@ __device__ __forceinline__ uint16_t ld_u16(const uint16_t* p, bool co) {
 }
 
 // The tail of one decode step for KV head h (of sequence b when paged), by the 8 waves of the
-// calling workgroup: attends over the ring (or the group the token completed), merges the
-// prefix partials and the ring's partials by log-sum-exp and writes out / lse. Every phase is
-// spread over the waves (a wave's dependent instruction chain is what bounds it), and every
-// load it needs is issued at its start.
+// calling workgroup. The prefix partials merge into (m_p, l_p, acc_p): m_p = max_s m_s,
+// w_s = 2^(m_s - m_p), l_p = sum_s w_s l_s, acc_p = sum_s w_s acc_s (waves 4..7, one head
+// each, two columns per lane); meanwhile waves 0..3 attend over the ring, one partial of 16
+// tokens each; the ring's partials then join by log-sum-exp into out / lse. One round of
+// loads up front: the ring (or the completed group, or the new token), q, and each merging
+// wave's m / l and columns of the first MERGE_PRE partials.
 //
 // `inl`: run by the last prefix workgroup of the head inside the fused launch. The partials,
 // the codes of a completed group and a new per-token symmetric token were then written in
@@ -1035,19 +1037,18 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     U = prefix_limit(a, pos, pos_ok);
   }
   const bool ring = (PAGED || a.tail_mode != TAIL_NONE) && (!fused || pos_ok);
+  const bool ring_phase = ring;
+  const float* hws = PAGED ? a.ws + ((int64_t)h * a.total_parts + a.seq_parts[2 * b]) * pw : a.ws + (int64_t)h * P * pw;
   // while waves 0..3 attend over the ring, the others merge the prefix partials
-  const int mbase = ring ? RING_PARTS : 0, nmw = TB_WAVES - mbase;
-  const bool merger = wave >= mbase;
+  const int mbase = ring_phase ? RING_PARTS : 0, nmw = TB_WAVES - mbase;
 
-  // ---- every load up front: ring quarters (or the completed group), `first`, the mask, q;
-  // for a merging wave the m / l of its first head's partials (lane s) and its two columns
-  // (2 lane, 2 lane + 1) of the first MERGE_CHUNK partials
+  // ---- loads
   const int which = wave >> 2, qtr = wave & 3;
   const bool completes = fused && pos_ok && !a.tok && (pos + 1) % GT == 0;  // the token completed its group
-  const bool tok1 = !PAGED && ring && a.tok;  // per-token symmetric fused step: the tail is the new token
+  const bool tok1 = !PAGED && ring_phase && a.tok;  // per-token symmetric fused step: the tail is the new token
   const uint16_t* ring_h = PAGED ? a.rings + (((int64_t)b * a.hkv + h) * 2 + which) * GT * D : ring_of(a, h, which);
   RingQuarter rq;
-  if (ring && !completes && !tok1) {
+  if (ring_phase && !completes && !tok1) {
     ring_load_quarter(ring_h, PAGED ? GT : (int)a.tail_slots, qtr, rq);
     if (inl && !PAGED && a.tail_mode == TAIL_FUSED) {
       // the new token's slot: from the step's input, not the ring this launch writes
@@ -1067,7 +1068,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   }
   uint2 cw[4];
   uint4 cst, cmn;
-  if (completes) {
+  if (ring_phase && completes) {
     const int64_t gcur = pos / GT;
     const uint8_t* codes;
     const uint16_t *gst, *gmn;
@@ -1090,29 +1091,28 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     cmn = ld_u4(gmn + 8 * (lane & 15), co);
   }
   const int64_t first = (!PAGED && ring && a.first_dev) ? *a.first_dev : 0;
-  const bool mask_on = ring && a.tail_mode == TAIL_MASK && lane < a.tail_slots && a.tail_mask[lane] != 0;
+  const bool mask_on = ring_phase && a.tail_mode == TAIL_MASK && lane < a.tail_slots && a.tail_mask[lane] != 0;
   half8_t qb[4];
   const int64_t qh0 = (int64_t)b * a.hq + h * gq;  // first query head of this workgroup
-  if (ring && wave < RING_PARTS) load_q(a.q + qh0 * D, gq, qb);
-  const float* hws = PAGED ? a.ws + ((int64_t)h * a.total_parts + a.seq_parts[2 * b]) * pw : a.ws + (int64_t)h * P * pw;
+  if (ring_phase && wave < RING_PARTS) load_q(a.q + qh0 * D, gq, qb);
   const int head0 = wave - mbase;
-  float m0 = NEG_INF, l0 = 0.0f;
-  float2 v0[MERGE_CHUNK];
-  if (merger && head0 < gq) {
+  float mm = NEG_INF, ll = 0.0f;  // merging wave: lane s's m / l of its first head
+  float2 v0[MERGE_PRE];           // and its columns 2 lane, 2 lane + 1 of the first MERGE_PRE partials
+  if (head0 >= 0 && head0 < gq) {
     if (lane < P) {
-      m0 = ld_f(hws + (int64_t)lane * pw + gq * D + head0, inl);
-      l0 = ld_f(hws + (int64_t)lane * pw + gq * D + gq + head0, inl);
+      mm = ld_f(hws + (int64_t)lane * pw + gq * D + head0, inl);
+      ll = ld_f(hws + (int64_t)lane * pw + gq * D + gq + head0, inl);
     }
 #pragma unroll
-    for (int u = 0; u < MERGE_CHUNK; ++u)
+    for (int u = 0; u < MERGE_PRE; ++u)
       v0[u] = u < P ? ld_f2(hws + (int64_t)u * pw + head0 * D + 2 * lane, inl) : float2{0.f, 0.f};
   }
 
-  // ---- the ring into LDS. A token that completes its group is attended through the group's
-  // int8 values, dequantized as the prefix dequantizes them.
+  // ---- the ring, when not precomputed: into LDS (a token that completes its group through
+  // the group's int8 values, dequantized as the prefix dequantizes them)
   uint8_t* ring_k = sm.ring_lds;
   uint8_t* ring_v = sm.ring_lds + RING_BYTES;
-  if (ring) {
+  if (ring_phase) {
     if (completes) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) rq.rows[i] = __builtin_bit_cast(uint4, dq8(cw[i].x, cw[i].y, cst, cmn));
@@ -1128,7 +1128,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     }
     __syncthreads();
   }
-  if (!merger) {
+  if (wave < mbase) {
     // ---- ring attention: 4 waves x 16 tokens, one partial each
     const int64_t written = fused ? pos + 1 : (a.tail_mode == TAIL_SCALARS ? *a.written_dev : 0);
     uint64_t bits;
@@ -1141,39 +1141,36 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     attend_ring16(a, st, qb, ring_k, ring_v, wave, bits);
     store_wave_partial(st, gq, sm.ring_part[wave]);
   } else {
-    // ---- prefix merge, one head at a time: m_p = max_s m_s, w_s = 2^(m_s - m_p),
-    // l_p = sum_s w_s l_s, pre_acc = sum_s w_s acc_s (two columns per lane)
-    float* wb = sm.wbuf[wave];
+    // ---- prefix merge, one head at a time per merging wave (lane s (+ 64 k) = partial s for
+    // the weights, two columns per lane for the sum): m_p, w_s, l_p, pre_acc
+    float* wb = sm.wts + wave * WTS;
     for (int head = head0; head < gq; head += nmw) {
-      const bool first_head = head == head0;
-      float m = first_head ? m0 : NEG_INF;
-      for (int s = first_head ? lane + 64 : lane; s < P; s += 64) m = fmaxf(m, ld_f(hws + (int64_t)s * pw + gq * D + head, inl));
+      const bool own = head == head0;
+      float m = NEG_INF;
+      for (int s = lane; s < P; s += 64)
+        m = fmaxf(m, (own && s == lane) ? mm : ld_f(hws + (int64_t)s * pw + gq * D + head, inl));
       m = wave_max(m);
       float l = 0.0f;
       for (int s = lane; s < P; s += 64) {
-        const float ms = (first_head && s == lane) ? m0 : ld_f(hws + (int64_t)s * pw + gq * D + head, inl);
-        const float ls = (first_head && s == lane) ? l0 : ld_f(hws + (int64_t)s * pw + gq * D + gq + head, inl);
+        const float ms = (own && s == lane) ? mm : ld_f(hws + (int64_t)s * pw + gq * D + head, inl);
+        const float ls = (own && s == lane) ? ll : ld_f(hws + (int64_t)s * pw + gq * D + gq + head, inl);
         const float w = ms == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(ms - m);
         wb[s] = w;
         l += ls * w;
       }
       l = wave_sum(l);
       float2 acc = {0.0f, 0.0f};
-      if (first_head) {
+      int s0 = 0;
+      if (own) {
 #pragma unroll
-        for (int u = 0; u < MERGE_CHUNK; ++u) {
+        for (int u = 0; u < MERGE_PRE; ++u) {
           const float w = u < P ? wb[u] : 0.0f;
           acc.x += v0[u].x * w;
           acc.y += v0[u].y * w;
         }
-      } else {
-        for (int s = 0; s < min(P, MERGE_CHUNK); ++s) {
-          const float2 vv = ld_f2(hws + (int64_t)s * pw + head * D + 2 * lane, inl);
-          acc.x += vv.x * wb[s];
-          acc.y += vv.y * wb[s];
-        }
+        s0 = MERGE_PRE;
       }
-      for (int s = MERGE_CHUNK; s < P; ++s) {
+      for (int s = s0; s < P; ++s) {
         const float2 vv = ld_f2(hws + (int64_t)s * pw + head * D + 2 * lane, inl);
         acc.x += vv.x * wb[s];
         acc.y += vv.y * wb[s];
@@ -1184,26 +1181,34 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   }
   __syncthreads();
 
-  // ---- combine: prefix (m_p, l_p, pre_acc) and the ring's partials, one column per thread
+  // ---- combine: one column per thread. Prefix: acc_p = sum_s w_s acc_s; then with the
+  // ring's partials r: M = max(m_p, m_r), alpha = 2^(m_p - M), beta_r = 2^(m_r - M)
   for (int col = tid; col < cols; col += TB_THREADS) {
     const int head = col / D;
+    const float accp = sm.pre_acc[col];
     const float mp = sm.pre_m[head];
-    float M = mp;
-    if (ring) {
+    float M = mp, mr[RING_PARTS], lr[RING_PARTS], ar[RING_PARTS];
 #pragma unroll
-      for (int r = 0; r < RING_PARTS; ++r) M = fmaxf(M, sm.ring_part[r][gq * D + head]);
+    for (int r = 0; r < RING_PARTS; ++r) {
+      if (ring_phase) {
+        mr[r] = sm.ring_part[r][gq * D + head];
+        lr[r] = sm.ring_part[r][gq * D + gq + head];
+        ar[r] = sm.ring_part[r][col];
+      } else {
+        mr[r] = NEG_INF;
+        lr[r] = 0.0f;
+        ar[r] = 0.0f;
+      }
+      M = fmaxf(M, mr[r]);
     }
     const float Mu = M == NEG_INF ? 0.0f : M;
     const float alpha = mp == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mp - Mu);
-    float acc = alpha * sm.pre_acc[col], l = alpha * sm.pre_l[head];
-    if (ring) {
+    float acc = alpha * accp, l = alpha * sm.pre_l[head];
 #pragma unroll
-      for (int r = 0; r < RING_PARTS; ++r) {
-        const float mr = sm.ring_part[r][gq * D + head];
-        const float beta = mr == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mr - Mu);
-        acc += beta * sm.ring_part[r][col];
-        l += beta * sm.ring_part[r][gq * D + gq + head];
-      }
+    for (int r = 0; r < RING_PARTS; ++r) {
+      const float beta = mr[r] == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mr[r] - Mu);
+      acc += beta * ar[r];
+      l += beta * lr[r];
     }
     const int64_t qh = qh0 + head;
     const int d = col % D;
@@ -1219,7 +1224,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t unit_src[TOK || PAGED ? 8 : UNIT_SRC_BYTES / 2];
   __shared__ __attribute__((aligned(16))) uint16_t q_lds[16 * D];
   __shared__ __attribute__((aligned(16))) float xch[UNIT_CH * 2 * WAVES];
-  __shared__ int next_group;
+  __shared__ int ticket;
   float* lds = reinterpret_cast<float*>(lds_raw);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1257,14 +1262,12 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   const int64_t W = (U + GT - 1) / GT;
   const int64_t gs = prefix ? (int64_t)part * W / nparts : 0;
   const int64_t ge = prefix ? (int64_t)(part + 1) * W / nparts : 0;
-  // Groups gs + gi, gi < ng, are handed out to the waves one at a time: wave w starts with
-  // gi = w, and a wave claims the next one from `next_group` once the first half of its
-  // current group is done, so waves whose loads arrive early take more groups. A group's
+  // Groups gs + gi, gi < ng: wave w takes gi = w, w + WAVES, ... (a fixed assignment, so a
+  // partial's summation order, and the result, are the same on every run). A group's
   // halves (32 tokens) go to slots 0 and 1 (int8t64: its rulers to the wave's ruler set,
-  // alternating).
+  // alternating); the next group's halves are issued as each slot is freed.
   const int ng = (int)(ge - gs);
   const uint32_t rul_lds = my_lds + 2 * HALF_SLOT;
-  if (tid == 0) next_group = WAVES;
   // Q and the append unit's rows are loaded ahead of the groups, so that waiting for them
   // leaves the groups in flight
   if (wave == 0 && prefix)
@@ -1320,9 +1323,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_SECOND_HALF) : "memory");
         attend_block<1>(a, st, qb, my_stages, my_stages + HALF_CODE, rul, (int)min<int64_t>(32, U - grp * GT));
       }
-      int nx = 0;
-      if (lane == 0) nx = __hip_atomic_fetch_add(&next_group, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      nx = __builtin_amdgcn_readfirstlane(nx);
+      const int nx = gi + WAVES;
       // second half (slot 1)
       const int nv2 = (int)min<int64_t>(32, U - grp * GT - 32);
       if constexpr (TOK) {
@@ -1379,10 +1380,10 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   if (tid == 0) {
     const int t = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (t == last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    next_group = t;
+    ticket = t;
   }
   __syncthreads();
-  if (next_group == last) tail_body<PAGED>(a, h, b, *reinterpret_cast<TailSmem*>(lds_raw), true);
+  if (ticket == last) tail_body<PAGED>(a, h, b, *reinterpret_cast<TailSmem*>(lds_raw), true);
 }
 
 // ---------------------------------------------------------------- kernel B: ring + merge
@@ -1771,10 +1772,10 @@ static int launch_attn(AttnArgs& a, int64_t n_parts, int64_t workspace_bytes, hi
                        int launches = LAUNCH_PREFIX | LAUNCH_TAIL, bool fusable = false) {
   if (n_parts < 0) return fail(NKV_ERR_INVALID, "%s: n_parts %lld is negative", what, (long long)n_parts);
   a.n_parts = (int)n_parts;
-  const int64_t part_bytes = (int64_t)a.hkv * std::max<int64_t>(1, n_parts) * part_floats(a.hq, a.hkv) * (int64_t)sizeof(float);
   // both launches in one call: the prefix kernel's last workgroup per head runs the tail
   const bool fuse = fusable && n_parts > 0 && launches == (LAUNCH_PREFIX | LAUNCH_TAIL);
-  const int64_t need = part_bytes + ctr_bytes(a.hkv);  // the counters' bytes stay reserved in every mode
+  const int64_t part_bytes = (int64_t)a.hkv * std::max<int64_t>(1, n_parts) * part_floats(a.hq, a.hkv) * (int64_t)sizeof(float);
+  const int64_t need = part_bytes + (fuse ? ctr_bytes(a.hkv) : 0);
   if (n_parts > 0 && workspace_bytes < need)
     return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
   if (n_parts > 256) return fail(NKV_ERR_UNSUPPORTED, "%s: n_parts %lld exceeds the 256 partials the merge holds", what, (long long)n_parts);

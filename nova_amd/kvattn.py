@@ -49,11 +49,15 @@ def _is_capturing() -> bool:
         return False
 
 
-def _pick_parts(hkv: int, hq: int, groups: int, ws_bytes: int | None) -> int:
-    parts = int(_lib.load().nkv_attn_default_parts(hkv, groups))
+def _pick_parts(hkv: int, hq: int, groups: int, ws_bytes: int | None, fused: bool = False) -> int:
+    """Default prefix parts, capped by what ``ws_bytes`` holds: one partial per KV head per part,
+    plus, for the fused decode step, the completion counters."""
+    lib = _lib.load()
+    parts = int(lib.nkv_attn_default_parts(hkv, groups))
     if ws_bytes is not None:
-        per_part = int(_lib.load().nkv_attn_workspace_bytes(hkv, hq, 1))  # one partial per KV head
-        fit = ws_bytes // per_part
+        per_part = int(lib.nkv_attn_workspace_bytes(hkv, hq, 2)) - int(lib.nkv_attn_workspace_bytes(hkv, hq, 1))
+        extra = int(lib.nkv_attn_workspace_bytes(hkv, hq, 1)) - per_part if fused else 0
+        fit = (ws_bytes - extra) // per_part
         if fit < 1:
             raise ValueError(f"scratch too small: {ws_bytes} bytes")
         parts = max(1, min(parts, fit))
@@ -374,19 +378,24 @@ class KVInt8Cache:
         self._ninf = torch.full((), float("-inf"), dtype=dtype, device=device)
         self._mask = torch.zeros(self.group, dtype=torch.uint8, device=device)
 
-        # scratch: the reference's shapes; the kernel keeps its partials in `pa`'s memory
+        # scratch: the reference's shapes. The kernels keep their partials in the workspace
+        # `_ws`, whose first bytes `pa` views; `_ws` is zero-filled and serves this cache's
+        # decode launches only: the fused step keeps per-head completion counters in its
+        # last bytes (every launch leaves them at zero)
         self.n_splits = -(-self.max_len // self.chunk)
         sshape2 = (self.num_kv_heads, self.n_splits, PAD_M)
         self.pm = torch.zeros(sshape2, dtype=torch.float32, device=device)
         self.pl = torch.zeros_like(self.pm)
-        self.pa = torch.zeros((*sshape2, self.head_dim), dtype=torch.float32, device=device)
+        pa_numel = self.num_kv_heads * self.n_splits * PAD_M * self.head_dim
+        parts = int(_lib.load().nkv_attn_default_parts(self.num_kv_heads, n_groups))
+        need = int(_lib.load().nkv_attn_workspace_bytes(self.num_kv_heads, self.num_q_heads, parts))
+        self._ws = torch.zeros(max(pa_numel, -(-need // 4)), dtype=torch.float32, device=device)
+        self.pa = self._ws[:pa_numel].view(*sshape2, self.head_dim)
         self.out = torch.zeros((batch, self.num_q_heads, 1, self.head_dim), dtype=dtype, device=device)
         self.lse = torch.zeros((batch, self.num_q_heads), dtype=torch.float32, device=device)
         self.merged = torch.zeros((batch, self.num_q_heads, 1, self.head_dim), dtype=dtype, device=device)
-        self._n_parts = _pick_parts(self.num_kv_heads, self.num_q_heads, n_groups, self.pa.numel() * 4)
-        # zero-filled and used by this cache's decode launches only: the fused step keeps its
-        # per-head completion counters in the last bytes (every launch leaves them at zero)
-        self._ws_bytes = self.pa.numel() * 4
+        self._n_parts = _pick_parts(self.num_kv_heads, self.num_q_heads, n_groups, self._ws.numel() * 4, fused=True)
+        self._ws_bytes = self._ws.numel() * 4
 
         self.staging: Any = None
         self.stream_chunk = 0
@@ -663,7 +672,7 @@ class KVInt8Cache:
             self.vst[layer_idx].data_ptr(), self.num_q_heads, self.num_kv_heads, self.head_dim, self.max_len,
             0, 0, self._qlen.data_ptr(), self._pg.data_ptr(), self.tail_k[layer_idx].data_ptr(),
             self.tail_v[layer_idx].data_ptr(), self._written.data_ptr(), self.first.data_ptr(),
-            self.merged.data_ptr(), self.lse.data_ptr(), self.pa.data_ptr(), self._ws_bytes,
+            self.merged.data_ptr(), self.lse.data_ptr(), self._ws.data_ptr(), self._ws_bytes,
             self._n_parts, _lib.stream_ptr(self.pos.device))
         return self.merged
 
@@ -695,10 +704,21 @@ class KVInt8Cache:
                 self.tail_k[layer_idx].data_ptr(), self.tail_v[layer_idx].data_ptr(), self.pos.data_ptr(),
                 self.first.data_ptr(), self._written.data_ptr(), self._qlen.data_ptr(), self._pg.data_ptr(),
                 self.num_q_heads, self.num_kv_heads, self.head_dim, self.max_len, self.merged.data_ptr(),
-                self.lse.data_ptr(), self.pa.data_ptr(), self._ws_bytes, self._n_parts,
+                self.lse.data_ptr(), self._ws.data_ptr(), self._ws_bytes, self._n_parts,
                 _lib.stream_ptr(self.pos.device))
 
     # ---- memory accounting
+
+    def set_parts(self, n_parts: int) -> None:
+        """Prefix work units per KV head for the decode launches (before any capture); grows
+        the workspace when needed (zero-filled)."""
+        need = int(_lib.load().nkv_attn_workspace_bytes(self.num_kv_heads, self.num_q_heads, int(n_parts)))
+        if need > self._ws.numel() * 4:
+            pa_numel = self.pa.numel()
+            self._ws = torch.zeros(max(pa_numel, -(-need // 4)), dtype=torch.float32, device=self._ws.device)
+            self.pa = self._ws[:pa_numel].view(self.pa.shape)
+            self._ws_bytes = self._ws.numel() * 4
+        self._n_parts = int(n_parts)
 
     def nbytes(self) -> int:
         """Resident KV bytes: codes, rulers and ring (no scratch, no staging)."""

@@ -157,6 +157,15 @@ class KVInt8TokCache:
         self.lse = torch.zeros((1, self.num_q_heads), dtype=torch.float32, device=device)
         self.merged = torch.zeros((1, self.num_q_heads, 1, self.head_dim), dtype=dtype, device=device)
 
+    def set_parts(self, n_parts: int) -> None:
+        """Prefix work units per KV head for the decode launches (before any capture); grows
+        the zero-filled workspace when needed."""
+        need = int(_lib.load().nkv_attn_workspace_bytes(self.num_kv_heads, self.num_q_heads, int(n_parts)))
+        if need > self._ws_bytes:
+            self._ws_bytes = need
+            self.pa = torch.zeros(need // 4, dtype=torch.float32, device=self.pa.device)
+        self._n_parts = int(n_parts)
+
     def get_seq_length(self, layer_idx: int = 0) -> int:
         return int(self.pos.item())
 

@@ -340,7 +340,7 @@ def test_fused_tail_counters_return_to_zero_and_layers_interleave():
                 assert torch.equal(oa, b.merged), (step, layer, i)
                 assert torch.equal(a.lse, b.lse), (step, layer, i)
         for c in caches:
-            tail = c.pa.reshape(-1).view(torch.int32)[-64:]
+            tail = c._ws.view(torch.int32)[-64:]
             assert int(tail.abs().sum()) == 0, step
 
 
