@@ -94,6 +94,7 @@ def parse_args():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--ctx", type=int, default=CTX)
     ap.add_argument("--parts", type=int, default=0, help="work units per KV head (0 = library default)")
+    ap.add_argument("--splits", type=int, default=0, help="prefill: cache splits (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--workload", choices=("decode", "paged", "prefill"), default="decode",
@@ -255,8 +256,7 @@ def bench_prefill(args) -> int:
     kc = torch.randn(1, HKV, M, D, generator=g, device=dev).half()
     vc = torch.randn(1, HKV, M, D, generator=g, device=dev).half()
     out = torch.empty_like(q)
-    tiles = -(-(M * HQ // HKV) // 128)
-    splits = max(1, min(-(-256 // (HKV * tiles)), U // 64))
+    splits = args.splits or int(_lib.load().nkv_prefill_default_splits(HKV, HQ, M, U))
     scratch = torch.empty(int(_lib.load().nkv_prefill_workspace_bytes(HKV, HQ, M, splits)), dtype=torch.uint8, device=dev)
     int8_prefill_attend(q, kc, vc, *packed, used=U, out=out, scratch=scratch, splits=splits)
     torch.cuda.synchronize()

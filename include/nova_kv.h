@@ -326,11 +326,13 @@ int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const ui
  * int8t64: a chunk of m query tokens at positions used .. used + m - 1 attends causally to
  * the dequantized cache [0, used) and to its own fp16 K/V.
  * q [hq][m][128], k_chunk / v_chunk [hkv][m][128], out [hq][m][128], fp16.
- * Two launches: the chunk kernel (hkv * ceil(m * hq / hkv / 128) * splits workgroups on
+ * Two launches: the chunk kernel (hkv * ceil(m * hq / hkv / rows) * splits workgroups on
  * v_mfma_f32_16x16x32_f16, one partial per query row and split into `workspace`) and a
  * combine kernel. splits <= 0 picks one.
  */
 int64_t nkv_prefill_workspace_bytes(int64_t hkv, int64_t hq, int64_t m, int64_t splits);
+/* The splits value `splits <= 0` resolves to (enough workgroups to fill the GPU). */
+int64_t nkv_prefill_default_splits(int64_t hkv, int64_t hq, int64_t m, int64_t used);
 int nkv_prefill_attn_t64(const uint16_t* q, const uint16_t* k_chunk, const uint16_t* v_chunk, int64_t m,
                          const uint8_t* kq, const uint16_t* kmn, const uint16_t* kst, const uint8_t* vq,
                          const uint16_t* vmn, const uint16_t* vst, int64_t capacity, int64_t used,

@@ -66,6 +66,7 @@ SIGNATURES = {
     "nkv_paged_decode_step_t64": (c_int, [P, P, P, I64, I64, P, P, I64, P, P, I64, I64, I64, I64, P, P, I64, P, P,
                                           P, I64, P]),
     "nkv_prefill_workspace_bytes": (I64, [I64, I64, I64, I64]),
+    "nkv_prefill_default_splits": (I64, [I64, I64, I64, I64]),
     "nkv_prefill_attn_t64": (c_int, [P, P, P, I64, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, I64, I64, P]),
     "nkv_copy_bytes": (c_int, [P, P, I64, P]),
     "nkv_read_bw": (c_int, [P, I64, P, I64, P]),

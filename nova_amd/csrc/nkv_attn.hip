@@ -1463,6 +1463,7 @@ __global__ void ring_mask_kernel(const int64_t* written, const int64_t* qlen, co
 constexpr int PF_WAVES = 4;
 constexpr int PF_THREADS = 64 * PF_WAVES;
 constexpr int PF_RB = 2;                             // MFMA row blocks per wave
+constexpr int PF_WG_PER_CU = PF_RB <= 2 ? 2 : 1;     // workgroups resident per CU (registers)
 constexpr int PF_ROWS = PF_WAVES * PF_RB * 16;       // 128 query rows per workgroup
 constexpr int PF_KROW = D + 8;                       // fp16 K tile row stride (halves)
 constexpr int PF_VROW = GT + 8;                      // fp16 V^T tile row stride (halves, 16-byte rows)
@@ -1492,28 +1493,31 @@ struct PrefillArgs {
   uint16_t* out;   // [hq][M][D]
 };
 
-// Online softmax of one 16-row block over 64 tokens (s[b][i]: token 16b + 4g + i, row c),
-// returning P (scaled by 2^15) as two fp16 A operands (tokens of blocks 0,1 and 2,3).
-__device__ __forceinline__ void pf_softmax(WaveState& st, float (&s)[4][4], half8_t (&ph)[2]) {
+// Online softmax of one 16-row block over 64 tokens, from the raw scores S[b][i] (token
+// 16b + 4g + i, row c; -inf where masked): m is kept in the log2 domain (max S * sl2), and P
+// comes out as exp2(S sl2 - m + 15) = 2^15 p in two fp16 A operands (tokens of blocks 0,1 and
+// 2,3). l accumulates the same scaled weights, so acc / l needs no rescaling.
+__device__ __forceinline__ void pf_softmax(WaveState& st, const float (&S)[4][4], float sl2, half8_t (&ph)[2]) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
-  float mloc = NEG_INF;
+  float smax = NEG_INF;
 #pragma unroll
   for (int b = 0; b < 4; ++b)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mloc = fmaxf(mloc, s[b][i]);
-  mloc = max4rows(mloc);
-  const float m_new = fmaxf(st.m, mloc);
+    for (int i = 0; i < 4; ++i) smax = fmaxf(smax, S[b][i]);
+  smax = max4rows(smax);
+  const float m_new = fmaxf(st.m, smax * sl2);
   const float m_use = m_new == NEG_INF ? 0.0f : m_new;
   const float alpha = __builtin_amdgcn_exp2f(st.m - m_use);
+  const float off = 15.0f - m_use;
   float lsum = 0.0f;
   _Float16 p16[2][8];
 #pragma unroll
   for (int b = 0; b < 4; ++b)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float p = __builtin_amdgcn_exp2f(s[b][i] - m_use);
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(S[b][i], sl2, off));
       lsum += p;
-      p16[b >> 1][4 * (b & 1) + i] = (_Float16)(p * P_SCALE);
+      p16[b >> 1][4 * (b & 1) + i] = (_Float16)p;
     }
 #pragma unroll
   for (int B = 0; B < 2; ++B)
@@ -1530,7 +1534,7 @@ __device__ __forceinline__ void pf_softmax(WaveState& st, float (&s)[4][4], half
   }
 }
 
-__global__ __launch_bounds__(PF_THREADS, 2) void prefill_chunk_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t stage[2][2 * CODE_BYTES + RULER_BYTES];
   __shared__ __attribute__((aligned(16))) uint16_t ktile[GT * PF_KROW];
   __shared__ __attribute__((aligned(16))) uint16_t vtile[D * PF_VROW];
@@ -1609,11 +1613,11 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_chunk_kernel(PrefillArg
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int kt = mask_base + 16 * b + 4 * g + i;
-          sc[b][i] = (mask_base < 0 || kt <= tq) ? S[rb][b][i] * a.sl2 : NEG_INF;
+          sc[b][i] = (mask_base < 0 || kt <= tq) ? S[rb][b][i] : NEG_INF;
         }
       // rows of the S^T layout are q rows c; the causal test above needs the row of column
       // c, which is lane-independent of g: scores of lane (c, g) all belong to row c
-      pf_softmax(st[rb], sc, ph[rb]);
+      pf_softmax(st[rb], sc, a.sl2, ph[rb]);
     }
 #pragma unroll
     for (int B = 0; B < 2; ++B)
@@ -1694,7 +1698,7 @@ __global__ __launch_bounds__(PF_THREADS, 2) void prefill_chunk_kernel(PrefillArg
     attend_tiles(GT * j);
   }
 
-  // ---- one partial per row: acc[128] (x 2^15), m (log2 domain), l
+  // ---- one partial per row: acc[128] and l (both x 2^15), m (log2 domain)
   const int64_t total_rows = (int64_t)a.hkv * rows_h;
 #pragma unroll
   for (int rb = 0; rb < PF_RB; ++rb) {
@@ -1737,7 +1741,7 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
   }
   const int h = (int)(row / rows_h), r = (int)(row % rows_h);
   const int tk = r / a.gq, hd = h * a.gq + r % a.gq;
-  const float inv = l > 0.0f ? INV_P_SCALE / l : 0.0f;
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;  // acc and l carry the same 2^15 scale
   uint16_t* o = a.out + ((int64_t)hd * a.M + tk) * D + d4;
   *reinterpret_cast<uint2*>(o) = uint2{(uint32_t)f2h(acc.x * inv) | ((uint32_t)f2h(acc.y * inv) << 16),
                                        (uint32_t)f2h(acc.z * inv) | ((uint32_t)f2h(acc.w * inv) << 16)};
@@ -2169,6 +2173,14 @@ extern "C" int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_ne
 
 // ---------------------------------------------------------------- chunked prefill
 
+// Splits of the cache's groups: enough workgroups for every resident slot (256 CUs x
+// PF_WG_PER_CU), at least one group per split.
+extern "C" int64_t nkv_prefill_default_splits(int64_t hkv, int64_t hq, int64_t m, int64_t used) {
+  if (hkv <= 0 || hq <= 0 || m <= 0 || used < 0 || hq % hkv) return 0;
+  const int64_t tiles = cdiv(m * (hq / hkv), PF_ROWS);
+  return std::max<int64_t>(1, std::min<int64_t>(cdiv(256 * PF_WG_PER_CU, hkv * tiles), std::max<int64_t>(1, used / GT)));
+}
+
 extern "C" int64_t nkv_prefill_workspace_bytes(int64_t hkv, int64_t hq, int64_t m, int64_t splits) {
   if (hkv <= 0 || hq <= 0 || m <= 0 || splits <= 0 || hq % hkv) return 0;
   return splits * hq * m * PF_PART * (int64_t)sizeof(float);
@@ -2191,7 +2203,7 @@ extern "C" int nkv_prefill_attn_t64(const uint16_t* q, const uint16_t* k_chunk, 
       (used > 0 && (!al16(kq) || !al16(vq) || !al16(kmn) || !al16(kst) || !al16(vmn) || !al16(vst))))
     return fail(NKV_ERR_UNSUPPORTED, "prefill_attn: buffers must be 16-byte aligned");
   const int64_t gq = hq / hkv, rows_h = m * gq, tiles = cdiv(rows_h, PF_ROWS);
-  if (splits <= 0) splits = std::max<int64_t>(1, std::min<int64_t>(cdiv(256, hkv * tiles), std::max<int64_t>(1, used / GT)));
+  if (splits <= 0) splits = nkv_prefill_default_splits(hkv, hq, m, used);
   if (workspace_bytes < nkv_prefill_workspace_bytes(hkv, hq, m, splits))
     return fail(NKV_ERR_INVALID, "prefill_attn: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
                 (long long)nkv_prefill_workspace_bytes(hkv, hq, m, splits));

@@ -232,8 +232,7 @@ def int8_prefill_attend(query: torch.Tensor, key: torch.Tensor, value: torch.Ten
         out = torch.empty_like(query)
     lib = _lib.load()
     if splits <= 0:
-        tiles = -(-(n * hq // hkv) // 128)
-        splits = max(1, min(-(-256 // (hkv * tiles)), max(1, used // GROUP_T)))
+        splits = int(lib.nkv_prefill_default_splits(hkv, hq, n, used))
     need = int(lib.nkv_prefill_workspace_bytes(hkv, hq, n, splits))
     if scratch is None or scratch.numel() * scratch.element_size() < need:
         scratch = _lib.workspace(query.device, need)
