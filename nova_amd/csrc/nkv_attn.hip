@@ -67,6 +67,7 @@ constexpr int PAGE_BYTES = 2 * CODE_BYTES + RULER_BYTES;  // 17 KiB, a multiple 
 constexpr int DMA_FIRST_HALF_PAGED = 2 * (HALF_CODE / 1024) + 1;  // the rulers are one 1 KiB load
 enum Layout : int { CONTIG_T64 = 0, CONTIG_TOK = 1, PAGED_T64 = 2 };
 constexpr float P_SCALE = 32768.0f;       // 2^15
+constexpr float P_SCALE_LOG2 = 15.0f;
 constexpr float INV_P_SCALE = 1.0f / 32768.0f;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
@@ -343,11 +344,13 @@ __device__ __forceinline__ void wait_groups_all() { asm volatile("s_waitcnt vmcn
 
 // ---------------------------------------------------------------- one group's attention
 
-// Online-softmax update with the 16 masked scores s[b][i] (token 16b + 4g + i, head c);
-// returns P of token blocks (0,1) and (2,3) split into hi/lo fp16 A operands and
-// rescales the accumulator when a running maximum moved.
+// Online-softmax update from the raw scores S[b][i] (q.k, token 16b + 4g + i, head c; -inf
+// where masked), in the log2 domain: m = max S * sl2, p = 2^(S sl2 - m). P comes out scaled
+// by 2^15 (folded into the exponent) and split into hi/lo fp16 A operands of token blocks
+// (0,1) and (2,3); l accumulates the same scaled weights (out = acc / l). The accumulator is
+// rescaled when a running maximum moved.
 template <int NB>
-__device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[2 * NB][4], half8_t (&phi)[NB],
+__device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[2 * NB][4], float sl2, half8_t (&phi)[NB],
                                              half8_t (&plo)[NB], int gq) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
   float mloc = NEG_INF;
@@ -355,10 +358,11 @@ __device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[2 * NB][4
   for (int b = 0; b < 2 * NB; ++b)
 #pragma unroll
     for (int i = 0; i < 4; ++i) mloc = fmaxf(mloc, s[b][i]);
-  mloc = max4rows(mloc);
+  mloc = max4rows(mloc) * sl2;
   const float m_new = fmaxf(st.m, mloc);
   const float m_use = m_new == NEG_INF ? 0.0f : m_new;
   const float alpha = __builtin_amdgcn_exp2f(st.m - m_use);
+  const float off = P_SCALE_LOG2 - m_use;
   float lsum = 0.0f;
   _Float16 hi[NB][8], lo[NB][8];
 #pragma unroll
@@ -366,9 +370,8 @@ __device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[2 * NB][4
     float q[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float p = __builtin_amdgcn_exp2f(s[b][i] - m_use);
-      lsum += p;
-      q[i] = p * P_SCALE;
+      q[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[b][i], sl2, off));
+      lsum += q[i];
     }
 #pragma unroll
     for (int i = 0; i < 4; i += 2) {
@@ -448,10 +451,17 @@ __device__ __forceinline__ void attend_block(const AttnArgs& a, WaveState& st, c
 #pragma unroll
   for (int b = 0; b < 2 * NB; ++b)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s[b][i] = (16 * b + 4 * g + i) < nvalid ? S[b][i] * a.sl2 : NEG_INF;
+    for (int i = 0; i < 4; ++i) s[b][i] = S[b][i];
+  if (nvalid < 32 * NB) {
+#pragma unroll
+    for (int b = 0; b < 2 * NB; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (16 * b + 4 * g + i >= nvalid) s[b][i] = NEG_INF;
+  }
 
   half8_t phi[NB], plo[NB];
-  softmax_step<NB>(st, s, phi, plo, a.gq);
+  softmax_step<NB>(st, s, a.sl2, phi, plo, a.gq);
 
   // ---- O += P V. Lane (c, g) of a transpose read supplies row k(g, c >> 1) and half
   // (c & 1) of the 16-dim chunk; it receives dim 16cb + c of the 8 tokens k(g, 0..7),
@@ -470,24 +480,32 @@ __device__ __forceinline__ void attend_block(const AttnArgs& a, WaveState& st, c
     const int row = 16 * (2 * B + (r >> 2)) + 4 * g + (r & 3);
     const int key = swz(row);
     const uint8_t* rowp = vc + row * D + 8 * (c & 1);
-    // invalid tokens of a partial group get code 0 (finite value, weight 0)
-    u32x2 keep = {~0u, ~0u};
-    if (nvalid < 32 * NB) {
+    if (nvalid >= 32 * NB) {
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb) {
+        const u32x2 vw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                             (lds_v2i_t*)(const lds_void_t*)(rowp + ((cb ^ key) << 4))));
+        const half8_t vb = dq8_splat(vw.x, vw.y, vsp[cb], vmp[cb]);
+        st.acc[cb] = mfma32(phi[B], vb, st.acc[cb]);
+        st.acc[cb] = mfma32(plo[B], vb, st.acc[cb]);
+      }
+    } else {
+      // invalid tokens of a partial group get code 0 (finite value, weight 0)
       uint32_t m[2] = {0u, 0u};
 #pragma unroll
       for (int rr = 0; rr < 8; ++rr) {
         const int tok = 16 * (2 * B + (rr >> 2)) + 4 * g + (rr & 3);
         if (tok < nvalid) m[rr >> 2] |= 0xffu << (8 * (rr & 3));
       }
-      keep = u32x2{m[0], m[1]};
-    }
+      const u32x2 keep = u32x2{m[0], m[1]};
 #pragma unroll
-    for (int cb = 0; cb < 8; ++cb) {
-      const u32x2 vw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-                           (lds_v2i_t*)(const lds_void_t*)(rowp + ((cb ^ key) << 4)))) & keep;
-      const half8_t vb = dq8_splat(vw.x, vw.y, vsp[cb], vmp[cb]);
-      st.acc[cb] = mfma32(phi[B], vb, st.acc[cb]);
-      st.acc[cb] = mfma32(plo[B], vb, st.acc[cb]);
+      for (int cb = 0; cb < 8; ++cb) {
+        const u32x2 vw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                             (lds_v2i_t*)(const lds_void_t*)(rowp + ((cb ^ key) << 4)))) & keep;
+        const half8_t vb = dq8_splat(vw.x, vw.y, vsp[cb], vmp[cb]);
+        st.acc[cb] = mfma32(phi[B], vb, st.acc[cb]);
+        st.acc[cb] = mfma32(plo[B], vb, st.acc[cb]);
+      }
     }
   }
 }
@@ -536,9 +554,9 @@ __device__ __forceinline__ void attend_block_tok(const AttnArgs& a, WaveState& s
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s[b][i] = (16 * b + 4 * g + i) < nvalid ? S[b][i] * a.sl2 : NEG_INF;
+    for (int i = 0; i < 4; ++i) s[b][i] = (16 * b + 4 * g + i) < nvalid ? S[b][i] : NEG_INF;
   half8_t phi[1], plo[1];
-  softmax_step<1>(st, s, phi, plo, a.gq);
+  softmax_step<1>(st, s, a.sl2, phi, plo, a.gq);
 
   // ---- O += P V: lane (c, g) receives dim 16cb + c of tokens 4g + {0..3} and 16 + 4g +
   // {0..3}; their 8 scales are the same for every cb. Invalid tokens get code 0 and scale 0.
@@ -576,18 +594,19 @@ __device__ __forceinline__ void attend_block_tok(const AttnArgs& a, WaveState& s
 
 // Online-softmax update with the 4 masked scores s[i] (token 4g + i of a 16-token block,
 // head c); returns P as the A operand of v_mfma_f32_16x16x16_f16 (hi/lo halves).
-__device__ __forceinline__ void softmax_step4(WaveState& st, const float (&s)[4], half4_t& phi, half4_t& plo, int gq) {
+__device__ __forceinline__ void softmax_step4(WaveState& st, const float (&s)[4], float sl2, half4_t& phi,
+                                              half4_t& plo, int gq) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
-  const float mloc = max4rows(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+  const float mloc = max4rows(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]))) * sl2;
   const float m_new = fmaxf(st.m, mloc);
   const float m_use = m_new == NEG_INF ? 0.0f : m_new;
   const float alpha = __builtin_amdgcn_exp2f(st.m - m_use);
+  const float off = P_SCALE_LOG2 - m_use;
   float q[4], lsum = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float p = __builtin_amdgcn_exp2f(s[i] - m_use);
-    lsum += p;
-    q[i] = p * P_SCALE;
+    q[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sl2, off));
+    lsum += q[i];
   }
   const half2_t h01 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(q[0], q[1]));
   const half2_t h23 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(q[2], q[3]));
@@ -624,10 +643,10 @@ __device__ __forceinline__ void attend_ring16(const AttnArgs& a, WaveState& st, 
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int slot = 16 * blk + 4 * g + i;
-    sc[i] = ((valid_bits >> slot) & 1ull) ? S[i] * a.sl2 : NEG_INF;
+    sc[i] = ((valid_bits >> slot) & 1ull) ? S[i] : NEG_INF;
   }
   half4_t phi, plo;
-  softmax_step4(st, sc, phi, plo, a.gq);
+  softmax_step4(st, sc, a.sl2, phi, plo, a.gq);
   // V as the B operand: lane (c, g) holds tokens 16 blk + 4g + [0..3] of dim 16 cb + c
 #pragma unroll
   for (int cb = 0; cb < 8; ++cb) {
@@ -1212,8 +1231,9 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     }
     const int64_t qh = qh0 + head;
     const int d = col % D;
-    a.out[(int64_t)qh * D + d] = f2h(l > 0.0f ? acc * (INV_P_SCALE / l) : 0.0f);
-    if (a.lse && d == 0) a.lse[qh] = l > 0.0f ? (M + __log2f(l)) * LN2 : NEG_INF;
+    // acc and l carry the same 2^15 scale
+    a.out[(int64_t)qh * D + d] = f2h(l > 0.0f ? acc / l : 0.0f);
+    if (a.lse && d == 0) a.lse[qh] = l > 0.0f ? (M + __log2f(l) - P_SCALE_LOG2) * LN2 : NEG_INF;
   }
 }
 
