@@ -97,7 +97,8 @@ def parse_args():
     ap.add_argument("--splits", type=int, default=0, help="prefill: cache splits (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=("decode", "paged", "prefill"), default="decode",
+    ap.add_argument("--chunk", type=int, default=2048, help="e2e: streamed prefill chunk (a multiple of 64)")
+    ap.add_argument("--workload", choices=("decode", "paged", "prefill", "e2e"), default="decode",
                     help="decode: one 32k sequence (the headline); paged: 8 ragged sequences in a paged cache; "
                          "prefill: a 512-token chunk over a 16384-token int8 cache (MFMA)")
     ap.add_argument("--scheme", choices=("t64", "tok"), default="t64",
@@ -294,6 +295,216 @@ def bench_prefill(args) -> int:
     return 0
 
 
+VOCAB_QWEN3_4B = 151936
+
+
+def cpu_baseline_e2e(budget_s: float, layer_shapes: list, lm_shape: tuple) -> dict:
+    """The decode step of the random-weight decoder on the host: one layer's projections as
+    fp32 torch matrix-vector products (all host threads) plus the numpy oracle's attention for
+    one layer at 32k context, scaled to 36 layers, plus the lm_head product."""
+    import torch
+
+    att = cpu_baseline(budget_s * 0.6, "t64")
+    per_layer_attn = att["seconds_per_step"] / LAYERS
+    g = torch.Generator().manual_seed(0)
+    ws = [torch.randn(*shp, generator=g) for shp in layer_shapes]
+    lm = torch.randn(*lm_shape, generator=g)
+
+    def run(mats):
+        for w in mats:
+            torch.mv(w, torch.ones(w.shape[1]))
+
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        run(ws)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s * 0.3 or reps >= 50:
+            break
+    per_layer_mv = el / reps
+    t1 = time.perf_counter()
+    run([lm])
+    lm_s = time.perf_counter() - t1
+    per_step = LAYERS * (per_layer_mv + per_layer_attn) + lm_s
+    return {"value": 1.0 / per_step, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"one layer's projections as fp32 torch.mv ({reps} reps, {torch.get_num_threads()} threads) "
+                      f"+ {att['sample']} + the lm_head product once; scaled to {LAYERS} layers (extrapolated)"}
+
+
+def bench_e2e(args) -> int:
+    """End-to-end graph decode of the random-weight decoder with Qwen3-4B geometry (36 layers,
+    hidden 2560, 32 q / 8 KV heads of 128, SwiGLU 9728, vocab 151936, fp16 weights ~ N(0, 1/fan_in))
+    over the int8t64 KV cache: the prompt (seeded random ids, ``--ctx`` tokens) is prefilled in
+    streamed chunks, then each decode step (embed, 36 x [qkv GEMV + RMSNorm, q/k norm + RoPE,
+    fused int8 append + attention, o_proj + residual, SwiGLU gate/up + RMSNorm, down + residual],
+    final RMSNorm + lm_head, argmax, pos += 1) is one hipGraph replay. Each kernel is also timed
+    alone (a graph of its 36 launches per step with the same weights); ``roofline`` is the one
+    that takes the most time per step."""
+    import torch
+
+    from nova_amd import _lib
+    from nova_amd import gemv as G
+    from nova_amd.decode import GraphDecoder
+    from nova_amd.skeleton import SkeletonConfig, SkeletonForCausalLM
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    L, ctx, W = args.layers, args.ctx, args.warmup
+    K = args.steps
+    cfg = SkeletonConfig(num_hidden_layers=L, vocab_size=VOCAB_QWEN3_4B)
+    model = SkeletonForCausalLM(cfg, seed=5, device=dev, dtype=torch.float16).eval()
+    model.use_decode_kernels(True)
+    max_len = -(-(ctx + 4 + W + K + 1) // 64) * 64
+    dec = GraphDecoder(model, max_len=max_len, quant="int8", device=dev)
+    if args.parts:
+        dec.cache.set_parts(args.parts)
+    ids = torch.randint(0, cfg.vocab_size, (1, ctx), generator=torch.Generator().manual_seed(6)).to(dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dec.prefill(ids, chunk=args.chunk)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    dec.capture(warmup=3)
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(W):
+        dec.step()
+    torch.cuda.synchronize()
+    pos0 = int(dec.cache.pos.item())
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    e0.record(stream)
+    for _ in range(K):
+        dec.step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    ms = e0.elapsed_time(e1)
+    assert int(dec.cache.pos.item()) == pos0 + K
+    assert torch.isfinite(dec.logits).all()
+
+    # ---- algorithmic bytes of one step: every weight once, the attention's KV bytes, the append
+    layers = model.model.layers
+    lay0 = layers[0]
+    hid, inter = cfg.hidden_size, cfg.intermediate_size
+    w_layer = sum(t.numel() * 2 for t in (lay0.w_qkv, lay0.attn.o_proj.weight, lay0.w_gate_up,
+                                          lay0.mlp.down_proj.weight, lay0.norm, lay0.post_norm,
+                                          lay0.attn.q_norm, lay0.attn.k_norm))
+    w_head = model.lm_head.weight.numel() * 2 + hid * 2 + hid * 2  # lm_head, final norm, embedding row
+    us = [pos0 + i + 1 for i in range(K)]
+    kv_step = sum(attn_bytes(u) + APPEND_BYTES for u in us) / K * L
+    step_bytes = L * w_layer + w_head + kv_step
+
+    # ---- each kernel alone: a graph of its launches for one step, K replays
+    gen = torch.Generator(device=dev).manual_seed(7)
+    xh = torch.randn(hid, generator=gen, device=dev).half()
+    xa = torch.randn(cfg.num_attention_heads * cfg.head_dim, generator=gen, device=dev).half()
+    xi = torch.randn(inter, generator=gen, device=dev).half()
+    res = torch.randn(hid, generator=gen, device=dev).half()
+    o_h = torch.empty(hid, dtype=torch.float16, device=dev)
+    o_qkv = torch.empty(lay0.w_qkv.shape[0], dtype=torch.float16, device=dev)
+    o_i = torch.empty(inter, dtype=torch.float16, device=dev)
+    o_v = torch.empty(cfg.vocab_size, dtype=torch.float16, device=dev)
+    qkv = torch.randn(lay0.w_qkv.shape[0], generator=gen, device=dev).half()
+    pos = dec.cache.pos
+    inv = model.model.inv_freq32
+    hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+
+    def graph_of(fn, reps=1):
+        with torch.cuda.stream(stream):
+            fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        return g
+
+    def time_graph(g) -> float:
+        for _ in range(W):
+            g.replay()
+        torch.cuda.synchronize()
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record(stream)
+        for _ in range(K):
+            g.replay()
+        s1.record(stream)
+        torch.cuda.synchronize()
+        return s0.elapsed_time(s1)
+
+    kv_in = torch.randn(2, 1, hkv, 1, d, generator=gen, device=dev).half()
+    q_in = (torch.randn(1, hq, 1, d, generator=gen, device=dev) / d ** 0.5).half()
+    kernels = {
+        "nkv_gemv qkv+RMSNorm": (lambda: [G.rms_gemv(xh, ly.w_qkv, ly.norm, cfg.rms_eps, out=o_qkv) for ly in layers],
+                                 lay0.w_qkv.numel() * 2, L),
+        "nkv_qk_norm_rope": (lambda: [G.qk_norm_rope_(qkv, hq, hkv, ly.attn.q_norm, ly.attn.k_norm, cfg.rms_eps, inv, pos)
+                                      for ly in layers], (hq + hkv) * d * 4, L),
+        "nkv_decode_step_t64": (lambda: [dec.cache.update_attend(kv_in[0], kv_in[1], q_in, i) for i in range(L)],
+                                sum(attn_bytes(u) + APPEND_BYTES for u in us) / K, L),
+        "nkv_gemv o_proj+residual": (lambda: [G.rms_gemv(xa, ly.attn.o_proj.weight, residual=res, out=o_h)
+                                              for ly in layers], ly_bytes(lay0.attn.o_proj.weight), L),
+        "nkv_swiglu_gemv gate/up+RMSNorm": (lambda: [G.swiglu_gemv(xh, ly.w_gate_up, ly.post_norm, cfg.rms_eps, out=o_i)
+                                                     for ly in layers], ly_bytes(lay0.w_gate_up), L),
+        "nkv_gemv down+residual": (lambda: [G.rms_gemv(xi, ly.mlp.down_proj.weight, residual=res, out=o_h)
+                                            for ly in layers], ly_bytes(lay0.mlp.down_proj.weight), L),
+        "nkv_gemv lm_head+RMSNorm": (lambda: G.rms_gemv(xh, model.lm_head.weight, model.model.norm, cfg.rms_eps,
+                                                        out=o_v), ly_bytes(model.lm_head.weight), 1),
+    }
+    saved = dec._save_int8_state()
+    breakdown = {}
+    for name, (fn, nbytes, launches) in kernels.items():
+        with torch.inference_mode():  # the decoder's state tensors are inference tensors
+            g = graph_of(fn)
+            t = time_graph(g) / K  # ms per step
+        del g
+        per_launch = t / launches / 1e3
+        breakdown[name] = {"launches_per_step": launches, "ms_per_step": round(t, 4),
+                           "avg_launch_us": round(per_launch * 1e6, 3),
+                           "algorithmic_bytes_per_launch": round(nbytes),
+                           "gbs": round(nbytes / per_launch / 1e9, 1)}
+    dec._restore_int8_state(saved)
+    top = max(breakdown, key=lambda n: breakdown[n]["ms_per_step"])
+    tb = breakdown[top]
+
+    ms_step = ms / K
+    out = {
+        "metric": "end-to-end graph-decode tokens/s, 36-layer Qwen3-4B-geometry decoder (random weights) "
+                  "over the int8 KV cache at 32k ctx",
+        "value": round(K / (ms / 1e3), 2), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16", "data": "synthetic (random weights, random prompt ids)",
+        "config": {"workload": f"greedy decode, {L} layers x (hidden {hid}, 32 q / 8 kv heads x 128, SwiGLU {inter}), "
+                               f"vocab {cfg.vocab_size}, batch 1, int8t64 KV cache, {ctx}-token prompt prefilled in "
+                               f"{args.chunk}-token streamed chunks, {K} hipGraph-replayed steps",
+                   "layers": L, "context": ctx, "hidden": hid, "intermediate": inter, "vocab": cfg.vocab_size,
+                   "prefill_chunk": args.chunk, "parts_per_head": dec.cache._n_parts},
+        "algorithmic_bytes_per_step": round(step_bytes),
+        "step_gbs": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
+        "step_pct_of_hbm_peak": round(100 * step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS, 2),
+        "prefill_s": round(prefill_s, 3),
+        "prefill_tokens_per_s": round(ctx / prefill_s, 1),
+        "wall_s_timed": round(wall, 4),
+        "roofline": {"bound": "hbm", "achieved": tb["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(tb["gbs"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": top,
+                     "algorithmic_bytes_per_launch": tb["algorithmic_bytes_per_launch"],
+                     "avg_launch_us": tb["avg_launch_us"]},
+        "kernels": breakdown,
+        "kernels_sum_ms_per_step": round(sum(b["ms_per_step"] for b in breakdown.values()), 4),
+    }
+    if not args.no_cpu_baseline:
+        shapes = [tuple(t.shape) for t in (lay0.w_qkv, lay0.attn.o_proj.weight, lay0.w_gate_up,
+                                           lay0.mlp.down_proj.weight)]
+        out["cpu_baseline"] = cpu_baseline_e2e(args.cpu_seconds, shapes, tuple(model.lm_head.weight.shape))
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def ly_bytes(w) -> int:
+    return w.numel() * 2
+
+
 def bench_paged(args) -> int:
     """Batched ragged decode: 8 sequences with seeded uniform lengths in [1024, 16384]
     (seed 3), 36 layers, int8t64 pages of 64 tokens; one step = every layer's
@@ -376,6 +587,8 @@ def main() -> int:
         return bench_paged(args)
     if args.workload == "prefill" and args.gpus == 1:
         return bench_prefill(args)
+    if args.workload == "e2e" and args.gpus == 1:
+        return bench_e2e(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported on this path "
               "(the decode attention shards by KV head across GPUs; see the design notes)", file=sys.stderr)

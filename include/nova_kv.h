@@ -355,6 +355,40 @@ int nkv_copy_bytes(const void* src, void* dst, int64_t nbytes, void* stream);
  */
 int nkv_read_bw(const void* src, int64_t nbytes, uint32_t* sink, int64_t blocks, void* stream);
 
+/* ---------------------------------------------------------------- decode-step projections
+ *
+ * Batch-1 fp16 kernels of the synthetic decoder that drives the int8 KV path end to end.
+ * They replace torch ops of the decoder layer (RMSNorm + nn.Linear in src/nova/norm.py:35-41
+ * and src/nova/layers.py:99-162,165-195), not a kernel of the reference; they exist so that a
+ * captured decode step is a few launches per layer. All vectors are contiguous fp16; weights
+ * are row-major [out][in], 16-byte aligned; in_features a multiple of 8, at most 16384.
+ */
+
+/*
+ * y[o] = fp16(sum_i W[o][i] * xn[i]) (+ residual[o], added in fp16), xn = x when gamma is
+ * NULL, else RMSNorm(x) = fp16(fp16(x * rsqrt(mean(x^2) + eps)) * gamma) with an fp32 mean.
+ * Dot products accumulate in fp32. `residual` may be NULL; y may alias residual, not x.
+ */
+int nkv_gemv(const uint16_t* x, const uint16_t* gamma, float eps, const uint16_t* w, int64_t out_features,
+             int64_t in_features, const uint16_t* residual, uint16_t* y, void* stream);
+
+/*
+ * The SwiGLU MLP's first half: act[j] = fp16(silu(g_j)) * u_j, g = W[0:inter] xn and
+ * u = W[inter:2 inter] xn (each rounded to fp16), W the stacked [gate; up] weight of
+ * [2 * intermediate][in_features], xn as in nkv_gemv (LeanMLP, src/nova/layers.py:173-174).
+ */
+int nkv_swiglu_gemv(const uint16_t* x, const uint16_t* gamma, float eps, const uint16_t* w_gate_up,
+                    int64_t intermediate, int64_t in_features, uint16_t* act, void* stream);
+
+/*
+ * In place on one token's stacked projection qkv [hq + 2 hkv][128] (q heads, k heads, v heads):
+ * per-head RMSNorm of the q and k heads (q_gamma / k_gamma, fp32 mean of squares), then the
+ * rotary embedding at position *pos (device int64): x * cos + rotate_half(x) * sin with
+ * cos/sin = fp16(cos/sin((float)pos * inv_freq[i mod 64])), fp32 inv_freq[64]. v is untouched.
+ */
+int nkv_qk_norm_rope(uint16_t* qkv, int64_t hq, int64_t hkv, int64_t head_dim, const uint16_t* q_gamma,
+                     const uint16_t* k_gamma, float eps, const float* inv_freq, const int64_t* pos, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,6 +70,9 @@ SIGNATURES = {
     "nkv_prefill_attn_t64": (c_int, [P, P, P, I64, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, I64, I64, P]),
     "nkv_copy_bytes": (c_int, [P, P, I64, P]),
     "nkv_read_bw": (c_int, [P, I64, P, I64, P]),
+    "nkv_gemv": (c_int, [P, P, c_float, P, I64, I64, P, P, P]),
+    "nkv_swiglu_gemv": (c_int, [P, P, c_float, P, I64, I64, P, P]),
+    "nkv_qk_norm_rope": (c_int, [P, I64, I64, I64, P, P, c_float, P, P, P]),
 }
 
 ABI_VERSION = 3

@@ -23,7 +23,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libnova_kv.so"
-SOURCES = ("nkv_quant.hip", "nkv_attn.hip")
+SOURCES = ("nkv_quant.hip", "nkv_attn.hip", "nkv_gemv.hip")
 ARCH = "gfx950"
 
 COMMON_FLAGS = [

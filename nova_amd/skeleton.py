@@ -1,12 +1,22 @@
-"""Synthetic attention-only decoder with Qwen3-4B attention geometry and random weights.
+"""Synthetic decoder with Qwen3-4B geometry and random weights, the caller of the int8 KV path.
 
-It stands in for ``NovaForCausalLM`` (src/nova/model.py:183-215) as the caller of the
-int8 KV path, reproducing the caller contract of ``LeanAttention.forward``
-(src/nova/layers.py:99-162): q/k/v projection, RoPE, then either the int8 cache
-(``update`` + ``attend`` / ``attend_prefill``, or the fused ``update_attend`` for one
-decode token) or the fp16 cache (``update`` + SDPA with the additive mask). Its
-projections, norms and lm_head are plain torch ops — they sit outside the path.
-No checkpoint is loaded: weights are seeded random tensors.
+It stands in for ``NovaForCausalLM`` (src/nova/model.py:183-215) and reproduces the caller
+contract of ``LeanAttention.forward`` (src/nova/layers.py:99-162): q/k/v projection, q/k head
+norms, RoPE, then either the int8 cache (``update`` + ``attend`` / ``attend_prefill``, or the
+fused ``update_attend`` for one decode token) or the fp16 cache (``update`` + SDPA with the
+additive mask). Each layer is ``LeanDecoderLayer`` (layers.py:177-195): pre-norm attention and,
+when ``intermediate_size > 0``, the SwiGLU MLP ``LeanMLP`` (layers.py:165-174), each added to
+the residual stream. No checkpoint is loaded: weights are seeded random tensors.
+
+Two ways to run a layer:
+
+- torch (default): projections, norms and lm_head are plain torch ops around the KV path;
+- ``use_decode_kernels()``: a one-token decode step (batch 1, int8 cache) runs each layer as
+  five launches of this package's HIP kernels around the fused int8 decode step — qkv GEMV
+  with the input RMSNorm, q/k head norms + RoPE, ``update_attend``, o_proj GEMV with the
+  residual add, gate/up GEMV with SwiGLU and the post-attention RMSNorm, down GEMV with the
+  residual add — and the final RMSNorm is fused into the lm_head GEMV. The same fp16 roundings
+  as the torch path, up to fp32 summation order.
 """
 
 from __future__ import annotations
@@ -25,6 +35,7 @@ class SkeletonConfig:
     num_key_value_heads: int = 8
     head_dim: int = 128
     hidden_size: int = 2560
+    intermediate_size: int = 9728  # 0: attention-only layers
     vocab_size: int = 2048
     rope_theta: float = 1_000_000.0
     rms_eps: float = 1e-6
@@ -53,18 +64,18 @@ def repeat_kv(x: torch.Tensor, n_rep: int) -> torch.Tensor:
 
 
 class SkeletonAttention(nn.Module):
-    def __init__(self, cfg: SkeletonConfig, layer_idx: int):
+    def __init__(self, cfg: SkeletonConfig, layer_idx: int, **factory):
         super().__init__()
         self.cfg = cfg
         self.layer_idx = layer_idx
         self.head_dim = cfg.head_dim
         self.scaling = cfg.head_dim ** -0.5
-        self.q_proj = nn.Linear(cfg.hidden_size, cfg.num_attention_heads * cfg.head_dim, bias=False)
-        self.k_proj = nn.Linear(cfg.hidden_size, cfg.num_key_value_heads * cfg.head_dim, bias=False)
-        self.v_proj = nn.Linear(cfg.hidden_size, cfg.num_key_value_heads * cfg.head_dim, bias=False)
-        self.o_proj = nn.Linear(cfg.num_attention_heads * cfg.head_dim, cfg.hidden_size, bias=False)
-        self.q_norm = nn.Parameter(torch.ones(cfg.head_dim))
-        self.k_norm = nn.Parameter(torch.ones(cfg.head_dim))
+        self.q_proj = nn.Linear(cfg.hidden_size, cfg.num_attention_heads * cfg.head_dim, bias=False, **factory)
+        self.k_proj = nn.Linear(cfg.hidden_size, cfg.num_key_value_heads * cfg.head_dim, bias=False, **factory)
+        self.v_proj = nn.Linear(cfg.hidden_size, cfg.num_key_value_heads * cfg.head_dim, bias=False, **factory)
+        self.o_proj = nn.Linear(cfg.num_attention_heads * cfg.head_dim, cfg.hidden_size, bias=False, **factory)
+        self.q_norm = nn.Parameter(torch.ones(cfg.head_dim, **factory))
+        self.k_norm = nn.Parameter(torch.ones(cfg.head_dim, **factory))
 
     def forward(self, hidden: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                 attention_mask: torch.Tensor | None, cache) -> torch.Tensor:
@@ -94,26 +105,88 @@ class SkeletonAttention(nn.Module):
         return self.o_proj(out.transpose(1, 2).reshape(b, n, -1).contiguous())
 
 
-class SkeletonLayer(nn.Module):
-    def __init__(self, cfg: SkeletonConfig, layer_idx: int):
+class SkeletonMLP(nn.Module):
+    """``down(silu(gate(x)) * up(x))`` (``LeanMLP``, src/nova/layers.py:165-174)."""
+
+    def __init__(self, cfg: SkeletonConfig, **factory):
         super().__init__()
-        self.norm = nn.Parameter(torch.ones(cfg.hidden_size))
-        self.attn = SkeletonAttention(cfg, layer_idx)
+        self.gate_proj = nn.Linear(cfg.hidden_size, cfg.intermediate_size, bias=False, **factory)
+        self.up_proj = nn.Linear(cfg.hidden_size, cfg.intermediate_size, bias=False, **factory)
+        self.down_proj = nn.Linear(cfg.intermediate_size, cfg.hidden_size, bias=False, **factory)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+def _stack_linears(*lins: nn.Linear) -> torch.Tensor:
+    """One ``[sum(out), in]`` weight holding the given layers' weights, which become views of it."""
+    w = torch.cat([lin.weight.detach() for lin in lins]).contiguous()
+    o = 0
+    for lin in lins:
+        n = lin.weight.shape[0]
+        lin.weight.data = w[o:o + n]
+        o += n
+    return w
+
+
+class SkeletonLayer(nn.Module):
+    def __init__(self, cfg: SkeletonConfig, layer_idx: int, **factory):
+        super().__init__()
+        self.norm = nn.Parameter(torch.ones(cfg.hidden_size, **factory))
+        self.attn = SkeletonAttention(cfg, layer_idx, **factory)
         self.eps = cfg.rms_eps
+        self.mlp = SkeletonMLP(cfg, **factory) if cfg.intermediate_size else None
+        self.post_norm = nn.Parameter(torch.ones(cfg.hidden_size, **factory)) if self.mlp is not None else None
+        self.w_qkv: torch.Tensor | None = None
+        self.w_gate_up: torch.Tensor | None = None
 
     def forward(self, h, cos, sin, mask, cache):
-        return h + self.attn(_rms(h, self.norm, self.eps), cos, sin, mask, cache)
+        h = h + self.attn(_rms(h, self.norm, self.eps), cos, sin, mask, cache)
+        if self.mlp is not None:
+            h = h + self.mlp(_rms(h, self.post_norm, self.eps))
+        return h
+
+    def stack_weights(self) -> None:
+        """Stack q/k/v and gate/up into single weights (the Linear weights become views)."""
+        if self.w_qkv is None:
+            a = self.attn
+            self.w_qkv = _stack_linears(a.q_proj, a.k_proj, a.v_proj)
+            if self.mlp is not None:
+                self.w_gate_up = _stack_linears(self.mlp.gate_proj, self.mlp.up_proj)
+
+    def decode_kernels(self, h: torch.Tensor, cache, pos: torch.Tensor, inv_freq: torch.Tensor) -> torch.Tensor:
+        """One decode token (``h`` of ``hidden_size`` elements) through the layer on the HIP
+        kernels; returns the new residual stream (a new tensor)."""
+        from . import gemv as G
+
+        cfg, a = self.attn.cfg, self.attn
+        hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        x = h.reshape(-1)
+        qkv = G.rms_gemv(x, self.w_qkv, self.norm, self.eps)
+        G.qk_norm_rope_(qkv, hq, hkv, a.q_norm, a.k_norm, cfg.rms_eps, inv_freq, pos)
+        q = qkv[:hq * d].view(1, hq, 1, d)
+        k = qkv[hq * d:(hq + hkv) * d].view(1, hkv, 1, d)
+        v = qkv[(hq + hkv) * d:].view(1, hkv, 1, d)
+        o = cache.update_attend(k, v, q, a.layer_idx)
+        h1 = G.rms_gemv(o.reshape(-1), a.o_proj.weight, residual=x)
+        if self.mlp is not None:
+            act = G.swiglu_gemv(h1, self.w_gate_up, self.post_norm, self.eps)
+            G.rms_gemv(act, self.mlp.down_proj.weight, residual=h1, out=h1)
+        return h1.view(h.shape)
 
 
 class SkeletonText(nn.Module):
-    def __init__(self, cfg: SkeletonConfig):
+    def __init__(self, cfg: SkeletonConfig, **factory):
         super().__init__()
         self.cfg = cfg
-        self.embed_tokens = nn.Embedding(cfg.vocab_size, cfg.hidden_size)
-        self.layers = nn.ModuleList([SkeletonLayer(cfg, i) for i in range(cfg.num_hidden_layers)])
-        self.norm = nn.Parameter(torch.ones(cfg.hidden_size))
+        self.embed_tokens = nn.Embedding(cfg.vocab_size, cfg.hidden_size, **factory)
+        self.layers = nn.ModuleList([SkeletonLayer(cfg, i, **factory) for i in range(cfg.num_hidden_layers)])
+        self.norm = nn.Parameter(torch.ones(cfg.hidden_size, **factory))
         inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2, dtype=torch.float32) / cfg.head_dim))
-        self.register_buffer("inv_freq", inv, persistent=False)
+        self.register_buffer("inv_freq", inv.to(factory.get("device")), persistent=False)
+        # kernel mode: one-token steps over an int8 cache run on the HIP kernels, and the final
+        # RMSNorm moves into the lm_head (``forward`` then returns the pre-norm hidden states)
+        self.decode_kernels = False
 
     @property
     def num_cache_layers(self) -> int:
@@ -130,30 +203,73 @@ class SkeletonText(nn.Module):
             position_ids = past_key_values.pos.view(1, 1) + torch.arange(n, device=input_ids.device).view(1, n)
         elif position_ids.dim() == 3:  # [3, B, n] multimodal positions: the text axis
             position_ids = position_ids[0]
+        if self.decode_kernels:
+            if (b == 1 and n == 1 and hasattr(past_key_values, "update_attend")
+                    and not getattr(past_key_values, "prefilling", False)):
+                h = self.embed_tokens(input_ids)
+                pos = position_ids.reshape(-1)[:1]
+                for layer in self.layers:
+                    h = layer.decode_kernels(h, past_key_values, pos, self.inv_freq32)
+                return h
+            return self._layers_torch(input_ids, position_ids, attention_mask, past_key_values)
+        return _rms(self._layers_torch(input_ids, position_ids, attention_mask, past_key_values), self.norm,
+                    self.cfg.rms_eps)
+
+    def _layers_torch(self, input_ids, position_ids, attention_mask, past_key_values):
         freqs = position_ids.float()[..., None] * self.inv_freq  # [B, n, D/2]
         emb = torch.cat((freqs, freqs), dim=-1)[:, None]  # [B, 1, n, D]
         h = self.embed_tokens(input_ids)
         cos, sin = emb.cos().to(h.dtype), emb.sin().to(h.dtype)
         for layer in self.layers:
             h = layer(h, cos, sin, attention_mask, past_key_values)
-        return _rms(h, self.norm, self.cfg.rms_eps)
+        return h
 
 
 class SkeletonForCausalLM(nn.Module):
-    def __init__(self, cfg: SkeletonConfig | None = None, seed: int = 0):
+    """Random-weight decoder: weights ~ N(0, 1) / sqrt(fan_in), norms 1.
+
+    With ``device`` unset it is built in fp32 on the CPU from ``torch.Generator().manual_seed(seed)``
+    (move it with ``.half().cuda()``); with ``device`` (and ``dtype``) it is built there
+    directly, from a generator of that device, which a 4B-parameter geometry needs."""
+
+    def __init__(self, cfg: SkeletonConfig | None = None, seed: int = 0, device=None, dtype: torch.dtype | None = None):
         super().__init__()
         cfg = cfg or SkeletonConfig()
         self.config = cfg
-        g = torch.Generator().manual_seed(seed)
-        self.model = SkeletonText(cfg)
-        self.lm_head = nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False)
+        factory = {} if device is None else {"device": torch.device(device), "dtype": dtype or torch.float16}
+        self.model = SkeletonText(cfg, **factory)
+        self.lm_head = nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False, **factory)
+        g = torch.Generator(device=factory.get("device", "cpu")).manual_seed(seed)
         with torch.no_grad():
             for p in self.parameters():
                 if p.dim() >= 2:
-                    p.copy_(torch.randn(p.shape, generator=g) * (p.shape[-1] ** -0.5))
+                    r = torch.randn(p.shape, generator=g, device=p.device, dtype=torch.float32)
+                    p.copy_(r.mul_(p.shape[-1] ** -0.5))
+                    del r
+
+    def use_decode_kernels(self, on: bool = True) -> "SkeletonForCausalLM":
+        """Run one-token decode steps on the HIP kernels (fp16 CUDA model, int8 cache)."""
+        if on:
+            w = self.lm_head.weight
+            if not w.is_cuda or w.dtype != torch.float16:
+                raise ValueError("use_decode_kernels() needs the model in fp16 on the GPU")
+            for layer in self.model.layers:
+                layer.stack_weights()
+            # the RoPE frequencies as the torch path promotes them (fp16 after ``.half()``)
+            self.model.inv_freq32 = self.model.inv_freq.float().contiguous()
+        self.model.decode_kernels = bool(on)
+        return self
 
     def lm_head_forward(self, hidden: torch.Tensor) -> torch.Tensor:
-        return self.lm_head(hidden)
+        if not self.model.decode_kernels:
+            return self.lm_head(hidden)
+        # kernel mode: ``hidden`` is pre-norm; the final RMSNorm is part of the lm_head
+        if hidden.shape[:-1].numel() == 1:
+            from . import gemv as G
+
+            logits = G.rms_gemv(hidden.reshape(-1), self.lm_head.weight, self.model.norm, self.config.rms_eps)
+            return logits.view(*hidden.shape[:-1], -1)
+        return self.lm_head(_rms(hidden, self.model.norm, self.config.rms_eps))
 
     def forward(self, input_ids, past_key_values=None, attention_mask=None, window_mask=None,
                 cross_mode: str = "off", logits_to_keep: int = 0, position_ids=None):

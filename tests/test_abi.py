@@ -93,6 +93,17 @@ def test_validation_errors_return_before_launch(lib):
     assert b"head_dim" in lib.nkv_last_error()
     assert lib.nkv_copy_bytes(None, None, 15, None) == _lib.NKV_ERR_INVALID
     assert lib.nkv_ring_mask(None, None, None, 64, None, None) == _lib.NKV_ERR_INVALID
+    # decode-step projections: sizes and layouts are checked before anything is launched
+    # (the non-null pointers below are never dereferenced)
+    fake = 1 << 20
+    assert lib.nkv_gemv(None, None, 1e-6, None, 4, 64, None, None, None) == _lib.NKV_ERR_INVALID
+    assert lib.nkv_gemv(fake, None, 1e-6, fake, 4, 100, None, fake, None) == _lib.NKV_ERR_INVALID
+    assert b"multiple of 8" in lib.nkv_last_error()
+    assert lib.nkv_gemv(fake, None, 1e-6, fake, 4, 16392, None, fake, None) == _lib.NKV_ERR_INVALID
+    assert lib.nkv_gemv(fake + 2, None, 1e-6, fake, 4, 64, None, fake, None) == _lib.NKV_ERR_UNSUPPORTED
+    assert lib.nkv_swiglu_gemv(fake, None, 1e-6, fake, 0, 64, fake, None) == _lib.NKV_ERR_INVALID
+    assert lib.nkv_qk_norm_rope(fake, 32, 8, 64, fake, fake, 1e-6, fake, fake, None) == _lib.NKV_ERR_UNSUPPORTED
+    assert b"head_dim" in lib.nkv_last_error()
 
 
 def test_product_path_refuses_to_run_without_gpu():

@@ -17,7 +17,7 @@ MAX_LEN = 256
 def model():
     from nova_amd.skeleton import SkeletonConfig, SkeletonForCausalLM
 
-    cfg = SkeletonConfig(num_hidden_layers=4, hidden_size=1024, vocab_size=1024)
+    cfg = SkeletonConfig(num_hidden_layers=4, hidden_size=1024, vocab_size=1024, intermediate_size=0)
     return SkeletonForCausalLM(cfg, seed=0).half().cuda().eval()
 
 

@@ -125,7 +125,7 @@ def test_graph_decoder_streamed_prefill():
     from nova_amd.decode import GraphDecoder
     from nova_amd.skeleton import SkeletonConfig, SkeletonForCausalLM
 
-    cfg = SkeletonConfig(num_hidden_layers=3, hidden_size=1024, vocab_size=1024)
+    cfg = SkeletonConfig(num_hidden_layers=3, hidden_size=1024, vocab_size=1024, intermediate_size=0)
     model = SkeletonForCausalLM(cfg, seed=0).half().cuda().eval()
     g = torch.Generator().manual_seed(5)
     ids = torch.randint(0, 1024, (1, 333), generator=g).cuda()
