@@ -361,7 +361,7 @@ int nkv_read_bw(const void* src, int64_t nbytes, uint32_t* sink, int64_t blocks,
  * They replace torch ops of the decoder layer (RMSNorm + nn.Linear in src/nova/norm.py:35-41
  * and src/nova/layers.py:99-162,165-195), not a kernel of the reference; they exist so that a
  * captured decode step is a few launches per layer. All vectors are contiguous fp16; weights
- * are row-major [out][in], 16-byte aligned; in_features a multiple of 8, at most 16384.
+ * are row-major [out][in]; x, gamma and W 16-byte aligned; in_features a multiple of 8, at most 16384.
  */
 
 /*

@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "nkv_common.h"
 
@@ -19,7 +20,7 @@ namespace nkv {
 namespace {
 
 constexpr int GV_MAX_IN = 16384;  // input features (the LDS copy takes 2 bytes each)
-constexpr int GV_UNROLL = 4;      // 16-byte chunks per lane per row in one load batch
+constexpr int GV_WAVES = 8;       // rows (waves) per workgroup
 
 __device__ __forceinline__ float hsum64(float v) {
 #pragma unroll
@@ -38,140 +39,159 @@ __device__ __forceinline__ float dot8(uint4 w, uint4 x, float acc) {
 __device__ __forceinline__ _Float16 as_half(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ uint16_t half_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 
-// The input into LDS as fp16: x itself, or its RMSNorm in the order torch evaluates
-// fp16(fp16(x * rsqrt(mean(x^2) + eps)) * gamma), with the mean in fp32.
-template <int W>
-__device__ __forceinline__ void load_input(const uint16_t* x, const uint16_t* gamma, float eps, int n, uint16_t* xs) {
-  __shared__ float part[W];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float r = 1.0f;
-  if (gamma) {
-    float ss = 0.0f;
-    for (int i = tid; i < n; i += 64 * W) {
-      const float v = (float)as_half(x[i]);
-      ss += v * v;
-    }
-    ss = hsum64(ss);
-    if (lane == 0) part[wave] = ss;
-    __syncthreads();
-    float tot = 0.0f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) tot += part[w];
-    r = rsqrtf(tot * (1.0f / (float)n) + eps);  // torch: mean = sum * (1/n), then rsqrt
-  }
-  for (int i = tid; i < n; i += 64 * W) {
-    _Float16 v = as_half(x[i]);
-    if (gamma) v = (_Float16)((float)(_Float16)((float)v * r) * (float)as_half(gamma[i]));
-    xs[i] = half_bits(v);
-  }
-  __syncthreads();
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// A weight load: 16 bytes, nontemporal (weights stream through once per decode step).
+__device__ __forceinline__ uint4 ld_weight(const uint16_t* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return uint4{v.x, v.y, v.z, v.w};
 }
 
-// One load batch: chunks c0 + 64 u (u < GV_UNROLL) of each of the NR rows (row j at rp[j],
-// absent when !rv[j]); chunks past the row end read as zero.
-template <int NR>
-__device__ __forceinline__ void load_batch(const uint16_t* const (&rp)[NR], const bool (&rv)[NR], int c0, int nch,
-                                           uint4 (&wv)[NR][GV_UNROLL]) {
+// The workgroup's share of the input vector: thread t holds 16-byte chunks t + 64 W k of x (and
+// of gamma when NORM), k < XC, so that XC 64 W >= 64 NL >= the input's chunk count.
+template <int NL, int W, bool NORM>
+struct InputChunks {
+  static constexpr int XC = (NL + W - 1) / W;
+  uint4 x[XC];
+  uint4 g[NORM ? XC : 1];
+
+  __device__ __forceinline__ void issue(const uint16_t* xp, const uint16_t* gp, int nch) {
+#pragma unroll
+    for (int k = 0; k < XC; ++k) {
+      const int c = (int)threadIdx.x + 64 * W * k;
+      x[k] = c < nch ? *reinterpret_cast<const uint4*>(xp + 8 * c) : uint4{0, 0, 0, 0};
+      if (NORM) g[k] = c < nch ? *reinterpret_cast<const uint4*>(gp + 8 * c) : uint4{0, 0, 0, 0};
+    }
+  }
+
+  // The input into LDS as fp16: x itself, or its RMSNorm in the order torch evaluates
+  // fp16(fp16(x * rsqrt(mean(x^2) + eps)) * gamma), with the mean in fp32.
+  __device__ __forceinline__ void stage(float eps, int n, int nch, uint16_t* xs) {
+    __shared__ float part[W];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float r = 1.0f;
+    if (NORM) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int k = 0; k < XC; ++k) {
+        const uint32_t u[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const half2_t h = as_h2(u[e]);
+          ss += (float)h.x * (float)h.x;
+          ss += (float)h.y * (float)h.y;
+        }
+      }
+      ss = hsum64(ss);
+      if (lane == 0) part[wave] = ss;
+      __syncthreads();
+      float tot = 0.0f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) tot += part[w];
+      r = rsqrtf(tot * (1.0f / (float)n) + eps);  // torch: mean = sum * (1/n), then rsqrt
+    }
+#pragma unroll
+    for (int k = 0; k < XC; ++k) {
+      const int c = tid + 64 * W * k;
+      if (c < nch) {
+        uint4 v = x[k];
+        if (NORM) {
+          uint32_t u[4] = {v.x, v.y, v.z, v.w};
+          const uint32_t gu[4] = {g[k].x, g[k].y, g[k].z, g[k].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const half2_t h = as_h2(u[e]), gg = as_h2(gu[e]);
+            half2_t o;
+            o.x = (_Float16)((float)(_Float16)((float)h.x * r) * (float)gg.x);
+            o.y = (_Float16)((float)(_Float16)((float)h.y * r) * (float)gg.y);
+            u[e] = as_u32(o);
+          }
+          v = uint4{u[0], u[1], u[2], u[3]};
+        }
+        *reinterpret_cast<uint4*>(xs + 8 * c) = v;
+      }
+    }
+    __syncthreads();
+  }
+};
+
+// acc[j] = row j . xn for the NR rows rp[] (absent when !rv[j]), each row of nch 16-byte
+// chunks: lane l holds chunks l + 64 u (u < NL; NL * 64 >= nch), so that a wave load covers
+// 1 KiB of a row. The input chunks are loaded first, then every weight load of the wave's
+// rows; the input is normalized into LDS while the weights are in flight (the in-order load
+// counter lets the input arrive without waiting for the weights), and a wave waits for HBM once.
+// Wave sums land in every lane.
+template <int NL, int NR, int W, bool NORM>
+__device__ __forceinline__ void rows_dot(InputChunks<NL, W, NORM>& ic, const uint16_t* const (&rp)[NR],
+                                         const bool (&rv)[NR], int in, float eps, uint16_t* xs, float (&acc)[NR]) {
+  const int lane = threadIdx.x & 63, nch = in / 8;
+  uint4 wv[NR][NL];
 #pragma unroll
   for (int j = 0; j < NR; ++j)
 #pragma unroll
-    for (int u = 0; u < GV_UNROLL; ++u) {
-      const int c = c0 + 64 * u;
-      wv[j][u] = (rv[j] && c < nch) ? *reinterpret_cast<const uint4*>(rp[j] + 8 * c) : uint4{0, 0, 0, 0};
+    for (int u = 0; u < NL; ++u) {
+      const int c = lane + 64 * u;
+      wv[j][u] = (rv[j] && c < nch) ? ld_weight(rp[j] + 8 * c) : uint4{0, 0, 0, 0};
     }
-}
-
-template <int NR>
-__device__ __forceinline__ void dot_batch(const uint4 (&wv)[NR][GV_UNROLL], const uint16_t* xs, int c0, int nch,
-                                          float (&acc)[NR]) {
+  ic.stage(eps, in, nch, xs);
 #pragma unroll
-  for (int u = 0; u < GV_UNROLL; ++u) {
-    const int c = c0 + 64 * u;
+  for (int j = 0; j < NR; ++j) acc[j] = 0.0f;
+#pragma unroll
+  for (int u = 0; u < NL; ++u) {
+    const int c = lane + 64 * u;
     if (c < nch) {
       const uint4 xv = *reinterpret_cast<const uint4*>(xs + 8 * c);
 #pragma unroll
       for (int j = 0; j < NR; ++j) acc[j] = dot8(wv[j][u], xv, acc[j]);
     }
   }
-}
-
-// acc[j] = row j . xn for the NR rows rp[], the input normalized into LDS between the first
-// load batch and its products; wave sums land in every lane.
-template <int NR, int W>
-__device__ __forceinline__ void rows_dot(const uint16_t* const (&rp)[NR], const bool (&rv)[NR], int in,
-                                         const uint16_t* x, const uint16_t* gamma, float eps, uint16_t* xs,
-                                         float (&acc)[NR]) {
-  const int lane = threadIdx.x & 63, nch = in / 8;
-  uint4 wv[NR][GV_UNROLL];
-  load_batch<NR>(rp, rv, lane, nch, wv);
-  load_input<W>(x, gamma, eps, in, xs);
-#pragma unroll
-  for (int j = 0; j < NR; ++j) acc[j] = 0.0f;
-  for (int c0 = lane;;) {
-    dot_batch<NR>(wv, xs, c0, nch, acc);
-    c0 += 64 * GV_UNROLL;
-    if (c0 >= nch) break;
-    load_batch<NR>(rp, rv, c0, nch, wv);
-  }
 #pragma unroll
   for (int j = 0; j < NR; ++j) acc[j] = hsum64(acc[j]);
 }
 
-// y = W xn (+ residual) in fp16: wave w of workgroup b takes rows (b W + w) R ... + R - 1.
-template <int R, int W>
+// y = W xn (+ residual) in fp16, one row per wave: wave w of workgroup b takes row b W + w.
+template <int NL, int W, bool NORM>
 __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint16_t* x, const uint16_t* gamma, float eps,
                                                       const uint16_t* w, int64_t out, int in,
                                                       const uint16_t* residual, uint16_t* y) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t o0 = ((int64_t)blockIdx.x * W + wave) * R;
-  const uint16_t* rp[R];
-  bool rv[R];
-#pragma unroll
-  for (int j = 0; j < R; ++j) {
-    rv[j] = o0 + j < out;
-    rp[j] = w + (rv[j] ? o0 + j : 0) * (int64_t)in;
-  }
-  float acc[R];
-  rows_dot<R, W>(rp, rv, in, x, gamma, eps, xs, acc);
-  if (lane == 0) {
-#pragma unroll
-    for (int j = 0; j < R; ++j) {
-      if (!rv[j]) break;
-      _Float16 r = (_Float16)acc[j];  // the projection's fp16 result, then the residual add in fp16
-      if (residual) r = (_Float16)((float)r + (float)as_half(residual[o0 + j]));
-      y[o0 + j] = half_bits(r);
-    }
+  const int64_t o = (int64_t)blockIdx.x * W + wave;
+  const bool rv[1] = {o < out};
+  InputChunks<NL, W, NORM> ic;
+  ic.issue(x, gamma, in / 8);
+  const uint16_t res = (residual && rv[0]) ? residual[o] : (uint16_t)0;  // before the weights, too
+  const uint16_t* const rp[1] = {w + (rv[0] ? o : 0) * (int64_t)in};
+  float acc[1];
+  rows_dot<NL, 1, W, NORM>(ic, rp, rv, in, eps, xs, acc);
+  if (lane == 0 && rv[0]) {
+    _Float16 r = (_Float16)acc[0];  // the projection's fp16 result, then the residual add in fp16
+    if (residual) r = (_Float16)((float)r + (float)as_half(res));
+    y[o] = half_bits(r);
   }
 }
 
 // act[j] = fp16(silu(g_j)) * u_j with g = rows [0, inter) and u = rows [inter, 2 inter) of the
 // stacked gate/up weight, as torch evaluates F.silu(gate(x)) * up(x) in fp16. Each wave takes
-// R gate rows and the R matching up rows.
-template <int R, int W>
+// one gate row and the matching up row.
+template <int NL, int W, bool NORM>
 __global__ __launch_bounds__(64 * W) void swiglu_kernel(const uint16_t* x, const uint16_t* gamma, float eps,
                                                         const uint16_t* wgu, int64_t inter, int in, uint16_t* act) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t j0 = ((int64_t)blockIdx.x * W + wave) * R;
-  const uint16_t* rp[2 * R];
-  bool rv[2 * R];
-#pragma unroll
-  for (int j = 0; j < R; ++j) {
-    rv[j] = rv[R + j] = j0 + j < inter;
-    rp[j] = wgu + (rv[j] ? j0 + j : 0) * (int64_t)in;
-    rp[R + j] = rp[j] + inter * (int64_t)in;
-  }
-  float acc[2 * R];
-  rows_dot<2 * R, W>(rp, rv, in, x, gamma, eps, xs, acc);
-  if (lane == 0) {
-#pragma unroll
-    for (int j = 0; j < R; ++j) {
-      if (!rv[j]) break;
-      const float g = (float)(_Float16)acc[j], u = (float)(_Float16)acc[R + j];
-      const _Float16 s = (_Float16)(g / (1.0f + expf(-g)));
-      act[j0 + j] = half_bits((_Float16)((float)s * u));
-    }
+  const int64_t j = (int64_t)blockIdx.x * W + wave;
+  const bool ok = j < inter;
+  const bool rv[2] = {ok, ok};
+  InputChunks<NL, W, NORM> ic;
+  ic.issue(x, gamma, in / 8);
+  const uint16_t* g_row = wgu + (ok ? j : 0) * (int64_t)in;
+  const uint16_t* const rp[2] = {g_row, g_row + inter * (int64_t)in};
+  float acc[2];
+  rows_dot<NL, 2, W, NORM>(ic, rp, rv, in, eps, xs, acc);
+  if (lane == 0 && ok) {
+    const float g = (float)(_Float16)acc[0], u = (float)(_Float16)acc[1];
+    const _Float16 s = (_Float16)(g / (1.0f + expf(-g)));
+    act[j] = half_bits((_Float16)((float)s * u));
   }
 }
 
@@ -183,6 +203,8 @@ __global__ __launch_bounds__(64 * W) void swiglu_kernel(const uint16_t* x, const
 __global__ __launch_bounds__(64) void qk_norm_rope_kernel(uint16_t* qkv, int hq, const uint16_t* q_gamma,
                                                           const uint16_t* k_gamma, float eps, const float* inv_freq,
                                                           const int64_t* pos) {
+  // torch rounds each product to fp16 before the sum: no fusing into an fp16 fma here
+#pragma clang fp contract(off)
   const int head = blockIdx.x, l = threadIdx.x;
   uint16_t* p = qkv + (int64_t)head * 128;
   const uint16_t* g = head < hq ? q_gamma : k_gamma;
@@ -210,12 +232,77 @@ int check(const char* what, const void* x, const void* w, const void* y, int64_t
   return NKV_OK;
 }
 
-template <int R, int W>
+template <int N>
+using nl_t = std::integral_constant<int, N>;
+
+// Calls f(nl_t<NL>{}) for the smallest supported NL with 64 NL >= nch (16-byte chunks per
+// row), so that a lane holds its chunks of a row in NL registers of 16 bytes.
+template <class F>
+void with_nl(int nch, F&& f) {
+  const int nl = (nch + 63) / 64;
+  if (nl <= 1) f(nl_t<1>{});
+  else if (nl <= 2) f(nl_t<2>{});
+  else if (nl <= 3) f(nl_t<3>{});
+  else if (nl <= 4) f(nl_t<4>{});
+  else if (nl <= 5) f(nl_t<5>{});
+  else if (nl <= 6) f(nl_t<6>{});
+  else if (nl <= 8) f(nl_t<8>{});
+  else if (nl <= 10) f(nl_t<10>{});
+  else if (nl <= 12) f(nl_t<12>{});
+  else if (nl <= 16) f(nl_t<16>{});
+  else if (nl <= 20) f(nl_t<20>{});
+  else if (nl <= 24) f(nl_t<24>{});
+  else f(nl_t<32>{});  // GV_MAX_IN / 8 / 64 = 32
+}
+
+template <int W>
+void launch_gemv_w(const uint16_t* x, const uint16_t* gamma, float eps, const uint16_t* w, int64_t out, int in,
+                   const uint16_t* residual, uint16_t* y, hipStream_t s) {
+  const unsigned blocks = (unsigned)((out + W - 1) / W);
+  with_nl(in / 8, [&](auto nl) {
+    constexpr int NL = decltype(nl)::value;
+    if (gamma)
+      hipLaunchKernelGGL((gemv_kernel<NL, W, true>), dim3(blocks), dim3(64 * W), (size_t)in * 2, s, x, gamma, eps, w,
+                         out, in, residual, y);
+    else
+      hipLaunchKernelGGL((gemv_kernel<NL, W, false>), dim3(blocks), dim3(64 * W), (size_t)in * 2, s, x, gamma, eps, w,
+                         out, in, residual, y);
+  });
+}
+
+template <int W>
+void launch_swiglu_w(const uint16_t* x, const uint16_t* gamma, float eps, const uint16_t* wgu, int64_t inter, int in,
+                     uint16_t* act, hipStream_t s) {
+  const unsigned blocks = (unsigned)((inter + W - 1) / W);
+  with_nl(in / 8, [&](auto nl) {
+    constexpr int NL = decltype(nl)::value;
+    if (gamma)
+      hipLaunchKernelGGL((swiglu_kernel<NL, W, true>), dim3(blocks), dim3(64 * W), (size_t)in * 2, s, x, gamma, eps,
+                         wgu, inter, in, act);
+    else
+      hipLaunchKernelGGL((swiglu_kernel<NL, W, false>), dim3(blocks), dim3(64 * W), (size_t)in * 2, s, x, gamma, eps,
+                         wgu, inter, in, act);
+  });
+}
+
+// Eight rows (waves) per workgroup, so the input is read and normalized once per eight rows;
+// four for outputs under 4096 rows, which keeps 2560 rows at 640 workgroups (2.5 per CU).
 void launch_gemv(const uint16_t* x, const uint16_t* gamma, float eps, const uint16_t* w, int64_t out, int in,
                  const uint16_t* residual, uint16_t* y, hipStream_t s) {
-  const unsigned blocks = (unsigned)((out + R * W - 1) / (R * W));
-  hipLaunchKernelGGL((gemv_kernel<R, W>), dim3(blocks), dim3(64 * W), (size_t)in * 2, s, x, gamma, eps, w, out, in,
-                     residual, y);
+  if (out < 4096)
+    launch_gemv_w<4>(x, gamma, eps, w, out, in, residual, y, s);
+  else
+    launch_gemv_w<GV_WAVES>(x, gamma, eps, w, out, in, residual, y, s);
+}
+
+// (two rows per wave: beyond 16 chunks per lane and row, four waves per workgroup leave each
+// wave the registers for both rows' loads)
+void launch_swiglu(const uint16_t* x, const uint16_t* gamma, float eps, const uint16_t* wgu, int64_t inter, int in,
+                   uint16_t* act, hipStream_t s) {
+  if (in / 8 > 16 * 64)
+    launch_swiglu_w<4>(x, gamma, eps, wgu, inter, in, act, s);
+  else
+    launch_swiglu_w<GV_WAVES>(x, gamma, eps, wgu, inter, in, act, s);
 }
 
 }  // namespace
@@ -228,14 +315,8 @@ extern "C" int nkv_gemv(const uint16_t* x, const uint16_t* gamma, float eps, con
                         int64_t in_features, const uint16_t* residual, uint16_t* y, void* stream) {
   set_error("");
   if (int rc = check("gemv", x, w, y, out_features, in_features)) return rc;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int in = (int)in_features;
-  // large outputs (the lm_head): 4 rows per wave; otherwise one row per wave and two waves
-  // per workgroup, so that a 2560-row projection is 1280 workgroups, 5 per CU
-  if (out_features >= 16384)
-    launch_gemv<4, 4>(x, gamma, eps, w, out_features, in, residual, y, s);
-  else
-    launch_gemv<1, 2>(x, gamma, eps, w, out_features, in, residual, y, s);
+  if (gamma && !al16(gamma)) return fail(NKV_ERR_UNSUPPORTED, "gemv: gamma must be 16-byte aligned");
+  launch_gemv(x, gamma, eps, w, out_features, (int)in_features, residual, y, static_cast<hipStream_t>(stream));
   return check_launch("gemv");
 }
 
@@ -243,11 +324,8 @@ extern "C" int nkv_swiglu_gemv(const uint16_t* x, const uint16_t* gamma, float e
                                int64_t intermediate, int64_t in_features, uint16_t* act, void* stream) {
   set_error("");
   if (int rc = check("swiglu_gemv", x, w_gate_up, act, intermediate, in_features)) return rc;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  constexpr int R = 1, W = 2;
-  const unsigned blocks = (unsigned)((intermediate + R * W - 1) / (R * W));
-  hipLaunchKernelGGL((swiglu_kernel<R, W>), dim3(blocks), dim3(64 * W), (size_t)in_features * 2, s, x, gamma, eps,
-                     w_gate_up, intermediate, (int)in_features, act);
+  if (gamma && !al16(gamma)) return fail(NKV_ERR_UNSUPPORTED, "swiglu_gemv: gamma must be 16-byte aligned");
+  launch_swiglu(x, gamma, eps, w_gate_up, intermediate, (int)in_features, act, static_cast<hipStream_t>(stream));
   return check_launch("swiglu_gemv");
 }
 
