@@ -1046,22 +1046,13 @@ __device__ __forceinline__ uint16_t ld_u16(const uint16_t* p, bool co) {
 // loads; the ring slot of the new token is taken from k_new / v_new (this launch's append
 // writes it concurrently), every other slot was written by earlier launches.
 template <bool PAGED>
-__device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailSmem& sm, bool inl) {
+__device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailSmem& sm, bool inl, int64_t pos,
+                                          bool pos_ok, int64_t U) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int gq = a.gq, pw = part_stride(gq), cols = gq * D;
   const int P = PAGED ? a.seq_parts[2 * b + 1] : a.n_parts;
   const bool fused = PAGED || a.tail_mode == TAIL_FUSED;
 
-  int64_t pos;
-  bool pos_ok;
-  int64_t U;
-  if constexpr (PAGED) {
-    pos = a.pos_dev[b];
-    pos_ok = pos >= 0 && pos / GT < a.table_stride;
-    U = pos_ok ? pos / GT * GT : 0;
-  } else {
-    U = prefix_limit(a, pos, pos_ok);
-  }
   const bool ring = (PAGED || a.tail_mode != TAIL_NONE) && (!fused || pos_ok);
   const bool ring_phase = ring;
   const float* hws = PAGED ? a.ws + ((int64_t)h * a.total_parts + a.seq_parts[2 * b]) * pw : a.ws + (int64_t)h * P * pw;
@@ -1410,7 +1401,8 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
     ticket = t;
   }
   __syncthreads();
-  if (ticket == last) tail_body<PAGED>(a, h, b, *reinterpret_cast<TailSmem*>(lds_raw), true);
+  // (pos, pos_ok, U as the prologue read them: the tail needs no second round trip for them)
+  if (ticket == last) tail_body<PAGED>(a, h, b, *reinterpret_cast<TailSmem*>(lds_raw), true, pos, pos_ok, U);
 }
 
 // ---------------------------------------------------------------- kernel B: ring + merge
@@ -1421,7 +1413,17 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) TailSmem sm;
   const int h = PAGED ? blockIdx.x % a.hkv : blockIdx.x;
   const int b = PAGED ? blockIdx.x / a.hkv : 0;
-  tail_body<PAGED>(a, h, b, sm, false);
+  int64_t pos;
+  bool pos_ok;
+  int64_t U;
+  if constexpr (PAGED) {
+    pos = a.pos_dev[b];
+    pos_ok = pos >= 0 && pos / GT < a.table_stride;
+    U = pos_ok ? pos / GT * GT : 0;
+  } else {
+    U = prefix_limit(a, pos, pos_ok);
+  }
+  tail_body<PAGED>(a, h, b, sm, false, pos, pos_ok, U);
 }
 
 // Standalone append: one workgroup per append unit (APPEND_UNITS per KV head).
