@@ -4,7 +4,7 @@ It stands in for ``NovaForCausalLM`` (src/nova/model.py:183-215) and reproduces 
 contract of ``LeanAttention.forward`` (src/nova/layers.py:99-162): q/k/v projection, q/k head
 norms, RoPE, then either the int8 cache (``update`` + ``attend`` / ``attend_prefill``, or the
 fused ``update_attend`` for one decode token) or the fp16 cache (``update`` + SDPA with the
-additive mask). Each layer is ``LeanDecoderLayer`` (layers.py:177-195): pre-norm attention and,
+additive mask). Each layer is ``LeanDecoderLayer`` (layers.py:177-218): pre-norm attention and,
 when ``intermediate_size > 0``, the SwiGLU MLP ``LeanMLP`` (layers.py:165-174), each added to
 the residual stream. No checkpoint is loaded: weights are seeded random tensors.
 

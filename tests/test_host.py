@@ -45,3 +45,66 @@ def test_bytes_per_token_int8():
     assert a == okq.bytes_per_token_int8(36, 8, 128)
     assert b == okq.bytes_per_token_int8(36, 8, 128, k_axis="token", token_group=64)
     assert 1.85 <= b["ratio"] <= 1.95
+
+
+def _tiny_model(intermediate: int = 96):
+    from nova_amd.skeleton import SkeletonConfig, SkeletonForCausalLM
+
+    cfg = SkeletonConfig(num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2, head_dim=128,
+                         hidden_size=64, intermediate_size=intermediate, vocab_size=50)
+    return cfg, SkeletonForCausalLM(cfg, seed=3).eval()
+
+
+def test_skeleton_mlp_is_leanmlp_and_layer_is_pre_norm_residual():
+    """``SkeletonMLP`` computes ``down(silu(gate(x)) * up(x))`` (``LeanMLP``, src/nova/layers.py:
+    173-174) and a layer adds attention and MLP to the residual stream after their RMSNorms
+    (``LeanDecoderLayer.forward``, layers.py:195-218); the MLP is absent with intermediate_size 0."""
+    import torch.nn.functional as F
+
+    cfg, model = _tiny_model()
+    layer = model.model.layers[0]
+    x = torch.randn(1, 3, cfg.hidden_size, generator=torch.Generator().manual_seed(0))
+    m = layer.mlp
+    want = (F.silu(x @ m.gate_proj.weight.T) * (x @ m.up_proj.weight.T)) @ m.down_proj.weight.T
+    assert torch.allclose(m(x), want, atol=1e-5)
+    _, no_mlp = _tiny_model(0)
+    assert no_mlp.model.layers[0].mlp is None and no_mlp.model.layers[0].post_norm is None
+
+
+def test_skeleton_stacked_weights_are_views_of_one_buffer():
+    """``stack_weights`` puts q/k/v and gate/up into single row-stacked weights whose slices
+    the Linear layers keep using, so the torch path and the kernel path read the same bytes."""
+    _, model = _tiny_model()
+    layer = model.model.layers[1]
+    before = [t.clone() for t in (layer.attn.q_proj.weight, layer.attn.k_proj.weight, layer.attn.v_proj.weight,
+                                  layer.mlp.gate_proj.weight, layer.mlp.up_proj.weight)]
+    layer.stack_weights()
+    qkv, gu = layer.w_qkv, layer.w_gate_up
+    assert torch.equal(qkv, torch.cat(before[:3])) and torch.equal(gu, torch.cat(before[3:]))
+    assert layer.attn.k_proj.weight.data_ptr() == qkv[before[0].shape[0]:].data_ptr()
+    assert layer.mlp.up_proj.weight.data_ptr() == gu[before[3].shape[0]:].data_ptr()
+
+
+def test_kernel_mode_needs_an_fp16_gpu_model():
+    _, model = _tiny_model()
+    import pytest
+
+    with pytest.raises(ValueError, match="fp16 on the GPU"):
+        model.use_decode_kernels(True)
+    assert model.model.decode_kernels is False
+
+
+def test_gemv_wrappers_refuse_cpu_tensors():
+    """The projection wrappers check their tensors before any library call (no fallback)."""
+    import pytest
+
+    from nova_amd import gemv as G
+
+    x = torch.zeros(64, dtype=torch.float16)
+    w = torch.zeros(8, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="CUDA"):
+        G.rms_gemv(x, w)
+    with pytest.raises(ValueError, match="CUDA"):
+        G.swiglu_gemv(x, torch.zeros(16, 64, dtype=torch.float16))
+    with pytest.raises(ValueError):
+        G.qk_norm_rope_(torch.zeros(6 * 128, dtype=torch.float16), 4, 1, x, x, 1e-6, torch.zeros(64), torch.zeros(1))
