@@ -1065,16 +1065,18 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   const bool tok1 = !PAGED && ring_phase && a.tok;  // per-token symmetric fused step: the tail is the new token
   const uint16_t* ring_h = PAGED ? a.rings + (((int64_t)b * a.hkv + h) * 2 + which) * GT * D : ring_of(a, h, which);
   RingQuarter rq;
+  // the new token's slot: from the step's input, not the ring this launch writes. Loaded
+  // into registers of its own and stored over its row once the quarter is in LDS: replacing
+  // a row whose load is still in flight would make every later load wait for it.
+  // (`fresh` is read only when fresh_on, which implies the block that loads it; a value on
+  // the other path would cost a merge copy, and with it a wait for the load)
+  const bool fresh_on = ring_phase && !completes && !tok1 && inl && !PAGED && a.tail_mode == TAIL_FUSED;
+  const int fresh_slot = (int)(pos % GT);
+  uint4 fresh;
   if (ring_phase && !completes && !tok1) {
     ring_load_quarter(ring_h, PAGED ? GT : (int)a.tail_slots, qtr, rq);
-    if (inl && !PAGED && a.tail_mode == TAIL_FUSED) {
-      // the new token's slot: from the step's input, not the ring this launch writes
-      const int slot = (int)(pos % GT), rl = lane >> 4, cl = lane & 15;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (16 * qtr + rl + 4 * i == slot)
-          rq.rows[i] = *reinterpret_cast<const uint4*>(fresh_of(a, h, which) + 8 * cl);
-    }
+    const uint16_t* fp = fresh_on ? fresh_of(a, h, which) : ring_h;  // a valid row either way
+    fresh = *reinterpret_cast<const uint4*>(fp + 8 * (lane & 15));
   }
   uint2 tw = {0u, 0u};
   uint16_t tsc = 0;
@@ -1141,7 +1143,11 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
             dq8_sym(tw.x, tw.y, half2_t{sc, sc});
       }
     } else {
-      ring_quarter_to_lds(rq.rows, qtr, which == 0 ? ring_k : ring_v);
+      uint8_t* rl_lds = which == 0 ? ring_k : ring_v;
+      ring_quarter_to_lds(rq.rows, qtr, rl_lds);
+      // (program order: this store lands after the quarter's store of the same row)
+      if (fresh_on && fresh_slot >> 4 == qtr && (fresh_slot & 3) == lane >> 4)
+        *reinterpret_cast<uint4*>(rl_lds + fresh_slot * (2 * D) + (ring_chunk_pos(fresh_slot, lane & 15) << 4)) = fresh;
     }
     __syncthreads();
   }
