@@ -1488,18 +1488,18 @@ __global__ void ring_mask_kernel(const int64_t* written, const int64_t* qlen, co
 // Causal attention of a chunk of M query tokens (positions U .. U + M - 1) over the int8t64
 // cache [0, U) (U a multiple of 64) and over the chunk's own fp16 K/V. Query rows of KV head
 // h: row r = (token r / gq, q head h gq + r % gq), M gq rows per head. Workgroup (h, tile,
-// split) takes rows 128 tile .. + 127 (4 waves x 2 MFMA row blocks of 16) and the split's
+// split) takes rows 256 tile .. + 255 (8 waves x 2 MFMA row blocks of 16) and the split's
 // share of the 64-token groups: cache groups [split G / S, (split + 1) G / S) and chunk
-// groups j = split (mod S) up to its last query token. Per group, the 4 waves dequantize
+// groups j = split (mod S) up to its last query token. Per group, the 8 waves dequantize
 // the int8 codes once into fp16 LDS tiles (K row-major, V transposed, both padded against
 // bank conflicts), then every wave runs QK^T and PV on v_mfma_f32_16x16x32_f16 for its 32
 // rows. P is a single fp16 operand (scaled by 2^15), as a fused fp16 attention kernel
 // computes it. Each workgroup writes one partial per row; a combine kernel merges the splits.
-constexpr int PF_WAVES = 4;
+constexpr int PF_WAVES = 8;
 constexpr int PF_THREADS = 64 * PF_WAVES;
 constexpr int PF_RB = 2;                             // MFMA row blocks per wave
-constexpr int PF_WG_PER_CU = PF_RB <= 2 ? 2 : 1;     // workgroups resident per CU (registers)
-constexpr int PF_ROWS = PF_WAVES * PF_RB * 16;       // 128 query rows per workgroup
+constexpr int PF_WG_PER_CU = 1;                      // workgroups resident per CU (~206 VGPRs per lane)
+constexpr int PF_ROWS = PF_WAVES * PF_RB * 16;       // 256 query rows per workgroup
 constexpr int PF_KROW = D + 8;                       // fp16 K tile row stride (halves)
 constexpr int PF_VROW = GT + 8;                      // fp16 V^T tile row stride (halves, 16-byte rows)
 constexpr int PF_PART = D + 4;                       // floats per row partial: acc[128], m, l, pad
@@ -1605,23 +1605,22 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
   const int last_tok = min(rows_h - 1, (tile + 1) * PF_ROWS - 1) / a.gq;  // last query token of the tile
   const int nchunk = min((a.M + GT - 1) / GT, last_tok / GT + 1);
 
-  // cache group loads: wave w issues K and V code rows 16w .. 16w + 15 and ruler w
+  // cache group loads: wave w issues K and V code rows 8w .. 8w + 7 and half w & 1 of ruler
+  // w >> 1 (kst, kmn, vst, vmn)
   auto issue = [&](int64_t grp, int sb) {
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(stage[sb]));
     const void* kb = uniform_ptr(a.kq + ((int64_t)h * a.capacity + grp * GT) * D);
     const void* vb = uniform_ptr(a.vq + ((int64_t)h * a.capacity + grp * GT) * D);
-#pragma unroll
-    for (int j = 2 * wave; j < 2 * wave + 2; ++j) {
-      const int row = 8 * j + (lane >> 3);
-      const uint32_t off = (uint32_t)(row * D + (((lane & 7) ^ swz(row)) << 4));
-      dma16(kb, off, base + 1024 * j);
-      dma16(vb, off, base + CODE_BYTES + 1024 * j);
-    }
-    const int64_t ro = ((int64_t)h * a.ngroups_cap + grp) * D;
-    const uint16_t* rsrc = wave == 0 ? a.kst : wave == 1 ? a.kmn : wave == 2 ? a.vst : a.vmn;
-    if (lane < 16) dma16(uniform_ptr(rsrc + ro), (uint32_t)(16 * lane), base + 2 * CODE_BYTES + 256 * wave);
+    const int row = 8 * wave + (lane >> 3);
+    const uint32_t off = (uint32_t)(row * D + (((lane & 7) ^ swz(row)) << 4));
+    dma16(kb, off, base + 1024 * wave);
+    dma16(vb, off, base + CODE_BYTES + 1024 * wave);
+    const int64_t ro = ((int64_t)h * a.ngroups_cap + grp) * D + 64 * (wave & 1);
+    const int rw = wave >> 1;
+    const uint16_t* rsrc = rw == 0 ? a.kst : rw == 1 ? a.kmn : rw == 2 ? a.vst : a.vmn;
+    if (lane < 8) dma16(uniform_ptr(rsrc + ro), (uint32_t)(16 * lane), base + 2 * CODE_BYTES + 256 * rw + 128 * (wave & 1));
   };
-  constexpr int DMA_PF = 5;  // loads per wave and group
+  constexpr int DMA_PF = 3;  // loads per wave and group
 
   // ---- MFMA phase over the tiles in LDS; `mask_base` >= 0: chunk tokens from that index (causal)
   auto attend_tiles = [&](int mask_base) {
@@ -1678,24 +1677,22 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
     {
       const uint8_t* sg = stage[sb];
       const uint16_t* rks = reinterpret_cast<const uint16_t*>(sg + 2 * CODE_BYTES);
-      // K: thread t dequantizes row t >> 2, dims 32 (t & 3) .. + 31
-      const int row = tid >> 2, cp = tid & 3, key = swz(row);
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int ch = 2 * cp + e;  // 16-dim chunk
+      // K: thread t dequantizes row t >> 3, dims 16 (t & 7) .. + 15
+      const int row = tid >> 3, key = swz(row);
+      {
+        const int ch = tid & 7;  // 16-dim chunk
         const uint4 kw = *reinterpret_cast<const uint4*>(sg + row * D + ((ch ^ key) << 4));
         const uint4 s0 = *reinterpret_cast<const uint4*>(rks + 16 * ch), s1 = *reinterpret_cast<const uint4*>(rks + 16 * ch + 8);
         const uint4 m0 = *reinterpret_cast<const uint4*>(rks + D + 16 * ch), m1 = *reinterpret_cast<const uint4*>(rks + D + 16 * ch + 8);
         *reinterpret_cast<half8_t*>(ktile + row * PF_KROW + 16 * ch) = dq8(kw.x, kw.y, s0, m0);
         *reinterpret_cast<half8_t*>(ktile + row * PF_KROW + 16 * ch + 8) = dq8(kw.z, kw.w, s1, m1);
       }
-      // V: transposed reads; wave w covers dim blocks 2w, 2w + 1 of both 32-token blocks
+      // V: transposed reads; wave w covers dim block w of both 32-token blocks
       const int r = c >> 1;
 #pragma unroll
       for (int B = 0; B < 2; ++B)
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int cb = 2 * wave + e;
+        {
+          const int cb = wave;
           const int vrow = 16 * (2 * B + (r >> 2)) + 4 * g + (r & 3);
           const u32x2 vw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
               (lds_v2i_t*)(const lds_void_t*)(sg + CODE_BYTES + vrow * D + 8 * (c & 1) + ((cb ^ swz(vrow)) << 4))));
@@ -1713,20 +1710,20 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
   for (int j = split; j < nchunk; j += a.splits) {
     __syncthreads();  // every wave is done with the tiles
     {
-      const int row = tid >> 2, cp = tid & 3, t = GT * j + row;
+      const int row = tid >> 3, cp = tid & 7, t = GT * j + row;
       const bool ok = t < a.M;
-      const uint16_t* kr = a.kc + ((int64_t)h * a.M + (ok ? t : 0)) * D + 32 * cp;
-      const uint16_t* vr = a.vc + ((int64_t)h * a.M + (ok ? t : 0)) * D + 32 * cp;
+      const uint16_t* kr = a.kc + ((int64_t)h * a.M + (ok ? t : 0)) * D + 16 * cp;
+      const uint16_t* vr = a.vc + ((int64_t)h * a.M + (ok ? t : 0)) * D + 16 * cp;
       const int vs = pf_vslot(row);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
+      for (int e = 0; e < 2; ++e) {
         const uint4 kw = ok ? *reinterpret_cast<const uint4*>(kr + 8 * e) : uint4{0, 0, 0, 0};
         const uint4 vw = ok ? *reinterpret_cast<const uint4*>(vr + 8 * e) : uint4{0, 0, 0, 0};
-        *reinterpret_cast<uint4*>(ktile + row * PF_KROW + 32 * cp + 8 * e) = kw;
+        *reinterpret_cast<uint4*>(ktile + row * PF_KROW + 16 * cp + 8 * e) = kw;
         const uint32_t wv[4] = {vw.x, vw.y, vw.z, vw.w};
 #pragma unroll
         for (int q2 = 0; q2 < 8; ++q2)
-          vtile[(32 * cp + 8 * e + q2) * PF_VROW + vs] = (uint16_t)(wv[q2 >> 1] >> (16 * (q2 & 1)));
+          vtile[(16 * cp + 8 * e + q2) * PF_VROW + vs] = (uint16_t)(wv[q2 >> 1] >> (16 * (q2 & 1)));
       }
     }
     __syncthreads();
