@@ -72,12 +72,27 @@ def _check_state(paged, conts, lens, step):
             assert torch.equal(paged.rings[layer][b, :, 1], c.tail_v[layer][0]), (b, layer)
 
 
-@pytest.mark.parametrize("lens", [[70, 200, 1000, 64], [1, 63, 129]])
-def test_paged_batch_matches_contiguous_caches(lens):
+def _set_parts(cache, parts):
+    """A caller's own work plan, as the C entry points accept it: ``parts[b]`` prefix parts
+    for sequence b (here fewer than ``plan()`` gives, down to one part per sequence)."""
+    wg_map, seq_parts = [], []
+    for b, p in enumerate(parts):
+        seq_parts += [len(wg_map), p]
+        wg_map += [(b << 16) | i for i in range(p)]
+    cache.wg_map = torch.tensor(wg_map, dtype=torch.int32, device="cuda")
+    cache.seq_parts = torch.tensor(seq_parts, dtype=torch.int32, device="cuda")
+    cache.total_parts = len(wg_map)
+
+
+@pytest.mark.parametrize("lens,parts", [([70, 200, 1000, 64], None), ([1, 63, 129], None),
+                                        ([70, 200, 1000, 64], [1, 2, 3, 1])])
+def test_paged_batch_matches_contiguous_caches(lens, parts):
     steps = 70
-    print(f"case lens={lens}", flush=True)
+    print(f"case lens={lens} parts={parts}", flush=True)
     ks, vs, qs = _data(lens, steps, seed=40)
     paged = _paged(lens, steps, ks, vs, seed=41)
+    if parts is not None:
+        _set_parts(paged, parts)
     conts = [_contiguous(n, steps, ks[b], vs[b]) for b, n in enumerate(lens)]
     _check_state(paged, conts, lens, -1)
     for i in range(steps):
