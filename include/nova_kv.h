@@ -367,7 +367,8 @@ int nkv_read_bw(const void* src, int64_t nbytes, uint32_t* sink, int64_t blocks,
 /*
  * y[o] = fp16(sum_i W[o][i] * xn[i]) (+ residual[o], added in fp16), xn = x when gamma is
  * NULL, else RMSNorm(x) = fp16(fp16(x * rsqrt(mean(x^2) + eps)) * gamma) with an fp32 mean.
- * Dot products accumulate in fp32. `residual` may be NULL; y may alias residual, not x.
+ * Dot products accumulate in fp32. `residual` may be NULL; y may be residual itself but must not
+ * overlap x or a shifted view of residual (NKV_ERR_INVALID).
  */
 int nkv_gemv(const uint16_t* x, const uint16_t* gamma, float eps, const uint16_t* w, int64_t out_features,
              int64_t in_features, const uint16_t* residual, uint16_t* y, void* stream);
@@ -376,6 +377,7 @@ int nkv_gemv(const uint16_t* x, const uint16_t* gamma, float eps, const uint16_t
  * The SwiGLU MLP's first half: act[j] = fp16(silu(g_j)) * u_j, g = W[0:inter] xn and
  * u = W[inter:2 inter] xn (each rounded to fp16), W the stacked [gate; up] weight of
  * [2 * intermediate][in_features], xn as in nkv_gemv (LeanMLP, src/nova/layers.py:173-174).
+ * act must not overlap x (NKV_ERR_INVALID).
  */
 int nkv_swiglu_gemv(const uint16_t* x, const uint16_t* gamma, float eps, const uint16_t* w_gate_up,
                     int64_t intermediate, int64_t in_features, uint16_t* act, void* stream);

@@ -223,12 +223,20 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(uint16_t* qkv, int hq,
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Whether the fp16 ranges [a, a + an) and [b, b + bn) share an element.
+bool overlap(const void* a, int64_t an, const void* b, int64_t bn) {
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return pa < pb + 2 * (uintptr_t)bn && pb < pa + 2 * (uintptr_t)an;
+}
+
+// Every workgroup reads all of x while others write their rows of y: y must not overlap x.
 int check(const char* what, const void* x, const void* w, const void* y, int64_t out, int64_t in) {
   if (!x || !w || !y) return fail(NKV_ERR_INVALID, "%s: null pointer argument", what);
-  if (out <= 0 || in <= 0 || in % 8 || in > GV_MAX_IN)
-    return fail(NKV_ERR_INVALID, "%s: sizes out=%lld in=%lld (in a positive multiple of 8, at most %d)", what,
-                (long long)out, (long long)in, GV_MAX_IN);
+  if (out <= 0 || out > INT32_MAX || in <= 0 || in % 8 || in > GV_MAX_IN)
+    return fail(NKV_ERR_INVALID, "%s: sizes out=%lld in=%lld (out in [1, 2^31), in a positive multiple of 8, at most %d)",
+                what, (long long)out, (long long)in, GV_MAX_IN);
   if (!al16(x) || !al16(w)) return fail(NKV_ERR_UNSUPPORTED, "%s: x and W must be 16-byte aligned", what);
+  if (overlap(x, in, y, out)) return fail(NKV_ERR_INVALID, "%s: the output overlaps x", what);
   return NKV_OK;
 }
 
@@ -316,6 +324,9 @@ extern "C" int nkv_gemv(const uint16_t* x, const uint16_t* gamma, float eps, con
   set_error("");
   if (int rc = check("gemv", x, w, y, out_features, in_features)) return rc;
   if (gamma && !al16(gamma)) return fail(NKV_ERR_UNSUPPORTED, "gemv: gamma must be 16-byte aligned");
+  // row o reads residual[o] and writes y[o] in one wave: y may be the residual, not a shifted view of it
+  if (residual && residual != y && overlap(residual, out_features, y, out_features))
+    return fail(NKV_ERR_INVALID, "gemv: y must be the residual itself or not overlap it");
   launch_gemv(x, gamma, eps, w, out_features, (int)in_features, residual, y, static_cast<hipStream_t>(stream));
   return check_launch("gemv");
 }

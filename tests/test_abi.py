@@ -102,6 +102,15 @@ def test_validation_errors_return_before_launch(lib):
     assert lib.nkv_gemv(fake, None, 1e-6, fake, 4, 16392, None, fake, None) == _lib.NKV_ERR_INVALID
     assert lib.nkv_gemv(fake + 2, None, 1e-6, fake, 4, 64, None, fake, None) == _lib.NKV_ERR_UNSUPPORTED
     assert lib.nkv_swiglu_gemv(fake, None, 1e-6, fake, 0, 64, fake, None) == _lib.NKV_ERR_INVALID
+    # outputs that overlap the input vector, or a residual they are shifted against, are races
+    w2, r3 = 1 << 21, 1 << 22
+    assert lib.nkv_gemv(fake, None, 1e-6, w2, 4, 64, None, fake + 16, None) == _lib.NKV_ERR_INVALID
+    assert b"overlaps x" in lib.nkv_last_error()
+    assert lib.nkv_gemv(fake, None, 1e-6, w2, 4, 64, r3, r3 + 2, None) == _lib.NKV_ERR_INVALID
+    assert b"residual" in lib.nkv_last_error()
+    assert lib.nkv_swiglu_gemv(fake, None, 1e-6, w2, 8, 64, fake + 120, None) == _lib.NKV_ERR_INVALID
+    assert b"overlaps x" in lib.nkv_last_error()
+    assert lib.nkv_gemv(fake, None, 1e-6, w2, 1 << 31, 64, None, r3, None) == _lib.NKV_ERR_INVALID
     assert lib.nkv_qk_norm_rope(fake, 32, 8, 64, fake, fake, 1e-6, fake, fake, None) == _lib.NKV_ERR_UNSUPPORTED
     assert b"head_dim" in lib.nkv_last_error()
 
