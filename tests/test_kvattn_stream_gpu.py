@@ -299,6 +299,46 @@ def test_partials_then_combine_equals_fused_step():
         assert torch.equal(a.lse, b.lse), p
 
 
+def test_fused_step_at_32k_context():
+    """The decode step at the benchmark's context (32 parts per KV head over 512 groups),
+    across the 512th group boundary: the fused step equals its two launches called one by
+    one bit for bit (state and output), the two-call ``update`` + ``attend`` within the
+    streaming criterion, and the dequantize-then-attend oracle likewise."""
+    from nova_amd import _lib
+
+    used0, steps = 32766, 4
+    _, k, v = make(used0 + steps, seed=61)
+    q = randn((1, HQ, 1, D), 62).cuda()
+    k, v = k.cuda(), v.cuda()
+    caches = [_cache(max_len=used0 + 128) for _ in range(3)]
+    for c in caches:
+        c.begin_prefill(used0)
+        c.set_prefill_pos(0)
+        c.update(k[:, :, :used0], v[:, :, :used0], 0)
+        c.finish_prefill(used0)
+    fused, split, two = caches
+    for p in range(used0, used0 + steps):
+        print(f"case 32k step pos={p}", flush=True)
+        for c in caches:
+            c.pos.fill_(p)
+        kn, vn = k[:, :, p:p + 1], v[:, :, p:p + 1]
+        of = fused.update_attend(kn, vn, q, 0).clone()
+        args = split.step_args(kn, vn, q, 0)
+        _lib.call("nkv_decode_step_partials_t64", *args)
+        _lib.call("nkv_decode_step_combine_t64", *args)
+        two.update(kn, vn, 0)
+        ot = two.attend(q, 0).clone()
+        for nm in ("kq", "vq", "kmn", "kst", "vmn", "vst", "tail_k", "tail_v"):
+            assert torch.equal(getattr(fused, nm)[0], getattr(split, nm)[0]), (p, nm)
+            assert torch.equal(getattr(fused, nm)[0], getattr(two, nm)[0]), (p, nm)
+        assert torch.equal(of, split.merged), p
+        assert_ulp_or_abs(npy(of)[0, :, 0], npy(ot)[0, :, 0].astype(np.float64), MAX_ULP, ABS_TOL, f"two-call p={p}")
+        qlen = int(fused._qlen.item())
+        assert qlen == (p + 1) // 64 * 64
+        want = _reference(k, v, q, p + 1, qlen)
+        assert_ulp_or_abs(npy(of)[0, :, 0], want, MAX_ULP, ABS_TOL, f"oracle p={p}")
+
+
 def test_fused_tail_counters_return_to_zero_and_layers_interleave():
     """The fused step's last-workgroup tail keeps one completion counter per head at the
     end of the workspace: after every call they read zero. Two caches of different
