@@ -84,10 +84,10 @@ def _set_parts(cache, parts):
     cache.total_parts = len(wg_map)
 
 
-@pytest.mark.parametrize("lens,parts", [([70, 200, 1000, 64], None), ([1, 63, 129], None),
-                                        ([70, 200, 1000, 64], [1, 2, 3, 1])])
-def test_paged_batch_matches_contiguous_caches(lens, parts):
-    steps = 70
+@pytest.mark.parametrize("lens,parts,steps", [([70, 200, 1000, 64], None, 70), ([1, 63, 129], None, 70),
+                                              ([70, 200, 1000, 64], [1, 2, 3, 1], 70),
+                                              ([9000, 13000, 4600], None, 3)])  # the benchmark's scale
+def test_paged_batch_matches_contiguous_caches(lens, parts, steps):
     print(f"case lens={lens} parts={parts}", flush=True)
     ks, vs, qs = _data(lens, steps, seed=40)
     paged = _paged(lens, steps, ks, vs, seed=41)
