@@ -1502,6 +1502,7 @@ constexpr int PF_WG_PER_CU = 1;                      // workgroups resident per 
 constexpr int PF_ROWS = PF_WAVES * PF_RB * 16;       // 256 query rows per workgroup
 constexpr int PF_KROW = D + 8;                       // fp16 K tile row stride (halves)
 constexpr int PF_VROW = GT + 8;                      // fp16 V^T tile row stride (halves, 16-byte rows)
+constexpr float PF_TAU = 8.0f;                       // lazy softmax rescaling threshold (log2)
 constexpr int PF_PART = D + 4;                       // floats per row partial: acc[128], m, l, pad
 
 // token slot of the V^T tile: P's k-slot order (slot 8g + r of a 32-token block <-> token
@@ -1529,9 +1530,10 @@ struct PrefillArgs {
 };
 
 // Online softmax of one 16-row block over 64 tokens, from the raw scores S[b][i] (token
-// 16b + 4g + i, row c; -inf where masked): m is kept in the log2 domain (max S * sl2), and P
-// comes out as exp2(S sl2 - m + 15) = 2^15 p in two fp16 A operands (tokens of blocks 0,1 and
-// 2,3). l accumulates the same scaled weights, so acc / l needs no rescaling.
+// 16b + 4g + i, row c; -inf where masked): m is a reference maximum in the log2 domain, within
+// PF_TAU below the row's maximum of S * sl2, and P comes out as exp2(S sl2 - m + 15 - PF_TAU)
+// <= 2^15 in two fp16 A operands (tokens of blocks 0,1 and 2,3). l accumulates the same scaled
+// weights, so acc / l needs no rescaling; acc and l are rescaled only when m moves.
 __device__ __forceinline__ void pf_softmax(WaveState& st, const float (&S)[4][4], float sl2, half8_t (&ph)[2]) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
   float smax = NEG_INF;
@@ -1540,10 +1542,13 @@ __device__ __forceinline__ void pf_softmax(WaveState& st, const float (&S)[4][4]
 #pragma unroll
     for (int i = 0; i < 4; ++i) smax = fmaxf(smax, S[b][i]);
   smax = max4rows(smax);
-  const float m_new = fmaxf(st.m, smax * sl2);
+  // the reference maximum moves only when the row's maximum grows by more than PF_TAU (log2):
+  // P = 2^(S sl2 - m + 15 - PF_TAU) <= 2^15 still, and the accumulators are rescaled rarely
+  const float m_cand = fmaxf(st.m, smax * sl2);
+  const float m_new = m_cand > st.m + PF_TAU ? m_cand : st.m;
   const float m_use = m_new == NEG_INF ? 0.0f : m_new;
   const float alpha = __builtin_amdgcn_exp2f(st.m - m_use);
-  const float off = 15.0f - m_use;
+  const float off = 15.0f - PF_TAU - m_use;
   float lsum = 0.0f;
   _Float16 p16[2][8];
 #pragma unroll
