@@ -163,8 +163,9 @@ __device__ __forceinline__ float sum4rows(float v) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// Online-softmax state of one wave. m, l: head (lane & 15), log2 domain.
-// acc[cb][i]: head 4*(lane>>4) + i, dim 16*cb + (lane&15), scaled by 2^15.
+// Online-softmax state of one wave. m, l: head (lane & 15), log2 domain; m is a reference
+// maximum (at least every score seen so far, times sl2), the weights are 2^(s sl2 - m + 15).
+// acc[cb][i]: head 4*(lane>>4) + i, dim 16*cb + (lane&15), in the same scale.
 struct WaveState {
   float m, l;
   float4_t acc[8];
@@ -356,6 +357,8 @@ __device__ __forceinline__ void wait_groups_all() { asm volatile("s_waitcnt vmcn
 // by 2^15 (folded into the exponent) and split into hi/lo fp16 A operands of token blocks
 // (0,1) and (2,3); l accumulates the same scaled weights (out = acc / l). The accumulator is
 // rescaled when a running maximum moved.
+constexpr float DEC_TAU = 8.0f;
+
 template <int NB>
 __device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[2 * NB][4], float sl2, half8_t (&phi)[NB],
                                              half8_t (&plo)[NB], int gq) {
@@ -366,7 +369,9 @@ __device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[2 * NB][4
 #pragma unroll
     for (int i = 0; i < 4; ++i) mloc = fmaxf(mloc, s[b][i]);
   mloc = max4rows(mloc) * sl2;
-  const float m_new = fmaxf(st.m, mloc);
+  // the reference maximum moves only when a score passes it, and then DEC_TAU above the new
+  // maximum: P = 2^(S sl2 - m + 15) <= 2^15 always, and the accumulators are rescaled rarely
+  const float m_new = mloc > st.m ? mloc + DEC_TAU : st.m;
   const float m_use = m_new == NEG_INF ? 0.0f : m_new;
   const float alpha = __builtin_amdgcn_exp2f(st.m - m_use);
   const float off = P_SCALE_LOG2 - m_use;
