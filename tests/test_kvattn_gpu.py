@@ -254,3 +254,34 @@ def test_other_gqa_ratios(gq):
     want, _ = _want(q, packed, used)
     got = int8_attn_decode(q.cuda(), *packed, used=used)
     assert_ulp_or_abs(npy(got)[0, :, 0], want, 2.0, 1e-5, f"gq={gq}")
+
+
+def _steer(k: torch.Tensor, q: torch.Tensor, profile: str) -> torch.Tensor:
+    """K with scores shaped along each KV head's first q head: ``jump`` adds 40 q/|q| to one
+    token 300 before the end (its score passes every earlier one by ~40 in log2 units, far
+    beyond the softmax's rescale headroom); ``rise`` adds a ramp 0 .. 20 q/|q| over the
+    tokens (the reference maximum moves again and again)."""
+    kf, qf = k.float(), q.float()[0, :, 0]
+    n, gq = kf.shape[2], qf.shape[0] // kf.shape[1]
+    for h in range(kf.shape[1]):
+        dirv = qf[h * gq] / qf[h * gq].norm()
+        if profile == "jump":
+            kf[0, h, n - 300] += 40.0 * dirv
+        else:
+            kf[0, h] += torch.linspace(0.0, 20.0, n)[:, None] * dirv[None, :]
+    return kf.half()
+
+
+@pytest.mark.parametrize("profile", ["jump", "rise"])
+def test_scores_that_move_the_softmax_reference(profile):
+    """The online softmax moves its reference maximum only past a headroom; scores built to
+    force a late large move, or many small ones, meet the ULP criterion against the oracle."""
+    from nova_amd.kvattn import int8_attn_decode
+
+    used = 4096
+    q, k, v = make(used, seed=71)
+    k = _steer(k, q, profile)
+    packed = _packed(k, v)
+    want, _ = _want(q, packed, used)
+    got = int8_attn_decode(q.cuda(), *packed, used=used)
+    assert_ulp_or_abs(npy(got)[0, :, 0], want, 2.0, 1e-5, profile)

@@ -82,3 +82,25 @@ def test_prefill_chunk_512_over_16k():
     got = int8_prefill_attend(q, kch, vch, *packed, used=16384)
     assert torch.isfinite(got).all()
     _check(got, q, kch, vch, packed, 16384, heads=[0, 7], tag="16k")
+
+
+@pytest.mark.parametrize("profile", ["jump", "rise"])
+def test_prefill_scores_that_move_the_softmax_reference(profile):
+    """As the decode test of the same name: cache scores with a late large jump, or rising over
+    the whole cache, against the oracle at the prefill criterion."""
+    from nova_amd.kvattn import int8_prefill_attend, pack_int8_kv
+
+    used, m = 2048, 65
+    q, kch, vch, _ = _case(32, 8, used, m, seed=81)
+    k = randn((1, 8, used + 64, D), 81, 1.0)
+    v = randn((1, 8, used + 64, D), 82, 1.0)
+    kf, qf = k.float(), q.float().cpu()[0, :, 0]
+    for h in range(8):
+        dirv = qf[4 * h] / qf[4 * h].norm()
+        if profile == "jump":
+            kf[0, h, used - 300] += 40.0 * dirv
+        else:
+            kf[0, h, :used] += torch.linspace(0.0, 20.0, used)[:, None] * dirv[None, :]
+    packed = [t.contiguous() for t in pack_int8_kv(kf.half().cuda(), v.cuda())]
+    got = int8_prefill_attend(q, kch, vch, *packed, used=used)
+    _check(got, q, kch, vch, packed, used, tag=profile)
