@@ -428,24 +428,40 @@ __device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[2 * NB][4
 // 32 NB tokens of one int8 group resident in LDS: K codes at `kc`, V codes at `vc` (rows of
 // 128 bytes, chunks swizzled by swz(row)), the group's rulers at `rul` (kst | kmn | vst |
 // vmn, 128 fp16 each); `nvalid` of the tokens are valid.
-template <int NB>
-__device__ __forceinline__ void attend_block(const AttnArgs& a, WaveState& st, const half8_t (&qb)[4],
-                                             const uint8_t* kc, const uint8_t* vc, const uint8_t* rul, int nvalid) {
+// One group's rulers as a lane uses them: K's step and min for the dims of its K operand
+// chunks, V's (splatted) for dim 16 cb + c. Read from LDS once per group, used by both halves.
+struct LaneRulers {
+  uint4 kst4[2][2], kmn4[2][2];
+  half2_t vsp[8], vmp[8];
+};
+
+__device__ __forceinline__ void load_rulers(const uint8_t* rul, LaneRulers& r) {
   const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
   const uint16_t* rks = reinterpret_cast<const uint16_t*>(rul);
-  const uint16_t* rkm = rks + D;
-  const uint16_t* rvs = rks + 2 * D;
-  const uint16_t* rvm = rks + 3 * D;
-
-  // ---- S^T = K Q^T
-  uint4 kst4[2][2], kmn4[2][2];
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      kst4[hh][e] = *reinterpret_cast<const uint4*>(rks + 16 * g + 64 * hh + 8 * e);
-      kmn4[hh][e] = *reinterpret_cast<const uint4*>(rkm + 16 * g + 64 * hh + 8 * e);
+      r.kst4[hh][e] = *reinterpret_cast<const uint4*>(rks + 16 * g + 64 * hh + 8 * e);
+      r.kmn4[hh][e] = *reinterpret_cast<const uint4*>(rks + D + 16 * g + 64 * hh + 8 * e);
     }
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb) {
+    const _Float16 vs = __builtin_bit_cast(_Float16, rks[2 * D + 16 * cb + c]);
+    const _Float16 vm = __builtin_bit_cast(_Float16, rks[3 * D + 16 * cb + c]);
+    r.vsp[cb] = half2_t{vs, vs};
+    r.vmp[cb] = half2_t{vm, vm};
+  }
+}
+
+template <int NB>
+__device__ __forceinline__ void attend_block(const AttnArgs& a, WaveState& st, const half8_t (&qb)[4],
+                                             const uint8_t* kc, const uint8_t* vc, const LaneRulers& ru, int nvalid) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  const auto& kst4 = ru.kst4;
+  const auto& kmn4 = ru.kmn4;
+
+  // ---- S^T = K Q^T
   float4_t S[2 * NB];
 #pragma unroll
   for (int b = 0; b < 2 * NB; ++b) {
@@ -478,14 +494,8 @@ __device__ __forceinline__ void attend_block(const AttnArgs& a, WaveState& st, c
   // ---- O += P V. Lane (c, g) of a transpose read supplies row k(g, c >> 1) and half
   // (c & 1) of the 16-dim chunk; it receives dim 16cb + c of the 8 tokens k(g, 0..7),
   // k(g, r) = 16 * (2B + (r >> 2)) + 4g + (r & 3), the token order of P's k-slots.
-  half2_t vsp[8], vmp[8];
-#pragma unroll
-  for (int cb = 0; cb < 8; ++cb) {
-    const _Float16 vs = __builtin_bit_cast(_Float16, rvs[16 * cb + c]);
-    const _Float16 vm = __builtin_bit_cast(_Float16, rvm[16 * cb + c]);
-    vsp[cb] = half2_t{vs, vs};
-    vmp[cb] = half2_t{vm, vm};
-  }
+  const auto& vsp = ru.vsp;
+  const auto& vmp = ru.vmp;
   const int r = c >> 1;
 #pragma unroll
   for (int B = 0; B < NB; ++B) {
@@ -1341,6 +1351,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
       const int64_t grp = gs + gi;
       const uint8_t* rul = my_stages + 2 * HALF_SLOT + rs * RULER_BYTES;
       const uint8_t* slot1 = my_stages + slot_bytes;
+      LaneRulers ru;
       // first half (slot 0); the second half, issued after it, may stay in flight
       if constexpr (TOK) {
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_HALF_TOK) : "memory");
@@ -1350,7 +1361,8 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
                          (int)min<int64_t>(32, U - grp * GT));
       } else {
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_SECOND_HALF) : "memory");
-        attend_block<1>(a, st, qb, my_stages, my_stages + HALF_CODE, rul, (int)min<int64_t>(32, U - grp * GT));
+        load_rulers(rul, ru);  // the group's rulers, for both halves
+        attend_block<1>(a, st, qb, my_stages, my_stages + HALF_CODE, ru, (int)min<int64_t>(32, U - grp * GT));
       }
       const int nx = gi + WAVES;
       // second half (slot 1)
@@ -1367,13 +1379,13 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
         if (nx < ng) issue_half_paged(a, b, h, gs + nx, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
         if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF_PAGED) : "memory");
         else wait_groups_all();
-        if (nv2 > 0) attend_block<1>(a, st, qb, slot1, slot1 + HALF_CODE, rul, nv2);
+        if (nv2 > 0) attend_block<1>(a, st, qb, slot1, slot1 + HALF_CODE, ru, nv2);
         if (nx < ng) issue_half_paged(a, b, h, gs + nx, 1, my_lds + HALF_SLOT, 0u);
       } else {
         if (nx < ng) issue_half(a, h, gs + nx, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
         if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF) : "memory");
         else wait_groups_all();
-        if (nv2 > 0) attend_block<1>(a, st, qb, slot1, slot1 + HALF_CODE, rul, nv2);
+        if (nv2 > 0) attend_block<1>(a, st, qb, slot1, slot1 + HALF_CODE, ru, nv2);
         if (nx < ng) issue_half(a, h, gs + nx, 1, my_lds + HALF_SLOT, 0u);
       }
       gi = nx;
