@@ -352,13 +352,14 @@ __device__ __forceinline__ void wait_groups_all() { asm volatile("s_waitcnt vmcn
 
 // ---------------------------------------------------------------- one group's attention
 
-// Online-softmax update from the raw scores S[b][i] (q.k, token 16b + 4g + i, head c; -inf
-// where masked), in the log2 domain: m = max S * sl2, p = 2^(S sl2 - m). P comes out scaled
-// by 2^15 (folded into the exponent) and split into hi/lo fp16 A operands of token blocks
-// (0,1) and (2,3); l accumulates the same scaled weights (out = acc / l). The accumulator is
-// rescaled when a running maximum moved.
-constexpr float DEC_TAU = 8.0f;
+constexpr float DEC_TAU = 8.0f;  // headroom of the reference maximum (log2 domain)
 
+// Online-softmax update from the raw scores S[b][i] (q.k, token 16b + 4g + i, head c; -inf
+// where masked), in the log2 domain: m is a reference maximum, at least every S * sl2 seen,
+// and p = 2^(S sl2 - m). P comes out scaled by 2^15 (folded into the exponent) and split into
+// hi/lo fp16 A operands of token blocks (0,1) and (2,3); l accumulates the same scaled weights
+// (out = acc / l). m moves only when a score passes it, to DEC_TAU above the block's maximum,
+// and only then are the accumulators rescaled.
 template <int NB>
 __device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[2 * NB][4], float sl2, half8_t (&phi)[NB],
                                              half8_t (&plo)[NB], int gq) {
@@ -425,11 +426,9 @@ __device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[2 * NB][4
   }
 }
 
-// 32 NB tokens of one int8 group resident in LDS: K codes at `kc`, V codes at `vc` (rows of
-// 128 bytes, chunks swizzled by swz(row)), the group's rulers at `rul` (kst | kmn | vst |
-// vmn, 128 fp16 each); `nvalid` of the tokens are valid.
 // One group's rulers as a lane uses them: K's step and min for the dims of its K operand
-// chunks, V's (splatted) for dim 16 cb + c. Read from LDS once per group, used by both halves.
+// chunks, V's (splatted) for dim 16 cb + c, read from the group's ruler rows in LDS (kst | kmn
+// | vst | vmn, 128 fp16 each) once per group and used by both halves.
 struct LaneRulers {
   uint4 kst4[2][2], kmn4[2][2];
   half2_t vsp[8], vmp[8];
@@ -454,6 +453,9 @@ __device__ __forceinline__ void load_rulers(const uint8_t* rul, LaneRulers& r) {
   }
 }
 
+// 32 NB tokens of one int8 group resident in LDS: K codes at `kc`, V codes at `vc` (rows of
+// 128 bytes, chunks swizzled by swz(row)), the group's rulers in `ru`; `nvalid` of the tokens
+// are valid.
 template <int NB>
 __device__ __forceinline__ void attend_block(const AttnArgs& a, WaveState& st, const half8_t (&qb)[4],
                                              const uint8_t* kc, const uint8_t* vc, const LaneRulers& ru, int nvalid) {
