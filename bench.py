@@ -1,32 +1,30 @@
 """Benchmark: int8-KV decode attention over 36 layers at 32k context on one MI355X.
 
-Workload (the long-context decode configuration): 36 layers x (32 q heads, 8 KV heads,
-head_dim 128), batch 1, int8t64 KV cache prefilled to 32768 tokens from seeded N(0,1)
-fp16 K/V with 4 random K channels per head scaled x8. One decode step = for each layer
-one fused append + attention launch (``KVInt8Cache.update_attend``) with that layer's
-synthetic q/k/v, then ``pos += 1``; the step is captured once as a hipGraph and
-replayed (one replay per token). W untimed replays, then K timed replays bracketed by
+Headline workload (the long-context decode configuration): 36 layers x (32 q heads, 8 KV heads,
+head_dim 128), batch 1, int8t64 KV cache prefilled to 32768 tokens from seeded N(0,1) fp16 K/V
+with 4 random K channels per head scaled x8. One decode step = for each layer one fused append +
+attention launch (``KVInt8Cache.update_attend``), then ``pos += 1``. The layers are chained as in
+a model: layer l's query and its new K/V token are views of layer l-1's attention output (q = the
+whole output, k = q heads 0, 4, .., v = q heads 1, 5, ..), and layer 0 reads the previous step's
+last output, so no launch can start before the previous one has finished. The step is captured
+once as a hipGraph; W untimed replays, then K timed replays bracketed by
 ``torch.cuda.synchronize()`` and HIP events on the replay stream.
 
-Each layer's step is two launches: the prefix kernel (the append and the split-K
-partials over the int8 prefix) and the tail kernel (ring attention and the combine).
+One JSON line (the driver's contract). ``value`` = decode tokens/s of the whole job.
+``roofline`` is the fused decode-step launch the step runs (``attn_prefix_kernel<0>``: append,
+split-K partials, last-workgroup tail): algorithmic bytes per launch / its average duration,
+timed with HIP events over K replays of a graph of the 36 chained launches of one step.
+``traffic`` comes from the committed rocprofv3 --pmc summary of that kernel (FETCH_SIZE +
+WRITE_SIZE per dispatch, each scaled by what the counter reads for the library's copy kernel of
+known size). ``cpu_baseline`` times the repo's torch fp32 restatement of the reference algorithm
+(dequantize the int8 prefix, append the ring, repeat KV heads, softmax attention) on the host
+cores for one layer and a few steps, scaled to the 36-layer step. ``gpu_clock`` is read with
+amd-smi while the step graph replays. ``workloads`` carries the other configurations measured in
+the same run: the per-token symmetric format, the paged ragged batch, the MFMA chunked prefill.
 
-Prints one JSON line (the driver's contract). ``value`` = decode tokens/s of the whole
-job. ``roofline`` refers to the dominant kernel, the prefix kernel: its algorithmic bytes
-per launch / its average launch duration, timed with HIP events over K replays of a
-graph holding only its 36 launches per step (``nkv_decode_step_partials_t64``, the same
-kernel and arguments as in the full step); the tail kernel is timed the same way and
-reported beside it. ``traffic`` comes from the committed rocprofv3 --pmc summary
-(FETCH_SIZE + WRITE_SIZE per dispatch of the prefix kernel, scaled by what the same
-counters read for the library's plain copy kernel of known size). ``cpu_baseline`` times
-the numpy oracle (dequantize + softmax attention, threads over KV heads) on one layer for
-~10-30 s and scales to the 36-layer step.
-
-    python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu-baseline] [--scheme t64|tok]
-
-``--scheme tok`` runs the same workload on the per-token symmetric int8 format
-(``KVInt8TokCache``: every token int8 with one fp16 scale per token and KV head).
-    python bench.py --traffic-from FETCH_DIR WRITE_DIR   # summarize two rocprofv3 --pmc runs
+    python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu-baseline] [--only]
+    python bench.py --workload decode|paged|prefill|e2e [--scheme t64|tok]   # one workload alone
+    python bench.py --traffic-from FETCH_DIR WRITE_DIR [--scheme tok]      # summarize --pmc runs
 """
 
 from __future__ import annotations
@@ -35,9 +33,10 @@ import argparse
 import json
 import os
 import re
+import subprocess
 import sys
+import threading
 import time
-from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
@@ -45,45 +44,38 @@ sys.path.insert(0, str(ROOT))
 
 LAYERS, HQ, HKV, D, CTX = 36, 32, 8, 128, 32768
 HBM_PEAK_GBS = 8000.0
-# the fused step's append per layer: K and V ring read (64 x 128 fp16 each per KV head),
-# new token read and written into the ring, 64 code rows and 4 ruler rows written
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+COPY_BYTES = 64 << 20
+# the int8t64 append per layer and step: K and V rings read (64 x 128 fp16 per KV head), the new
+# token read and written into the ring, 64 code rows and 4 ruler rows written
 APPEND_BYTES = 64 * 128 * 2 * 2 * HKV + 2 * 2 * 128 * 2 * HKV + 64 * 128 * 2 * HKV + 4 * 128 * 2 * HKV
-Q_BYTES = HQ * D * 2
-PREFIX_KERNEL = "attn_prefix_kernel"
-COPY_KERNEL = "copy16_kernel"
-TRAFFIC_FILE = ROOT / "profiles" / "attn_prefix_kernel_32k_traffic.txt"
-TRAFFIC_FILE_TOK = ROOT / "profiles" / "attn_prefix_kernel_tok_32k_traffic.txt"
-# per-token symmetric format: the new token read, its codes and scale written (8 KV heads)
+# the per-token symmetric append: the new token read, its codes and scale written
 APPEND_BYTES_TOK = 2 * 128 * 2 * HKV + 2 * 128 * HKV + 2 * 2 * HKV
+STEP_KERNEL = "attn_prefix_kernel"
+COPY_KERNEL = "copy16_kernel"
+TRAFFIC = {"t64": ROOT / "profiles" / "decode_step_32k_traffic.txt",
+           "tok": ROOT / "profiles" / "decode_step_tok_32k_traffic.txt"}
+VOCAB_QWEN3_4B = 151936
 
 
 def attn_bytes(u: int) -> int:
-    """Algorithmic bytes of one layer's decode attention with ``u`` tokens written:
-    int8 codes + fp16 rulers of whole groups (2176 B per token over 8 KV heads), fp16
-    ring tokens (4096 B), q and out (16384 B)."""
+    """Algorithmic bytes of one layer's int8t64 decode attention with ``u`` tokens written:
+    codes + fp16 rulers of the whole groups (2176 B per token over 8 KV heads), the fp16 ring
+    tokens (4096 B each), q and out (16384 B)."""
     q = u // 64 * 64
     return 2176 * q + 4096 * (u - q) + 16384
 
 
 def attn_bytes_tok(u: int) -> int:
-    """Algorithmic bytes of one layer's decode attention over ``u`` tokens of the per-token
-    symmetric format: int8 codes + one fp16 scale per token, K and V, 8 KV heads (2080 B
-    per token), q and out (16384 B)."""
+    """The same for the per-token symmetric format: int8 codes + one fp16 scale per token, K and
+    V, 8 KV heads (2080 B per token), q and out."""
     return 2080 * u + 16384
 
 
-def prefix_launch_bytes_tok(u: int) -> int:
-    """One prefix-kernel launch of the per-token symmetric step: the ``u - 1`` tokens before
-    the new one, q, and the append."""
-    return 2080 * max(u - 1, 0) + Q_BYTES + APPEND_BYTES_TOK
-
-
-def prefix_launch_bytes(u: int) -> int:
-    """Algorithmic bytes of one prefix-kernel launch with ``u`` tokens written: int8 codes
-    + fp16 rulers of the whole groups before the ring's group (2176 B per token over 8 KV
-    heads), q, and the append."""
-    prefix = max(u - 1, 0) // 64 * 64
-    return 2176 * prefix + Q_BYTES + APPEND_BYTES
+def step_launch_bytes(u: int, scheme: str = "t64") -> int:
+    """Algorithmic bytes of one fused decode-step launch (append + attention) at ``u`` tokens
+    written after the append."""
+    return attn_bytes_tok(u) + APPEND_BYTES_TOK if scheme == "tok" else attn_bytes(u) + APPEND_BYTES
 
 
 def parse_args():
@@ -97,19 +89,24 @@ def parse_args():
     ap.add_argument("--splits", type=int, default=0, help="prefill: cache splits (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--only", action="store_true", help="the headline workload alone (no extra workloads)")
+    ap.add_argument("--no-clock", action="store_true", help="skip the amd-smi clock reading")
     ap.add_argument("--chunk", type=int, default=2048, help="e2e: streamed prefill chunk (a multiple of 64)")
-    ap.add_argument("--workload", choices=("decode", "paged", "prefill", "e2e"), default="decode",
-                    help="decode: one 32k sequence (the headline); paged: 8 ragged sequences in a paged cache; "
-                         "prefill: a 512-token chunk over a 16384-token int8 cache (MFMA)")
+    ap.add_argument("--workload", choices=("decode", "paged", "prefill", "e2e"), default=None,
+                    help="run one workload alone and print its line")
     ap.add_argument("--scheme", choices=("t64", "tok"), default="t64",
-                    help="KV format: int8t64 (the reference's) or per-token symmetric")
+                    help="--workload decode: KV format, int8t64 (the reference's) or per-token symmetric")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
-                    help="summarize two rocprofv3 --pmc runs of this script into the traffic file")
+                    help="summarize two rocprofv3 --pmc runs of the decode workload into the traffic file")
     return ap.parse_args()
 
 
+# ---------------------------------------------------------------- rocprof traffic summaries
+
+
 def _pmc_means(run_dir: str, counter: str) -> dict:
-    """Mean per-dispatch value of ``counter`` for each kernel in a rocprofv3 --pmc CSV run."""
+    """Mean per-dispatch value of ``counter`` per kernel (the step kernel, the copy kernel) in a
+    rocprofv3 --pmc CSV run."""
     import csv
 
     files = sorted(Path(run_dir).rglob("*counter_collection.csv"))
@@ -121,408 +118,314 @@ def _pmc_means(run_dir: str, counter: str) -> dict:
             for row in csv.DictReader(fh):
                 if row.get("Counter_Name") != counter:
                     continue
-                name = row["Kernel_Name"]
-                for key in (PREFIX_KERNEL, "attn_tail_kernel", COPY_KERNEL):
-                    if key in name:
+                for key in (STEP_KERNEL, COPY_KERNEL):
+                    if key in row["Kernel_Name"]:
                         acc.setdefault(key, []).append(float(row["Counter_Value"]))
     return {k: sum(v) / len(v) for k, v in acc.items()}
 
 
-def write_traffic(fetch_dir: str, write_dir: str, scheme: str = "t64") -> None:
-    """Traffic of the prefix kernel from FETCH_SIZE and WRITE_SIZE (KiB per dispatch),
-    each scaled by the factor that makes the same counter read the copy kernel's known
-    byte count (COPY_BYTES read and written)."""
+def write_traffic(fetch_dir: str, write_dir: str, scheme: str) -> None:
+    """HBM bytes per dispatch of the fused step kernel from FETCH_SIZE and WRITE_SIZE (KiB),
+    each scaled by the factor that makes the same counter read the copy kernel's known bytes."""
     fetch, write = _pmc_means(fetch_dir, "FETCH_SIZE"), _pmc_means(write_dir, "WRITE_SIZE")
     f_scale = COPY_BYTES / (fetch[COPY_KERNEL] * 1024)
     w_scale = COPY_BYTES / (write[COPY_KERNEL] * 1024)
-    f_bytes = fetch[PREFIX_KERNEL] * 1024 * f_scale
-    w_bytes = write[PREFIX_KERNEL] * 1024 * w_scale
-    tok = scheme == "tok"
-    alg = prefix_launch_bytes_tok(CTX + 1) if tok else prefix_launch_bytes(CTX + 1)
-    flag = " --scheme tok" if tok else ""
+    f_bytes = fetch[STEP_KERNEL] * 1024 * f_scale
+    w_bytes = write[STEP_KERNEL] * 1024 * w_scale
+    alg = step_launch_bytes(CTX + 1, scheme)
+    flag = " --scheme tok" if scheme == "tok" else ""
+    cmd = f"python3 bench.py --workload decode{flag} --steps 4 --warmup 1 --no-cpu-baseline --no-clock"
     lines = [
-        f"# HBM traffic of nkv::attn_prefix_kernel ({'per-token symmetric' if tok else 'int8t64'} format), "
-        "32k-context decode step (36 layers, 32 q / 8 kv heads)",
-        "# made by (rocprofv3 --pmc runs of bench.py, then this summary):",
-        f"#   rocprofv3 --pmc FETCH_SIZE -d FETCH_DIR -o run --output-format csv -- python3 bench.py --steps 4 --warmup 1 --no-cpu-baseline{flag}",
-        f"#   rocprofv3 --pmc WRITE_SIZE -d WRITE_DIR -o run --output-format csv -- python3 bench.py --steps 4 --warmup 1 --no-cpu-baseline{flag}",
+        f"# HBM traffic of the fused decode-step launch nkv::attn_prefix_kernel<{1 if scheme == 'tok' else 0}> "
+        f"({'per-token symmetric' if scheme == 'tok' else 'int8t64'} format), 32k context, 32 q / 8 kv heads",
+        "# made by (two rocprofv3 --pmc runs of the decode workload, then this summary):",
+        f"#   rocprofv3 --pmc FETCH_SIZE -d FETCH_DIR -o run --output-format csv -- {cmd}",
+        f"#   rocprofv3 --pmc WRITE_SIZE -d WRITE_DIR -o run --output-format csv -- {cmd}",
         f"#   python3 bench.py --traffic-from FETCH_DIR WRITE_DIR{flag}",
         f"copy_kernel_bytes: {COPY_BYTES}  (read, and again written, by nkv_copy_bytes)",
         f"copy_kernel_FETCH_SIZE_KiB: {fetch[COPY_KERNEL]:.1f}  -> fetch scale {f_scale:.4f}",
         f"copy_kernel_WRITE_SIZE_KiB: {write[COPY_KERNEL]:.1f}  -> write scale {w_scale:.4f}",
-        f"prefix_kernel_FETCH_SIZE_KiB: {fetch[PREFIX_KERNEL]:.1f}  -> {f_bytes:.0f} B",
-        f"prefix_kernel_WRITE_SIZE_KiB: {write[PREFIX_KERNEL]:.1f}  -> {w_bytes:.0f} B",
+        f"step_kernel_FETCH_SIZE_KiB: {fetch[STEP_KERNEL]:.1f}  -> {f_bytes:.0f} B",
+        f"step_kernel_WRITE_SIZE_KiB: {write[STEP_KERNEL]:.1f}  -> {w_bytes:.0f} B",
         f"algorithmic_bytes_per_launch: {alg}",
         f"traffic_bytes_per_launch: {f_bytes + w_bytes:.0f}",
         f"traffic_over_algorithmic: {(f_bytes + w_bytes) / alg:.4f}",
     ]
-    if "attn_tail_kernel" in fetch and "attn_tail_kernel" in write:
-        lines.append(f"tail_kernel_traffic_bytes_per_launch: "
-                     f"{fetch['attn_tail_kernel'] * 1024 * f_scale + write['attn_tail_kernel'] * 1024 * w_scale:.0f}")
-    (TRAFFIC_FILE_TOK if tok else TRAFFIC_FILE).write_text("\n".join(lines) + "\n")
+    TRAFFIC[scheme].write_text("\n".join(lines) + "\n")
     print("\n".join(lines))
 
 
-def read_traffic(path: Path = TRAFFIC_FILE):
-    """HBM bytes per launch of the prefix kernel from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), or None."""
+def read_traffic(scheme: str):
+    """HBM bytes per launch of the fused step kernel from the committed summary, or None."""
+    path = TRAFFIC[scheme]
     if not path.exists():
         return None
     m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text(), re.M)
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(budget_s: float, scheme: str = "t64") -> dict:
-    """Time the numpy oracle's decode step for one layer at 32k context: dequantize the
-    int8 prefix with the stored rulers, softmax attention over prefix + ring. Threads run
-    the 8 KV heads in parallel (numpy releases the GIL inside its kernels)."""
-    import numpy as np
-
-    from oracle import attn as oattn
-    from oracle import kvquant as okq
-
-    rng = np.random.default_rng(0)
-    n = CTX
-    k = rng.standard_normal((HKV, n, D), dtype=np.float32).astype(np.float16)
-    v = rng.standard_normal((HKV, n, D), dtype=np.float32).astype(np.float16)
-    tok = scheme == "tok"
-    if tok:
-        kq, ks = okq.quantize_tok(k)
-        vq, vs = okq.quantize_tok(v)
-    else:
-        kq, kmn, kst = okq.quantize_int8_token(k, 64)
-        vq, vmn, vst = okq.quantize_int8_token(v, 64)
-    ring_k = k[:, -64:].copy()
-    ring_v = v[:, -64:].copy()
-    q = (rng.standard_normal((HQ, D)) / D ** 0.5).astype(np.float16)
-    gq = HQ // HKV
-    threads = min(HKV, os.cpu_count() or 1)
-
-    def head(h):
-        if tok:
-            k16 = okq.dequantize_tok(kq[h], ks[h])
-            v16 = okq.dequantize_tok(vq[h], vs[h])
-        else:
-            k16 = okq.dequantize_int8_token(kq[h:h + 1], kmn[h:h + 1], kst[h:h + 1], 64)[0]
-            v16 = okq.dequantize_int8_token(vq[h:h + 1], vmn[h:h + 1], vst[h:h + 1], 64)[0]
-        kk = np.concatenate([k16, ring_k[h, :1]], 0)
-        vv = np.concatenate([v16, ring_v[h, :1]], 0)
-        return oattn.attend_fp16_kv(q[h * gq:(h + 1) * gq], kk[None], vv[None])[0]
-
-    reps = 0
-    t0 = time.perf_counter()
-    with ThreadPoolExecutor(threads) as ex:
-        while True:
-            list(ex.map(head, range(HKV)))
-            reps += 1
-            el = time.perf_counter() - t0
-            if el >= budget_s or (reps >= 3 and el > budget_s * 0.7):
-                break
-    per_layer = el / reps
-    per_step = per_layer * LAYERS
-    return {"value": 1.0 / per_step, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"numpy oracle ({scheme}), 1 layer x {reps} decode steps at {CTX} ctx ({el:.1f} s), "
-                      f"scaled x{LAYERS} layers (extrapolated)",
-            "seconds_per_step": per_step}
+# ---------------------------------------------------------------- host side: CPU baseline, clock
 
 
-COPY_BYTES = 64 << 20
+def host_threads() -> int:
+    """The host threads this process may use: the CPUs it is pinned to, capped by OMP_NUM_THREADS."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
 
 
-MFMA_FP16_PEAK_TFLOPS = 2500.0
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
-def bench_prefill(args) -> int:
-    """Chunked prefill over int8 KV: a 512-token fp16 query chunk attending causally to a
-    16384-token int8t64 cache plus itself, 32 q / 8 KV heads, head_dim 128 (seed 4). Timed
-    with HIP events over K graph replays of the two launches. Prints one JSON line: chunks/s,
-    achieved TFLOP/s and MFMA utilisation (against the dense fp16 peak), GB/s."""
+def cpu_baseline(budget_s: float, scheme: str, ctx: int, layers: int) -> dict:
+    """The reference algorithm on the host: the torch fp32 restatement (dequantize the int8
+    prefix, append the valid ring slots, repeat the KV heads, softmax attention) of one layer's
+    decode step at ``ctx`` tokens, timed over a few steps with every host thread, scaled to the
+    ``layers``-layer step. The codes and rulers are synthetic (the timing does not depend on them)."""
     import torch
 
-    from nova_amd import _lib
-    from nova_amd.kvattn import int8_prefill_attend, pack_int8_kv
+    from oracle import torch_ref
 
-    _lib.load()
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    M, U = 512, 16384
-    K = args.steps if args.steps != 256 else 64
-    W = args.warmup
-    g = torch.Generator(device=dev).manual_seed(4)
-    k = torch.randn(1, HKV, U, D, generator=g, device=dev).half()
-    v = torch.randn(1, HKV, U, D, generator=g, device=dev).half()
-    packed = [t.contiguous() for t in pack_int8_kv(k, v)]
-    del k, v
-    q = torch.randn(1, HQ, M, D, generator=g, device=dev).half()
-    kc = torch.randn(1, HKV, M, D, generator=g, device=dev).half()
-    vc = torch.randn(1, HKV, M, D, generator=g, device=dev).half()
-    out = torch.empty_like(q)
-    splits = args.splits or int(_lib.load().nkv_prefill_default_splits(HKV, HQ, M, U))
-    scratch = torch.empty(int(_lib.load().nkv_prefill_workspace_bytes(HKV, HQ, M, splits)), dtype=torch.uint8, device=dev)
-    int8_prefill_attend(q, kc, vc, *packed, used=U, out=out, scratch=scratch, splits=splits)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        int8_prefill_attend(q, kc, vc, *packed, used=U, out=out, scratch=scratch, splits=splits)
-    stream = torch.cuda.current_stream(dev)
-    for _ in range(W):
+    torch.set_num_threads(host_threads())
+    g = torch.Generator().manual_seed(0)
+    q = (torch.randn(HQ, D, generator=g) / D ** 0.5).half()
+    if scheme == "tok":
+        kq = torch.randint(-127, 128, (HKV, ctx, D), generator=g, dtype=torch.int8)
+        vq = torch.randint(-127, 128, (HKV, ctx, D), generator=g, dtype=torch.int8)
+        ks = (torch.rand(HKV, ctx, generator=g) * 0.02 + 0.01).half()
+        vs = (torch.rand(HKV, ctx, generator=g) * 0.02 + 0.01).half()
+        run = lambda: torch_ref.decode_step_tok(q, kq, ks, vq, vs, ctx)  # noqa: E731
+    else:
+        ng = -(-ctx // 64)
+        kq = torch.randint(0, 256, (HKV, ctx + 64, D), generator=g, dtype=torch.uint8)
+        vq = torch.randint(0, 256, (HKV, ctx + 64, D), generator=g, dtype=torch.uint8)
+        rul = [(torch.rand(HKV, ng + 1, D, generator=g) * s + o).half() for s, o in ((2, -3), (0.02, 0.01))] * 2
+        ring_k = torch.randn(HKV, 64, D, generator=g).half()
+        ring_v = torch.randn(HKV, 64, D, generator=g).half()
+        written = ctx + 1  # the step after a 32768-token prefill: one token in the ring
+        run = lambda: torch_ref.decode_step_t64(q, kq, rul[0], rul[1], vq, rul[2], rul[3], ring_k,  # noqa: E731
+                                                ring_v, written)
+    run()  # warm up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        run()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 64:
+            break
+    per_step = el / reps * layers
+    return {"value": round(1.0 / per_step, 4), "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"torch fp32 restatement ({scheme}): 1 layer x {reps} decode steps at {ctx} ctx + ring "
+                      f"({el:.1f} s, {torch.get_num_threads()} threads), scaled x{layers} layers (extrapolated)"}
+
+
+def _walk_clocks(obj, path=""):
+    """(path, MHz) of every ``{"clk": {"value": v}}``-like leaf of amd-smi's JSON."""
+    if isinstance(obj, dict):
+        for k, v in obj.items():
+            p = f"{path}/{k}"
+            if k in ("clk", "cur_clk", "current") and isinstance(v, dict) and "value" in v:
+                try:
+                    yield p, float(v["value"])
+                except (TypeError, ValueError):
+                    pass
+            else:
+                yield from _walk_clocks(v, p)
+    elif isinstance(obj, list):
+        for i, v in enumerate(obj):
+            yield from _walk_clocks(v, f"{path}[{i}]")
+
+
+def read_gpu_clock(timeout: float = 30.0) -> dict:
+    """The GPU clocks as amd-smi reports them (``amd-smi metric --clock --json``)."""
+    try:
+        r = subprocess.run(["amd-smi", "metric", "--clock", "--json"], capture_output=True, text=True,
+                           timeout=timeout)
+    except (OSError, subprocess.TimeoutExpired) as e:
+        return {"source": "amd-smi metric --clock", "error": str(e)[:200]}
+    try:
+        found = list(_walk_clocks(json.loads(r.stdout)))
+    except ValueError:
+        return {"source": "amd-smi metric --clock", "error": (r.stdout + r.stderr)[:300]}
+    gfx = [v for p, v in found if "gfx" in p.lower()]
+    mem = [v for p, v in found if "mem" in p.lower()]
+    return {"source": "amd-smi metric --clock --json", "gfx_mhz": gfx[:8] or None, "mem_mhz": mem[:1] or None}
+
+
+def clock_under_load(replay) -> dict:
+    """Read the clock in a thread while ``replay()`` keeps the GPU busy (bounded to ~40 s)."""
+    box: dict = {}
+    t = threading.Thread(target=lambda: box.update(read_gpu_clock()), daemon=True)
+    t.start()
+    t0 = time.perf_counter()
+    while t.is_alive() and time.perf_counter() - t0 < 40.0:
+        replay()
+    t.join(timeout=1.0)
+    return box or {"source": "amd-smi metric --clock", "error": "no reading"}
+
+
+# ---------------------------------------------------------------- the decode workloads
+
+
+def _time_graph(graph, stream, reps: int, warmup: int) -> float:
+    """ms per replay of ``graph`` over ``reps`` replays, HIP events on ``stream``."""
+    import torch
+
+    for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for _ in range(K):
+    for _ in range(reps):
         graph.replay()
     e1.record(stream)
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / K
-    assert torch.isfinite(out).all()
-    flop = 2 * 2 * D * HQ * (M * U + M * (M + 1) // 2)
-    nbytes = U * 2176 + 2 * M * HQ * D * 2 + 2 * M * HKV * D * 2  # codes + rulers, q + out, chunk K/V
-    tflops = flop / (ms / 1e3) / 1e12
-    res = {
-        "metric": "chunked-prefill attention over int8 KV: chunks/s, TFLOP/s, MFMA utilisation, GB/s",
-        "value": round(1e3 / ms, 2), "unit": "chunks/s", "n_gpus": 1, "steps": K, "warmup": W,
-        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp16", "data": "synthetic",
-        "config": {"workload": f"{M}-token fp16 chunk causally over a {U}-token int8t64 cache plus itself, "
-                               "32 q / 8 kv heads, head_dim 128", "chunk": M, "cache_tokens": U, "splits": splits},
-        "flop_per_step": flop,
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": None},
-        "gbs": round(nbytes / (ms / 1e3) / 1e9, 1),
-    }
-    print(json.dumps(res), flush=True)
-    return 0
+    return e0.elapsed_time(e1) / reps
 
 
-VOCAB_QWEN3_4B = 151936
-
-
-def cpu_baseline_e2e(budget_s: float, layer_shapes: list, lm_shape: tuple) -> dict:
-    """The decode step of the random-weight decoder on the host: one layer's projections as
-    fp32 torch matrix-vector products (all host threads) plus the numpy oracle's attention for
-    one layer at 32k context, scaled to 36 layers, plus the lm_head product."""
+def run_decode(args, scheme: str, headline: bool) -> dict:
+    """The 36-layer, 32k-context chained decode step on the int8t64 (``t64``) or per-token
+    symmetric (``tok``) cache; returns the result dict (the headline line when ``headline``)."""
     import torch
 
-    att = cpu_baseline(budget_s * 0.6, "t64")
-    per_layer_attn = att["seconds_per_step"] / LAYERS
-    g = torch.Generator().manual_seed(0)
-    ws = [torch.randn(*shp, generator=g) for shp in layer_shapes]
-    lm = torch.randn(*lm_shape, generator=g)
+    from nova_amd.kvattn import KVInt8Cache
+    from nova_amd.kvtok import KVInt8TokCache
 
-    def run(mats):
-        for w in mats:
-            torch.mv(w, torch.ones(w.shape[1]))
-
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        run(ws)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s * 0.3 or reps >= 50:
-            break
-    per_layer_mv = el / reps
-    t1 = time.perf_counter()
-    run([lm])
-    lm_s = time.perf_counter() - t1
-    per_step = LAYERS * (per_layer_mv + per_layer_attn) + lm_s
-    return {"value": 1.0 / per_step, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"one layer's projections as fp32 torch.mv ({reps} reps, {torch.get_num_threads()} threads) "
-                      f"+ {att['sample']} + the lm_head product once; scaled to {LAYERS} layers (extrapolated)"}
-
-
-def bench_e2e(args) -> int:
-    """End-to-end graph decode of the random-weight decoder with Qwen3-4B geometry (36 layers,
-    hidden 2560, 32 q / 8 KV heads of 128, SwiGLU 9728, vocab 151936, fp16 weights ~ N(0, 1/fan_in))
-    over the int8t64 KV cache: the prompt (seeded random ids, ``--ctx`` tokens) is prefilled in
-    streamed chunks, then each decode step (embed, 36 x [qkv GEMV + RMSNorm, q/k norm + RoPE,
-    fused int8 append + attention, o_proj + residual, SwiGLU gate/up + RMSNorm, down + residual],
-    final RMSNorm + lm_head, argmax, pos += 1) is one hipGraph replay. Each kernel is also timed
-    alone (a graph of its 36 launches per step with the same weights); ``roofline`` is the one
-    that takes the most time per step."""
-    import torch
-
-    from nova_amd import _lib
-    from nova_amd import gemv as G
-    from nova_amd.decode import GraphDecoder
-    from nova_amd.skeleton import SkeletonConfig, SkeletonForCausalLM
-
-    _lib.load()
     dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    L, ctx, W = args.layers, args.ctx, args.warmup
-    K = args.steps
-    cfg = SkeletonConfig(num_hidden_layers=L, vocab_size=VOCAB_QWEN3_4B)
-    model = SkeletonForCausalLM(cfg, seed=5, device=dev, dtype=torch.float16).eval()
-    model.use_decode_kernels(True)
-    max_len = -(-(ctx + 4 + W + K + 1) // 64) * 64
-    dec = GraphDecoder(model, max_len=max_len, quant="int8", device=dev)
+    L, ctx, W, K = args.layers, args.ctx, args.warmup, args.steps
+    max_len = -(-(ctx + 3 * (W + K) + 8) // 64) * 64
+    cls = KVInt8TokCache if scheme == "tok" else KVInt8Cache
+    cache = cls(num_slots=L, num_kv_heads=HKV, head_dim=D, max_len=max_len, num_q_heads=HQ, device=dev)
     if args.parts:
-        dec.cache.set_parts(args.parts)
-    ids = torch.randint(0, cfg.vocab_size, (1, ctx), generator=torch.Generator().manual_seed(6)).to(dev)
+        cache.set_parts(args.parts)
+
+    # ---- prefill: seeded N(0,1) K/V, 4 random K channels per head x8, quantized into the cache
+    gen = torch.Generator(device=dev).manual_seed(2)
+    cpu_gen = torch.Generator().manual_seed(3)
+    cache.begin_prefill(ctx)
+    cache.set_prefill_pos(0)
+    for layer in range(L):
+        k = torch.randn(1, HKV, ctx, D, generator=gen, device=dev)
+        for h in range(HKV):
+            ch = torch.randperm(D, generator=cpu_gen)[:4].to(dev)
+            k[0, h, :, ch] *= 8.0
+        v = torch.randn(1, HKV, ctx, D, generator=gen, device=dev)
+        cache.update(k.half(), v.half(), layer)
+        del k, v
+    cache.finish_prefill(ctx)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    dec.prefill(ids, chunk=args.chunk)
-    torch.cuda.synchronize()
-    prefill_s = time.perf_counter() - t0
-    dec.capture(warmup=3)
+
+    # ---- chained layers: layer l reads q / k / v from layer l-1's output buffer
+    outs = (torch.randn(L, 1, HQ, 1, D, generator=gen, device=dev) / D ** 0.5).half()
+
+    def layer_inputs(layer: int):
+        prev = outs[layer - 1]  # layer 0: the previous step's last layer
+        return prev[:, 0::HQ // HKV], prev[:, 1::HQ // HKV], prev
+
+    def launches():
+        for layer in range(L):
+            k, v, q = layer_inputs(layer)
+            cache.update_attend(k, v, q, layer, out=outs[layer])
+
+    def step():
+        launches()
+        cache.pos.add_(1)
+
     stream = torch.cuda.current_stream(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
     for _ in range(W):
-        dec.step()
+        graph.replay()
     torch.cuda.synchronize()
-    pos0 = int(dec.cache.pos.item())
+    pos0 = int(cache.pos.item())
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t_wall = time.perf_counter()
     e0.record(stream)
     for _ in range(K):
-        dec.step()
+        graph.replay()
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
     ms = e0.elapsed_time(e1)
-    assert int(dec.cache.pos.item()) == pos0 + K
-    assert torch.isfinite(dec.logits).all()
+    assert int(cache.pos.item()) == pos0 + K
+    assert torch.isfinite(outs).all()
 
-    # ---- algorithmic bytes of one step: every weight once, the attention's KV bytes, the append
-    layers = model.model.layers
-    lay0 = layers[0]
-    hid, inter = cfg.hidden_size, cfg.intermediate_size
-    w_layer = sum(t.numel() * 2 for t in (lay0.w_qkv, lay0.attn.o_proj.weight, lay0.w_gate_up,
-                                          lay0.mlp.down_proj.weight, lay0.norm, lay0.post_norm,
-                                          lay0.attn.q_norm, lay0.attn.k_norm))
-    w_head = model.lm_head.weight.numel() * 2 + hid * 2 + hid * 2  # lm_head, final norm, embedding row
-    us = [pos0 + i + 1 for i in range(K)]
-    kv_step = sum(attn_bytes(u) + APPEND_BYTES for u in us) / K * L
-    step_bytes = L * w_layer + w_head + kv_step
+    # ---- the fused launch alone: a graph of the step's 36 chained launches (pos fixed), timed
+    g_launch = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_launch):
+        launches()
+    pos_l = int(cache.pos.item())
+    ms_launches = _time_graph(g_launch, stream, K, W)
+    clock = None if args.no_clock else clock_under_load(graph.replay)
 
-    # ---- each kernel alone: a graph of its launches for one step, K replays
-    gen = torch.Generator(device=dev).manual_seed(7)
-    xh = torch.randn(hid, generator=gen, device=dev).half()
-    xa = torch.randn(cfg.num_attention_heads * cfg.head_dim, generator=gen, device=dev).half()
-    xi = torch.randn(inter, generator=gen, device=dev).half()
-    res = torch.randn(hid, generator=gen, device=dev).half()
-    o_h = torch.empty(hid, dtype=torch.float16, device=dev)
-    o_qkv = torch.empty(lay0.w_qkv.shape[0], dtype=torch.float16, device=dev)
-    o_i = torch.empty(inter, dtype=torch.float16, device=dev)
-    o_v = torch.empty(cfg.vocab_size, dtype=torch.float16, device=dev)
-    qkv = torch.randn(lay0.w_qkv.shape[0], generator=gen, device=dev).half()
-    pos = dec.cache.pos
-    inv = model.model.inv_freq32
-    hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    # ---- traffic calibration copy (known byte count; the --pmc runs read its counters)
+    cal = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)
+    cal2 = torch.empty_like(cal)
+    from nova_amd import _lib
 
-    def graph_of(fn, reps=1):
-        with torch.cuda.stream(stream):
-            fn()
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for _ in range(reps):
-                fn()
-        return g
-
-    def time_graph(g) -> float:
-        for _ in range(W):
-            g.replay()
-        torch.cuda.synchronize()
-        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s0.record(stream)
-        for _ in range(K):
-            g.replay()
-        s1.record(stream)
-        torch.cuda.synchronize()
-        return s0.elapsed_time(s1)
-
-    kv_in = torch.randn(2, 1, hkv, 1, d, generator=gen, device=dev).half()
-    q_in = (torch.randn(1, hq, 1, d, generator=gen, device=dev) / d ** 0.5).half()
-    kernels = {
-        "nkv_gemv qkv+RMSNorm": (lambda: [G.rms_gemv(xh, ly.w_qkv, ly.norm, cfg.rms_eps, out=o_qkv) for ly in layers],
-                                 lay0.w_qkv.numel() * 2, L),
-        "nkv_qk_norm_rope": (lambda: [G.qk_norm_rope_(qkv, hq, hkv, ly.attn.q_norm, ly.attn.k_norm, cfg.rms_eps, inv, pos)
-                                      for ly in layers], (hq + hkv) * d * 4, L),
-        "nkv_decode_step_t64": (lambda: [dec.cache.update_attend(kv_in[0], kv_in[1], q_in, i) for i in range(L)],
-                                sum(attn_bytes(u) + APPEND_BYTES for u in us) / K, L),
-        "nkv_gemv o_proj+residual": (lambda: [G.rms_gemv(xa, ly.attn.o_proj.weight, residual=res, out=o_h)
-                                              for ly in layers], ly_bytes(lay0.attn.o_proj.weight), L),
-        "nkv_swiglu_gemv gate/up+RMSNorm": (lambda: [G.swiglu_gemv(xh, ly.w_gate_up, ly.post_norm, cfg.rms_eps, out=o_i)
-                                                     for ly in layers], ly_bytes(lay0.w_gate_up), L),
-        "nkv_gemv down+residual": (lambda: [G.rms_gemv(xi, ly.mlp.down_proj.weight, residual=res, out=o_h)
-                                            for ly in layers], ly_bytes(lay0.mlp.down_proj.weight), L),
-        "nkv_gemv lm_head+RMSNorm": (lambda: G.rms_gemv(xh, model.lm_head.weight, model.model.norm, cfg.rms_eps,
-                                                        out=o_v), ly_bytes(model.lm_head.weight), 1),
-    }
-    saved = dec._save_int8_state()
-    breakdown = {}
-    for name, (fn, nbytes, launches) in kernels.items():
-        with torch.inference_mode():  # the decoder's state tensors are inference tensors
-            g = graph_of(fn)
-            t = time_graph(g) / K  # ms per step
-        del g
-        per_launch = t / launches / 1e3
-        breakdown[name] = {"launches_per_step": launches, "ms_per_step": round(t, 4),
-                           "avg_launch_us": round(per_launch * 1e6, 3),
-                           "algorithmic_bytes_per_launch": round(nbytes),
-                           "gbs": round(nbytes / per_launch / 1e9, 1)}
-    dec._restore_int8_state(saved)
-    top = max(breakdown, key=lambda n: breakdown[n]["ms_per_step"])
-    tb = breakdown[top]
+    _lib.call("nkv_copy_bytes", cal.data_ptr(), cal2.data_ptr(), cal.numel(), _lib.stream_ptr(dev))
+    torch.cuda.synchronize()
+    del cal, cal2
 
     ms_step = ms / K
-    out = {
-        "metric": "end-to-end graph-decode tokens/s, 36-layer Qwen3-4B-geometry decoder (random weights) "
-                  "over the int8 KV cache at 32k ctx",
+    us = [pos0 + i + 1 for i in range(K)]  # tokens written when each timed step attends
+    step_bytes = sum(step_launch_bytes(u, scheme) for u in us) / K * L
+    launch_bytes = step_launch_bytes(pos_l + 1, scheme)
+    per_launch_s = ms_launches / 1e3 / L
+    achieved = launch_bytes / per_launch_s / 1e9
+    fmt = ("tok (int8 codes, one fp16 absmax scale per token and KV head)" if scheme == "tok"
+           else "int8t64 (uint8 codes, fp16 min/step per 64 tokens per channel)")
+    res = {
+        "metric": "int8-KV decode attention tokens/s + achieved HBM GB/s (% of peak) at 32k ctx",
         "value": round(K / (ms / 1e3), 2), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp16", "data": "synthetic (random weights, random prompt ids)",
-        "config": {"workload": f"greedy decode, {L} layers x (hidden {hid}, 32 q / 8 kv heads x 128, SwiGLU {inter}), "
-                               f"vocab {cfg.vocab_size}, batch 1, int8t64 KV cache, {ctx}-token prompt prefilled in "
-                               f"{args.chunk}-token streamed chunks, {K} hipGraph-replayed steps",
-                   "layers": L, "context": ctx, "hidden": hid, "intermediate": inter, "vocab": cfg.vocab_size,
-                   "prefill_chunk": args.chunk, "parts_per_head": dec.cache._n_parts},
-        "algorithmic_bytes_per_step": round(step_bytes),
+        "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": f"{'per-token symmetric int8' if scheme == 'tok' else 'int8t64'} KV decode step, "
+                               f"{L} layers x (32 q / 8 kv heads, head_dim 128), batch 1, {ctx}-token prefilled "
+                               f"cache, layers chained through their outputs, {K} hipGraph-replayed steps",
+                   "layers": L, "context": ctx, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "batch": 1,
+                   "kv_format": fmt, "parts_per_head": cache._n_parts},
         "step_gbs": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
         "step_pct_of_hbm_peak": round(100 * step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS, 2),
-        "prefill_s": round(prefill_s, 3),
-        "prefill_tokens_per_s": round(ctx / prefill_s, 1),
         "wall_s_timed": round(wall, 4),
-        "roofline": {"bound": "hbm", "achieved": tb["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(tb["gbs"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": top,
-                     "algorithmic_bytes_per_launch": tb["algorithmic_bytes_per_launch"],
-                     "avg_launch_us": tb["avg_launch_us"]},
-        "kernels": breakdown,
-        "kernels_sum_ms_per_step": round(sum(b["ms_per_step"] for b in breakdown.values()), 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(scheme),
+                     "kernel": f"nkv::attn_prefix_kernel<{1 if scheme == 'tok' else 0}> fused decode step "
+                               "(append + split-K partials + last-workgroup tail), one launch per layer",
+                     "algorithmic_bytes_per_launch": round(launch_bytes),
+                     "avg_launch_us": round(per_launch_s * 1e6, 3),
+                     "launches_per_step": L},
+        "gpu_clock": clock,
     }
-    if not args.no_cpu_baseline:
-        shapes = [tuple(t.shape) for t in (lay0.w_qkv, lay0.attn.o_proj.weight, lay0.w_gate_up,
-                                           lay0.mlp.down_proj.weight)]
-        out["cpu_baseline"] = cpu_baseline_e2e(args.cpu_seconds, shapes, tuple(model.lm_head.weight.shape))
-    else:
-        out["cpu_baseline"] = None
-    print(json.dumps(out), flush=True)
-    return 0
+    del graph, g_launch, cache, outs
+    torch.cuda.empty_cache()
+    return res
 
 
-def ly_bytes(w) -> int:
-    return w.numel() * 2
-
-
-def bench_paged(args) -> int:
-    """Batched ragged decode: 8 sequences with seeded uniform lengths in [1024, 16384]
-    (seed 3), 36 layers, int8t64 pages of 64 tokens; one step = every layer's
-    append + attention for all 8 sequences, captured as one hipGraph. Prints one JSON line
-    (batch tokens/s; GB/s over the algorithmic bytes of the valid tokens, padding excluded)."""
+def run_paged(args, steps: int | None = None) -> dict:
+    """Batched ragged decode: 8 sequences with seeded uniform lengths in [1024, 16384] (seed 3),
+    36 layers, int8t64 pages of 64 tokens; one step = every layer's append + attention for all 8
+    sequences, captured as one hipGraph. Batch tokens/s; GB/s over the algorithmic bytes of the
+    valid tokens (padding excluded)."""
     import torch
 
-    from nova_amd import _lib
     from nova_amd.paged import PagedKVInt8Cache
 
-    _lib.load()
     dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    L, B = args.layers, 8
-    K = args.steps if args.steps != 256 else 128
-    W = args.warmup
-    gen = torch.Generator().manual_seed(3)
-    lens = [int(x) for x in torch.randint(1024, 16385, (B,), generator=gen)]
+    L, B, W = args.layers, 8, args.warmup
+    K = steps or 128
+    lens = [int(x) for x in torch.randint(1024, 16385, (B,), generator=torch.Generator().manual_seed(3))]
     per_seq = max(-(-(n + W + K + 2) // 64) for n in lens)
     total_pages = sum(-(-(n + W + K + 2) // 64) for n in lens)
     cache = PagedKVInt8Cache(L, HKV, D, HQ, max_seqs=B, num_pages=total_pages, max_pages_per_seq=per_seq, device=dev)
@@ -546,36 +449,139 @@ def bench_paged(args) -> int:
     stream = torch.cuda.current_stream(dev)
     for _ in range(W):
         graph.replay()
+    cache.note_advanced(W)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t_wall = time.perf_counter()
-    e0.record(stream)
-    for _ in range(K):
-        graph.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_wall
-    ms = e0.elapsed_time(e1)
+    ms = _time_graph(graph, stream, K, 0)
+    cache.note_advanced(K)
     assert torch.isfinite(cache.merged[:B]).all()
     step_bytes = sum(sum(attn_bytes(n + W + i + 1) + APPEND_BYTES for n in lens) for i in range(K)) / K * L
-    ms_step = ms / K
-    gbs = step_bytes / (ms_step / 1e3) / 1e9
-    out = {
-        "metric": "paged ragged batch int8-KV decode: batch tokens/s + achieved HBM GB/s (% of peak)",
-        "value": round(B * K / (ms / 1e3), 2),
-        "unit": "tokens/s",
-        "n_gpus": 1, "steps": K, "warmup": W, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
-        "config": {"workload": f"paged int8t64 decode, {B} ragged sequences (lengths {lens}), {L} layers x "
-                               "(32 q / 8 kv heads, head_dim 128), 64-token pages, hipGraph-replayed steps",
-                   "lengths": lens, "layers": L, "page_tokens": 64, "work_units_per_head": cache.total_parts},
-        "step_gbs": round(gbs, 1),
-        "step_pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-        "algorithmic_bytes_per_step": round(step_bytes),
-        "wall_s_timed": round(wall, 4),
-    }
-    print(json.dumps(out), flush=True)
-    return 0
+    gbs = step_bytes / (ms / 1e3) / 1e9
+    res = {"metric": "paged ragged batch int8-KV decode: batch tokens/s + achieved HBM GB/s (% of peak)",
+           "value": round(B / (ms / 1e3), 2), "unit": "tokens/s", "steps": K, "ms_per_step": round(ms, 4),
+           "config": {"workload": f"paged int8t64 decode, {B} ragged sequences (lengths {lens}), {L} layers x "
+                                  "(32 q / 8 kv heads, head_dim 128), 64-token pages, hipGraph-replayed steps",
+                      "lengths": lens, "layers": L, "page_tokens": 64, "work_units_per_head": cache.total_parts},
+           "step_gbs": round(gbs, 1), "step_pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+           "algorithmic_bytes_per_step": round(step_bytes)}
+    del graph, cache
+    torch.cuda.empty_cache()
+    return res
+
+
+def run_prefill(args, steps: int | None = None) -> dict:
+    """Chunked prefill over int8 KV: a 512-token fp16 query chunk attending causally to a
+    16384-token int8t64 cache plus itself, 32 q / 8 KV heads, head_dim 128 (seed 4). HIP events
+    over K graph replays of its two launches; TFLOP/s and MFMA utilisation against the dense
+    fp16 peak, GB/s."""
+    import torch
+
+    from nova_amd import _lib
+    from nova_amd.kvattn import int8_prefill_attend, pack_int8_kv
+
+    dev = torch.device("cuda:0")
+    M, U = 512, 16384
+    K, W = steps or 64, args.warmup
+    g = torch.Generator(device=dev).manual_seed(4)
+    k = torch.randn(1, HKV, U, D, generator=g, device=dev).half()
+    v = torch.randn(1, HKV, U, D, generator=g, device=dev).half()
+    packed = pack_int8_kv(k, v)
+    del k, v
+    q = torch.randn(1, HQ, M, D, generator=g, device=dev).half()
+    kc = torch.randn(1, HKV, M, D, generator=g, device=dev).half()
+    vc = torch.randn(1, HKV, M, D, generator=g, device=dev).half()
+    out = torch.empty_like(q)
+    lib = _lib.load()
+    splits = args.splits or int(lib.nkv_prefill_default_splits(HKV, HQ, M, U))
+    scratch = torch.empty(int(lib.nkv_prefill_workspace_bytes(HKV, HQ, M, splits)), dtype=torch.uint8, device=dev)
+    int8_prefill_attend(q, kc, vc, *packed, used=U, out=out, scratch=scratch, splits=splits)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        int8_prefill_attend(q, kc, vc, *packed, used=U, out=out, scratch=scratch, splits=splits)
+    ms = _time_graph(graph, torch.cuda.current_stream(dev), K, W)
+    assert torch.isfinite(out).all()
+    flop = 2 * 2 * D * HQ * (M * U + M * (M + 1) // 2)
+    nbytes = U * 2176 + 2 * M * HQ * D * 2 + 2 * M * HKV * D * 2  # codes + rulers, q + out, chunk K/V
+    tflops = flop / (ms / 1e3) / 1e12
+    return {"metric": "chunked-prefill attention over int8 KV: chunks/s, TFLOP/s, MFMA utilisation, GB/s",
+            "value": round(1e3 / ms, 2), "unit": "chunks/s", "steps": K, "ms_per_step": round(ms, 4),
+            "config": {"workload": f"{M}-token fp16 chunk causally over a {U}-token int8t64 cache plus itself, "
+                                   "32 q / 8 kv heads, head_dim 128", "chunk": M, "cache_tokens": U,
+                       "splits": splits},
+            "flop_per_step": flop,
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_FP16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": None},
+            "gbs": round(nbytes / (ms / 1e3) / 1e9, 1)}
+
+
+def _standalone(res: dict, args) -> dict:
+    """A workload's dict as its own contract line."""
+    out = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
+           "steps": res["steps"], "warmup": args.warmup, "ms_per_step": res["ms_per_step"],
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic"}
+    out.update({k: v for k, v in res.items() if k not in out})
+    return out
+
+
+# ---------------------------------------------------------------- end to end (random-weight decoder)
+
+
+def bench_e2e(args) -> dict:
+    """End-to-end graph decode of the random-weight decoder with Qwen3-4B geometry (36 layers,
+    hidden 2560, 32 q / 8 KV heads of 128, SwiGLU 9728, vocab 151936, fp16 weights) over the
+    int8t64 cache: the prompt (``--ctx`` random ids) is prefilled in streamed chunks, then each
+    step (embed, 36 x [qkv GEMV + RMSNorm, q/k norm + RoPE, fused int8 append + attention, o_proj +
+    residual, SwiGLU gate/up + RMSNorm, down + residual], final RMSNorm + lm_head, argmax,
+    pos += 1) is one hipGraph replay."""
+    import torch
+
+    from nova_amd.decode import GraphDecoder
+    from nova_amd.skeleton import SkeletonConfig, SkeletonForCausalLM
+
+    dev = torch.device("cuda:0")
+    L, ctx, W, K = args.layers, args.ctx, args.warmup, args.steps
+    cfg = SkeletonConfig(num_hidden_layers=L, vocab_size=VOCAB_QWEN3_4B)
+    model = SkeletonForCausalLM(cfg, seed=5, device=dev, dtype=torch.float16).eval()
+    model.use_decode_kernels(True)
+    max_len = -(-(ctx + 4 + W + K + 1) // 64) * 64
+    dec = GraphDecoder(model, max_len=max_len, quant="int8", device=dev)
+    if args.parts:
+        dec.cache.set_parts(args.parts)
+    ids = torch.randint(0, cfg.vocab_size, (1, ctx), generator=torch.Generator().manual_seed(6)).to(dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dec.prefill(ids, chunk=args.chunk)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    dec.capture(warmup=3)
+    for _ in range(W):
+        dec.step()
+    torch.cuda.synchronize()
+    pos0 = int(dec.cache.pos.item())
+    ms = _time_graph(dec.graph, torch.cuda.current_stream(dev), K, 0)
+    assert int(dec.cache.pos.item()) == pos0 + K
+    assert torch.isfinite(dec.logits).all()
+    lay0 = model.model.layers[0]
+    w_layer = sum(t.numel() * 2 for t in (lay0.w_qkv, lay0.attn.o_proj.weight, lay0.w_gate_up,
+                                          lay0.mlp.down_proj.weight, lay0.norm, lay0.post_norm,
+                                          lay0.attn.q_norm, lay0.attn.k_norm))
+    w_head = model.lm_head.weight.numel() * 2 + 4 * cfg.hidden_size
+    kv_step = sum(attn_bytes(pos0 + i + 1) + APPEND_BYTES for i in range(K)) / K * L
+    step_bytes = L * w_layer + w_head + kv_step
+    gbs = step_bytes / (ms / 1e3) / 1e9
+    return {"metric": "end-to-end graph-decode tokens/s, 36-layer Qwen3-4B-geometry decoder (random weights) "
+                      "over the int8 KV cache at 32k ctx",
+            "value": round(1e3 / ms, 2), "unit": "tokens/s", "steps": K, "ms_per_step": round(ms, 4),
+            "config": {"workload": f"greedy decode, {L} layers (hidden {cfg.hidden_size}, SwiGLU "
+                                   f"{cfg.intermediate_size}), vocab {cfg.vocab_size}, int8t64 KV, {ctx}-token "
+                                   f"prompt prefilled in {args.chunk}-token streamed chunks",
+                       "layers": L, "context": ctx, "prefill_chunk": args.chunk},
+            "algorithmic_bytes_per_step": round(step_bytes), "step_gbs": round(gbs, 1),
+            "step_pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2), "prefill_s": round(prefill_s, 3),
+            "prefill_tokens_per_s": round(ctx / prefill_s, 1)}
+
+
+# ---------------------------------------------------------------- main
 
 
 def main() -> int:
@@ -583,180 +589,44 @@ def main() -> int:
     if args.traffic_from:
         write_traffic(*args.traffic_from, scheme=args.scheme)
         return 0
-    if args.workload == "paged" and args.gpus == 1:
-        return bench_paged(args)
-    if args.workload == "prefill" and args.gpus == 1:
-        return bench_prefill(args)
-    if args.workload == "e2e" and args.gpus == 1:
-        return bench_e2e(args)
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported on this path "
-              "(the decode attention shards by KV head across GPUs; see the design notes)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not run here (the decode attention shards by "
+              "KV head across GPUs with no exchange; see the design notes)", file=sys.stderr)
         return 2
 
     import torch
 
     from nova_amd import _lib
-    from nova_amd.kvattn import KVInt8Cache
-    from nova_amd.kvtok import KVInt8TokCache
 
     _lib.load()
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    L, ctx, W, K = args.layers, args.ctx, args.warmup, args.steps
-    max_len = -(-(ctx + 3 * (W + K) + 1) // 64) * 64
-
-    # ---- prefill: seeded N(0,1) K/V, 4 random K channels per head x8, quantized by the
-    # bulk HIP quantizer into the cache (staging area -> finish_prefill)
-    tok = args.scheme == "tok"
-    cls = KVInt8TokCache if tok else KVInt8Cache
-    cache = cls(num_slots=L, num_kv_heads=HKV, head_dim=D, max_len=max_len, num_q_heads=HQ, device=dev)
-    if args.parts:
-        cache.set_parts(args.parts)
-    gen = torch.Generator(device=dev).manual_seed(2)
-    cpu_gen = torch.Generator().manual_seed(3)
-    cache.begin_prefill(ctx)
-    cache.set_prefill_pos(0)
-    for layer in range(L):
-        k = torch.randn(1, HKV, ctx, D, generator=gen, device=dev)
-        for h in range(HKV):
-            ch = torch.randperm(D, generator=cpu_gen)[:4].to(dev)
-            k[0, h, :, ch] *= 8.0
-        v = torch.randn(1, HKV, ctx, D, generator=gen, device=dev)
-        cache.update(k.half(), v.half(), layer)
-        del k, v
-    cache.finish_prefill(ctx)
-    torch.cuda.synchronize()
-
-    # ---- per-layer synthetic decode inputs (q ~ N(0,1)/sqrt(128))
-    qs = [(torch.randn(1, HQ, 1, D, generator=gen, device=dev) / D ** 0.5).half() for _ in range(L)]
-    ks = [torch.randn(1, HKV, 1, D, generator=gen, device=dev).half() for _ in range(L)]
-    vs = [torch.randn(1, HKV, 1, D, generator=gen, device=dev).half() for _ in range(L)]
-
-    def step():
-        for layer in range(L):
-            cache.update_attend(ks[layer], vs[layer], qs[layer], layer)
-        cache.pos.add_(1)
-
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
-    stream = torch.cuda.current_stream(dev)
-    for _ in range(W):
-        graph.replay()
-    torch.cuda.synchronize()
-    pos0 = int(cache.pos.item())
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_wall = time.perf_counter()
-    e0.record(stream)
-    for _ in range(K):
-        graph.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_wall
-    ms = e0.elapsed_time(e1)
-    assert int(cache.pos.item()) == pos0 + K
-    assert torch.isfinite(cache.merged).all()
-
-    # ---- each of the step's two kernels alone: a graph of its 36 launches per step (the
-    # same kernel and arguments as above), K replays timed with HIP events
-    def kernel_graph(entry: str, advance: bool):
-        args_per_layer = [cache.step_args(ks[layer], vs[layer], qs[layer], layer) for layer in range(L)]
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for a in args_per_layer:
-                _lib.call(entry, *a[:-1], _lib.stream_ptr(dev))
-            if advance:
-                cache.pos.add_(1)
-        return g, args_per_layer
-
-    def time_graph(g) -> float:
-        for _ in range(W):
-            g.replay()
-        torch.cuda.synchronize()
-        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s0.record(stream)
-        for _ in range(K):
-            g.replay()
-        s1.record(stream)
-        torch.cuda.synchronize()
-        return s0.elapsed_time(s1)
-
-    sfx = "tok" if tok else "t64"
-    g_prefix, keep = kernel_graph(f"nkv_decode_step_partials_{sfx}", True)
-    pos_a = int(cache.pos.item()) + W
-    ms_prefix = time_graph(g_prefix)
-    g_tail, keep2 = kernel_graph(f"nkv_decode_step_combine_{sfx}", False)
-    ms_tail = time_graph(g_tail)
-    del keep, keep2
-
-    # ---- traffic calibration copy (known byte count; read by the --pmc runs)
-    cal = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)
-    cal2 = torch.empty_like(cal)
-    _lib.call("nkv_copy_bytes", cal.data_ptr(), cal2.data_ptr(), cal.numel(), _lib.stream_ptr(dev))
-    torch.cuda.synchronize()
-
-    ms_step = ms / K
-    tok_s = K / (ms / 1e3)
-    us = [pos0 + i + 1 for i in range(K)]  # tokens written when each timed step attends
-    if tok:
-        step_bytes = sum(attn_bytes_tok(u) + APPEND_BYTES_TOK for u in us) / K * L
+    torch.cuda.set_device(0)
+    if args.workload == "paged":
+        res = _standalone(run_paged(args, args.steps if args.steps != 256 else None), args)
+    elif args.workload == "prefill":
+        res = _standalone(run_prefill(args, args.steps if args.steps != 256 else None), args)
+    elif args.workload == "e2e":
+        res = _standalone(bench_e2e(args), args)
     else:
-        step_bytes = sum(attn_bytes(u) + APPEND_BYTES for u in us) / K * L
-    ua = [pos_a + i + 1 for i in range(K)]  # the same for the prefix-kernel graph's replays
-    launch_bytes = sum((prefix_launch_bytes_tok if tok else prefix_launch_bytes)(u) for u in ua) / K
-    per_launch_s = ms_prefix / 1e3 / (K * L)
-    achieved = launch_bytes / per_launch_s / 1e9
-    traffic = read_traffic(TRAFFIC_FILE_TOK if tok else TRAFFIC_FILE)
-    out = {
-        "metric": "int8-KV decode attention tokens/s + achieved HBM GB/s (% of peak) at 32k ctx",
-        "value": round(tok_s, 2),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": K,
-        "warmup": W,
-        "ms_per_step": round(ms_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp16",
-        "data": "synthetic",
-        "config": {
-            "workload": f"{'per-token symmetric int8' if tok else 'int8t64'} KV decode step, {L} layers x "
-                        f"(32 q / 8 kv heads, head_dim 128), batch 1, "
-                        f"{ctx}-token prefilled cache, {K} hipGraph-replayed steps",
-            "layers": L, "context": ctx, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "batch": 1,
-            "kv_format": ("tok (int8 codes, one fp16 absmax scale per token and KV head)" if tok
-                          else "int8t64 (uint8 codes, fp16 min/step per 64 tokens per channel)"),
-            "parts_per_head": cache._n_parts,
-        },
-        "step_gbs": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
-        "step_pct_of_hbm_peak": round(100 * step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS, 2),
-        "wall_s_timed": round(wall, 4),
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "kernel": f"nkv::attn_prefix_kernel<{'true' if tok else 'false'}> (append + split-K partials over the int8 prefix)",
-            "algorithmic_bytes_per_launch": round(launch_bytes),
-            "avg_launch_us": round(per_launch_s * 1e6, 3),
-        },
-        "tail_kernel": {
-            "kernel": "nkv::attn_tail_kernel (ring attention + log-sum-exp combine)",
-            "avg_launch_us": round(ms_tail / (K * L) * 1e3, 3),
-        },
-    }
-    if not args.no_cpu_baseline:
-        cb = cpu_baseline(args.cpu_seconds, args.scheme)
-        cb.pop("seconds_per_step")
-        out["cpu_baseline"] = cb
-    else:
-        out["cpu_baseline"] = None
-    print(json.dumps(out), flush=True)
+        res = run_decode(args, args.scheme, headline=True)
+        if not args.no_cpu_baseline:
+            res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, args.scheme, args.ctx, args.layers)
+        else:
+            res["cpu_baseline"] = None
+        if args.workload is None and not args.only:
+            extra = {}
+            for name, fn in (("tok_decode", lambda: run_decode(args, "tok", headline=False)),
+                             ("paged_batch", lambda: run_paged(args)),
+                             ("chunked_prefill", lambda: run_prefill(args))):
+                try:
+                    extra[name] = fn()
+                except Exception as e:  # noqa: BLE001 - one extra workload failing must not hide the headline
+                    extra[name] = {"error": f"{type(e).__name__}: {e}"[:400]}
+            if "tok_decode" in extra and "error" not in extra["tok_decode"]:
+                t = extra["tok_decode"]
+                extra["tok_decode"] = {k: t[k] for k in ("value", "unit", "ms_per_step", "step_gbs",
+                                                         "step_pct_of_hbm_peak", "roofline", "config")}
+            res["workloads"] = extra
+    print(json.dumps(res), flush=True)
     return 0
 
 

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 3
+#define NKV_ABI_VERSION 4
 
 #define NKV_OK 0
 #define NKV_ERR_INVALID 1     /* argument outside what the reference accepts */
@@ -338,6 +338,21 @@ int nkv_prefill_attn_t64(const uint16_t* q, const uint16_t* k_chunk, const uint1
                          const uint16_t* vmn, const uint16_t* vst, int64_t capacity, int64_t used,
                          int64_t hq, int64_t hkv, int64_t head_dim, uint16_t* out, void* workspace,
                          int64_t workspace_bytes, int64_t splits, void* stream);
+
+/*
+ * The same attention with an fp16 history before the chunk: replaces the staged branch of
+ * KVInt8Cache.attend_prefill (src/nova/kvattn.py:791-815), where the prompt's earlier chunks
+ * are still fp16 in the staging area. k16 / v16 hold m_kv >= m fp16 tokens per KV head (head
+ * h's token j at k16 + h * kv_head_stride + j * 128); query token i (i < m) attends the int8
+ * tokens [0, used) and the fp16 tokens j <= (m_kv - m) + i. With m_kv == m and
+ * kv_head_stride == m * 128 this is nkv_prefill_attn_t64.
+ */
+int nkv_prefill_attn_hist_t64(const uint16_t* q, int64_t m, const uint16_t* k16, const uint16_t* v16,
+                              int64_t m_kv, int64_t kv_head_stride, const uint8_t* kq, const uint16_t* kmn,
+                              const uint16_t* kst, const uint8_t* vq, const uint16_t* vmn, const uint16_t* vst,
+                              int64_t capacity, int64_t used, int64_t hq, int64_t hkv, int64_t head_dim,
+                              uint16_t* out, void* workspace, int64_t workspace_bytes, int64_t splits,
+                              void* stream);
 
 /*
  * Plain device copy (16-byte vector loads and stores). Used to calibrate the

@@ -68,6 +68,8 @@ SIGNATURES = {
     "nkv_prefill_workspace_bytes": (I64, [I64, I64, I64, I64]),
     "nkv_prefill_default_splits": (I64, [I64, I64, I64, I64]),
     "nkv_prefill_attn_t64": (c_int, [P, P, P, I64, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, I64, I64, P]),
+    "nkv_prefill_attn_hist_t64": (c_int, [P, I64, P, P, I64, I64, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P,
+                                          I64, I64, P]),
     "nkv_copy_bytes": (c_int, [P, P, I64, P]),
     "nkv_read_bw": (c_int, [P, I64, P, I64, P]),
     "nkv_gemv": (c_int, [P, P, c_float, P, I64, I64, P, P, P]),
@@ -75,7 +77,7 @@ SIGNATURES = {
     "nkv_qk_norm_rope": (c_int, [P, I64, I64, I64, P, P, c_float, P, P, P]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib = None
 _lock = threading.Lock()
@@ -135,16 +137,24 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 _WORKSPACES: dict[str, torch.Tensor] = {}
+# Workspaces replaced by larger ones. A graph captured earlier may still hold a raw pointer
+# into one, so they stay allocated for the life of the process.
+_RETIRED: list[torch.Tensor] = []
 
 
 def workspace(device: torch.device, nbytes: int, kind: str = "scratch") -> torch.Tensor:
-    """A cached per-device, zero-filled byte workspace of at least ``nbytes`` (grown eagerly,
-    never inside capture). ``kind="decode"`` is the decode attention's own buffer: its last
-    bytes hold completion counters that every launch leaves at zero, so no other kernel may
-    write there; callers pass the whole buffer (``numel()`` bytes)."""
+    """A cached per-device, zero-filled byte workspace of at least ``nbytes``. It grows only
+    outside graph capture (a capture that needs more raises); the buffer it replaces is kept,
+    never freed, because a captured graph may point into it. Callers pass the whole buffer
+    (``numel()`` bytes)."""
     key = f"{device}/{kind}"
     w = _WORKSPACES.get(key)
     if w is None or w.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f"workspace '{kind}' must grow to {nbytes} bytes inside a graph capture; "
+                               "pass a preallocated scratch buffer")
+        if w is not None:
+            _RETIRED.append(w)
         w = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = w
     return w

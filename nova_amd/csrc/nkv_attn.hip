@@ -1504,8 +1504,11 @@ __global__ void ring_mask_kernel(const int64_t* written, const int64_t* qlen, co
 
 // ---------------------------------------------------------------- chunked prefill (MFMA)
 //
-// Causal attention of a chunk of M query tokens (positions U .. U + M - 1) over the int8t64
-// cache [0, U) (U a multiple of 64) and over the chunk's own fp16 K/V. Query rows of KV head
+// Causal attention of a chunk of M query tokens over the int8t64 cache [0, U) (U a multiple
+// of 64) and over Mk >= M fp16 K/V tokens that follow it: query token i sits at fp16 index
+// qoff + i (qoff = Mk - M) and attends fp16 tokens j <= qoff + i. With qoff = 0 the fp16
+// tokens are the chunk's own; with qoff > 0 they are an fp16 history plus the chunk (the
+// staged prefill, whose history is not quantized yet). Query rows of KV head
 // h: row r = (token r / gq, q head h gq + r % gq), M gq rows per head. Workgroup (h, tile,
 // split) takes rows 256 tile .. + 255 (8 waves x 2 MFMA row blocks of 16) and the split's
 // share of the 64-token groups: cache groups [split G / S, (split + 1) G / S) and chunk
@@ -1533,8 +1536,8 @@ __device__ __forceinline__ int pf_vslot(int t) {
 
 struct PrefillArgs {
   const uint16_t* q;   // [hq][M][D]
-  const uint16_t* kc;  // chunk K [hkv][M][D]
-  const uint16_t* vc;  // chunk V [hkv][M][D]
+  const uint16_t* kc;  // fp16 K: head h's token j at kc + h * kc_hs + j * D, j < Mk
+  const uint16_t* vc;  // fp16 V, the same layout
   const uint8_t* kq;
   const uint16_t* kmn;
   const uint16_t* kst;
@@ -1543,6 +1546,8 @@ struct PrefillArgs {
   const uint16_t* vst;
   int64_t capacity, ngroups_cap, U;
   int M, hq, hkv, gq, splits, tiles;
+  int Mk, qoff;    // fp16 tokens, and the fp16 index of query token 0
+  int64_t kc_hs;   // head stride of kc / vc (elements)
   float sl2;
   float* ws;       // [splits][hkv * M * gq][PF_PART]
   uint16_t* out;   // [hq][M][D]
@@ -1627,7 +1632,7 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
   const int64_t G = a.U / GT;
   const int64_t cs = (int64_t)split * G / a.splits, ce = (int64_t)(split + 1) * G / a.splits;
   const int last_tok = min(rows_h - 1, (tile + 1) * PF_ROWS - 1) / a.gq;  // last query token of the tile
-  const int nchunk = min((a.M + GT - 1) / GT, last_tok / GT + 1);
+  const int nchunk = min((a.Mk + GT - 1) / GT, (last_tok + a.qoff) / GT + 1);
 
   // cache group loads: wave w issues K and V code rows 8w .. 8w + 7 and half w & 1 of ruler
   // w >> 1 (kst, kmn, vst, vmn)
@@ -1671,7 +1676,7 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int kt = mask_base + 16 * b + 4 * g + i;
-          sc[b][i] = (mask_base < 0 || kt <= tq) ? S[rb][b][i] : NEG_INF;
+          sc[b][i] = (mask_base < 0 || kt <= tq + a.qoff) ? S[rb][b][i] : NEG_INF;
         }
       // rows of the S^T layout are q rows c; the causal test above needs the row of column
       // c, which is lane-independent of g: scores of lane (c, g) all belong to row c
@@ -1730,14 +1735,14 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
     attend_tiles(-1);
   }
 
-  // ---- chunk groups (fp16, causal): j = split, split + S, ...
+  // ---- fp16 groups (causal): j = split, split + S, ...
   for (int j = split; j < nchunk; j += a.splits) {
     __syncthreads();  // every wave is done with the tiles
     {
       const int row = tid >> 3, cp = tid & 7, t = GT * j + row;
-      const bool ok = t < a.M;
-      const uint16_t* kr = a.kc + ((int64_t)h * a.M + (ok ? t : 0)) * D + 16 * cp;
-      const uint16_t* vr = a.vc + ((int64_t)h * a.M + (ok ? t : 0)) * D + 16 * cp;
+      const bool ok = t < a.Mk;
+      const uint16_t* kr = a.kc + (int64_t)h * a.kc_hs + (int64_t)(ok ? t : 0) * D + 16 * cp;
+      const uint16_t* vr = a.vc + (int64_t)h * a.kc_hs + (int64_t)(ok ? t : 0) * D + 16 * cp;
       const int vs = pf_vslot(row);
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
@@ -2242,38 +2247,63 @@ extern "C" int64_t nkv_prefill_workspace_bytes(int64_t hkv, int64_t hq, int64_t 
   return splits * hq * m * PF_PART * (int64_t)sizeof(float);
 }
 
+static int prefill_attn(const char* what, const uint16_t* q, int64_t m, const uint16_t* k16, const uint16_t* v16,
+                        int64_t m_kv, int64_t kv_head_stride, const uint8_t* kq, const uint16_t* kmn,
+                        const uint16_t* kst, const uint8_t* vq, const uint16_t* vmn, const uint16_t* vst,
+                        int64_t capacity, int64_t used, int64_t hq, int64_t hkv, int64_t head_dim, uint16_t* out,
+                        void* workspace, int64_t workspace_bytes, int64_t splits, void* stream) {
+  set_error("");
+  if (int rc = check_heads(hq, hkv, head_dim)) return rc;
+  if (m <= 0 || m > (1 << 20)) return fail(NKV_ERR_INVALID, "%s: query length %lld", what, (long long)m);
+  if (m_kv < m || m_kv > (1 << 24))
+    return fail(NKV_ERR_INVALID, "%s: %lld fp16 tokens for %lld queries", what, (long long)m_kv, (long long)m);
+  if (kv_head_stride < m_kv * D || kv_head_stride % 8)
+    return fail(NKV_ERR_INVALID, "%s: fp16 K/V head stride %lld (need >= %lld, a multiple of 8)", what,
+                (long long)kv_head_stride, (long long)(m_kv * D));
+  if (used < 0 || used % GT || used > capacity)
+    return fail(NKV_ERR_INVALID, "%s: used=%lld must be a multiple of 64 within the capacity %lld", what,
+                (long long)used, (long long)capacity);
+  if (!q || !k16 || !v16 || !out || !workspace || (used > 0 && (!kq || !kmn || !kst || !vq || !vmn || !vst)))
+    return fail(NKV_ERR_INVALID, "%s: null pointer argument", what);
+  if (!al16(q) || !al16(k16) || !al16(v16) || !al16(out) || !al16(workspace) ||
+      (used > 0 && (!al16(kq) || !al16(vq) || !al16(kmn) || !al16(kst) || !al16(vmn) || !al16(vst))))
+    return fail(NKV_ERR_UNSUPPORTED, "%s: buffers must be 16-byte aligned", what);
+  const int64_t gq = hq / hkv, rows_h = m * gq, tiles = cdiv(rows_h, PF_ROWS);
+  if (splits <= 0) splits = nkv_prefill_default_splits(hkv, hq, m, used);
+  if (workspace_bytes < nkv_prefill_workspace_bytes(hkv, hq, m, splits))
+    return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes,
+                (long long)nkv_prefill_workspace_bytes(hkv, hq, m, splits));
+  PrefillArgs a{};
+  a.q = q; a.kc = k16; a.vc = v16;
+  a.kq = kq; a.kmn = kmn; a.kst = kst; a.vq = vq; a.vmn = vmn; a.vst = vst;
+  a.capacity = capacity; a.ngroups_cap = cdiv(capacity, GT); a.U = used;
+  a.M = (int)m; a.hq = (int)hq; a.hkv = (int)hkv; a.gq = (int)gq; a.splits = (int)splits; a.tiles = (int)tiles;
+  a.Mk = (int)m_kv; a.qoff = (int)(m_kv - m); a.kc_hs = kv_head_stride;
+  a.sl2 = LOG2E / sqrtf((float)head_dim);
+  a.ws = static_cast<float*>(workspace); a.out = out;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(prefill_chunk_kernel, dim3((unsigned)(hkv * tiles * splits)), dim3(PF_THREADS), 0, s, a);
+  if (int rc = check_launch(what)) return rc;
+  const int64_t items = hq * m * (D / 4);
+  hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)cdiv(items, 256)), dim3(256), 0, s, a);
+  return check_launch(what);
+}
+
 extern "C" int nkv_prefill_attn_t64(const uint16_t* q, const uint16_t* k_chunk, const uint16_t* v_chunk, int64_t m,
                                     const uint8_t* kq, const uint16_t* kmn, const uint16_t* kst, const uint8_t* vq,
                                     const uint16_t* vmn, const uint16_t* vst, int64_t capacity, int64_t used,
                                     int64_t hq, int64_t hkv, int64_t head_dim, uint16_t* out, void* workspace,
                                     int64_t workspace_bytes, int64_t splits, void* stream) {
-  set_error("");
-  if (int rc = check_heads(hq, hkv, head_dim)) return rc;
-  if (m <= 0 || m > (1 << 20)) return fail(NKV_ERR_INVALID, "prefill_attn: chunk length %lld", (long long)m);
-  if (used < 0 || used % GT || used > capacity)
-    return fail(NKV_ERR_INVALID, "prefill_attn: used=%lld must be a multiple of 64 within the capacity %lld",
-                (long long)used, (long long)capacity);
-  if (!q || !k_chunk || !v_chunk || !out || !workspace || (used > 0 && (!kq || !kmn || !kst || !vq || !vmn || !vst)))
-    return fail(NKV_ERR_INVALID, "prefill_attn: null pointer argument");
-  if (!al16(q) || !al16(k_chunk) || !al16(v_chunk) || !al16(out) || !al16(workspace) ||
-      (used > 0 && (!al16(kq) || !al16(vq) || !al16(kmn) || !al16(kst) || !al16(vmn) || !al16(vst))))
-    return fail(NKV_ERR_UNSUPPORTED, "prefill_attn: buffers must be 16-byte aligned");
-  const int64_t gq = hq / hkv, rows_h = m * gq, tiles = cdiv(rows_h, PF_ROWS);
-  if (splits <= 0) splits = nkv_prefill_default_splits(hkv, hq, m, used);
-  if (workspace_bytes < nkv_prefill_workspace_bytes(hkv, hq, m, splits))
-    return fail(NKV_ERR_INVALID, "prefill_attn: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
-                (long long)nkv_prefill_workspace_bytes(hkv, hq, m, splits));
-  PrefillArgs a{};
-  a.q = q; a.kc = k_chunk; a.vc = v_chunk;
-  a.kq = kq; a.kmn = kmn; a.kst = kst; a.vq = vq; a.vmn = vmn; a.vst = vst;
-  a.capacity = capacity; a.ngroups_cap = cdiv(capacity, GT); a.U = used;
-  a.M = (int)m; a.hq = (int)hq; a.hkv = (int)hkv; a.gq = (int)gq; a.splits = (int)splits; a.tiles = (int)tiles;
-  a.sl2 = LOG2E / sqrtf((float)head_dim);
-  a.ws = static_cast<float*>(workspace); a.out = out;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(prefill_chunk_kernel, dim3((unsigned)(hkv * tiles * splits)), dim3(PF_THREADS), 0, s, a);
-  if (int rc = check_launch("prefill_attn_t64")) return rc;
-  const int64_t items = hq * m * (D / 4);
-  hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)cdiv(items, 256)), dim3(256), 0, s, a);
-  return check_launch("prefill_attn_t64");
+  return prefill_attn("prefill_attn_t64", q, m, k_chunk, v_chunk, m, m * D, kq, kmn, kst, vq, vmn, vst, capacity,
+                      used, hq, hkv, head_dim, out, workspace, workspace_bytes, splits, stream);
+}
+
+extern "C" int nkv_prefill_attn_hist_t64(const uint16_t* q, int64_t m, const uint16_t* k16, const uint16_t* v16,
+                                         int64_t m_kv, int64_t kv_head_stride, const uint8_t* kq, const uint16_t* kmn,
+                                         const uint16_t* kst, const uint8_t* vq, const uint16_t* vmn,
+                                         const uint16_t* vst, int64_t capacity, int64_t used, int64_t hq, int64_t hkv,
+                                         int64_t head_dim, uint16_t* out, void* workspace, int64_t workspace_bytes,
+                                         int64_t splits, void* stream) {
+  return prefill_attn("prefill_attn_hist_t64", q, m, k16, v16, m_kv, kv_head_stride, kq, kmn, kst, vq, vmn, vst,
+                      capacity, used, hq, hkv, head_dim, out, workspace, workspace_bytes, splits, stream);
 }

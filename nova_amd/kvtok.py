@@ -248,20 +248,32 @@ class KVInt8TokCache:
                   _lib.stream_ptr(self.pos.device))
         return self.merged
 
-    def step_args(self, key: torch.Tensor, value: torch.Tensor, query: torch.Tensor, layer_idx: int) -> tuple:
+    def _output(self, out: torch.Tensor | None) -> torch.Tensor:
+        if out is None:
+            return self.merged
+        if (tuple(out.shape) != tuple(self.merged.shape) or out.dtype != self.dtype or not out.is_contiguous()
+                or out.data_ptr() % 16 or out.device != self.merged.device):
+            raise ValueError(f"out must be a contiguous, 16-byte aligned {self.dtype} tensor of shape "
+                             f"{tuple(self.merged.shape)} on {self.merged.device}")
+        return out
+
+    def step_args(self, key: torch.Tensor, value: torch.Tensor, query: torch.Tensor, layer_idx: int,
+                  out: torch.Tensor | None = None) -> tuple:
         """Arguments of ``nkv_decode_step_tok`` for one decode token of ``layer_idx``."""
         k, v, q = self._token(key, "key"), self._token(value, "value"), self._q(query)
+        o = self._output(out)
         return (q.data_ptr(), k.data_ptr(), v.data_ptr(), k.stride(1), self.kq[layer_idx].data_ptr(),
                 self.ksc[layer_idx].data_ptr(), self.vq[layer_idx].data_ptr(), self.vsc[layer_idx].data_ptr(),
                 self.pos.data_ptr(), self._written.data_ptr(), self.num_q_heads, self.num_kv_heads, self.head_dim,
-                self.max_len, self.merged.data_ptr(), self.lse.data_ptr(), self.pa.data_ptr(), self._ws_bytes,
+                self.max_len, o.data_ptr(), self.lse.data_ptr(), self.pa.data_ptr(), self._ws_bytes,
                 self._n_parts, _lib.stream_ptr(self.pos.device))
 
-    def update_attend(self, key: torch.Tensor, value: torch.Tensor, query: torch.Tensor,
-                      layer_idx: int) -> torch.Tensor:
-        """Append of the token at ``pos`` + attention over ``[0, pos]`` (two HIP launches)."""
-        _lib.call("nkv_decode_step_tok", *self.step_args(key, value, query, layer_idx))
-        return self.merged
+    def update_attend(self, key: torch.Tensor, value: torch.Tensor, query: torch.Tensor, layer_idx: int,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+        """Append of the token at ``pos`` + attention over ``[0, pos]`` in one launch; the output
+        goes to ``out`` when given, else to ``merged``."""
+        _lib.call("nkv_decode_step_tok", *self.step_args(key, value, query, layer_idx, out))
+        return self._output(out)
 
     def nbytes(self) -> int:
         """Resident KV bytes: codes and scales."""

@@ -159,6 +159,16 @@ class PagedKVInt8Cache:
 
     def advance(self) -> None:
         """``pos += 1`` for every planned sequence (device op, graph-safe)."""
+        self.note_advanced(1)
         self.pos[:self.nseq].add_(1)
+
+    def note_advanced(self, steps: int) -> None:
+        """Host bookkeeping of ``steps`` decode steps that advanced every planned sequence on the
+        device (``advance()``, or a replayed graph that adds to ``pos``). Raises when a sequence
+        would write past the pages reserved for it."""
         for b in range(self.nseq):
-            self._len[b] += 1
+            if (self._len[b] + steps) // GT >= len(self._owned[b]):
+                raise RuntimeError(f"sequence {b}: {steps} more steps reach token {self._len[b] + steps}, beyond "
+                                   f"its {len(self._owned[b])} reserved pages; reserve() more first")
+        for b in range(self.nseq):
+            self._len[b] += steps

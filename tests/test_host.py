@@ -108,3 +108,49 @@ def test_gemv_wrappers_refuse_cpu_tensors():
         G.swiglu_gemv(x, torch.zeros(16, 64, dtype=torch.float16))
     with pytest.raises(ValueError):
         G.qk_norm_rope_(torch.zeros(6 * 128, dtype=torch.float16), 4, 1, x, x, 1e-6, torch.zeros(64), torch.zeros(1))
+
+
+def test_capture_pool_choices():
+    """``capture(pool=...)`` takes the reference's choices (src/nova/decode.py:379-442): "off" and
+    None mean no pool, "auto"/"shared" the shared pool (registered), anything else passes through;
+    other strings are refused."""
+    import pytest
+
+    from nova_amd import decode as dec
+
+    assert dec.resolve_pool("off") == (None, False)
+    assert dec.resolve_pool(None) == (None, False)
+    handle = object()
+    assert dec.resolve_pool(handle) == (handle, False)
+    with pytest.raises(ValueError, match="pool"):
+        dec.resolve_pool("bogus")
+    # the shared-pool bookkeeping, with a stand-in for torch's handle
+    calls = []
+    reg = dec._PoolRegistry()
+    orig = torch.cuda.graph_pool_handle
+    torch.cuda.graph_pool_handle = lambda: calls.append(1) or ("pool", len(calls))
+    try:
+        a = reg.pool(fresh_if_idle=True)
+        assert reg.pool(fresh_if_idle=False) == a          # "shared": the same pool
+        b = reg.pool(fresh_if_idle=True)                    # "auto", no live user: a fresh pool
+        assert b != a
+
+        class G:  # a graph stand-in (weakly referenced)
+            pass
+
+        g = G()
+        reg.register(g)
+        assert reg.pool(fresh_if_idle=True) == b            # a live user keeps the pool
+        del g
+        assert reg.pool(fresh_if_idle=True) != b            # its graph is gone: fresh again
+    finally:
+        torch.cuda.graph_pool_handle = orig
+
+
+def test_mask_table_rows():
+    from nova_amd.decode import GraphDecoder
+
+    t = GraphDecoder._build_mask_table(5, torch.float16, "cpu")
+    lo = torch.finfo(torch.float16).min
+    for p in range(5):
+        assert all(float(t[p, j]) == (0.0 if j <= p else lo) for j in range(5))

@@ -356,3 +356,67 @@ def test_chunk_prefill_oracle_pinned():
     vqc, vmc, vsc = okq.quantize_int8_token(np.full_like(vc, 0.375), 64)
     const = oattn.chunk_prefill_attend(q, kq, kmn, kst, vqc, vmc, vsc, used, k_ch, vconst)
     np.testing.assert_allclose(const, np.full_like(const, 0.375), rtol=0, atol=1e-12)
+
+
+# ---------------------------------------------------------------- torch fp32 restatement (CPU baseline)
+
+
+@pytest.mark.parametrize("path", [p for p in QUANT_FILES if "tok64" in p.stem], ids=lambda p: p.stem)
+def test_torch_dequant_matches_reference_vectors(path):
+    """The CPU baseline's torch dequantization reproduces the reference's dequantized values
+    bit for bit (vectors written by the reference, replicate pad included)."""
+    from oracle import torch_ref
+
+    z = np.load(path)
+    got = torch_ref.dequantize_int8_token(torch.from_numpy(z["q"]), torch.from_numpy(z["mins"]),
+                                          torch.from_numpy(z["steps"]), 64)
+    np.testing.assert_array_equal(got.numpy().view(np.uint16), z["deq"].view(np.uint16))
+
+
+def test_torch_decode_step_matches_oracle_stream():
+    """The torch decode step (dequantized prefix + valid ring slots, GQA, fp32 softmax) equals
+    the numpy oracle's exact single softmax within one fp16 rounding, at a ring that straddles
+    a group boundary and with a nonzero ``first``."""
+    from oracle import torch_ref
+
+    rng = np.random.default_rng(11)
+    hq, hkv, d, n0 = 8, 2, 128, 150
+    sc = ostream.StreamCache(1, hkv, d, 256, hq)
+    k = (rng.standard_normal((hkv, n0 + 3, d)) * 0.7).astype(np.float16)
+    v = (rng.standard_normal((hkv, n0 + 3, d)) * 0.7).astype(np.float16)
+    sc.begin_prefill(n0)
+    sc.set_prefill_pos(0)
+    sc.update(k[:, :n0], v[:, :n0], 0)
+    sc.finish_prefill(n0)
+    for t in range(3):
+        sc.update(k[:, n0 + t:n0 + t + 1], v[:, n0 + t:n0 + t + 1], 0)
+        sc.pos += 1
+    q = (rng.standard_normal((hq, d)) * 0.7).astype(np.float16)
+    for first in (0, sc.written - 10):
+        sc.first = first
+        want = sc.attend_exact(q, 0).astype(np.float64)
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a))  # noqa: E731
+        got = torch_ref.decode_step_t64(t(q), t(sc.kq[0]), t(sc.kmn[0]), t(sc.kst[0]), t(sc.vq[0]), t(sc.vmn[0]),
+                                        t(sc.vst[0]), t(sc.tail_k[0]), t(sc.tail_v[0]), sc.written, first)
+        got = got.numpy().astype(np.float64)
+        spacing = np.abs(np.spacing(want.astype(np.float16)).astype(np.float64))
+        assert np.all(np.abs(got - want) <= 1.01 * spacing + 1e-7), float(np.abs(got - want).max())
+    # the ring mask agrees with the oracle's
+    assert np.array_equal(torch_ref.ring_mask(sc.written, sc.qlen, sc.first).numpy(), sc.ring_mask())
+
+
+def test_torch_tok_step_matches_oracle():
+    from oracle import torch_ref
+
+    rng = np.random.default_rng(12)
+    hq, hkv, d, n = 8, 2, 128, 77
+    x = (rng.standard_normal((hkv, n, d)) * 0.9).astype(np.float16)
+    y = (rng.standard_normal((hkv, n, d)) * 0.9).astype(np.float16)
+    kq, ks = okq.quantize_tok(x)
+    vq, vs = okq.quantize_tok(y)
+    q = (rng.standard_normal((hq, d)) * 0.7).astype(np.float16)
+    want, _ = oattn.tok_attn_decode(q, kq, ks, vq, vs, n)
+    t = torch.from_numpy
+    got = torch_ref.decode_step_tok(t(q), t(kq), t(ks), t(vq), t(vs), n).numpy()
+    spacing = np.abs(np.spacing(want.astype(np.float16)).astype(np.float64))
+    assert np.all(np.abs(got.astype(np.float64) - want.astype(np.float64)) <= 1.01 * spacing + 1e-7)
