@@ -281,22 +281,37 @@ int nkv_decode_step_combine_tok(const uint16_t* q, const uint16_t* k_new, const 
  * pages: uint8 [num_pages][hkv][17408], one page = one 64-token group of one KV head:
  *   K codes [64][128], V codes [64][128], then fp16 kst[128], kmn[128], vst[128], vmn[128].
  * page_table: int32 [nseq][table_stride], group g of sequence b lives in page
- *   page_table[b * table_stride + g] (the same ids in every layer's pool).
+ *   page_table[b * table_stride + g] (the same ids in every layer's pool); an entry outside
+ *   [0, num_pages), such as -1 for an unassigned slot, is no page: a sequence whose current group
+ *   (pos / 64) has no page neither appends nor attends (its output is 0, its lse -inf), and a
+ *   prefix group without a page reads page 0 rather than memory outside the pool.
  * rings: fp16 [nseq][hkv][2][64][128] (K then V; slot = position mod 64).
  * pos_dev: int64 [nseq], the position each sequence appends at this step.
  * k_new / v_new: [nseq][hkv][128] fp16 with strides kv_seq_stride / kv_head_stride.
  * Prefix work unit w (w < total_parts) serves sequence wg_map[w] >> 16, part
- * wg_map[w] & 0xffff of its seq_parts[2b + 1] parts; seq_parts[2b] is its first unit.
+ * wg_map[w] & 0xffff of its seq_parts[2b + 1] parts; seq_parts[2b] is its first unit. A sequence
+ * has at most 256 parts (the tail's merge holds 256 partials; it ignores partials beyond them).
  * q / out: [nseq][hq][128] fp16; lse_out [nseq][hq] fp32 (may be NULL).
  */
 int64_t nkv_paged_workspace_bytes(int64_t hkv, int64_t hq, int64_t total_parts);
+
+/* Whole groups of one sequence's prompt quantized straight into its pages (the int8t64
+ * arithmetic of nkv_quantize_int8, bit for bit): x [hkv][n][128] (head stride x_head_stride
+ * elements, NKV_F16 / NKV_BF16 / NKV_F32), n a multiple of 64; tokens 64 g .. 64 g + 63 of x form
+ * the sequence's group first_group + g, stored as tensor `which` (0 K, 1 V) of KV head h in page
+ * table_row[first_group + g] (codes and that tensor's two rulers). Groups whose entry is outside
+ * [0, num_pages) are skipped. Replaces the bulk quantize of KVInt8Cache.finish_prefill
+ * (src/nova/kvattn.py:745-783) for a paged cache; the reference has no paged layout. */
+int nkv_paged_quantize_t64(const void* x, int x_dtype, int64_t x_head_stride, int64_t hkv, int64_t n, int which,
+                           uint8_t* pages, const int32_t* table_row, int64_t first_group, int64_t num_pages,
+                           void* stream);
 
 /* Append of one token per sequence: ring slot pos % 64, requantization of the ring into
  * the sequence's page of group pos / 64 (which must be assigned). */
 int nkv_paged_append_t64(const uint16_t* k_new, const uint16_t* v_new, int64_t kv_seq_stride,
                          int64_t kv_head_stride, uint8_t* pages, const int32_t* page_table,
-                         int64_t table_stride, uint16_t* rings, const int64_t* pos_dev, int64_t nseq,
-                         int64_t hkv, int64_t head_dim, void* stream);
+                         int64_t table_stride, int64_t num_pages, uint16_t* rings, const int64_t* pos_dev,
+                         int64_t nseq, int64_t hkv, int64_t head_dim, void* stream);
 
 /* Decode attention of every sequence over its whole groups before pos and its ring
  * (tokens up to and including pos). One launch of the prefix kernel (total_parts * hkv
@@ -304,8 +319,8 @@ int nkv_paged_append_t64(const uint16_t* k_new, const uint16_t* v_new, int64_t k
  * zero-filled before its first use, >= nkv_paged_workspace_bytes bytes, its last bytes
  * hold the completion counters (left at zero by every call). */
 int nkv_paged_attn_decode_t64(const uint16_t* q, const uint8_t* pages, const int32_t* page_table,
-                              int64_t table_stride, const uint16_t* rings, const int64_t* pos_dev,
-                              int64_t nseq, int64_t hq, int64_t hkv, int64_t head_dim,
+                              int64_t table_stride, int64_t num_pages, const uint16_t* rings,
+                              const int64_t* pos_dev, int64_t nseq, int64_t hq, int64_t hkv, int64_t head_dim,
                               const int32_t* wg_map, const int32_t* seq_parts, int64_t total_parts,
                               uint16_t* out, float* lse_out, void* workspace, int64_t workspace_bytes,
                               void* stream);
@@ -313,8 +328,8 @@ int nkv_paged_attn_decode_t64(const uint16_t* q, const uint8_t* pages, const int
 /* nkv_paged_append_t64 then nkv_paged_attn_decode_t64 (two launches). */
 int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                               int64_t kv_seq_stride, int64_t kv_head_stride, uint8_t* pages,
-                              const int32_t* page_table, int64_t table_stride, uint16_t* rings,
-                              const int64_t* pos_dev, int64_t nseq, int64_t hq, int64_t hkv,
+                              const int32_t* page_table, int64_t table_stride, int64_t num_pages,
+                              uint16_t* rings, const int64_t* pos_dev, int64_t nseq, int64_t hq, int64_t hkv,
                               int64_t head_dim, const int32_t* wg_map, const int32_t* seq_parts,
                               int64_t total_parts, uint16_t* out, float* lse_out, void* workspace,
                               int64_t workspace_bytes, void* stream);

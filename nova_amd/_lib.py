@@ -61,10 +61,11 @@ SIGNATURES = {
     "nkv_decode_step_partials_tok": (c_int, _STEP_TOK),
     "nkv_decode_step_combine_tok": (c_int, _STEP_TOK),
     "nkv_paged_workspace_bytes": (I64, [I64, I64, I64]),
-    "nkv_paged_append_t64": (c_int, [P, P, I64, I64, P, P, I64, P, P, I64, I64, I64, P]),
-    "nkv_paged_attn_decode_t64": (c_int, [P, P, P, I64, P, P, I64, I64, I64, I64, P, P, I64, P, P, P, I64, P]),
-    "nkv_paged_decode_step_t64": (c_int, [P, P, P, I64, I64, P, P, I64, P, P, I64, I64, I64, I64, P, P, I64, P, P,
-                                          P, I64, P]),
+    "nkv_paged_quantize_t64": (c_int, [P, c_int, I64, I64, I64, c_int, P, P, I64, I64, P]),
+    "nkv_paged_append_t64": (c_int, [P, P, I64, I64, P, P, I64, I64, P, P, I64, I64, I64, P]),
+    "nkv_paged_attn_decode_t64": (c_int, [P, P, P, I64, I64, P, P, I64, I64, I64, I64, P, P, I64, P, P, P, I64, P]),
+    "nkv_paged_decode_step_t64": (c_int, [P, P, P, I64, I64, P, P, I64, I64, P, P, I64, I64, I64, I64, P, P, I64, P,
+                                          P, P, I64, P]),
     "nkv_prefill_workspace_bytes": (I64, [I64, I64, I64, I64]),
     "nkv_prefill_default_splits": (I64, [I64, I64, I64, I64]),
     "nkv_prefill_attn_t64": (c_int, [P, P, P, I64, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, I64, I64, P]),

@@ -115,6 +115,7 @@ struct AttnArgs {
   uint8_t* pages;
   const int32_t* table;
   int64_t table_stride;
+  int64_t num_pages;   // page ids outside [0, num_pages) (e.g. -1, unassigned) are no page
   uint16_t* rings;
   const int32_t* wg_map;
   const int32_t* seq_parts;
@@ -304,14 +305,24 @@ __device__ __forceinline__ void issue_half_tok(const AttnArgs& a, int h, int64_t
   if (lane < 4) dma16_stream(uniform_ptr(a.vsc + (int64_t)h * a.capacity + t0), 16u * lane, slot + 2 * HALF_CODE + TOK_SCALE_BYTES);
 }
 
+// Page of group `grp` of sequence b, or -1 when the table has no valid page there (an entry
+// outside [0, num_pages), such as the -1 of an unassigned or released slot).
+__device__ __forceinline__ int64_t page_of(const AttnArgs& a, int b, int64_t grp) {
+  if (grp < 0 || grp >= a.table_stride) return -1;
+  const int32_t page = a.table[(int64_t)b * a.table_stride + grp];
+  return page >= 0 && page < a.num_pages ? page : -1;
+}
+
 // The paged layout's half group: the group's page holds K code rows, V code rows and the
 // four rulers contiguously; 4 + 4 loads of code rows and, with hf == 0, one 1 KiB load of
 // the rulers (kst | kmn | vst | vmn, the order of a ruler set in LDS).
 __device__ __forceinline__ void issue_half_paged(const AttnArgs& a, int b, int h, int64_t grp, int hf, uint32_t slot,
                                                  uint32_t rs) {
   const int lane = threadIdx.x & 63;
-  const int32_t page = a.table[(int64_t)b * a.table_stride + grp];
-  const uint8_t* base = a.pages + ((int64_t)page * a.hkv + h) * PAGE_BYTES;
+  // a prefix group's page is valid whenever the current group's is (pages are reserved from
+  // group 0 up); should the table say otherwise, page 0 is read rather than memory outside the pool
+  const int64_t page = max<int64_t>(page_of(a, b, grp), 0);
+  const uint8_t* base = a.pages + (page * a.hkv + h) * PAGE_BYTES;
   const void* pb = uniform_ptr(base);
   slot = __builtin_amdgcn_readfirstlane(slot);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // earlier reads of this slot are done
@@ -697,30 +708,6 @@ __device__ __forceinline__ float min4rows(float v) {
   return fminf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-// One quarter (16 rows) of one ring tensor as one wave holds it: lanes (l & 15) own 8
-// channels, lanes (l >> 4) own rows 16 qtr + (l >> 4) + 4i, i < 4. Rows at or beyond
-// `slots` repeat the last one (never attended).
-struct RingQuarter {
-  uint4 rows[4];
-};
-
-__device__ __forceinline__ void ring_load_quarter(const uint16_t* ring_h, int slots, int qtr, RingQuarter& rq) {
-  const int lane = threadIdx.x & 63, cl = lane & 15, rl = lane >> 4;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    rq.rows[i] = *reinterpret_cast<const uint4*>(ring_h + min(16 * qtr + rl + 4 * i, slots - 1) * D + 8 * cl);
-}
-
-// The quarter's rows as the ring attention reads them: into the LDS ring buffer.
-__device__ __forceinline__ void ring_quarter_to_lds(const uint4 (&rows)[4], int qtr, uint8_t* ring_lds) {
-  const int lane = threadIdx.x & 63, cl = lane & 15, rl = lane >> 4;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 16 * qtr + rl + 4 * i;
-    *reinterpret_cast<uint4*>(ring_lds + r * (2 * D) + (ring_chunk_pos(r, cl) << 4)) = rows[i];
-  }
-}
-
 __device__ __forceinline__ const uint16_t* ring_of(const AttnArgs& a, int h, int which) {
   return (which == 0 ? a.tail_k : a.tail_v) + (int64_t)h * a.tail_slots * D;
 }
@@ -804,8 +791,8 @@ __device__ __forceinline__ UnitIO unit_io(const AttnArgs& a, int h, int unit, in
 // A unit of the paged layout: sequence b's ring and page of the current group.
 __device__ __forceinline__ UnitIO unit_io_paged(const AttnArgs& a, int b, int h, int unit, int64_t pos) {
   const int which = unit / (D / UNIT_CH);
-  const int32_t page = a.table[(int64_t)b * a.table_stride + pos / GT];
-  uint8_t* base = a.pages + ((int64_t)page * a.hkv + h) * PAGE_BYTES;
+  const int64_t page = page_of(a, b, pos / GT);  // checked >= 0 by the caller
+  uint8_t* base = a.pages + (page * a.hkv + h) * PAGE_BYTES;
   UnitIO io;
   io.ring = a.rings + (((int64_t)b * a.hkv + h) * 2 + which) * GT * D;
   io.fresh = (which == 0 ? a.k_new : a.v_new) + (int64_t)b * a.kv_ss + (int64_t)h * a.kv_hs;
@@ -1019,7 +1006,11 @@ struct TailSmem {
   float wts[TB_WAVES * WTS];                 // prefix merge weights, per merging wave
   float pre_acc[16 * D];                     // prefix: sum_s w_s acc_s per column
   float pre_m[16], pre_l[16];                // per head: m_p, l_p
+  float rq_ext[2][2 * D];                    // local requantization: per channel min / max of two half rings
+  int incomplete;                            // the merger gave up waiting for a partial
 };
+constexpr int MERGER_MAX_PARTS = 64;         // partials one merging wave tracks in a 64-bit ballot
+constexpr int MERGER_SPIN_LIMIT = 1 << 22;   // polls (each followed by a short sleep) before giving up
 static_assert(sizeof(TailSmem) <= LDS_BYTES && sizeof(TailSmem) <= LDS_BYTES_TOK,
               "the tail's LDS fits in the prefix kernel's stages");
 
@@ -1049,125 +1040,169 @@ __device__ __forceinline__ uint16_t ld_u16(const uint16_t* p, bool co) {
   return co ? __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *p;
 }
 
+// Publication area of the fused step, in the workspace's last bytes: one counter per head
+// (paged: per sequence and head) at tail_ctr_end[-1 - i], and for the contiguous layouts one flag
+// per prefix partial below the counters. Every launch leaves all of them at zero.
+__device__ __forceinline__ int* partial_flags(const AttnArgs& a, int h) {
+  return a.tail_ctr_end - a.hkv - (int64_t)(h + 1) * a.n_parts;
+}
+
+// The ring held in LDS (64 rows of K, then of V; ring_chunk_pos layout) requantized in place as
+// one int8t64 group, exactly as the append rules the group the new token completes: per channel
+// min / max over the 64 rows, step = max((max - min) / 255, 1e-8), codes by ruler_code_rcp,
+// then the values the prefix kernel would read back, fp16(code * step16 + min16) with one
+// rounding. Thread t takes channel t & 255 (K, then V) and rows 32 (t >> 8) .. + 31.
+__device__ __forceinline__ void requant_ring_lds(uint8_t* ring_lds, float (&ext)[2][2 * D]) {
+  const int t = threadIdx.x, ch = t & (2 * D - 1), half = t >> 8;
+  uint8_t* base = ring_lds + (ch >> 7) * RING_BYTES;
+  const int c = ch & (D - 1);
+  float v[32];
+  float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const int r = 32 * half + i;
+    v[i] = h2f(*reinterpret_cast<const uint16_t*>(base + r * (2 * D) + (ring_chunk_pos(r, c >> 3) << 4) + 2 * (c & 7)));
+    mn = fminf(mn, v[i]);
+    mx = fmaxf(mx, v[i]);
+  }
+  // the two halves' extremes meet in `ext` (row = half): first the minima, then the maxima
+  ext[half][ch] = mn;
+  __syncthreads();
+  const float lo = fminf(ext[0][ch], ext[1][ch]);
+  __syncthreads();
+  ext[half][ch] = mx;
+  __syncthreads();
+  const float hi = fmaxf(ext[0][ch], ext[1][ch]);
+  const float step = ruler_step(lo, hi), inv = ruler_inv(step);
+  const half2_t st2 = half2_t{(_Float16)step, (_Float16)step};
+  const half2_t mn2 = half2_t{(_Float16)lo, (_Float16)lo};
+#pragma unroll
+  for (int i = 0; i < 32; i += 2) {
+    const half2_t code = half2_t{(_Float16)(float)ruler_code_rcp(v[i], lo, step, inv),
+                                 (_Float16)(float)ruler_code_rcp(v[i + 1], lo, step, inv)};
+    const half2_t y = __builtin_elementwise_fma(code, st2, mn2);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int r = 32 * half + i + e;
+      *reinterpret_cast<_Float16*>(base + r * (2 * D) + (ring_chunk_pos(r, c >> 3) << 4) + 2 * (c & 7)) = y[e];
+    }
+  }
+}
+
 // The tail of one decode step for KV head h (of sequence b when paged), by the 8 waves of the
 // calling workgroup. The prefix partials merge into (m_p, l_p, acc_p): m_p = max_s m_s,
 // w_s = 2^(m_s - m_p), l_p = sum_s w_s l_s, acc_p = sum_s w_s acc_s (waves 4..7, one head
 // each, two columns per lane); meanwhile waves 0..3 attend over the ring, one partial of 16
-// tokens each; the ring's partials then join by log-sum-exp into out / lse. One round of
-// loads up front: the ring (or the completed group, or the new token), q, and each merging
-// wave's m / l and columns of the first MERGE_PRE partials.
+// tokens each; the ring's partials then join by log-sum-exp into out / lse.
 //
-// `inl`: run by the last prefix workgroup of the head inside the fused launch. The partials,
-// the codes of a completed group and a new per-token symmetric token were then written in
-// this launch by other workgroups with agent-scope stores and are read with agent-scope
-// loads; the ring slot of the new token is taken from k_new / v_new (this launch's append
-// writes it concurrently), every other slot was written by earlier launches.
+// The ring: the 64 fp16 slots of earlier launches, with the new token's slot taken from k_new /
+// v_new in the fused step (this launch's append writes that slot concurrently). When the new
+// token completes its group, the group is read as int8, as the prefix will read it: the ring is
+// requantized and dequantized here, bit for bit as the append computes it. In the per-token
+// symmetric format the new token alone is the tail, quantized here as the append quantizes it.
+// So the tail reads nothing that this launch writes except the partials.
+//
+// `poll`: run inside the fused launch by the head's merger, while other workgroups may still be
+// computing their partials. Each merging wave polls the partials' flags with relaxed agent-scope
+// loads (sleeping between polls, giving up after MERGER_SPIN_LIMIT polls), then takes one
+// agent-scope acquire and loads the partials; the producers publish each flag after an
+// agent-scope release. The merge runs in partial order, so the result does not depend on the
+// order of arrival. (An acquire per batch of newly set flags, to load early partials while
+// waiting for late ones, measured 0.6 us slower per launch: each acquire invalidates the L2.)
+// Without `poll` (the separate tail kernel) the launch boundary orders the partials before the
+// tail.
+enum TailRun : int { TAIL_KERNEL = 0, TAIL_LAST = 1, TAIL_MERGER = 2 };
+
 template <bool PAGED>
-__device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailSmem& sm, bool inl, int64_t pos,
+__device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailSmem& sm, int run, int64_t pos,
                                           bool pos_ok, int64_t U) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const bool poll = run == TAIL_MERGER;
+  const bool co = run != TAIL_KERNEL;  // partials written in this launch: agent-scope loads
   const int gq = a.gq, pw = part_stride(gq), cols = gq * D;
-  const int P = PAGED ? a.seq_parts[2 * b + 1] : a.n_parts;
+  const int P = PAGED ? min(a.seq_parts[2 * b + 1], WTS) : a.n_parts;
   const bool fused = PAGED || a.tail_mode == TAIL_FUSED;
-
   const bool ring = (PAGED || a.tail_mode != TAIL_NONE) && (!fused || pos_ok);
-  const bool ring_phase = ring;
   const float* hws = PAGED ? a.ws + ((int64_t)h * a.total_parts + a.seq_parts[2 * b]) * pw : a.ws + (int64_t)h * P * pw;
   // while waves 0..3 attend over the ring, the others merge the prefix partials
-  const int mbase = ring_phase ? RING_PARTS : 0, nmw = TB_WAVES - mbase;
+  const int mbase = ring ? RING_PARTS : 0, nmw = TB_WAVES - mbase;
 
-  // ---- loads
+  // ---- loads: the ring quarters (or the new token), q, the merging waves' partial columns
   const int which = wave >> 2, qtr = wave & 3;
-  const bool completes = fused && pos_ok && !a.tok && (pos + 1) % GT == 0;  // the token completed its group
-  const bool tok1 = !PAGED && ring_phase && a.tok;  // per-token symmetric fused step: the tail is the new token
+  const bool completes = fused && pos_ok && !a.tok && (pos + 1) % GT == 0;  // the token completes its group
+  const bool tok1 = !PAGED && ring && a.tok;  // per-token symmetric fused step: the tail is the new token
   const uint16_t* ring_h = PAGED ? a.rings + (((int64_t)b * a.hkv + h) * 2 + which) * GT * D : ring_of(a, h, which);
-  RingQuarter rq;
-  // the new token's slot: from the step's input, not the ring this launch writes. Loaded
-  // into registers of its own and stored over its row once the quarter is in LDS: replacing
-  // a row whose load is still in flight would make every later load wait for it.
-  // (`fresh` is read only when fresh_on, which implies the block that loads it; a value on
-  // the other path would cost a merge copy, and with it a wait for the load)
-  const bool fresh_on = ring_phase && !completes && !tok1 && inl && !PAGED && a.tail_mode == TAIL_FUSED;
+  const bool fresh_on = ring && !tok1 && !PAGED && a.tail_mode == TAIL_FUSED;
   const int fresh_slot = (int)(pos % GT);
-  uint4 fresh;
-  if (ring_phase && !completes && !tok1) {
-    ring_load_quarter(ring_h, PAGED ? GT : (int)a.tail_slots, qtr, rq);
+  uint4 rq0 = {0u, 0u, 0u, 0u}, rq1 = rq0, rq2 = rq0, rq3 = rq0;  // rows 16 qtr + (lane >> 4) + 4 i
+  uint4 fresh = rq0;
+  if (ring && !tok1) {
+    const int slots = PAGED ? GT : (int)a.tail_slots, cl = lane & 15, rl = lane >> 4;
+    rq0 = *reinterpret_cast<const uint4*>(ring_h + min(16 * qtr + rl, slots - 1) * D + 8 * cl);
+    rq1 = *reinterpret_cast<const uint4*>(ring_h + min(16 * qtr + rl + 4, slots - 1) * D + 8 * cl);
+    rq2 = *reinterpret_cast<const uint4*>(ring_h + min(16 * qtr + rl + 8, slots - 1) * D + 8 * cl);
+    rq3 = *reinterpret_cast<const uint4*>(ring_h + min(16 * qtr + rl + 12, slots - 1) * D + 8 * cl);
+    // the new token's slot: from the step's input, not the ring this launch writes. Loaded into
+    // registers of its own and stored over its row once the quarter is in LDS.
     const uint16_t* fp = fresh_on ? fresh_of(a, h, which) : ring_h;  // a valid row either way
     fresh = *reinterpret_cast<const uint4*>(fp + 8 * (lane & 15));
   }
-  uint2 tw = {0u, 0u};
-  uint16_t tsc = 0;
-  if (tok1 && qtr == 0 && lane < 16) {
-    const int64_t row = (int64_t)h * a.capacity + pos;
-    tw = ld_u2((which == 0 ? a.kq : a.vq) + row * D + 8 * lane, inl);
-    tsc = ld_u16((which == 0 ? a.ksc : a.vsc) + row, inl);
-  }
-  uint2 cw[4];
-  uint4 cst, cmn;
-  if (ring_phase && completes) {
-    const int64_t gcur = pos / GT;
-    const uint8_t* codes;
-    const uint16_t *gst, *gmn;
-    if constexpr (PAGED) {
-      const uint8_t* base = a.pages + ((int64_t)a.table[(int64_t)b * a.table_stride + gcur] * a.hkv + h) * PAGE_BYTES;
-      codes = base + which * CODE_BYTES;
-      gst = reinterpret_cast<const uint16_t*>(base + 2 * CODE_BYTES) + which * 2 * D;
-      gmn = gst + D;
-    } else {
-      const int64_t ro = ((int64_t)h * a.ngroups_cap + gcur) * D;
-      codes = (which == 0 ? a.kq : a.vq) + ((int64_t)h * a.capacity + gcur * GT) * D;
-      gst = (which == 0 ? a.kst : a.vst) + ro;
-      gmn = (which == 0 ? a.kmn : a.vmn) + ro;
-    }
-    const bool co = inl && !PAGED;
-    codes += 8 * (lane & 15);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) cw[i] = ld_u2(codes + (16 * qtr + (lane >> 4) + 4 * i) * D, co);
-    cst = ld_u4(gst + 8 * (lane & 15), co);
-    cmn = ld_u4(gmn + 8 * (lane & 15), co);
-  }
+  uint4 tokw = {0u, 0u, 0u, 0u};
+  if (tok1 && qtr == 0 && lane < 16) tokw = *reinterpret_cast<const uint4*>(fresh_of(a, h, which) + 8 * lane);
   const int64_t first = (!PAGED && ring && a.first_dev) ? *a.first_dev : 0;
-  const bool mask_on = ring_phase && a.tail_mode == TAIL_MASK && lane < a.tail_slots && a.tail_mask[lane] != 0;
+  const bool mask_on = ring && a.tail_mode == TAIL_MASK && lane < a.tail_slots && a.tail_mask[lane] != 0;
   half8_t qb[4];
   const int64_t qh0 = (int64_t)b * a.hq + h * gq;  // first query head of this workgroup
-  if (ring_phase && wave < RING_PARTS) load_q(a.q + qh0 * D, gq, qb);
+  if (ring && wave < RING_PARTS) load_q(a.q + qh0 * D, gq, qb);
   const int head0 = wave - mbase;
+  const bool merging = head0 >= 0 && head0 < gq;
   float mm = NEG_INF, ll = 0.0f;  // merging wave: lane s's m / l of its first head
   float2 v0[MERGE_PRE];           // and its columns 2 lane, 2 lane + 1 of the first MERGE_PRE partials
-  if (head0 >= 0 && head0 < gq) {
+  if (merging && !poll) {
     if (lane < P) {
-      mm = ld_f(hws + (int64_t)lane * pw + gq * D + head0, inl);
-      ll = ld_f(hws + (int64_t)lane * pw + gq * D + gq + head0, inl);
+      mm = ld_f(hws + (int64_t)lane * pw + gq * D + head0, co);
+      ll = ld_f(hws + (int64_t)lane * pw + gq * D + gq + head0, co);
     }
 #pragma unroll
     for (int u = 0; u < MERGE_PRE; ++u)
-      v0[u] = u < P ? ld_f2(hws + (int64_t)u * pw + head0 * D + 2 * lane, inl) : float2{0.f, 0.f};
+      v0[u] = u < P ? ld_f2(hws + (int64_t)u * pw + head0 * D + 2 * lane, co) : float2{0.f, 0.f};
   }
+  if (tid == 0) sm.incomplete = 0;
 
-  // ---- the ring, when not precomputed: into LDS (a token that completes its group through
-  // the group's int8 values, dequantized as the prefix dequantizes them)
+  // ---- the ring into LDS (chunk ^ (row & 15) layout), the new token over its slot
   uint8_t* ring_k = sm.ring_lds;
   uint8_t* ring_v = sm.ring_lds + RING_BYTES;
-  if (ring_phase) {
-    if (completes) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) rq.rows[i] = __builtin_bit_cast(uint4, dq8(cw[i].x, cw[i].y, cst, cmn));
-    }
+  if (ring) {
     if (tok1) {
       if (qtr == 0 && lane < 16) {
-        const _Float16 sc = __builtin_bit_cast(_Float16, tsc);
+        const uint32_t wv[4] = {tokw.x, tokw.y, tokw.z, tokw.w};
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = h2f((uint16_t)(wv[j >> 1] >> (16 * (j & 1))));
+        float scale;
+        const uint2 cw = sym_quant8(v, scale);
+        const _Float16 sc = (_Float16)scale;
         *reinterpret_cast<half8_t*>((which == 0 ? ring_k : ring_v) + (ring_chunk_pos(0, lane) << 4)) =
-            dq8_sym(tw.x, tw.y, half2_t{sc, sc});
+            dq8_sym(cw.x, cw.y, half2_t{sc, sc});
       }
     } else {
       uint8_t* rl_lds = which == 0 ? ring_k : ring_v;
-      ring_quarter_to_lds(rq.rows, qtr, rl_lds);
+      const int cl = lane & 15, rl = lane >> 4;
+      const uint4 rows[4] = {rq0, rq1, rq2, rq3};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * qtr + rl + 4 * i;
+        *reinterpret_cast<uint4*>(rl_lds + r * (2 * D) + (ring_chunk_pos(r, cl) << 4)) = rows[i];
+      }
       // (program order: this store lands after the quarter's store of the same row)
       if (fresh_on && fresh_slot >> 4 == qtr && (fresh_slot & 3) == lane >> 4)
         *reinterpret_cast<uint4*>(rl_lds + fresh_slot * (2 * D) + (ring_chunk_pos(fresh_slot, lane & 15) << 4)) = fresh;
     }
     __syncthreads();
+    if (completes) requant_ring_lds(sm.ring_lds, sm.rq_ext);
+    __syncthreads();
   }
+
   if (wave < mbase) {
     // ---- ring attention: 4 waves x 16 tokens, one partial each
     const int64_t written = fused ? pos + 1 : (a.tail_mode == TAIL_SCALARS ? *a.written_dev : 0);
@@ -1180,7 +1215,36 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     state_init(st);
     attend_ring16(a, st, qb, ring_k, ring_v, wave, bits);
     store_wave_partial(st, gq, sm.ring_part[wave]);
-  } else {
+  } else if (merging) {
+    if (poll) {
+      // ---- wait for every partial's flag (P <= MERGER_MAX_PARTS, checked at launch), then one
+      // agent-scope acquire and the loads of each partial's m, l and first MERGE_PRE column pairs
+      const int* flags = partial_flags(a, h);
+      const uint64_t want = P >= 64 ? ~0ull : ((1ull << P) - 1);
+      uint64_t have = 0;
+#pragma unroll
+      for (int u = 0; u < MERGE_PRE; ++u) v0[u] = float2{0.f, 0.f};
+      for (int spin = 0; have != want;) {
+        const bool up = lane < P && !((have >> lane) & 1) &&
+                        __hip_atomic_load(flags + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+        const uint64_t now = __builtin_amdgcn_ballot_w64(up);
+        if (now == 0) {
+          if (++spin > MERGER_SPIN_LIMIT) break;
+          __builtin_amdgcn_s_sleep(1);
+          continue;
+        }
+        have |= now;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      if (lane < P) {
+        mm = ld_f(hws + (int64_t)lane * pw + gq * D + head0, true);
+        ll = ld_f(hws + (int64_t)lane * pw + gq * D + gq + head0, true);
+      }
+#pragma unroll
+      for (int u = 0; u < MERGE_PRE; ++u)
+        if (u < P) v0[u] = ld_f2(hws + (int64_t)u * pw + head0 * D + 2 * lane, true);
+      if (have != want && lane == 0) sm.incomplete = 1;
+    }
     // ---- prefix merge, one head at a time per merging wave (lane s (+ 64 k) = partial s for
     // the weights, two columns per lane for the sum): m_p, w_s, l_p, pre_acc
     float* wb = sm.wts + wave * WTS;
@@ -1188,12 +1252,12 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
       const bool own = head == head0;
       float m = NEG_INF;
       for (int s = lane; s < P; s += 64)
-        m = fmaxf(m, (own && s == lane) ? mm : ld_f(hws + (int64_t)s * pw + gq * D + head, inl));
+        m = fmaxf(m, (own && s == lane) ? mm : ld_f(hws + (int64_t)s * pw + gq * D + head, co));
       m = wave_max(m);
       float l = 0.0f;
       for (int s = lane; s < P; s += 64) {
-        const float ms = (own && s == lane) ? mm : ld_f(hws + (int64_t)s * pw + gq * D + head, inl);
-        const float ls = (own && s == lane) ? ll : ld_f(hws + (int64_t)s * pw + gq * D + gq + head, inl);
+        const float ms = (own && s == lane) ? mm : ld_f(hws + (int64_t)s * pw + gq * D + head, co);
+        const float ls = (own && s == lane) ? ll : ld_f(hws + (int64_t)s * pw + gq * D + gq + head, co);
         const float w = ms == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(ms - m);
         wb[s] = w;
         l += ls * w;
@@ -1211,7 +1275,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
         s0 = MERGE_PRE;
       }
       for (int s = s0; s < P; ++s) {
-        const float2 vv = ld_f2(hws + (int64_t)s * pw + head * D + 2 * lane, inl);
+        const float2 vv = ld_f2(hws + (int64_t)s * pw + head * D + 2 * lane, co);
         acc.x += vv.x * wb[s];
         acc.y += vv.y * wb[s];
       }
@@ -1223,6 +1287,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
 
   // ---- combine: one column per thread. Prefix: acc_p = sum_s w_s acc_s; then with the
   // ring's partials r: M = max(m_p, m_r), alpha = 2^(m_p - M), beta_r = 2^(m_r - M)
+  const bool failed = sm.incomplete != 0;
   for (int col = tid; col < cols; col += TB_THREADS) {
     const int head = col / D;
     const float accp = sm.pre_acc[col];
@@ -1230,7 +1295,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     float M = mp, mr[RING_PARTS], lr[RING_PARTS], ar[RING_PARTS];
 #pragma unroll
     for (int r = 0; r < RING_PARTS; ++r) {
-      if (ring_phase) {
+      if (ring) {
         mr[r] = sm.ring_part[r][gq * D + head];
         lr[r] = sm.ring_part[r][gq * D + gq + head];
         ar[r] = sm.ring_part[r][col];
@@ -1252,9 +1317,16 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     }
     const int64_t qh = qh0 + head;
     const int d = col % D;
-    // acc and l carry the same 2^15 scale
-    a.out[(int64_t)qh * D + d] = f2h(l > 0.0f ? acc / l : 0.0f);
-    if (a.lse && d == 0) a.lse[qh] = l > 0.0f ? (M + __log2f(l) - P_SCALE_LOG2) * LN2 : NEG_INF;
+    // acc and l carry the same 2^15 scale; a merger that gave up writes NaN
+    const float o = failed ? __builtin_nanf("") : (l > 0.0f ? acc / l : 0.0f);
+    a.out[(int64_t)qh * D + d] = f2h(o);
+    if (a.lse && d == 0) a.lse[qh] = failed ? __builtin_nanf("") : (l > 0.0f ? (M + __log2f(l) - P_SCALE_LOG2) * LN2 : NEG_INF);
+  }
+  // ---- the merger leaves the publication area at zero for the next launch: every producer
+  // set its flag after taking its ticket, and every flag has been seen
+  if (poll) {
+    if (tid == 0) __hip_atomic_store(a.tail_ctr_end - 1 - h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < P) __hip_atomic_store(partial_flags(a, h) + tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1290,7 +1362,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   int64_t U;
   if constexpr (PAGED) {
     pos = a.pos_dev[b];  // the ring holds the group of pos (appended before this launch)
-    pos_ok = pos >= 0 && pos / GT < a.table_stride;
+    pos_ok = pos >= 0 && page_of(a, b, pos / GT) >= 0;  // the current group has a page
     U = pos_ok ? pos / GT * GT : 0;
   } else {
     U = prefix_limit(a, pos, pos_ok);
@@ -1413,21 +1485,45 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
     }
   }  // prefix
 
-  // ---- fused tail: once every store of this workgroup (partial, append) is done, take a
-  // ticket; the head's last workgroup resets the counter and runs the tail
+  // ---- fused tail. Every wave's partial stores are complete (vmcnt) before the workgroup
+  // barrier; thread 0 then publishes the partial with an agent-scope release fence (the
+  // barrier orders the other waves' stores before it) and an atomic on the head's counter.
   if (!a.inline_tail) return;
+  if constexpr (!PAGED) {
+    if (!prefix) return;  // append-only workgroups publish nothing: the tail reads none of their stores
+  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  const int last = (PAGED ? nparts : (int)(gridDim.x / a.hkv)) - 1;
-  int* ctr = a.tail_ctr_end - 1 - (PAGED ? b * a.hkv + h : h);
-  if (tid == 0) {
-    const int t = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (t == last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    ticket = t;
-  }
-  __syncthreads();
+  TailSmem& sm = *reinterpret_cast<TailSmem*>(lds_raw);
   // (pos, pos_ok, U as the prologue read them: the tail needs no second round trip for them)
-  if (ticket == last) tail_body<PAGED>(a, h, b, *reinterpret_cast<TailSmem*>(lds_raw), true, pos, pos_ok, U);
+  if constexpr (PAGED) {
+    // the last of the sequence's workgroups to publish runs the tail, after an acquire
+    const int last = nparts - 1;
+    int* ctr = a.tail_ctr_end - 1 - (b * a.hkv + h);
+    if (tid == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      const int t = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (t == last) {
+        __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      }
+      ticket = t;
+    }
+    __syncthreads();
+    if (ticket == last) tail_body<true>(a, h, b, sm, TAIL_LAST, pos, pos_ok, U);
+  } else {
+    // the first of the head's workgroups to publish becomes its merger: it attends over the ring
+    // and collects the other partials as their flags appear. It only waits for workgroups of
+    // this launch that never wait themselves, so it cannot deadlock them.
+    if (tid == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      const int t = __hip_atomic_fetch_add(a.tail_ctr_end - 1 - h, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(partial_flags(a, h) + part, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ticket = t;
+    }
+    __syncthreads();
+    if (ticket == 0) tail_body<false>(a, h, b, sm, TAIL_MERGER, pos, pos_ok, U);
+  }
 }
 
 // ---------------------------------------------------------------- kernel B: ring + merge
@@ -1443,12 +1539,12 @@ __global__ __launch_bounds__(TB_THREADS, 1) void attn_tail_kernel(AttnArgs a) {
   int64_t U;
   if constexpr (PAGED) {
     pos = a.pos_dev[b];
-    pos_ok = pos >= 0 && pos / GT < a.table_stride;
+    pos_ok = pos >= 0 && page_of(a, b, pos / GT) >= 0;  // the current group has a page
     U = pos_ok ? pos / GT * GT : 0;
   } else {
     U = prefix_limit(a, pos, pos_ok);
   }
-  tail_body<PAGED>(a, h, b, sm, false, pos, pos_ok, U);
+  tail_body<PAGED>(a, h, b, sm, TAIL_KERNEL, pos, pos_ok, U);
 }
 
 // Standalone append: one workgroup per append unit (APPEND_UNITS per KV head).
@@ -1474,7 +1570,7 @@ __global__ __launch_bounds__(THREADS) void append_paged_kernel(AttnArgs a) {
   const int w = blockIdx.x % WIDE_UNITS, h = (blockIdx.x / WIDE_UNITS) % a.hkv;
   const int b = blockIdx.x / (WIDE_UNITS * a.hkv);
   const int64_t pos = a.pos_dev[b];
-  if (pos < 0 || pos / GT >= a.table_stride) return;  // a position without a page appends nothing
+  if (pos < 0 || page_of(a, b, pos / GT) < 0) return;  // a position without a page appends nothing
   const int which = w / (D / WIDE_CH), ch0 = (w % (D / WIDE_CH)) * WIDE_CH;
   const UnitIO io = unit_io_paged(a, b, h, which * (D / UNIT_CH), pos);
   issue_wide_rows(io, ch0, lds_addr(src));
@@ -1818,8 +1914,10 @@ static int64_t default_parts(int64_t hkv, int64_t groups) {
 }
 
 static int64_t part_floats(int64_t hq, int64_t hkv) { return part_stride((int)(hq / hkv)); }
-// Bytes of the fused tail's completion counters (one int per head, or per sequence and head).
+// Bytes of the fused tail's publication area: `n` ints (per head a counter and a flag per
+// partial; paged, a counter per sequence and head), rounded up to 256 bytes.
 static int64_t ctr_bytes(int64_t n) { return (n * (int64_t)sizeof(int) + 255) / 256 * 256; }
+static int64_t sync_bytes(int64_t hkv, int64_t n_parts) { return ctr_bytes(hkv * (1 + std::max<int64_t>(1, n_parts))); }
 
 static int check_heads(int64_t hq, int64_t hkv, int64_t head_dim) {
   if (hkv <= 0 || hq <= 0 || hq % hkv) return fail(NKV_ERR_INVALID, "Q heads %lld not divisible by KV heads %lld", (long long)hq, (long long)hkv);
@@ -1838,9 +1936,10 @@ static int launch_attn(AttnArgs& a, int64_t n_parts, int64_t workspace_bytes, hi
   if (n_parts < 0) return fail(NKV_ERR_INVALID, "%s: n_parts %lld is negative", what, (long long)n_parts);
   a.n_parts = (int)n_parts;
   // both launches in one call: the prefix kernel's last workgroup per head runs the tail
-  const bool fuse = fusable && n_parts > 0 && launches == (LAUNCH_PREFIX | LAUNCH_TAIL);
+  // (the merger tracks at most MERGER_MAX_PARTS partials; more parts take the two launches)
+  const bool fuse = fusable && n_parts > 0 && n_parts <= MERGER_MAX_PARTS && launches == (LAUNCH_PREFIX | LAUNCH_TAIL);
   const int64_t part_bytes = (int64_t)a.hkv * std::max<int64_t>(1, n_parts) * part_floats(a.hq, a.hkv) * (int64_t)sizeof(float);
-  const int64_t need = part_bytes + (fuse ? ctr_bytes(a.hkv) : 0);
+  const int64_t need = part_bytes + (fuse ? sync_bytes(a.hkv, n_parts) : 0);
   if (n_parts > 0 && workspace_bytes < need)
     return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
   if (n_parts > 256) return fail(NKV_ERR_UNSUPPORTED, "%s: n_parts %lld exceeds the 256 partials the merge holds", what, (long long)n_parts);
@@ -1867,7 +1966,7 @@ using namespace nkv;
 
 extern "C" int64_t nkv_attn_workspace_bytes(int64_t hkv, int64_t hq, int64_t n_parts) {
   if (hkv <= 0 || hq <= 0 || n_parts < 0 || hq % hkv) return 0;
-  return hkv * std::max<int64_t>(1, n_parts) * part_floats(hq, hkv) * (int64_t)sizeof(float) + ctr_bytes(hkv);
+  return hkv * std::max<int64_t>(1, n_parts) * part_floats(hq, hkv) * (int64_t)sizeof(float) + sync_bytes(hkv, n_parts);
 }
 
 extern "C" int64_t nkv_attn_default_parts(int64_t hkv, int64_t groups) { return default_parts(hkv, groups); }
@@ -2140,9 +2239,11 @@ extern "C" int64_t nkv_paged_workspace_bytes(int64_t hkv, int64_t hq, int64_t to
 }
 
 static int paged_args(const char* what, AttnArgs& a, const uint8_t* pages, const int32_t* page_table,
-                      int64_t table_stride, const uint16_t* rings, const int64_t* pos_dev, int64_t nseq, int64_t hkv,
-                      int64_t head_dim) {
+                      int64_t table_stride, int64_t num_pages, const uint16_t* rings, const int64_t* pos_dev,
+                      int64_t nseq, int64_t hkv, int64_t head_dim) {
   if (head_dim != D) return fail(NKV_ERR_UNSUPPORTED, "head_dim %lld: the HIP kernels are built for head_dim 128", (long long)head_dim);
+  if (num_pages <= 0 || num_pages > (int64_t(1) << 31))
+    return fail(NKV_ERR_INVALID, "%s: num_pages %lld", what, (long long)num_pages);
   if (nseq <= 0 || nseq > 32767 || hkv <= 0 || table_stride <= 0)
     return fail(NKV_ERR_INVALID, "%s: bad sizes nseq=%lld hkv=%lld table_stride=%lld", what, (long long)nseq,
                 (long long)hkv, (long long)table_stride);
@@ -2151,6 +2252,7 @@ static int paged_args(const char* what, AttnArgs& a, const uint8_t* pages, const
   a.pages = const_cast<uint8_t*>(pages);
   a.table = page_table;
   a.table_stride = table_stride;
+  a.num_pages = num_pages;
   a.rings = const_cast<uint16_t*>(rings);
   a.pos_dev = pos_dev;
   a.nseq = (int)nseq;
@@ -2162,11 +2264,13 @@ static int paged_args(const char* what, AttnArgs& a, const uint8_t* pages, const
 
 extern "C" int nkv_paged_append_t64(const uint16_t* k_new, const uint16_t* v_new, int64_t kv_seq_stride,
                                     int64_t kv_head_stride, uint8_t* pages, const int32_t* page_table,
-                                    int64_t table_stride, uint16_t* rings, const int64_t* pos_dev, int64_t nseq,
-                                    int64_t hkv, int64_t head_dim, void* stream) {
+                                    int64_t table_stride, int64_t num_pages, uint16_t* rings, const int64_t* pos_dev,
+                                    int64_t nseq, int64_t hkv, int64_t head_dim, void* stream) {
   set_error("");
   AttnArgs a{};
-  if (int rc = paged_args("paged_append_t64", a, pages, page_table, table_stride, rings, pos_dev, nseq, hkv, head_dim)) return rc;
+  if (int rc = paged_args("paged_append_t64", a, pages, page_table, table_stride, num_pages, rings, pos_dev, nseq, hkv,
+                          head_dim))
+    return rc;
   if (!k_new || !v_new) return fail(NKV_ERR_INVALID, "paged_append_t64: null pointer argument");
   if (!al16(k_new) || !al16(v_new) || kv_head_stride % 8 || kv_seq_stride % 8)
     return fail(NKV_ERR_UNSUPPORTED, "paged_append_t64: k_new / v_new must be 16-byte aligned");
@@ -2178,14 +2282,16 @@ extern "C" int nkv_paged_append_t64(const uint16_t* k_new, const uint16_t* v_new
 
 static int paged_attn(const char* what, const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                       int64_t kv_seq_stride, int64_t kv_head_stride, const uint8_t* pages, const int32_t* page_table,
-                      int64_t table_stride, const uint16_t* rings, const int64_t* pos_dev, int64_t nseq, int64_t hq,
+                      int64_t table_stride, int64_t num_pages, const uint16_t* rings, const int64_t* pos_dev,
+                      int64_t nseq, int64_t hq,
                       int64_t hkv, int64_t head_dim, const int32_t* wg_map, const int32_t* seq_parts,
                       int64_t total_parts, uint16_t* out, float* lse_out, void* workspace, int64_t workspace_bytes,
                       void* stream) {
   set_error("");
   if (int rc = check_heads(hq, hkv, head_dim)) return rc;
   AttnArgs a{};
-  if (int rc = paged_args(what, a, pages, page_table, table_stride, rings, pos_dev, nseq, hkv, head_dim)) return rc;
+  if (int rc = paged_args(what, a, pages, page_table, table_stride, num_pages, rings, pos_dev, nseq, hkv, head_dim))
+    return rc;
   if (!q || !wg_map || !seq_parts || !out || !workspace) return fail(NKV_ERR_INVALID, "%s: null pointer argument", what);
   if (!al16(q) || !al16(workspace)) return fail(NKV_ERR_UNSUPPORTED, "%s: buffers must be 16-byte aligned", what);
   if (total_parts < nseq || total_parts > 65535)
@@ -2207,29 +2313,29 @@ static int paged_attn(const char* what, const uint16_t* q, const uint16_t* k_new
 }
 
 extern "C" int nkv_paged_attn_decode_t64(const uint16_t* q, const uint8_t* pages, const int32_t* page_table,
-                                         int64_t table_stride, const uint16_t* rings, const int64_t* pos_dev,
-                                         int64_t nseq, int64_t hq, int64_t hkv, int64_t head_dim,
-                                         const int32_t* wg_map, const int32_t* seq_parts, int64_t total_parts,
-                                         uint16_t* out, float* lse_out, void* workspace, int64_t workspace_bytes,
-                                         void* stream) {
-  return paged_attn("paged_attn_decode_t64", q, nullptr, nullptr, 0, 0, pages, page_table, table_stride, rings,
-                    pos_dev, nseq, hq, hkv, head_dim, wg_map, seq_parts, total_parts, out, lse_out, workspace,
+                                         int64_t table_stride, int64_t num_pages, const uint16_t* rings,
+                                         const int64_t* pos_dev, int64_t nseq, int64_t hq, int64_t hkv,
+                                         int64_t head_dim, const int32_t* wg_map, const int32_t* seq_parts,
+                                         int64_t total_parts, uint16_t* out, float* lse_out, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+  return paged_attn("paged_attn_decode_t64", q, nullptr, nullptr, 0, 0, pages, page_table, table_stride, num_pages,
+                    rings, pos_dev, nseq, hq, hkv, head_dim, wg_map, seq_parts, total_parts, out, lse_out, workspace,
                     workspace_bytes, stream);
 }
 
 extern "C" int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                                          int64_t kv_seq_stride, int64_t kv_head_stride, uint8_t* pages,
-                                         const int32_t* page_table, int64_t table_stride, uint16_t* rings,
-                                         const int64_t* pos_dev, int64_t nseq, int64_t hq, int64_t hkv,
-                                         int64_t head_dim, const int32_t* wg_map, const int32_t* seq_parts,
-                                         int64_t total_parts, uint16_t* out, float* lse_out, void* workspace,
-                                         int64_t workspace_bytes, void* stream) {
+                                         const int32_t* page_table, int64_t table_stride, int64_t num_pages,
+                                         uint16_t* rings, const int64_t* pos_dev, int64_t nseq, int64_t hq,
+                                         int64_t hkv, int64_t head_dim, const int32_t* wg_map,
+                                         const int32_t* seq_parts, int64_t total_parts, uint16_t* out, float* lse_out,
+                                         void* workspace, int64_t workspace_bytes, void* stream) {
   if (int rc = nkv_paged_append_t64(k_new, v_new, kv_seq_stride, kv_head_stride, pages, page_table, table_stride,
-                                    rings, pos_dev, nseq, hkv, head_dim, stream))
+                                    num_pages, rings, pos_dev, nseq, hkv, head_dim, stream))
     return rc;
   return paged_attn("paged_decode_step_t64", q, k_new, v_new, kv_seq_stride, kv_head_stride, pages, page_table,
-                    table_stride, rings, pos_dev, nseq, hq, hkv, head_dim, wg_map, seq_parts, total_parts, out,
-                    lse_out, workspace, workspace_bytes, stream);
+                    table_stride, num_pages, rings, pos_dev, nseq, hq, hkv, head_dim, wg_map, seq_parts, total_parts,
+                    out, lse_out, workspace, workspace_bytes, stream);
 }
 
 // ---------------------------------------------------------------- chunked prefill

@@ -114,12 +114,21 @@ struct QuantTokArgs {
   uint16_t* steps;
   int64_t s_rs;
   int64_t items;
+  // page destination (paged cache): group gi of slab r goes to page table[first_group + gi], KV
+  // head r, tensor `which` (0 K, 1 V) of the page layout [K codes 64 x 128 | V codes | kst | kmn |
+  // vst | vmn]; groups whose table entry is outside [0, num_pages) are skipped
+  uint8_t* pages;
+  const int32_t* table;
+  int64_t first_group, num_pages;
+  int which;
 };
+
+constexpr int64_t PAGE_GROUP_BYTES = 2 * 64 * 128 + 4 * 128 * 2;  // 17408
 
 constexpr int kQuantWaves = 4;
 constexpr int kCacheRows = 16;  // rows per lane kept in registers (groups of <= 64 tokens)
 
-template <int DT, bool CACHE>
+template <int DT, bool CACHE, bool PAGES = false>
 __global__ __launch_bounds__(64 * kQuantWaves) void quant_token_kernel(QuantTokArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t item = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
@@ -170,24 +179,38 @@ __global__ __launch_bounds__(64 * kQuantWaves) void quant_token_kernel(QuantTokA
   float st[8], inv[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) { st[j] = ruler_step(mn[j], mx[j]); inv[j] = ruler_inv(st[j]); }
-  if (rl == 0) {
-    const int64_t so = r * a.s_rs + gi * a.dim + ch;
-    *reinterpret_cast<uint4*>(a.mins + so) = pack_h8(mn);
-    *reinterpret_cast<uint4*>(a.steps + so) = pack_h8(st);
+  uint8_t* codes = a.codes;
+  uint16_t* mins = a.mins;
+  uint16_t* steps = a.steps;
+  int64_t so = r * a.s_rs + gi * a.dim + ch;
+  int64_t cbase = r * a.c_rs + ch;
+  if constexpr (PAGES) {
+    // token t of the group is row t of its page's code block; the rulers follow the code blocks
+    const int32_t page = a.table[a.first_group + gi];
+    if (page < 0 || page >= a.num_pages) return;
+    uint8_t* pg = a.pages + ((int64_t)page * a.rows + r) * PAGE_GROUP_BYTES;
+    codes = pg + a.which * 64 * 128;
+    cbase = ch - t0 * a.dim;  // (t0 + t) * dim below addresses row t
+    steps = reinterpret_cast<uint16_t*>(pg + 2 * 64 * 128) + a.which * 2 * 128;
+    mins = steps + 128;
+    so = ch;
   }
-  const int64_t cbase = r * a.c_rs + ch;
+  if (rl == 0) {
+    *reinterpret_cast<uint4*>(mins + so) = pack_h8(mn);
+    *reinterpret_cast<uint4*>(steps + so) = pack_h8(st);
+  }
   if (CACHE) {
 #pragma unroll
     for (int i = 0; i < kCacheRows; ++i) {
       const int64_t t = rl + 4 * i;
-      if (t < nr) *reinterpret_cast<uint2*>(a.codes + cbase + (t0 + t) * a.dim) = pack_codes8(cache[i], mn, st, inv);
+      if (t < nr) *reinterpret_cast<uint2*>(codes + cbase + (t0 + t) * a.dim) = pack_codes8(cache[i], mn, st, inv);
     }
   } else {
     const int64_t base = r * a.x_rs + ch;
     for (int64_t t = rl; t < nr; t += 4) {
       float v[8];
       Elem8<DT>::load(a.x, base + (t0 + t) * a.dim, v);
-      *reinterpret_cast<uint2*>(a.codes + cbase + (t0 + t) * a.dim) = pack_codes8(v, mn, st, inv);
+      *reinterpret_cast<uint2*>(codes + cbase + (t0 + t) * a.dim) = pack_codes8(v, mn, st, inv);
     }
   }
 }
@@ -440,6 +463,32 @@ extern "C" int nkv_quantize_int8(const void* x, int x_dtype, int64_t x_row_strid
     return check_launch("quantize_int8(channel)");
   }
   return fail(NKV_ERR_INVALID, "axis must be channel (0) or token (1), got %d", axis);
+}
+
+extern "C" int nkv_paged_quantize_t64(const void* x, int x_dtype, int64_t x_head_stride, int64_t hkv, int64_t n,
+                                      int which, uint8_t* pages, const int32_t* table_row, int64_t first_group,
+                                      int64_t num_pages, void* stream) {
+  g_err.clear();
+  if (x_dtype != NKV_F16 && x_dtype != NKV_BF16 && x_dtype != NKV_F32)
+    return fail(NKV_ERR_INVALID, "paged_quantize: unknown dtype %d", x_dtype);
+  if (hkv <= 0 || n < 0 || n % 64 || first_group < 0 || (which != 0 && which != 1) || num_pages <= 0)
+    return fail(NKV_ERR_INVALID, "paged_quantize: bad sizes hkv=%lld n=%lld (whole groups of 64) first_group=%lld "
+                "which=%d num_pages=%lld", (long long)hkv, (long long)n, (long long)first_group, which,
+                (long long)num_pages);
+  if (n == 0) return NKV_OK;
+  if (!x || !pages || !table_row) return fail(NKV_ERR_INVALID, "paged_quantize: null pointer argument");
+  const int esz = x_dtype == NKV_F32 ? 4 : 2;
+  if (!aligned16(x) || !aligned16(pages) || (x_head_stride * esz) % 16 || x_head_stride < n * 128)
+    return fail(NKV_ERR_UNSUPPORTED, "paged_quantize: x must be 16-byte aligned with a head stride >= n * 128");
+  QuantTokArgs a{x, x_head_stride, hkv, n, 128, 64, n / 64, 1, nullptr, 0, nullptr, nullptr, 0, 0,
+                 pages, table_row, first_group, num_pages, which};
+  a.items = hkv * a.ngroups;
+  const dim3 grid((unsigned)cdiv(a.items, kQuantWaves)), block(64 * kQuantWaves);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (x_dtype == NKV_F16) hipLaunchKernelGGL((quant_token_kernel<NKV_F16, true, true>), grid, block, 0, s, a);
+  else if (x_dtype == NKV_BF16) hipLaunchKernelGGL((quant_token_kernel<NKV_BF16, true, true>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((quant_token_kernel<NKV_F32, true, true>), grid, block, 0, s, a);
+  return check_launch("paged_quantize_t64");
 }
 
 extern "C" int nkv_dequantize_int8(const uint8_t* codes, int64_t codes_row_stride,

@@ -153,3 +153,49 @@ class StreamCache:
         """Resident bytes: codes + rulers + ring (``kvattn.py:866-872``)."""
         per_layer = (2 * self.kq[0].nbytes + 4 * self.kmn[0].nbytes + 2 * self.tail_k[0].nbytes)
         return per_layer * self.num_slots
+
+
+def decode_trajectory(k, v, qs, n0: int, group: int = 64, scale: float | None = None) -> np.ndarray:
+    """Outputs of every decode step of a streaming cache, computed in batches (checker only).
+
+    A prefill of ``n0`` tokens is followed by ``S = len(qs)`` decode steps: step i appends token
+    ``p = n0 + i`` of ``k`` / ``v`` (``[Hkv, n0 + S, D]`` fp16) and attends with ``qs[i]``
+    (``[Hq, D]`` fp16). Each step's value is what :meth:`StreamCache.attend_exact` computes after
+    that append: one softmax (fp64) over the int8 prefix ``[0, qlen)``, ``qlen = 64 floor((p + 1)
+    / 64)``, dequantized, and the fp16 ring tokens ``[qlen, p]``. An int8 group is the quantizer's
+    rounding of its 64 fp16 tokens (the prefill quantizes whole groups; a decode group is the ring
+    requantized when its 64th token lands, ``kvattn.py:716-743``), so the prefix is dequantized
+    once. Steps that share ``qlen`` share their keys and are computed together, the ring tokens
+    under a causal mask. Returns fp64 ``[S, Hq, D]``.
+    """
+    k = np.asarray(k)
+    v = np.asarray(v)
+    qs = np.asarray(qs)
+    hkv, _, d = k.shape
+    S, hq, _ = qs.shape
+    gq = hq // hkv
+    scale = d ** -0.5 if scale is None else scale
+    total = n0 + S
+    full = total // group * group
+    deq_k = okq.dequantize_int8_token(*okq.quantize_int8_token(k[:, :full], group), group).astype(np.float64)
+    deq_v = okq.dequantize_int8_token(*okq.quantize_int8_token(v[:, :full], group), group).astype(np.float64)
+    kf, vf = k.astype(np.float64), v.astype(np.float64)
+    out = np.zeros((S, hq, d))
+    p_all = n0 + np.arange(S)
+    qlen_all = (p_all + 1) // group * group
+    for qlen in np.unique(qlen_all):
+        idx = np.nonzero(qlen_all == qlen)[0]
+        ps = p_all[idx]
+        t_end = int(ps.max()) + 1  # ring tokens [qlen, t_end)
+        ring_pos = np.arange(qlen, t_end)
+        keep = ring_pos[None, :] <= ps[:, None]  # [steps, ring tokens]
+        for h in range(hkv):
+            kk = np.concatenate([deq_k[h, :qlen], kf[h, qlen:t_end]], 0)
+            vv = np.concatenate([deq_v[h, :qlen], vf[h, qlen:t_end]], 0)
+            q = qs[idx, h * gq:(h + 1) * gq].astype(np.float64)  # [steps, gq, D]
+            s = (q @ kk.T) * scale  # [steps, gq, keys]
+            s[:, :, qlen:][~np.broadcast_to(keep[:, None, :], s[:, :, qlen:].shape)] = -np.inf
+            s -= s.max(axis=2, keepdims=True)
+            w = np.exp(s)
+            out[idx, h * gq:(h + 1) * gq] = (w @ vv) / w.sum(axis=2, keepdims=True)
+    return out

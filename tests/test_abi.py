@@ -59,11 +59,14 @@ def test_abi_version_and_host_helpers(lib):
     assert lib.nkv_attn_default_parts(8, 1) == 1
     assert lib.nkv_attn_default_parts(2, 4096) == 128
     # one partial = [acc: 4 heads x 128][m: 4][l: 4] floats, 16-byte aligned, per KV head,
-    # plus the fused tail's completion counters (one int per head, in 256-byte blocks)
+    # plus the fused tail's publication area: per head a counter and a flag per partial (ints,
+    # in 256-byte blocks)
     per_part = 8 * (4 * 128 + 8) * 4
-    assert lib.nkv_attn_workspace_bytes(8, 32, 64) == 64 * per_part + 256
-    assert lib.nkv_attn_workspace_bytes(8, 32, 0) == per_part + 256
-    assert lib.nkv_attn_workspace_bytes(128, 128, 1) == 128 * (128 + 4) * 4 + 512
+    sync = lambda hkv, parts: -(-(hkv * (1 + max(1, parts)) * 4) // 256) * 256  # noqa: E731
+    assert lib.nkv_attn_workspace_bytes(8, 32, 64) == 64 * per_part + sync(8, 64) == 64 * per_part + 2304
+    assert lib.nkv_attn_workspace_bytes(8, 32, 32) == 32 * per_part + 1280
+    assert lib.nkv_attn_workspace_bytes(8, 32, 0) == per_part + sync(8, 1)
+    assert lib.nkv_attn_workspace_bytes(128, 128, 1) == 128 * (128 + 4) * 4 + sync(128, 1)
     assert lib.nkv_paged_workspace_bytes(8, 32, 40) == 40 * per_part + 8 * 40 * 4  # one counter per (unit, head) bound
 
 

@@ -154,3 +154,50 @@ def test_mask_table_rows():
     lo = torch.finfo(torch.float16).min
     for p in range(5):
         assert all(float(t[p, j]) == (0.0 if j <= p else lo) for j in range(5))
+
+
+def test_page_pool_guards():
+    """Host bookkeeping of the paged cache: reservations grow from group 0, a release returns every
+    page, a step past the reserved pages is refused (before any kernel could write through a page
+    table entry the sequence does not own), and the pool refuses to overcommit."""
+    import pytest
+
+    from nova_amd.paged import GT, PagePool
+
+    pool = PagePool(num_pages=10, max_seqs=3, max_pages_per_seq=6)
+    assert pool.reserve(0, 65) == [(0, 0), (1, 1)]           # groups 0 and 1, pages from the free list
+    assert pool.reserve(0, 100) == []                         # already covered
+    assert [g for g, _ in pool.reserve(1, 3 * GT)] == [0, 1, 2]
+    pool.set_length(0, 65)
+    pool.advance(1, 63)                                       # tokens 65 .. 127 stay in page 1
+    with pytest.raises(RuntimeError, match="reserve"):
+        pool.advance(1, 1)                                    # token 128 would need group 2
+    assert pool.length[0] == 128
+    with pytest.raises(RuntimeError, match="reserved"):
+        pool.set_length(1, 3 * GT + 1)
+    with pytest.raises(RuntimeError, match="exhausted"):
+        pool.reserve(2, 6 * GT)                               # 6 pages, 5 free
+    with pytest.raises(ValueError, match="max_pages_per_seq"):
+        pool.reserve(2, 7 * GT)
+    owned0 = list(pool.owned[0])
+    pool.release(0)
+    assert pool.owned[0] == [] and pool.length[0] == 0 and set(owned0) <= set(pool.free)
+    assert sorted(pool.free + pool.owned[1]) == list(range(10))
+    with pytest.raises(ValueError):
+        pool.reserve(3, 1)                                    # no such sequence
+
+
+def test_plan_parts_bounds():
+    """The paged work plan gives every sequence at least one and at most 256 parts, in proportion
+    to its groups, and numbers the units consecutively per sequence."""
+    from nova_amd.paged import MAX_PARTS_PER_SEQ, plan_parts
+
+    wg, sp = plan_parts([4566, 13658, 10122, 8480, 9727, 12101, 7956, 10569], 32)
+    assert len(sp) == 16 and sum(sp[1::2]) == len(wg)
+    for b in range(8):
+        first, n = sp[2 * b], sp[2 * b + 1]
+        assert n >= 1 and [w >> 16 for w in wg[first:first + n]] == [b] * n
+        assert [w & 0xffff for w in wg[first:first + n]] == list(range(n))
+    # a long sequence beside short ones still gets at most MAX_PARTS_PER_SEQ parts
+    wg, sp = plan_parts([1 << 20, 64, 64], 4096)
+    assert sp[1] == MAX_PARTS_PER_SEQ and sp[3] >= 1 and sp[5] >= 1

@@ -420,3 +420,31 @@ def test_torch_tok_step_matches_oracle():
     got = torch_ref.decode_step_tok(t(q), t(kq), t(ks), t(vq), t(vs), n).numpy()
     spacing = np.abs(np.spacing(want.astype(np.float16)).astype(np.float64))
     assert np.all(np.abs(got.astype(np.float64) - want.astype(np.float64)) <= 1.01 * spacing + 1e-7)
+
+
+def test_decode_trajectory_equals_step_by_step_state_machine():
+    """The batched trajectory oracle equals the state machine's per-step single softmax (fp64 over
+    the dequantized int8 prefix and the valid ring slots) at every step, across several group
+    completions, from a prefill that ends inside a group."""
+    rng = np.random.default_rng(21)
+    hq, hkv, d, n0, S = 8, 2, 128, 100, 150
+    k = (rng.standard_normal((hkv, n0 + S, d)) * 0.8).astype(np.float16)
+    v = (rng.standard_normal((hkv, n0 + S, d)) * 0.8).astype(np.float16)
+    qs = (rng.standard_normal((S, hq, d)) * 0.6).astype(np.float16)
+    traj = ostream.decode_trajectory(k, v, qs, n0)
+    sc = ostream.StreamCache(1, hkv, d, 256, hq)
+    sc.begin_prefill(n0)
+    sc.set_prefill_pos(0)
+    sc.update(k[:, :n0], v[:, :n0], 0)
+    sc.finish_prefill(n0)
+    for i in range(S):
+        p = n0 + i
+        sc.pos = p
+        sc.update(k[:, p:p + 1], v[:, p:p + 1], 0)
+        n_g, qlen = sc.pg, sc.qlen
+        k16 = okq.dequantize_int8_token(sc.kq[0][:, :qlen], sc.kmn[0][:, :n_g], sc.kst[0][:, :n_g], 64)
+        v16 = okq.dequantize_int8_token(sc.vq[0][:, :qlen], sc.vmn[0][:, :n_g], sc.vst[0][:, :n_g], 64)
+        m = sc.ring_mask()
+        want, _ = oattn.attend_fp16_kv(qs[i], np.concatenate([k16, sc.tail_k[0][:, m]], 1),
+                                       np.concatenate([v16, sc.tail_v[0][:, m]], 1))
+        np.testing.assert_allclose(traj[i], want, rtol=1e-12, atol=1e-12, err_msg=f"step {i}")

@@ -146,3 +146,98 @@ def test_paged_graph_replay_equals_eager():
     for layer in range(LAYERS):
         assert torch.equal(e.pages[layer], g.pages[layer])
         assert torch.equal(e.rings[layer], g.rings[layer])
+
+
+def _bench_lengths():
+    """The batched ragged decode configuration's 8 sequence lengths (seed 3, uniform in [1024, 16384])."""
+    return [int(x) for x in torch.randint(1024, 16385, (8,), generator=torch.Generator().manual_seed(3))]
+
+
+def test_paged_bench_batch_against_oracle():
+    """The batched ragged configuration itself: the benchmark's 8 seeded lengths (4.6k-13.7k
+    tokens), 2 layers x 3 decode steps, every sequence's output against the oracle's single
+    softmax over its own int8 prefix and fp16 ring (the streaming criterion: 4 ULP or 1e-3)."""
+    from oracle import stream as ostream
+
+    lens, steps = _bench_lengths(), 3
+    print(f"case lens={lens}", flush=True)
+    ks, vs, qs = _data(lens, steps, seed=60)
+    paged = _paged(lens, steps, ks, vs, seed=61)
+    outs = torch.empty(steps, LAYERS, len(lens), HQ, 1, D, dtype=torch.float16, device="cuda")
+    for i in range(steps):
+        kn = torch.cat([ks[b][:, :, n + i:n + i + 1] for b, n in enumerate(lens)], 0)
+        vn = torch.cat([vs[b][:, :, n + i:n + i + 1] for b, n in enumerate(lens)], 0)
+        for layer in range(LAYERS):
+            outs[i, layer].copy_(paged.decode_step(kn, vn, qs[i], layer))
+        paged.advance()
+    torch.cuda.synchronize()
+    got = npy(outs)
+    q_all = np.stack([npy(q) for q in qs])  # [steps, B, HQ, 1, D]
+    for b, n in enumerate(lens):
+        want = ostream.decode_trajectory(npy(ks[b])[0], npy(vs[b])[0], q_all[:, b, :, 0], n)
+        for layer in range(LAYERS):  # the layers hold the same tokens in separate page pools
+            for i in range(steps):
+                assert_ulp_or_abs(got[i, layer, b, :, 0], want[i], 4.0, 1e-3, f"b={b} n={n} layer={layer} step={i}")
+
+
+def test_bucket_padding_is_never_read():
+    """The reference pads a sequence's capacity to its bucket (src/nova/decode.py:39-48) and
+    masks the padding to -inf (decode.py:200-205). Here the padding is never read: with every
+    sequence's pages reserved up to bucket_for(its length), the padded pages and the ring slots
+    holding positions already in the int8 prefix filled with garbage, decoding gives outputs
+    identical bit for bit to a cache without padding."""
+    from nova_amd.decode import bucket_for
+
+    lens, steps = [1000, 2100, 70, 4100], 70
+    ks, vs, qs = _data(lens, steps, seed=70)
+    plain = _paged(lens, steps, ks, vs, seed=71)
+    from nova_amd.paged import PagedKVInt8Cache
+
+    per_seq = max(-(-bucket_for(n + steps + 1) // 64) for n in lens)
+    padded = PagedKVInt8Cache(LAYERS, H_KV, D, HQ, max_seqs=len(lens), num_pages=per_seq * len(lens),
+                              max_pages_per_seq=per_seq)
+    g = torch.Generator(device="cuda").manual_seed(72)
+    for b, n in enumerate(lens):
+        padded.reserve(b, bucket_for(n + steps + 1))
+        for layer in range(LAYERS):
+            pool = padded.pages[layer]
+            pool.copy_(torch.randint(0, 256, pool.shape, generator=g, device="cuda", dtype=torch.uint8))
+    for b, n in enumerate(lens):
+        for layer in range(LAYERS):
+            padded.prefill(b, layer, ks[b][:, :, :n], vs[b][:, :, :n])
+            # stale ring slots (positions already in the int8 prefix) get garbage too
+            for i in range(64):
+                pos = (n - 1) - ((n - 1 - i) % 64)
+                if pos < n // 64 * 64:
+                    padded.rings[layer][b, :, :, i] = torch.randn(H_KV, 2, D, generator=g, device="cuda").half() * 50
+    padded.plan(lens)
+    _set_parts(padded, [int(plain.seq_parts[2 * b + 1]) for b in range(len(lens))])
+    for i in range(steps):
+        kn = torch.cat([ks[b][:, :, n + i:n + i + 1] for b, n in enumerate(lens)], 0)
+        vn = torch.cat([vs[b][:, :, n + i:n + i + 1] for b, n in enumerate(lens)], 0)
+        for layer in range(LAYERS):
+            a = plain.decode_step(kn, vn, qs[i], layer).clone()
+            p = padded.decode_step(kn, vn, qs[i], layer)
+            assert torch.equal(a, p), (i, layer)
+            assert torch.equal(plain.lse[:len(lens)], padded.lse[:len(lens)]), (i, layer)
+        plain.advance()
+        padded.advance()
+
+
+def test_released_sequence_appends_and_attends_nothing():
+    """A released sequence's table row is -1: a plan that still names it neither writes into the
+    pages (which may now belong to another sequence) nor reads them; its output is 0."""
+    lens, steps = [300, 500], 2
+    ks, vs, qs = _data(lens, steps, seed=80)
+    cache = _paged(lens, steps, ks, vs, seed=81)
+    before = [p.clone() for p in cache.pages]
+    cache.release(1)
+    kn = torch.cat([ks[b][:, :, n:n + 1] for b, n in enumerate(lens)], 0)
+    vn = torch.cat([vs[b][:, :, n:n + 1] for b, n in enumerate(lens)], 0)
+    cache.pos[1] = lens[1]  # a stale position, as a plan captured before the release would hold
+    out = cache.decode_step(kn, vn, qs[0], 0).clone()
+    torch.cuda.synchronize()
+    assert int(out[1].abs().sum()) == 0 and bool(torch.isinf(cache.lse[1]).all())
+    assert torch.isfinite(out[0]).all() and float(out[0].abs().sum()) > 0
+    changed = (cache.pages[0] != before[0]).any(dim=2).any(dim=1).nonzero().flatten().tolist()
+    assert set(changed) <= set(cache._owned[0]), "only sequence 0's pages may change"
