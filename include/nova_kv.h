@@ -6,7 +6,8 @@
  * that torch is capturing on to record the launch into a hipGraph). Nothing
  * here allocates device memory, synchronizes the device or reads device memory
  * on the host, so every call is safe inside stream capture. Scratch memory
- * (`workspace`) is owned by the caller.
+ * (`workspace`) is owned by the caller, except for nkv_decode_step_static_t64, whose
+ * scratch is a fixed array the library holds on each GPU.
  *
  * Return value: NKV_OK, or a NKV_ERR_* code; `nkv_last_error()` then returns
  * a message for the calling thread. Launches are asynchronous: a fault inside
@@ -28,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 4
+#define NKV_ABI_VERSION 5
 
 #define NKV_OK 0
 #define NKV_ERR_INVALID 1     /* argument outside what the reference accepts */
@@ -185,6 +186,36 @@ int nkv_decode_step_combine_t64(const uint16_t* q, const uint16_t* k_new, const 
                                 int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out,
                                 float* lse_out, void* workspace, int64_t workspace_bytes,
                                 int64_t n_parts, void* stream);
+
+/* Limits of nkv_decode_step_static_t64's scratch: partial results, and the publication
+ * area (completion counters and flags). */
+#define NKV_STATIC_PART_BYTES (4 << 20)
+#define NKV_STATIC_SYNC_BYTES 16384
+
+/*
+ * nkv_decode_step_t64 without a workspace argument. It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under hipGraph
+ * capture that may not call hipMalloc, tight serving loops, harnesses that forbid
+ * allocation). Same arguments, kernels, cache state and output, bit for bit, as
+ * nkv_decode_step_t64 with the same n_parts; neither the caller nor the call allocates.
+ * The partials and the counters live in a scratch array of NKV_STATIC_PART_BYTES +
+ * NKV_STATIC_SYNC_BYTES bytes that the library holds on every GPU it runs on until the
+ * process ends. Its address is looked up on the first call on a device (the current
+ * device), which also clears the publication area with a kernel on `stream`; every
+ * call leaves it cleared.
+ * A call needs hkv * n_parts * 4 * (gq * 128 + ((2 * gq + 3) & ~3)) partial bytes
+ * (gq = hq / hkv) <= NKV_STATIC_PART_BYTES and 4 * hkv * (1 + n_parts) publication bytes
+ * <= NKV_STATIC_SYNC_BYTES; larger calls return NKV_ERR_UNSUPPORTED.
+ * All calls on one GPU share its array: calls that overlap on one GPU (other streams,
+ * other threads) race and give wrong results. Calls in order on one stream do not.
+ */
+int nkv_decode_step_static_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                               int64_t kv_head_stride, uint8_t* kq, uint16_t* kmn, uint16_t* kst,
+                               uint8_t* vq, uint16_t* vmn, uint16_t* vst, uint16_t* tail_k,
+                               uint16_t* tail_v, const int64_t* pos_dev, const int64_t* first_dev,
+                               int64_t* written_dev, int64_t* qlen_dev, int64_t* pg_dev, int64_t hq,
+                               int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out,
+                               float* lse_out, int64_t n_parts, void* stream);
 
 /*
  * fp16 ring attention with a boolean slot mask and its log-sum-exp.

@@ -34,6 +34,8 @@ I64 = c_int64
 # q, k_new, v_new, kv_head_stride, kq, kmn, kst, vq, vmn, vst, tail_k, tail_v, pos, first, written,
 # qlen, pg, hq, hkv, head_dim, capacity, out, lse, workspace, workspace_bytes, n_parts, stream
 _STEP = [P, P, P, I64, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, P, P, P, I64, I64, P]
+# the same without workspace and workspace_bytes
+_STEP_STATIC = _STEP[:23] + _STEP[25:]
 # q, k_new, v_new, kv_head_stride, kq, ksc, vq, vsc, pos, written, hq, hkv, head_dim, capacity, out,
 # lse, workspace, workspace_bytes, n_parts, stream
 _STEP_TOK = [P, P, P, I64, P, P, P, P, P, P, I64, I64, I64, I64, P, P, P, I64, I64, P]
@@ -51,6 +53,7 @@ SIGNATURES = {
     "nkv_decode_step_t64": (c_int, _STEP),
     "nkv_decode_step_partials_t64": (c_int, _STEP),
     "nkv_decode_step_combine_t64": (c_int, _STEP),
+    "nkv_decode_step_static_t64": (c_int, _STEP_STATIC),
     "nkv_tail_attend": (c_int, [P, P, P, P, I64, I64, I64, I64, P, P, P]),
     "nkv_ring_mask": (c_int, [P, P, P, I64, P, P]),
     "nkv_quantize_tok": (c_int, [P, c_int, I64, I64, I64, I64, P, I64, P, I64, P]),
@@ -78,7 +81,7 @@ SIGNATURES = {
     "nkv_qk_norm_rope": (c_int, [P, I64, I64, I64, P, P, c_float, P, P, P]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lib = None
 _lock = threading.Lock()

@@ -35,6 +35,8 @@
 // blocks, so no data moves between the two products.
 #include "nkv_common.h"
 
+#include <mutex>
+
 namespace nkv {
 
 #ifndef NKV_WAVES
@@ -1587,6 +1589,12 @@ __global__ __launch_bounds__(128) void append_tok_kernel(AttnArgs a) {
   if (blockIdx.x == 0 && threadIdx.x == 0) write_scalars(a, pos);
 }
 
+// Zeroes `n` ints (n a multiple of 4, p 16-byte aligned) with vector stores.
+__global__ __launch_bounds__(256) void clear_ints_kernel(int* p, int n) {
+  for (int i = 4 * (blockIdx.x * 256 + threadIdx.x); i < n; i += 4 * 256 * gridDim.x)
+    *reinterpret_cast<int4*>(p + i) = int4{0, 0, 0, 0};
+}
+
 __global__ void ring_mask_kernel(const int64_t* written, const int64_t* qlen, const int64_t* first,
                                  int64_t slots, uint8_t* mask) {
   const int i = threadIdx.x;
@@ -2106,6 +2114,73 @@ extern "C" int nkv_decode_step_combine_t64(const uint16_t* q, const uint16_t* k_
   return decode_step("decode_step_combine_t64", LAUNCH_TAIL, q, k_new, v_new, kv_head_stride, kq, kmn, kst, vq, vmn, vst, tail_k, tail_v, pos_dev, first_dev,
                      written_dev, qlen_dev, pg_dev, hq, hkv, head_dim, capacity, out, lse_out, workspace,
                      workspace_bytes, n_parts, stream);
+}
+
+// ---- the decode step on a library-held scratch array (no allocation anywhere)
+//
+// Layout: [partials: NKV_STATIC_PART_BYTES | publication area: NKV_STATIC_SYNC_BYTES]. The
+// step writes partials upward from the start and keeps its counters and flags downward from
+// the end, so any mix of configurations within the limits keeps the two regions apart, and
+// the publication area, cleared once, stays cleared (each call leaves its counters at zero).
+constexpr int64_t STATIC_BYTES = int64_t(NKV_STATIC_PART_BYTES) + NKV_STATIC_SYNC_BYTES;
+static_assert(NKV_STATIC_PART_BYTES % 256 == 0 && NKV_STATIC_SYNC_BYTES % 256 == 0, "256-byte regions");
+
+static __device__ __align__(256) unsigned char scratch[STATIC_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[MAX_DEVICES];  // device address of `scratch` per device, set once
+
+// Device address of the current device's `scratch`. The first call on a device looks it up
+// (the host-side name is not a device address) and clears the publication area with a kernel
+// on `s`, ordered before the caller's launches on that stream.
+int static_scratch(hipStream_t s, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+    return fail(NKV_ERR_HIP, "decode_step_static_t64: no usable current device (%d)", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(NKV_ERR_HIP, "decode_step_static_t64: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    int* sync = reinterpret_cast<int*>(static_cast<unsigned char*>(p) + NKV_STATIC_PART_BYTES);
+    const int n = NKV_STATIC_SYNC_BYTES / (int)sizeof(int);
+    hipLaunchKernelGGL(clear_ints_kernel, dim3((unsigned)cdiv(n, 4 * 256)), dim3(256), 0, s, sync, n);
+    if (int rc = check_launch("decode_step_static_t64: clear")) return rc;
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return NKV_OK;
+}
+}  // namespace
+
+extern "C" int nkv_decode_step_static_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                                          int64_t kv_head_stride, uint8_t* kq, uint16_t* kmn, uint16_t* kst,
+                                          uint8_t* vq, uint16_t* vmn, uint16_t* vst, uint16_t* tail_k,
+                                          uint16_t* tail_v, const int64_t* pos_dev, const int64_t* first_dev,
+                                          int64_t* written_dev, int64_t* qlen_dev, int64_t* pg_dev, int64_t hq,
+                                          int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out,
+                                          float* lse_out, int64_t n_parts, void* stream) {
+  const char* what = "decode_step_static_t64";
+  set_error("");
+  if (int rc = check_heads(hq, hkv, head_dim)) return rc;
+  if (capacity <= 0) return fail(NKV_ERR_INVALID, "capacity must be positive");
+  if (n_parts < 0) return fail(NKV_ERR_INVALID, "%s: n_parts %lld is negative", what, (long long)n_parts);
+  if (n_parts == 0) n_parts = default_parts(hkv, cdiv(capacity, GT));
+  const int64_t part_bytes = hkv * n_parts * part_floats(hq, hkv) * (int64_t)sizeof(float);
+  const int64_t sync = sync_bytes(hkv, n_parts);
+  if (part_bytes > NKV_STATIC_PART_BYTES || sync > NKV_STATIC_SYNC_BYTES)
+    return fail(NKV_ERR_UNSUPPORTED,
+                "%s: %lld partial bytes and %lld publication bytes exceed the static scratch (%d and %d bytes)",
+                what, (long long)part_bytes, (long long)sync, NKV_STATIC_PART_BYTES, NKV_STATIC_SYNC_BYTES);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  if (int rc = static_scratch(s, &ws)) return rc;
+  return decode_step(what, LAUNCH_PREFIX | LAUNCH_TAIL, q, k_new, v_new, kv_head_stride, kq, kmn, kst, vq, vmn, vst,
+                     tail_k, tail_v, pos_dev, first_dev, written_dev, qlen_dev, pg_dev, hq, hkv, head_dim, capacity,
+                     out, lse_out, ws, STATIC_BYTES, n_parts, stream);
 }
 
 extern "C" int nkv_tail_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v,

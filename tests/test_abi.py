@@ -116,6 +116,12 @@ def test_validation_errors_return_before_launch(lib):
     assert lib.nkv_gemv(fake, None, 1e-6, w2, 1 << 31, 64, None, r3, None) == _lib.NKV_ERR_INVALID
     assert lib.nkv_qk_norm_rope(fake, 32, 8, 64, fake, fake, 1e-6, fake, fake, None) == _lib.NKV_ERR_UNSUPPORTED
     assert b"head_dim" in lib.nkv_last_error()
+    # the decode step on the library's scratch array: 8 KV heads x 64 parts of 16 query
+    # heads need 4.26 MB of partials, more than the array's 4 MiB
+    step = [fake] * 3 + [128] + [fake] * 13 + [128, 8, 128, 1 << 16, fake, fake]
+    assert lib.nkv_decode_step_static_t64(*step, 64, None) == _lib.NKV_ERR_UNSUPPORTED
+    assert b"static scratch" in lib.nkv_last_error()
+    assert lib.nkv_decode_step_static_t64(*step, -1, None) == _lib.NKV_ERR_INVALID
 
 
 def test_product_path_refuses_to_run_without_gpu():
