@@ -413,14 +413,15 @@ def run_decode(args, scheme: str, headline: bool) -> dict:
     return res
 
 
-def run_paged(args, steps: int | None = None) -> dict:
+def run_paged(args, steps: int | None = None, scheme: str = "t64") -> dict:
     """Batched ragged decode: 8 sequences with seeded uniform lengths in [1024, 16384] (seed 3),
-    36 layers, int8t64 pages of 64 tokens; one step = every layer's append + attention for all 8
-    sequences, captured as one hipGraph. Batch tokens/s; GB/s over the algorithmic bytes of the
-    valid tokens (padding excluded)."""
+    36 layers, pages of 64 tokens (int8t64, or the per-token symmetric format with
+    ``scheme="tok"``); one step = every layer's append + attention for all 8 sequences, captured
+    as one hipGraph. Batch tokens/s; GB/s over the algorithmic bytes of the valid tokens (padding
+    excluded)."""
     import torch
 
-    from nova_amd.paged import PagedKVInt8Cache
+    from nova_amd.paged import PagedKVInt8Cache, PagedKVInt8TokCache
 
     dev = torch.device("cuda:0")
     L, B, W = args.layers, 8, args.warmup
@@ -428,7 +429,8 @@ def run_paged(args, steps: int | None = None) -> dict:
     lens = [int(x) for x in torch.randint(1024, 16385, (B,), generator=torch.Generator().manual_seed(3))]
     per_seq = max(-(-(n + W + K + 2) // 64) for n in lens)
     total_pages = sum(-(-(n + W + K + 2) // 64) for n in lens)
-    cache = PagedKVInt8Cache(L, HKV, D, HQ, max_seqs=B, num_pages=total_pages, max_pages_per_seq=per_seq, device=dev)
+    cls = PagedKVInt8TokCache if scheme == "tok" else PagedKVInt8Cache
+    cache = cls(L, HKV, D, HQ, max_seqs=B, num_pages=total_pages, max_pages_per_seq=per_seq, device=dev)
     g = torch.Generator(device=dev).manual_seed(3)
     for b, n in enumerate(lens):
         cache.reserve(b, n + W + K + 1)
@@ -454,11 +456,12 @@ def run_paged(args, steps: int | None = None) -> dict:
     ms = _time_graph(graph, stream, K, 0)
     cache.note_advanced(K)
     assert torch.isfinite(cache.merged[:B]).all()
-    step_bytes = sum(sum(attn_bytes(n + W + i + 1) + APPEND_BYTES for n in lens) for i in range(K)) / K * L
+    step_bytes = sum(sum(step_launch_bytes(n + W + i + 1, scheme) for n in lens) for i in range(K)) / K * L
     gbs = step_bytes / (ms / 1e3) / 1e9
     res = {"metric": "paged ragged batch int8-KV decode: batch tokens/s + achieved HBM GB/s (% of peak)",
            "value": round(B / (ms / 1e3), 2), "unit": "tokens/s", "steps": K, "ms_per_step": round(ms, 4),
-           "config": {"workload": f"paged int8t64 decode, {B} ragged sequences (lengths {lens}), {L} layers x "
+           "config": {"workload": f"paged {'per-token symmetric int8' if scheme == 'tok' else 'int8t64'} decode, "
+                                  f"{B} ragged sequences (lengths {lens}), {L} layers x "
                                   "(32 q / 8 kv heads, head_dim 128), 64-token pages, hipGraph-replayed steps",
                       "lengths": lens, "layers": L, "page_tokens": 64, "work_units_per_head": cache.total_parts},
            "step_gbs": round(gbs, 1), "step_pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
@@ -601,7 +604,7 @@ def main() -> int:
     _lib.load()
     torch.cuda.set_device(0)
     if args.workload == "paged":
-        res = _standalone(run_paged(args, args.steps if args.steps != 256 else None), args)
+        res = _standalone(run_paged(args, args.steps if args.steps != 256 else None, args.scheme), args)
     elif args.workload == "prefill":
         res = _standalone(run_prefill(args, args.steps if args.steps != 256 else None), args)
     elif args.workload == "e2e":
@@ -616,6 +619,7 @@ def main() -> int:
             extra = {}
             for name, fn in (("tok_decode", lambda: run_decode(args, "tok", headline=False)),
                              ("paged_batch", lambda: run_paged(args)),
+                             ("paged_batch_tok", lambda: run_paged(args, scheme="tok")),
                              ("chunked_prefill", lambda: run_prefill(args))):
                 try:
                     extra[name] = fn()

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 5
+#define NKV_ABI_VERSION 6
 
 #define NKV_OK 0
 #define NKV_ERR_INVALID 1     /* argument outside what the reference accepts */
@@ -364,6 +364,44 @@ int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const ui
                               int64_t head_dim, const int32_t* wg_map, const int32_t* seq_parts,
                               int64_t total_parts, uint16_t* out, float* lse_out, void* workspace,
                               int64_t workspace_bytes, void* stream);
+
+/*
+ * ---- Paged batch in the per-token symmetric format ----
+ * Per-token, per-KV-head symmetric int8 codes with one fp16 scale per token and KV head (the
+ * arithmetic of nkv_quantize_tok) in a paged, 128-byte-aligned layout. It replaces the
+ * contiguous [B, H_kv, max_len, D] storage of KVInt8Cache (src/nova/kvattn.py:589-601) for a
+ * batch of sequences; the reference has no paged layout and no per-token format.
+ * pages: uint8 [num_pages][hkv][NKV_PAGE_TOK_BYTES], one page = 64 tokens of one KV head:
+ *   K codes int8 [64][128], V codes int8 [64][128], then fp16 K scales [64], V scales [64].
+ *   Token p of a sequence is row p % 64 of its page page_table[b * table_stride + p / 64].
+ * page_table, pos_dev, k_new / v_new, wg_map / seq_parts, q / out / lse_out, workspace: as for
+ *   the int8t64 paged batch above. There are no rings.
+ */
+#define NKV_PAGE_T64_BYTES 17408
+#define NKV_PAGE_TOK_BYTES 16640
+
+/* Tokens first_token .. first_token + n - 1 of one sequence quantized straight into its pages
+ * (nkv_quantize_tok's arithmetic, bit for bit): x [hkv][n][128] (head stride x_head_stride
+ * elements, NKV_F16 / NKV_BF16 / NKV_F32); token first_token + t goes to row (first_token + t)
+ * % 64 of tensor `which` (0 K, 1 V) of KV head h in page table_row[(first_token + t) / 64],
+ * its scale beside. Tokens whose entry is outside [0, num_pages) are skipped. Replaces the
+ * prefill store of KVInt8Cache.update (src/nova/kvattn.py:668-698) for this layout. */
+int nkv_paged_quantize_tok(const void* x, int x_dtype, int64_t x_head_stride, int64_t hkv, int64_t n, int which,
+                           uint8_t* pages, const int32_t* table_row, int64_t first_token, int64_t num_pages,
+                           void* stream);
+
+/* One decode step of every sequence in one launch: the token at pos_dev[b] is quantized into
+ * its page (by the first prefix workgroup of each sequence and KV head), and each sequence
+ * attends over its tokens [0, pos_b] (the prefix [0, pos_b) from the pages, the new token
+ * quantized and dequantized in the tail exactly as stored). A sequence whose page of pos_b is
+ * missing neither appends nor attends (output 0, lse -inf). */
+int nkv_paged_decode_step_tok(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                              int64_t kv_seq_stride, int64_t kv_head_stride, uint8_t* pages,
+                              const int32_t* page_table, int64_t table_stride, int64_t num_pages,
+                              const int64_t* pos_dev, int64_t nseq, int64_t hq, int64_t hkv, int64_t head_dim,
+                              const int32_t* wg_map, const int32_t* seq_parts, int64_t total_parts,
+                              uint16_t* out, float* lse_out, void* workspace, int64_t workspace_bytes,
+                              void* stream);
 
 /*
  * ---- Chunked prefill attention over the int8t64 cache (MFMA) ----

@@ -69,6 +69,9 @@ SIGNATURES = {
     "nkv_paged_attn_decode_t64": (c_int, [P, P, P, I64, I64, P, P, I64, I64, I64, I64, P, P, I64, P, P, P, I64, P]),
     "nkv_paged_decode_step_t64": (c_int, [P, P, P, I64, I64, P, P, I64, I64, P, P, I64, I64, I64, I64, P, P, I64, P,
                                           P, P, I64, P]),
+    "nkv_paged_quantize_tok": (c_int, [P, c_int, I64, I64, I64, c_int, P, P, I64, I64, P]),
+    "nkv_paged_decode_step_tok": (c_int, [P, P, P, I64, I64, P, P, I64, I64, P, I64, I64, I64, I64, P, P, I64, P,
+                                          P, P, I64, P]),
     "nkv_prefill_workspace_bytes": (I64, [I64, I64, I64, I64]),
     "nkv_prefill_default_splits": (I64, [I64, I64, I64, I64]),
     "nkv_prefill_attn_t64": (c_int, [P, P, P, I64, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, I64, I64, P]),
@@ -81,7 +84,7 @@ SIGNATURES = {
     "nkv_qk_norm_rope": (c_int, [P, I64, I64, I64, P, P, c_float, P, P, P]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lib = None
 _lock = threading.Lock()

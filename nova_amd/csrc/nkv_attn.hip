@@ -67,7 +67,10 @@ constexpr int RING_BYTES = GT * D * 2;                    // one fp16 ring tenso
 // paged layout: one page = one 64-token group of one KV head, K codes | V codes | kst | kmn | vst | vmn
 constexpr int PAGE_BYTES = 2 * CODE_BYTES + RULER_BYTES;  // 17 KiB, a multiple of 128
 constexpr int DMA_FIRST_HALF_PAGED = 2 * (HALF_CODE / 1024) + 1;  // the rulers are one 1 KiB load
-enum Layout : int { CONTIG_T64 = 0, CONTIG_TOK = 1, PAGED_T64 = 2 };
+// paged per-token symmetric layout: one page = 64 tokens of one KV head, K codes | V codes |
+// K scales (64 fp16) | V scales
+constexpr int PAGE_TOK_BYTES = 2 * CODE_BYTES + 2 * GT * 2;  // 16640, a multiple of 128
+enum Layout : int { CONTIG_T64 = 0, CONTIG_TOK = 1, PAGED_T64 = 2, PAGED_TOK = 3 };
 constexpr float P_SCALE = 32768.0f;       // 2^15
 constexpr float P_SCALE_LOG2 = 15.0f;
 constexpr float INV_P_SCALE = 1.0f / 32768.0f;
@@ -76,6 +79,7 @@ constexpr float LN2 = 0.6931471805599453f;
 constexpr float NEG_INF = -__builtin_huge_valf();
 
 static_assert(DMA_FIRST_HALF == 12 && DMA_SECOND_HALF == 8 && DMA_HALF_TOK == 10, "loads per half group");
+static_assert(PAGE_BYTES % 128 == 0 && PAGE_TOK_BYTES % 128 == 0, "pages are 128-byte aligned");
 static_assert(LDS_BYTES <= 150 * 1024 && LDS_BYTES_TOK <= 150 * 1024, "LDS of one workgroup");
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -339,6 +343,37 @@ __device__ __forceinline__ void issue_half_paged(const AttnArgs& a, int b, int h
     dma16_stream(pb, (uint32_t)(CODE_BYTES + (32 * hf + row) * D + (((lane & 7) ^ swz(row)) << 4)), slot + HALF_CODE + 1024 * j);
   }
   if (hf == 0) dma16_stream(pb, (uint32_t)(2 * CODE_BYTES + 16 * lane), __builtin_amdgcn_readfirstlane(rs));
+}
+
+// The paged per-token symmetric layout's half group: 4 + 4 loads of code rows from the page,
+// then the half's 32 K and 32 V scales (one load each, 4 lanes), into the same slot layout as
+// issue_half_tok.
+__device__ __forceinline__ void issue_half_paged_tok(const AttnArgs& a, int b, int h, int64_t grp, int hf,
+                                                     uint32_t slot) {
+  const int lane = threadIdx.x & 63;
+  const int64_t page = max<int64_t>(page_of(a, b, grp), 0);  // as in issue_half_paged
+  const void* pb = uniform_ptr(a.pages + (page * a.hkv + h) * PAGE_TOK_BYTES);
+  slot = __builtin_amdgcn_readfirstlane(slot);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // earlier reads of this slot are done
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    dma16_stream(pb, (uint32_t)((32 * hf + row) * D + (((lane & 7) ^ swz(row)) << 4)), slot + 1024 * j);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    dma16_stream(pb, (uint32_t)(CODE_BYTES + (32 * hf + row) * D + (((lane & 7) ^ swz(row)) << 4)), slot + HALF_CODE + 1024 * j);
+  }
+  if (lane < 4) dma16_stream(pb, (uint32_t)(2 * CODE_BYTES + 64 * hf + 16 * lane), slot + 2 * HALF_CODE);
+  if (lane < 4) dma16_stream(pb, (uint32_t)(2 * CODE_BYTES + 2 * GT + 64 * hf + 16 * lane), slot + 2 * HALF_CODE + TOK_SCALE_BYTES);
+}
+
+// Half `hf` of group `grp` in the per-token symmetric format, from either layout.
+template <bool PAGED>
+__device__ __forceinline__ void issue_tok(const AttnArgs& a, int b, int h, int64_t grp, int hf, uint32_t slot) {
+  if constexpr (PAGED) issue_half_paged_tok(a, b, h, grp, hf, slot);
+  else issue_half_tok(a, h, grp, hf, slot);
 }
 
 // Q of KV head h (gq rows of 256 bytes) into LDS at `dst`, by one wave.
@@ -713,17 +748,20 @@ __device__ __forceinline__ float min4rows(float v) {
 __device__ __forceinline__ const uint16_t* ring_of(const AttnArgs& a, int h, int which) {
   return (which == 0 ? a.tail_k : a.tail_v) + (int64_t)h * a.tail_slots * D;
 }
-__device__ __forceinline__ const uint16_t* fresh_of(const AttnArgs& a, int h, int which) {
-  return (which == 0 ? a.k_new : a.v_new) + h * a.kv_hs;
+// The step's new token of KV head h (of sequence b in a batch: kv_ss is 0 otherwise).
+__device__ __forceinline__ const uint16_t* fresh_of(const AttnArgs& a, int b, int h, int which) {
+  return (which == 0 ? a.k_new : a.v_new) + (int64_t)b * a.kv_ss + (int64_t)h * a.kv_hs;
 }
 
 // The per-token symmetric append of the token at `pos`: waves 0 and 1 of the calling
 // workgroup quantize K and V of KV head h (lanes 0..15, 8 values each) and store the codes
 // and the fp16 scale at position pos.
+// (The fused tail quantizes the new token itself from k_new / v_new, so nothing in the launch
+// reads these stores; the prefix reads only the tokens before pos.)
 __device__ __forceinline__ void append_tok_rows(const AttnArgs& a, int h, int64_t pos) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (wave > 1 || lane >= 16) return;
-  const uint4 w = *reinterpret_cast<const uint4*>(fresh_of(a, h, wave) + 8 * lane);
+  const uint4 w = *reinterpret_cast<const uint4*>(fresh_of(a, 0, h, wave) + 8 * lane);
   const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
   float v[8];
 #pragma unroll
@@ -731,11 +769,26 @@ __device__ __forceinline__ void append_tok_rows(const AttnArgs& a, int h, int64_
   float scale;
   const uint2 cw = sym_quant8(v, scale);
   const int64_t row = (int64_t)h * a.capacity + pos;
-  // agent-scope stores: the fused tail of this launch reads the token
-  __hip_atomic_store(reinterpret_cast<uint64_t*>((wave == 0 ? a.kq : a.vq) + row * D + 8 * lane),
-                     __builtin_bit_cast(uint64_t, cw), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (lane == 0)
-    __hip_atomic_store((wave == 0 ? a.ksc : a.vsc) + row, f2h(scale), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  *reinterpret_cast<uint2*>((wave == 0 ? a.kq : a.vq) + row * D + 8 * lane) = cw;
+  if (lane == 0) ((wave == 0 ? a.ksc : a.vsc))[row] = f2h(scale);
+}
+
+// The same for sequence b of the paged layout: row pos % 64 of the page of pos (a valid page,
+// checked by the caller) and its scale.
+__device__ __forceinline__ void append_tok_rows_paged(const AttnArgs& a, int b, int h, int64_t pos) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (wave > 1 || lane >= 16) return;
+  const uint4 w = *reinterpret_cast<const uint4*>(fresh_of(a, b, h, wave) + 8 * lane);
+  const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = h2f((uint16_t)(wv[j >> 1] >> (16 * (j & 1))));
+  float scale;
+  const uint2 cw = sym_quant8(v, scale);
+  uint8_t* pg = a.pages + (page_of(a, b, pos / GT) * a.hkv + h) * PAGE_TOK_BYTES;
+  const int slot = (int)(pos % GT);
+  *reinterpret_cast<uint2*>(pg + wave * CODE_BYTES + slot * D + 8 * lane) = cw;
+  if (lane == 0) reinterpret_cast<uint16_t*>(pg + 2 * CODE_BYTES)[wave * GT + slot] = f2h(scale);
 }
 
 __device__ __forceinline__ void write_scalars(const AttnArgs& a, int64_t pos) {
@@ -782,7 +835,7 @@ __device__ __forceinline__ UnitIO unit_io(const AttnArgs& a, int h, int unit, in
   const int64_t gcur = pos / GT, ro = ((int64_t)h * a.ngroups_cap + gcur) * D;
   UnitIO io;
   io.ring = ring_of(a, h, which);
-  io.fresh = fresh_of(a, h, which);
+  io.fresh = fresh_of(a, 0, h, which);
   io.codes = (which == 0 ? a.kq : a.vq) + ((int64_t)h * a.capacity + gcur * GT) * D;
   io.code_rows = (int)min<int64_t>(GT, a.capacity - gcur * GT);
   io.mn = (which == 0 ? a.kmn : a.vmn) + ro;
@@ -1132,8 +1185,9 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   // ---- loads: the ring quarters (or the new token), q, the merging waves' partial columns
   const int which = wave >> 2, qtr = wave & 3;
   const bool completes = fused && pos_ok && !a.tok && (pos + 1) % GT == 0;  // the token completes its group
-  const bool tok1 = !PAGED && ring && a.tok;  // per-token symmetric fused step: the tail is the new token
-  const uint16_t* ring_h = PAGED ? a.rings + (((int64_t)b * a.hkv + h) * 2 + which) * GT * D : ring_of(a, h, which);
+  const bool tok1 = ring && a.tok;  // per-token symmetric fused step: the tail is the new token
+  const uint16_t* ring_h = tok1 ? nullptr
+                          : PAGED ? a.rings + (((int64_t)b * a.hkv + h) * 2 + which) * GT * D : ring_of(a, h, which);
   const bool fresh_on = ring && !tok1 && !PAGED && a.tail_mode == TAIL_FUSED;
   const int fresh_slot = (int)(pos % GT);
   uint4 rq0 = {0u, 0u, 0u, 0u}, rq1 = rq0, rq2 = rq0, rq3 = rq0;  // rows 16 qtr + (lane >> 4) + 4 i
@@ -1146,11 +1200,11 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     rq3 = *reinterpret_cast<const uint4*>(ring_h + min(16 * qtr + rl + 12, slots - 1) * D + 8 * cl);
     // the new token's slot: from the step's input, not the ring this launch writes. Loaded into
     // registers of its own and stored over its row once the quarter is in LDS.
-    const uint16_t* fp = fresh_on ? fresh_of(a, h, which) : ring_h;  // a valid row either way
+    const uint16_t* fp = fresh_on ? fresh_of(a, b, h, which) : ring_h;  // a valid row either way
     fresh = *reinterpret_cast<const uint4*>(fp + 8 * (lane & 15));
   }
   uint4 tokw = {0u, 0u, 0u, 0u};
-  if (tok1 && qtr == 0 && lane < 16) tokw = *reinterpret_cast<const uint4*>(fresh_of(a, h, which) + 8 * lane);
+  if (tok1 && qtr == 0 && lane < 16) tokw = *reinterpret_cast<const uint4*>(fresh_of(a, b, h, which) + 8 * lane);
   const int64_t first = (!PAGED && ring && a.first_dev) ? *a.first_dev : 0;
   const bool mask_on = ring && a.tail_mode == TAIL_MASK && lane < a.tail_slots && a.tail_mask[lane] != 0;
   half8_t qb[4];
@@ -1334,7 +1388,8 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
 
 template <int LAYOUT>
 __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
-  constexpr bool TOK = LAYOUT == CONTIG_TOK, PAGED = LAYOUT == PAGED_T64;
+  constexpr bool TOK = LAYOUT == CONTIG_TOK || LAYOUT == PAGED_TOK;
+  constexpr bool PAGED = LAYOUT == PAGED_T64 || LAYOUT == PAGED_TOK;
   __shared__ __attribute__((aligned(16))) uint8_t lds_raw[TOK ? LDS_BYTES_TOK : LDS_BYTES];
   __shared__ __attribute__((aligned(16))) uint16_t unit_src[TOK || PAGED ? 8 : UNIT_SRC_BYTES / 2];
   __shared__ __attribute__((aligned(16))) uint16_t q_lds[16 * D];
@@ -1363,15 +1418,18 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   bool pos_ok;
   int64_t U;
   if constexpr (PAGED) {
-    pos = a.pos_dev[b];  // the ring holds the group of pos (appended before this launch)
+    // int8t64: the ring holds the group of pos (appended before this launch); per-token
+    // symmetric: the prefix is every token before pos, and this launch appends pos
+    pos = a.pos_dev[b];
     pos_ok = pos >= 0 && page_of(a, b, pos / GT) >= 0;  // the current group has a page
-    U = pos_ok ? pos / GT * GT : 0;
+    U = pos_ok ? (TOK ? pos : pos / GT * GT) : 0;
   } else {
     U = prefix_limit(a, pos, pos_ok);
   }
   // the fused step's append: int8t64 units in parts < APPEND_UNITS (the grid has at least
-  // that many parts), the per-token symmetric token in part 0
-  const bool append = !PAGED && a.tail_mode == TAIL_FUSED && pos_ok && (TOK ? part == 0 : part < APPEND_UNITS);
+  // that many parts), the per-token symmetric token in part 0 (of each sequence when paged;
+  // the paged int8t64 step appends in a launch of its own)
+  const bool append = (PAGED ? TOK : a.tail_mode == TAIL_FUSED) && pos_ok && (TOK ? part == 0 : part < APPEND_UNITS);
   const bool prefix = part < nparts;
 
   const int64_t W = (U + GT - 1) / GT;
@@ -1393,8 +1451,8 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
 
   if (wave < ng) {
     if constexpr (TOK) {
-      issue_half_tok(a, h, gs + wave, 0, my_lds);
-      issue_half_tok(a, h, gs + wave, 1, my_lds + HALF_SLOT_TOK);
+      issue_tok<PAGED>(a, b, h, gs + wave, 0, my_lds);
+      issue_tok<PAGED>(a, b, h, gs + wave, 1, my_lds + HALF_SLOT_TOK);
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_HALF_TOK) : "memory");
     } else if constexpr (PAGED) {
       issue_half_paged(a, b, h, gs + wave, 0, my_lds, rul_lds);
@@ -1411,9 +1469,10 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   __syncthreads();
 
   if (append) {
-    if constexpr (TOK) append_tok_rows(a, h, pos);
+    if constexpr (PAGED) append_tok_rows_paged(a, b, h, pos);
+    else if constexpr (TOK) append_tok_rows(a, h, pos);
     else append_unit(uio, part, pos, unit_src, xch);
-    if (blockIdx.x == 0 && tid == 0) write_scalars(a, pos);
+    if (!PAGED && blockIdx.x == 0 && tid == 0) write_scalars(a, pos);
   }
 
   if (prefix) {
@@ -1444,13 +1503,13 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
       // second half (slot 1)
       const int nv2 = (int)min<int64_t>(32, U - grp * GT - 32);
       if constexpr (TOK) {
-        if (nx < ng) issue_half_tok(a, h, gs + nx, 0, my_lds);
+        if (nx < ng) issue_tok<PAGED>(a, b, h, gs + nx, 0, my_lds);
         if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_HALF_TOK) : "memory");
         else wait_groups_all();
         if (nv2 > 0)
           attend_block_tok(a, st, qb, slot1, slot1 + HALF_CODE, reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE),
                            reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE + TOK_SCALE_BYTES), nv2);
-        if (nx < ng) issue_half_tok(a, h, gs + nx, 1, my_lds + HALF_SLOT_TOK);
+        if (nx < ng) issue_tok<PAGED>(a, b, h, gs + nx, 1, my_lds + HALF_SLOT_TOK);
       } else if constexpr (PAGED) {
         if (nx < ng) issue_half_paged(a, b, h, gs + nx, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
         if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF_PAGED) : "memory");
@@ -2313,17 +2372,18 @@ extern "C" int64_t nkv_paged_workspace_bytes(int64_t hkv, int64_t hq, int64_t to
   return hkv * total_parts * part_floats(hq, hkv) * (int64_t)sizeof(float) + ctr_bytes(hkv * total_parts);
 }
 
+// (`rings` is NULL for the per-token symmetric format, which keeps none)
 static int paged_args(const char* what, AttnArgs& a, const uint8_t* pages, const int32_t* page_table,
                       int64_t table_stride, int64_t num_pages, const uint16_t* rings, const int64_t* pos_dev,
-                      int64_t nseq, int64_t hkv, int64_t head_dim) {
+                      int64_t nseq, int64_t hkv, int64_t head_dim, bool tok = false) {
   if (head_dim != D) return fail(NKV_ERR_UNSUPPORTED, "head_dim %lld: the HIP kernels are built for head_dim 128", (long long)head_dim);
   if (num_pages <= 0 || num_pages > (int64_t(1) << 31))
     return fail(NKV_ERR_INVALID, "%s: num_pages %lld", what, (long long)num_pages);
   if (nseq <= 0 || nseq > 32767 || hkv <= 0 || table_stride <= 0)
     return fail(NKV_ERR_INVALID, "%s: bad sizes nseq=%lld hkv=%lld table_stride=%lld", what, (long long)nseq,
                 (long long)hkv, (long long)table_stride);
-  if (!pages || !page_table || !rings || !pos_dev) return fail(NKV_ERR_INVALID, "%s: null pointer argument", what);
-  if (!al16(pages) || !al16(rings)) return fail(NKV_ERR_UNSUPPORTED, "%s: buffers must be 16-byte aligned", what);
+  if (!pages || !page_table || (!tok && !rings) || !pos_dev) return fail(NKV_ERR_INVALID, "%s: null pointer argument", what);
+  if (!al16(pages) || (!tok && !al16(rings))) return fail(NKV_ERR_UNSUPPORTED, "%s: buffers must be 16-byte aligned", what);
   a.pages = const_cast<uint8_t*>(pages);
   a.table = page_table;
   a.table_stride = table_stride;
@@ -2334,6 +2394,7 @@ static int paged_args(const char* what, AttnArgs& a, const uint8_t* pages, const
   a.hkv = (int)hkv;
   a.tail_mode = TAIL_FUSED;
   a.tail_slots = GT;
+  a.tok = tok ? 1 : 0;
   return NKV_OK;
 }
 
@@ -2355,18 +2416,27 @@ extern "C" int nkv_paged_append_t64(const uint16_t* k_new, const uint16_t* v_new
   return check_launch("paged_append_t64");
 }
 
+// The paged prefix launch with its fused tails. int8t64 (`tok` false): the step's token is
+// already in its sequence's ring (nkv_paged_append_t64 ran before), k_new / v_new are unused.
+// Per-token symmetric (`tok`): the launch appends k_new / v_new itself and attends them as the tail.
 static int paged_attn(const char* what, const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                       int64_t kv_seq_stride, int64_t kv_head_stride, const uint8_t* pages, const int32_t* page_table,
                       int64_t table_stride, int64_t num_pages, const uint16_t* rings, const int64_t* pos_dev,
                       int64_t nseq, int64_t hq,
                       int64_t hkv, int64_t head_dim, const int32_t* wg_map, const int32_t* seq_parts,
                       int64_t total_parts, uint16_t* out, float* lse_out, void* workspace, int64_t workspace_bytes,
-                      void* stream) {
+                      void* stream, bool tok = false) {
   set_error("");
   if (int rc = check_heads(hq, hkv, head_dim)) return rc;
   AttnArgs a{};
-  if (int rc = paged_args(what, a, pages, page_table, table_stride, num_pages, rings, pos_dev, nseq, hkv, head_dim))
+  if (int rc = paged_args(what, a, pages, page_table, table_stride, num_pages, rings, pos_dev, nseq, hkv, head_dim, tok))
     return rc;
+  if (tok) {
+    if (!k_new || !v_new) return fail(NKV_ERR_INVALID, "%s: null pointer argument", what);
+    if (!al16(k_new) || !al16(v_new) || kv_head_stride % 8 || kv_seq_stride % 8)
+      return fail(NKV_ERR_UNSUPPORTED, "%s: k_new / v_new must be 16-byte aligned", what);
+    a.k_new = k_new; a.v_new = v_new; a.kv_hs = kv_head_stride; a.kv_ss = kv_seq_stride;
+  }
   if (!q || !wg_map || !seq_parts || !out || !workspace) return fail(NKV_ERR_INVALID, "%s: null pointer argument", what);
   if (!al16(q) || !al16(workspace)) return fail(NKV_ERR_UNSUPPORTED, "%s: buffers must be 16-byte aligned", what);
   if (total_parts < nseq || total_parts > 65535)
@@ -2376,14 +2446,14 @@ static int paged_attn(const char* what, const uint16_t* q, const uint16_t* k_new
     return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
   a.q = q; a.hq = (int)hq; a.gq = (int)(hq / hkv);
   a.wg_map = wg_map; a.seq_parts = seq_parts; a.total_parts = (int)total_parts;
-  (void)k_new; (void)v_new; (void)kv_seq_stride; (void)kv_head_stride;
   a.sl2 = LOG2E / sqrtf((float)head_dim);
   a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace);
   // one launch: the last prefix workgroup of each (sequence, KV head) runs its tail
   a.inline_tail = 1;
   a.tail_ctr_end = reinterpret_cast<int*>(static_cast<char*>(workspace) + (workspace_bytes & ~int64_t(3)));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(attn_prefix_kernel<PAGED_T64>, dim3((unsigned)(hkv * total_parts)), dim3(THREADS), 0, s, a);
+  if (tok) hipLaunchKernelGGL(attn_prefix_kernel<PAGED_TOK>, dim3((unsigned)(hkv * total_parts)), dim3(THREADS), 0, s, a);
+  else hipLaunchKernelGGL(attn_prefix_kernel<PAGED_T64>, dim3((unsigned)(hkv * total_parts)), dim3(THREADS), 0, s, a);
   return check_launch(what);
 }
 
@@ -2411,6 +2481,18 @@ extern "C" int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_ne
   return paged_attn("paged_decode_step_t64", q, k_new, v_new, kv_seq_stride, kv_head_stride, pages, page_table,
                     table_stride, num_pages, rings, pos_dev, nseq, hq, hkv, head_dim, wg_map, seq_parts, total_parts,
                     out, lse_out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int nkv_paged_decode_step_tok(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                                         int64_t kv_seq_stride, int64_t kv_head_stride, uint8_t* pages,
+                                         const int32_t* page_table, int64_t table_stride, int64_t num_pages,
+                                         const int64_t* pos_dev, int64_t nseq, int64_t hq, int64_t hkv,
+                                         int64_t head_dim, const int32_t* wg_map, const int32_t* seq_parts,
+                                         int64_t total_parts, uint16_t* out, float* lse_out, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+  return paged_attn("paged_decode_step_tok", q, k_new, v_new, kv_seq_stride, kv_head_stride, pages, page_table,
+                    table_stride, num_pages, nullptr, pos_dev, nseq, hq, hkv, head_dim, wg_map, seq_parts, total_parts,
+                    out, lse_out, workspace, workspace_bytes, stream, true);
 }
 
 // ---------------------------------------------------------------- chunked prefill

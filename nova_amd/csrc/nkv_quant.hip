@@ -331,9 +331,19 @@ struct QuantSymArgs {
   uint16_t* scales;
   int64_t s_rs;
   int64_t items;  // rows * n
+  // page destination (paged cache): token t of slab r is token first_token + t of a sequence,
+  // stored in page table[(first_token + t) / 64], KV head r, row (first_token + t) % 64 of
+  // tensor `which` (0 K, 1 V) of the page layout [K codes 64 x 128 | V codes | K scales 64 |
+  // V scales 64]; tokens whose table entry is outside [0, num_pages) are skipped
+  uint8_t* pages;
+  const int32_t* table;
+  int64_t first_token, num_pages;
+  int which;
 };
 
-template <int DT>
+constexpr int64_t PAGE_TOK_BYTES = 2 * 64 * 128 + 2 * 64 * 2;  // 16640
+
+template <int DT, bool PAGES = false>
 __global__ __launch_bounds__(256) void quant_sym_kernel(QuantSymArgs a) {
   const int64_t item = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   const bool on = item < a.items;  // whole 16-lane rows agree
@@ -344,8 +354,18 @@ __global__ __launch_bounds__(256) void quant_sym_kernel(QuantSymArgs a) {
   float scale;
   const uint2 cw = sym_quant8(v, scale);
   if (!on) return;
-  *reinterpret_cast<uint2*>(a.codes + r * a.c_rs + t * 128 + c8) = cw;
-  if (c8 == 0) a.scales[r * a.s_rs + t] = f2h(scale);
+  uint8_t* code_row = a.codes + r * a.c_rs + t * 128;
+  uint16_t* scale_at = a.scales + r * a.s_rs + t;
+  if constexpr (PAGES) {
+    const int64_t tok = a.first_token + t;
+    const int32_t page = a.table[tok / 64];
+    if (page < 0 || page >= a.num_pages) return;
+    uint8_t* pg = a.pages + ((int64_t)page * a.rows + r) * PAGE_TOK_BYTES;
+    code_row = pg + a.which * 64 * 128 + (tok % 64) * 128;
+    scale_at = reinterpret_cast<uint16_t*>(pg + 2 * 64 * 128) + a.which * 64 + tok % 64;
+  }
+  *reinterpret_cast<uint2*>(code_row + c8) = cw;
+  if (c8 == 0) *scale_at = f2h(scale);
 }
 
 struct DequantSymArgs {
@@ -543,6 +563,30 @@ extern "C" int nkv_quantize_tok(const void* x, int x_dtype, int64_t x_row_stride
   else if (x_dtype == NKV_BF16) hipLaunchKernelGGL(quant_sym_kernel<NKV_BF16>, grid, block, 0, s, a);
   else hipLaunchKernelGGL(quant_sym_kernel<NKV_F32>, grid, block, 0, s, a);
   return check_launch("quantize_tok");
+}
+
+extern "C" int nkv_paged_quantize_tok(const void* x, int x_dtype, int64_t x_head_stride, int64_t hkv, int64_t n,
+                                      int which, uint8_t* pages, const int32_t* table_row, int64_t first_token,
+                                      int64_t num_pages, void* stream) {
+  g_err.clear();
+  if (x_dtype != NKV_F16 && x_dtype != NKV_BF16 && x_dtype != NKV_F32)
+    return fail(NKV_ERR_INVALID, "paged_quantize_tok: unknown dtype %d", x_dtype);
+  if (hkv <= 0 || n < 0 || first_token < 0 || (which != 0 && which != 1) || num_pages <= 0)
+    return fail(NKV_ERR_INVALID, "paged_quantize_tok: bad sizes hkv=%lld n=%lld first_token=%lld which=%d "
+                "num_pages=%lld", (long long)hkv, (long long)n, (long long)first_token, which, (long long)num_pages);
+  if (n == 0) return NKV_OK;
+  if (!x || !pages || !table_row) return fail(NKV_ERR_INVALID, "paged_quantize_tok: null pointer argument");
+  const int esz = x_dtype == NKV_F32 ? 4 : 2;
+  if (!aligned16(x) || !aligned16(pages) || (x_head_stride * esz) % 16 || x_head_stride < n * 128)
+    return fail(NKV_ERR_UNSUPPORTED, "paged_quantize_tok: x must be 16-byte aligned with a head stride >= n * 128");
+  QuantSymArgs a{x, x_head_stride, hkv, n, nullptr, 0, nullptr, 0, hkv * n, pages, table_row, first_token,
+                 num_pages, which};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)cdiv(a.items, 16)), block(256);
+  if (x_dtype == NKV_F16) hipLaunchKernelGGL((quant_sym_kernel<NKV_F16, true>), grid, block, 0, s, a);
+  else if (x_dtype == NKV_BF16) hipLaunchKernelGGL((quant_sym_kernel<NKV_BF16, true>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((quant_sym_kernel<NKV_F32, true>), grid, block, 0, s, a);
+  return check_launch("paged_quantize_tok");
 }
 
 extern "C" int nkv_dequantize_tok(const int8_t* codes, int64_t codes_row_stride, const uint16_t* scales,

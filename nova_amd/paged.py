@@ -19,6 +19,12 @@ the bucket-padded positions the reference masks to -inf are not read, so whateve
 cannot change an output. Every computation is a HIP launch (``nkv_paged_decode_step_t64``);
 lengths are device scalars, so one captured graph serves every step while pages stay reserved.
 
+``PagedKVInt8TokCache`` holds the per-token symmetric format (one fp16 scale per token and KV
+head) in the same page pool scheme: a page is 64 tokens of one KV head, K codes | V codes | K
+scales (64 fp16) | V scales = 16640 bytes, 128-byte aligned. It keeps no ring; a decode step is
+one launch (``nkv_paged_decode_step_tok``) that stores each sequence's new token into its page and
+attends over ``[0, pos_b]``.
+
 Host bookkeeping (``PagePool``: free pages, reservations, lengths; ``plan_parts``: the prefix
 work plan) is plain Python so that its guards are testable without a GPU.
 """
@@ -33,6 +39,7 @@ from .kvquant import _DT
 D = 128
 GT = 64
 PAGE_BYTES = 2 * GT * D + 4 * D * 2
+PAGE_BYTES_TOK = 2 * GT * D + 2 * GT * 2
 CODE_BYTES = GT * D
 MAX_PARTS_PER_SEQ = 256  # partials the tail's merge holds for one sequence
 
@@ -116,6 +123,9 @@ def plan_parts(lengths: list[int], target_parts: int) -> tuple[list[int], list[i
 
 
 class PagedKVInt8Cache:
+    page_bytes = PAGE_BYTES  # bytes of one page of one KV head
+    has_rings = True
+
     def __init__(self, num_layers: int, num_kv_heads: int, head_dim: int, num_q_heads: int, max_seqs: int,
                  num_pages: int, max_pages_per_seq: int, device: str | torch.device = "cuda",
                  target_parts: int | None = None) -> None:
@@ -128,10 +138,10 @@ class PagedKVInt8Cache:
         self.num_q_heads, self.max_seqs, self.num_pages = int(num_q_heads), int(max_seqs), int(num_pages)
         self.max_pages_per_seq, self.device = int(max_pages_per_seq), device
         self.pool = PagePool(self.num_pages, self.max_seqs, self.max_pages_per_seq)
-        self.pages = [torch.zeros((self.num_pages, self.num_kv_heads, PAGE_BYTES), dtype=torch.uint8, device=device)
-                      for _ in range(self.num_layers)]
-        self.rings = [torch.zeros((self.max_seqs, self.num_kv_heads, 2, GT, D), dtype=torch.float16, device=device)
-                      for _ in range(self.num_layers)]
+        self.pages = [torch.zeros((self.num_pages, self.num_kv_heads, self.page_bytes), dtype=torch.uint8,
+                                  device=device) for _ in range(self.num_layers)]
+        self.rings = ([torch.zeros((self.max_seqs, self.num_kv_heads, 2, GT, D), dtype=torch.float16, device=device)
+                       for _ in range(self.num_layers)] if self.has_rings else None)
         self.page_table = torch.full((self.max_seqs, self.max_pages_per_seq), -1, dtype=torch.int32, device=device)
         self.pos = torch.zeros(self.max_seqs, dtype=torch.long, device=device)
         self.merged = torch.zeros((self.max_seqs, self.num_q_heads, 1, D), dtype=torch.float16, device=device)
@@ -177,16 +187,22 @@ class PagedKVInt8Cache:
 
     # ---- prefill of one sequence
 
+    def _check_prompt(self, key: torch.Tensor, value: torch.Tensor) -> int:
+        h = self.num_kv_heads
+        for name, x in (("key", key), ("value", value)):
+            if x.dim() != 4 or x.shape[0] != 1 or x.shape[1] != h or x.shape[3] != D or x.dtype not in _DT:
+                raise ValueError(f"{name} must be [1, {h}, n, {D}] fp16 / bf16 / fp32, got {tuple(x.shape)} {x.dtype}")
+        if key.shape != value.shape:
+            raise ValueError(f"key {tuple(key.shape)} and value {tuple(value.shape)} differ")
+        return key.shape[2]
+
     def prefill(self, b: int, layer: int, key: torch.Tensor, value: torch.Tensor) -> None:
         """Store a prompt of n tokens (``[1, H_kv, n, 128]``) for sequence ``b``: whole groups
         quantized by the HIP quantizer straight into their pages (``nkv_paged_quantize_t64``, the
         int8t64 arithmetic bit for bit), the newest <= 64 tokens into its ring (slot = position
         mod 64)."""
-        n = key.shape[2]
+        n = self._check_prompt(key, value)
         h = self.num_kv_heads
-        for name, x in (("key", key), ("value", value)):
-            if x.dim() != 4 or x.shape[0] != 1 or x.shape[1] != h or x.shape[3] != D or x.dtype not in _DT:
-                raise ValueError(f"{name} must be [1, {h}, n, {D}] fp16 / bf16 / fp32, got {tuple(x.shape)} {x.dtype}")
         self.reserve(b, n + 1)
         q = n // GT * GT
         if q:
@@ -253,3 +269,42 @@ class PagedKVInt8Cache:
         device (``advance()``, or a replayed graph that adds to ``pos``). Raises when a sequence
         would write past the pages reserved for it."""
         self.pool.advance(self.nseq, steps)
+
+
+class PagedKVInt8TokCache(PagedKVInt8Cache):
+    """A batch of ragged sequences in the per-token symmetric format, in pages of 64 tokens of
+    one KV head: K codes int8 ``[64, 128]``, V codes, K scales fp16 ``[64]``, V scales
+    (16640 bytes). Codes and scales are those of ``nkv_quantize_tok`` bit for bit, token p of
+    sequence b at row ``p % 64`` of page ``page_table[b, p // 64]``. Same pool, table, plan and
+    graph-safe ``pos`` as ``PagedKVInt8Cache``; no rings."""
+
+    page_bytes = PAGE_BYTES_TOK
+    has_rings = False
+
+    def prefill(self, b: int, layer: int, key: torch.Tensor, value: torch.Tensor) -> None:
+        """Store a prompt of n tokens (``[1, H_kv, n, 128]``) for sequence ``b``: every token
+        quantized by the HIP quantizer straight into its page (``nkv_paged_quantize_tok``)."""
+        n = self._check_prompt(key, value)
+        h = self.num_kv_heads
+        self.reserve(b, n + 1)
+        if n:
+            row = self.page_table[b]
+            for which, x in enumerate((key, value)):
+                xc = x if x.stride(3) == 1 and x.stride(2) == D and x.data_ptr() % 16 == 0 else x.contiguous()
+                _lib.call("nkv_paged_quantize_tok", xc.data_ptr(), _DT[x.dtype], xc.stride(1), h, n, which,
+                          self.pages[layer].data_ptr(), row.data_ptr(), 0, self.num_pages, _lib.stream_ptr(row.device))
+        self.pool.set_length(b, n)
+        self.pos[b] = n
+
+    def decode_step(self, key: torch.Tensor, value: torch.Tensor, query: torch.Tensor, layer: int) -> torch.Tensor:
+        """Store one token per sequence at ``pos`` and attend each sequence over ``[0, pos_b]``, in
+        one launch. Returns ``merged[:B]`` ``[B, Hq, 1, 128]``; ``lse`` holds the log-sum-exp."""
+        if self.wg_map is None:
+            raise RuntimeError("call plan() before decoding")
+        q, k, v = self._step_args(query, key, value)
+        _lib.call("nkv_paged_decode_step_tok", q.data_ptr(), k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
+                  self.pages[layer].data_ptr(), self.page_table.data_ptr(), self.page_table.stride(0), self.num_pages,
+                  self.pos.data_ptr(), self.nseq, self.num_q_heads, self.num_kv_heads, D, self.wg_map.data_ptr(),
+                  self.seq_parts.data_ptr(), self.total_parts, self.merged.data_ptr(), self.lse.data_ptr(),
+                  self.ws.data_ptr(), self.ws.numel() * 4, _lib.stream_ptr(self.pos.device))
+        return self.merged[:self.nseq]
