@@ -1064,7 +1064,8 @@ struct TailSmem {
   float rq_ext[2][2 * D];                    // local requantization: per channel min / max of two half rings
   int incomplete;                            // the merger gave up waiting for a partial
 };
-constexpr int MERGER_MAX_PARTS = 64;         // partials one merging wave tracks in a 64-bit ballot
+constexpr int MERGER_MAX_PARTS = 64;         // prefix parts per head of a fused launch
+constexpr int MERGER_MAX_HEADS = 64;         // KV heads of a fused launch: its part-0 workgroups wait for the others
 constexpr int MERGER_SPIN_LIMIT = 1 << 22;   // polls (each followed by a short sleep) before giving up
 static_assert(sizeof(TailSmem) <= LDS_BYTES && sizeof(TailSmem) <= LDS_BYTES_TOK,
               "the tail's LDS fits in the prefix kernel's stages");
@@ -1095,11 +1096,57 @@ __device__ __forceinline__ uint16_t ld_u16(const uint16_t* p, bool co) {
   return co ? __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *p;
 }
 
-// Publication area of the fused step, in the workspace's last bytes: one counter per head
-// (paged: per sequence and head) at tail_ctr_end[-1 - i], and for the contiguous layouts one flag
-// per prefix partial below the counters. Every launch leaves all of them at zero.
-__device__ __forceinline__ int* partial_flags(const AttnArgs& a, int h) {
-  return a.tail_ctr_end - a.hkv - (int64_t)(h + 1) * a.n_parts;
+// ---- published partials. A prefix partial's values are stored as their float bits XOR PUB_KEY,
+// with relaxed agent-scope atomic stores, and every tail sets the words it consumed back to zero:
+// between launches a workspace's partials are zero, and in a launch a zero word is one not
+// written yet. PUB_KEY is a signalling-NaN pattern, and arithmetic never returns a signalling NaN
+// (IEEE operations quiet them), so no value encodes to zero. A tail in the same launch as its
+// producers polls the words themselves (relaxed agent-scope atomic loads): per-location
+// coherence hands it each producer's value once the word is non-zero, without a flag, fence or
+// counter (a flag would need release / acquire ordering, i.e. L2 writeback and invalidation).
+constexpr uint32_t PUB_KEY = 0x7FBADBADu;
+constexpr uint64_t PUB_KEY2 = ((uint64_t)PUB_KEY << 32) | PUB_KEY;
+
+__device__ __forceinline__ void pub_st(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v) ^ PUB_KEY, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void pub_st2(float* p, float x, float y) {
+  const uint64_t w = (((uint64_t)__float_as_uint(y) << 32) | __float_as_uint(x)) ^ PUB_KEY2;
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t pub_ld(const float* p) {
+  return __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t pub_ld2(const float* p) {
+  return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float pub_f(uint32_t w) { return __uint_as_float(w ^ PUB_KEY); }
+__device__ __forceinline__ float2 pub_f2(uint64_t w) {
+  w ^= PUB_KEY2;
+  return float2{__uint_as_float((uint32_t)w), __uint_as_float((uint32_t)(w >> 32))};
+}
+// Words a tail consumed back to zero. Plain stores: no one touches the word again in this launch,
+// and the launch boundary orders them before the next launch's accesses.
+__device__ __forceinline__ void pub_clear(float* p) { *reinterpret_cast<uint32_t*>(p) = 0u; }
+__device__ __forceinline__ void pub_clear2(float* p) { *reinterpret_cast<uint64_t*>(p) = 0ull; }
+// Reload a word while it is zero, sleeping between polls; `budget` is the caller's remaining
+// polls (a word still zero when it runs out stays zero: the caller reports it).
+__device__ __forceinline__ uint32_t pub_repoll(const float* p, uint32_t w, int& budget) {
+  while (w == 0 && budget > 0) {
+    --budget;
+    __builtin_amdgcn_s_sleep(1);
+    w = pub_ld(p);
+  }
+  return w;
+}
+__device__ __forceinline__ uint64_t pub_repoll2(const float* p, uint64_t w, int& budget) {
+  while (w == 0 && budget > 0) {
+    --budget;
+    __builtin_amdgcn_s_sleep(1);
+    w = pub_ld2(p);
+  }
+  return w;
 }
 
 // The ring held in LDS (64 rows of K, then of V; ring_chunk_pos layout) requantized in place as
@@ -1157,28 +1204,25 @@ __device__ __forceinline__ void requant_ring_lds(uint8_t* ring_lds, float (&ext)
 // symmetric format the new token alone is the tail, quantized here as the append quantizes it.
 // So the tail reads nothing that this launch writes except the partials.
 //
-// `poll`: run inside the fused launch by the head's merger, while other workgroups may still be
-// computing their partials. Each merging wave polls the partials' flags with relaxed agent-scope
-// loads (sleeping between polls, giving up after MERGER_SPIN_LIMIT polls), then takes one
-// agent-scope acquire and loads the partials; the producers publish each flag after an
-// agent-scope release. The merge runs in partial order, so the result does not depend on the
-// order of arrival. (An acquire per batch of newly set flags, to load early partials while
-// waiting for late ones, measured 0.6 us slower per launch: each acquire invalidates the L2.)
-// Without `poll` (the separate tail kernel) the launch boundary orders the partials before the
-// tail.
+// The prefix partials are published words (pub_st). In the fused launch (`run` TAIL_MERGER: the
+// head's part-0 workgroup; TAIL_LAST: the last of a paged sequence's workgroups to take its
+// ticket) other workgroups may still be writing them: the merging waves load each partial's m
+// and l, re-polling the words still zero (sleeping between polls, giving up after
+// MERGER_SPIN_LIMIT polls: the output is then NaN), then the column pairs likewise. The merge
+// runs in partial order, so the result does not depend on the order of arrival. Every consumed
+// word is set back to zero. TAIL_KERNEL (the separate tail kernel) finds every word written.
 enum TailRun : int { TAIL_KERNEL = 0, TAIL_LAST = 1, TAIL_MERGER = 2 };
 
 template <bool PAGED>
 __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailSmem& sm, int run, int64_t pos,
                                           bool pos_ok, int64_t U) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const bool poll = run == TAIL_MERGER;
-  const bool co = run != TAIL_KERNEL;  // partials written in this launch: agent-scope loads
+  const bool poll = run != TAIL_KERNEL;  // partials written in this launch: poll their words
   const int gq = a.gq, pw = part_stride(gq), cols = gq * D;
   const int P = PAGED ? min(a.seq_parts[2 * b + 1], WTS) : a.n_parts;
   const bool fused = PAGED || a.tail_mode == TAIL_FUSED;
   const bool ring = (PAGED || a.tail_mode != TAIL_NONE) && (!fused || pos_ok);
-  const float* hws = PAGED ? a.ws + ((int64_t)h * a.total_parts + a.seq_parts[2 * b]) * pw : a.ws + (int64_t)h * P * pw;
+  float* hws = PAGED ? a.ws + ((int64_t)h * a.total_parts + a.seq_parts[2 * b]) * pw : a.ws + (int64_t)h * P * pw;
   // while waves 0..3 attend over the ring, the others merge the prefix partials
   const int mbase = ring ? RING_PARTS : 0, nmw = TB_WAVES - mbase;
 
@@ -1213,15 +1257,17 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   const int head0 = wave - mbase;
   const bool merging = head0 >= 0 && head0 < gq;
   float mm = NEG_INF, ll = 0.0f;  // merging wave: lane s's m / l of its first head
-  float2 v0[MERGE_PRE];           // and its columns 2 lane, 2 lane + 1 of the first MERGE_PRE partials
-  if (merging && !poll) {
+  uint32_t rm = PUB_KEY, rl = PUB_KEY;  // their published words (beyond P: words of 0.0)
+  uint64_t rv[MERGE_PRE];               // and those of its columns 2 lane, 2 lane + 1 of the first MERGE_PRE partials
+  int budget = MERGER_SPIN_LIMIT;
+  if (merging) {
+    // issued ahead of the ring work (their latency overlaps it); polled below if still zero
     if (lane < P) {
-      mm = ld_f(hws + (int64_t)lane * pw + gq * D + head0, co);
-      ll = ld_f(hws + (int64_t)lane * pw + gq * D + gq + head0, co);
+      rm = pub_ld(hws + (int64_t)lane * pw + gq * D + head0);
+      rl = pub_ld(hws + (int64_t)lane * pw + gq * D + gq + head0);
     }
 #pragma unroll
-    for (int u = 0; u < MERGE_PRE; ++u)
-      v0[u] = u < P ? ld_f2(hws + (int64_t)u * pw + head0 * D + 2 * lane, co) : float2{0.f, 0.f};
+    for (int u = 0; u < MERGE_PRE; ++u) rv[u] = u < P ? pub_ld2(hws + (int64_t)u * pw + head0 * D + 2 * lane) : PUB_KEY2;
   }
   if (tid == 0) sm.incomplete = 0;
 
@@ -1272,72 +1318,159 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     attend_ring16(a, st, qb, ring_k, ring_v, wave, bits);
     store_wave_partial(st, gq, sm.ring_part[wave]);
   } else if (merging) {
+    // (this code runs once per launch on a cold instruction cache, at ~30 ns per 64-byte line:
+    // the common shape, one head per merging wave and P <= 64, takes a short straight path)
+    bool lost = false;  // a word never arrived (the wait gave up)
     if (poll) {
-      // ---- wait for every partial's flag (P <= MERGER_MAX_PARTS, checked at launch), then one
-      // agent-scope acquire and the loads of each partial's m, l and first MERGE_PRE column pairs
-      const int* flags = partial_flags(a, h);
-      const uint64_t want = P >= 64 ? ~0ull : ((1ull << P) - 1);
-      uint64_t have = 0;
+      // ---- every word still zero is reloaded together (m, l and the column pairs: the last
+      // partial's words then arrive in one round trip), until none is left
+      for (;;) {
+        bool miss = rm == 0 || rl == 0;
 #pragma unroll
-      for (int u = 0; u < MERGE_PRE; ++u) v0[u] = float2{0.f, 0.f};
-      for (int spin = 0; have != want;) {
-        const bool up = lane < P && !((have >> lane) & 1) &&
-                        __hip_atomic_load(flags + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
-        const uint64_t now = __builtin_amdgcn_ballot_w64(up);
-        if (now == 0) {
-          if (++spin > MERGER_SPIN_LIMIT) break;
-          __builtin_amdgcn_s_sleep(1);
-          continue;
+        for (int u = 0; u < MERGE_PRE; ++u) miss |= rv[u] == 0;
+        if (!__builtin_amdgcn_ballot_w64(miss)) break;
+        if (budget <= 0) {
+          lost = true;
+          break;
         }
-        have |= now;
-      }
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      if (lane < P) {
-        mm = ld_f(hws + (int64_t)lane * pw + gq * D + head0, true);
-        ll = ld_f(hws + (int64_t)lane * pw + gq * D + gq + head0, true);
-      }
+        --budget;
+        __builtin_amdgcn_s_sleep(1);
+        if (rm == 0) rm = pub_ld(hws + (int64_t)lane * pw + gq * D + head0);
+        if (rl == 0) rl = pub_ld(hws + (int64_t)lane * pw + gq * D + gq + head0);
 #pragma unroll
-      for (int u = 0; u < MERGE_PRE; ++u)
-        if (u < P) v0[u] = ld_f2(hws + (int64_t)u * pw + head0 * D + 2 * lane, true);
-      if (have != want && lane == 0) sm.incomplete = 1;
+        for (int u = 0; u < MERGE_PRE; ++u)
+          if (rv[u] == 0) rv[u] = pub_ld2(hws + (int64_t)u * pw + head0 * D + 2 * lane);
+      }
+    }
+    if (lane < P) {
+      mm = pub_f(rm);
+      ll = pub_f(rl);
     }
     // ---- prefix merge, one head at a time per merging wave (lane s (+ 64 k) = partial s for
-    // the weights, two columns per lane for the sum): m_p, w_s, l_p, pre_acc
+    // the weights, two columns per lane for the sum): m_p = max_s m_s, w_s = 2^(m_s - m_p),
+    // l_p = sum_s w_s l_s, pre_acc = sum_s w_s acc_s; then the head's words go back to zero
     float* wb = sm.wts + wave * WTS;
-    for (int head = head0; head < gq; head += nmw) {
-      const bool own = head == head0;
-      float m = NEG_INF;
-      for (int s = lane; s < P; s += 64)
-        m = fmaxf(m, (own && s == lane) ? mm : ld_f(hws + (int64_t)s * pw + gq * D + head, co));
-      m = wave_max(m);
-      float l = 0.0f;
-      for (int s = lane; s < P; s += 64) {
-        const float ms = (own && s == lane) ? mm : ld_f(hws + (int64_t)s * pw + gq * D + head, co);
-        const float ls = (own && s == lane) ? ll : ld_f(hws + (int64_t)s * pw + gq * D + gq + head, co);
-        const float w = ms == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(ms - m);
-        wb[s] = w;
-        l += ls * w;
-      }
-      l = wave_sum(l);
+    if (P <= 64 && head0 + nmw >= gq) {
+      // one head, one chunk of partials: lane s holds m_s and l_s already
+      const float ms = lane < P ? mm : NEG_INF;
+      const float m = wave_max(ms);
+      const float w = (lane < P && ms != NEG_INF) ? __builtin_amdgcn_exp2f(ms - m) : 0.0f;
+      wb[lane] = w;
+      const float l = wave_sum(lane < P ? ll * w : 0.0f);
       float2 acc = {0.0f, 0.0f};
-      int s0 = 0;
-      if (own) {
 #pragma unroll
-        for (int u = 0; u < MERGE_PRE; ++u) {
-          const float w = u < P ? wb[u] : 0.0f;
-          acc.x += v0[u].x * w;
-          acc.y += v0[u].y * w;
+      for (int u = 0; u < MERGE_PRE; ++u) {
+        const float2 vv = pub_f2(rv[u]);
+        acc.x += vv.x * wb[u];
+        acc.y += vv.y * wb[u];
+      }
+#pragma unroll 1
+      for (int sb = MERGE_PRE; sb < P; sb += 8) {
+        uint64_t w8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          w8[j] = sb + j < P ? pub_ld2(hws + (int64_t)(sb + j) * pw + head0 * D + 2 * lane) : 1;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (sb + j >= P) break;
+          const uint64_t wv = pub_repoll2(hws + (int64_t)(sb + j) * pw + head0 * D + 2 * lane, w8[j], budget);
+          lost |= wv == 0;
+          const float2 vv = pub_f2(wv);
+          acc.x += vv.x * wb[sb + j];
+          acc.y += vv.y * wb[sb + j];
         }
-        s0 = MERGE_PRE;
       }
-      for (int s = s0; s < P; ++s) {
-        const float2 vv = ld_f2(hws + (int64_t)s * pw + head * D + 2 * lane, co);
-        acc.x += vv.x * wb[s];
-        acc.y += vv.y * wb[s];
+      *reinterpret_cast<float2*>(sm.pre_acc + head0 * D + 2 * lane) = acc;
+      if (lane == 0) {
+        sm.pre_m[head0] = m;
+        sm.pre_l[head0] = l;
       }
-      *reinterpret_cast<float2*>(sm.pre_acc + head * D + 2 * lane) = acc;
-      if (lane == 0) { sm.pre_m[head] = m; sm.pre_l[head] = l; }
+      if (lane < P) {
+        pub_clear(hws + (int64_t)lane * pw + gq * D + head0);
+        pub_clear(hws + (int64_t)lane * pw + gq * D + gq + head0);
+      }
+#pragma unroll 1
+      for (int s = 0; s < P; ++s) pub_clear2(hws + (int64_t)s * pw + head0 * D + 2 * lane);
+    } else {
+      for (int head = head0; head < gq; head += nmw) {
+        const bool own = head == head0;
+        float ls[WTS / 64];
+        float m = NEG_INF;
+#pragma unroll 1
+        for (int k = 0; k < WTS / 64; ++k) {
+          const int s = 64 * k + lane;
+          ls[k] = 0.0f;
+          if (s >= P) continue;
+          float ms;
+          if (own && k == 0) {
+            ms = mm;
+            ls[k] = ll;
+          } else {
+            const float* pm = hws + (int64_t)s * pw + gq * D + head;
+            const uint32_t wm = pub_repoll(pm, pub_ld(pm), budget);
+            const uint32_t wl = pub_repoll(pm + gq, pub_ld(pm + gq), budget);
+            lost |= wm == 0 || wl == 0;
+            ms = pub_f(wm);
+            ls[k] = pub_f(wl);
+          }
+          wb[s] = ms;
+          m = fmaxf(m, ms);
+        }
+        m = wave_max(m);
+        float l = 0.0f;
+#pragma unroll 1
+        for (int k = 0; k < WTS / 64; ++k) {
+          const int s = 64 * k + lane;
+          if (s >= P) continue;
+          const float ms = wb[s];
+          const float w = ms == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(ms - m);
+          wb[s] = w;
+          l += ls[k] * w;
+        }
+        l = wave_sum(l);
+        float2 acc = {0.0f, 0.0f};
+        int s0 = 0;
+        if (own) {
+#pragma unroll
+          for (int u = 0; u < MERGE_PRE; ++u) {
+            const float w = u < P ? wb[u] : 0.0f;
+            const float2 vv = pub_f2(rv[u]);
+            acc.x += vv.x * w;
+            acc.y += vv.y * w;
+          }
+          s0 = MERGE_PRE;
+        }
+#pragma unroll 1
+        for (int sb = s0; sb < P; sb += 8) {
+          uint64_t w8[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            w8[j] = sb + j < P ? pub_ld2(hws + (int64_t)(sb + j) * pw + head * D + 2 * lane) : 1;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            if (sb + j >= P) break;
+            const uint64_t wv = pub_repoll2(hws + (int64_t)(sb + j) * pw + head * D + 2 * lane, w8[j], budget);
+            lost |= wv == 0;
+            const float2 vv = pub_f2(wv);
+            acc.x += vv.x * wb[sb + j];
+            acc.y += vv.y * wb[sb + j];
+          }
+        }
+        *reinterpret_cast<float2*>(sm.pre_acc + head * D + 2 * lane) = acc;
+        if (lane == 0) {
+          sm.pre_m[head] = m;
+          sm.pre_l[head] = l;
+        }
+#pragma unroll 1
+        for (int s = lane; s < P; s += 64) {
+          pub_clear(hws + (int64_t)s * pw + gq * D + head);
+          pub_clear(hws + (int64_t)s * pw + gq * D + gq + head);
+        }
+#pragma unroll 1
+        for (int s = 0; s < P; ++s) pub_clear2(hws + (int64_t)s * pw + head * D + 2 * lane);
+      }
     }
+    if (__builtin_amdgcn_ballot_w64(lost) && lane == 0) sm.incomplete = 1;
   }
   __syncthreads();
 
@@ -1377,12 +1510,6 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     const float o = failed ? __builtin_nanf("") : (l > 0.0f ? acc / l : 0.0f);
     a.out[(int64_t)qh * D + d] = f2h(o);
     if (a.lse && d == 0) a.lse[qh] = failed ? __builtin_nanf("") : (l > 0.0f ? (M + __log2f(l) - P_SCALE_LOG2) * LN2 : NEG_INF);
-  }
-  // ---- the merger leaves the publication area at zero for the next launch: every producer
-  // set its flag after taking its ticket, and every flag has been seen
-  if (poll) {
-    if (tid == 0) __hip_atomic_store(a.tail_ctr_end - 1 - h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (tid < P) __hip_atomic_store(partial_flags(a, h) + tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1526,64 +1653,71 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
       gi = nx;
     }
 
-    // ---- merge the waves through LDS (the stages are dead once every wave is here)
+    // ---- merge the waves through LDS (the stages are dead once every wave is here): per head
+    // m = max_w m_w and the waves' weights 2^(m_w - m) once (threads < gq, into xch), then the
+    // columns; the partial is published word by word (pub_st)
     __syncthreads();
     const int gq = a.gq, pw = part_stride(gq);
     store_wave_partial(st, gq, lds + wave * pw);
     __syncthreads();
     float* dst = a.ws + ((int64_t)h * (PAGED ? a.total_parts : a.n_parts) + pslot) * pw;
-    for (int e = tid; e < gq * D + 2 * gq; e += THREADS) {
-      const int head = e < gq * D ? e / D : (e - gq * D) % gq;
-      float m = NEG_INF;
-      for (int w = 0; w < WAVES; ++w) m = fmaxf(m, lds[w * pw + gq * D + head]);
-      const float mu = m == NEG_INF ? 0.0f : m;
-      float sum = 0.0f;
-      const int src = e < gq * D ? e : gq * D + gq + head;  // acc element, or l for both m and l slots
-      for (int w = 0; w < WAVES; ++w) sum += lds[w * pw + src] * __builtin_amdgcn_exp2f(lds[w * pw + gq * D + head] - mu);
-      const float v = e < gq * D ? sum : (e < gq * D + gq ? m : sum);
-      if (a.inline_tail) __hip_atomic_store(dst + e, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      else dst[e] = v;
+    float* wt = xch;  // [gq][WAVES]
+    float pm = NEG_INF, pl = 0.0f;
+    if (tid < gq) {
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) pm = fmaxf(pm, lds[w * pw + gq * D + tid]);
+      const float mu = pm == NEG_INF ? 0.0f : pm;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        const float x = __builtin_amdgcn_exp2f(lds[w * pw + gq * D + tid] - mu);
+        wt[tid * WAVES + w] = x;
+        pl += lds[w * pw + gq * D + gq + tid] * x;
+      }
+    }
+    __syncthreads();
+    // (a paged sequence's partials beyond the WTS its tail merges are not published)
+    const bool publish = !PAGED || part < WTS;
+    for (int e = 2 * tid; e < gq * D && publish; e += 2 * THREADS) {
+      const float* c = wt + (e / D) * WAVES;
+      float x = 0.0f, y = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        x += lds[w * pw + e] * c[w];
+        y += lds[w * pw + e + 1] * c[w];
+      }
+      pub_st2(dst + e, x, y);
+    }
+    if (tid < gq && publish) {
+      pub_st(dst + gq * D + tid, pm);
+      pub_st(dst + gq * D + gq + tid, pl);
     }
   }  // prefix
 
-  // ---- fused tail. Every wave's partial stores are complete (vmcnt) before the workgroup
-  // barrier; thread 0 then publishes the partial with an agent-scope release fence (the
-  // barrier orders the other waves' stores before it) and an atomic on the head's counter.
+  // ---- fused tail. The contiguous layouts: part 0 of each head merges, polling the other
+  // partials' words (the other workgroups never wait, and the hkv merging workgroups leave the
+  // rest of the device to them, so every partial arrives). Paged: each workgroup takes a ticket on
+  // its (sequence, head) counter once its partial is issued; the last one merges (every other
+  // partial is then issued: it polls for the words still in flight) and sets the counter back to
+  // zero (every other increment precedes its own in the counter's modification order).
+  // (pos, pos_ok, U as the prologue read them: the tail needs no second round trip for them)
   if (!a.inline_tail) return;
   if constexpr (!PAGED) {
-    if (!prefix) return;  // append-only workgroups publish nothing: the tail reads none of their stores
+    if (part != 0) return;
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+  __syncthreads();  // the stages and the merge's LDS are dead: the tail reuses them
   TailSmem& sm = *reinterpret_cast<TailSmem*>(lds_raw);
-  // (pos, pos_ok, U as the prologue read them: the tail needs no second round trip for them)
   if constexpr (PAGED) {
-    // the last of the sequence's workgroups to publish runs the tail, after an acquire
     const int last = nparts - 1;
     int* ctr = a.tail_ctr_end - 1 - (b * a.hkv + h);
     if (tid == 0) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
       const int t = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (t == last) {
-        __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      }
+      if (t == last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       ticket = t;
     }
     __syncthreads();
     if (ticket == last) tail_body<true>(a, h, b, sm, TAIL_LAST, pos, pos_ok, U);
   } else {
-    // the first of the head's workgroups to publish becomes its merger: it attends over the ring
-    // and collects the other partials as their flags appear. It only waits for workgroups of
-    // this launch that never wait themselves, so it cannot deadlock them.
-    if (tid == 0) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-      const int t = __hip_atomic_fetch_add(a.tail_ctr_end - 1 - h, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(partial_flags(a, h) + part, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      ticket = t;
-    }
-    __syncthreads();
-    if (ticket == 0) tail_body<false>(a, h, b, sm, TAIL_MERGER, pos, pos_ok, U);
+    tail_body<false>(a, h, b, sm, TAIL_MERGER, pos, pos_ok, U);
   }
 }
 
@@ -2002,9 +2136,10 @@ static int launch_attn(AttnArgs& a, int64_t n_parts, int64_t workspace_bytes, hi
                        int launches = LAUNCH_PREFIX | LAUNCH_TAIL, bool fusable = false) {
   if (n_parts < 0) return fail(NKV_ERR_INVALID, "%s: n_parts %lld is negative", what, (long long)n_parts);
   a.n_parts = (int)n_parts;
-  // both launches in one call: the prefix kernel's last workgroup per head runs the tail
-  // (the merger tracks at most MERGER_MAX_PARTS partials; more parts take the two launches)
-  const bool fuse = fusable && n_parts > 0 && n_parts <= MERGER_MAX_PARTS && launches == (LAUNCH_PREFIX | LAUNCH_TAIL);
+  // both launches in one call: the prefix kernel's part-0 workgroup of each head runs the tail
+  // (at most MERGER_MAX_PARTS parts and MERGER_MAX_HEADS heads; beyond, the two launches)
+  const bool fuse = fusable && n_parts > 0 && n_parts <= MERGER_MAX_PARTS && a.hkv <= MERGER_MAX_HEADS &&
+                    launches == (LAUNCH_PREFIX | LAUNCH_TAIL);
   const int64_t part_bytes = (int64_t)a.hkv * std::max<int64_t>(1, n_parts) * part_floats(a.hq, a.hkv) * (int64_t)sizeof(float);
   const int64_t need = part_bytes + (fuse ? sync_bytes(a.hkv, n_parts) : 0);
   if (n_parts > 0 && workspace_bytes < need)
@@ -2204,9 +2339,8 @@ int static_scratch(hipStream_t s, void** out) {
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
       return fail(NKV_ERR_HIP, "decode_step_static_t64: hipGetSymbolAddress: %s", hipGetErrorString(e));
-    int* sync = reinterpret_cast<int*>(static_cast<unsigned char*>(p) + NKV_STATIC_PART_BYTES);
-    const int n = NKV_STATIC_SYNC_BYTES / (int)sizeof(int);
-    hipLaunchKernelGGL(clear_ints_kernel, dim3((unsigned)cdiv(n, 4 * 256)), dim3(256), 0, s, sync, n);
+    const int n = (int)(STATIC_BYTES / (int64_t)sizeof(int));
+    hipLaunchKernelGGL(clear_ints_kernel, dim3((unsigned)cdiv(n, 4 * 256)), dim3(256), 0, s, static_cast<int*>(p), n);
     if (int rc = check_launch("decode_step_static_t64: clear")) return rc;
     g_scratch_dev[dev] = p;
   }
