@@ -1062,7 +1062,7 @@ struct TailSmem {
   float pre_acc[16 * D];                     // prefix: sum_s w_s acc_s per column
   float pre_m[16], pre_l[16];                // per head: m_p, l_p
   float rq_ext[2][2 * D];                    // local requantization: per channel min / max of two half rings
-  int incomplete;                            // the merger gave up waiting for a partial
+  int lost[TB_WAVES];                        // a merging wave gave up waiting for a partial word
 };
 constexpr int MERGER_MAX_PARTS = 64;         // prefix parts per head of a fused launch
 constexpr int MERGER_MAX_HEADS = 64;         // KV heads of a fused launch: its part-0 workgroups wait for the others
@@ -1126,10 +1126,6 @@ __device__ __forceinline__ float2 pub_f2(uint64_t w) {
   w ^= PUB_KEY2;
   return float2{__uint_as_float((uint32_t)w), __uint_as_float((uint32_t)(w >> 32))};
 }
-// Words a tail consumed back to zero. Plain stores: no one touches the word again in this launch,
-// and the launch boundary orders them before the next launch's accesses.
-__device__ __forceinline__ void pub_clear(float* p) { *reinterpret_cast<uint32_t*>(p) = 0u; }
-__device__ __forceinline__ void pub_clear2(float* p) { *reinterpret_cast<uint64_t*>(p) = 0ull; }
 // Reload a word while it is zero, sleeping between polls; `budget` is the caller's remaining
 // polls (a word still zero when it runs out stays zero: the caller reports it).
 __device__ __forceinline__ uint32_t pub_repoll(const float* p, uint32_t w, int& budget) {
@@ -1213,9 +1209,50 @@ __device__ __forceinline__ void requant_ring_lds(uint8_t* ring_lds, float (&ext)
 // word is set back to zero. TAIL_KERNEL (the separate tail kernel) finds every word written.
 enum TailRun : int { TAIL_KERNEL = 0, TAIL_LAST = 1, TAIL_MERGER = 2 };
 
+// What a ring wave (wave < RING_PARTS) loads before the tail's LDS work: the K and V rows of
+// its 16 ring slots (rows 16 wave + (lane >> 4) + 4 i, 16-byte chunk lane & 15) and, in the wave
+// that holds the new token's slot, that token's K and V rows; or, in the per-token symmetric
+// format, the new token alone (wave 0: lanes 0..15 K, 16..31 V). The contiguous fused step's
+// merger issues these loads as its prefix loop ends, so their latency overlaps its own partial.
+struct TailLoads {
+  uint4 k[4], v[4], fk, fv, tok;
+};
+
+template <bool PAGED>
+__device__ __forceinline__ void tail_load_rows(const AttnArgs& a, int h, int b, int64_t pos, bool pos_ok, TailLoads& t) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, cl = lane & 15, rl = lane >> 4;
+  const bool fused = PAGED || a.tail_mode == TAIL_FUSED;
+  const bool ring = (PAGED || a.tail_mode != TAIL_NONE) && (!fused || pos_ok);
+  const bool tok1 = ring && a.tok;
+  const uint4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) t.k[i] = t.v[i] = z;
+  t.fk = t.fv = t.tok = z;
+  if (!ring || wave >= RING_PARTS) return;
+  if (tok1) {
+    if (wave == 0 && lane < 32) t.tok = *reinterpret_cast<const uint4*>(fresh_of(a, b, h, rl) + 8 * cl);
+    return;
+  }
+  const uint16_t* rk = PAGED ? a.rings + (((int64_t)b * a.hkv + h) * 2) * GT * D : ring_of(a, h, 0);
+  const uint16_t* rv = PAGED ? rk + GT * D : ring_of(a, h, 1);
+  const int slots = PAGED ? GT : (int)a.tail_slots;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t o = (int64_t)min(16 * wave + rl + 4 * i, slots - 1) * D + 8 * cl;
+    t.k[i] = *reinterpret_cast<const uint4*>(rk + o);
+    t.v[i] = *reinterpret_cast<const uint4*>(rv + o);
+  }
+  // the new token's slot: from the step's input, not the ring this launch writes
+  if (!PAGED && a.tail_mode == TAIL_FUSED && (int)(pos % GT) >> 4 == wave) {
+    t.fk = *reinterpret_cast<const uint4*>(fresh_of(a, b, h, 0) + 8 * cl);
+    t.fv = *reinterpret_cast<const uint4*>(fresh_of(a, b, h, 1) + 8 * cl);
+  }
+}
+
 template <bool PAGED>
 __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailSmem& sm, int run, int64_t pos,
-                                          bool pos_ok, int64_t U) {
+                                          bool pos_ok, int64_t U, const TailLoads* pre = nullptr,
+                                          const half8_t (*pre_q)[4] = nullptr) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const bool poll = run != TAIL_KERNEL;  // partials written in this launch: poll their words
   const int gq = a.gq, pw = part_stride(gq), cols = gq * D;
@@ -1226,34 +1263,27 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   // while waves 0..3 attend over the ring, the others merge the prefix partials
   const int mbase = ring ? RING_PARTS : 0, nmw = TB_WAVES - mbase;
 
-  // ---- loads: the ring quarters (or the new token), q, the merging waves' partial columns
-  const int which = wave >> 2, qtr = wave & 3;
+  // ---- loads: the ring rows (or the new token) and q of the ring waves, the merging waves'
+  // partial words
   const bool completes = fused && pos_ok && !a.tok && (pos + 1) % GT == 0;  // the token completes its group
   const bool tok1 = ring && a.tok;  // per-token symmetric fused step: the tail is the new token
-  const uint16_t* ring_h = tok1 ? nullptr
-                          : PAGED ? a.rings + (((int64_t)b * a.hkv + h) * 2 + which) * GT * D : ring_of(a, h, which);
   const bool fresh_on = ring && !tok1 && !PAGED && a.tail_mode == TAIL_FUSED;
   const int fresh_slot = (int)(pos % GT);
-  uint4 rq0 = {0u, 0u, 0u, 0u}, rq1 = rq0, rq2 = rq0, rq3 = rq0;  // rows 16 qtr + (lane >> 4) + 4 i
-  uint4 fresh = rq0;
-  if (ring && !tok1) {
-    const int slots = PAGED ? GT : (int)a.tail_slots, cl = lane & 15, rl = lane >> 4;
-    rq0 = *reinterpret_cast<const uint4*>(ring_h + min(16 * qtr + rl, slots - 1) * D + 8 * cl);
-    rq1 = *reinterpret_cast<const uint4*>(ring_h + min(16 * qtr + rl + 4, slots - 1) * D + 8 * cl);
-    rq2 = *reinterpret_cast<const uint4*>(ring_h + min(16 * qtr + rl + 8, slots - 1) * D + 8 * cl);
-    rq3 = *reinterpret_cast<const uint4*>(ring_h + min(16 * qtr + rl + 12, slots - 1) * D + 8 * cl);
-    // the new token's slot: from the step's input, not the ring this launch writes. Loaded into
-    // registers of its own and stored over its row once the quarter is in LDS.
-    const uint16_t* fp = fresh_on ? fresh_of(a, b, h, which) : ring_h;  // a valid row either way
-    fresh = *reinterpret_cast<const uint4*>(fp + 8 * (lane & 15));
-  }
-  uint4 tokw = {0u, 0u, 0u, 0u};
-  if (tok1 && qtr == 0 && lane < 16) tokw = *reinterpret_cast<const uint4*>(fresh_of(a, b, h, which) + 8 * lane);
+  TailLoads tl;
+  if (pre) tl = *pre;
+  else tail_load_rows<PAGED>(a, h, b, pos, pos_ok, tl);
   const int64_t first = (!PAGED && ring && a.first_dev) ? *a.first_dev : 0;
   const bool mask_on = ring && a.tail_mode == TAIL_MASK && lane < a.tail_slots && a.tail_mask[lane] != 0;
   half8_t qb[4];
   const int64_t qh0 = (int64_t)b * a.hq + h * gq;  // first query head of this workgroup
-  if (ring && wave < RING_PARTS) load_q(a.q + qh0 * D, gq, qb);
+  if (ring && wave < RING_PARTS) {
+    if (pre_q) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) qb[k] = (*pre_q)[k];
+    } else {
+      load_q(a.q + qh0 * D, gq, qb);
+    }
+  }
   const int head0 = wave - mbase;
   const bool merging = head0 >= 0 && head0 < gq;
   float mm = NEG_INF, ll = 0.0f;  // merging wave: lane s's m / l of its first head
@@ -1261,7 +1291,6 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   uint64_t rv[MERGE_PRE];               // and those of its columns 2 lane, 2 lane + 1 of the first MERGE_PRE partials
   int budget = MERGER_SPIN_LIMIT;
   if (merging) {
-    // issued ahead of the ring work (their latency overlaps it); polled below if still zero
     if (lane < P) {
       rm = pub_ld(hws + (int64_t)lane * pw + gq * D + head0);
       rl = pub_ld(hws + (int64_t)lane * pw + gq * D + gq + head0);
@@ -1269,40 +1298,47 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
 #pragma unroll
     for (int u = 0; u < MERGE_PRE; ++u) rv[u] = u < P ? pub_ld2(hws + (int64_t)u * pw + head0 * D + 2 * lane) : PUB_KEY2;
   }
-  if (tid == 0) sm.incomplete = 0;
 
-  // ---- the ring into LDS (chunk ^ (row & 15) layout), the new token over its slot
+  // ---- each ring wave stages its own 16 slots in LDS (chunk ^ (row & 15) layout), the new token
+  // over its slot, and attends over them: no workgroup barrier, except when the token completes
+  // its group (the whole ring is then requantized, by every thread, between two barriers)
   uint8_t* ring_k = sm.ring_lds;
   uint8_t* ring_v = sm.ring_lds + RING_BYTES;
-  if (ring) {
+  if (ring && wave < RING_PARTS) {
+    const int cl = lane & 15, rw = lane >> 4;
     if (tok1) {
-      if (qtr == 0 && lane < 16) {
-        const uint32_t wv[4] = {tokw.x, tokw.y, tokw.z, tokw.w};
+      if (wave == 0 && lane < 32) {
+        const uint32_t wv[4] = {tl.tok.x, tl.tok.y, tl.tok.z, tl.tok.w};
         float v[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = h2f((uint16_t)(wv[j >> 1] >> (16 * (j & 1))));
         float scale;
         const uint2 cw = sym_quant8(v, scale);
         const _Float16 sc = (_Float16)scale;
-        *reinterpret_cast<half8_t*>((which == 0 ? ring_k : ring_v) + (ring_chunk_pos(0, lane) << 4)) =
+        *reinterpret_cast<half8_t*>((rw == 0 ? ring_k : ring_v) + (ring_chunk_pos(0, cl) << 4)) =
             dq8_sym(cw.x, cw.y, half2_t{sc, sc});
       }
     } else {
-      uint8_t* rl_lds = which == 0 ? ring_k : ring_v;
-      const int cl = lane & 15, rl = lane >> 4;
-      const uint4 rows[4] = {rq0, rq1, rq2, rq3};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 16 * qtr + rl + 4 * i;
-        *reinterpret_cast<uint4*>(rl_lds + r * (2 * D) + (ring_chunk_pos(r, cl) << 4)) = rows[i];
+        const int r = 16 * wave + rw + 4 * i, o = r * (2 * D) + (ring_chunk_pos(r, cl) << 4);
+        *reinterpret_cast<uint4*>(ring_k + o) = tl.k[i];
+        *reinterpret_cast<uint4*>(ring_v + o) = tl.v[i];
       }
-      // (program order: this store lands after the quarter's store of the same row)
-      if (fresh_on && fresh_slot >> 4 == qtr && (fresh_slot & 3) == lane >> 4)
-        *reinterpret_cast<uint4*>(rl_lds + fresh_slot * (2 * D) + (ring_chunk_pos(fresh_slot, lane & 15) << 4)) = fresh;
+      // (program order: these stores land after the quarter's stores of the same row)
+      if (fresh_on && fresh_slot >> 4 == wave && (fresh_slot & 3) == rw) {
+        const int o = fresh_slot * (2 * D) + (ring_chunk_pos(fresh_slot, cl) << 4);
+        *reinterpret_cast<uint4*>(ring_k + o) = tl.fk;
+        *reinterpret_cast<uint4*>(ring_v + o) = tl.fv;
+      }
     }
+  }
+  if (completes) {
     __syncthreads();
-    if (completes) requant_ring_lds(sm.ring_lds, sm.rq_ext);
+    requant_ring_lds(sm.ring_lds, sm.rq_ext);
     __syncthreads();
+  } else {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's slots are in LDS
   }
 
   if (wave < mbase) {
@@ -1346,11 +1382,12 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
       mm = pub_f(rm);
       ll = pub_f(rl);
     }
+    const bool one_head = P <= 64 && head0 + nmw >= gq;  // the common shape
     // ---- prefix merge, one head at a time per merging wave (lane s (+ 64 k) = partial s for
     // the weights, two columns per lane for the sum): m_p = max_s m_s, w_s = 2^(m_s - m_p),
-    // l_p = sum_s w_s l_s, pre_acc = sum_s w_s acc_s; then the head's words go back to zero
+    // l_p = sum_s w_s l_s, pre_acc = sum_s w_s acc_s
     float* wb = sm.wts + wave * WTS;
-    if (P <= 64 && head0 + nmw >= gq) {
+    if (one_head) {
       // one head, one chunk of partials: lane s holds m_s and l_s already
       const float ms = lane < P ? mm : NEG_INF;
       const float m = wave_max(ms);
@@ -1385,12 +1422,6 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
         sm.pre_m[head0] = m;
         sm.pre_l[head0] = l;
       }
-      if (lane < P) {
-        pub_clear(hws + (int64_t)lane * pw + gq * D + head0);
-        pub_clear(hws + (int64_t)lane * pw + gq * D + gq + head0);
-      }
-#pragma unroll 1
-      for (int s = 0; s < P; ++s) pub_clear2(hws + (int64_t)s * pw + head0 * D + 2 * lane);
     } else {
       for (int head = head0; head < gq; head += nmw) {
         const bool own = head == head0;
@@ -1461,22 +1492,16 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
           sm.pre_m[head] = m;
           sm.pre_l[head] = l;
         }
-#pragma unroll 1
-        for (int s = lane; s < P; s += 64) {
-          pub_clear(hws + (int64_t)s * pw + gq * D + head);
-          pub_clear(hws + (int64_t)s * pw + gq * D + gq + head);
-        }
-#pragma unroll 1
-        for (int s = 0; s < P; ++s) pub_clear2(hws + (int64_t)s * pw + head * D + 2 * lane);
       }
     }
-    if (__builtin_amdgcn_ballot_w64(lost) && lane == 0) sm.incomplete = 1;
+    if (lane == 0) sm.lost[wave] = __builtin_amdgcn_ballot_w64(lost) != 0;
   }
   __syncthreads();
 
   // ---- combine: one column per thread. Prefix: acc_p = sum_s w_s acc_s; then with the
   // ring's partials r: M = max(m_p, m_r), alpha = 2^(m_p - M), beta_r = 2^(m_r - M)
-  const bool failed = sm.incomplete != 0;
+  bool failed = false;
+  for (int w = mbase; w < TB_WAVES; ++w) failed |= w - mbase < gq && sm.lost[w] != 0;
   for (int col = tid; col < cols; col += TB_THREADS) {
     const int head = col / D;
     const float accp = sm.pre_acc[col];
@@ -1511,6 +1536,12 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     a.out[(int64_t)qh * D + d] = f2h(o);
     if (a.lse && d == 0) a.lse[qh] = failed ? __builtin_nanf("") : (l > 0.0f ? (M + __log2f(l) - P_SCALE_LOG2) * LN2 : NEG_INF);
   }
+  // ---- every word of the head's partials was consumed before the barrier above: the whole
+  // block [hws, hws + P pw) goes back to zero (plain 16-byte stores by every thread; pw is a
+  // multiple of 4; no one touches these words again in this launch, and the launch boundary
+  // orders the stores before the next launch's accesses)
+  uint4* blk = reinterpret_cast<uint4*>(hws);
+  for (int i = tid; i < P * pw / 4; i += TB_THREADS) blk[i] = uint4{0u, 0u, 0u, 0u};
 }
 
 template <int LAYOUT>
@@ -1602,10 +1633,12 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
     if (!PAGED && blockIdx.x == 0 && tid == 0) write_scalars(a, pos);
   }
 
+  half8_t qb[4];  // (kept for the merger's tail: the ring attention uses the same operand)
+  TailLoads tl;
+  const bool merger = !PAGED && a.inline_tail && part == 0;  // the contiguous fused step's merging workgroup
   if (prefix) {
     WaveState st;
     state_init(st);
-    half8_t qb[4];
     load_q_lds(q_lds, a.gq, qb);
 
     int gi = wave;
@@ -1653,6 +1686,8 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
       gi = nx;
     }
 
+    // the merger's ring rows, loaded while the partial below is merged and published
+    if (merger) tail_load_rows<false>(a, h, b, pos, pos_ok, tl);
     // ---- merge the waves through LDS (the stages are dead once every wave is here): per head
     // m = max_w m_w and the waves' weights 2^(m_w - m) once (threads < gq, into xch), then the
     // columns; the partial is published word by word (pub_st)
@@ -1702,7 +1737,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   // (pos, pos_ok, U as the prologue read them: the tail needs no second round trip for them)
   if (!a.inline_tail) return;
   if constexpr (!PAGED) {
-    if (part != 0) return;
+    if (!merger) return;
   }
   __syncthreads();  // the stages and the merge's LDS are dead: the tail reuses them
   TailSmem& sm = *reinterpret_cast<TailSmem*>(lds_raw);
@@ -1717,7 +1752,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
     __syncthreads();
     if (ticket == last) tail_body<true>(a, h, b, sm, TAIL_LAST, pos, pos_ok, U);
   } else {
-    tail_body<false>(a, h, b, sm, TAIL_MERGER, pos, pos_ok, U);
+    tail_body<false>(a, h, b, sm, TAIL_MERGER, pos, pos_ok, U, &tl, &qb);
   }
 }
 
