@@ -51,10 +51,12 @@ COPY_BYTES = 64 << 20
 APPEND_BYTES = 64 * 128 * 2 * 2 * HKV + 2 * 2 * 128 * 2 * HKV + 64 * 128 * 2 * HKV + 4 * 128 * 2 * HKV
 # the per-token symmetric append: the new token read, its codes and scale written
 APPEND_BYTES_TOK = 2 * 128 * 2 * HKV + 2 * 128 * HKV + 2 * 2 * HKV
-STEP_KERNEL = "attn_prefix_kernel"
+STEP_KERNEL = {"chain": "attn_layers_kernel", "layers": "attn_prefix_kernel"}
 COPY_KERNEL = "copy16_kernel"
-TRAFFIC = {"t64": ROOT / "profiles" / "decode_step_32k_traffic.txt",
-           "tok": ROOT / "profiles" / "decode_step_tok_32k_traffic.txt"}
+TRAFFIC = {("t64", "layers"): ROOT / "profiles" / "decode_step_32k_traffic.txt",
+           ("tok", "layers"): ROOT / "profiles" / "decode_step_tok_32k_traffic.txt",
+           ("t64", "chain"): ROOT / "profiles" / "decode_chain_32k_traffic.txt",
+           ("tok", "chain"): ROOT / "profiles" / "decode_chain_tok_32k_traffic.txt"}
 VOCAB_QWEN3_4B = 151936
 
 
@@ -96,6 +98,8 @@ def parse_args():
                     help="run one workload alone and print its line")
     ap.add_argument("--scheme", choices=("t64", "tok"), default="t64",
                     help="--workload decode: KV format, int8t64 (the reference's) or per-token symmetric")
+    ap.add_argument("--mode", choices=("chain", "layers"), default="chain",
+                    help="--workload decode: every layer in one launch (chain) or one launch per layer")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarize two rocprofv3 --pmc runs of the decode workload into the traffic file")
     return ap.parse_args()
@@ -104,8 +108,8 @@ def parse_args():
 # ---------------------------------------------------------------- rocprof traffic summaries
 
 
-def _pmc_means(run_dir: str, counter: str) -> dict:
-    """Mean per-dispatch value of ``counter`` per kernel (the step kernel, the copy kernel) in a
+def _pmc_means(run_dir: str, counter: str, kernel: str) -> dict:
+    """Mean per-dispatch value of ``counter`` per kernel (``kernel``, the copy kernel) in a
     rocprofv3 --pmc CSV run."""
     import csv
 
@@ -118,46 +122,51 @@ def _pmc_means(run_dir: str, counter: str) -> dict:
             for row in csv.DictReader(fh):
                 if row.get("Counter_Name") != counter:
                     continue
-                for key in (STEP_KERNEL, COPY_KERNEL):
+                for key in (kernel, COPY_KERNEL):
                     if key in row["Kernel_Name"]:
                         acc.setdefault(key, []).append(float(row["Counter_Value"]))
     return {k: sum(v) / len(v) for k, v in acc.items()}
 
 
-def write_traffic(fetch_dir: str, write_dir: str, scheme: str) -> None:
-    """HBM bytes per dispatch of the fused step kernel from FETCH_SIZE and WRITE_SIZE (KiB),
-    each scaled by the factor that makes the same counter read the copy kernel's known bytes."""
-    fetch, write = _pmc_means(fetch_dir, "FETCH_SIZE"), _pmc_means(write_dir, "WRITE_SIZE")
+def write_traffic(fetch_dir: str, write_dir: str, scheme: str, mode: str) -> None:
+    """HBM bytes per dispatch of the decode-step kernel (the chained launch, or one layer's fused
+    launch) from FETCH_SIZE and WRITE_SIZE (KiB), each scaled by the factor that makes the same
+    counter read the copy kernel's known bytes."""
+    kernel = STEP_KERNEL[mode]
+    fetch, write = _pmc_means(fetch_dir, "FETCH_SIZE", kernel), _pmc_means(write_dir, "WRITE_SIZE", kernel)
     f_scale = COPY_BYTES / (fetch[COPY_KERNEL] * 1024)
     w_scale = COPY_BYTES / (write[COPY_KERNEL] * 1024)
-    f_bytes = fetch[STEP_KERNEL] * 1024 * f_scale
-    w_bytes = write[STEP_KERNEL] * 1024 * w_scale
-    alg = step_launch_bytes(CTX + 1, scheme)
-    flag = " --scheme tok" if scheme == "tok" else ""
-    cmd = f"python3 bench.py --workload decode{flag} --steps 4 --warmup 1 --no-cpu-baseline --no-clock"
+    f_bytes = fetch[kernel] * 1024 * f_scale
+    w_bytes = write[kernel] * 1024 * w_scale
+    alg = step_launch_bytes(CTX + 1, scheme) * (LAYERS if mode == "chain" else 1)
+    flags = (" --scheme tok" if scheme == "tok" else "") + f" --mode {mode}"
+    cmd = f"python3 bench.py --workload decode{flags} --steps 4 --warmup 1 --no-cpu-baseline --no-clock"
+    what = (f"the chained decode step nkv::attn_layers_kernel<{1 if scheme == 'tok' else 0}> ({LAYERS} layers "
+            "in one launch)" if mode == "chain" else
+            f"the fused decode-step launch nkv::attn_prefix_kernel<{1 if scheme == 'tok' else 0}> (one layer)")
     lines = [
-        f"# HBM traffic of the fused decode-step launch nkv::attn_prefix_kernel<{1 if scheme == 'tok' else 0}> "
-        f"({'per-token symmetric' if scheme == 'tok' else 'int8t64'} format), 32k context, 32 q / 8 kv heads",
+        f"# HBM traffic of {what}, "
+        f"{'per-token symmetric' if scheme == 'tok' else 'int8t64'} format, 32k context, 32 q / 8 kv heads",
         "# made by (two rocprofv3 --pmc runs of the decode workload, then this summary):",
         f"#   rocprofv3 --pmc FETCH_SIZE -d FETCH_DIR -o run --output-format csv -- {cmd}",
         f"#   rocprofv3 --pmc WRITE_SIZE -d WRITE_DIR -o run --output-format csv -- {cmd}",
-        f"#   python3 bench.py --traffic-from FETCH_DIR WRITE_DIR{flag}",
+        f"#   python3 bench.py --traffic-from FETCH_DIR WRITE_DIR{flags}",
         f"copy_kernel_bytes: {COPY_BYTES}  (read, and again written, by nkv_copy_bytes)",
         f"copy_kernel_FETCH_SIZE_KiB: {fetch[COPY_KERNEL]:.1f}  -> fetch scale {f_scale:.4f}",
         f"copy_kernel_WRITE_SIZE_KiB: {write[COPY_KERNEL]:.1f}  -> write scale {w_scale:.4f}",
-        f"step_kernel_FETCH_SIZE_KiB: {fetch[STEP_KERNEL]:.1f}  -> {f_bytes:.0f} B",
-        f"step_kernel_WRITE_SIZE_KiB: {write[STEP_KERNEL]:.1f}  -> {w_bytes:.0f} B",
+        f"step_kernel_FETCH_SIZE_KiB: {fetch[kernel]:.1f}  -> {f_bytes:.0f} B",
+        f"step_kernel_WRITE_SIZE_KiB: {write[kernel]:.1f}  -> {w_bytes:.0f} B",
         f"algorithmic_bytes_per_launch: {alg}",
         f"traffic_bytes_per_launch: {f_bytes + w_bytes:.0f}",
         f"traffic_over_algorithmic: {(f_bytes + w_bytes) / alg:.4f}",
     ]
-    TRAFFIC[scheme].write_text("\n".join(lines) + "\n")
+    TRAFFIC[(scheme, mode)].write_text("\n".join(lines) + "\n")
     print("\n".join(lines))
 
 
-def read_traffic(scheme: str):
-    """HBM bytes per launch of the fused step kernel from the committed summary, or None."""
-    path = TRAFFIC[scheme]
+def read_traffic(scheme: str, mode: str):
+    """HBM bytes per launch of the decode-step kernel from the committed summary, or None."""
+    path = TRAFFIC[(scheme, mode)]
     if not path.exists():
         return None
     m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text(), re.M)
@@ -293,11 +302,14 @@ def _time_graph(graph, stream, reps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
-def run_decode(args, scheme: str, headline: bool) -> dict:
+def run_decode(args, scheme: str, headline: bool, mode: str = "chain") -> dict:
     """The 36-layer, 32k-context chained decode step on the int8t64 (``t64``) or per-token
-    symmetric (``tok``) cache; returns the result dict (the headline line when ``headline``)."""
+    symmetric (``tok``) cache; returns the result dict (the headline line when ``headline``).
+    ``mode`` "chain": every layer in one launch (``ChainedStep``, ``nkv_decode_layers_*``);
+    "layers": one fused launch per layer (``update_attend``, ``nkv_decode_step_*``)."""
     import torch
 
+    from nova_amd.chain import ChainedStep
     from nova_amd.kvattn import KVInt8Cache
     from nova_amd.kvtok import KVInt8TokCache
 
@@ -332,10 +344,18 @@ def run_decode(args, scheme: str, headline: bool) -> dict:
         prev = outs[layer - 1]  # layer 0: the previous step's last layer
         return prev[:, 0::HQ // HKV], prev[:, 1::HQ // HKV], prev
 
-    def launches():
-        for layer in range(L):
-            k, v, q = layer_inputs(layer)
-            cache.update_attend(k, v, q, layer, out=outs[layer])
+    if mode == "chain":
+        ins = [layer_inputs(layer) for layer in range(L)]
+        chain = ChainedStep(cache, [i[0] for i in ins], [i[1] for i in ins], [i[2] for i in ins],
+                            [outs[layer] for layer in range(L)])
+
+        def launches():
+            chain()
+    else:
+        def launches():
+            for layer in range(L):
+                k, v, q = layer_inputs(layer)
+                cache.update_attend(k, v, q, layer, out=outs[layer])
 
     def step():
         launches()
@@ -361,7 +381,7 @@ def run_decode(args, scheme: str, headline: bool) -> dict:
     assert int(cache.pos.item()) == pos0 + K
     assert torch.isfinite(outs).all()
 
-    # ---- the fused launch alone: a graph of the step's 36 chained launches (pos fixed), timed
+    # ---- the launches alone (pos fixed): the chained launch, or the step's 36 chained launches
     g_launch = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_launch):
         launches()
@@ -381,9 +401,17 @@ def run_decode(args, scheme: str, headline: bool) -> dict:
     ms_step = ms / K
     us = [pos0 + i + 1 for i in range(K)]  # tokens written when each timed step attends
     step_bytes = sum(step_launch_bytes(u, scheme) for u in us) / K * L
-    launch_bytes = step_launch_bytes(pos_l + 1, scheme)
-    per_launch_s = ms_launches / 1e3 / L
+    n_launch = 1 if mode == "chain" else L
+    launch_bytes = step_launch_bytes(pos_l + 1, scheme) * (L // n_launch)
+    per_launch_s = ms_launches / 1e3 / n_launch
     achieved = launch_bytes / per_launch_s / 1e9
+    kidx = 1 if scheme == "tok" else 0
+    if mode == "chain":
+        kname = (f"nkv::attn_layers_kernel<{kidx}> chained decode step ({L} layers x (append + split-K "
+                 f"partials + merge), one launch per step, {cache_parts(chain)})")
+    else:
+        kname = (f"nkv::attn_prefix_kernel<{kidx}> fused decode step (append + split-K partials + "
+                 "last-workgroup tail), one launch per layer")
     fmt = ("tok (int8 codes, one fp16 absmax scale per token and KV head)" if scheme == "tok"
            else "int8t64 (uint8 codes, fp16 min/step per 64 tokens per channel)")
     res = {
@@ -393,24 +421,31 @@ def run_decode(args, scheme: str, headline: bool) -> dict:
         "dtype": "fp16", "data": "synthetic",
         "config": {"workload": f"{'per-token symmetric int8' if scheme == 'tok' else 'int8t64'} KV decode step, "
                                f"{L} layers x (32 q / 8 kv heads, head_dim 128), batch 1, {ctx}-token prefilled "
-                               f"cache, layers chained through their outputs, {K} hipGraph-replayed steps",
+                               f"cache, layers chained through their outputs, {K} hipGraph-replayed steps, "
+                               f"{'all layers in one launch' if mode == 'chain' else 'one launch per layer'}",
                    "layers": L, "context": ctx, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "batch": 1,
-                   "kv_format": fmt, "parts_per_head": cache._n_parts},
+                   "kv_format": fmt, "launch": mode,
+                   "parts_per_head": chain.n_parts if mode == "chain" else cache._n_parts},
         "step_gbs": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
         "step_pct_of_hbm_peak": round(100 * step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS, 2),
         "wall_s_timed": round(wall, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(scheme),
-                     "kernel": f"nkv::attn_prefix_kernel<{1 if scheme == 'tok' else 0}> fused decode step "
-                               "(append + split-K partials + last-workgroup tail), one launch per layer",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(scheme, mode),
+                     "kernel": kname,
                      "algorithmic_bytes_per_launch": round(launch_bytes),
                      "avg_launch_us": round(per_launch_s * 1e6, 3),
-                     "launches_per_step": L},
+                     "launches_per_step": n_launch},
         "gpu_clock": clock,
     }
     del graph, g_launch, cache, outs
+    if mode == "chain":
+        del chain
     torch.cuda.empty_cache()
     return res
+
+
+def cache_parts(chain) -> str:
+    return f"{chain.n_parts} streaming + 1 merging workgroups per KV head"
 
 
 def run_paged(args, steps: int | None = None, scheme: str = "t64") -> dict:
@@ -590,7 +625,7 @@ def bench_e2e(args) -> dict:
 def main() -> int:
     args = parse_args()
     if args.traffic_from:
-        write_traffic(*args.traffic_from, scheme=args.scheme)
+        write_traffic(*args.traffic_from, scheme=args.scheme, mode=args.mode)
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not run here (the decode attention shards by "
@@ -610,14 +645,17 @@ def main() -> int:
     elif args.workload == "e2e":
         res = _standalone(bench_e2e(args), args)
     else:
-        res = run_decode(args, args.scheme, headline=True)
+        res = run_decode(args, args.scheme, headline=True, mode=args.mode)
         if not args.no_cpu_baseline:
             res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, args.scheme, args.ctx, args.layers)
         else:
             res["cpu_baseline"] = None
         if args.workload is None and not args.only:
             extra = {}
-            for name, fn in (("tok_decode", lambda: run_decode(args, "tok", headline=False)),
+            for name, fn in (("layer_launch_decode", lambda: run_decode(args, "t64", headline=False, mode="layers")),
+                             ("tok_decode", lambda: run_decode(args, "tok", headline=False)),
+                             ("tok_layer_launch_decode", lambda: run_decode(args, "tok", headline=False,
+                                                                            mode="layers")),
                              ("paged_batch", lambda: run_paged(args)),
                              ("paged_batch_tok", lambda: run_paged(args, scheme="tok")),
                              ("chunked_prefill", lambda: run_prefill(args))):
@@ -625,10 +663,11 @@ def main() -> int:
                     extra[name] = fn()
                 except Exception as e:  # noqa: BLE001 - one extra workload failing must not hide the headline
                     extra[name] = {"error": f"{type(e).__name__}: {e}"[:400]}
-            if "tok_decode" in extra and "error" not in extra["tok_decode"]:
-                t = extra["tok_decode"]
-                extra["tok_decode"] = {k: t[k] for k in ("value", "unit", "ms_per_step", "step_gbs",
-                                                         "step_pct_of_hbm_peak", "roofline", "config")}
+            for name in ("layer_launch_decode", "tok_decode", "tok_layer_launch_decode"):
+                if "error" not in extra[name]:
+                    t = extra[name]
+                    extra[name] = {k: t[k] for k in ("value", "unit", "ms_per_step", "step_gbs",
+                                                     "step_pct_of_hbm_peak", "roofline", "config")}
             res["workloads"] = extra
     print(json.dumps(res), flush=True)
     return 0

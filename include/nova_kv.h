@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 6
+#define NKV_ABI_VERSION 7
 
 #define NKV_OK 0
 #define NKV_ERR_INVALID 1     /* argument outside what the reference accepts */
@@ -301,6 +301,81 @@ int nkv_decode_step_combine_tok(const uint16_t* q, const uint16_t* k_new, const 
                                 int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out,
                                 float* lse_out, void* workspace, int64_t workspace_bytes,
                                 int64_t n_parts, void* stream);
+
+/*
+ * ---- Chained decode step: every layer of one token in one launch ----
+ * The decode step of a stack of layers whose inputs may be outputs of the layer before
+ * (q, k_new, v_new of layer l read from what layer l - 1 wrote, as a model's layers are
+ * chained). Layer l computes exactly nkv_decode_step_t64 (nkv_decode_step_tok) on its own
+ * cache: the same cache state and scalars bit for bit, the same output up to float
+ * summation order. Replaces the per-layer `KVInt8Cache.update` + `KVInt8Cache.attend` pairs
+ * that the graph-decode loop issues once per layer (src/nova/decode.py:301-320 running
+ * src/nova/layers.py:132-136 for every layer), for stacks whose inter-layer work is itself
+ * in the chain (here: outputs consumed directly as the next layer's inputs).
+ *
+ * One launch of hkv * (n_parts + 1) workgroups that must all be resident at once; the call
+ * checks that against the device's occupancy and returns NKV_ERR_UNSUPPORTED when they are
+ * not. Per KV head, n_parts workgroups stream the int8 prefix and one merges (append, ring,
+ * combine). No input of layer l is read before every output of layer l - 1 is written (a
+ * completion counter per layer, agent-scope release / acquire); layer l + 1's codes, which
+ * do not depend on layer l, stream in while layer l is merged.
+ *
+ * layers_dev: device array of n_layers entries, read by the kernel (it must stay unchanged
+ * while launches that use it are pending); layers_host: the same entries in host memory,
+ * checked here (every pointer non-null and 16-byte aligned, lse may be NULL), or NULL to
+ * skip the check. Every layer shares the device scalars (pos_dev, first_dev: the step's
+ * position; written/qlen/pg written once), capacity, head counts and kv_head_stride.
+ * workspace: nkv_layers_workspace_bytes(hkv, hq, n_parts, n_layers) bytes, zero-filled
+ * before its first use and kept for these calls of one configuration; every call leaves it
+ * zero-filled. n_parts <= 0 takes nkv_layers_default_parts. A wait that gives up (it cannot
+ * when the grid is resident) makes the affected outputs NaN and sets the int at byte offset
+ * (workspace_bytes & ~3) - 4 * (n_layers + 2) to 1; it stays set.
+ */
+typedef struct nkv_layer_t64 {
+  const uint16_t* q;      /* [hq, 128] fp16 */
+  const uint16_t* k_new;  /* [hkv, 128] fp16, head stride kv_head_stride */
+  const uint16_t* v_new;
+  uint8_t* kq;            /* the layer's cache, as nkv_decode_step_t64 takes it */
+  uint16_t* kmn;
+  uint16_t* kst;
+  uint8_t* vq;
+  uint16_t* vmn;
+  uint16_t* vst;
+  uint16_t* tail_k;
+  uint16_t* tail_v;
+  uint16_t* out;          /* [hq, 128] fp16 */
+  float* lse;             /* [hq] fp32, or NULL */
+} nkv_layer_t64;
+
+typedef struct nkv_layer_tok {
+  const uint16_t* q;
+  const uint16_t* k_new;
+  const uint16_t* v_new;
+  int8_t* kq;             /* the layer's cache, as nkv_decode_step_tok takes it */
+  uint16_t* ksc;
+  int8_t* vq;
+  uint16_t* vsc;
+  uint16_t* out;
+  float* lse;
+} nkv_layer_tok;
+
+int64_t nkv_layers_workspace_bytes(int64_t hkv, int64_t hq, int64_t n_parts, int64_t n_layers);
+
+/* Streaming parts per KV head for a cache of `capacity` tokens on the current device
+ * (tok != 0: the per-token symmetric kernel); 0 when the device cannot hold the grid. */
+int64_t nkv_layers_default_parts(int64_t hkv, int64_t capacity, int tok);
+
+int nkv_decode_layers_t64(const nkv_layer_t64* layers_dev, const nkv_layer_t64* layers_host,
+                          int64_t n_layers, int64_t kv_head_stride, const int64_t* pos_dev,
+                          const int64_t* first_dev, int64_t* written_dev, int64_t* qlen_dev,
+                          int64_t* pg_dev, int64_t hq, int64_t hkv, int64_t head_dim, int64_t capacity,
+                          void* workspace, int64_t workspace_bytes, int64_t n_parts, void* stream);
+
+int nkv_decode_layers_tok(const nkv_layer_tok* layers_dev, const nkv_layer_tok* layers_host,
+                          int64_t n_layers, int64_t kv_head_stride, const int64_t* pos_dev,
+                          int64_t* written_dev, int64_t hq, int64_t hkv, int64_t head_dim,
+                          int64_t capacity, void* workspace, int64_t workspace_bytes, int64_t n_parts,
+                          void* stream);
 
 /*
  * ---- Paged batch of ragged sequences (int8t64) ----

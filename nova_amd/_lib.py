@@ -63,6 +63,14 @@ SIGNATURES = {
     "nkv_decode_step_tok": (c_int, _STEP_TOK),
     "nkv_decode_step_partials_tok": (c_int, _STEP_TOK),
     "nkv_decode_step_combine_tok": (c_int, _STEP_TOK),
+    "nkv_layers_workspace_bytes": (I64, [I64, I64, I64, I64]),
+    "nkv_layers_default_parts": (I64, [I64, I64, c_int]),
+    # layers_dev, layers_host, n_layers, kv_head_stride, pos, first, written, qlen, pg, hq, hkv, head_dim,
+    # capacity, workspace, workspace_bytes, n_parts, stream
+    "nkv_decode_layers_t64": (c_int, [P, P, I64, I64, P, P, P, P, P, I64, I64, I64, I64, P, I64, I64, P]),
+    # layers_dev, layers_host, n_layers, kv_head_stride, pos, written, hq, hkv, head_dim, capacity,
+    # workspace, workspace_bytes, n_parts, stream
+    "nkv_decode_layers_tok": (c_int, [P, P, I64, I64, P, P, I64, I64, I64, I64, P, I64, I64, P]),
     "nkv_paged_workspace_bytes": (I64, [I64, I64, I64]),
     "nkv_paged_quantize_t64": (c_int, [P, c_int, I64, I64, I64, c_int, P, P, I64, I64, P]),
     "nkv_paged_append_t64": (c_int, [P, P, I64, I64, P, P, I64, I64, P, P, I64, I64, I64, P]),
@@ -84,7 +92,7 @@ SIGNATURES = {
     "nkv_qk_norm_rope": (c_int, [P, I64, I64, I64, P, P, c_float, P, P, P]),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lib = None
 _lock = threading.Lock()

@@ -1,0 +1,124 @@
+"""Chained decode step: the append + attention of every layer of one token in one launch.
+
+A model's layers are chained through their outputs: layer ``l``'s query and new K/V token
+come from what layer ``l - 1`` wrote. The per-layer decode step (``KVInt8Cache.update_attend``,
+one ``nkv_decode_step_t64`` launch per layer, replacing the ``update`` + ``attend`` pair that
+``LeanAttention.forward`` issues for every layer, src/nova/layers.py:132-136) pays one launch's
+ramp-up, drain and merge per layer. :class:`ChainedStep` runs the same per-layer computation
+for all layers in one launch (``nkv_decode_layers_t64`` / ``_tok``): each layer's inputs are
+read only after every output of the layer before is written, and the int8 prefix of layer
+``l + 1``, which does not depend on layer ``l``, streams into on-chip memory while layer ``l``
+is merged. Cache state and scalars are bit-identical to the per-layer launches; outputs agree
+up to float summation order.
+
+    chain = ChainedStep(cache, keys, values, queries, outs)   # outside graph capture
+    chain()                                                   # one step (capturable)
+    cache.pos.add_(1)
+
+The table of per-layer pointers is built once, on the host and in device memory, so the
+tensors passed in must stay allocated (the object keeps references to them) and a captured
+graph that launches the chain stays valid while the object lives.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _lib
+
+D = 128
+
+
+def _flat_ptr(x: torch.Tensor, name: str, shape: tuple, dtype: torch.dtype, device) -> int:
+    if tuple(x.shape) != shape or x.dtype != dtype or x.device != device:
+        raise ValueError(f"{name} must be {dtype} {list(shape)} on {device}, got {x.dtype} {list(x.shape)} on {x.device}")
+    if not x.is_contiguous() or x.data_ptr() % 16:
+        raise ValueError(f"{name} must be contiguous and 16-byte aligned")
+    return x.data_ptr()
+
+
+class ChainedStep:
+    """One decode token through ``len(queries)`` layers of ``cache`` (layer ``i`` of the list is
+    layer ``i`` of the cache) in one launch.
+
+    keys / values: per layer ``[1, H_kv, 1, 128]`` fp16 (rows contiguous and 16-byte aligned, one
+    head stride shared by every layer; views into another layer's output are fine); queries /
+    outs: per layer ``[1, H_q, 1, 128]`` contiguous fp16; lses: per layer ``[1, H_q]`` fp32, or
+    None. ``cache`` is a :class:`~nova_amd.kvattn.KVInt8Cache` (int8t64) or a
+    :class:`~nova_amd.kvtok.KVInt8TokCache` (per-token symmetric). ``n_parts`` is the number of
+    streaming workgroups per KV head (0: the library's default for this device).
+    """
+
+    def __init__(self, cache, keys, values, queries, outs, lses=None, n_parts: int = 0):
+        from .kvtok import KVInt8TokCache
+
+        lib = _lib.load()
+        self.cache = cache
+        self.tok = isinstance(cache, KVInt8TokCache)
+        if getattr(cache, "prefilling", False) or getattr(cache, "_in_prefill", False):
+            raise RuntimeError("the chained step decodes one token; finish the prefill first")
+        n = len(queries)
+        if not (len(keys) == len(values) == len(outs) == n) or (lses is not None and len(lses) != n):
+            raise ValueError("keys, values, queries, outs (and lses) need one entry per layer")
+        if n < 1 or n > cache.num_slots:
+            raise ValueError(f"{n} layers: the cache holds {cache.num_slots}")
+        hq, hkv, dev = cache.num_q_heads, cache.num_kv_heads, cache.pos.device
+        stride = None
+        rows = []
+        for i in range(n):
+            k, v = keys[i], values[i]
+            for name, t in (("key", k), ("value", v)):
+                if tuple(t.shape) != (1, hkv, 1, D) or t.dtype != torch.float16 or t.device != dev:
+                    raise ValueError(f"{name}[{i}] must be float16 [1, {hkv}, 1, {D}] on {dev}")
+                if t.stride(3) != 1 or t.stride(1) % 8 or t.data_ptr() % 16:
+                    raise ValueError(f"{name}[{i}] rows must be contiguous and 16-byte aligned")
+                if stride is None:
+                    stride = t.stride(1)
+                elif t.stride(1) != stride:
+                    raise ValueError("every key and value must share one head stride")
+            q = _flat_ptr(queries[i], f"queries[{i}]", (1, hq, 1, D), torch.float16, dev)
+            o = _flat_ptr(outs[i], f"outs[{i}]", (1, hq, 1, D), torch.float16, dev)
+            lse = 0
+            if lses is not None:
+                lse = _flat_ptr(lses[i], f"lses[{i}]", (1, hq), torch.float32, dev)
+            if self.tok:
+                rows.append([q, k.data_ptr(), v.data_ptr(), cache.kq[i].data_ptr(), cache.ksc[i].data_ptr(),
+                             cache.vq[i].data_ptr(), cache.vsc[i].data_ptr(), o, lse])
+            else:
+                rows.append([q, k.data_ptr(), v.data_ptr(), cache.kq[i].data_ptr(), cache.kmn[i].data_ptr(),
+                             cache.kst[i].data_ptr(), cache.vq[i].data_ptr(), cache.vmn[i].data_ptr(),
+                             cache.vst[i].data_ptr(), cache.tail_k[i].data_ptr(), cache.tail_v[i].data_ptr(), o, lse])
+        # nkv_layer_t64 / nkv_layer_tok: structs of 8-byte pointers, so an int64 array of rows
+        self._host = np.ascontiguousarray(np.array(rows, dtype=np.uint64).view(np.int64))
+        self._dev = torch.from_numpy(self._host.copy()).to(dev)
+        self._keep = (list(keys), list(values), list(queries), list(outs), list(lses or []))
+        self.n_layers, self.kv_head_stride = n, int(stride)
+        # (the default also caches the device's occupancy, so no query runs under a later capture)
+        default = int(lib.nkv_layers_default_parts(hkv, cache.max_len, int(self.tok)))
+        parts = int(n_parts) or default
+        if parts <= 0:
+            raise NotImplementedError("this device cannot hold the chained step's workgroups at once")
+        self.n_parts = parts
+        self.ws_bytes = int(lib.nkv_layers_workspace_bytes(hkv, hq, parts, n))
+        self.workspace = torch.zeros(-(-self.ws_bytes // 4), dtype=torch.int32, device=dev)
+        self.ws_bytes = self.workspace.numel() * 4
+
+    def _args(self) -> tuple:
+        c = self.cache
+        head = (self._dev.data_ptr(), self._host.ctypes.data, self.n_layers, self.kv_head_stride)
+        tail = (self.workspace.data_ptr(), self.ws_bytes, self.n_parts, _lib.stream_ptr(c.pos.device))
+        if self.tok:
+            return (*head, c.pos.data_ptr(), c._written.data_ptr(), c.num_q_heads, c.num_kv_heads, c.head_dim,
+                    c.max_len, *tail)
+        return (*head, c.pos.data_ptr(), c.first.data_ptr(), c._written.data_ptr(), c._qlen.data_ptr(),
+                c._pg.data_ptr(), c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_len, *tail)
+
+    def __call__(self) -> None:
+        """Launch the step on the current stream (capturable: no allocation, no host sync)."""
+        _lib.call("nkv_decode_layers_tok" if self.tok else "nkv_decode_layers_t64", *self._args())
+
+    def gave_up(self) -> bool:
+        """Whether a launch's wait ever gave up (its outputs are then NaN). Synchronizes."""
+        word = ((self.ws_bytes & ~3) - 4 * (self.n_layers + 2)) // 4
+        return bool(int(self.workspace[word].item()) != 0)

@@ -1145,12 +1145,17 @@ __device__ __forceinline__ uint64_t pub_repoll2(const float* p, uint64_t w, int&
   return w;
 }
 
-// The ring held in LDS (64 rows of K, then of V; ring_chunk_pos layout) requantized in place as
-// one int8t64 group, exactly as the append rules the group the new token completes: per channel
-// min / max over the 64 rows, step = max((max - min) / 255, 1e-8), codes by ruler_code_rcp,
-// then the values the prefix kernel would read back, fp16(code * step16 + min16) with one
-// rounding. Thread t takes channel t & 255 (K, then V) and rows 32 (t >> 8) .. + 31.
-__device__ __forceinline__ void requant_ring_lds(uint8_t* ring_lds, float (&ext)[2][2 * D]) {
+// The ring held in LDS (64 rows of K, then of V; ring_chunk_pos layout) requantized as one
+// int8t64 group, exactly as the append rules the group of the token at `pos`: per channel
+// min / max over the 64 rows, step = max((max - min) / 255, 1e-8), codes by ruler_code_rcp.
+// With STORE the codes (rows below the capacity) and the rulers go to group pos / 64 of head
+// h's cache: the append itself, from the ring that holds the new token in its slot. With `deq`
+// the LDS values become the ones the prefix kernel would read back, fp16(code * step16 +
+// min16) with one rounding (when the token completes its group, the tail attends those).
+// Thread t takes channel t & 255 (K, then V) and rows 32 (t >> 8) .. + 31.
+template <bool STORE>
+__device__ __forceinline__ void requant_ring_lds(uint8_t* ring_lds, float (&ext)[2][2 * D], bool deq,
+                                                 const AttnArgs* a = nullptr, int h = 0, int64_t pos = 0) {
   const int t = threadIdx.x, ch = t & (2 * D - 1), half = t >> 8;
   uint8_t* base = ring_lds + (ch >> 7) * RING_BYTES;
   const int c = ch & (D - 1);
@@ -1174,10 +1179,29 @@ __device__ __forceinline__ void requant_ring_lds(uint8_t* ring_lds, float (&ext)
   const float step = ruler_step(lo, hi), inv = ruler_inv(step);
   const half2_t st2 = half2_t{(_Float16)step, (_Float16)step};
   const half2_t mn2 = half2_t{(_Float16)lo, (_Float16)lo};
+  uint8_t* codes = nullptr;
+  int rows = 0;
+  if constexpr (STORE) {
+    // group pos / 64: code rows at the group's first token, rulers at its ruler row
+    const int which = ch >> 7;
+    const int64_t gcur = pos / GT, ro = ((int64_t)h * a->ngroups_cap + gcur) * D + c;
+    codes = (which ? a->vq : a->kq) + ((int64_t)h * a->capacity + gcur * GT) * D + c;
+    rows = (int)min<int64_t>(GT, a->capacity - gcur * GT);
+    if (half == 0) {
+      (which ? a->vmn : a->kmn)[ro] = f2h(lo);
+      (which ? a->vst : a->kst)[ro] = f2h(step);
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 32; i += 2) {
-    const half2_t code = half2_t{(_Float16)(float)ruler_code_rcp(v[i], lo, step, inv),
-                                 (_Float16)(float)ruler_code_rcp(v[i + 1], lo, step, inv)};
+    const uint32_t c0 = ruler_code_rcp(v[i], lo, step, inv), c1 = ruler_code_rcp(v[i + 1], lo, step, inv);
+    if constexpr (STORE) {
+      const int r = 32 * half + i;
+      if (r < rows) codes[r * D] = (uint8_t)c0;
+      if (r + 1 < rows) codes[(r + 1) * D] = (uint8_t)c1;
+    }
+    if (!deq) continue;
+    const half2_t code = half2_t{(_Float16)(float)c0, (_Float16)(float)c1};
     const half2_t y = __builtin_elementwise_fma(code, st2, mn2);
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
@@ -1249,10 +1273,18 @@ __device__ __forceinline__ void tail_load_rows(const AttnArgs& a, int h, int b, 
   }
 }
 
+// `flags` (the chained-layer kernel's merger): TB_APPEND, the tail also appends the new token:
+// it stores the token into its ring slot (per-token symmetric: the token's codes and scale) and,
+// when the token completes its group, requantizes the ring from LDS into group pos / 64 (else the
+// caller does that afterwards with the ring still in sm.ring_lds: append_from_ring);
+// TB_KEEP_BLOCK, the consumed partial block is left for the caller to zero; TB_POISON, the
+// caller's own wait for its inputs gave up: the output is NaN.
+constexpr int TB_APPEND = 1, TB_KEEP_BLOCK = 2, TB_POISON = 4;
+
 template <bool PAGED>
 __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailSmem& sm, int run, int64_t pos,
                                           bool pos_ok, int64_t U, const TailLoads* pre = nullptr,
-                                          const half8_t (*pre_q)[4] = nullptr) {
+                                          const half8_t (*pre_q)[4] = nullptr, int flags = 0) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const bool poll = run != TAIL_KERNEL;  // partials written in this launch: poll their words
   const int gq = a.gq, pw = part_stride(gq), cols = gq * D;
@@ -1269,6 +1301,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   const bool tok1 = ring && a.tok;  // per-token symmetric fused step: the tail is the new token
   const bool fresh_on = ring && !tok1 && !PAGED && a.tail_mode == TAIL_FUSED;
   const int fresh_slot = (int)(pos % GT);
+  const bool appends = !PAGED && (flags & TB_APPEND) && fused && pos_ok;  // (the merger of the chained step)
   TailLoads tl;
   if (pre) tl = *pre;
   else tail_load_rows<PAGED>(a, h, b, pos, pos_ok, tl);
@@ -1289,14 +1322,18 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   float mm = NEG_INF, ll = 0.0f;  // merging wave: lane s's m / l of its first head
   uint32_t rm = PUB_KEY, rl = PUB_KEY;  // their published words (beyond P: words of 0.0)
   uint64_t rv[MERGE_PRE];               // and those of its columns 2 lane, 2 lane + 1 of the first MERGE_PRE partials
-  int budget = MERGER_SPIN_LIMIT;
+  int budget = (flags & TB_POISON) ? 0 : MERGER_SPIN_LIMIT;  // (poisoned: the output is NaN anyway)
   if (merging) {
+    // (appending, the words are first loaded by the poll below: their registers would otherwise
+    // stay live across the requantization, which the partials are far from being ready for)
+    const bool pre_ld = !(flags & TB_APPEND);
     if (lane < P) {
-      rm = pub_ld(hws + (int64_t)lane * pw + gq * D + head0);
-      rl = pub_ld(hws + (int64_t)lane * pw + gq * D + gq + head0);
+      rm = pre_ld ? pub_ld(hws + (int64_t)lane * pw + gq * D + head0) : 0u;
+      rl = pre_ld ? pub_ld(hws + (int64_t)lane * pw + gq * D + gq + head0) : 0u;
     }
 #pragma unroll
-    for (int u = 0; u < MERGE_PRE; ++u) rv[u] = u < P ? pub_ld2(hws + (int64_t)u * pw + head0 * D + 2 * lane) : PUB_KEY2;
+    for (int u = 0; u < MERGE_PRE; ++u)
+      rv[u] = u < P ? (pre_ld ? pub_ld2(hws + (int64_t)u * pw + head0 * D + 2 * lane) : 0ull) : PUB_KEY2;
   }
 
   // ---- each ring wave stages its own 16 slots in LDS (chunk ^ (row & 15) layout), the new token
@@ -1317,6 +1354,11 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
         const _Float16 sc = (_Float16)scale;
         *reinterpret_cast<half8_t*>((rw == 0 ? ring_k : ring_v) + (ring_chunk_pos(0, cl) << 4)) =
             dq8_sym(cw.x, cw.y, half2_t{sc, sc});
+        if (appends) {
+          const int64_t row = (int64_t)h * a.capacity + pos;
+          *reinterpret_cast<uint2*>((rw == 0 ? a.kq : a.vq) + row * D + 8 * cl) = cw;
+          if (cl == 0) (rw == 0 ? a.ksc : a.vsc)[row] = f2h(scale);
+        }
       }
     } else {
 #pragma unroll
@@ -1330,12 +1372,22 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
         const int o = fresh_slot * (2 * D) + (ring_chunk_pos(fresh_slot, cl) << 4);
         *reinterpret_cast<uint4*>(ring_k + o) = tl.fk;
         *reinterpret_cast<uint4*>(ring_v + o) = tl.fv;
+        if (appends) {  // the ring slot of the new token
+          *reinterpret_cast<uint4*>(const_cast<uint16_t*>(ring_of(a, h, 0)) + fresh_slot * D + 8 * cl) = tl.fk;
+          *reinterpret_cast<uint4*>(const_cast<uint16_t*>(ring_of(a, h, 1)) + fresh_slot * D + 8 * cl) = tl.fv;
+        }
       }
     }
   }
-  if (completes) {
+  if (appends && completes) {
+    // (a token that does not complete its group is requantized into it by the caller, after the
+    // output: nothing in the launch reads that group, and the merging waves poll meanwhile)
     __syncthreads();
-    requant_ring_lds(sm.ring_lds, sm.rq_ext);
+    requant_ring_lds<true>(sm.ring_lds, sm.rq_ext, true, &a, h, pos);
+    __syncthreads();
+  } else if (completes) {
+    __syncthreads();
+    requant_ring_lds<false>(sm.ring_lds, sm.rq_ext, true);
     __syncthreads();
   } else {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's slots are in LDS
@@ -1500,7 +1552,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
 
   // ---- combine: one column per thread. Prefix: acc_p = sum_s w_s acc_s; then with the
   // ring's partials r: M = max(m_p, m_r), alpha = 2^(m_p - M), beta_r = 2^(m_r - M)
-  bool failed = false;
+  bool failed = (flags & TB_POISON) != 0;
   for (int w = mbase; w < TB_WAVES; ++w) failed |= w - mbase < gq && sm.lost[w] != 0;
   for (int col = tid; col < cols; col += TB_THREADS) {
     const int head = col / D;
@@ -1540,6 +1592,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   // block [hws, hws + P pw) goes back to zero (plain 16-byte stores by every thread; pw is a
   // multiple of 4; no one touches these words again in this launch, and the launch boundary
   // orders the stores before the next launch's accesses)
+  if (flags & TB_KEEP_BLOCK) return;
   uint4* blk = reinterpret_cast<uint4*>(hws);
   for (int i = tid; i < P * pw / 4; i += TB_THREADS) blk[i] = uint4{0u, 0u, 0u, 0u};
 }
@@ -1753,6 +1806,327 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
     if (ticket == last) tail_body<true>(a, h, b, sm, TAIL_LAST, pos, pos_ok, U);
   } else {
     tail_body<false>(a, h, b, sm, TAIL_MERGER, pos, pos_ok, U, &tl, &qb);
+  }
+}
+
+// ---------------------------------------------------------------- kernel C: chained layers
+//
+// One decode step of n_layers layers in one launch (nkv_decode_layers_t64 / _tok). Layer l is
+// the fused step of its own cache (append, split-K prefix, ring, merge), and its inputs (q,
+// k_new, v_new) may be outputs of layer l - 1: a model's layers chained through their outputs.
+//
+// Grid: hkv x (P + 1) workgroups of 8 waves, all resident at once (one per CU; the host checks
+// the occupancy before launching). Workgroup (h, 0) is head h's merger: per layer it appends
+// the new token (the ring, staged in LDS for the ring attention, requantized into the current
+// group), attends over the ring, merges the P prefix partials of its head, writes out / lse and
+// counts itself on the layer's completion counter. Workgroup (h, p + 1) streams part p of
+// head h's int8 prefix into one published partial, as the prefix kernel does.
+//
+// Ordering. Before a workgroup reads layer l's inputs, one lane waits for layer l - 1's counter
+// to reach hkv (relaxed agent-scope polls, then an agent-scope acquire fence); a merger adds to
+// its layer's counter with an agent-scope release after every wave's out / lse stores have
+// completed and the workgroup has met at a barrier. So every output of layer l - 1 happens
+// before every read of layer l's inputs. The prefix partials use the published-word protocol of
+// the fused tail (per-location coherence, no flag); each layer has its own partial block.
+//
+// Overlap. Nothing in a layer's prefix depends on an earlier layer (the append writes only the
+// current group, which the prefix does not read), so as soon as a streaming workgroup has
+// published its layer-l partial, its waves issue their first group of layer l + 1 into their
+// LDS stages, and HBM keeps streaming while the mergers finish layer l. Wave 7 loads q after the
+// counter wait.
+//
+// Termination. Every wait gives up after a bounded number of polls; a streaming workgroup that
+// gave up publishes an l of NaN, so the merged output is NaN, and sets the error word. At the
+// end every workgroup takes an exit ticket (acquire-release); the last one sets the layer
+// counters and the ticket back to zero, so every launch starts and ends with them at zero.
+constexpr int IN_WAVE = WAVES - 1;                 // a streaming workgroup's input wave
+constexpr uint64_t LAYER_WAIT_TICKS = 20000000ull;  // 0.2 s of the 100 MHz real-time counter per wait
+
+// The sync words of a chained launch at the workspace's end (tail_ctr_end): done[l] at
+// end[-1 - l], the exit ticket at end[-1 - n_layers], the error word at end[-2 - n_layers].
+__device__ __forceinline__ int* layer_done(const AttnArgs& a, int l) { return a.tail_ctr_end - 1 - l; }
+
+// Layer l's arguments: the cache and step pointers of its table entry (nkv_layer_t64, or
+// nkv_layer_tok for the per-token symmetric format), and its own partial block.
+template <bool TOK>
+__device__ __forceinline__ AttnArgs layer_args(const AttnArgs& a, const void* layers, int l) {
+  AttnArgs la = a;
+  if constexpr (TOK) {
+    const nkv_layer_tok& e = static_cast<const nkv_layer_tok*>(layers)[l];
+    la.q = e.q;
+    la.k_new = e.k_new;
+    la.v_new = e.v_new;
+    la.kq = reinterpret_cast<uint8_t*>(e.kq);
+    la.vq = reinterpret_cast<uint8_t*>(e.vq);
+    la.ksc = e.ksc;
+    la.vsc = e.vsc;
+    la.out = e.out;
+    la.lse = e.lse;
+  } else {
+    const nkv_layer_t64& e = static_cast<const nkv_layer_t64*>(layers)[l];
+    la.q = e.q;
+    la.k_new = e.k_new;
+    la.v_new = e.v_new;
+    la.kq = e.kq;
+    la.kmn = e.kmn;
+    la.kst = e.kst;
+    la.vq = e.vq;
+    la.vmn = e.vmn;
+    la.vst = e.vst;
+    la.tail_k = e.tail_k;
+    la.tail_v = e.tail_v;
+    la.out = e.out;
+    la.lse = e.lse;
+  }
+  la.ws = a.ws + (int64_t)l * a.hkv * a.n_parts * part_stride(a.gq);
+  return la;
+}
+
+// Wait (lane 0 of the calling wave) until layer l's counter reaches `target`, then an
+// agent-scope acquire fence by the whole wave; false when the wait gave up (after
+// LAYER_WAIT_TICKS, or at once when an earlier wait of the workgroup gave up: `lost`).
+__device__ __forceinline__ bool wait_layer(const AttnArgs& a, int l, int target, bool lost) {
+  bool ok = !lost;
+  if ((threadIdx.x & 63) == 0 && ok) {
+    const int* ctr = layer_done(a, l);
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > LAYER_WAIT_TICKS) {
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  return __builtin_amdgcn_readfirstlane(ok ? 1 : 0) != 0;
+}
+
+// The append of the token at `pos` from the ring held in LDS (the 64 slots, the new token in its
+// slot; ring_chunk_pos layout) by the 256 threads of waves 0..3: thread t rules channel t & 127 of K
+// (t < 128) or V over the 64 slots, exactly as append_unit rules it, and stores its two ruler
+// values; the wave's 64 x 64 codes go through `xpose` (4 KiB of LDS per wave) so that lane r
+// stores row r's 64 codes with four 16-byte stores (rows below the capacity). No workgroup
+// barrier: the caller's waves 0..3 staged the ring and a workgroup barrier followed.
+__device__ __forceinline__ void append_ring_channels(const AttnArgs& a, int h, int64_t pos, const uint8_t* ring_lds,
+                                                     uint8_t* xpose) {
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, which = t >> 7, c = t & (D - 1);
+  const uint8_t* base = ring_lds + which * RING_BYTES;
+  float v[GT];
+  float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+#pragma unroll
+  for (int r = 0; r < GT; ++r) {
+    v[r] = h2f(*reinterpret_cast<const uint16_t*>(base + r * (2 * D) + (ring_chunk_pos(r, c >> 3) << 4) + 2 * (c & 7)));
+    mn = fminf(mn, v[r]);
+    mx = fmaxf(mx, v[r]);
+  }
+  const float step = ruler_step(mn, mx), inv = ruler_inv(step);
+  const int64_t gcur = pos / GT, ro = ((int64_t)h * a.ngroups_cap + gcur) * D + c;
+  (which ? a.vmn : a.kmn)[ro] = f2h(mn);
+  (which ? a.vst : a.kst)[ro] = f2h(step);
+  // codes: column `lane` of the wave's [64 rows][64 channels] block, then row `lane` of it
+  uint8_t* xw = xpose + wave * (GT * 64);
+#pragma unroll
+  for (int r = 0; r < GT; ++r) xw[r * 64 + lane] = (uint8_t)ruler_code_rcp(v[r], mn, step, inv);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // (one wave: its LDS accesses run in order)
+  const int rows = (int)min<int64_t>(GT, a.capacity - gcur * GT);
+  if (lane < rows) {
+    uint4* dst = reinterpret_cast<uint4*>((which ? a.vq : a.kq) + ((int64_t)h * a.capacity + gcur * GT + lane) * D +
+                                          64 * (wave & 1));
+    const uint4* src = reinterpret_cast<const uint4*>(xw + lane * 64);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) dst[k] = src[k];
+  }
+}
+
+// One layer of head h's merger (workgroup (h, 0) of the chained kernel): wait for layer l - 1,
+// append + ring + merge of layer l into out / lse, count itself on layer l's counter. Returns
+// whether its wait gave up. (The consumed partial block is zeroed at the end of the launch.) (Not inlined: inside the layer loop
+// the compiler would keep the tail's loop-invariant addresses live across the streaming code.)
+template <bool TOK>
+__device__ __noinline__ bool merger_layer(const AttnArgs& la, int l, int h, uint8_t* lds_raw, int64_t pos, bool pos_ok,
+                                          int64_t U, bool lost) {
+  __shared__ int lost_sh;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int P = la.n_parts, pw = part_stride(la.gq);
+  if (wave == IN_WAVE) {
+    const bool ok = l == 0 || wait_layer(la, l - 1, la.hkv, lost);
+    if (tid == IN_WAVE * 64) lost_sh = ok ? 0 : 1;
+  }
+  __syncthreads();
+  const bool gave_up = lost_sh != 0;
+  if (l == 0 && blockIdx.x == 0 && tid == 0 && pos_ok) write_scalars(la, pos);
+  TailSmem& sm = *reinterpret_cast<TailSmem*>(lds_raw);
+  tail_body<false>(la, h, 0, sm, TAIL_MERGER, pos, pos_ok, U, nullptr, nullptr,
+                   TB_APPEND | TB_KEEP_BLOCK | (lost || gave_up ? TB_POISON : 0));
+  // every wave's stores (out, lse, the ring slot) complete before the workgroup meets; then one
+  // release at agent scope publishes them all with the count
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) __hip_atomic_fetch_add(layer_done(la, l), 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  // Waves 0..3 finish the layer after the count; wave 7, which waits for the next layer's counter,
+  // then has no stores of its own in flight (a wait for its polls would wait for them too).
+  // (the append's requantization of the ring, still in LDS, into group pos / 64, unless the tail
+  // did it because the token completed the group; the next launch is the first to read the group)
+  if (wave < RING_PARTS && !TOK && pos_ok && (pos + 1) % GT != 0)
+    append_ring_channels(la, h, pos, sm.ring_lds, reinterpret_cast<uint8_t*>(sm.ring_part));
+  return gave_up;
+}
+
+template <int LAYOUT>
+__global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, const void* layers, int n_layers) {
+  static_assert(LAYOUT == CONTIG_T64 || LAYOUT == CONTIG_TOK, "contiguous caches");
+  constexpr bool TOK = LAYOUT == CONTIG_TOK;
+  __shared__ __attribute__((aligned(16))) uint8_t lds_raw[TOK ? LDS_BYTES_TOK : LDS_BYTES];
+  __shared__ __attribute__((aligned(16))) uint16_t q_lds[16 * D];
+  __shared__ __attribute__((aligned(16))) float xch[16 * WAVES];
+  __shared__ int lost_sh;
+  float* lds = reinterpret_cast<float*>(lds_raw);
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = blockIdx.x % a.hkv, role = blockIdx.x / a.hkv;
+  const int P = a.n_parts, gq = a.gq, pw = part_stride(gq);
+  int64_t pos;
+  bool pos_ok;
+  const int64_t U = prefix_limit(a, pos, pos_ok);
+  const int64_t W = (U + GT - 1) / GT;
+  const bool merger = role == 0;
+  const int part = role - 1;
+  const int64_t gs = merger ? 0 : (int64_t)part * W / P;
+  const int64_t ge = merger ? 0 : (int64_t)(part + 1) * W / P;
+  const int ng = (int)(ge - gs);
+  constexpr int wave_lds = TOK ? WAVE_LDS_TOK : WAVE_LDS;
+  constexpr int slot_bytes = TOK ? HALF_SLOT_TOK : HALF_SLOT;
+  uint8_t* my_stages = lds_raw + wave * wave_lds;
+  const uint32_t my_lds = __builtin_amdgcn_readfirstlane(lds_addr(my_stages));
+  const uint32_t rul_lds = my_lds + 2 * HALF_SLOT;
+  bool lost = false;  // a counter wait of this workgroup gave up
+
+  // the wave's first group (both halves; int8t64: its rulers into ruler set 0)
+  auto issue_first = [&](const AttnArgs& la) {
+    if (wave >= ng) return;
+    if constexpr (TOK) {
+      issue_tok<false>(la, 0, h, gs + wave, 0, my_lds);
+      issue_tok<false>(la, 0, h, gs + wave, 1, my_lds + HALF_SLOT_TOK);
+    } else {
+      issue_half(la, h, gs + wave, 0, my_lds, rul_lds);
+      issue_half(la, h, gs + wave, 1, my_lds + HALF_SLOT, rul_lds);
+    }
+  };
+  if (merger) {
+    for (int l = 0; l < n_layers; ++l) lost |= merger_layer<TOK>(layer_args<TOK>(a, layers, l), l, h, lds_raw, pos, pos_ok, U, lost);
+    // the last layer's consumed partial block back to zero (the earlier layers' slots are zeroed
+    // by their writers, below)
+    uint4* blk = reinterpret_cast<uint4*>(layer_args<TOK>(a, layers, n_layers - 1).ws + (int64_t)h * P * pw);
+    for (int i = tid; i < P * pw / 4; i += THREADS) blk[i] = uint4{0u, 0u, 0u, 0u};
+  } else {
+  if (wave != IN_WAVE) issue_first(layer_args<TOK>(a, layers, 0));
+  for (int l = 0; l < n_layers; ++l) {
+    const AttnArgs la = layer_args<TOK>(a, layers, l);
+
+    // ---- streaming part: q of layer l once layer l - 1 is complete (layer 0: the input wave's
+    // first group goes behind q; later layers: it was prefetched with the others' and has long
+    // landed when the counter wait ends, so waiting for q waits for nothing else)
+    if (wave == IN_WAVE) {
+      const bool ok = l == 0 || wait_layer(a, l - 1, a.hkv, lost);
+      if (tid == IN_WAVE * 64) lost_sh = ok ? 0 : 1;
+      issue_q(la.q + (int64_t)h * gq * D, gq, __builtin_amdgcn_readfirstlane(lds_addr(q_lds)));
+      wait_groups_all();
+      if (l == 0) issue_first(la);
+    }
+    __syncthreads();
+    lost |= lost_sh != 0;
+    WaveState st;
+    state_init(st);
+    half8_t qb[4];
+    load_q_lds(q_lds, gq, qb);
+    int gi = wave;
+    for (int rs = 0; gi < ng; rs ^= 1) {
+      const int64_t grp = gs + gi;
+      const uint8_t* rul = my_stages + 2 * HALF_SLOT + rs * RULER_BYTES;
+      const uint8_t* slot1 = my_stages + slot_bytes;
+      const int nx = gi + WAVES;
+      const int nv1 = (int)min<int64_t>(32, U - grp * GT), nv2 = (int)min<int64_t>(32, U - grp * GT - 32);
+      if constexpr (TOK) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_HALF_TOK) : "memory");
+        attend_block_tok(la, st, qb, my_stages, my_stages + HALF_CODE,
+                         reinterpret_cast<const uint16_t*>(my_stages + 2 * HALF_CODE),
+                         reinterpret_cast<const uint16_t*>(my_stages + 2 * HALF_CODE + TOK_SCALE_BYTES), nv1);
+        if (nx < ng) issue_tok<false>(la, 0, h, gs + nx, 0, my_lds);
+        if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_HALF_TOK) : "memory");
+        else wait_groups_all();
+        if (nv2 > 0)
+          attend_block_tok(la, st, qb, slot1, slot1 + HALF_CODE, reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE),
+                           reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE + TOK_SCALE_BYTES), nv2);
+        if (nx < ng) issue_tok<false>(la, 0, h, gs + nx, 1, my_lds + HALF_SLOT_TOK);
+      } else {
+        LaneRulers ru;
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_SECOND_HALF) : "memory");
+        load_rulers(rul, ru);
+        attend_block<1>(la, st, qb, my_stages, my_stages + HALF_CODE, ru, nv1);
+        if (nx < ng) issue_half(la, h, gs + nx, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
+        if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF) : "memory");
+        else wait_groups_all();
+        if (nv2 > 0) attend_block<1>(la, st, qb, slot1, slot1 + HALF_CODE, ru, nv2);
+        if (nx < ng) issue_half(la, h, gs + nx, 1, my_lds + HALF_SLOT, 0u);
+      }
+      gi = nx;
+    }
+
+    // ---- merge the waves through LDS and publish the partial word by word
+    __syncthreads();
+    store_wave_partial(st, gq, lds + wave * pw);
+    __syncthreads();
+    float* dst = la.ws + ((int64_t)h * P + part) * pw;
+    float pm = NEG_INF, pl = 0.0f;
+    if (tid < gq) {
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) pm = fmaxf(pm, lds[w * pw + gq * D + tid]);
+      const float mu = pm == NEG_INF ? 0.0f : pm;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        const float x = __builtin_amdgcn_exp2f(lds[w * pw + gq * D + tid] - mu);
+        xch[tid * WAVES + w] = x;
+        pl += lds[w * pw + gq * D + gq + tid] * x;
+      }
+    }
+    __syncthreads();
+    for (int e = 2 * tid; e < gq * D; e += 2 * THREADS) {
+      const float* c = xch + (e / D) * WAVES;
+      float x = 0.0f, y = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        x += lds[w * pw + e] * c[w];
+        y += lds[w * pw + e + 1] * c[w];
+      }
+      pub_st2(dst + e, x, y);
+    }
+    if (tid < gq) {
+      pub_st(dst + gq * D + tid, pm);
+      pub_st(dst + gq * D + gq + tid, lost ? __builtin_nanf("") : pl);  // a lost wait poisons the merge
+    }
+    // ---- the stages are free: the next layer's first groups stream while this layer merges
+    __syncthreads();
+    if (l + 1 < n_layers) issue_first(layer_args<TOK>(a, layers, l + 1));
+  }
+  // every merger has consumed layers 0 .. n_layers - 2 (this workgroup passed the last counter
+  // wait): their slots of this part back to zero, read again by the next launch
+  for (int l = 0; l + 1 < n_layers; ++l) {
+    uint4* slot = reinterpret_cast<uint4*>(a.ws + ((int64_t)l * a.hkv * P + (int64_t)h * P + part) * pw);
+    for (int i = tid; i < pw / 4; i += THREADS) slot[i] = uint4{0u, 0u, 0u, 0u};
+  }
+  }
+
+  // ---- exit ticket: the last workgroup sets the counters back to zero
+  __syncthreads();
+  if (tid == 0) {
+    int* exit_ctr = a.tail_ctr_end - 1 - n_layers;
+    if (lost) __hip_atomic_store(exit_ctr - 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int t = __hip_atomic_fetch_add(exit_ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (t == (int)gridDim.x - 1) {
+      for (int l = 0; l < n_layers; ++l) __hip_atomic_store(layer_done(a, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(exit_ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -2738,4 +3112,145 @@ extern "C" int nkv_prefill_attn_hist_t64(const uint16_t* q, int64_t m, const uin
                                          int64_t splits, void* stream) {
   return prefill_attn("prefill_attn_hist_t64", q, m, k16, v16, m_kv, kv_head_stride, kq, kmn, kst, vq, vmn, vst,
                       capacity, used, hq, hkv, head_dim, out, workspace, workspace_bytes, splits, stream);
+}
+
+// ---- the chained decode step: every layer of one token in one launch (kernel C)
+
+namespace {
+std::mutex g_layers_mu;
+int g_layers_resident[MAX_DEVICES][2];  // workgroups of attn_layers_kernel resident at once (0: not known yet)
+
+// Workgroups of the chained kernel (int8t64 or per-token symmetric) that the current device
+// holds at once: CUs x workgroups per CU from the occupancy query.
+int layers_resident(bool tok, int* out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+    return fail(NKV_ERR_HIP, "decode_layers: no usable current device (%d)", dev);
+  std::lock_guard<std::mutex> lock(g_layers_mu);
+  int& r = g_layers_resident[dev][tok ? 1 : 0];
+  if (!r) {
+    int cus = 0, per_cu = 0;
+    hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess)
+      e = tok ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_layers_kernel<CONTIG_TOK>, THREADS, 0)
+              : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_layers_kernel<CONTIG_T64>, THREADS, 0);
+    if (e != hipSuccess) return fail(NKV_ERR_HIP, "decode_layers: occupancy query: %s", hipGetErrorString(e));
+    r = cus * per_cu;
+  }
+  *out = r;
+  return NKV_OK;
+}
+
+int64_t layers_sync_bytes(int64_t n_layers) { return ctr_bytes(n_layers + 2); }
+
+// Streaming parts per KV head: one workgroup per 8 groups at most, and hkv (parts + 1) workgroups
+// resident at once.
+int64_t layers_parts(int64_t hkv, int64_t groups, int resident) {
+  const int64_t fit = resident / std::max<int64_t>(1, hkv) - 1;
+  return std::min<int64_t>(std::min<int64_t>(fit, WTS), std::max<int64_t>(1, cdiv(groups, 8)));
+}
+
+bool al8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+
+// Launch of attn_layers_kernel: the checks common to both formats, the grid, the launch.
+int launch_layers(AttnArgs& a, bool tok, const void* layers_dev, int64_t n_layers, int64_t n_parts,
+                  int64_t workspace_bytes, hipStream_t s, const char* what) {
+  if (n_layers <= 0 || n_layers > (1 << 20)) return fail(NKV_ERR_INVALID, "%s: n_layers %lld outside [1, 2^20]", what, (long long)n_layers);
+  if (!layers_dev || !al8(layers_dev)) return fail(NKV_ERR_INVALID, "%s: the layer table must be a non-null, 8-byte aligned device array", what);
+  if (a.capacity > (int64_t(1) << 24)) return fail(NKV_ERR_UNSUPPORTED, "%s: capacity %lld exceeds 16M tokens", what, (long long)a.capacity);
+  int resident = 0;
+  if (int rc = layers_resident(tok, &resident)) return rc;
+  if (n_parts <= 0) n_parts = layers_parts(a.hkv, a.ngroups_cap, resident);
+  if (n_parts < 1 || n_parts > WTS)
+    return fail(NKV_ERR_UNSUPPORTED, "%s: %lld streaming parts per KV head (1..%d)", what, (long long)n_parts, WTS);
+  const int64_t grid = (int64_t)a.hkv * (n_parts + 1);
+  if (grid > resident)
+    return fail(NKV_ERR_UNSUPPORTED,
+                "%s: %lld workgroups (%d KV heads x (%lld parts + 1)) exceed the %d this device holds at once",
+                what, (long long)grid, a.hkv, (long long)n_parts, resident);
+  const int64_t need = n_layers * a.hkv * n_parts * part_floats(a.hq, a.hkv) * (int64_t)sizeof(float) + layers_sync_bytes(n_layers);
+  if (!a.ws || !al16(a.ws)) return fail(NKV_ERR_INVALID, "%s: the workspace must be a non-null, 16-byte aligned buffer", what);
+  if (workspace_bytes < need)
+    return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
+  a.n_parts = (int)n_parts;
+  a.tail_ctr_end = reinterpret_cast<int*>(reinterpret_cast<char*>(a.ws) + (workspace_bytes & ~int64_t(3)));
+  if (tok) hipLaunchKernelGGL(attn_layers_kernel<CONTIG_TOK>, dim3((unsigned)grid), dim3(THREADS), 0, s, a, layers_dev, (int)n_layers);
+  else hipLaunchKernelGGL(attn_layers_kernel<CONTIG_T64>, dim3((unsigned)grid), dim3(THREADS), 0, s, a, layers_dev, (int)n_layers);
+  return check_launch(what);
+}
+}  // namespace
+
+extern "C" int64_t nkv_layers_workspace_bytes(int64_t hkv, int64_t hq, int64_t n_parts, int64_t n_layers) {
+  if (hkv <= 0 || hq <= 0 || hq % hkv || n_parts <= 0 || n_layers <= 0) return 0;
+  return n_layers * hkv * n_parts * part_floats(hq, hkv) * (int64_t)sizeof(float) + layers_sync_bytes(n_layers);
+}
+
+extern "C" int64_t nkv_layers_default_parts(int64_t hkv, int64_t capacity, int tok) {
+  set_error("");
+  int resident = 0;
+  if (hkv <= 0 || capacity <= 0 || layers_resident(tok != 0, &resident) != NKV_OK) return 0;
+  const int64_t parts = layers_parts(hkv, cdiv(capacity, GT), resident);
+  return parts >= 1 && hkv * (parts + 1) <= resident ? parts : 0;
+}
+
+extern "C" int nkv_decode_layers_t64(const nkv_layer_t64* layers_dev, const nkv_layer_t64* layers_host,
+                                     int64_t n_layers, int64_t kv_head_stride, const int64_t* pos_dev,
+                                     const int64_t* first_dev, int64_t* written_dev, int64_t* qlen_dev,
+                                     int64_t* pg_dev, int64_t hq, int64_t hkv, int64_t head_dim, int64_t capacity,
+                                     void* workspace, int64_t workspace_bytes, int64_t n_parts, void* stream) {
+  const char* what = "decode_layers_t64";
+  set_error("");
+  if (int rc = check_heads(hq, hkv, head_dim)) return rc;
+  if (capacity <= 0) return fail(NKV_ERR_INVALID, "capacity must be positive");
+  if (!pos_dev || !written_dev || !qlen_dev || !pg_dev) return fail(NKV_ERR_INVALID, "%s: null scalar pointer", what);
+  if (kv_head_stride % 8) return fail(NKV_ERR_UNSUPPORTED, "%s: kv_head_stride must keep 16-byte alignment", what);
+  for (int64_t l = 0; layers_host && l < n_layers; ++l) {
+    const nkv_layer_t64& e = layers_host[l];
+    const void* p[] = {e.q, e.k_new, e.v_new, e.kq, e.kmn, e.kst, e.vq, e.vmn, e.vst, e.tail_k, e.tail_v, e.out};
+    for (const void* x : p)
+      if (!x || !al16(x)) return fail(NKV_ERR_INVALID, "%s: layer %lld: null or unaligned pointer", what, (long long)l);
+    if (e.lse && (reinterpret_cast<uintptr_t>(e.lse) & 3u)) return fail(NKV_ERR_INVALID, "%s: layer %lld: unaligned lse", what, (long long)l);
+  }
+  AttnArgs a{};
+  a.kv_hs = kv_head_stride;
+  a.pos_dev = pos_dev; a.first_dev = first_dev;
+  a.written_out = written_dev; a.qlen_out = qlen_dev; a.pg_out = pg_dev;
+  a.capacity = capacity; a.ngroups_cap = cdiv(capacity, GT); a.tail_slots = GT;
+  a.hq = (int)hq; a.hkv = (int)hkv; a.gq = (int)(hq / hkv);
+  a.tail_mode = TAIL_FUSED;
+  a.inline_tail = 1;
+  a.sl2 = LOG2E / sqrtf((float)head_dim);
+  a.ws = static_cast<float*>(workspace);
+  return launch_layers(a, false, layers_dev, n_layers, n_parts, workspace_bytes, static_cast<hipStream_t>(stream), what);
+}
+
+extern "C" int nkv_decode_layers_tok(const nkv_layer_tok* layers_dev, const nkv_layer_tok* layers_host,
+                                     int64_t n_layers, int64_t kv_head_stride, const int64_t* pos_dev,
+                                     int64_t* written_dev, int64_t hq, int64_t hkv, int64_t head_dim,
+                                     int64_t capacity, void* workspace, int64_t workspace_bytes, int64_t n_parts,
+                                     void* stream) {
+  const char* what = "decode_layers_tok";
+  set_error("");
+  if (int rc = check_heads(hq, hkv, head_dim)) return rc;
+  if (capacity <= 0 || capacity % GT) return fail(NKV_ERR_INVALID, "%s: capacity %lld must be a positive multiple of 64", what, (long long)capacity);
+  if (!pos_dev || !written_dev) return fail(NKV_ERR_INVALID, "%s: null scalar pointer", what);
+  if (kv_head_stride % 8) return fail(NKV_ERR_UNSUPPORTED, "%s: kv_head_stride must keep 16-byte alignment", what);
+  for (int64_t l = 0; layers_host && l < n_layers; ++l) {
+    const nkv_layer_tok& e = layers_host[l];
+    const void* p[] = {e.q, e.k_new, e.v_new, e.kq, e.ksc, e.vq, e.vsc, e.out};
+    for (const void* x : p)
+      if (!x || !al16(x)) return fail(NKV_ERR_INVALID, "%s: layer %lld: null or unaligned pointer", what, (long long)l);
+    if (e.lse && (reinterpret_cast<uintptr_t>(e.lse) & 3u)) return fail(NKV_ERR_INVALID, "%s: layer %lld: unaligned lse", what, (long long)l);
+  }
+  AttnArgs a{};
+  a.kv_hs = kv_head_stride;
+  a.tok = 1;
+  a.pos_dev = pos_dev; a.written_out = written_dev;
+  a.capacity = capacity; a.ngroups_cap = capacity / GT; a.tail_slots = GT;
+  a.hq = (int)hq; a.hkv = (int)hkv; a.gq = (int)(hq / hkv);
+  a.tail_mode = TAIL_FUSED;
+  a.inline_tail = 1;
+  a.sl2 = LOG2E / sqrtf((float)head_dim);
+  a.ws = static_cast<float*>(workspace);
+  return launch_layers(a, true, layers_dev, n_layers, n_parts, workspace_bytes, static_cast<hipStream_t>(stream), what);
 }

@@ -145,3 +145,37 @@ def test_ctypes_argument_counts_match_header():
         n = 0 if params in ("", "void") else params.count(",") + 1
         assert len(_lib.SIGNATURES[name][1]) == n, name
     assert ctypes.sizeof(ctypes.c_void_p) == 8
+
+
+def test_chained_step_sizes_and_checks(lib):
+    """Workspace sizing of the chained decode step (one partial block per layer and the sync
+    words) and its argument checks, which return before any device query or launch."""
+    import numpy as np
+
+    from nova_amd import _lib
+
+    per_part = 8 * (4 * 128 + 8) * 4  # one partial of 4 query heads, per KV head
+    sync = lambda n: -(-((n + 2) * 4) // 256) * 256  # noqa: E731  (n layer counters, exit ticket, error word)
+    assert lib.nkv_layers_workspace_bytes(8, 32, 31, 36) == 36 * 31 * per_part + sync(36)
+    assert lib.nkv_layers_workspace_bytes(8, 32, 1, 1) == per_part + 256
+    assert lib.nkv_layers_workspace_bytes(8, 30, 31, 36) == 0 and lib.nkv_layers_workspace_bytes(8, 32, 0, 4) == 0
+    fake = 1 << 20
+    table = np.full((2, 13), fake, dtype=np.int64)
+    scalars = [fake] * 5
+    args = lambda hq, tab, n=2: ([fake, tab.ctypes.data, n, 128] + scalars  # noqa: E731
+                                 + [hq, 8, 128, 4096, fake, 1 << 24, 0, None])
+    assert lib.nkv_decode_layers_t64(*args(30, table)) == _lib.NKV_ERR_INVALID
+    assert b"divisible" in lib.nkv_last_error()
+    bad = table.copy()
+    bad[1, 4] = 0  # layer 1's kmn
+    assert lib.nkv_decode_layers_t64(*args(32, bad)) == _lib.NKV_ERR_INVALID
+    assert b"layer 1" in lib.nkv_last_error()
+    bad[1, 4] = fake + 8  # unaligned
+    assert lib.nkv_decode_layers_t64(*args(32, bad)) == _lib.NKV_ERR_INVALID
+    no_scalars = [fake, table.ctypes.data, 2, 128, fake, fake, None, fake, fake, 32, 8, 128, 4096, fake, 1 << 24, 0,
+                  None]
+    assert lib.nkv_decode_layers_t64(*no_scalars) == _lib.NKV_ERR_INVALID
+    tok = np.full((2, 9), fake, dtype=np.int64)
+    assert lib.nkv_decode_layers_tok(fake, tok.ctypes.data, 2, 128, fake, fake, 32, 8, 128, 100, fake, 1 << 24, 0,
+                                     None) == _lib.NKV_ERR_INVALID
+    assert b"multiple of 64" in lib.nkv_last_error()

@@ -1,0 +1,247 @@
+"""GPU parity of the chained decode step (``nkv_decode_layers_t64`` / ``_tok``): every layer of
+one token in one launch, each layer's inputs views of the previous layer's output.
+
+Each layer is checked against the oracle applied to the inputs that layer actually received
+(so float differences do not compound along the chain): the cache state bit for bit against
+``oracle.stream.StreamCache`` (int8t64) or ``oracle.kvquant.quantize_tok`` (per-token
+symmetric), every output within the streaming criterion of ``tests/test_kvattn_stream.py:39-57``
+(<= 4 fp16 ULP or <= 1e-3; per-token symmetric: the int8 criterion, 2 ULP or 1e-5). Against
+the per-layer launches (``nkv_decode_step_t64``) the state is bit-identical.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attn as oattn
+from oracle import kvquant as okq
+from oracle import stream as ostream
+from tests.helpers import D, H_KV, HQ, assert_ulp_or_abs, bench_outliers, npy, randn
+
+pytestmark = pytest.mark.gpu
+
+GQ = HQ // H_KV
+MAX_ULP, ABS_TOL = 4.0, 1e-3
+
+
+def _chain_views(outs: torch.Tensor, layers: int):
+    """Layer l reads layer l - 1's output (layer 0: the last layer's, from the step before):
+    q = the whole output, k = its q heads 0, 4, .., v = its q heads 1, 5, .."""
+    qs = [outs[(l - 1) % layers] for l in range(layers)]
+    ks = [q[:, 0::GQ] for q in qs]
+    vs = [q[:, 1::GQ] for q in qs]
+    return ks, vs, qs, [outs[l] for l in range(layers)]
+
+
+def _prefill_t64(cache, layers: int, n0: int, seed: int, oracle=None):
+    cache.begin_prefill(n0)
+    cache.set_prefill_pos(0)
+    if oracle is not None:
+        oracle.begin_prefill(n0)
+        oracle.set_prefill_pos(0)
+    for l in range(layers):
+        k = bench_outliers(randn((1, H_KV, n0, D), seed + 10 * l), seed + 10 * l + 1)
+        v = randn((1, H_KV, n0, D), seed + 10 * l + 2)
+        cache.update(k.cuda(), v.cuda(), l)
+        if oracle is not None:
+            oracle.update(npy(k)[0], npy(v)[0], l)
+    cache.finish_prefill(n0)
+    if oracle is not None:
+        oracle.finish_prefill(n0)
+
+
+def _assert_state(cache, oracle, layers: int):
+    for l in range(layers):
+        for nm in ("kq", "vq"):
+            np.testing.assert_array_equal(npy(getattr(cache, nm)[l])[0], getattr(oracle, nm)[l], err_msg=f"{nm}[{l}]")
+        for nm in ("kmn", "kst", "vmn", "vst", "tail_k", "tail_v"):
+            np.testing.assert_array_equal(npy(getattr(cache, nm)[l])[0].view(np.uint16),
+                                          getattr(oracle, nm)[l].view(np.uint16), err_msg=f"{nm}[{l}]")
+    assert int(cache._written.item()) == oracle.written
+    assert int(cache._qlen.item()) == oracle.qlen
+    assert int(cache._pg.item()) == oracle.pg
+
+
+@pytest.mark.parametrize("n_parts", [0, 3])
+def test_chain_t64_against_oracle(n_parts):
+    """3 chained layers, prefill 250, then 72 steps across the group boundaries at 256 and 320:
+    every layer's output against the oracle on its own inputs, state bit for bit."""
+    from nova_amd.chain import ChainedStep
+    from nova_amd.kvattn import KVInt8Cache
+
+    print(f"case chain t64 n_parts={n_parts}", flush=True)
+    L, n0, steps, cap = 3, 250, 72, 512
+    cache = KVInt8Cache(num_slots=L, num_kv_heads=H_KV, head_dim=D, max_len=cap, num_q_heads=HQ)
+    ref = ostream.StreamCache(L, H_KV, D, cap, HQ)
+    _prefill_t64(cache, L, n0, seed=40, oracle=ref)
+    outs = randn((L, 1, HQ, 1, D), 41, scale=0.5).cuda()
+    chain = ChainedStep(cache, *_chain_views(outs, L), n_parts=n_parts)
+    for s in range(steps):
+        prev = npy(outs)  # layer 0's input is outs[L - 1] before the step
+        chain()
+        got = npy(outs)
+        for l in range(L):
+            q = (prev if l == 0 else got)[(l - 1) % L][0, :, 0]
+            ref.update(q[0::GQ, None], q[1::GQ, None], l)
+            want = ref.attend_exact(q, l)
+            assert_ulp_or_abs(got[l][0, :, 0], want, MAX_ULP, ABS_TOL, f"step {s} layer {l}")
+        cache.pos.add_(1)
+        ref.pos += 1
+    _assert_state(cache, ref, L)
+    assert not chain.gave_up()
+    assert int(chain.workspace.abs().sum().item()) == 0, "the workspace is left zero-filled"
+
+
+def test_chain_equals_per_layer_launches_at_32k():
+    """2 layers at 32768 tokens with the default grid (one workgroup per CU), 3 steps across
+    the 512th group boundary, independent inputs: cache state bit-identical to the per-layer
+    fused launches, outputs within the streaming criterion of them and of the oracle."""
+    from nova_amd.chain import ChainedStep
+    from nova_amd.kvattn import KVInt8Cache
+
+    print("case chain 32k", flush=True)
+    L, n0, cap = 2, 32765, 32768 + 128
+    a = KVInt8Cache(num_slots=L, num_kv_heads=H_KV, head_dim=D, max_len=cap, num_q_heads=HQ)
+    b = KVInt8Cache(num_slots=L, num_kv_heads=H_KV, head_dim=D, max_len=cap, num_q_heads=HQ)
+    _prefill_t64(a, L, n0, seed=50)
+    _prefill_t64(b, L, n0, seed=50)
+    dev = torch.device("cuda")
+    qs = [randn((1, HQ, 1, D), 51 + l, 0.5).to(dev) for l in range(L)]
+    ks = [randn((1, H_KV, 1, D), 53 + l).to(dev) for l in range(L)]
+    vs = [randn((1, H_KV, 1, D), 55 + l).to(dev) for l in range(L)]
+    oa = [torch.zeros(1, HQ, 1, D, dtype=torch.float16, device=dev) for _ in range(L)]
+    ob = [torch.zeros_like(o) for o in oa]
+    chain = ChainedStep(a, ks, vs, qs, oa)
+    assert chain.n_parts >= 16
+    for step in range(3):
+        chain()
+        for l in range(L):
+            b.update_attend(ks[l], vs[l], qs[l], l, out=ob[l])
+        for l in range(L):
+            assert_ulp_or_abs(npy(oa[l])[0, :, 0], npy(ob[l])[0, :, 0].astype(np.float64), MAX_ULP, ABS_TOL,
+                              f"step {step} layer {l}")
+        a.pos.add_(1)
+        b.pos.add_(1)
+        for nm in ("_codes", "_rulers", "_ring", "_scalars"):
+            assert torch.equal(getattr(a, nm), getattr(b, nm)), f"{nm} after step {step}"
+    # the last step against the oracle: layer 1's state, dequantized, one softmax
+    ref = ostream.StreamCache(1, H_KV, D, cap, HQ)
+    ref.kq[0], ref.vq[0] = npy(a.kq[1])[0], npy(a.vq[1])[0]
+    for nm in ("kmn", "kst", "vmn", "vst", "tail_k", "tail_v"):
+        getattr(ref, nm)[0] = npy(getattr(a, nm)[1])[0]
+    ref.pos = int(a.pos.item()) - 1
+    ref._sync_scalars()
+    want = ref.attend_exact(npy(qs[1])[0, :, 0], 0)
+    assert_ulp_or_abs(npy(oa[1])[0, :, 0], want, MAX_ULP, ABS_TOL, "32k vs oracle")
+    assert not chain.gave_up()
+
+
+def test_chain_graph_replay_equals_eager():
+    """The chained step captured with ``pos += 1`` in a graph, replayed, equals eager calls bit
+    for bit (outputs and state), with eager work between the replays."""
+    from nova_amd.chain import ChainedStep
+    from nova_amd.kvattn import KVInt8Cache
+
+    print("case chain graph", flush=True)
+    L, n0, cap = 4, 1000, 1280
+    caches, outs, chains = [], [], []
+    for _ in range(2):
+        c = KVInt8Cache(num_slots=L, num_kv_heads=H_KV, head_dim=D, max_len=cap, num_q_heads=HQ)
+        _prefill_t64(c, L, n0, seed=60)
+        o = randn((L, 1, HQ, 1, D), 61, scale=0.5).cuda()
+        caches.append(c)
+        outs.append(o)
+        chains.append(ChainedStep(c, *_chain_views(o, L)))
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g):
+            chains[1]()
+            caches[1].pos.add_(1)
+    torch.cuda.current_stream().wait_stream(side)
+    for step in range(30):
+        chains[0]()
+        caches[0].pos.add_(1)
+        g.replay()
+        _ = torch.randn(1000, device="cuda").sum()  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], outs[1]), f"outputs differ at step {step}"
+    for nm in ("_codes", "_rulers", "_ring", "_scalars"):
+        assert torch.equal(getattr(caches[0], nm), getattr(caches[1], nm)), nm
+
+
+def test_chain_tok_against_oracle():
+    """Per-token symmetric caches, 2 chained layers, prefill 190 then 70 steps: codes and scales
+    of every token bit for bit against the quantizer oracle, every output against the oracle."""
+    from nova_amd.chain import ChainedStep
+    from nova_amd.kvtok import KVInt8TokCache
+
+    print("case chain tok", flush=True)
+    L, n0, steps, cap = 2, 190, 70, 320
+    cache = KVInt8TokCache(L, H_KV, D, cap, HQ)
+    cache.begin_prefill(n0)
+    cache.set_prefill_pos(0)
+    ks_all, vs_all = [], []
+    for l in range(L):
+        k = bench_outliers(randn((1, H_KV, n0, D), 70 + l), 72 + l)
+        v = randn((1, H_KV, n0, D), 74 + l)
+        cache.update(k.cuda(), v.cuda(), l)
+        ks_all.append([npy(k)[0]])
+        vs_all.append([npy(v)[0]])
+    cache.finish_prefill(n0)
+    outs = randn((L, 1, HQ, 1, D), 76, scale=0.5).cuda()
+    chain = ChainedStep(cache, *_chain_views(outs, L))
+    for s in range(steps):
+        prev = npy(outs)
+        chain()
+        got = npy(outs)
+        p = n0 + s
+        for l in range(L):
+            q = (prev if l == 0 else got)[(l - 1) % L][0, :, 0]
+            ks_all[l].append(q[0::GQ, None])
+            vs_all[l].append(q[1::GQ, None])
+            kq, ksc = okq.quantize_tok(np.concatenate(ks_all[l], axis=1))
+            vq, vsc = okq.quantize_tok(np.concatenate(vs_all[l], axis=1))
+            want, _ = oattn.tok_attn_decode(q, kq, ksc, vq, vsc, p + 1)
+            assert_ulp_or_abs(got[l][0, :, 0], want, 2.0, 1e-5, f"step {s} layer {l}")
+        cache.pos.add_(1)
+    n = n0 + steps
+    for l in range(L):
+        kq, ksc = okq.quantize_tok(np.concatenate(ks_all[l], axis=1))
+        vq, vsc = okq.quantize_tok(np.concatenate(vs_all[l], axis=1))
+        np.testing.assert_array_equal(npy(cache.kq[l])[0, :, :n], kq)
+        np.testing.assert_array_equal(npy(cache.vq[l])[0, :, :n], vq)
+        np.testing.assert_array_equal(npy(cache.ksc[l])[0, :, :n].view(np.uint16), ksc.view(np.uint16))
+        np.testing.assert_array_equal(npy(cache.vsc[l])[0, :, :n].view(np.uint16), vsc.view(np.uint16))
+    assert int(cache._written.item()) == n
+    assert not chain.gave_up()
+
+
+def test_chain_argument_checks():
+    """Inputs the launch cannot take are refused before anything runs."""
+    from nova_amd.chain import ChainedStep
+    from nova_amd.kvattn import KVInt8Cache
+
+    L = 2
+    cache = KVInt8Cache(num_slots=L, num_kv_heads=H_KV, head_dim=D, max_len=256, num_q_heads=HQ)
+    cache.begin_prefill(100)
+    cache.set_prefill_pos(0)
+    for l in range(L):
+        cache.update(randn((1, H_KV, 100, D), l).cuda(), randn((1, H_KV, 100, D), l + 5).cuda(), l)
+    with pytest.raises(RuntimeError):
+        ChainedStep(cache, [], [], [], [])  # still prefilling
+    cache.finish_prefill(100)
+    outs = torch.zeros(L, 1, HQ, 1, D, dtype=torch.float16, device="cuda")
+    ks, vs, qs, os_ = _chain_views(outs, L)
+    with pytest.raises(ValueError):  # one head stride for every key and value
+        ChainedStep(cache, [ks[0], ks[1].contiguous()], vs, qs, os_)
+    with pytest.raises(ValueError):  # more layers than the cache holds
+        ChainedStep(cache, ks * 2, vs * 2, qs * 2, os_ * 2)
+    with pytest.raises(ValueError):
+        ChainedStep(cache, ks, vs, qs, [o.float() for o in os_])
+    with pytest.raises(NotImplementedError):  # more workgroups than the device holds at once
+        ChainedStep(cache, ks, vs, qs, os_, n_parts=100)()
