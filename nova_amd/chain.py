@@ -118,7 +118,24 @@ class ChainedStep:
         """Launch the step on the current stream (capturable: no allocation, no host sync)."""
         _lib.call("nkv_decode_layers_tok" if self.tok else "nkv_decode_layers_t64", *self._args())
 
+    def _sync_words(self) -> list:
+        """The sync words at the workspace's end, from the last: the layer counters, the exit
+        ticket, the error word, the launch counter (synchronizes)."""
+        end = (self.ws_bytes & ~3) // 4
+        n = self.n_layers
+        return self.workspace[end - n - 3:end].flip(0).tolist()
+
     def gave_up(self) -> bool:
         """Whether a launch's wait ever gave up (its outputs are then NaN). Synchronizes."""
-        word = ((self.ws_bytes & ~3) - 4 * (self.n_layers + 2)) // 4
-        return bool(int(self.workspace[word].item()) != 0)
+        return self._sync_words()[self.n_layers + 1] != 0
+
+    def idle_state(self) -> dict:
+        """Between launches: whether the partial blocks and the counters are back at zero, and the
+        number of launches so far (the forwarding tags' counter). Synchronizes."""
+        c = self.cache
+        part_words = self.n_layers * c.num_kv_heads * self.n_parts * (c.num_q_heads // c.num_kv_heads * 128 +
+                                                                      ((2 * (c.num_q_heads // c.num_kv_heads) + 3) & ~3))
+        w = self._sync_words()
+        n = self.n_layers
+        return {"partials_zero": bool(int(self.workspace[:part_words].abs().sum().item()) == 0),
+                "counters_zero": all(x == 0 for x in w[:n + 1]), "error": w[n + 1], "launches": w[n + 2]}

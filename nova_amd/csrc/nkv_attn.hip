@@ -143,6 +143,10 @@ struct AttnArgs {
   // last bytes; the counters start at zero and every launch leaves them at zero.
   int inline_tail;
   int* tail_ctr_end;
+  // the chained step: this layer's output also as tagged words (two fp16 values in the low 32
+  // bits, `ftag` in the high 32) for the next layer's inputs that are views of it; null otherwise
+  uint64_t* fwd_out;
+  uint32_t ftag;
 };
 
 // XOR key of the 16-byte chunk positions of LDS row `row` (a token within its group).
@@ -209,10 +213,20 @@ __device__ __forceinline__ half8_t dq8_splat(uint32_t w0, uint32_t w1, half2_t s
   return half8_t{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
 }
 
+// The thread index for code that runs once per layer (the tails, the chained step's merger):
+// read through an opaque move, so that values derived from it are recomputed where they are used
+// rather than hoisted out of the chained kernel's layer loop and kept live across it (which
+// exhausts the register file there).
+__device__ __forceinline__ int tail_tid() {
+  int t;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)__builtin_amdgcn_workitem_id_x()));
+  return t;
+}
+
 // Q as the B operand of v_mfma_f32_16x16x32_f16: lane (c, g) holds head c's dims
 // 16g + 64hh + 8e + [0..7] for k-step 2hh + e (zeros for c >= gq).
 __device__ __forceinline__ void load_q(const uint16_t* qh, int gq, half8_t (&qb)[4]) {
-  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  const int lane = tail_tid() & 63, c = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     uint4 w = {0, 0, 0, 0};
@@ -387,7 +401,7 @@ __device__ __forceinline__ void issue_q(const uint16_t* qh, int gq, uint32_t dst
 
 // The B operand of load_q, from Q rows in LDS.
 __device__ __forceinline__ void load_q_lds(const uint16_t* q_lds, int gq, half8_t (&qb)[4]) {
-  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  const int lane = tail_tid() & 63, c = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     uint4 w = {0, 0, 0, 0};
@@ -668,7 +682,7 @@ __device__ __forceinline__ void attend_block_tok(const AttnArgs& a, WaveState& s
 // head c); returns P as the A operand of v_mfma_f32_16x16x16_f16 (hi/lo halves).
 __device__ __forceinline__ void softmax_step4(WaveState& st, const float (&s)[4], float sl2, half4_t& phi,
                                               half4_t& plo, int gq) {
-  const int lane = threadIdx.x & 63, g = lane >> 4;
+  const int lane = tail_tid() & 63, g = lane >> 4;
   const float mloc = max4rows(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]))) * sl2;
   const float m_new = fmaxf(st.m, mloc);
   const float m_use = m_new == NEG_INF ? 0.0f : m_new;
@@ -702,7 +716,7 @@ __device__ __forceinline__ void softmax_step4(WaveState& st, const float (&s)[4]
 // S^T output layout of the block.
 __device__ __forceinline__ void attend_ring16(const AttnArgs& a, WaveState& st, const half8_t (&qb)[4],
                                               const uint8_t* rk, const uint8_t* rv, int blk, uint64_t valid_bits) {
-  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  const int lane = tail_tid() & 63, c = lane & 15, g = lane >> 4;
   float4_t S = {0.f, 0.f, 0.f, 0.f};
   const int row = 16 * blk + c;
 #pragma unroll
@@ -802,7 +816,7 @@ __device__ __forceinline__ void write_scalars(const AttnArgs& a, int64_t pos) {
 // Slot validity of the ring: slot i holds p = u - ((u - i) mod 64), valid iff qlen <= p <= u,
 // p >= first (u = written - 1). Lane i decides slot i; the wave's ballot is the mask.
 __device__ __forceinline__ uint64_t ring_bits(int64_t written, int64_t qlen, int64_t first) {
-  const int i = threadIdx.x & 63;
+  const int i = tail_tid() & 63;
   const int64_t u = written - 1;
   const int64_t p = u - ((u - i) & (GT - 1));
   return __builtin_amdgcn_ballot_w64(p >= qlen && p <= u && p >= first);
@@ -1008,7 +1022,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 // Write one wave's online-softmax state as a partial at `dst` (LDS or memory): lane (c, g)
 // holds m, l of head c (replicated over g) and acc of heads 4g + i, dims 16cb + c.
 __device__ __forceinline__ void store_wave_partial(const WaveState& st, int gq, float* dst) {
-  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  const int lane = tail_tid() & 63, c = lane & 15, g = lane >> 4;
   if (g == 0 && c < gq) { dst[gq * D + c] = st.m; dst[gq * D + gq + c] = st.l; }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -1063,6 +1077,9 @@ struct TailSmem {
   float pre_m[16], pre_l[16];                // per head: m_p, l_p
   float rq_ext[2][2 * D];                    // local requantization: per channel min / max of two half rings
   int lost[TB_WAVES];                        // a merging wave gave up waiting for a partial word
+  uint32_t fwd[(16 + 2) * D / 2];            // the chained step: forwarded q, k_new, v_new of the head (fp16 pairs)
+  uint8_t xpose[RING_PARTS * GT * 64];       // the chained step's append: each ring wave's 64 x 64 codes
+  int ring_staged;                           // ring waves that have staged their slots (the chained step's append)
 };
 constexpr int MERGER_MAX_PARTS = 64;         // prefix parts per head of a fused launch
 constexpr int MERGER_MAX_HEADS = 64;         // KV heads of a fused launch: its part-0 workgroups wait for the others
@@ -1156,7 +1173,7 @@ __device__ __forceinline__ uint64_t pub_repoll2(const float* p, uint64_t w, int&
 template <bool STORE>
 __device__ __forceinline__ void requant_ring_lds(uint8_t* ring_lds, float (&ext)[2][2 * D], bool deq,
                                                  const AttnArgs* a = nullptr, int h = 0, int64_t pos = 0) {
-  const int t = threadIdx.x, ch = t & (2 * D - 1), half = t >> 8;
+  const int t = tail_tid(), ch = t & (2 * D - 1), half = t >> 8;
   uint8_t* base = ring_lds + (ch >> 7) * RING_BYTES;
   const int c = ch & (D - 1);
   float v[32];
@@ -1211,6 +1228,43 @@ __device__ __forceinline__ void requant_ring_lds(uint8_t* ring_lds, float (&ext)
   }
 }
 
+// The append of the token at `pos` from the ring held in LDS (the 64 slots, the new token in its
+// slot; ring_chunk_pos layout) by the 256 threads of waves 0..3: thread t rules channel t & 127 of K
+// (t < 128) or V over the 64 slots, exactly as append_unit rules it, and stores its two ruler
+// values; the wave's 64 x 64 codes go through `xpose` (4 KiB of LDS per wave) so that lane r
+// stores row r's 64 codes with four 16-byte stores (rows below the capacity). No workgroup
+// barrier: the caller's waves 0..3 have all staged the ring before.
+__device__ __forceinline__ void append_ring_channels(const AttnArgs& a, int h, int64_t pos, const uint8_t* ring_lds,
+                                                     uint8_t* xpose) {
+  const int t = tail_tid(), wave = t >> 6, lane = t & 63, which = t >> 7, c = t & (D - 1);
+  const uint8_t* base = ring_lds + which * RING_BYTES;
+  float v[GT];
+  float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+#pragma unroll
+  for (int r = 0; r < GT; ++r) {
+    v[r] = h2f(*reinterpret_cast<const uint16_t*>(base + r * (2 * D) + (ring_chunk_pos(r, c >> 3) << 4) + 2 * (c & 7)));
+    mn = fminf(mn, v[r]);
+    mx = fmaxf(mx, v[r]);
+  }
+  const float step = ruler_step(mn, mx), inv = ruler_inv(step);
+  const int64_t gcur = pos / GT, ro = ((int64_t)h * a.ngroups_cap + gcur) * D + c;
+  (which ? a.vmn : a.kmn)[ro] = f2h(mn);
+  (which ? a.vst : a.kst)[ro] = f2h(step);
+  // codes: column `lane` of the wave's [64 rows][64 channels] block, then row `lane` of it
+  uint8_t* xw = xpose + wave * (GT * 64);
+#pragma unroll
+  for (int r = 0; r < GT; ++r) xw[r * 64 + lane] = (uint8_t)ruler_code_rcp(v[r], mn, step, inv);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // (one wave: its LDS accesses run in order)
+  const int rows = (int)min<int64_t>(GT, a.capacity - gcur * GT);
+  if (lane < rows) {
+    uint4* dst = reinterpret_cast<uint4*>((which ? a.vq : a.kq) + ((int64_t)h * a.capacity + gcur * GT + lane) * D +
+                                          64 * (wave & 1));
+    const uint4* src = reinterpret_cast<const uint4*>(xw + lane * 64);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) dst[k] = src[k];
+  }
+}
+
 // The tail of one decode step for KV head h (of sequence b when paged), by the 8 waves of the
 // calling workgroup. The prefix partials merge into (m_p, l_p, acc_p): m_p = max_s m_s,
 // w_s = 2^(m_s - m_p), l_p = sum_s w_s l_s, acc_p = sum_s w_s acc_s (waves 4..7, one head
@@ -1244,7 +1298,7 @@ struct TailLoads {
 
 template <bool PAGED>
 __device__ __forceinline__ void tail_load_rows(const AttnArgs& a, int h, int b, int64_t pos, bool pos_ok, TailLoads& t) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, cl = lane & 15, rl = lane >> 4;
+  const int wave = tail_tid() >> 6, lane = tail_tid() & 63, cl = lane & 15, rl = lane >> 4;
   const bool fused = PAGED || a.tail_mode == TAIL_FUSED;
   const bool ring = (PAGED || a.tail_mode != TAIL_NONE) && (!fused || pos_ok);
   const bool tok1 = ring && a.tok;
@@ -1285,7 +1339,7 @@ template <bool PAGED>
 __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailSmem& sm, int run, int64_t pos,
                                           bool pos_ok, int64_t U, const TailLoads* pre = nullptr,
                                           const half8_t (*pre_q)[4] = nullptr, int flags = 0) {
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = tail_tid(), wave = tid >> 6, lane = tid & 63;
   const bool poll = run != TAIL_KERNEL;  // partials written in this launch: poll their words
   const int gq = a.gq, pw = part_stride(gq), cols = gq * D;
   const int P = PAGED ? min(a.seq_parts[2 * b + 1], WTS) : a.n_parts;
@@ -1379,9 +1433,15 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
       }
     }
   }
+  // the chained step's append of a token that does not complete its group: the ring waves rule it
+  // from the staged ring after their attention, while the merging waves poll (nothing in the launch
+  // reads that group); they meet through ring_staged (set to zero by the caller before the tail)
+  const bool ring_append = appends && !completes && !tok1;
+  if (ring_append && wave < RING_PARTS) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (lane == 0) __hip_atomic_fetch_add(&sm.ring_staged, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
   if (appends && completes) {
-    // (a token that does not complete its group is requantized into it by the caller, after the
-    // output: nothing in the launch reads that group, and the merging waves poll meanwhile)
     __syncthreads();
     requant_ring_lds<true>(sm.ring_lds, sm.rq_ext, true, &a, h, pos);
     __syncthreads();
@@ -1405,6 +1465,11 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     state_init(st);
     attend_ring16(a, st, qb, ring_k, ring_v, wave, bits);
     store_wave_partial(st, gq, sm.ring_part[wave]);
+    if (ring_append) {
+      while (__hip_atomic_load(&sm.ring_staged, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < RING_PARTS)
+        __builtin_amdgcn_s_sleep(1);
+      append_ring_channels(a, h, pos, sm.ring_lds, sm.xpose);
+    }
   } else if (merging) {
     // (this code runs once per launch on a cold instruction cache, at ~30 ns per 64-byte line:
     // the common shape, one head per merging wave and P <= 64, takes a short straight path)
@@ -1585,7 +1650,14 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     const int d = col % D;
     // acc and l carry the same 2^15 scale; a merger that gave up writes NaN
     const float o = failed ? __builtin_nanf("") : (l > 0.0f ? acc / l : 0.0f);
-    a.out[(int64_t)qh * D + d] = f2h(o);
+    const uint16_t o16 = f2h(o);
+    a.out[(int64_t)qh * D + d] = o16;
+    if (a.fwd_out) {  // (columns come in pairs of neighbouring lanes: d even in the even lane)
+      const uint32_t pair = (uint32_t)__shfl_xor((int)o16, 1, 64);
+      if ((d & 1) == 0)
+        __hip_atomic_store(a.fwd_out + ((int64_t)qh * D + d) / 2, ((uint64_t)a.ftag << 32) | o16 | (pair << 16),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     if (a.lse && d == 0) a.lse[qh] = failed ? __builtin_nanf("") : (l > 0.0f ? (M + __log2f(l) - P_SCALE_LOG2) * LN2 : NEG_INF);
   }
   // ---- every word of the head's partials was consumed before the barrier above: the whole
@@ -1843,14 +1915,16 @@ constexpr int IN_WAVE = WAVES - 1;                 // a streaming workgroup's in
 constexpr uint64_t LAYER_WAIT_TICKS = 20000000ull;  // 0.2 s of the 100 MHz real-time counter per wait
 
 // The sync words of a chained launch at the workspace's end (tail_ctr_end): done[l] at
-// end[-1 - l], the exit ticket at end[-1 - n_layers], the error word at end[-2 - n_layers].
+// end[-1 - l], the exit ticket at end[-1 - n_layers], the error word at end[-2 - n_layers], the
+// launch counter (the forwarding tags) at end[-3 - n_layers].
 __device__ __forceinline__ int* layer_done(const AttnArgs& a, int l) { return a.tail_ctr_end - 1 - l; }
 
 // Layer l's arguments: the cache and step pointers of its table entry (nkv_layer_t64, or
 // nkv_layer_tok for the per-token symmetric format), and its own partial block.
 template <bool TOK>
-__device__ __forceinline__ AttnArgs layer_args(const AttnArgs& a, const void* layers, int l) {
+__device__ __forceinline__ AttnArgs layer_args(const AttnArgs& a, const void* layers, int l, uint32_t ftag) {
   AttnArgs la = a;
+  la.ftag = ftag;
   if constexpr (TOK) {
     const nkv_layer_tok& e = static_cast<const nkv_layer_tok*>(layers)[l];
     la.q = e.q;
@@ -1879,7 +1953,62 @@ __device__ __forceinline__ AttnArgs layer_args(const AttnArgs& a, const void* la
     la.lse = e.lse;
   }
   la.ws = a.ws + (int64_t)l * a.hkv * a.n_parts * part_stride(a.gq);
+  la.fwd_out = a.fwd_out + (int64_t)l * a.hq * D / 2;  // (read by layer l + 1 only)
   return la;
+}
+
+// The previous layer's output pointer (the chained step's forwarding source).
+template <bool TOK>
+__device__ __forceinline__ const uint16_t* layer_out(const void* layers, int l) {
+  if constexpr (TOK) return static_cast<const nkv_layer_tok*>(layers)[l].out;
+  else return static_cast<const nkv_layer_t64*>(layers)[l].out;
+}
+
+// Whether [p, p + n) (fp16 elements) lies inside [base, base + len).
+__device__ __forceinline__ bool within(const uint16_t* p, int64_t n, const uint16_t* base, int64_t len) {
+  return p >= base && p + n <= base + len;
+}
+
+// Forwarded inputs: layer l's q, and the merger's k_new / v_new rows of head h, when they are views
+// of layer l - 1's output, are read from that output's tagged words (AttnArgs::fwd_out of layer
+// l - 1): lane i takes words i + 64 j, reloading those whose tag is not yet `tag` (relaxed
+// agent-scope loads: per-location coherence hands over each word once written, no counter or
+// fence), and stores their fp16 pairs to LDS at `dst` (q rows, then k_new, then v_new).
+// gq <= FWD_MAX_GQ. false when the wait gave up (after LAYER_WAIT_TICKS, or at once with `lost`).
+constexpr int FWD_MAX_GQ = 4;
+__device__ __forceinline__ bool fwd_fetch(const uint64_t* q, const uint64_t* k, const uint64_t* v, int gq,
+                                          uint32_t tag, uint32_t* dst, bool lost) {
+  const int lane = tail_tid() & 63;
+  uint64_t w[FWD_MAX_GQ + 2];
+#pragma unroll
+  for (int j = 0; j < FWD_MAX_GQ + 2; ++j) w[j] = 0;  // (tag 0 is never current)
+  const bool kv = k != nullptr;
+  bool ok = !lost;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  while (ok) {
+#pragma unroll
+    for (int j = 0; j < FWD_MAX_GQ; ++j)
+      if (j < gq && (uint32_t)(w[j] >> 32) != tag) w[j] = __hip_atomic_load(q + lane + 64 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (kv && (uint32_t)(w[FWD_MAX_GQ] >> 32) != tag)
+      w[FWD_MAX_GQ] = __hip_atomic_load(k + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (kv && (uint32_t)(w[FWD_MAX_GQ + 1] >> 32) != tag)
+      w[FWD_MAX_GQ + 1] = __hip_atomic_load(v + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool miss = false;
+#pragma unroll
+    for (int j = 0; j < FWD_MAX_GQ; ++j) miss |= j < gq && (uint32_t)(w[j] >> 32) != tag;
+    miss |= kv && ((uint32_t)(w[FWD_MAX_GQ] >> 32) != tag || (uint32_t)(w[FWD_MAX_GQ + 1] >> 32) != tag);
+    if (!__builtin_amdgcn_ballot_w64(miss)) break;
+    if (__builtin_amdgcn_s_memrealtime() - t0 > LAYER_WAIT_TICKS) ok = false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+#pragma unroll
+  for (int j = 0; j < FWD_MAX_GQ; ++j)
+    if (j < gq) dst[lane + 64 * j] = (uint32_t)w[j];
+  if (kv) {
+    dst[gq * 64 + lane] = (uint32_t)w[FWD_MAX_GQ];
+    dst[gq * 64 + 64 + lane] = (uint32_t)w[FWD_MAX_GQ + 1];
+  }
+  return ok;
 }
 
 // Wait (lane 0 of the calling wave) until layer l's counter reaches `target`, then an
@@ -1887,7 +2016,7 @@ __device__ __forceinline__ AttnArgs layer_args(const AttnArgs& a, const void* la
 // LAYER_WAIT_TICKS, or at once when an earlier wait of the workgroup gave up: `lost`).
 __device__ __forceinline__ bool wait_layer(const AttnArgs& a, int l, int target, bool lost) {
   bool ok = !lost;
-  if ((threadIdx.x & 63) == 0 && ok) {
+  if ((tail_tid() & 63) == 0 && ok) {
     const int* ctr = layer_done(a, l);
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
@@ -1902,74 +2031,55 @@ __device__ __forceinline__ bool wait_layer(const AttnArgs& a, int l, int target,
   return __builtin_amdgcn_readfirstlane(ok ? 1 : 0) != 0;
 }
 
-// The append of the token at `pos` from the ring held in LDS (the 64 slots, the new token in its
-// slot; ring_chunk_pos layout) by the 256 threads of waves 0..3: thread t rules channel t & 127 of K
-// (t < 128) or V over the 64 slots, exactly as append_unit rules it, and stores its two ruler
-// values; the wave's 64 x 64 codes go through `xpose` (4 KiB of LDS per wave) so that lane r
-// stores row r's 64 codes with four 16-byte stores (rows below the capacity). No workgroup
-// barrier: the caller's waves 0..3 staged the ring and a workgroup barrier followed.
-__device__ __forceinline__ void append_ring_channels(const AttnArgs& a, int h, int64_t pos, const uint8_t* ring_lds,
-                                                     uint8_t* xpose) {
-  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, which = t >> 7, c = t & (D - 1);
-  const uint8_t* base = ring_lds + which * RING_BYTES;
-  float v[GT];
-  float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
-#pragma unroll
-  for (int r = 0; r < GT; ++r) {
-    v[r] = h2f(*reinterpret_cast<const uint16_t*>(base + r * (2 * D) + (ring_chunk_pos(r, c >> 3) << 4) + 2 * (c & 7)));
-    mn = fminf(mn, v[r]);
-    mx = fmaxf(mx, v[r]);
-  }
-  const float step = ruler_step(mn, mx), inv = ruler_inv(step);
-  const int64_t gcur = pos / GT, ro = ((int64_t)h * a.ngroups_cap + gcur) * D + c;
-  (which ? a.vmn : a.kmn)[ro] = f2h(mn);
-  (which ? a.vst : a.kst)[ro] = f2h(step);
-  // codes: column `lane` of the wave's [64 rows][64 channels] block, then row `lane` of it
-  uint8_t* xw = xpose + wave * (GT * 64);
-#pragma unroll
-  for (int r = 0; r < GT; ++r) xw[r * 64 + lane] = (uint8_t)ruler_code_rcp(v[r], mn, step, inv);
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // (one wave: its LDS accesses run in order)
-  const int rows = (int)min<int64_t>(GT, a.capacity - gcur * GT);
-  if (lane < rows) {
-    uint4* dst = reinterpret_cast<uint4*>((which ? a.vq : a.kq) + ((int64_t)h * a.capacity + gcur * GT + lane) * D +
-                                          64 * (wave & 1));
-    const uint4* src = reinterpret_cast<const uint4*>(xw + lane * 64);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) dst[k] = src[k];
-  }
-}
-
 // One layer of head h's merger (workgroup (h, 0) of the chained kernel): wait for layer l - 1,
 // append + ring + merge of layer l into out / lse, count itself on layer l's counter. Returns
-// whether its wait gave up. (The consumed partial block is zeroed at the end of the launch.) (Not inlined: inside the layer loop
-// the compiler would keep the tail's loop-invariant addresses live across the streaming code.)
+// whether its wait gave up. (The consumed partial block is zeroed at the end of the launch.)
 template <bool TOK>
-__device__ __noinline__ bool merger_layer(const AttnArgs& la, int l, int h, uint8_t* lds_raw, int64_t pos, bool pos_ok,
-                                          int64_t U, bool lost) {
+__device__ __forceinline__ bool merger_layer(const AttnArgs& args, const void* layers, int l, int h, uint8_t* lds_raw,
+                                          int64_t pos, bool pos_ok, int64_t U, bool lost) {
   __shared__ int lost_sh;
-  const int tid = threadIdx.x, wave = tid >> 6;
-  const int P = la.n_parts, pw = part_stride(la.gq);
+  const int tid = tail_tid(), wave = tid >> 6;
+  AttnArgs la = args;
+  const int P = la.n_parts, pw = part_stride(la.gq), gq = la.gq;
+  TailSmem& sm = *reinterpret_cast<TailSmem*>(lds_raw);
+  // q, k_new and v_new all views of layer l - 1's output: forwarded, no counter wait
+  bool fwd = false;
+  const uint16_t* prev = nullptr;
+  if (l > 0 && gq <= FWD_MAX_GQ) {
+    prev = layer_out<TOK>(layers, l - 1);
+    const int64_t n = (int64_t)la.hq * D, span = (int64_t)(la.hkv - 1) * la.kv_hs + D;
+    fwd = la.q == prev && within(la.k_new, span, prev, n) && within(la.v_new, span, prev, n);
+  }
+  if (tid == 0) sm.ring_staged = 0;
   if (wave == IN_WAVE) {
-    const bool ok = l == 0 || wait_layer(la, l - 1, la.hkv, lost);
+    bool ok = true;
+    if (fwd) {
+      const uint64_t* src = la.fwd_out - (int64_t)la.hq * D / 2;  // layer l - 1's tagged words
+      ok = fwd_fetch(src + (int64_t)h * gq * D / 2, src + ((la.k_new - prev) + (int64_t)h * la.kv_hs) / 2,
+                     src + ((la.v_new - prev) + (int64_t)h * la.kv_hs) / 2, gq, la.ftag, sm.fwd, lost);
+    } else if (l > 0) {
+      ok = wait_layer(la, l - 1, la.hkv, lost);
+    }
     if (tid == IN_WAVE * 64) lost_sh = ok ? 0 : 1;
   }
   __syncthreads();
   const bool gave_up = lost_sh != 0;
   if (l == 0 && blockIdx.x == 0 && tid == 0 && pos_ok) write_scalars(la, pos);
-  TailSmem& sm = *reinterpret_cast<TailSmem*>(lds_raw);
-  tail_body<false>(la, h, 0, sm, TAIL_MERGER, pos, pos_ok, U, nullptr, nullptr,
+  half8_t qb[4];
+  if (fwd) {  // the tail reads them from LDS
+    const uint16_t* f = reinterpret_cast<const uint16_t*>(sm.fwd);
+    load_q_lds(f, gq, qb);
+    la.k_new = f + gq * D;
+    la.v_new = f + gq * D + D;
+    la.kv_hs = 0;
+  }
+  tail_body<false>(la, h, 0, sm, TAIL_MERGER, pos, pos_ok, U, nullptr, fwd ? &qb : nullptr,
                    TB_APPEND | TB_KEEP_BLOCK | (lost || gave_up ? TB_POISON : 0));
   // every wave's stores (out, lse, the ring slot) complete before the workgroup meets; then one
   // release at agent scope publishes them all with the count
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) __hip_atomic_fetch_add(layer_done(la, l), 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-  // Waves 0..3 finish the layer after the count; wave 7, which waits for the next layer's counter,
-  // then has no stores of its own in flight (a wait for its polls would wait for them too).
-  // (the append's requantization of the ring, still in LDS, into group pos / 64, unless the tail
-  // did it because the token completed the group; the next launch is the first to read the group)
-  if (wave < RING_PARTS && !TOK && pos_ok && (pos + 1) % GT != 0)
-    append_ring_channels(la, h, pos, sm.ring_lds, reinterpret_cast<uint8_t*>(sm.ring_part));
   return gave_up;
 }
 
@@ -2001,6 +2111,10 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
   const uint32_t my_lds = __builtin_amdgcn_readfirstlane(lds_addr(my_stages));
   const uint32_t rul_lds = my_lds + 2 * HALF_SLOT;
   bool lost = false;  // a counter wait of this workgroup gave up
+  // this launch's forwarding tag: the launch counter (advanced at the exit) + 1; tag 0, that of
+  // a zero-filled workspace, is never current
+  int* const epoch = a.tail_ctr_end - 3 - n_layers;
+  const uint32_t ftag = (uint32_t)__hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
 
   // the wave's first group (both halves; int8t64: its rulers into ruler set 0)
   auto issue_first = [&](const AttnArgs& la) {
@@ -2014,24 +2128,31 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
     }
   };
   if (merger) {
-    for (int l = 0; l < n_layers; ++l) lost |= merger_layer<TOK>(layer_args<TOK>(a, layers, l), l, h, lds_raw, pos, pos_ok, U, lost);
+    for (int l = 0; l < n_layers; ++l) lost |= merger_layer<TOK>(layer_args<TOK>(a, layers, l, ftag), layers, l, h, lds_raw, pos, pos_ok, U, lost);
     // the last layer's consumed partial block back to zero (the earlier layers' slots are zeroed
     // by their writers, below)
-    uint4* blk = reinterpret_cast<uint4*>(layer_args<TOK>(a, layers, n_layers - 1).ws + (int64_t)h * P * pw);
+    uint4* blk = reinterpret_cast<uint4*>(layer_args<TOK>(a, layers, n_layers - 1, ftag).ws + (int64_t)h * P * pw);
     for (int i = tid; i < P * pw / 4; i += THREADS) blk[i] = uint4{0u, 0u, 0u, 0u};
   } else {
-  if (wave != IN_WAVE) issue_first(layer_args<TOK>(a, layers, 0));
+  if (wave != IN_WAVE) issue_first(layer_args<TOK>(a, layers, 0, ftag));
   for (int l = 0; l < n_layers; ++l) {
-    const AttnArgs la = layer_args<TOK>(a, layers, l);
+    const AttnArgs la = layer_args<TOK>(a, layers, l, ftag);
 
     // ---- streaming part: q of layer l once layer l - 1 is complete (layer 0: the input wave's
     // first group goes behind q; later layers: it was prefetched with the others' and has long
     // landed when the counter wait ends, so waiting for q waits for nothing else)
     if (wave == IN_WAVE) {
-      const bool ok = l == 0 || wait_layer(a, l - 1, a.hkv, lost);
+      bool ok = true;
+      if (l > 0 && gq <= FWD_MAX_GQ && la.q == layer_out<TOK>(layers, l - 1)) {
+        // q is layer l - 1's output: its tagged words, no counter wait
+        ok = fwd_fetch(la.fwd_out - (int64_t)la.hq * D / 2 + (int64_t)h * gq * D / 2, nullptr, nullptr, gq, la.ftag,
+                       reinterpret_cast<uint32_t*>(q_lds), lost);
+      } else {
+        ok = l == 0 || wait_layer(a, l - 1, a.hkv, lost);
+        issue_q(la.q + (int64_t)h * gq * D, gq, __builtin_amdgcn_readfirstlane(lds_addr(q_lds)));
+        wait_groups_all();
+      }
       if (tid == IN_WAVE * 64) lost_sh = ok ? 0 : 1;
-      issue_q(la.q + (int64_t)h * gq * D, gq, __builtin_amdgcn_readfirstlane(lds_addr(q_lds)));
-      wait_groups_all();
       if (l == 0) issue_first(la);
     }
     __syncthreads();
@@ -2107,7 +2228,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
     }
     // ---- the stages are free: the next layer's first groups stream while this layer merges
     __syncthreads();
-    if (l + 1 < n_layers) issue_first(layer_args<TOK>(a, layers, l + 1));
+    if (l + 1 < n_layers) issue_first(layer_args<TOK>(a, layers, l + 1, ftag));
   }
   // every merger has consumed layers 0 .. n_layers - 2 (this workgroup passed the last counter
   // wait): their slots of this part back to zero, read again by the next launch
@@ -2126,6 +2247,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
     if (t == (int)gridDim.x - 1) {
       for (int l = 0; l < n_layers; ++l) __hip_atomic_store(layer_done(a, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(exit_ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(epoch, (int)ftag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -3141,7 +3263,10 @@ int layers_resident(bool tok, int* out) {
   return NKV_OK;
 }
 
-int64_t layers_sync_bytes(int64_t n_layers) { return ctr_bytes(n_layers + 2); }
+// n_layers counters, the exit ticket, the error word, the launch counter
+int64_t layers_sync_bytes(int64_t n_layers) { return ctr_bytes(n_layers + 3); }
+// each layer's output as tagged words (forwarded to the next layer's inputs)
+int64_t layers_fwd_bytes(int64_t hq, int64_t n_layers) { return n_layers * hq * D / 2 * (int64_t)sizeof(uint64_t); }
 
 // Streaming parts per KV head: one workgroup per 8 groups at most, and hkv (parts + 1) workgroups
 // resident at once.
@@ -3168,12 +3293,14 @@ int launch_layers(AttnArgs& a, bool tok, const void* layers_dev, int64_t n_layer
     return fail(NKV_ERR_UNSUPPORTED,
                 "%s: %lld workgroups (%d KV heads x (%lld parts + 1)) exceed the %d this device holds at once",
                 what, (long long)grid, a.hkv, (long long)n_parts, resident);
-  const int64_t need = n_layers * a.hkv * n_parts * part_floats(a.hq, a.hkv) * (int64_t)sizeof(float) + layers_sync_bytes(n_layers);
+  const int64_t part_bytes = n_layers * a.hkv * n_parts * part_floats(a.hq, a.hkv) * (int64_t)sizeof(float);
+  const int64_t need = part_bytes + layers_fwd_bytes(a.hq, n_layers) + layers_sync_bytes(n_layers);
   if (!a.ws || !al16(a.ws)) return fail(NKV_ERR_INVALID, "%s: the workspace must be a non-null, 16-byte aligned buffer", what);
   if (workspace_bytes < need)
     return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
   a.n_parts = (int)n_parts;
   a.tail_ctr_end = reinterpret_cast<int*>(reinterpret_cast<char*>(a.ws) + (workspace_bytes & ~int64_t(3)));
+  a.fwd_out = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(a.ws) + part_bytes);
   if (tok) hipLaunchKernelGGL(attn_layers_kernel<CONTIG_TOK>, dim3((unsigned)grid), dim3(THREADS), 0, s, a, layers_dev, (int)n_layers);
   else hipLaunchKernelGGL(attn_layers_kernel<CONTIG_T64>, dim3((unsigned)grid), dim3(THREADS), 0, s, a, layers_dev, (int)n_layers);
   return check_launch(what);
@@ -3182,7 +3309,8 @@ int launch_layers(AttnArgs& a, bool tok, const void* layers_dev, int64_t n_layer
 
 extern "C" int64_t nkv_layers_workspace_bytes(int64_t hkv, int64_t hq, int64_t n_parts, int64_t n_layers) {
   if (hkv <= 0 || hq <= 0 || hq % hkv || n_parts <= 0 || n_layers <= 0) return 0;
-  return n_layers * hkv * n_parts * part_floats(hq, hkv) * (int64_t)sizeof(float) + layers_sync_bytes(n_layers);
+  return n_layers * hkv * n_parts * part_floats(hq, hkv) * (int64_t)sizeof(float) + layers_fwd_bytes(hq, n_layers) +
+         layers_sync_bytes(n_layers);
 }
 
 extern "C" int64_t nkv_layers_default_parts(int64_t hkv, int64_t capacity, int tok) {

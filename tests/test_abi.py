@@ -155,9 +155,11 @@ def test_chained_step_sizes_and_checks(lib):
     from nova_amd import _lib
 
     per_part = 8 * (4 * 128 + 8) * 4  # one partial of 4 query heads, per KV head
-    sync = lambda n: -(-((n + 2) * 4) // 256) * 256  # noqa: E731  (n layer counters, exit ticket, error word)
-    assert lib.nkv_layers_workspace_bytes(8, 32, 31, 36) == 36 * 31 * per_part + sync(36)
-    assert lib.nkv_layers_workspace_bytes(8, 32, 1, 1) == per_part + 256
+    # n layer counters, the exit ticket, the error word and the launch counter
+    sync = lambda n: -(-((n + 3) * 4) // 256) * 256  # noqa: E731
+    fwd = 32 * 128 // 2 * 8  # one layer's output as tagged words (two fp16 values per 8 bytes)
+    assert lib.nkv_layers_workspace_bytes(8, 32, 31, 36) == 36 * (31 * per_part + fwd) + sync(36)
+    assert lib.nkv_layers_workspace_bytes(8, 32, 1, 1) == per_part + fwd + 256
     assert lib.nkv_layers_workspace_bytes(8, 30, 31, 36) == 0 and lib.nkv_layers_workspace_bytes(8, 32, 0, 4) == 0
     fake = 1 << 20
     table = np.full((2, 13), fake, dtype=np.int64)
