@@ -268,9 +268,10 @@ __device__ __forceinline__ void dma16_stream(const void* sbase, uint32_t voff, u
 
 // Issue the loads of half `hf` (tokens 32 hf .. 32 hf + 31) of group `grp` of head h: 32
 // K and 32 V code rows (4 + 4 loads) into the slot at `slot` (K codes, then V codes), and
-// for hf == 0 the group's rulers (4 loads) into `rs`. Rows are swizzled as in a full
+// with `with_rulers` (by default for hf == 0) the group's rulers (4 loads) into `rs`. Rows are swizzled as in a full
 // stage; token rows at or beyond the capacity are never read (the last row is repeated).
-__device__ __forceinline__ void issue_half(const AttnArgs& a, int h, int64_t grp, int hf, uint32_t slot, uint32_t rs) {
+__device__ __forceinline__ void issue_half(const AttnArgs& a, int h, int64_t grp, int hf, uint32_t slot, uint32_t rs,
+                                           bool with_rulers) {
   const int lane = threadIdx.x & 63;
   const int64_t t0 = grp * GT + 32 * hf;
   const void* kb = uniform_ptr(a.kq + (int64_t)h * a.capacity * D);
@@ -289,7 +290,7 @@ __device__ __forceinline__ void issue_half(const AttnArgs& a, int h, int64_t grp
     const uint32_t off = (uint32_t)(min<int64_t>(t0 + row, a.capacity - 1) * D) + (((lane & 7) ^ swz(row)) << 4);
     dma16_stream(vb, off, slot + HALF_CODE + 1024 * j);
   }
-  if (hf == 0) {
+  if (with_rulers) {
     rs = __builtin_amdgcn_readfirstlane(rs);
     const int64_t ro = ((int64_t)h * a.ngroups_cap + grp) * D;
     const uint32_t roff = (uint32_t)(8 * (lane & 15)) * 2;
@@ -299,6 +300,9 @@ __device__ __forceinline__ void issue_half(const AttnArgs& a, int h, int64_t grp
     if (which == 2) dma16_stream(uniform_ptr(a.vst + ro), roff, rs);
     if (which == 3) dma16_stream(uniform_ptr(a.vmn + ro), roff, rs);
   }
+}
+__device__ __forceinline__ void issue_half(const AttnArgs& a, int h, int64_t grp, int hf, uint32_t slot, uint32_t rs) {
+  issue_half(a, h, grp, hf, slot, rs, hf == 0);
 }
 
 // The per-token symmetric format's half group: 32 K and 32 V code rows (4 + 4 loads) into
@@ -2117,14 +2121,32 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
   const uint32_t ftag = (uint32_t)__hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
 
   // the wave's first group (both halves; int8t64: its rulers into ruler set 0)
+  // The part's groups: the first `whole` go whole to the waves, strided (wave w takes w, w + 8,
+  // ..); when at most 4 groups are left over a multiple of 8, their halves go one per wave to
+  // waves 0 .. extra - 1 (no wave then takes more than one half beyond the others), else they go
+  // whole as well. An extra half brings its group's rulers.
+  const int rest = ng % WAVES;
+  const int whole = 2 * rest <= WAVES ? ng - rest : ng, extra = 2 * (ng - whole);
+  const bool has_x = wave < extra;
+  const int64_t xg = gs + whole + (wave >> 1);
+  const int xh = wave & 1;
+  // the half of the extra group, with the rulers, into slot 0 and ruler set `set`
+  auto issue_extra = [&](const AttnArgs& la, int set) {
+    if constexpr (TOK) issue_tok<false>(la, 0, h, xg, xh, my_lds);
+    else issue_half(la, h, xg, xh, my_lds, rul_lds + set * RULER_BYTES, true);
+  };
+  // the wave's first item: its first whole group (both halves), or its extra half
   auto issue_first = [&](const AttnArgs& la) {
-    if (wave >= ng) return;
-    if constexpr (TOK) {
-      issue_tok<false>(la, 0, h, gs + wave, 0, my_lds);
-      issue_tok<false>(la, 0, h, gs + wave, 1, my_lds + HALF_SLOT_TOK);
-    } else {
-      issue_half(la, h, gs + wave, 0, my_lds, rul_lds);
-      issue_half(la, h, gs + wave, 1, my_lds + HALF_SLOT, rul_lds);
+    if (wave < whole) {
+      if constexpr (TOK) {
+        issue_tok<false>(la, 0, h, gs + wave, 0, my_lds);
+        issue_tok<false>(la, 0, h, gs + wave, 1, my_lds + HALF_SLOT_TOK);
+      } else {
+        issue_half(la, h, gs + wave, 0, my_lds, rul_lds);
+        issue_half(la, h, gs + wave, 1, my_lds + HALF_SLOT, rul_lds);
+      }
+    } else if (has_x) {
+      issue_extra(la, 0);
     }
   };
   if (merger) {
@@ -2161,58 +2183,79 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
     state_init(st);
     half8_t qb[4];
     load_q_lds(q_lds, gq, qb);
-    int gi = wave;
-    for (int rs = 0; gi < ng; rs ^= 1) {
+    int rs = 0;  // ruler set of the group in the slots
+    for (int gi = wave; gi < whole; gi += WAVES, rs ^= 1) {
       const int64_t grp = gs + gi;
       const uint8_t* rul = my_stages + 2 * HALF_SLOT + rs * RULER_BYTES;
       const uint8_t* slot1 = my_stages + slot_bytes;
-      const int nx = gi + WAVES;
+      const bool nx_whole = gi + WAVES < whole, nx_extra = !nx_whole && has_x;
       const int nv1 = (int)min<int64_t>(32, U - grp * GT), nv2 = (int)min<int64_t>(32, U - grp * GT - 32);
+      // first half (slot 0; the second half may still be in flight), then the next item's first
+      // loads into slot 0 (the next group's half 0 and rulers, or the extra half and its rulers)
       if constexpr (TOK) {
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_HALF_TOK) : "memory");
         attend_block_tok(la, st, qb, my_stages, my_stages + HALF_CODE,
                          reinterpret_cast<const uint16_t*>(my_stages + 2 * HALF_CODE),
                          reinterpret_cast<const uint16_t*>(my_stages + 2 * HALF_CODE + TOK_SCALE_BYTES), nv1);
-        if (nx < ng) issue_tok<false>(la, 0, h, gs + nx, 0, my_lds);
-        if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_HALF_TOK) : "memory");
+        if (nx_whole) issue_tok<false>(la, 0, h, grp + WAVES, 0, my_lds);
+        else if (nx_extra) issue_extra(la, rs ^ 1);
+        if (nx_whole || nx_extra) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_HALF_TOK) : "memory");
         else wait_groups_all();
         if (nv2 > 0)
           attend_block_tok(la, st, qb, slot1, slot1 + HALF_CODE, reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE),
                            reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE + TOK_SCALE_BYTES), nv2);
-        if (nx < ng) issue_tok<false>(la, 0, h, gs + nx, 1, my_lds + HALF_SLOT_TOK);
+        if (nx_whole) issue_tok<false>(la, 0, h, grp + WAVES, 1, my_lds + HALF_SLOT_TOK);
       } else {
         LaneRulers ru;
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_SECOND_HALF) : "memory");
         load_rulers(rul, ru);
         attend_block<1>(la, st, qb, my_stages, my_stages + HALF_CODE, ru, nv1);
-        if (nx < ng) issue_half(la, h, gs + nx, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
-        if (nx < ng) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF) : "memory");
+        if (nx_whole) issue_half(la, h, grp + WAVES, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
+        else if (nx_extra) issue_extra(la, rs ^ 1);
+        if (nx_whole || nx_extra) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF) : "memory");
         else wait_groups_all();
         if (nv2 > 0) attend_block<1>(la, st, qb, slot1, slot1 + HALF_CODE, ru, nv2);
-        if (nx < ng) issue_half(la, h, gs + nx, 1, my_lds + HALF_SLOT, 0u);
+        if (nx_whole) issue_half(la, h, grp + WAVES, 1, my_lds + HALF_SLOT, 0u);
       }
-      gi = nx;
+    }
+    if (has_x) {
+      // the extra half, in slot 0 with its rulers in set rs (issued by the last whole group, or
+      // by issue_first when the wave has none)
+      const int nvx = (int)max<int64_t>(0, min<int64_t>(32, U - xg * GT - 32 * xh));
+      wait_groups_all();
+      if (nvx > 0) {
+        if constexpr (TOK) {
+          attend_block_tok(la, st, qb, my_stages, my_stages + HALF_CODE,
+                           reinterpret_cast<const uint16_t*>(my_stages + 2 * HALF_CODE),
+                           reinterpret_cast<const uint16_t*>(my_stages + 2 * HALF_CODE + TOK_SCALE_BYTES), nvx);
+        } else {
+          LaneRulers ru;
+          load_rulers(my_stages + 2 * HALF_SLOT + rs * RULER_BYTES, ru);
+          attend_block<1>(la, st, qb, my_stages, my_stages + HALF_CODE, ru, nvx);
+        }
+      }
     }
 
     // ---- merge the waves through LDS and publish the partial word by word
+    const int ptid = tail_tid();  // (per layer: nothing derived from it stays live across the loop)
     __syncthreads();
     store_wave_partial(st, gq, lds + wave * pw);
     __syncthreads();
     float* dst = la.ws + ((int64_t)h * P + part) * pw;
     float pm = NEG_INF, pl = 0.0f;
-    if (tid < gq) {
+    if (ptid < gq) {
 #pragma unroll
-      for (int w = 0; w < WAVES; ++w) pm = fmaxf(pm, lds[w * pw + gq * D + tid]);
+      for (int w = 0; w < WAVES; ++w) pm = fmaxf(pm, lds[w * pw + gq * D + ptid]);
       const float mu = pm == NEG_INF ? 0.0f : pm;
 #pragma unroll
       for (int w = 0; w < WAVES; ++w) {
-        const float x = __builtin_amdgcn_exp2f(lds[w * pw + gq * D + tid] - mu);
-        xch[tid * WAVES + w] = x;
-        pl += lds[w * pw + gq * D + gq + tid] * x;
+        const float x = __builtin_amdgcn_exp2f(lds[w * pw + gq * D + ptid] - mu);
+        xch[ptid * WAVES + w] = x;
+        pl += lds[w * pw + gq * D + gq + ptid] * x;
       }
     }
     __syncthreads();
-    for (int e = 2 * tid; e < gq * D; e += 2 * THREADS) {
+    for (int e = 2 * ptid; e < gq * D; e += 2 * THREADS) {
       const float* c = xch + (e / D) * WAVES;
       float x = 0.0f, y = 0.0f;
 #pragma unroll
@@ -2222,9 +2265,9 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
       }
       pub_st2(dst + e, x, y);
     }
-    if (tid < gq) {
-      pub_st(dst + gq * D + tid, pm);
-      pub_st(dst + gq * D + gq + tid, lost ? __builtin_nanf("") : pl);  // a lost wait poisons the merge
+    if (ptid < gq) {
+      pub_st(dst + gq * D + ptid, pm);
+      pub_st(dst + gq * D + gq + ptid, lost ? __builtin_nanf("") : pl);  // a lost wait poisons the merge
     }
     // ---- the stages are free: the next layer's first groups stream while this layer merges
     __syncthreads();
