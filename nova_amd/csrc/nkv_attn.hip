@@ -1084,6 +1084,7 @@ struct TailSmem {
   uint32_t fwd[(16 + 2) * D / 2];            // the chained step: forwarded q, k_new, v_new of the head (fp16 pairs)
   uint8_t xpose[RING_PARTS * GT * 64];       // the chained step's append: each ring wave's 64 x 64 codes
   int ring_staged;                           // ring waves that have staged their slots (the chained step's append)
+  int ring_done;                             // ring waves whose partial is in ring_part (TB_DIRECT)
 };
 constexpr int MERGER_MAX_PARTS = 64;         // prefix parts per head of a fused launch
 constexpr int MERGER_MAX_HEADS = 64;         // KV heads of a fused launch: its part-0 workgroups wait for the others
@@ -1332,12 +1333,16 @@ __device__ __forceinline__ void tail_load_rows(const AttnArgs& a, int h, int b, 
 }
 
 // `flags` (the chained-layer kernel's merger): TB_APPEND, the tail also appends the new token:
-// it stores the token into its ring slot (per-token symmetric: the token's codes and scale) and,
-// when the token completes its group, requantizes the ring from LDS into group pos / 64 (else the
-// caller does that afterwards with the ring still in sm.ring_lds: append_from_ring);
-// TB_KEEP_BLOCK, the consumed partial block is left for the caller to zero; TB_POISON, the
-// caller's own wait for its inputs gave up: the output is NaN.
-constexpr int TB_APPEND = 1, TB_KEEP_BLOCK = 2, TB_POISON = 4;
+// it stores the token into its ring slot (per-token symmetric: the token's codes and scale) and
+// rules its group: from the staged ring into the token's channels of group pos / 64
+// (append_ring_channels), or, when the token completes the group, by requantizing the whole ring
+// from LDS; TB_KEEP_BLOCK, the consumed partial block is left for the caller to zero;
+// TB_POISON, the caller's own wait for its inputs gave up: the output is NaN; TB_DIRECT (with
+// TB_KEEP_BLOCK, the caller having set sm.ring_done to zero), when every merging wave owns one
+// head: each merging wave combines its head with the ring partials and stores the outputs itself
+// as soon as its merge is done (no workgroup barrier; a head whose words never arrived is NaN
+// alone), and the tail returns without a final barrier.
+constexpr int TB_APPEND = 1, TB_KEEP_BLOCK = 2, TB_POISON = 4, TB_DIRECT = 8;
 
 template <bool PAGED>
 __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailSmem& sm, int run, int64_t pos,
@@ -1352,6 +1357,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   float* hws = PAGED ? a.ws + ((int64_t)h * a.total_parts + a.seq_parts[2 * b]) * pw : a.ws + (int64_t)h * P * pw;
   // while waves 0..3 attend over the ring, the others merge the prefix partials
   const int mbase = ring ? RING_PARTS : 0, nmw = TB_WAVES - mbase;
+  const bool direct = (flags & TB_DIRECT) && (flags & TB_KEEP_BLOCK) && P <= 64 && nmw >= gq;
 
   // ---- loads: the ring rows (or the new token) and q of the ring waves, the merging waves'
   // partial words
@@ -1469,6 +1475,10 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     state_init(st);
     attend_ring16(a, st, qb, ring_k, ring_v, wave, bits);
     store_wave_partial(st, gq, sm.ring_part[wave]);
+    if (direct) {  // the merging waves read it as soon as every ring wave has counted itself
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (lane == 0) __hip_atomic_fetch_add(&sm.ring_done, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
     if (ring_append) {
       while (__hip_atomic_load(&sm.ring_staged, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < RING_PARTS)
         __builtin_amdgcn_s_sleep(1);
@@ -1538,10 +1548,48 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
           acc.y += vv.y * wb[sb + j];
         }
       }
-      *reinterpret_cast<float2*>(sm.pre_acc + head0 * D + 2 * lane) = acc;
-      if (lane == 0) {
-        sm.pre_m[head0] = m;
-        sm.pre_l[head0] = l;
+      if (direct) {
+        // ---- combine (the combine below, for this head's column pair 2 lane, 2 lane + 1)
+        if (ring)
+          while (__hip_atomic_load(&sm.ring_done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < RING_PARTS)
+            __builtin_amdgcn_s_sleep(1);
+        const bool failed = (flags & TB_POISON) != 0 || __builtin_amdgcn_ballot_w64(lost) != 0;
+        const int col = head0 * D + 2 * lane;
+        float M = m, mr[RING_PARTS], lr[RING_PARTS];
+        float2 ar[RING_PARTS];
+#pragma unroll
+        for (int r = 0; r < RING_PARTS; ++r) {
+          mr[r] = ring ? sm.ring_part[r][gq * D + head0] : NEG_INF;
+          lr[r] = ring ? sm.ring_part[r][gq * D + gq + head0] : 0.0f;
+          ar[r] = ring ? *reinterpret_cast<const float2*>(sm.ring_part[r] + col) : float2{0.0f, 0.0f};
+          M = fmaxf(M, mr[r]);
+        }
+        const float Mu = M == NEG_INF ? 0.0f : M;
+        const float alpha = m == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m - Mu);
+        float ox = alpha * acc.x, oy = alpha * acc.y, lt = alpha * l;
+#pragma unroll
+        for (int r = 0; r < RING_PARTS; ++r) {
+          const float beta = mr[r] == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mr[r] - Mu);
+          ox += beta * ar[r].x;
+          oy += beta * ar[r].y;
+          lt += beta * lr[r];
+        }
+        const int64_t qh = qh0 + head0;
+        ox = failed ? __builtin_nanf("") : (lt > 0.0f ? ox / lt : 0.0f);
+        oy = failed ? __builtin_nanf("") : (lt > 0.0f ? oy / lt : 0.0f);
+        const uint32_t pair = (uint32_t)f2h(ox) | ((uint32_t)f2h(oy) << 16);
+        *reinterpret_cast<uint32_t*>(a.out + qh * D + 2 * lane) = pair;
+        if (a.fwd_out)
+          __hip_atomic_store(a.fwd_out + qh * D / 2 + lane, ((uint64_t)a.ftag << 32) | pair, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        if (a.lse && lane == 0)
+          a.lse[qh] = failed ? __builtin_nanf("") : (lt > 0.0f ? (M + __log2f(lt) - P_SCALE_LOG2) * LN2 : NEG_INF);
+      } else {
+        *reinterpret_cast<float2*>(sm.pre_acc + head0 * D + 2 * lane) = acc;
+        if (lane == 0) {
+          sm.pre_m[head0] = m;
+          sm.pre_l[head0] = l;
+        }
       }
     } else {
       for (int head = head0; head < gq; head += nmw) {
@@ -1617,6 +1665,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     }
     if (lane == 0) sm.lost[wave] = __builtin_amdgcn_ballot_w64(lost) != 0;
   }
+  if (direct) return;
   __syncthreads();
 
   // ---- combine: one column per thread. Prefix: acc_p = sum_s w_s acc_s; then with the
@@ -2054,7 +2103,10 @@ __device__ __forceinline__ bool merger_layer(const AttnArgs& args, const void* l
     const int64_t n = (int64_t)la.hq * D, span = (int64_t)(la.hkv - 1) * la.kv_hs + D;
     fwd = la.q == prev && within(la.k_new, span, prev, n) && within(la.v_new, span, prev, n);
   }
-  if (tid == 0) sm.ring_staged = 0;
+  if (tid == 0) {
+    sm.ring_staged = 0;
+    sm.ring_done = 0;
+  }
   if (wave == IN_WAVE) {
     bool ok = true;
     if (fwd) {
@@ -2078,7 +2130,7 @@ __device__ __forceinline__ bool merger_layer(const AttnArgs& args, const void* l
     la.kv_hs = 0;
   }
   tail_body<false>(la, h, 0, sm, TAIL_MERGER, pos, pos_ok, U, nullptr, fwd ? &qb : nullptr,
-                   TB_APPEND | TB_KEEP_BLOCK | (lost || gave_up ? TB_POISON : 0));
+                   TB_APPEND | TB_KEEP_BLOCK | TB_DIRECT | (lost || gave_up ? TB_POISON : 0));
   // every wave's stores (out, lse, the ring slot) complete before the workgroup meets; then one
   // release at agent scope publishes them all with the count
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
