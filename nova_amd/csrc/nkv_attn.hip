@@ -492,24 +492,32 @@ __device__ __forceinline__ void softmax_step(WaveState& st, float (&s)[2 * NB][4
   }
 }
 
-// One group's rulers as a lane uses them: K's step and min for the dims of its K operand
-// chunks, V's (splatted) for dim 16 cb + c, read from the group's ruler rows in LDS (kst | kmn
-// | vst | vmn, 128 fp16 each) once per group and used by both halves.
+// One group's rulers as a lane uses them: V's (splatted) for dim 16 cb + c, read from the
+// group's ruler rows in LDS (kst | kmn | vst | vmn, 128 fp16 each) once per group and used by
+// both halves; K's step and min for the dims of the lane's K operand chunks are read from `rul`
+// by each half, so that they are not live across the softmax and the PV product (keeping them
+// for both halves took 32 more VGPRs, and the chained kernel's loop had none to spare).
 struct LaneRulers {
-  uint4 kst4[2][2], kmn4[2][2];
   half2_t vsp[8], vmp[8];
+  const uint8_t* rul;
 };
 
-__device__ __forceinline__ void load_rulers(const uint8_t* rul, LaneRulers& r) {
-  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+__device__ __forceinline__ void load_k_rulers(const uint8_t* rul, uint4 (&kst4)[2][2], uint4 (&kmn4)[2][2]) {
+  const int g = (threadIdx.x & 63) >> 4;
   const uint16_t* rks = reinterpret_cast<const uint16_t*>(rul);
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      r.kst4[hh][e] = *reinterpret_cast<const uint4*>(rks + 16 * g + 64 * hh + 8 * e);
-      r.kmn4[hh][e] = *reinterpret_cast<const uint4*>(rks + D + 16 * g + 64 * hh + 8 * e);
+      kst4[hh][e] = *reinterpret_cast<const uint4*>(rks + 16 * g + 64 * hh + 8 * e);
+      kmn4[hh][e] = *reinterpret_cast<const uint4*>(rks + D + 16 * g + 64 * hh + 8 * e);
     }
+}
+
+__device__ __forceinline__ void load_rulers(const uint8_t* rul, LaneRulers& r) {
+  const int lane = threadIdx.x & 63, c = lane & 15;
+  const uint16_t* rks = reinterpret_cast<const uint16_t*>(rul);
+  r.rul = rul;
 #pragma unroll
   for (int cb = 0; cb < 8; ++cb) {
     const _Float16 vs = __builtin_bit_cast(_Float16, rks[2 * D + 16 * cb + c]);
@@ -526,8 +534,8 @@ template <int NB>
 __device__ __forceinline__ void attend_block(const AttnArgs& a, WaveState& st, const half8_t (&qb)[4],
                                              const uint8_t* kc, const uint8_t* vc, const LaneRulers& ru, int nvalid) {
   const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-  const auto& kst4 = ru.kst4;
-  const auto& kmn4 = ru.kmn4;
+  uint4 kst4[2][2], kmn4[2][2];
+  load_k_rulers(ru.rul, kst4, kmn4);
 
   // ---- S^T = K Q^T
   float4_t S[2 * NB];
@@ -561,21 +569,28 @@ __device__ __forceinline__ void attend_block(const AttnArgs& a, WaveState& st, c
 
   // ---- O += P V. Lane (c, g) of a transpose read supplies row k(g, c >> 1) and half
   // (c & 1) of the 16-dim chunk; it receives dim 16cb + c of the 8 tokens k(g, 0..7),
-  // k(g, r) = 16 * (2B + (r >> 2)) + 4g + (r & 3), the token order of P's k-slots.
+  // k(g, r) = 16 * (2B + (r >> 2)) + 4g + (r & 3), the token order of P's k-slots. All the
+  // half's transpose reads are issued before the first product (one wait for all of them;
+  // reading them before the softmax instead measured slower).
   const auto& vsp = ru.vsp;
   const auto& vmp = ru.vmp;
   const int r = c >> 1;
+  u32x2 vw[NB][8];
 #pragma unroll
   for (int B = 0; B < NB; ++B) {
     const int row = 16 * (2 * B + (r >> 2)) + 4 * g + (r & 3);
-    const int key = swz(row);
-    const uint8_t* rowp = vc + row * D + 8 * (c & 1);
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb)
+      vw[B][cb] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                      (lds_v2i_t*)(const lds_void_t*)(vc + row * D + 8 * (c & 1) + ((cb ^ swz(row)) << 4))));
+  }
+
+#pragma unroll
+  for (int B = 0; B < NB; ++B) {
     if (nvalid >= 32 * NB) {
 #pragma unroll
       for (int cb = 0; cb < 8; ++cb) {
-        const u32x2 vw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-                             (lds_v2i_t*)(const lds_void_t*)(rowp + ((cb ^ key) << 4))));
-        const half8_t vb = dq8_splat(vw.x, vw.y, vsp[cb], vmp[cb]);
+        const half8_t vb = dq8_splat(vw[B][cb].x, vw[B][cb].y, vsp[cb], vmp[cb]);
         st.acc[cb] = mfma32(phi[B], vb, st.acc[cb]);
         st.acc[cb] = mfma32(plo[B], vb, st.acc[cb]);
       }
@@ -590,9 +605,8 @@ __device__ __forceinline__ void attend_block(const AttnArgs& a, WaveState& st, c
       const u32x2 keep = u32x2{m[0], m[1]};
 #pragma unroll
       for (int cb = 0; cb < 8; ++cb) {
-        const u32x2 vw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-                             (lds_v2i_t*)(const lds_void_t*)(rowp + ((cb ^ key) << 4)))) & keep;
-        const half8_t vb = dq8_splat(vw.x, vw.y, vsp[cb], vmp[cb]);
+        const u32x2 vm = vw[B][cb] & keep;
+        const half8_t vb = dq8_splat(vm.x, vm.y, vsp[cb], vmp[cb]);
         st.acc[cb] = mfma32(phi[B], vb, st.acc[cb]);
         st.acc[cb] = mfma32(plo[B], vb, st.acc[cb]);
       }
@@ -671,11 +685,15 @@ __device__ __forceinline__ void attend_block_tok(const AttnArgs& a, WaveState& s
     keep = u32x2{m[0], m[1]};
     vs = uint4{vs.x & hm[0], vs.y & hm[1], vs.z & hm[2], vs.w & hm[3]};
   }
+  u32x2 vw[8];  // (all eight transpose reads before the first product)
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb)
+    vw[cb] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                 (lds_v2i_t*)(const lds_void_t*)(rowp + ((cb ^ key) << 4))));
 #pragma unroll
   for (int cb = 0; cb < 8; ++cb) {
-    const u32x2 vw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-                         (lds_v2i_t*)(const lds_void_t*)(rowp + ((cb ^ key) << 4)))) & keep;
-    const half8_t vb = dq8_sym_v(vw.x, vw.y, vs);
+    const u32x2 vm = vw[cb] & keep;
+    const half8_t vb = dq8_sym_v(vm.x, vm.y, vs);
     st.acc[cb] = mfma32(phi[0], vb, st.acc[cb]);
     st.acc[cb] = mfma32(plo[0], vb, st.acc[cb]);
   }
