@@ -270,25 +270,43 @@ __device__ __forceinline__ void dma16_stream(const void* sbase, uint32_t voff, u
 // K and 32 V code rows (4 + 4 loads) into the slot at `slot` (K codes, then V codes), and
 // with `with_rulers` (by default for hf == 0) the group's rulers (4 loads) into `rs`. Rows are swizzled as in a full
 // stage; token rows at or beyond the capacity are never read (the last row is repeated).
+// Lane `lane`'s byte offset within a half's rows for load j: row 8 j + lane / 8, its 16-byte
+// chunk lane % 8 at the swizzled position (the same for every half, so the compiler keeps the
+// four offsets in registers across the streaming loop).
+__device__ __forceinline__ uint32_t half_row_off(int lane, int j) {
+  const int row = 8 * j + (lane >> 3);
+  return (uint32_t)(row * D) + (((lane & 7) ^ swz(row)) << 4);
+}
+
 __device__ __forceinline__ void issue_half(const AttnArgs& a, int h, int64_t grp, int hf, uint32_t slot, uint32_t rs,
                                            bool with_rulers) {
   const int lane = threadIdx.x & 63;
   const int64_t t0 = grp * GT + 32 * hf;
-  const void* kb = uniform_ptr(a.kq + (int64_t)h * a.capacity * D);
-  const void* vb = uniform_ptr(a.vq + (int64_t)h * a.capacity * D);
   slot = __builtin_amdgcn_readfirstlane(slot);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // earlier reads of this slot are done
+  if (t0 + 32 <= a.capacity) {
+    // the half's rows from the half's first row on: per-lane offsets that do not change
+    const void* kb = uniform_ptr(a.kq + ((int64_t)h * a.capacity + t0) * D);
+    const void* vb = uniform_ptr(a.vq + ((int64_t)h * a.capacity + t0) * D);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int row = 8 * j + (lane >> 3);
-    const uint32_t off = (uint32_t)(min<int64_t>(t0 + row, a.capacity - 1) * D) + (((lane & 7) ^ swz(row)) << 4);
-    dma16_stream(kb, off, slot + 1024 * j);
-  }
+    for (int j = 0; j < 4; ++j) dma16_stream(kb, half_row_off(lane, j), slot + 1024 * j);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int row = 8 * j + (lane >> 3);
-    const uint32_t off = (uint32_t)(min<int64_t>(t0 + row, a.capacity - 1) * D) + (((lane & 7) ^ swz(row)) << 4);
-    dma16_stream(vb, off, slot + HALF_CODE + 1024 * j);
+    for (int j = 0; j < 4; ++j) dma16_stream(vb, half_row_off(lane, j), slot + HALF_CODE + 1024 * j);
+  } else {
+    const void* kb = uniform_ptr(a.kq + (int64_t)h * a.capacity * D);
+    const void* vb = uniform_ptr(a.vq + (int64_t)h * a.capacity * D);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = 8 * j + (lane >> 3);
+      const uint32_t off = (uint32_t)(min<int64_t>(t0 + row, a.capacity - 1) * D) + (((lane & 7) ^ swz(row)) << 4);
+      dma16_stream(kb, off, slot + 1024 * j);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = 8 * j + (lane >> 3);
+      const uint32_t off = (uint32_t)(min<int64_t>(t0 + row, a.capacity - 1) * D) + (((lane & 7) ^ swz(row)) << 4);
+      dma16_stream(vb, off, slot + HALF_CODE + 1024 * j);
+    }
   }
   if (with_rulers) {
     rs = __builtin_amdgcn_readfirstlane(rs);
@@ -311,20 +329,14 @@ __device__ __forceinline__ void issue_half(const AttnArgs& a, int h, int64_t grp
 __device__ __forceinline__ void issue_half_tok(const AttnArgs& a, int h, int64_t grp, int hf, uint32_t slot) {
   const int lane = threadIdx.x & 63;
   const int64_t t0 = grp * GT + 32 * hf;
-  const void* kb = uniform_ptr(a.kq + (int64_t)h * a.capacity * D);
-  const void* vb = uniform_ptr(a.vq + (int64_t)h * a.capacity * D);
+  const void* kb = uniform_ptr(a.kq + ((int64_t)h * a.capacity + t0) * D);
+  const void* vb = uniform_ptr(a.vq + ((int64_t)h * a.capacity + t0) * D);
   slot = __builtin_amdgcn_readfirstlane(slot);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // earlier reads of this slot are done
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int row = 8 * j + (lane >> 3);
-    dma16_stream(kb, (uint32_t)((t0 + row) * D) + (((lane & 7) ^ swz(row)) << 4), slot + 1024 * j);
-  }
+  for (int j = 0; j < 4; ++j) dma16_stream(kb, half_row_off(lane, j), slot + 1024 * j);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int row = 8 * j + (lane >> 3);
-    dma16_stream(vb, (uint32_t)((t0 + row) * D) + (((lane & 7) ^ swz(row)) << 4), slot + HALF_CODE + 1024 * j);
-  }
+  for (int j = 0; j < 4; ++j) dma16_stream(vb, half_row_off(lane, j), slot + HALF_CODE + 1024 * j);
   if (lane < 4) dma16_stream(uniform_ptr(a.ksc + (int64_t)h * a.capacity + t0), 16u * lane, slot + 2 * HALF_CODE);
   if (lane < 4) dma16_stream(uniform_ptr(a.vsc + (int64_t)h * a.capacity + t0), 16u * lane, slot + 2 * HALF_CODE + TOK_SCALE_BYTES);
 }
