@@ -2175,9 +2175,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
   constexpr bool TOK = LAYOUT == CONTIG_TOK;
   __shared__ __attribute__((aligned(16))) uint8_t lds_raw[TOK ? LDS_BYTES_TOK : LDS_BYTES];
   __shared__ __attribute__((aligned(16))) uint16_t q_lds[16 * D];
-  __shared__ __attribute__((aligned(16))) float xch[16 * WAVES];
   __shared__ int lost_sh;
-  float* lds = reinterpret_cast<float*>(lds_raw);
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.x % a.hkv, role = blockIdx.x / a.hkv;
@@ -2318,38 +2316,39 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
       }
     }
 
-    // ---- merge the waves through LDS and publish the partial word by word
+    // ---- merge the waves through LDS and publish the partial word by word: each wave puts its
+    // partial into its own stage (free once its own loop has ended), then each thread merges two
+    // columns, computing its head's wave weights 2^(m_w - m) itself (one barrier on the way)
     const int ptid = tail_tid();  // (per layer: nothing derived from it stays live across the loop)
+    store_wave_partial(st, gq, reinterpret_cast<float*>(my_stages));
     __syncthreads();
-    store_wave_partial(st, gq, lds + wave * pw);
-    __syncthreads();
-    float* dst = la.ws + ((int64_t)h * P + part) * pw;
-    float pm = NEG_INF, pl = 0.0f;
-    if (ptid < gq) {
+    {
+      float* dst = la.ws + ((int64_t)h * P + part) * pw;
+      auto wpart = [&](int w) { return reinterpret_cast<const float*>(lds_raw + w * wave_lds); };
+      for (int e = 2 * ptid; e < gq * D; e += 2 * THREADS) {
+        const int head = e / D;
+        float pm = NEG_INF;
 #pragma unroll
-      for (int w = 0; w < WAVES; ++w) pm = fmaxf(pm, lds[w * pw + gq * D + ptid]);
-      const float mu = pm == NEG_INF ? 0.0f : pm;
+        for (int w = 0; w < WAVES; ++w) pm = fmaxf(pm, wpart(w)[gq * D + head]);
+        const float mu = pm == NEG_INF ? 0.0f : pm;
+        float cw[WAVES], pl = 0.0f;
 #pragma unroll
-      for (int w = 0; w < WAVES; ++w) {
-        const float x = __builtin_amdgcn_exp2f(lds[w * pw + gq * D + ptid] - mu);
-        xch[ptid * WAVES + w] = x;
-        pl += lds[w * pw + gq * D + gq + ptid] * x;
+        for (int w = 0; w < WAVES; ++w) {
+          cw[w] = __builtin_amdgcn_exp2f(wpart(w)[gq * D + head] - mu);
+          pl += wpart(w)[gq * D + gq + head] * cw[w];
+        }
+        float x = 0.0f, y = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+          x += wpart(w)[e] * cw[w];
+          y += wpart(w)[e + 1] * cw[w];
+        }
+        pub_st2(dst + e, x, y);
+        if (e % D == 0) {
+          pub_st(dst + gq * D + head, pm);
+          pub_st(dst + gq * D + gq + head, lost ? __builtin_nanf("") : pl);  // a lost wait poisons the merge
+        }
       }
-    }
-    __syncthreads();
-    for (int e = 2 * ptid; e < gq * D; e += 2 * THREADS) {
-      const float* c = xch + (e / D) * WAVES;
-      float x = 0.0f, y = 0.0f;
-#pragma unroll
-      for (int w = 0; w < WAVES; ++w) {
-        x += lds[w * pw + e] * c[w];
-        y += lds[w * pw + e + 1] * c[w];
-      }
-      pub_st2(dst + e, x, y);
-    }
-    if (ptid < gq) {
-      pub_st(dst + gq * D + ptid, pm);
-      pub_st(dst + gq * D + gq + ptid, lost ? __builtin_nanf("") : pl);  // a lost wait poisons the merge
     }
     // ---- the stages are free: the next layer's first groups stream while this layer merges
     __syncthreads();
