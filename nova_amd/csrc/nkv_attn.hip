@@ -293,18 +293,21 @@ __device__ __forceinline__ void issue_half(const AttnArgs& a, int h, int64_t grp
 #pragma unroll
     for (int j = 0; j < 4; ++j) dma16_stream(vb, half_row_off(lane, j), slot + HALF_CODE + 1024 * j);
   } else {
+    // (a half that reaches the capacity: rows clamped to the last one; the opaque lane keeps
+    // the compiler from precomputing these offsets for every fixed group and holding them)
     const void* kb = uniform_ptr(a.kq + (int64_t)h * a.capacity * D);
     const void* vb = uniform_ptr(a.vq + (int64_t)h * a.capacity * D);
+    const int olane = tail_tid() & 63;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int row = 8 * j + (lane >> 3);
-      const uint32_t off = (uint32_t)(min<int64_t>(t0 + row, a.capacity - 1) * D) + (((lane & 7) ^ swz(row)) << 4);
+      const int row = 8 * j + (olane >> 3);
+      const uint32_t off = (uint32_t)(min<int64_t>(t0 + row, a.capacity - 1) * D) + (((olane & 7) ^ swz(row)) << 4);
       dma16_stream(kb, off, slot + 1024 * j);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int row = 8 * j + (lane >> 3);
-      const uint32_t off = (uint32_t)(min<int64_t>(t0 + row, a.capacity - 1) * D) + (((lane & 7) ^ swz(row)) << 4);
+      const int row = 8 * j + (olane >> 3);
+      const uint32_t off = (uint32_t)(min<int64_t>(t0 + row, a.capacity - 1) * D) + (((olane & 7) ^ swz(row)) << 4);
       dma16_stream(vb, off, slot + HALF_CODE + 1024 * j);
     }
   }
