@@ -326,6 +326,52 @@ __device__ __forceinline__ void issue_half(const AttnArgs& a, int h, int64_t grp
   issue_half(a, h, grp, hf, slot, rs, hf == 0);
 }
 
+// The code rows of one tensor (K or V) of half `hf` of group `grp` (4 loads into `dst`), and a
+// group's rulers (4 loads into `rs`): issue_half in pieces, for the chained step's pipelined
+// loop, which reloads a K slot and a V slot at different times.
+__device__ __forceinline__ void issue_rows(const uint8_t* codes, const AttnArgs& a, int h, int64_t grp, int hf,
+                                           uint32_t dst) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t0 = grp * GT + 32 * hf;
+  dst = __builtin_amdgcn_readfirstlane(dst);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // earlier reads of this slot are done
+  if (t0 + 32 <= a.capacity) {
+    const void* b = uniform_ptr(codes + ((int64_t)h * a.capacity + t0) * D);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16_stream(b, half_row_off(lane, j), dst + 1024 * j);
+  } else {
+    const void* b = uniform_ptr(codes + (int64_t)h * a.capacity * D);
+    const int olane = tail_tid() & 63;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = 8 * j + (olane >> 3);
+      const uint32_t off = (uint32_t)(min<int64_t>(t0 + row, a.capacity - 1) * D) + (((olane & 7) ^ swz(row)) << 4);
+      dma16_stream(b, off, dst + 1024 * j);
+    }
+  }
+}
+__device__ __forceinline__ void issue_rulers(const AttnArgs& a, int h, int64_t grp, uint32_t rs) {
+  const int lane = threadIdx.x & 63;
+  rs = __builtin_amdgcn_readfirstlane(rs);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  const int64_t ro = ((int64_t)h * a.ngroups_cap + grp) * D;
+  const uint32_t roff = (uint32_t)(8 * (lane & 15)) * 2;
+  const int which = lane >> 4;
+  if (which == 0) dma16_stream(uniform_ptr(a.kst + ro), roff, rs);
+  if (which == 1) dma16_stream(uniform_ptr(a.kmn + ro), roff, rs);
+  if (which == 2) dma16_stream(uniform_ptr(a.vst + ro), roff, rs);
+  if (which == 3) dma16_stream(uniform_ptr(a.vmn + ro), roff, rs);
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in {0, 4, 8, 12, 16}
+__device__ __forceinline__ void vm_wait_n(int n) {
+  if (n <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if (n == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else if (n == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else if (n == 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+}
+
 // The per-token symmetric format's half group: 32 K and 32 V code rows (4 + 4 loads) into
 // the slot, then the 32 K and 32 V scales of those tokens (one load each, 4 lanes).
 // Token rows stay below the capacity (a multiple of 64 in this format).
@@ -627,6 +673,91 @@ __device__ __forceinline__ void attend_block(const AttnArgs& a, WaveState& st, c
       }
     }
   }
+}
+
+// The two halves of attend_block<1> for a full half (32 valid tokens), so that a caller can put
+// one half's PV product and the next half's QK product in one basic block, where the compiler
+// interleaves them (the chained step's software-pipelined loop).
+// S[b][i]: q.k of token 16b + 4g + i and head c (the layout softmax_step takes).
+__device__ __forceinline__ void qk_half(const uint8_t* kc, const uint8_t* rul, const half8_t (&qb)[4], float (&s)[2][4]) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  uint4 kst4[2][2], kmn4[2][2];
+  load_k_rulers(rul, kst4, kmn4);
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    float4_t S = float4_t{0.f, 0.f, 0.f, 0.f};
+    const int row = 16 * b + c;
+    const int key = swz(row);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const uint4 kw = *reinterpret_cast<const uint4*>(kc + row * D + (((g + 4 * hh) ^ key) << 4));
+      S = mfma32(dq8(kw.x, kw.y, kst4[hh][0], kmn4[hh][0]), qb[2 * hh], S);
+      S = mfma32(dq8(kw.z, kw.w, kst4[hh][1], kmn4[hh][1]), qb[2 * hh + 1], S);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[b][i] = S[i];
+  }
+}
+
+// O += P V for a full half: V codes at `vc`, the lane's V rulers in `ru` (the product of
+// attend_block<1> for nvalid = 32).
+__device__ __forceinline__ void pv_half(WaveState& st, const uint8_t* vc, const LaneRulers& ru, const half8_t& phi,
+                                        const half8_t& plo) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  const int r = c >> 1;
+  const int row = 16 * (r >> 2) + 4 * g + (r & 3);
+  u32x2 vw[8];
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb)
+    vw[cb] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                 (lds_v2i_t*)(const lds_void_t*)(vc + row * D + 8 * (c & 1) + ((cb ^ swz(row)) << 4))));
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb) {
+    const half8_t vb = dq8_splat(vw[cb].x, vw[cb].y, ru.vsp[cb], ru.vmp[cb]);
+    st.acc[cb] = mfma32(phi, vb, st.acc[cb]);
+    st.acc[cb] = mfma32(plo, vb, st.acc[cb]);
+  }
+}
+
+// PV of one full half fused with QK of the next: all LDS reads first, then each of the 8
+// V column blocks (dequantize + 2 MFMA) alternates with one of the 8 K operand pieces
+// (dequantize + 1 MFMA, the two token blocks' chains alternating), so that the matrix core and
+// the VALU each have independent work in flight.
+__device__ __forceinline__ void pv_qk_half(WaveState& st, const uint8_t* vc, const LaneRulers& ru, const half8_t& phi,
+                                           const half8_t& plo, const uint8_t* kc, const uint8_t* rul,
+                                           const half8_t (&qb)[4], float (&s)[2][4]) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  const int r = c >> 1;
+  const int vrow = 16 * (r >> 2) + 4 * g + (r & 3);
+  u32x2 vw[8];
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb)
+    vw[cb] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                 (lds_v2i_t*)(const lds_void_t*)(vc + vrow * D + 8 * (c & 1) + ((cb ^ swz(vrow)) << 4))));
+  uint4 kst4[2][2], kmn4[2][2];
+  load_k_rulers(rul, kst4, kmn4);
+  uint4 kw[2][2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int row = 16 * b + c;
+      kw[b][hh] = *reinterpret_cast<const uint4*>(kc + row * D + (((g + 4 * hh) ^ swz(row)) << 4));
+    }
+  float4_t S[2] = {float4_t{0.f, 0.f, 0.f, 0.f}, float4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const half8_t vb = dq8_splat(vw[i].x, vw[i].y, ru.vsp[i], ru.vmp[i]);
+    st.acc[i] = mfma32(phi, vb, st.acc[i]);
+    st.acc[i] = mfma32(plo, vb, st.acc[i]);
+    const int b = i & 1, j = i >> 1, hh = j >> 1, e = j & 1;
+    const uint32_t w0 = e ? kw[b][hh].z : kw[b][hh].x, w1 = e ? kw[b][hh].w : kw[b][hh].y;
+    S[b] = mfma32(dq8(w0, w1, kst4[hh][e], kmn4[hh][e]), qb[2 * hh + e], S[b]);
+  }
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[b][i] = S[b][i];
 }
 
 // fp16(code * scale) for 8 signed codes sharing one fp16 scale, and for 8 codes with one
@@ -2266,16 +2397,16 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
     state_init(st);
     half8_t qb[4];
     load_q_lds(q_lds, gq, qb);
-    int rs = 0;  // ruler set of the group in the slots
-    for (int gi = wave; gi < whole; gi += WAVES, rs ^= 1) {
-      const int64_t grp = gs + gi;
-      const uint8_t* rul = my_stages + 2 * HALF_SLOT + rs * RULER_BYTES;
-      const uint8_t* slot1 = my_stages + slot_bytes;
-      const bool nx_whole = gi + WAVES < whole, nx_extra = !nx_whole && has_x;
-      const int nv1 = (int)min<int64_t>(32, U - grp * GT), nv2 = (int)min<int64_t>(32, U - grp * GT - 32);
-      // first half (slot 0; the second half may still be in flight), then the next item's first
-      // loads into slot 0 (the next group's half 0 and rulers, or the extra half and its rulers)
-      if constexpr (TOK) {
+    if constexpr (TOK) {
+      int rs = 0;  // ruler set of the group in the slots
+      for (int gi = wave; gi < whole; gi += WAVES, rs ^= 1) {
+        const int64_t grp = gs + gi;
+        const uint8_t* rul = my_stages + 2 * HALF_SLOT + rs * RULER_BYTES;
+        const uint8_t* slot1 = my_stages + slot_bytes;
+        const bool nx_whole = gi + WAVES < whole, nx_extra = !nx_whole && has_x;
+        const int nv1 = (int)min<int64_t>(32, U - grp * GT), nv2 = (int)min<int64_t>(32, U - grp * GT - 32);
+        // first half (slot 0; the second half may still be in flight), then the next item's first
+        // loads into slot 0 (the next group's half 0 and rulers, or the extra half and its rulers)
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_HALF_TOK) : "memory");
         attend_block_tok(la, st, qb, my_stages, my_stages + HALF_CODE,
                          reinterpret_cast<const uint16_t*>(my_stages + 2 * HALF_CODE),
@@ -2288,34 +2419,67 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
           attend_block_tok(la, st, qb, slot1, slot1 + HALF_CODE, reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE),
                            reinterpret_cast<const uint16_t*>(slot1 + 2 * HALF_CODE + TOK_SCALE_BYTES), nv2);
         if (nx_whole) issue_tok<false>(la, 0, h, grp + WAVES, 1, my_lds + HALF_SLOT_TOK);
-      } else {
-        LaneRulers ru;
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_SECOND_HALF) : "memory");
-        load_rulers(rul, ru);
-        attend_block<1>(la, st, qb, my_stages, my_stages + HALF_CODE, ru, nv1);
-        if (nx_whole) issue_half(la, h, grp + WAVES, 0, my_lds, rul_lds + (rs ^ 1) * RULER_BYTES);
-        else if (nx_extra) issue_extra(la, rs ^ 1);
-        if (nx_whole || nx_extra) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_FIRST_HALF) : "memory");
-        else wait_groups_all();
-        if (nv2 > 0) attend_block<1>(la, st, qb, slot1, slot1 + HALF_CODE, ru, nv2);
-        if (nx_whole) issue_half(la, h, grp + WAVES, 1, my_lds + HALF_SLOT, 0u);
       }
-    }
-    if (has_x) {
-      // the extra half, in slot 0 with its rulers in set rs (issued by the last whole group, or
-      // by issue_first when the wave has none)
-      const int nvx = (int)max<int64_t>(0, min<int64_t>(32, U - xg * GT - 32 * xh));
-      wait_groups_all();
-      if (nvx > 0) {
-        if constexpr (TOK) {
+      if (has_x) {
+        // the extra half, in slot 0 with its rulers in set rs (issued by the last whole group, or
+        // by issue_first when the wave has none)
+        const int nvx = (int)max<int64_t>(0, min<int64_t>(32, U - xg * GT - 32 * xh));
+        wait_groups_all();
+        if (nvx > 0) {
           attend_block_tok(la, st, qb, my_stages, my_stages + HALF_CODE,
                            reinterpret_cast<const uint16_t*>(my_stages + 2 * HALF_CODE),
                            reinterpret_cast<const uint16_t*>(my_stages + 2 * HALF_CODE + TOK_SCALE_BYTES), nvx);
-        } else {
-          LaneRulers ru;
-          load_rulers(my_stages + 2 * HALF_SLOT + rs * RULER_BYTES, ru);
-          attend_block<1>(la, st, qb, my_stages, my_stages + HALF_CODE, ru, nvx);
         }
+      }
+    } else {
+      // ---- int8t64 (here every half is full: U is a multiple of 64), software-pipelined over
+      // the wave's halves k = 0 .. nh - 1 (its whole groups' halves, then its extra half). Half
+      // k has its K codes in K slot k % 2, its V codes in V slot k % 2 and its group's rulers in
+      // set (item of k) % 2. Region k holds PV(k) and QK(k + 1) in one basic block, which the
+      // compiler interleaves; after it V slot k % 2 takes V(k + 2) and K slot (k + 1) % 2 takes
+      // K(k + 3) (with its group's rulers when it starts an item), both read two regions later.
+      const int nwh = wave < whole ? 2 * ((whole - 1 - wave) / WAVES + 1) : 0;
+      const int nh = nwh + (has_x ? 1 : 0);
+      auto hgrp = [&](int k) { return k < nwh ? gs + wave + (int64_t)WAVES * (k >> 1) : xg; };
+      auto hhf = [&](int k) { return k < nwh ? (k & 1) : xh; };
+      auto hset = [&](int k) { return (k < nwh ? (k >> 1) : (nwh >> 1)) & 1; };
+      auto hstart = [&](int k) { return k >= nwh || (k & 1) == 0; };
+      auto kslot = [&](int k) { return my_stages + (k & 1) * HALF_SLOT; };
+      auto rset = [&](int k) { return my_stages + 2 * HALF_SLOT + hset(k) * RULER_BYTES; };
+      // the loads issued (counted for the waits: 0, 4 or 8, and 0 or 4)
+      auto issue_k = [&](int k) -> int {
+        if (k >= nh) return 0;
+        issue_rows(la.kq, la, h, hgrp(k), hhf(k), my_lds + (k & 1) * HALF_SLOT);
+        if (!hstart(k)) return 4;
+        issue_rulers(la, h, hgrp(k), rul_lds + hset(k) * RULER_BYTES);
+        return 8;
+      };
+      auto issue_v = [&](int k) -> int {
+        if (k >= nh) return 0;
+        issue_rows(la.vq, la, h, hgrp(k), hhf(k), my_lds + (k & 1) * HALF_SLOT + HALF_CODE);
+        return 4;
+      };
+      if (nh > 0) {
+        // the prefetched first item (K0 V0 R0, then K1 V1 when it has two halves): QK(0) needs
+        // K0 and R0
+        vm_wait_n(nh >= 2 && !hstart(1) ? DMA_SECOND_HALF : 0);
+        float s[2][4];
+        half8_t phi[1], plo[1];
+        qk_half(kslot(0), rset(0), qb, s);
+        int pend = issue_k(2);
+        softmax_step<1>(st, s, la.sl2, phi, plo, gq);
+        LaneRulers ru;
+        for (int k = 0; k + 1 < nh; ++k) {
+          vm_wait_n(pend);  // V(k), K(k + 1) and its rulers have landed
+          if (hstart(k)) load_rulers(rset(k), ru);
+          pv_qk_half(st, kslot(k) + HALF_CODE, ru, phi[0], plo[0], kslot(k + 1), rset(k + 1), qb, s);
+          pend = issue_v(k + 2);
+          pend += issue_k(k + 3);
+          softmax_step<1>(st, s, la.sl2, phi, plo, gq);
+        }
+        vm_wait_n(pend);
+        if (hstart(nh - 1)) load_rulers(rset(nh - 1), ru);
+        pv_half(st, kslot(nh - 1) + HALF_CODE, ru, phi[0], plo[0]);
       }
     }
 
