@@ -71,9 +71,7 @@ constexpr int DMA_FIRST_HALF_PAGED = 2 * (HALF_CODE / 1024) + 1;  // the rulers 
 // K scales (64 fp16) | V scales
 constexpr int PAGE_TOK_BYTES = 2 * CODE_BYTES + 2 * GT * 2;  // 16640, a multiple of 128
 enum Layout : int { CONTIG_T64 = 0, CONTIG_TOK = 1, PAGED_T64 = 2, PAGED_TOK = 3 };
-constexpr float P_SCALE = 32768.0f;       // 2^15
-constexpr float P_SCALE_LOG2 = 15.0f;
-constexpr float INV_P_SCALE = 1.0f / 32768.0f;
+constexpr float P_SCALE_LOG2 = 15.0f;  // the softmax weights carry a factor 2^15
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 constexpr float NEG_INF = -__builtin_huge_valf();
@@ -1896,7 +1894,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) float xch[UNIT_CH * 2 * WAVES];
   __shared__ int ticket;
   float* lds = reinterpret_cast<float*>(lds_raw);
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.x % a.hkv;
   // work unit -> (sequence, part of its prefix, parts of that sequence, partial slot)
@@ -2257,7 +2255,7 @@ __device__ __forceinline__ bool merger_layer(const AttnArgs& args, const void* l
   __shared__ int lost_sh;
   const int tid = tail_tid(), wave = tid >> 6;
   AttnArgs la = args;
-  const int P = la.n_parts, pw = part_stride(la.gq), gq = la.gq;
+  const int gq = la.gq;
   TailSmem& sm = *reinterpret_cast<TailSmem*>(lds_raw);
   // q, k_new and v_new all views of layer l - 1's output: forwarded, no counter wait
   bool fwd = false;
@@ -2401,7 +2399,6 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
       int rs = 0;  // ruler set of the group in the slots
       for (int gi = wave; gi < whole; gi += WAVES, rs ^= 1) {
         const int64_t grp = gs + gi;
-        const uint8_t* rul = my_stages + 2 * HALF_SLOT + rs * RULER_BYTES;
         const uint8_t* slot1 = my_stages + slot_bytes;
         const bool nx_whole = gi + WAVES < whole, nx_extra = !nx_whole && has_x;
         const int nv1 = (int)min<int64_t>(32, U - grp * GT), nv2 = (int)min<int64_t>(32, U - grp * GT - 32);
@@ -2676,9 +2673,10 @@ struct PrefillArgs {
 // 16b + 4g + i, row c; -inf where masked): m is a reference maximum in the log2 domain, within
 // PF_TAU below the row's maximum of S * sl2, and P comes out as exp2(S sl2 - m + 15 - PF_TAU)
 // <= 2^15 in two fp16 A operands (tokens of blocks 0,1 and 2,3). l accumulates the same scaled
-// weights, so acc / l needs no rescaling; acc and l are rescaled only when m moves.
-__device__ __forceinline__ void pf_softmax(WaveState& st, const float (&S)[4][4], float sl2, half8_t (&ph)[2]) {
-  const int lane = threadIdx.x & 63, g = lane >> 4;
+// weights, so acc / l needs no rescaling; l is rescaled here and acc by pf_rescale (the caller
+// runs it before the next PV product), both only when m moves.
+__device__ __forceinline__ void pf_softmax(WaveState& st, const float (&S)[4][4], float sl2, half8_t (&ph)[2],
+                                           float& alpha_out, bool& moved_out) {
   float smax = NEG_INF;
 #pragma unroll
   for (int b = 0; b < 4; ++b)
@@ -2706,8 +2704,13 @@ __device__ __forceinline__ void pf_softmax(WaveState& st, const float (&S)[4][4]
   for (int B = 0; B < 2; ++B)
     ph[B] = half8_t{p16[B][0], p16[B][1], p16[B][2], p16[B][3], p16[B][4], p16[B][5], p16[B][6], p16[B][7]};
   st.l = st.l * alpha + sum4rows(lsum);
-  const bool moved = st.m != m_new;
+  moved_out = st.m != m_new;
+  alpha_out = alpha;
   st.m = m_new;
+}
+// the accumulator rescale that goes with pf_softmax, when any row's reference maximum moved
+__device__ __forceinline__ void pf_rescale(WaveState& st, float alpha, bool moved) {
+  const int g = (threadIdx.x & 63) >> 4;
   if (__builtin_amdgcn_ballot_w64(moved) == 0) return;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -2777,17 +2780,19 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
     for (int rb = 0; rb < PF_RB; ++rb)
 #pragma unroll
       for (int b = 0; b < 4; ++b) S[rb][b] = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const half8_t ka = *reinterpret_cast<const half8_t*>(ktile + (16 * b + c) * PF_KROW + 16 * g + 64 * (k >> 1) + 8 * (k & 1));
-#pragma unroll
-        for (int rb = 0; rb < PF_RB; ++rb) S[rb][b] = mfma32(ka, qb[rb][k], S[rb][b]);
-      }
     half8_t ph[PF_RB][2];
+    float alpha[PF_RB];
+    bool moved[PF_RB];
+    auto qk = [&](int rb) {
 #pragma unroll
-    for (int rb = 0; rb < PF_RB; ++rb) {
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const half8_t ka = *reinterpret_cast<const half8_t*>(ktile + (16 * b + c) * PF_KROW + 16 * g + 64 * (k >> 1) + 8 * (k & 1));
+          S[rb][b] = mfma32(ka, qb[rb][k], S[rb][b]);
+        }
+    };
+    auto softmax = [&](int rb) {
       float sc[4][4];
       const int tq = (row0 + 16 * rb + c) / a.gq;  // query token of row c (score column)
 #pragma unroll
@@ -2799,16 +2804,28 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
         }
       // rows of the S^T layout are q rows c; the causal test above needs the row of column
       // c, which is lane-independent of g: scores of lane (c, g) all belong to row c
-      pf_softmax(st[rb], sc, a.sl2, ph[rb]);
-    }
+      pf_softmax(st[rb], sc, a.sl2, ph[rb], alpha[rb], moved[rb]);
+    };
+    auto pv = [&](int rb) {
 #pragma unroll
-    for (int B = 0; B < 2; ++B)
+      for (int B = 0; B < 2; ++B)
 #pragma unroll
-      for (int cb = 0; cb < 8; ++cb) {
-        const half8_t vb = *reinterpret_cast<const half8_t*>(vtile + (16 * cb + c) * PF_VROW + 32 * B + 8 * g);
-#pragma unroll
-        for (int rb = 0; rb < PF_RB; ++rb) st[rb].acc[cb] = mfma32(ph[rb][B], vb, st[rb].acc[cb]);
-      }
+        for (int cb = 0; cb < 8; ++cb) {
+          const half8_t vb = *reinterpret_cast<const half8_t*>(vtile + (16 * cb + c) * PF_VROW + 32 * B + 8 * g);
+          st[rb].acc[cb] = mfma32(ph[rb][B], vb, st[rb].acc[cb]);
+        }
+    };
+    // QK(1) beside softmax(0), PV(0) beside softmax(1): the matrix core and the VALU each have
+    // the other row block's work (the rescales, rare, between)
+    static_assert(PF_RB == 2, "two row blocks per wave");
+    qk(0);
+    qk(1);
+    softmax(0);
+    pf_rescale(st[0], alpha[0], moved[0]);
+    pv(0);
+    softmax(1);
+    pf_rescale(st[1], alpha[1], moved[1]);
+    pv(1);
   };
 
   // ---- cache groups: double-buffered LDS stages, dequantized once into the fp16 tiles
