@@ -64,15 +64,16 @@ def _assert_state(cache, oracle, layers: int):
     assert int(cache._pg.item()) == oracle.pg
 
 
-@pytest.mark.parametrize("n_parts", [0, 3])
-def test_chain_t64_against_oracle(n_parts):
-    """3 chained layers, prefill 250, then 72 steps across the group boundaries at 256 and 320:
-    every layer's output against the oracle on its own inputs, state bit for bit."""
+@pytest.mark.parametrize("n_parts,L,n0,steps,cap", [(0, 3, 250, 72, 512), (3, 3, 250, 72, 512), (3, 2, 1750, 48, 2048)])
+def test_chain_t64_against_oracle(n_parts, L, n0, steps, cap):
+    """Chained layers from a prefill of n0 tokens, then steps across group boundaries (250: the
+    boundaries at 256 and 320, one or two halves per wave; 1750 over 3 parts: 9 and then 10
+    groups per part, so that waves take two or three halves): every layer's output against the
+    oracle on its own inputs, state bit for bit."""
     from nova_amd.chain import ChainedStep
     from nova_amd.kvattn import KVInt8Cache
 
-    print(f"case chain t64 n_parts={n_parts}", flush=True)
-    L, n0, steps, cap = 3, 250, 72, 512
+    print(f"case chain t64 n_parts={n_parts} L={L} n0={n0} steps={steps}", flush=True)
     cache = KVInt8Cache(num_slots=L, num_kv_heads=H_KV, head_dim=D, max_len=cap, num_q_heads=HQ)
     ref = ostream.StreamCache(L, H_KV, D, cap, HQ)
     _prefill_t64(cache, L, n0, seed=40, oracle=ref)
