@@ -174,14 +174,17 @@ def test_chain_graph_replay_equals_eager():
         assert torch.equal(getattr(caches[0], nm), getattr(caches[1], nm)), nm
 
 
-def test_chain_tok_against_oracle():
-    """Per-token symmetric caches, 2 chained layers, prefill 190 then 70 steps: codes and scales
-    of every token bit for bit against the quantizer oracle, every output against the oracle."""
+@pytest.mark.parametrize("n_parts,n0,steps,cap", [(0, 190, 70, 320), (3, 1750, 48, 2048), (1, 1200, 40, 1280)])
+def test_chain_tok_against_oracle(n_parts, n0, steps, cap):
+    """Per-token symmetric caches, 2 chained layers, a prefill of n0 tokens and then steps that
+    end at every offset within a group (190: one half per wave; 1750 over 3 parts: two or three
+    halves per wave; 1200 in one part: four or five): codes and scales of every token bit for
+    bit against the quantizer oracle, every output against the oracle."""
     from nova_amd.chain import ChainedStep
     from nova_amd.kvtok import KVInt8TokCache
 
-    print("case chain tok", flush=True)
-    L, n0, steps, cap = 2, 190, 70, 320
+    print(f"case chain tok n_parts={n_parts} n0={n0} steps={steps}", flush=True)
+    L = 2
     cache = KVInt8TokCache(L, H_KV, D, cap, HQ)
     cache.begin_prefill(n0)
     cache.set_prefill_pos(0)
@@ -194,7 +197,7 @@ def test_chain_tok_against_oracle():
         vs_all.append([npy(v)[0]])
     cache.finish_prefill(n0)
     outs = randn((L, 1, HQ, 1, D), 76, scale=0.5).cuda()
-    chain = ChainedStep(cache, *_chain_views(outs, L))
+    chain = ChainedStep(cache, *_chain_views(outs, L), n_parts=n_parts)
     for s in range(steps):
         prev = npy(outs)
         chain()
