@@ -347,7 +347,7 @@ def run_decode(args, scheme: str, headline: bool, mode: str = "chain") -> dict:
     if mode == "chain":
         ins = [layer_inputs(layer) for layer in range(L)]
         chain = ChainedStep(cache, [i[0] for i in ins], [i[1] for i in ins], [i[2] for i in ins],
-                            [outs[layer] for layer in range(L)])
+                            [outs[layer] for layer in range(L)], n_parts=args.parts)
 
         def launches():
             chain()
