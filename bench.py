@@ -2,29 +2,34 @@
 
 Headline workload (the long-context decode configuration): 36 layers x (32 q heads, 8 KV heads,
 head_dim 128), batch 1, int8t64 KV cache prefilled to 32768 tokens from seeded N(0,1) fp16 K/V
-with 4 random K channels per head scaled x8. One decode step = for each layer one fused append +
-attention launch (``KVInt8Cache.update_attend``), then ``pos += 1``. The layers are chained as in
-a model: layer l's query and its new K/V token are views of layer l-1's attention output (q = the
-whole output, k = q heads 0, 4, .., v = q heads 1, 5, ..), and layer 0 reads the previous step's
-last output, so no launch can start before the previous one has finished. The step is captured
-once as a hipGraph; W untimed replays, then K timed replays bracketed by
-``torch.cuda.synchronize()`` and HIP events on the replay stream.
+with 4 random K channels per head scaled x8. One decode step = every layer's append + attention
+in one chained launch (``ChainedStep``, ``nkv_decode_layers_t64``), then ``pos += 1``. The
+layers are chained as in a model: layer l's query and its new K/V token are views of layer l-1's
+attention output (q = the whole output, k = q heads 0, 4, .., v = q heads 1, 5, ..; layer 0 reads
+the previous step's last output), and with the default ``--dep all`` no input of layer l is read
+before every KV head of layer l-1 has finished (the all-head dependency of a model, where every
+q head of layer l depends on every head of layer l-1 through o_proj). The step is captured once
+as a hipGraph; W untimed replays, then K timed replays bracketed by ``torch.cuda.synchronize()``
+and HIP events on the replay stream; afterwards the launch's error word is checked.
 
 One JSON line (the driver's contract). ``value`` = decode tokens/s of the whole job.
-``roofline`` is the fused decode-step launch the step runs (``attn_prefix_kernel<0>``: append,
-split-K partials, last-workgroup tail): algorithmic bytes per launch / its average duration,
-timed with HIP events over K replays of a graph of the 36 chained launches of one step.
-``traffic`` comes from the committed rocprofv3 --pmc summary of that kernel (FETCH_SIZE +
-WRITE_SIZE per dispatch, each scaled by what the counter reads for the library's copy kernel of
-known size). ``cpu_baseline`` times the repo's torch fp32 restatement of the reference algorithm
-(dequantize the int8 prefix, append the ring, repeat KV heads, softmax attention) on the host
-cores for one layer and a few steps, scaled to the 36-layer step. ``gpu_clock`` is read with
-amd-smi while the step graph replays. ``workloads`` carries the other configurations measured in
-the same run: the per-token symmetric format, the paged ragged batch, the MFMA chunked prefill.
+``roofline`` is the chained launch: algorithmic bytes per launch / its average duration, timed
+with HIP events over K replays of a graph of the launch alone. ``traffic`` comes from the
+committed rocprofv3 --pmc summary of that kernel (FETCH_SIZE + WRITE_SIZE per dispatch, each
+scaled by what the counter reads for the library's copy kernel of known size). ``cpu_baseline``
+times the repo's torch fp32 restatement of the reference algorithm (dequantize the int8 prefix,
+append the ring, repeat KV heads, softmax attention) on the host cores for one layer and a few
+steps, scaled to the 36-layer step. ``gpu_clock`` is read with amd-smi while the step graph
+replays. ``workloads`` carries the other configurations measured in the same run: the per-head
+dependency, one launch per layer (what a model's layer loop calls), the per-token symmetric
+format, the paged ragged batch, the MFMA chunked prefill, the read ceiling of the decode path's
+load pattern and the end-to-end random-weight decoder.
 
     python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu-baseline] [--only]
-    python bench.py --workload decode|paged|prefill|e2e [--scheme t64|tok]   # one workload alone
-    python bench.py --traffic-from FETCH_DIR WRITE_DIR [--scheme tok]      # summarize --pmc runs
+    python bench.py --workload decode|paged|prefill|e2e|read [--scheme t64|tok] [--mode chain|layers]
+                    [--dep all|head]                                        # one workload alone
+    python bench.py --traffic-from FETCH_DIR WRITE_DIR --traffic-key KEY    # summarize --pmc runs
+    python bench.py --stats-from OUT_DIR --stats-name NAME --stats-cmd CMD  # summarize a --stats run
 """
 
 from __future__ import annotations
@@ -51,12 +56,24 @@ COPY_BYTES = 64 << 20
 APPEND_BYTES = 64 * 128 * 2 * 2 * HKV + 2 * 2 * 128 * 2 * HKV + 64 * 128 * 2 * HKV + 4 * 128 * 2 * HKV
 # the per-token symmetric append: the new token read, its codes and scale written
 APPEND_BYTES_TOK = 2 * 128 * 2 * HKV + 2 * 128 * HKV + 2 * 2 * HKV
-STEP_KERNEL = {"chain": "attn_layers_kernel", "layers": "attn_prefix_kernel"}
 COPY_KERNEL = "copy16_kernel"
-TRAFFIC = {("t64", "layers"): ROOT / "profiles" / "decode_step_32k_traffic.txt",
-           ("tok", "layers"): ROOT / "profiles" / "decode_step_tok_32k_traffic.txt",
-           ("t64", "chain"): ROOT / "profiles" / "decode_chain_32k_traffic.txt",
-           ("tok", "chain"): ROOT / "profiles" / "decode_chain_tok_32k_traffic.txt"}
+PROFILES = ROOT / "profiles"
+# traffic summaries: key -> (file, the kernel's name in rocprof's CSV, the command profiled)
+_DEC = "python3 bench.py --workload decode --steps 4 --warmup 1 --no-cpu-baseline --no-clock"
+TRAFFIC = {
+    "chain_t64": (PROFILES / "decode_chain_32k_traffic.txt", "attn_layers_kernel<0>", _DEC + " --mode chain"),
+    "chain_tok": (PROFILES / "decode_chain_tok_32k_traffic.txt", "attn_layers_kernel<1>",
+                  _DEC + " --mode chain --scheme tok"),
+    "layers_t64": (PROFILES / "decode_step_32k_traffic.txt", "attn_prefix_kernel<0>", _DEC + " --mode layers"),
+    "layers_tok": (PROFILES / "decode_step_tok_32k_traffic.txt", "attn_prefix_kernel<1>",
+                   _DEC + " --mode layers --scheme tok"),
+    "paged_t64": (PROFILES / "paged_batch_decode_traffic.txt", "attn_prefix_kernel<2>",
+                  "python3 bench.py --workload paged --steps 4 --warmup 1 --no-clock"),
+    "paged_tok": (PROFILES / "paged_batch_decode_tok_traffic.txt", "attn_prefix_kernel<3>",
+                  "python3 bench.py --workload paged --scheme tok --steps 4 --warmup 1 --no-clock"),
+    "prefill": (PROFILES / "prefill_chunk_512_over_16k_traffic.txt", "prefill_chunk_kernel",
+                "python3 bench.py --workload prefill --steps 4 --warmup 1 --no-clock"),
+}
 VOCAB_QWEN3_4B = 151936
 
 
@@ -94,14 +111,22 @@ def parse_args():
     ap.add_argument("--only", action="store_true", help="the headline workload alone (no extra workloads)")
     ap.add_argument("--no-clock", action="store_true", help="skip the amd-smi clock reading")
     ap.add_argument("--chunk", type=int, default=2048, help="e2e: streamed prefill chunk (a multiple of 64)")
-    ap.add_argument("--workload", choices=("decode", "paged", "prefill", "e2e"), default=None,
+    ap.add_argument("--workload", choices=("decode", "paged", "prefill", "e2e", "read"), default=None,
                     help="run one workload alone and print its line")
     ap.add_argument("--scheme", choices=("t64", "tok"), default="t64",
                     help="--workload decode: KV format, int8t64 (the reference's) or per-token symmetric")
     ap.add_argument("--mode", choices=("chain", "layers"), default="chain",
                     help="--workload decode: every layer in one launch (chain) or one launch per layer")
+    ap.add_argument("--dep", choices=("all", "head"), default="all",
+                    help="--mode chain: every layer waits for every head of the layer before (all), or forwarded "
+                         "inputs wait only for their own head (head)")
+    ap.add_argument("--e2e-steps", type=int, default=32, help="steps of the end-to-end workload in the default run")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
-                    help="summarize two rocprofv3 --pmc runs of the decode workload into the traffic file")
+                    help="summarize two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into a traffic file")
+    ap.add_argument("--traffic-key", choices=sorted(TRAFFIC), default="chain_t64")
+    ap.add_argument("--stats-from", metavar="OUT_DIR", help="summarize a rocprofv3 --kernel-trace --stats run")
+    ap.add_argument("--stats-name", help="--stats-from: the summary's file name under profiles/")
+    ap.add_argument("--stats-cmd", help="--stats-from: the command that was profiled")
     return ap.parse_args()
 
 
@@ -128,49 +153,70 @@ def _pmc_means(run_dir: str, counter: str, kernel: str) -> dict:
     return {k: sum(v) / len(v) for k, v in acc.items()}
 
 
-def write_traffic(fetch_dir: str, write_dir: str, scheme: str, mode: str) -> None:
-    """HBM bytes per dispatch of the decode-step kernel (the chained launch, or one layer's fused
-    launch) from FETCH_SIZE and WRITE_SIZE (KiB), each scaled by the factor that makes the same
-    counter read the copy kernel's known bytes."""
-    kernel = STEP_KERNEL[mode]
+def write_traffic(fetch_dir: str, write_dir: str, key: str) -> None:
+    """HBM bytes per dispatch of the workload's dominant kernel from FETCH_SIZE and WRITE_SIZE
+    (KiB), each scaled by the factor that makes the same counter read the copy kernel's known
+    bytes."""
+    path, kernel, cmd = TRAFFIC[key]
     fetch, write = _pmc_means(fetch_dir, "FETCH_SIZE", kernel), _pmc_means(write_dir, "WRITE_SIZE", kernel)
     f_scale = COPY_BYTES / (fetch[COPY_KERNEL] * 1024)
     w_scale = COPY_BYTES / (write[COPY_KERNEL] * 1024)
     f_bytes = fetch[kernel] * 1024 * f_scale
     w_bytes = write[kernel] * 1024 * w_scale
-    alg = step_launch_bytes(CTX + 1, scheme) * (LAYERS if mode == "chain" else 1)
-    flags = (" --scheme tok" if scheme == "tok" else "") + f" --mode {mode}"
-    cmd = f"python3 bench.py --workload decode{flags} --steps 4 --warmup 1 --no-cpu-baseline --no-clock"
-    what = (f"the chained decode step nkv::attn_layers_kernel<{1 if scheme == 'tok' else 0}> ({LAYERS} layers "
-            "in one launch)" if mode == "chain" else
-            f"the fused decode-step launch nkv::attn_prefix_kernel<{1 if scheme == 'tok' else 0}> (one layer)")
     lines = [
-        f"# HBM traffic of {what}, "
-        f"{'per-token symmetric' if scheme == 'tok' else 'int8t64'} format, 32k context, 32 q / 8 kv heads",
-        "# made by (two rocprofv3 --pmc runs of the decode workload, then this summary):",
+        f"# HBM traffic per dispatch of nkv::{kernel} ({key})",
+        "# made by (two rocprofv3 --pmc runs of the workload, then this summary; from the repository root):",
         f"#   rocprofv3 --pmc FETCH_SIZE -d FETCH_DIR -o run --output-format csv -- {cmd}",
         f"#   rocprofv3 --pmc WRITE_SIZE -d WRITE_DIR -o run --output-format csv -- {cmd}",
-        f"#   python3 bench.py --traffic-from FETCH_DIR WRITE_DIR{flags}",
+        f"#   python3 bench.py --traffic-from FETCH_DIR WRITE_DIR --traffic-key {key}",
         f"copy_kernel_bytes: {COPY_BYTES}  (read, and again written, by nkv_copy_bytes)",
         f"copy_kernel_FETCH_SIZE_KiB: {fetch[COPY_KERNEL]:.1f}  -> fetch scale {f_scale:.4f}",
         f"copy_kernel_WRITE_SIZE_KiB: {write[COPY_KERNEL]:.1f}  -> write scale {w_scale:.4f}",
-        f"step_kernel_FETCH_SIZE_KiB: {fetch[kernel]:.1f}  -> {f_bytes:.0f} B",
-        f"step_kernel_WRITE_SIZE_KiB: {write[kernel]:.1f}  -> {w_bytes:.0f} B",
-        f"algorithmic_bytes_per_launch: {alg}",
+        f"kernel_FETCH_SIZE_KiB: {fetch[kernel]:.1f}  -> {f_bytes:.0f} B",
+        f"kernel_WRITE_SIZE_KiB: {write[kernel]:.1f}  -> {w_bytes:.0f} B",
         f"traffic_bytes_per_launch: {f_bytes + w_bytes:.0f}",
-        f"traffic_over_algorithmic: {(f_bytes + w_bytes) / alg:.4f}",
+        "(bench.py divides this by its own algorithmic bytes per launch: roofline.traffic_over_algorithmic)",
     ]
-    TRAFFIC[(scheme, mode)].write_text("\n".join(lines) + "\n")
+    path.write_text("\n".join(lines) + "\n")
     print("\n".join(lines))
 
 
-def read_traffic(scheme: str, mode: str):
-    """HBM bytes per launch of the decode-step kernel from the committed summary, or None."""
-    path = TRAFFIC[(scheme, mode)]
+def read_traffic(key: str):
+    """HBM bytes per launch of a workload's dominant kernel from the committed summary, or None."""
+    path = TRAFFIC[key][0]
     if not path.exists():
         return None
     m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text(), re.M)
     return float(m.group(1)) if m else None
+
+
+def write_stats(out_dir: str, name: str, cmd: str) -> None:
+    """A short summary of a rocprofv3 --kernel-trace --stats run: per kernel the calls and the
+    average, minimum, maximum and median duration, from the run's kernel trace."""
+    import csv
+    import statistics
+
+    traces = sorted(Path(out_dir).rglob("*kernel_trace.csv"))
+    if not traces:
+        raise SystemExit(f"no kernel_trace.csv under {out_dir}")
+    durs: dict = {}
+    for f in traces:
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                nm = row["Kernel_Name"]
+                durs.setdefault(nm, []).append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
+    total = sum(sum(v) for v in durs.values())
+    lines = [f"# rocprofv3 kernel trace summary ({name}); durations in ns",
+             "# made by (from the repository root, one MI355X):",
+             f"#   rocprofv3 --kernel-trace --stats -d OUT -o run --output-format csv -- {cmd}",
+             f"#   python3 bench.py --stats-from OUT --stats-name {name} --stats-cmd '{cmd}'",
+             f"{'kernel':<72} {'calls':>6} {'avg':>11} {'min':>9} {'max':>9} {'median':>11} {'share':>7}"]
+    for nm, v in sorted(durs.items(), key=lambda kv: -sum(kv[1])):
+        short = re.sub(r"\(.*", "", nm.replace("void ", ""))[:72]
+        lines.append(f"{short:<72} {len(v):>6} {sum(v) / len(v):>11.1f} {min(v):>9} {max(v):>9} "
+                     f"{statistics.median(v):>11.1f} {100 * sum(v) / total:>6.2f}%")
+    (PROFILES / name).write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
 
 
 # ---------------------------------------------------------------- host side: CPU baseline, clock
@@ -302,11 +348,42 @@ def _time_graph(graph, stream, reps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
-def run_decode(args, scheme: str, headline: bool, mode: str = "chain") -> dict:
+def _calibration_copy(dev) -> None:
+    """One launch of the library's copy kernel over a known byte count: the --pmc runs scale
+    FETCH_SIZE and WRITE_SIZE by what they read for it."""
+    import torch
+
+    from nova_amd import _lib
+
+    cal = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)
+    cal2 = torch.empty_like(cal)
+    _lib.call("nkv_copy_bytes", cal.data_ptr(), cal2.data_ptr(), cal.numel(), _lib.stream_ptr(dev))
+    torch.cuda.synchronize()
+    del cal, cal2
+
+
+def _roofline_hbm(launch_bytes: float, per_launch_s: float, key: str, kernel: str, n_launch: int) -> dict:
+    achieved = launch_bytes / per_launch_s / 1e9
+    traffic = read_traffic(key)
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "traffic_over_algorithmic": round(traffic / launch_bytes, 4) if traffic else None,
+            "kernel": kernel, "algorithmic_bytes_per_launch": round(launch_bytes),
+            "avg_launch_us": round(per_launch_s * 1e6, 3), "launches_per_step": n_launch}
+
+
+DEP_TEXT = {"all": "every input of layer l read after every KV head of layer l-1 has finished (a model's "
+                   "dependency: each q head of layer l depends on every head of layer l-1)",
+            "head": "layer l's inputs of KV head h read as soon as head h of layer l-1 has written them "
+                    "(each KV head's layers chain on their own)"}
+
+
+def run_decode(args, scheme: str, headline: bool, mode: str = "chain", dep: str = "all") -> dict:
     """The 36-layer, 32k-context chained decode step on the int8t64 (``t64``) or per-token
     symmetric (``tok``) cache; returns the result dict (the headline line when ``headline``).
-    ``mode`` "chain": every layer in one launch (``ChainedStep``, ``nkv_decode_layers_*``);
-    "layers": one fused launch per layer (``update_attend``, ``nkv_decode_step_*``)."""
+    ``mode`` "chain": every layer in one launch (``ChainedStep``, ``nkv_decode_layers_*``), with
+    the inter-layer dependency ``dep``; "layers": one fused launch per layer (``update_attend``,
+    ``nkv_decode_step_*``), each launch after the one before."""
     import torch
 
     from nova_amd.chain import ChainedStep
@@ -344,10 +421,11 @@ def run_decode(args, scheme: str, headline: bool, mode: str = "chain") -> dict:
         prev = outs[layer - 1]  # layer 0: the previous step's last layer
         return prev[:, 0::HQ // HKV], prev[:, 1::HQ // HKV], prev
 
+    chain = None
     if mode == "chain":
         ins = [layer_inputs(layer) for layer in range(L)]
         chain = ChainedStep(cache, [i[0] for i in ins], [i[1] for i in ins], [i[2] for i in ins],
-                            [outs[layer] for layer in range(L)], n_parts=args.parts)
+                            [outs[layer] for layer in range(L)], n_parts=args.parts, dep=dep)
 
         def launches():
             chain()
@@ -379,6 +457,8 @@ def run_decode(args, scheme: str, headline: bool, mode: str = "chain") -> dict:
     wall = time.perf_counter() - t_wall
     ms = e0.elapsed_time(e1)
     assert int(cache.pos.item()) == pos0 + K
+    if chain is not None:
+        chain.check()  # no wait gave up (every workgroup was resident)
     assert torch.isfinite(outs).all()
 
     # ---- the launches alone (pos fixed): the chained launch, or the step's 36 chained launches
@@ -387,16 +467,10 @@ def run_decode(args, scheme: str, headline: bool, mode: str = "chain") -> dict:
         launches()
     pos_l = int(cache.pos.item())
     ms_launches = _time_graph(g_launch, stream, K, W)
+    if chain is not None:
+        chain.check()
     clock = None if args.no_clock else clock_under_load(graph.replay)
-
-    # ---- traffic calibration copy (known byte count; the --pmc runs read its counters)
-    cal = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)
-    cal2 = torch.empty_like(cal)
-    from nova_amd import _lib
-
-    _lib.call("nkv_copy_bytes", cal.data_ptr(), cal2.data_ptr(), cal.numel(), _lib.stream_ptr(dev))
-    torch.cuda.synchronize()
-    del cal, cal2
+    _calibration_copy(dev)
 
     ms_step = ms / K
     us = [pos0 + i + 1 for i in range(K)]  # tokens written when each timed step attends
@@ -404,7 +478,6 @@ def run_decode(args, scheme: str, headline: bool, mode: str = "chain") -> dict:
     n_launch = 1 if mode == "chain" else L
     launch_bytes = step_launch_bytes(pos_l + 1, scheme) * (L // n_launch)
     per_launch_s = ms_launches / 1e3 / n_launch
-    achieved = launch_bytes / per_launch_s / 1e9
     kidx = 1 if scheme == "tok" else 0
     if mode == "chain":
         kname = (f"nkv::attn_layers_kernel<{kidx}> chained decode step ({L} layers x (append + split-K "
@@ -414,6 +487,8 @@ def run_decode(args, scheme: str, headline: bool, mode: str = "chain") -> dict:
                  "last-workgroup tail), one launch per layer")
     fmt = ("tok (int8 codes, one fp16 absmax scale per token and KV head)" if scheme == "tok"
            else "int8t64 (uint8 codes, fp16 min/step per 64 tokens per channel)")
+    how = (f"all layers in one launch, {'all-head' if dep == 'all' else 'per-head'} dependency between layers"
+           if mode == "chain" else "one launch per layer, each after the one before")
     res = {
         "metric": "int8-KV decode attention tokens/s + achieved HBM GB/s (% of peak) at 32k ctx",
         "value": round(K / (ms / 1e3), 2), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -421,25 +496,18 @@ def run_decode(args, scheme: str, headline: bool, mode: str = "chain") -> dict:
         "dtype": "fp16", "data": "synthetic",
         "config": {"workload": f"{'per-token symmetric int8' if scheme == 'tok' else 'int8t64'} KV decode step, "
                                f"{L} layers x (32 q / 8 kv heads, head_dim 128), batch 1, {ctx}-token prefilled "
-                               f"cache, layers chained through their outputs, {K} hipGraph-replayed steps, "
-                               f"{'all layers in one launch' if mode == 'chain' else 'one launch per layer'}",
+                               f"cache, layers chained through their outputs, {K} hipGraph-replayed steps, {how}",
                    "layers": L, "context": ctx, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "batch": 1,
                    "kv_format": fmt, "launch": mode,
+                   "dependency": DEP_TEXT[dep] if mode == "chain" else "each layer's launch after the layer before",
                    "parts_per_head": chain.n_parts if mode == "chain" else cache._n_parts},
         "step_gbs": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
         "step_pct_of_hbm_peak": round(100 * step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS, 2),
         "wall_s_timed": round(wall, 4),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(scheme, mode),
-                     "kernel": kname,
-                     "algorithmic_bytes_per_launch": round(launch_bytes),
-                     "avg_launch_us": round(per_launch_s * 1e6, 3),
-                     "launches_per_step": n_launch},
+        "roofline": _roofline_hbm(launch_bytes, per_launch_s, f"{mode}_{scheme}", kname, n_launch),
         "gpu_clock": clock,
     }
-    del graph, g_launch, cache, outs
-    if mode == "chain":
-        del chain
+    del graph, g_launch, cache, outs, chain
     torch.cuda.empty_cache()
     return res
 
@@ -493,15 +561,36 @@ def run_paged(args, steps: int | None = None, scheme: str = "t64") -> dict:
     assert torch.isfinite(cache.merged[:B]).all()
     step_bytes = sum(sum(step_launch_bytes(n + W + i + 1, scheme) for n in lens) for i in range(K)) / K * L
     gbs = step_bytes / (ms / 1e3) / 1e9
+
+    # ---- the dominant kernel alone (pos fixed): the prefix kernel with its fused tails, 36 launches
+    # (int8t64: the attention launch of each layer's step, without the append launch; per-token
+    # symmetric: the step's only launch, which also stores the new token)
+    g_launch = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_launch):
+        for layer in range(L):
+            if scheme == "tok":
+                cache.decode_step(ks[layer], vs[layer], qs[layer], layer)
+            else:
+                cache.attend(qs[layer], layer)
+    per_launch_s = _time_graph(g_launch, stream, K, W) / 1e3 / L
+    pos = [n + W + K for n in lens]
+    launch_bytes = sum((step_launch_bytes(p + 1, "tok") if scheme == "tok" else attn_bytes(p + 1)) for p in pos)
+    _calibration_copy(dev)
+    kidx = 3 if scheme == "tok" else 2
+    kname = (f"nkv::attn_prefix_kernel<{kidx}> paged "
+             f"{'decode step (store of the new token + attention)' if scheme == 'tok' else 'attention'} of the "
+             f"{B} sequences with fused per-(sequence, KV head) tails, one launch per layer")
     res = {"metric": "paged ragged batch int8-KV decode: batch tokens/s + achieved HBM GB/s (% of peak)",
            "value": round(B / (ms / 1e3), 2), "unit": "tokens/s", "steps": K, "ms_per_step": round(ms, 4),
            "config": {"workload": f"paged {'per-token symmetric int8' if scheme == 'tok' else 'int8t64'} decode, "
                                   f"{B} ragged sequences (lengths {lens}), {L} layers x "
                                   "(32 q / 8 kv heads, head_dim 128), 64-token pages, hipGraph-replayed steps",
-                      "lengths": lens, "layers": L, "page_tokens": 64, "work_units_per_head": cache.total_parts},
+                      "lengths": lens, "layers": L, "page_tokens": 64, "work_units_per_head": cache.total_parts,
+                      "launches_per_layer": 1 if scheme == "tok" else 2},
            "step_gbs": round(gbs, 1), "step_pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-           "algorithmic_bytes_per_step": round(step_bytes)}
-    del graph, cache
+           "algorithmic_bytes_per_step": round(step_bytes),
+           "roofline": _roofline_hbm(launch_bytes, per_launch_s, f"paged_{scheme}", kname, L)}
+    del graph, g_launch, cache
     torch.cuda.empty_cache()
     return res
 
@@ -538,9 +627,11 @@ def run_prefill(args, steps: int | None = None) -> dict:
         int8_prefill_attend(q, kc, vc, *packed, used=U, out=out, scratch=scratch, splits=splits)
     ms = _time_graph(graph, torch.cuda.current_stream(dev), K, W)
     assert torch.isfinite(out).all()
+    _calibration_copy(dev)
     flop = 2 * 2 * D * HQ * (M * U + M * (M + 1) // 2)
     nbytes = U * 2176 + 2 * M * HQ * D * 2 + 2 * M * HKV * D * 2  # codes + rulers, q + out, chunk K/V
     tflops = flop / (ms / 1e3) / 1e12
+    traffic = read_traffic("prefill")
     return {"metric": "chunked-prefill attention over int8 KV: chunks/s, TFLOP/s, MFMA utilisation, GB/s",
             "value": round(1e3 / ms, 2), "unit": "chunks/s", "steps": K, "ms_per_step": round(ms, 4),
             "config": {"workload": f"{M}-token fp16 chunk causally over a {U}-token int8t64 cache plus itself, "
@@ -548,8 +639,56 @@ def run_prefill(args, steps: int | None = None) -> dict:
                        "splits": splits},
             "flop_per_step": flop,
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_FP16_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": None},
+                         "unit": "TFLOP/s", "frac": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": traffic,
+                         "traffic_over_algorithmic": round(traffic / nbytes, 4) if traffic else None,
+                         "kernel": "nkv::prefill_chunk_kernel + nkv::prefill_combine_kernel (the chunk's two "
+                                   "launches, timed together)",
+                         "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(ms * 1e3, 3)},
             "gbs": round(nbytes / (ms / 1e3) / 1e9, 1)}
+
+
+def run_read_ceiling(args, steps: int | None = None) -> dict:
+    """The HBM read ceiling of the decode path's load pattern, over the bytes one 36-layer step
+    streams (36 buffers of one layer's 32k-context algorithmic bytes, 2.6 GB in all, rotated so
+    that nothing is served from the caches): ``nkv_read_bw_lds`` (8 KiB chunks by nontemporal
+    LDS-DMA, two per wave in flight, 256 workgroups of 8 waves, as the decode kernels stream)
+    over the whole 2.6 GB in one launch and as 36 launches of one layer's bytes, and
+    ``nkv_read_bw`` (plain 16-byte register loads) over the whole. HIP events over K graph
+    replays of each."""
+    import torch
+
+    from nova_amd import _lib
+
+    dev = torch.device("cuda:0")
+    K, W = steps or 16, args.warmup
+    per_layer = -(-attn_bytes(CTX + 1) // 8192) * 8192
+    L = LAYERS
+    buf = torch.empty(per_layer * L, dtype=torch.uint8, device=dev)
+    buf.random_(0, 256, generator=torch.Generator(device=dev).manual_seed(7))
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream(dev)
+    out = {}
+    for name, launches in (("lds_dma_one_launch", [(0, per_layer * L, "nkv_read_bw_lds", 256)]),
+                           ("lds_dma_per_layer_launches",
+                            [(i * per_layer, per_layer, "nkv_read_bw_lds", 256) for i in range(L)]),
+                           ("register_loads_one_launch", [(0, per_layer * L, "nkv_read_bw", 4096)])):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for off, n, fn, blocks in launches:
+                _lib.call(fn, buf.data_ptr() + off, n, sink.data_ptr(), blocks, _lib.stream_ptr(dev))
+        ms = _time_graph(g, s, K, W)
+        out[name] = {"tb_per_s": round(per_layer * L / (ms / 1e3) / 1e12, 3), "ms": round(ms, 4),
+                     "frac_of_peak": round(per_layer * L / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "launches": len(launches)}
+        del g
+    del buf, sink
+    torch.cuda.empty_cache()
+    best = out["lds_dma_one_launch"]["tb_per_s"]
+    return {"metric": "HBM read ceiling of the decode path's load pattern (TB/s)", "value": best,
+            "unit": "TB/s", "steps": K, "ms_per_step": out["lds_dma_one_launch"]["ms"],
+            "config": {"workload": f"{L} x {per_layer} B read ({per_layer * L / 1e9:.2f} GB, one 36-layer 32k "
+                                   "step's algorithmic bytes), rotating buffers", "bytes": per_layer * L},
+            "probes": out}
 
 
 def _standalone(res: dict, args) -> dict:
@@ -564,7 +703,7 @@ def _standalone(res: dict, args) -> dict:
 # ---------------------------------------------------------------- end to end (random-weight decoder)
 
 
-def bench_e2e(args) -> dict:
+def bench_e2e(args, steps: int | None = None) -> dict:
     """End-to-end graph decode of the random-weight decoder with Qwen3-4B geometry (36 layers,
     hidden 2560, 32 q / 8 KV heads of 128, SwiGLU 9728, vocab 151936, fp16 weights) over the
     int8t64 cache: the prompt (``--ctx`` random ids) is prefilled in streamed chunks, then each
@@ -577,7 +716,7 @@ def bench_e2e(args) -> dict:
     from nova_amd.skeleton import SkeletonConfig, SkeletonForCausalLM
 
     dev = torch.device("cuda:0")
-    L, ctx, W, K = args.layers, args.ctx, args.warmup, args.steps
+    L, ctx, W, K = args.layers, args.ctx, args.warmup, steps or args.steps
     cfg = SkeletonConfig(num_hidden_layers=L, vocab_size=VOCAB_QWEN3_4B)
     model = SkeletonForCausalLM(cfg, seed=5, device=dev, dtype=torch.float16).eval()
     model.use_decode_kernels(True)
@@ -625,7 +764,12 @@ def bench_e2e(args) -> dict:
 def main() -> int:
     args = parse_args()
     if args.traffic_from:
-        write_traffic(*args.traffic_from, scheme=args.scheme, mode=args.mode)
+        write_traffic(*args.traffic_from, key=args.traffic_key)
+        return 0
+    if args.stats_from:
+        if not args.stats_name or not args.stats_cmd:
+            raise SystemExit("--stats-from needs --stats-name and --stats-cmd")
+        write_stats(args.stats_from, args.stats_name, args.stats_cmd)
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not run here (the decode attention shards by "
@@ -638,37 +782,49 @@ def main() -> int:
 
     _lib.load()
     torch.cuda.set_device(0)
+    steps = args.steps if args.steps != 256 else None
     if args.workload == "paged":
-        res = _standalone(run_paged(args, args.steps if args.steps != 256 else None, args.scheme), args)
+        res = _standalone(run_paged(args, steps, args.scheme), args)
     elif args.workload == "prefill":
-        res = _standalone(run_prefill(args, args.steps if args.steps != 256 else None), args)
+        res = _standalone(run_prefill(args, steps), args)
     elif args.workload == "e2e":
         res = _standalone(bench_e2e(args), args)
+    elif args.workload == "read":
+        res = _standalone(run_read_ceiling(args, steps), args)
     else:
-        res = run_decode(args, args.scheme, headline=True, mode=args.mode)
+        res = run_decode(args, args.scheme, headline=True, mode=args.mode, dep=args.dep)
         if not args.no_cpu_baseline:
             res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, args.scheme, args.ctx, args.layers)
         else:
             res["cpu_baseline"] = None
         if args.workload is None and not args.only:
             extra = {}
-            for name, fn in (("layer_launch_decode", lambda: run_decode(args, "t64", headline=False, mode="layers")),
-                             ("tok_decode", lambda: run_decode(args, "tok", headline=False)),
-                             ("tok_layer_launch_decode", lambda: run_decode(args, "tok", headline=False,
-                                                                            mode="layers")),
+            for name, fn in (("head_dep_decode", lambda: run_decode(args, "t64", False, "chain", "head")),
+                             ("layer_launch_decode", lambda: run_decode(args, "t64", False, "layers")),
+                             ("tok_decode", lambda: run_decode(args, "tok", False, "chain", "all")),
+                             ("tok_head_dep_decode", lambda: run_decode(args, "tok", False, "chain", "head")),
+                             ("tok_layer_launch_decode", lambda: run_decode(args, "tok", False, "layers")),
                              ("paged_batch", lambda: run_paged(args)),
                              ("paged_batch_tok", lambda: run_paged(args, scheme="tok")),
-                             ("chunked_prefill", lambda: run_prefill(args))):
+                             ("chunked_prefill", lambda: run_prefill(args)),
+                             ("read_ceiling", lambda: run_read_ceiling(args)),
+                             ("e2e_decode", lambda: bench_e2e(args, args.e2e_steps))):
                 try:
                     extra[name] = fn()
                 except Exception as e:  # noqa: BLE001 - one extra workload failing must not hide the headline
                     extra[name] = {"error": f"{type(e).__name__}: {e}"[:400]}
-            for name in ("layer_launch_decode", "tok_decode", "tok_layer_launch_decode"):
+            for name in ("head_dep_decode", "layer_launch_decode", "tok_decode", "tok_head_dep_decode",
+                         "tok_layer_launch_decode"):
                 if "error" not in extra[name]:
                     t = extra[name]
                     extra[name] = {k: t[k] for k in ("value", "unit", "ms_per_step", "step_gbs",
                                                      "step_pct_of_hbm_peak", "roofline", "config")}
             res["workloads"] = extra
+            rc = extra["read_ceiling"]
+            if "error" not in rc:
+                # the headline's kernel against the read rate its own load pattern reaches
+                res["roofline"]["frac_of_read_ceiling"] = round(
+                    res["roofline"]["achieved"] / (rc["value"] * 1e3), 4)
     print(json.dumps(res), flush=True)
     return 0
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 7
+#define NKV_ABI_VERSION 8
 
 #define NKV_OK 0
 #define NKV_ERR_INVALID 1     /* argument outside what the reference accepts */
@@ -304,33 +304,62 @@ int nkv_decode_step_combine_tok(const uint16_t* q, const uint16_t* k_new, const 
 
 /*
  * ---- Chained decode step: every layer of one token in one launch ----
- * The decode step of a stack of layers whose inputs may be outputs of the layer before
- * (q, k_new, v_new of layer l read from what layer l - 1 wrote, as a model's layers are
- * chained). Layer l computes exactly nkv_decode_step_t64 (nkv_decode_step_tok) on its own
- * cache: the same cache state and scalars bit for bit, the same output up to float
- * summation order. Replaces the per-layer `KVInt8Cache.update` + `KVInt8Cache.attend` pairs
- * that the graph-decode loop issues once per layer (src/nova/decode.py:301-320 running
- * src/nova/layers.py:132-136 for every layer), for stacks whose inter-layer work is itself
- * in the chain (here: outputs consumed directly as the next layer's inputs).
+ * The decode step of a stack of layers whose inputs may be outputs of an earlier layer (q,
+ * k_new, v_new of layer l read from what layer l - 1 wrote, as a model's layers are chained).
+ * Layer l computes exactly nkv_decode_step_t64 (nkv_decode_step_tok) on its own cache: the same
+ * cache state and scalars bit for bit, the same output up to float summation order. Replaces
+ * the per-layer `KVInt8Cache.update` + `KVInt8Cache.attend` pairs that the graph-decode loop
+ * issues once per layer (src/nova/decode.py:301-320 running src/nova/layers.py:132-136 for every
+ * layer), for stacks whose inter-layer work is itself in the chain (here: outputs consumed
+ * directly as the next layer's inputs).
  *
  * One launch of hkv * (n_parts + 1) workgroups that must all be resident at once; the call
  * checks that against the device's occupancy and returns NKV_ERR_UNSUPPORTED when they are
  * not. Per KV head, n_parts workgroups stream the int8 prefix and one merges (append, ring,
- * combine). No input of layer l is read before every output of layer l - 1 is written (a
- * completion counter per layer, agent-scope release / acquire); layer l + 1's codes, which
- * do not depend on layer l, stream in while layer l is merged.
+ * combine). Layer l + 1's codes, which do not depend on layer l, stream in while layer l is
+ * merged.
+ *
+ * When the inputs of layer l are read (`dep`):
+ *  - Forwarded inputs. When q of layer l is the whole output of layer l - 1, head h's q rows
+ *    are read from a tagged copy of that output, each word as soon as head h's merger has
+ *    written it (no counter, no fence); the same for head h's k_new / v_new rows when they lie
+ *    in the rows of that output that head h's merger writes (its q heads h gq .. h gq + gq - 1).
+ *    With NKV_DEP_HEAD nothing else is waited for: each KV head's layers then chain on their
+ *    own, and head h may start layer l before another head has finished layer l - 1. With
+ *    NKV_DEP_ALL every input of layer l is read only after every head's merger has finished
+ *    layer l - 1 (its completion counter, polled in the same rounds as the words), which is the
+ *    dependency of a model, where every q head of layer l depends on every head of layer l - 1.
+ *  - Every other input of layer l is read after layer l - 1's completion counter has reached
+ *    hkv (an agent-scope release by each merger, acquire by the reader), in either mode.
+ *  Inputs these waits do not order are refused (NKV_ERR_INVALID) when layers_host is given:
+ *  a row that lies in layer j's output must lie within one head w's rows there; with w != h it
+ *  must not be layer l's own output (j == l), and j > l (a value of the previous step that head
+ *  w overwrites in this launch) needs NKV_DEP_ALL. With layers_host NULL the caller guarantees
+ *  this.
  *
  * layers_dev: device array of n_layers entries, read by the kernel (it must stay unchanged
  * while launches that use it are pending); layers_host: the same entries in host memory,
- * checked here (every pointer non-null and 16-byte aligned, lse may be NULL), or NULL to
- * skip the check. Every layer shares the device scalars (pos_dev, first_dev: the step's
- * position; written/qlen/pg written once), capacity, head counts and kv_head_stride.
- * workspace: nkv_layers_workspace_bytes(hkv, hq, n_parts, n_layers) bytes, zero-filled
- * before its first use and kept for these calls of one configuration; every call leaves it
- * zero-filled. n_parts <= 0 takes nkv_layers_default_parts. A wait that gives up (it cannot
- * when the grid is resident) makes the affected outputs NaN and sets the int at byte offset
- * (workspace_bytes & ~3) - 4 * (n_layers + 2) to 1; it stays set.
+ * checked here (every pointer non-null and 16-byte aligned, lse may be NULL; the input rules
+ * above), or NULL to skip the check. Every layer shares the device scalars (pos_dev, first_dev:
+ * the step's position; written/qlen/pg written once), capacity, head counts and kv_head_stride.
+ *
+ * workspace: nkv_layers_workspace_bytes(hkv, hq, n_parts, n_layers) bytes, zero-filled before
+ * its first use and then dedicated to calls with this (hkv, hq, n_parts, n_layers): a call
+ * leaves its partial blocks and layer counters at zero, but the tagged copies of the outputs
+ * and the launch counter (the tags' source) keep their values, so the buffer must be zero-filled
+ * again before it serves another configuration or another entry point. n_parts <= 0 takes
+ * nkv_layers_default_parts.
+ *
+ * Failure mode. The waits assume every workgroup of the grid runs at once. The occupancy check
+ * sees the device, not what else runs on it: when another kernel or process holds CUs, some
+ * workgroups start late, a wait may give up (after 0.2 s each), the affected outputs become NaN
+ * and the int at byte offset (workspace_bytes & ~3) - 4 * (n_layers + 2) is set to 1; it stays
+ * set. A caller polls that error word (ChainedStep.check() does) outside its timed or captured
+ * loop; a launch never hangs.
  */
+#define NKV_DEP_HEAD 0
+#define NKV_DEP_ALL 1
+
 typedef struct nkv_layer_t64 {
   const uint16_t* q;      /* [hq, 128] fp16 */
   const uint16_t* k_new;  /* [hkv, 128] fp16, head stride kv_head_stride */
@@ -369,13 +398,22 @@ int nkv_decode_layers_t64(const nkv_layer_t64* layers_dev, const nkv_layer_t64* 
                           int64_t n_layers, int64_t kv_head_stride, const int64_t* pos_dev,
                           const int64_t* first_dev, int64_t* written_dev, int64_t* qlen_dev,
                           int64_t* pg_dev, int64_t hq, int64_t hkv, int64_t head_dim, int64_t capacity,
-                          void* workspace, int64_t workspace_bytes, int64_t n_parts, void* stream);
+                          void* workspace, int64_t workspace_bytes, int64_t n_parts, int dep, void* stream);
 
 int nkv_decode_layers_tok(const nkv_layer_tok* layers_dev, const nkv_layer_tok* layers_host,
                           int64_t n_layers, int64_t kv_head_stride, const int64_t* pos_dev,
                           int64_t* written_dev, int64_t hq, int64_t hkv, int64_t head_dim,
                           int64_t capacity, void* workspace, int64_t workspace_bytes, int64_t n_parts,
-                          void* stream);
+                          int dep, void* stream);
+
+/* The input rules of nkv_decode_layers_t64 / _tok (above: which rows of earlier outputs a layer
+ * may read under `dep`) checked on a host table alone, without a GPU: NKV_OK, or NKV_ERR_INVALID
+ * with nkv_last_error() naming the first row refused. Only the pointer values are used. The
+ * launches run the same check when given layers_host. */
+int nkv_decode_layers_check_t64(const nkv_layer_t64* layers_host, int64_t n_layers, int64_t kv_head_stride,
+                                int64_t hq, int64_t hkv, int dep);
+int nkv_decode_layers_check_tok(const nkv_layer_tok* layers_host, int64_t n_layers, int64_t kv_head_stride,
+                                int64_t hq, int64_t hkv, int dep);
 
 /*
  * ---- Paged batch of ragged sequences (int8t64) ----
@@ -528,6 +566,15 @@ int nkv_copy_bytes(const void* src, void* dst, int64_t nbytes, void* stream);
  * nbytes must be a multiple of 16.
  */
 int nkv_read_bw(const void* src, int64_t nbytes, uint32_t* sink, int64_t blocks, void* stream);
+
+/*
+ * The same ceiling for the decode kernels' own load pattern: `blocks` workgroups of 8 waves
+ * (one per CU) read `src` in 8 KiB chunks with nontemporal LDS-DMA loads (global_load_lds,
+ * 16 bytes per lane), two chunks in flight per wave, as the prefix and chained kernels stream
+ * their codes; one XOR checksum per workgroup to sink[blocks]. nbytes must be a multiple of 8192.
+ * Counterpart of the reference's read + unpack ceiling (src/diagnostics/bench_int8_unpack.py:58-102).
+ */
+int nkv_read_bw_lds(const void* src, int64_t nbytes, uint32_t* sink, int64_t blocks, void* stream);
 
 /* ---------------------------------------------------------------- decode-step projections
  *

@@ -26,9 +26,11 @@ NKV_ERR_HIP = 3
 
 NKV_F16, NKV_BF16, NKV_F32 = 0, 1, 2
 NKV_AXIS_CHANNEL, NKV_AXIS_TOKEN = 0, 1
+NKV_DEP_HEAD, NKV_DEP_ALL = 0, 1
 
 P = c_void_p
 I64 = c_int64
+I32 = c_int
 
 # name -> (restype, argtypes); must match include/nova_kv.h
 # q, k_new, v_new, kv_head_stride, kq, kmn, kst, vq, vmn, vst, tail_k, tail_v, pos, first, written,
@@ -67,10 +69,12 @@ SIGNATURES = {
     "nkv_layers_default_parts": (I64, [I64, I64, c_int]),
     # layers_dev, layers_host, n_layers, kv_head_stride, pos, first, written, qlen, pg, hq, hkv, head_dim,
     # capacity, workspace, workspace_bytes, n_parts, stream
-    "nkv_decode_layers_t64": (c_int, [P, P, I64, I64, P, P, P, P, P, I64, I64, I64, I64, P, I64, I64, P]),
+    "nkv_decode_layers_t64": (c_int, [P, P, I64, I64, P, P, P, P, P, I64, I64, I64, I64, P, I64, I64, I32, P]),
     # layers_dev, layers_host, n_layers, kv_head_stride, pos, written, hq, hkv, head_dim, capacity,
     # workspace, workspace_bytes, n_parts, stream
-    "nkv_decode_layers_tok": (c_int, [P, P, I64, I64, P, P, I64, I64, I64, I64, P, I64, I64, P]),
+    "nkv_decode_layers_tok": (c_int, [P, P, I64, I64, P, P, I64, I64, I64, I64, P, I64, I64, I32, P]),
+    "nkv_decode_layers_check_t64": (c_int, [P, I64, I64, I64, I64, I32]),
+    "nkv_decode_layers_check_tok": (c_int, [P, I64, I64, I64, I64, I32]),
     "nkv_paged_workspace_bytes": (I64, [I64, I64, I64]),
     "nkv_paged_quantize_t64": (c_int, [P, c_int, I64, I64, I64, c_int, P, P, I64, I64, P]),
     "nkv_paged_append_t64": (c_int, [P, P, I64, I64, P, P, I64, I64, P, P, I64, I64, I64, P]),
@@ -87,12 +91,13 @@ SIGNATURES = {
                                           I64, I64, P]),
     "nkv_copy_bytes": (c_int, [P, P, I64, P]),
     "nkv_read_bw": (c_int, [P, I64, P, I64, P]),
+    "nkv_read_bw_lds": (c_int, [P, I64, P, I64, P]),
     "nkv_gemv": (c_int, [P, P, c_float, P, I64, I64, P, P, P]),
     "nkv_swiglu_gemv": (c_int, [P, P, c_float, P, I64, I64, P, P]),
     "nkv_qk_norm_rope": (c_int, [P, I64, I64, I64, P, P, c_float, P, P, P]),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lib = None
 _lock = threading.Lock()

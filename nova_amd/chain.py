@@ -5,19 +5,33 @@ come from what layer ``l - 1`` wrote. The per-layer decode step (``KVInt8Cache.u
 one ``nkv_decode_step_t64`` launch per layer, replacing the ``update`` + ``attend`` pair that
 ``LeanAttention.forward`` issues for every layer, src/nova/layers.py:132-136) pays one launch's
 ramp-up, drain and merge per layer. :class:`ChainedStep` runs the same per-layer computation
-for all layers in one launch (``nkv_decode_layers_t64`` / ``_tok``): each layer's inputs are
-read only after every output of the layer before is written, and the int8 prefix of layer
+for all layers in one launch (``nkv_decode_layers_t64`` / ``_tok``); the int8 prefix of layer
 ``l + 1``, which does not depend on layer ``l``, streams into on-chip memory while layer ``l``
 is merged. Cache state and scalars are bit-identical to the per-layer launches; outputs agree
 up to float summation order.
 
+When layer ``l``'s inputs are read (``dep``):
+
+- ``"all"`` (the default): only after every KV head of layer ``l - 1`` has finished, as in a
+  model, where every query head of layer ``l`` depends on every head of layer ``l - 1``.
+- ``"head"``: an input that is a view of the rows of layer ``l - 1``'s output that its own KV
+  head wrote (``q`` the whole output; head ``h``'s k/v rows among its own query heads) is read
+  as soon as that head has written it, so each KV head's layers chain on their own. Other
+  inputs still wait for every head.
+
+Inputs that neither wait orders (a row of another head's output of the same layer, or, with
+``"head"``, of a later layer) are refused when the object is built.
+
     chain = ChainedStep(cache, keys, values, queries, outs)   # outside graph capture
     chain()                                                   # one step (capturable)
     cache.pos.add_(1)
+    chain.check()                                             # outside the loop: raises if a wait gave up
 
 The table of per-layer pointers is built once, on the host and in device memory, so the
 tensors passed in must stay allocated (the object keeps references to them) and a captured
-graph that launches the chain stays valid while the object lives.
+graph that launches the chain stays valid while the object lives. The launch assumes every
+workgroup of its grid is resident at once; another kernel or process holding CUs can make a
+wait give up (after 0.2 s): the affected outputs are then NaN and :meth:`check` raises.
 """
 
 from __future__ import annotations
@@ -47,13 +61,19 @@ class ChainedStep:
     outs: per layer ``[1, H_q, 1, 128]`` contiguous fp16; lses: per layer ``[1, H_q]`` fp32, or
     None. ``cache`` is a :class:`~nova_amd.kvattn.KVInt8Cache` (int8t64) or a
     :class:`~nova_amd.kvtok.KVInt8TokCache` (per-token symmetric). ``n_parts`` is the number of
-    streaming workgroups per KV head (0: the library's default for this device).
+    streaming workgroups per KV head (0: the library's default for this device). ``dep``:
+    ``"all"`` or ``"head"``, when each layer's inputs are read (see the module docstring).
     """
 
-    def __init__(self, cache, keys, values, queries, outs, lses=None, n_parts: int = 0):
+    DEPS = {"head": _lib.NKV_DEP_HEAD, "all": _lib.NKV_DEP_ALL}
+
+    def __init__(self, cache, keys, values, queries, outs, lses=None, n_parts: int = 0, dep: str = "all"):
         from .kvtok import KVInt8TokCache
 
         lib = _lib.load()
+        if dep not in self.DEPS:
+            raise ValueError(f"dep must be one of {sorted(self.DEPS)}, got {dep!r}")
+        self.dep = dep
         self.cache = cache
         self.tok = isinstance(cache, KVInt8TokCache)
         if getattr(cache, "prefilling", False) or getattr(cache, "_in_prefill", False):
@@ -103,11 +123,20 @@ class ChainedStep:
         self.ws_bytes = int(lib.nkv_layers_workspace_bytes(hkv, hq, parts, n))
         self.workspace = torch.zeros(-(-self.ws_bytes // 4), dtype=torch.int32, device=dev)
         self.ws_bytes = self.workspace.numel() * 4
+        self._check_inputs()
+
+    def _check_inputs(self) -> None:
+        """Refuse inputs the launch's waits do not order: the library's check of the host table
+        (``nkv_decode_layers_check_*``, host only), once here rather than at every launch."""
+        _lib.call("nkv_decode_layers_check_tok" if self.tok else "nkv_decode_layers_check_t64", self._host.ctypes.data,
+                  self.n_layers, self.kv_head_stride, self.cache.num_q_heads, self.cache.num_kv_heads,
+                  self.DEPS[self.dep])
 
     def _args(self) -> tuple:
         c = self.cache
         head = (self._dev.data_ptr(), self._host.ctypes.data, self.n_layers, self.kv_head_stride)
-        tail = (self.workspace.data_ptr(), self.ws_bytes, self.n_parts, _lib.stream_ptr(c.pos.device))
+        tail = (self.workspace.data_ptr(), self.ws_bytes, self.n_parts, self.DEPS[self.dep],
+                _lib.stream_ptr(c.pos.device))
         if self.tok:
             return (*head, c.pos.data_ptr(), c._written.data_ptr(), c.num_q_heads, c.num_kv_heads, c.head_dim,
                     c.max_len, *tail)
@@ -128,6 +157,15 @@ class ChainedStep:
     def gave_up(self) -> bool:
         """Whether a launch's wait ever gave up (its outputs are then NaN). Synchronizes."""
         return self._sync_words()[self.n_layers + 1] != 0
+
+    def check(self) -> None:
+        """Raise ``RuntimeError`` if any launch so far had a wait give up (its outputs are NaN:
+        some workgroups were not resident with the others, e.g. another kernel or process held
+        CUs). One 4-byte read; synchronizes, so call it outside timed or captured loops."""
+        end = (self.ws_bytes & ~3) // 4
+        if int(self.workspace[end - self.n_layers - 2].item()) != 0:
+            raise RuntimeError("ChainedStep: a chained launch's wait gave up (outputs NaN); every workgroup of "
+                               "its grid must be resident at once, so nothing else may hold the GPU's CUs")
 
     def idle_state(self) -> dict:
         """Between launches: whether the partial blocks and the counters are back at zero, and the

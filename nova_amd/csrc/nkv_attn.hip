@@ -145,6 +145,10 @@ struct AttnArgs {
   // bits, `ftag` in the high 32) for the next layer's inputs that are views of it; null otherwise
   uint64_t* fwd_out;
   uint32_t ftag;
+  // the chained step's dependency between layers: 0, a forwarded input waits only for the words
+  // it reads (written by its own head's merger); 1, every input of layer l also waits until every
+  // head's merger has finished layer l - 1
+  int dep_all;
 };
 
 // XOR key of the 16-byte chunk positions of LDS row `row` (a token within its group).
@@ -2109,18 +2113,25 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
 // counts itself on the layer's completion counter. Workgroup (h, p + 1) streams part p of
 // head h's int8 prefix into one published partial, as the prefix kernel does.
 //
-// Ordering. Before a workgroup reads layer l's inputs, one lane waits for layer l - 1's counter
-// to reach hkv (relaxed agent-scope polls, then an agent-scope acquire fence); a merger adds to
-// its layer's counter with an agent-scope release after every wave's out / lse stores have
-// completed and the workgroup has met at a barrier. So every output of layer l - 1 happens
-// before every read of layer l's inputs. The prefix partials use the published-word protocol of
-// the fused tail (per-location coherence, no flag); each layer has its own partial block.
+// Ordering. A merger adds to its layer's counter with an agent-scope release after every wave's
+// out / lse stores have completed and the workgroup has met at a barrier, and it also stores the
+// output as tagged words. Layer l's inputs are read in one of two ways:
+//  - forwarded: q is the whole of layer l - 1's output, and (for a merger) head h's k_new / v_new
+//    rows lie in the rows head h's merger wrote. The reader reloads the tagged words it needs
+//    until they carry this launch's tag (per-location coherence, no fence). Without dep_all
+//    nothing else is waited for: each head's layers then chain on their own. With dep_all, lane
+//    0 also polls layer l - 1's counter in the same rounds until every head's merger is done.
+//  - otherwise one lane waits for layer l - 1's counter to reach hkv (relaxed agent-scope polls,
+//    then an agent-scope acquire fence) and the inputs are plain loads.
+// The host refuses inputs that these waits do not order (nkv_decode_layers_t64). The prefix
+// partials use the published-word protocol of the fused tail (per-location coherence, no flag);
+// each layer has its own partial block.
 //
 // Overlap. Nothing in a layer's prefix depends on an earlier layer (the append writes only the
 // current group, which the prefix does not read), so as soon as a streaming workgroup has
 // published its layer-l partial, its waves issue their first group of layer l + 1 into their
 // LDS stages, and HBM keeps streaming while the mergers finish layer l. Wave 7 loads q after the
-// counter wait.
+// wait.
 //
 // Termination. Every wait gives up after a bounded number of polls; a streaming workgroup that
 // gave up publishes an l of NaN, so the merged output is NaN, and sets the error word. At the
@@ -2189,16 +2200,22 @@ __device__ __forceinline__ bool within(const uint16_t* p, int64_t n, const uint1
 // l - 1): lane i takes words i + 64 j, reloading those whose tag is not yet `tag` (relaxed
 // agent-scope loads: per-location coherence hands over each word once written, no counter or
 // fence), and stores their fp16 pairs to LDS at `dst` (q rows, then k_new, then v_new).
+// With `ctr` (the all-head dependency), lane 0 also polls that counter in the same rounds until
+// it reaches `target`: the wait ends when every word carries the tag and the counter is reached,
+// with no extra round trip. The counter only orders (the words validate themselves), so its
+// polls are relaxed and no fence follows.
 // gq <= FWD_MAX_GQ. false when the wait gave up (after LAYER_WAIT_TICKS, or at once with `lost`).
 constexpr int FWD_MAX_GQ = 4;
 __device__ __forceinline__ bool fwd_fetch(const uint64_t* q, const uint64_t* k, const uint64_t* v, int gq,
-                                          uint32_t tag, uint32_t* dst, bool lost) {
+                                          uint32_t tag, uint32_t* dst, bool lost, const int* ctr = nullptr,
+                                          int target = 0) {
   const int lane = tail_tid() & 63;
   uint64_t w[FWD_MAX_GQ + 2];
 #pragma unroll
   for (int j = 0; j < FWD_MAX_GQ + 2; ++j) w[j] = 0;  // (tag 0 is never current)
   const bool kv = k != nullptr;
   bool ok = !lost;
+  int c = ctr != nullptr && lane == 0 ? target - 1 : target;  // (only lane 0 polls the counter)
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   while (ok) {
 #pragma unroll
@@ -2208,7 +2225,8 @@ __device__ __forceinline__ bool fwd_fetch(const uint64_t* q, const uint64_t* k, 
       w[FWD_MAX_GQ] = __hip_atomic_load(k + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (kv && (uint32_t)(w[FWD_MAX_GQ + 1] >> 32) != tag)
       w[FWD_MAX_GQ + 1] = __hip_atomic_load(v + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    bool miss = false;
+    if (c < target) c = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool miss = c < target;
 #pragma unroll
     for (int j = 0; j < FWD_MAX_GQ; ++j) miss |= j < gq && (uint32_t)(w[j] >> 32) != tag;
     miss |= kv && ((uint32_t)(w[FWD_MAX_GQ] >> 32) != tag || (uint32_t)(w[FWD_MAX_GQ + 1] >> 32) != tag);
@@ -2257,13 +2275,17 @@ __device__ __forceinline__ bool merger_layer(const AttnArgs& args, const void* l
   AttnArgs la = args;
   const int gq = la.gq;
   TailSmem& sm = *reinterpret_cast<TailSmem*>(lds_raw);
-  // q, k_new and v_new all views of layer l - 1's output: forwarded, no counter wait
+  // q the whole of layer l - 1's output, and head h's k_new and v_new rows inside the rows this
+  // merger wrote there (head h's q heads): forwarded from the tagged words, with no counter wait
+  // unless every head is waited for (dep_all). Rows written by another head's merger are read
+  // after layer l - 1's counter (that head's chain may run ahead or behind this one).
   bool fwd = false;
   const uint16_t* prev = nullptr;
   if (l > 0 && gq <= FWD_MAX_GQ) {
     prev = layer_out<TOK>(layers, l - 1);
-    const int64_t n = (int64_t)la.hq * D, span = (int64_t)(la.hkv - 1) * la.kv_hs + D;
-    fwd = la.q == prev && within(la.k_new, span, prev, n) && within(la.v_new, span, prev, n);
+    const uint16_t* mine = prev + (int64_t)h * gq * D;
+    fwd = la.q == prev && within(la.k_new + (int64_t)h * la.kv_hs, D, mine, (int64_t)gq * D) &&
+          within(la.v_new + (int64_t)h * la.kv_hs, D, mine, (int64_t)gq * D);
   }
   if (tid == 0) {
     sm.ring_staged = 0;
@@ -2274,7 +2296,8 @@ __device__ __forceinline__ bool merger_layer(const AttnArgs& args, const void* l
     if (fwd) {
       const uint64_t* src = la.fwd_out - (int64_t)la.hq * D / 2;  // layer l - 1's tagged words
       ok = fwd_fetch(src + (int64_t)h * gq * D / 2, src + ((la.k_new - prev) + (int64_t)h * la.kv_hs) / 2,
-                     src + ((la.v_new - prev) + (int64_t)h * la.kv_hs) / 2, gq, la.ftag, sm.fwd, lost);
+                     src + ((la.v_new - prev) + (int64_t)h * la.kv_hs) / 2, gq, la.ftag, sm.fwd, lost,
+                     la.dep_all ? layer_done(la, l - 1) : nullptr, la.hkv);
     } else if (l > 0) {
       ok = wait_layer(la, l - 1, la.hkv, lost);
     }
@@ -2378,9 +2401,10 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
     if (wave == IN_WAVE) {
       bool ok = true;
       if (l > 0 && gq <= FWD_MAX_GQ && la.q == layer_out<TOK>(layers, l - 1)) {
-        // q is layer l - 1's output: its tagged words, no counter wait
+        // q is layer l - 1's output: its tagged words (head h's rows, written by head h's merger),
+        // and with dep_all layer l - 1's counter as well
         ok = fwd_fetch(la.fwd_out - (int64_t)la.hq * D / 2 + (int64_t)h * gq * D / 2, nullptr, nullptr, gq, la.ftag,
-                       reinterpret_cast<uint32_t*>(q_lds), lost);
+                       reinterpret_cast<uint32_t*>(q_lds), lost, a.dep_all ? layer_done(a, l - 1) : nullptr, a.hkv);
       } else {
         ok = l == 0 || wait_layer(a, l - 1, a.hkv, lost);
         issue_q(la.q + (int64_t)h * gq * D, gq, __builtin_amdgcn_readfirstlane(lds_addr(q_lds)));
@@ -2518,8 +2542,10 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
     __syncthreads();
     if (l + 1 < n_layers) issue_first(layer_args<TOK>(a, layers, l + 1, ftag));
   }
-  // every merger has consumed layers 0 .. n_layers - 2 (this workgroup passed the last counter
-  // wait): their slots of this part back to zero, read again by the next launch
+  // head h's merger has consumed this part's partials of layers 0 .. n_layers - 2: this workgroup
+  // read layer n_layers - 1's q after that merger finished layer n_layers - 2 (from its tagged
+  // words, or after the counter that it joins only once it has merged). Those slots back to zero,
+  // read again by the next launch
   for (int l = 0; l + 1 < n_layers; ++l) {
     uint4* slot = reinterpret_cast<uint4*>(a.ws + ((int64_t)l * a.hkv * P + (int64_t)h * P + part) * pw);
     for (int i = tid; i < pw / 4; i += THREADS) slot[i] = uint4{0u, 0u, 0u, 0u};
@@ -2537,6 +2563,47 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
       __hip_atomic_store(exit_ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(epoch, (int)ftag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+  }
+}
+
+// ---------------------------------------------------------------- read-ceiling probe
+//
+// The streaming of the decode kernels without their math: `gridDim.x` workgroups of 8 waves, one
+// per CU (128 KiB of LDS each). The buffer is read in chunks of 8 KiB (8 nontemporal LDS-DMA loads
+// of 16 bytes per lane, as the prefix kernel issues them); chunk c goes to wave c mod (8 x blocks),
+// which keeps two chunks in flight in two 8 KiB LDS slots and folds one dword per lane of each
+// landed chunk into an XOR checksum (so every load is consumed). The achievable HBM read rate of
+// the decode path's load pattern, measured in the same process as the path itself.
+constexpr int RB_CHUNK = 8192;
+__global__ __launch_bounds__(THREADS, 1) void read_lds_kernel(const uint8_t* src, int64_t nchunks, uint32_t* sink) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[WAVES * 2 * RB_CHUNK];
+  __shared__ uint32_t part[WAVES];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int64_t nw = (int64_t)gridDim.x * WAVES;
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds + wave * 2 * RB_CHUNK));
+  auto issue = [&](int64_t ch, int slot) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot's last read is done
+    const void* sb = uniform_ptr(src + ch * RB_CHUNK);
+#pragma unroll
+    for (int j = 0; j < RB_CHUNK / 1024; ++j) dma16_stream(sb, (uint32_t)(1024 * j + 16 * lane), base + slot * RB_CHUNK + 1024 * j);
+  };
+  int64_t c = (int64_t)blockIdx.x * WAVES + wave;
+  if (c < nchunks) issue(c, 0);
+  if (c + nw < nchunks) issue(c + nw, 1);
+  uint32_t x = 0;
+  for (int slot = 0; c < nchunks; c += nw, slot ^= 1) {
+    if (c + nw < nchunks) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    x ^= *reinterpret_cast<const uint32_t*>(lds + (wave * 2 + slot) * RB_CHUNK + 16 * lane);
+    if (c + 2 * nw < nchunks) issue(c + 2 * nw, slot);
+  }
+  for (int m = 32; m >= 1; m >>= 1) x ^= (uint32_t)__shfl_xor((int)x, m, 64);
+  if (lane == 0) part[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t y = 0;
+    for (int w = 0; w < WAVES; ++w) y ^= part[w];
+    sink[blockIdx.x] = y;
   }
 }
 
@@ -3585,6 +3652,50 @@ int64_t layers_parts(int64_t hkv, int64_t groups, int resident) {
 
 bool al8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
+// Whether the chained launch's waits order every read of its inputs (the layer table in host
+// memory). Head h of layer l reads q rows h gq .. h gq + gq - 1 and the k_new / v_new rows at
+// h kv_head_stride. A row that lies in layer j's output must lie within the rows of one head w
+// (the rows w's merger writes), and then:
+//  - w == h: head h's own chain orders it (layer j before layer l, or layer l's reads before its
+//    merge, or the reads of layer l before layer j > l is merged);
+//  - j < l: read after layer l - 1's all-head counter (such a row is never forwarded);
+//  - j == l: refused, head w writes the row while head h may still have to read it;
+//  - j > l: ordered only when every layer waits for every head (dep_all: head w starts layer j
+//    after every head has finished layer j - 1 >= l); refused otherwise.
+template <class E>
+int check_chain_inputs(const E* t, int64_t n_layers, int64_t hq, int64_t hkv, int64_t kv_hs, bool dep_all,
+                       const char* what) {
+  const int64_t gq = hq / hkv, n = hq * D;
+  for (int64_t l = 0; l < n_layers; ++l) {
+    for (int64_t h = 0; h < hkv; ++h) {
+      for (int64_t r = 0; r < gq + 2; ++r) {
+        const char* nm = r < gq ? "q" : r == gq ? "k_new" : "v_new";
+        const uint16_t* p = r < gq ? t[l].q + (h * gq + r) * D : (r == gq ? t[l].k_new : t[l].v_new) + h * kv_hs;
+        const uintptr_t a0 = reinterpret_cast<uintptr_t>(p), a1 = a0 + 2 * D;
+        for (int64_t j = 0; j < n_layers; ++j) {
+          const uintptr_t o0 = reinterpret_cast<uintptr_t>(t[j].out), o1 = o0 + 2 * n;
+          if (a1 <= o0 || a0 >= o1) continue;
+          const int64_t w0 = a0 >= o0 ? (int64_t)(a0 - o0) / (2 * gq * D) : -1;
+          const int64_t w1 = a1 <= o1 ? (int64_t)(a1 - 1 - o0) / (2 * gq * D) : -1;
+          if (w0 < 0 || w1 != w0)
+            return fail(NKV_ERR_INVALID, "%s: layer %lld head %lld: a %s row straddles the rows of layer %lld's output "
+                        "that different heads write", what, (long long)l, (long long)h, nm, (long long)j);
+          if (w0 == h || j < l) continue;
+          if (j == l)
+            return fail(NKV_ERR_INVALID, "%s: layer %lld head %lld reads its %s row from the same layer's output of "
+                        "KV head %lld, which may already be overwritten", what, (long long)l, (long long)h, nm,
+                        (long long)w0);
+          if (!dep_all)
+            return fail(NKV_ERR_INVALID, "%s: layer %lld head %lld reads its %s row from layer %lld's output of KV "
+                        "head %lld, which that head's chain may overwrite first; only the all-head dependency "
+                        "orders this", what, (long long)l, (long long)h, nm, (long long)j, (long long)w0);
+        }
+      }
+    }
+  }
+  return NKV_OK;
+}
+
 // Launch of attn_layers_kernel: the checks common to both formats, the grid, the launch.
 int launch_layers(AttnArgs& a, bool tok, const void* layers_dev, int64_t n_layers, int64_t n_parts,
                   int64_t workspace_bytes, hipStream_t s, const char* what) {
@@ -3629,11 +3740,34 @@ extern "C" int64_t nkv_layers_default_parts(int64_t hkv, int64_t capacity, int t
   return parts >= 1 && hkv * (parts + 1) <= resident ? parts : 0;
 }
 
+// The input rules alone (host only; the chained launches run them too when given layers_host).
+template <class E>
+int chain_check(const char* what, const E* layers_host, int64_t n_layers, int64_t kv_head_stride, int64_t hq,
+                int64_t hkv, int dep) {
+  set_error("");
+  if (int rc = check_heads(hq, hkv, D)) return rc;
+  if (!layers_host) return fail(NKV_ERR_INVALID, "%s: null layer table", what);
+  if (n_layers <= 0 || n_layers > (1 << 20)) return fail(NKV_ERR_INVALID, "%s: n_layers %lld outside [1, 2^20]", what, (long long)n_layers);
+  if (dep != NKV_DEP_HEAD && dep != NKV_DEP_ALL) return fail(NKV_ERR_INVALID, "%s: dep %d is not NKV_DEP_HEAD or NKV_DEP_ALL", what, dep);
+  return check_chain_inputs(layers_host, n_layers, hq, hkv, kv_head_stride, dep == NKV_DEP_ALL, what);
+}
+
+extern "C" int nkv_decode_layers_check_t64(const nkv_layer_t64* layers_host, int64_t n_layers, int64_t kv_head_stride,
+                                           int64_t hq, int64_t hkv, int dep) {
+  return chain_check("decode_layers_check_t64", layers_host, n_layers, kv_head_stride, hq, hkv, dep);
+}
+
+extern "C" int nkv_decode_layers_check_tok(const nkv_layer_tok* layers_host, int64_t n_layers, int64_t kv_head_stride,
+                                           int64_t hq, int64_t hkv, int dep) {
+  return chain_check("decode_layers_check_tok", layers_host, n_layers, kv_head_stride, hq, hkv, dep);
+}
+
 extern "C" int nkv_decode_layers_t64(const nkv_layer_t64* layers_dev, const nkv_layer_t64* layers_host,
                                      int64_t n_layers, int64_t kv_head_stride, const int64_t* pos_dev,
                                      const int64_t* first_dev, int64_t* written_dev, int64_t* qlen_dev,
                                      int64_t* pg_dev, int64_t hq, int64_t hkv, int64_t head_dim, int64_t capacity,
-                                     void* workspace, int64_t workspace_bytes, int64_t n_parts, void* stream) {
+                                     void* workspace, int64_t workspace_bytes, int64_t n_parts, int dep,
+                                     void* stream) {
   const char* what = "decode_layers_t64";
   set_error("");
   if (int rc = check_heads(hq, hkv, head_dim)) return rc;
@@ -3647,8 +3781,12 @@ extern "C" int nkv_decode_layers_t64(const nkv_layer_t64* layers_dev, const nkv_
       if (!x || !al16(x)) return fail(NKV_ERR_INVALID, "%s: layer %lld: null or unaligned pointer", what, (long long)l);
     if (e.lse && (reinterpret_cast<uintptr_t>(e.lse) & 3u)) return fail(NKV_ERR_INVALID, "%s: layer %lld: unaligned lse", what, (long long)l);
   }
+  if (dep != NKV_DEP_HEAD && dep != NKV_DEP_ALL) return fail(NKV_ERR_INVALID, "%s: dep %d is not NKV_DEP_HEAD or NKV_DEP_ALL", what, dep);
+  if (layers_host && n_layers > 0 && n_layers <= (1 << 20))
+    if (int rc = check_chain_inputs(layers_host, n_layers, hq, hkv, kv_head_stride, dep == NKV_DEP_ALL, what)) return rc;
   AttnArgs a{};
   a.kv_hs = kv_head_stride;
+  a.dep_all = dep == NKV_DEP_ALL;
   a.pos_dev = pos_dev; a.first_dev = first_dev;
   a.written_out = written_dev; a.qlen_out = qlen_dev; a.pg_out = pg_dev;
   a.capacity = capacity; a.ngroups_cap = cdiv(capacity, GT); a.tail_slots = GT;
@@ -3664,7 +3802,7 @@ extern "C" int nkv_decode_layers_tok(const nkv_layer_tok* layers_dev, const nkv_
                                      int64_t n_layers, int64_t kv_head_stride, const int64_t* pos_dev,
                                      int64_t* written_dev, int64_t hq, int64_t hkv, int64_t head_dim,
                                      int64_t capacity, void* workspace, int64_t workspace_bytes, int64_t n_parts,
-                                     void* stream) {
+                                     int dep, void* stream) {
   const char* what = "decode_layers_tok";
   set_error("");
   if (int rc = check_heads(hq, hkv, head_dim)) return rc;
@@ -3678,8 +3816,12 @@ extern "C" int nkv_decode_layers_tok(const nkv_layer_tok* layers_dev, const nkv_
       if (!x || !al16(x)) return fail(NKV_ERR_INVALID, "%s: layer %lld: null or unaligned pointer", what, (long long)l);
     if (e.lse && (reinterpret_cast<uintptr_t>(e.lse) & 3u)) return fail(NKV_ERR_INVALID, "%s: layer %lld: unaligned lse", what, (long long)l);
   }
+  if (dep != NKV_DEP_HEAD && dep != NKV_DEP_ALL) return fail(NKV_ERR_INVALID, "%s: dep %d is not NKV_DEP_HEAD or NKV_DEP_ALL", what, dep);
+  if (layers_host && n_layers > 0 && n_layers <= (1 << 20))
+    if (int rc = check_chain_inputs(layers_host, n_layers, hq, hkv, kv_head_stride, dep == NKV_DEP_ALL, what)) return rc;
   AttnArgs a{};
   a.kv_hs = kv_head_stride;
+  a.dep_all = dep == NKV_DEP_ALL;
   a.tok = 1;
   a.pos_dev = pos_dev; a.written_out = written_dev;
   a.capacity = capacity; a.ngroups_cap = capacity / GT; a.tail_slots = GT;
@@ -3689,4 +3831,14 @@ extern "C" int nkv_decode_layers_tok(const nkv_layer_tok* layers_dev, const nkv_
   a.sl2 = LOG2E / sqrtf((float)head_dim);
   a.ws = static_cast<float*>(workspace);
   return launch_layers(a, true, layers_dev, n_layers, n_parts, workspace_bytes, static_cast<hipStream_t>(stream), what);
+}
+
+extern "C" int nkv_read_bw_lds(const void* src, int64_t nbytes, uint32_t* sink, int64_t blocks, void* stream) {
+  set_error("");
+  if (!src || !al16(src) || nbytes <= 0 || nbytes % RB_CHUNK)
+    return fail(NKV_ERR_INVALID, "read_bw_lds: nbytes must be a positive multiple of %d and src 16-byte aligned", RB_CHUNK);
+  if (!sink || blocks <= 0 || blocks > (1 << 20)) return fail(NKV_ERR_INVALID, "read_bw_lds: blocks must be in [1, 2^20] with a sink");
+  hipLaunchKernelGGL(read_lds_kernel, dim3((unsigned)blocks), dim3(THREADS), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint8_t*>(src), nbytes / RB_CHUNK, sink);
+  return check_launch("read_bw_lds");
 }

@@ -258,6 +258,23 @@ class PagedKVInt8Cache:
                   self.lse.data_ptr(), self.ws.data_ptr(), self.ws.numel() * 4, _lib.stream_ptr(self.pos.device))
         return self.merged[:self.nseq]
 
+    def attend(self, query: torch.Tensor, layer: int) -> torch.Tensor:
+        """Attention of each planned sequence over ``[0, pos_b]`` with nothing appended (the
+        token at ``pos_b`` read from its ring slot), into ``merged[:B]`` / ``lse``: the second
+        launch of ``decode_step`` alone (``nkv_paged_attn_decode_t64``)."""
+        if self.wg_map is None:
+            raise RuntimeError("call plan() before decoding")
+        n = self.nseq
+        if query.shape != (n, self.num_q_heads, 1, D):
+            raise ValueError("q [B, Hq, 1, 128] fp16, B = the planned sequences")
+        q = query.contiguous()
+        _lib.call("nkv_paged_attn_decode_t64", q.data_ptr(), self.pages[layer].data_ptr(), self.page_table.data_ptr(),
+                  self.page_table.stride(0), self.num_pages, self.rings[layer].data_ptr(), self.pos.data_ptr(), n,
+                  self.num_q_heads, self.num_kv_heads, D, self.wg_map.data_ptr(), self.seq_parts.data_ptr(),
+                  self.total_parts, self.merged.data_ptr(), self.lse.data_ptr(), self.ws.data_ptr(),
+                  self.ws.numel() * 4, _lib.stream_ptr(self.pos.device))
+        return self.merged[:n]
+
     def advance(self) -> None:
         """``pos += 1`` for every planned sequence (device op, graph-safe); refuses a step that
         would take a sequence past its reserved pages."""

@@ -113,22 +113,25 @@ def tok_attn_decode(q, kq, ks, vq, vs, used: int):
 
 
 def chunk_prefill_attend(q, kq, kmn, kst, vq, vmn, vst, used: int, k_chunk, v_chunk, heads=None):
-    """Causal attention of a prefill chunk over the int8t64 cache and itself.
+    """Causal attention of a prefill chunk over the int8t64 cache, an fp16 history and itself.
 
-    ``q`` [Hq, M, D] fp16 (query token i at position ``used + i``); ``kq``/``vq`` [Hkv, L, D]
-    uint8 with rulers [Hkv, ceil(L/64), D] (``used`` a multiple of 64); ``k_chunk``/``v_chunk``
-    [Hkv, M, D] fp16. Token i attends to the cache tokens [0, used), dequantized as
-    ``dequantize_int8_token`` does, and to chunk tokens [0, i] — the reference's
-    ``attend_prefill`` (``src/nova/kvattn.py:791-815``: causal SDPA over the positions
-    before and including each query) with the cache part read from int8. Returns fp64
-    ``[Hq, M, D]`` (only the KV heads in ``heads`` when given; other rows are 0).
+    ``q`` [Hq, M, D] fp16; ``kq``/``vq`` [Hkv, L, D] uint8 with rulers [Hkv, ceil(L/64), D]
+    (``used`` a multiple of 64); ``k_chunk``/``v_chunk`` [Hkv, m, D] fp16 with ``m >= M``: the
+    first ``m - M`` tokens are an fp16 history at positions ``used ..``, the last ``M`` the
+    chunk, so query token i sits at position ``used + m - M + i``. Token i attends to the cache
+    tokens [0, used), dequantized as ``dequantize_int8_token`` does, to the history and to chunk
+    tokens [0, i] — the reference's ``attend_prefill`` (``src/nova/kvattn.py:791-815``: causal
+    SDPA over the staged fp16 positions before and including each query) with the part already
+    quantized read from int8. Returns fp64 ``[Hq, M, D]`` (only the KV heads in ``heads`` when
+    given; other rows are 0).
     """
     q = np.asarray(q)
-    hq, m, d = q.shape
-    hkv = k_chunk.shape[0]
+    hq, n, d = q.shape
+    hkv, m = k_chunk.shape[0], k_chunk.shape[1]
+    assert m >= n, "the fp16 K/V must hold at least the chunk"
     gq = hq // hkv
     n_g = used // 64
-    out = np.zeros((hq, m, d))
+    out = np.zeros((hq, n, d))
     for h in (range(hkv) if heads is None else heads):
         if used:
             kc = okq.dequantize_int8_token(kq[h:h + 1, :used], kmn[h:h + 1, :n_g], kst[h:h + 1, :n_g], 64)[0]
@@ -139,7 +142,7 @@ def chunk_prefill_attend(q, kq, kmn, kst, vq, vmn, vst, used: int, k_chunk, v_ch
             k = k_chunk[h].astype(np.float64)
             v = v_chunk[h].astype(np.float64)
         keypos = np.arange(used + m)
-        mask = keypos[None, :] > (used + np.arange(m))[:, None]  # [M, used + M]
+        mask = keypos[None, :] > (used + m - n + np.arange(n))[:, None]  # [M, used + m]
         for j in range(gq):
             s = (q[h * gq + j].astype(np.float64) @ k.T) * d ** -0.5
             s[mask] = -np.inf

@@ -165,7 +165,7 @@ def test_chained_step_sizes_and_checks(lib):
     table = np.full((2, 13), fake, dtype=np.int64)
     scalars = [fake] * 5
     args = lambda hq, tab, n=2: ([fake, tab.ctypes.data, n, 128] + scalars  # noqa: E731
-                                 + [hq, 8, 128, 4096, fake, 1 << 24, 0, None])
+                                 + [hq, 8, 128, 4096, fake, 1 << 24, 0, 0, None])
     assert lib.nkv_decode_layers_t64(*args(30, table)) == _lib.NKV_ERR_INVALID
     assert b"divisible" in lib.nkv_last_error()
     bad = table.copy()
@@ -175,9 +175,67 @@ def test_chained_step_sizes_and_checks(lib):
     bad[1, 4] = fake + 8  # unaligned
     assert lib.nkv_decode_layers_t64(*args(32, bad)) == _lib.NKV_ERR_INVALID
     no_scalars = [fake, table.ctypes.data, 2, 128, fake, fake, None, fake, fake, 32, 8, 128, 4096, fake, 1 << 24, 0,
-                  None]
+                  0, None]
     assert lib.nkv_decode_layers_t64(*no_scalars) == _lib.NKV_ERR_INVALID
     tok = np.full((2, 9), fake, dtype=np.int64)
     assert lib.nkv_decode_layers_tok(fake, tok.ctypes.data, 2, 128, fake, fake, 32, 8, 128, 100, fake, 1 << 24, 0,
-                                     None) == _lib.NKV_ERR_INVALID
+                                     0, None) == _lib.NKV_ERR_INVALID
     assert b"multiple of 64" in lib.nkv_last_error()
+    assert lib.nkv_decode_layers_t64(*(args(32, table)[:-2] + [5, None])) == _lib.NKV_ERR_INVALID
+    assert b"NKV_DEP_ALL" in lib.nkv_last_error()
+
+
+def _chain_table(L: int, q_of, kv_of, gap: int = 1 << 16, tok: bool = False):
+    """A chained-step layer table of fake, aligned addresses: layer j's output at
+    base + j * (32 x 128 fp16 + gap); q_of(l) / kv_of(l) give layer l's q and k_new addresses
+    (v_new = k_new + 128 elements), the cache pointers lie far away."""
+    import numpy as np
+
+    base, out_bytes = 1 << 30, 32 * 128 * 2
+    out = [base + j * (out_bytes + gap) for j in range(L)]
+    cols = 9 if tok else 13
+    t = np.full((L, cols), 1 << 40, dtype=np.int64)
+    for l in range(L):
+        t[l, 0] = q_of(out, l)
+        t[l, 1] = kv_of(out, l)
+        t[l, 2] = kv_of(out, l) + 256
+        t[l, cols - 2] = out[l]
+        t[l, cols - 1] = 0  # no lse
+    return t
+
+
+def test_chained_step_input_rules(lib):
+    """The rows a chained layer may read from earlier outputs under each dependency mode
+    (host-only check, fake addresses): head-local views chain per head; another head's rows of
+    an earlier layer need its counter (always given); another head's rows of the previous step
+    (a later layer's output) need NKV_DEP_ALL; the same layer's output of another head, and rows
+    straddling two heads' rows, are refused."""
+    from nova_amd import _lib
+
+    L, HEAD, ALL, OK, BAD = 4, _lib.NKV_DEP_HEAD, _lib.NKV_DEP_ALL, _lib.NKV_OK, _lib.NKV_ERR_INVALID
+    prev = lambda out, l: out[(l - 1) % L]  # noqa: E731
+    cases = [
+        # (q, k_new, kv_head_stride, rc with HEAD, rc with ALL)
+        ("bench views", prev, lambda o, l: prev(o, l), 512, OK, OK),
+        ("k from the next KV head's rows", prev, lambda o, l: prev(o, l) + 4 * 128 * 2, 512, BAD, OK),
+        ("k straddling two heads' rows", prev, lambda o, l: prev(o, l) + 448 * 2, 512, BAD, BAD),
+        ("k from the same layer's output, next head", prev, lambda o, l: o[l] + 4 * 128 * 2, 512, BAD, BAD),
+        ("q and k in place, own head", lambda o, l: o[l], lambda o, l: o[l], 512, OK, OK),
+        ("k from two layers back, next head", prev, lambda o, l: o[(l - 2) % L] + 4 * 128 * 2, 512, BAD, OK),
+        ("inputs outside every output", lambda o, l: o[l] + 32 * 128 * 2, lambda o, l: o[l] + 32 * 128 * 2 + 4096,
+         256, OK, OK),
+    ]
+    for name, q_of, kv_of, hs, want_head, want_all in cases:
+        for tok in (False, True):
+            t = _chain_table(L, q_of, kv_of, tok=tok)
+            fn = lib.nkv_decode_layers_check_tok if tok else lib.nkv_decode_layers_check_t64
+            for dep, want in ((HEAD, want_head), (ALL, want_all)):
+                rc = fn(t.ctypes.data, L, hs, 32, 8, dep)
+                assert rc == want, f"{name} (tok={tok}, dep={dep}): {rc} {lib.nkv_last_error()}"
+    # layers 1.. read another head's rows of layer l - 1 (ordered by the counter), layer 0 reads
+    # its own head's rows of the last layer: accepted in both modes
+    kv = lambda o, l: prev(o, l) + (4 * 128 * 2 if l else 0)  # noqa: E731
+    t = _chain_table(L, prev, kv)
+    assert lib.nkv_decode_layers_check_t64(t.ctypes.data, L, 512, 32, 8, HEAD) == OK
+    assert lib.nkv_decode_layers_check_t64(None, L, 512, 32, 8, HEAD) == BAD
+    assert lib.nkv_decode_layers_check_t64(t.ctypes.data, L, 512, 32, 8, 2) == BAD

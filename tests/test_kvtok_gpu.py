@@ -16,6 +16,7 @@ import torch
 from oracle import attn as oattn
 from oracle import kvquant as okq
 from tests.helpers import D, H_KV, HQ, assert_ulp_or_abs, bench_outliers, make, npy, randn
+from tests.test_oracle import TOK_SPECIAL_CODES, TOK_SPECIAL_SCALES, _tok_special_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -33,6 +34,7 @@ def _quant_cases():
     x[1, 0, 6] = (torch.arange(D) - 64).to(torch.float16) * 1e-3   # tiny magnitudes
     yield "special", x
     yield "outliers", bench_outliers(randn((1, H_KV, 96, D), 12), seed=13)
+    yield "rounding", torch.from_numpy(_tok_special_rows()).reshape(1, 1, 2, D)
 
 
 @pytest.mark.parametrize("case", [c for c, _ in _quant_cases()])
@@ -46,6 +48,12 @@ def test_quantize_tok_bit_exact(case):
     np.testing.assert_array_equal(npy(s).view(np.uint16), ws.view(np.uint16))
     deq = dequantize_tok(q, s)
     np.testing.assert_array_equal(npy(deq).view(np.uint16), okq.dequantize_tok(wq, ws).view(np.uint16))
+    if case == "rounding":  # the literal codes and scales (round half to even, fp32 scale)
+        for r in range(2):
+            n = len(TOK_SPECIAL_CODES[r])
+            assert npy(q)[0, 0, r, :n].tolist() == TOK_SPECIAL_CODES[r]
+            assert not npy(q)[0, 0, r, n:].any()
+            assert int(npy(s)[0, 0, r:r + 1].view(np.uint16)[0]) == TOK_SPECIAL_SCALES[r]
 
 
 def test_quantize_tok_strided_slabs():

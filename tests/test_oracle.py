@@ -146,6 +146,46 @@ def test_tok_scheme_closed_form():
     np.testing.assert_array_equal(okq.dequantize_tok(qz, sz), z)
 
 
+def _tok_special_rows() -> np.ndarray:
+    """Two fp16 rows of 128 whose codes pin the per-token symmetric quantizer's rounding:
+    row 0 has absmax 127, so its fp32 scale is exactly 1.0 and x / scale is x itself: the ties
+    +-0.5, +-1.5, +-2.5, 3.5 code to 0, 0, +-2, +-2, 4 under round-half-to-even (half away from
+    zero would give +-1, +-2, +-3, 4). Row 1 has absmax 3: fp32 scale 3 / 127, fp16 scale
+    0.02362060546875 (0x260C); 1.759765625 / fp32 scale = 74.4967.. codes to 74, while dividing
+    by the fp16 scale (74.502..) would give 75."""
+    x = np.zeros((2, 128), np.float16)
+    x[0, :8] = [127.0, 0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 3.5]
+    x[1, :3] = [3.0, 1.759765625, -1.759765625]
+    return x
+
+
+TOK_SPECIAL_CODES = ([127, 0, 0, 2, -2, 2, -2, 4], [127, 74, -74])
+TOK_SPECIAL_SCALES = (0x3C00, 0x260C)
+
+
+def test_tok_scheme_rounding_conventions():
+    """The tie and scale-rounding rows code to the literal values above, and both pins
+    discriminate: half-away-from-zero rounding, or codes computed with the stored fp16 scale,
+    would differ on them."""
+    from fractions import Fraction
+
+    x = _tok_special_rows()
+    q, s = okq.quantize_tok(x)
+    for r in range(2):
+        want = np.zeros(128, np.int8)
+        want[:len(TOK_SPECIAL_CODES[r])] = TOK_SPECIAL_CODES[r]
+        np.testing.assert_array_equal(q[r], want)
+        assert int(s[r:r + 1].view(np.uint16)[0]) == TOK_SPECIAL_SCALES[r]
+    # the alternatives the rows rule out
+    half_away = np.sign(x[0, :8].astype(np.float32)) * np.floor(np.abs(x[0, :8].astype(np.float32)) + 0.5)
+    assert not np.array_equal(half_away.astype(np.int8), q[0, :8])
+    by_fp16_scale = np.rint(np.float32(1.759765625) / s[1].astype(np.float32))
+    assert by_fp16_scale == 75 and q[1, 1] == 74
+    # 74: the exact quotient by the fp32 scale, in rationals
+    s32 = np.float32(np.float32(3.0) / np.float32(127.0))
+    assert round(Fraction(1.759765625) / Fraction(float(s32))) == 74
+
+
 def test_bytes_accounting_matches_reference():
     """``tests/test_kvquant.py:261-270``: int8 is 1.85-1.95x smaller and ~77.6 KiB/token."""
     gold = json.loads((GOLD / "bytes.json").read_text())
@@ -356,6 +396,42 @@ def test_chunk_prefill_oracle_pinned():
     vqc, vmc, vsc = okq.quantize_int8_token(np.full_like(vc, 0.375), 64)
     const = oattn.chunk_prefill_attend(q, kq, kmn, kst, vqc, vmc, vsc, used, k_ch, vconst)
     np.testing.assert_allclose(const, np.full_like(const, 0.375), rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("used,hist", [(0, 192), (512, 192), (128, 5)])
+def test_chunk_prefill_with_fp16_history(used, hist):
+    """An fp16 history before the chunk (the staged prefill's later chunks): against torch's
+    SDPA in float64 with the causal mask shifted by the history, and equal to the last rows of
+    the same attention computed for history and chunk together as one chunk (the rows of a
+    causal attention do not depend on the other queries)."""
+    rng = np.random.default_rng(used + hist)
+    hq, hkv, d, n = 8, 2, 128, 37
+    m = hist + n
+    kc = (rng.standard_normal((hkv, max(used, 64), d)) * 0.7).astype(np.float16)
+    vc = (rng.standard_normal((hkv, max(used, 64), d)) * 0.7).astype(np.float16)
+    kq, kmn, kst = okq.quantize_int8_token(kc, 64)
+    vq, vmn, vst = okq.quantize_int8_token(vc, 64)
+    k16 = (rng.standard_normal((hkv, m, d)) * 0.7).astype(np.float16)
+    v16 = (rng.standard_normal((hkv, m, d)) * 0.7).astype(np.float16)
+    q_all = (rng.standard_normal((hq, m, d)) * 0.7).astype(np.float16)
+    q = q_all[:, hist:]
+    got = oattn.chunk_prefill_attend(q, kq, kmn, kst, vq, vmn, vst, used, k16, v16)
+    whole = oattn.chunk_prefill_attend(q_all, kq, kmn, kst, vq, vmn, vst, used, k16, v16)
+    np.testing.assert_allclose(got, whole[:, hist:], rtol=0, atol=1e-13)
+    kd = okq.dequantize_int8_token(kq, kmn, kst, 64)[:, :used]
+    vd = okq.dequantize_int8_token(vq, vmn, vst, 64)[:, :used]
+    kall = np.concatenate([kd, k16], 1).astype(np.float64)
+    vall = np.concatenate([vd, v16], 1).astype(np.float64)
+    kt = torch.from_numpy(kall).repeat_interleave(hq // hkv, 0)
+    vt = torch.from_numpy(vall).repeat_interleave(hq // hkv, 0)
+    mask = torch.arange(used + m)[None, :] <= (used + hist + torch.arange(n))[:, None]
+    sd = torch.nn.functional.scaled_dot_product_attention(torch.from_numpy(q.astype(np.float64))[None], kt[None],
+                                                          vt[None], attn_mask=mask)[0]
+    np.testing.assert_allclose(got, sd.numpy(), rtol=0, atol=1e-10)
+    # the first query sees the whole history: dropping the history's last token changes it
+    drop = lambda x: np.concatenate([x[:, :hist - 1], x[:, hist:hist + 1]], 1)  # noqa: E731
+    short = oattn.chunk_prefill_attend(q[:, :1], kq, kmn, kst, vq, vmn, vst, used, drop(k16), drop(v16))
+    assert np.abs(short[:, 0] - got[:, 0]).max() > 1e-6
 
 
 # ---------------------------------------------------------------- torch fp32 restatement (CPU baseline)

@@ -104,3 +104,47 @@ def test_prefill_scores_that_move_the_softmax_reference(profile):
     packed = [t.contiguous() for t in pack_int8_kv(kf.half().cuda(), v.cuda())]
     got = int8_prefill_attend(q, kch, vch, *packed, used=used)
     _check(got, q, kch, vch, packed, used, tag=profile)
+
+
+@pytest.mark.parametrize("used,n", [(0, 64), (0, 130), (512, 64), (512, 130)])
+def test_prefill_with_fp16_history(used, n):
+    """The fp16-history branch (``m > n``: a staged prefill's later chunks attend the earlier
+    ones in fp16): 192 history tokens before the chunk, after ``used`` int8 tokens."""
+    from nova_amd.kvattn import int8_prefill_attend
+
+    hist = 192
+    print(f"case history used={used} hist={hist} n={n}", flush=True)
+    q, kch, vch, packed = _case(32, 8, used, hist + n, seed=100 + used + n)
+    q = q[:, :, hist:].contiguous()
+    got = int8_prefill_attend(q, kch, vch, *packed, used=used)
+    _check(got, q, kch, vch, packed, used, tag=f"history used={used} n={n}")
+
+
+def test_staged_prefill_in_three_chunks_against_oracle():
+    """``KVInt8Cache`` staged prefill in three chunks of 100, 130 and 70 tokens over two layers:
+    every chunk's ``attend_prefill`` output (chunks 2 and 3 read the earlier chunks from the fp16
+    staging area) against the oracle's causal attention over the fp16 tokens up to it."""
+    from nova_amd.kvattn import KVInt8Cache
+
+    print("case staged prefill 3 chunks", flush=True)
+    L, hq, hkv, total, chunks = 2, 32, 8, 300, (100, 130, 70)
+    cache = KVInt8Cache(num_slots=L, num_kv_heads=hkv, head_dim=D, max_len=512, num_q_heads=hq)
+    ks = [randn((1, hkv, total, D), 110 + l, 1.0) for l in range(L)]
+    vs = [randn((1, hkv, total, D), 120 + l, 1.0) for l in range(L)]
+    qs = [randn((1, hq, total, D), 130 + l, 1.0) for l in range(L)]
+    none8 = np.zeros((hkv, 64, D), np.uint8)
+    none16 = np.zeros((hkv, 1, D), np.float16)
+    cache.begin_prefill(total)
+    off = 0
+    for n in chunks:
+        cache.set_prefill_pos(off)
+        for l in range(L):
+            cache.update(ks[l][:, :, off:off + n].cuda(), vs[l][:, :, off:off + n].cuda(), l)
+            got = npy(cache.attend_prefill(qs[l][:, :, off:off + n].cuda(), l))[0].astype(np.float64)
+            want = oattn.chunk_prefill_attend(npy(qs[l])[0, :, off:off + n], none8, none16, none16, none8, none16,
+                                              none16, 0, npy(ks[l])[0, :, :off + n], npy(vs[l])[0, :, :off + n])
+            err = np.abs(got - want)
+            assert err.max() <= 2e-3 and err.mean() <= 1.5e-4, (f"chunk at {off} layer {l}: max {err.max():.2e} "
+                                                                 f"mean {err.mean():.2e}")
+        off += n
+    cache.finish_prefill(total)
