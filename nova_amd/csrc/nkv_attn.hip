@@ -149,6 +149,11 @@ struct AttnArgs {
   // it reads (written by its own head's merger); 1, every input of layer l also waits until every
   // head's merger has finished layer l - 1
   int dep_all;
+  // the chained step with dep_all: this layer's `issued` counter. Every merger adds its gq query
+  // heads to it (relaxed, agent scope) as soon as their outputs' stores are issued (a merging wave
+  // adds 1 for its own head); the readers of layer l + 1 wait for it to reach hq. Null otherwise.
+  int* issued_ctr;
+  int n_layers;
 };
 
 // XOR key of the 16-byte chunk positions of LDS row `row` (a token within its group).
@@ -1750,6 +1755,9 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
                              __HIP_MEMORY_SCOPE_AGENT);
         if (a.lse && lane == 0)
           a.lse[qh] = failed ? __builtin_nanf("") : (lt > 0.0f ? (M + __log2f(lt) - P_SCALE_LOG2) * LN2 : NEG_INF);
+        // this head's outputs are issued: count it for the readers of the next layer (they
+        // validate the words themselves, so no ordering is needed)
+        if (a.issued_ctr && lane == 0) __hip_atomic_fetch_add(a.issued_ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       } else {
         *reinterpret_cast<float2*>(sm.pre_acc + head0 * D + 2 * lane) = acc;
         if (lane == 0) {
@@ -1878,6 +1886,10 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (a.lse && d == 0) a.lse[qh] = failed ? __builtin_nanf("") : (l > 0.0f ? (M + __log2f(l) - P_SCALE_LOG2) * LN2 : NEG_INF);
+  }
+  if (a.issued_ctr) {  // every column issued: the workgroup's gq heads count at once
+    __syncthreads();
+    if (tid == 0) __hip_atomic_fetch_add(a.issued_ctr, gq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   // ---- every word of the head's partials was consumed before the barrier above: the whole
   // block [hws, hws + P pw) goes back to zero (plain 16-byte stores by every thread; pw is a
@@ -2142,8 +2154,10 @@ constexpr uint64_t LAYER_WAIT_TICKS = 20000000ull;  // 0.2 s of the 100 MHz real
 
 // The sync words of a chained launch at the workspace's end (tail_ctr_end): done[l] at
 // end[-1 - l], the exit ticket at end[-1 - n_layers], the error word at end[-2 - n_layers], the
-// launch counter (the forwarding tags) at end[-3 - n_layers].
+// launch counter (the forwarding tags) at end[-3 - n_layers], issued[l] at end[-4 - n_layers - l].
 __device__ __forceinline__ int* layer_done(const AttnArgs& a, int l) { return a.tail_ctr_end - 1 - l; }
+// issued[l] (dep_all) below them: at end[-4 - n_layers - l]
+__device__ __forceinline__ int* layer_issued(const AttnArgs& a, int l) { return a.tail_ctr_end - 4 - a.n_layers - l; }
 
 // Layer l's arguments: the cache and step pointers of its table entry (nkv_layer_t64, or
 // nkv_layer_tok for the per-token symmetric format), and its own partial block.
@@ -2180,6 +2194,7 @@ __device__ __forceinline__ AttnArgs layer_args(const AttnArgs& a, const void* la
   }
   la.ws = a.ws + (int64_t)l * a.hkv * a.n_parts * part_stride(a.gq);
   la.fwd_out = a.fwd_out + (int64_t)l * a.hq * D / 2;  // (read by layer l + 1 only)
+  la.issued_ctr = a.dep_all ? layer_issued(a, l) : nullptr;
   return la;
 }
 
@@ -2297,7 +2312,7 @@ __device__ __forceinline__ bool merger_layer(const AttnArgs& args, const void* l
       const uint64_t* src = la.fwd_out - (int64_t)la.hq * D / 2;  // layer l - 1's tagged words
       ok = fwd_fetch(src + (int64_t)h * gq * D / 2, src + ((la.k_new - prev) + (int64_t)h * la.kv_hs) / 2,
                      src + ((la.v_new - prev) + (int64_t)h * la.kv_hs) / 2, gq, la.ftag, sm.fwd, lost,
-                     la.dep_all ? layer_done(la, l - 1) : nullptr, la.hkv);
+                     la.dep_all ? layer_issued(la, l - 1) : nullptr, la.hq);
     } else if (l > 0) {
       ok = wait_layer(la, l - 1, la.hkv, lost);
     }
@@ -2404,7 +2419,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
         // q is layer l - 1's output: its tagged words (head h's rows, written by head h's merger),
         // and with dep_all layer l - 1's counter as well
         ok = fwd_fetch(la.fwd_out - (int64_t)la.hq * D / 2 + (int64_t)h * gq * D / 2, nullptr, nullptr, gq, la.ftag,
-                       reinterpret_cast<uint32_t*>(q_lds), lost, a.dep_all ? layer_done(a, l - 1) : nullptr, a.hkv);
+                       reinterpret_cast<uint32_t*>(q_lds), lost, a.dep_all ? layer_issued(a, l - 1) : nullptr, a.hq);
       } else {
         ok = l == 0 || wait_layer(a, l - 1, a.hkv, lost);
         issue_q(la.q + (int64_t)h * gq * D, gq, __builtin_amdgcn_readfirstlane(lds_addr(q_lds)));
@@ -2559,7 +2574,10 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
     if (lost) __hip_atomic_store(exit_ctr - 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int t = __hip_atomic_fetch_add(exit_ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (t == (int)gridDim.x - 1) {
-      for (int l = 0; l < n_layers; ++l) __hip_atomic_store(layer_done(a, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int l = 0; l < n_layers; ++l) {
+        __hip_atomic_store(layer_done(a, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(layer_issued(a, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       __hip_atomic_store(exit_ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(epoch, (int)ftag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -3639,7 +3657,8 @@ int layers_resident(bool tok, int* out) {
 }
 
 // n_layers counters, the exit ticket, the error word, the launch counter
-int64_t layers_sync_bytes(int64_t n_layers) { return ctr_bytes(n_layers + 3); }
+// n_layers counters, the exit ticket, the error word, the launch counter, n_layers issued counters
+int64_t layers_sync_bytes(int64_t n_layers) { return ctr_bytes(2 * n_layers + 3); }
 // each layer's output as tagged words (forwarded to the next layer's inputs)
 int64_t layers_fwd_bytes(int64_t hq, int64_t n_layers) { return n_layers * hq * D / 2 * (int64_t)sizeof(uint64_t); }
 
@@ -3718,6 +3737,7 @@ int launch_layers(AttnArgs& a, bool tok, const void* layers_dev, int64_t n_layer
   if (workspace_bytes < need)
     return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
   a.n_parts = (int)n_parts;
+  a.n_layers = (int)n_layers;
   a.tail_ctr_end = reinterpret_cast<int*>(reinterpret_cast<char*>(a.ws) + (workspace_bytes & ~int64_t(3)));
   a.fwd_out = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(a.ws) + part_bytes);
   if (tok) hipLaunchKernelGGL(attn_layers_kernel<CONTIG_TOK>, dim3((unsigned)grid), dim3(THREADS), 0, s, a, layers_dev, (int)n_layers);
