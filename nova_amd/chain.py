@@ -149,10 +149,10 @@ class ChainedStep:
 
     def _sync_words(self) -> list:
         """The sync words at the workspace's end, from the last: the layer counters, the exit
-        ticket, the error word, the launch counter, the layers' issued counters (synchronizes)."""
+        ticket, the error word, the launch counter (synchronizes)."""
         end = (self.ws_bytes & ~3) // 4
         n = self.n_layers
-        return self.workspace[end - 2 * n - 3:end].flip(0).tolist()
+        return self.workspace[end - n - 3:end].flip(0).tolist()
 
     def gave_up(self) -> bool:
         """Whether a launch's wait ever gave up (its outputs are then NaN). Synchronizes."""
@@ -176,4 +176,4 @@ class ChainedStep:
         w = self._sync_words()
         n = self.n_layers
         return {"partials_zero": bool(int(self.workspace[:part_words].abs().sum().item()) == 0),
-                "counters_zero": all(x == 0 for x in w[:n + 1] + w[n + 3:]), "error": w[n + 1], "launches": w[n + 2]}
+                "counters_zero": all(x == 0 for x in w[:n + 1]), "error": w[n + 1], "launches": w[n + 2]}

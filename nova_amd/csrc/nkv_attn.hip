@@ -149,10 +149,11 @@ struct AttnArgs {
   // it reads (written by its own head's merger); 1, every input of layer l also waits until every
   // head's merger has finished layer l - 1
   int dep_all;
-  // the chained step with dep_all: this layer's `issued` counter. Every merger adds its gq query
-  // heads to it (relaxed, agent scope) as soon as their outputs' stores are issued (a merging wave
-  // adds 1 for its own head); the readers of layer l + 1 wait for it to reach hq. Null otherwise.
-  int* issued_ctr;
+  // the chained step with dep_all: this layer's issue flags, one word per query head, set to the
+  // launch's tag (relaxed, agent scope) as soon as that head's output stores are issued; the
+  // readers of layer l + 1 wait until all hq carry the tag. Null otherwise.
+  uint32_t* issue_flags;
+  uint32_t* flags_base;  // layer 0's issue flags; layer l's at flags_base + l hq
   int n_layers;
 };
 
@@ -1757,7 +1758,8 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
           a.lse[qh] = failed ? __builtin_nanf("") : (lt > 0.0f ? (M + __log2f(lt) - P_SCALE_LOG2) * LN2 : NEG_INF);
         // this head's outputs are issued: count it for the readers of the next layer (they
         // validate the words themselves, so no ordering is needed)
-        if (a.issued_ctr && lane == 0) __hip_atomic_fetch_add(a.issued_ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a.issue_flags && lane == 0)
+          __hip_atomic_store(a.issue_flags + qh, a.ftag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       } else {
         *reinterpret_cast<float2*>(sm.pre_acc + head0 * D + 2 * lane) = acc;
         if (lane == 0) {
@@ -1887,9 +1889,9 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     }
     if (a.lse && d == 0) a.lse[qh] = failed ? __builtin_nanf("") : (l > 0.0f ? (M + __log2f(l) - P_SCALE_LOG2) * LN2 : NEG_INF);
   }
-  if (a.issued_ctr) {  // every column issued: the workgroup's gq heads count at once
+  if (a.issue_flags) {  // every column issued: the workgroup's gq heads flagged at once
     __syncthreads();
-    if (tid == 0) __hip_atomic_fetch_add(a.issued_ctr, gq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < gq) __hip_atomic_store(a.issue_flags + qh0 + tid, a.ftag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   // ---- every word of the head's partials was consumed before the barrier above: the whole
   // block [hws, hws + P pw) goes back to zero (plain 16-byte stores by every thread; pw is a
@@ -2154,10 +2156,11 @@ constexpr uint64_t LAYER_WAIT_TICKS = 20000000ull;  // 0.2 s of the 100 MHz real
 
 // The sync words of a chained launch at the workspace's end (tail_ctr_end): done[l] at
 // end[-1 - l], the exit ticket at end[-1 - n_layers], the error word at end[-2 - n_layers], the
-// launch counter (the forwarding tags) at end[-3 - n_layers], issued[l] at end[-4 - n_layers - l].
+// launch counter (the forwarding tags) at end[-3 - n_layers].
 __device__ __forceinline__ int* layer_done(const AttnArgs& a, int l) { return a.tail_ctr_end - 1 - l; }
 // issued[l] (dep_all) below them: at end[-4 - n_layers - l]
-__device__ __forceinline__ int* layer_issued(const AttnArgs& a, int l) { return a.tail_ctr_end - 4 - a.n_layers - l; }
+// issue flags of layer l (dep_all): hq words after the tagged outputs of every layer
+__device__ __forceinline__ uint32_t* layer_flags(const AttnArgs& a, int l) { return a.flags_base + (int64_t)l * a.hq; }
 
 // Layer l's arguments: the cache and step pointers of its table entry (nkv_layer_t64, or
 // nkv_layer_tok for the per-token symmetric format), and its own partial block.
@@ -2194,7 +2197,7 @@ __device__ __forceinline__ AttnArgs layer_args(const AttnArgs& a, const void* la
   }
   la.ws = a.ws + (int64_t)l * a.hkv * a.n_parts * part_stride(a.gq);
   la.fwd_out = a.fwd_out + (int64_t)l * a.hq * D / 2;  // (read by layer l + 1 only)
-  la.issued_ctr = a.dep_all ? layer_issued(a, l) : nullptr;
+  la.issue_flags = a.dep_all ? layer_flags(a, l) : nullptr;
   return la;
 }
 
@@ -2215,22 +2218,22 @@ __device__ __forceinline__ bool within(const uint16_t* p, int64_t n, const uint1
 // l - 1): lane i takes words i + 64 j, reloading those whose tag is not yet `tag` (relaxed
 // agent-scope loads: per-location coherence hands over each word once written, no counter or
 // fence), and stores their fp16 pairs to LDS at `dst` (q rows, then k_new, then v_new).
-// With `ctr` (the all-head dependency), lane 0 also polls that counter in the same rounds until
-// it reaches `target`: the wait ends when every word carries the tag and the counter is reached,
-// with no extra round trip. The counter only orders (the words validate themselves), so its
-// polls are relaxed and no fence follows.
+// With `flags` (the all-head dependency: the layer's issue flags, nflags <= 64 of them), lane i
+// also polls flag i in the same rounds until it carries the tag: the wait ends when every word
+// and every flag does, with no extra round trip. The flags only order (the words validate
+// themselves), so their polls are relaxed and no fence follows.
 // gq <= FWD_MAX_GQ. false when the wait gave up (after LAYER_WAIT_TICKS, or at once with `lost`).
 constexpr int FWD_MAX_GQ = 4;
 __device__ __forceinline__ bool fwd_fetch(const uint64_t* q, const uint64_t* k, const uint64_t* v, int gq,
-                                          uint32_t tag, uint32_t* dst, bool lost, const int* ctr = nullptr,
-                                          int target = 0) {
+                                          uint32_t tag, uint32_t* dst, bool lost, const uint32_t* flags = nullptr,
+                                          int nflags = 0) {
   const int lane = tail_tid() & 63;
   uint64_t w[FWD_MAX_GQ + 2];
 #pragma unroll
   for (int j = 0; j < FWD_MAX_GQ + 2; ++j) w[j] = 0;  // (tag 0 is never current)
   const bool kv = k != nullptr;
   bool ok = !lost;
-  int c = ctr != nullptr && lane == 0 ? target - 1 : target;  // (only lane 0 polls the counter)
+  uint32_t fl = flags != nullptr && lane < nflags ? 0u : tag;  // (lanes beyond nflags poll nothing)
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   while (ok) {
 #pragma unroll
@@ -2240,8 +2243,8 @@ __device__ __forceinline__ bool fwd_fetch(const uint64_t* q, const uint64_t* k, 
       w[FWD_MAX_GQ] = __hip_atomic_load(k + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (kv && (uint32_t)(w[FWD_MAX_GQ + 1] >> 32) != tag)
       w[FWD_MAX_GQ + 1] = __hip_atomic_load(v + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (c < target) c = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    bool miss = c < target;
+    if (fl != tag) fl = __hip_atomic_load(flags + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool miss = fl != tag;
 #pragma unroll
     for (int j = 0; j < FWD_MAX_GQ; ++j) miss |= j < gq && (uint32_t)(w[j] >> 32) != tag;
     miss |= kv && ((uint32_t)(w[FWD_MAX_GQ] >> 32) != tag || (uint32_t)(w[FWD_MAX_GQ + 1] >> 32) != tag);
@@ -2312,7 +2315,7 @@ __device__ __forceinline__ bool merger_layer(const AttnArgs& args, const void* l
       const uint64_t* src = la.fwd_out - (int64_t)la.hq * D / 2;  // layer l - 1's tagged words
       ok = fwd_fetch(src + (int64_t)h * gq * D / 2, src + ((la.k_new - prev) + (int64_t)h * la.kv_hs) / 2,
                      src + ((la.v_new - prev) + (int64_t)h * la.kv_hs) / 2, gq, la.ftag, sm.fwd, lost,
-                     la.dep_all ? layer_issued(la, l - 1) : nullptr, la.hq);
+                     la.dep_all ? layer_flags(la, l - 1) : nullptr, la.hq);
     } else if (l > 0) {
       ok = wait_layer(la, l - 1, la.hkv, lost);
     }
@@ -2419,7 +2422,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
         // q is layer l - 1's output: its tagged words (head h's rows, written by head h's merger),
         // and with dep_all layer l - 1's counter as well
         ok = fwd_fetch(la.fwd_out - (int64_t)la.hq * D / 2 + (int64_t)h * gq * D / 2, nullptr, nullptr, gq, la.ftag,
-                       reinterpret_cast<uint32_t*>(q_lds), lost, a.dep_all ? layer_issued(a, l - 1) : nullptr, a.hq);
+                       reinterpret_cast<uint32_t*>(q_lds), lost, a.dep_all ? layer_flags(a, l - 1) : nullptr, a.hq);
       } else {
         ok = l == 0 || wait_layer(a, l - 1, a.hkv, lost);
         issue_q(la.q + (int64_t)h * gq * D, gq, __builtin_amdgcn_readfirstlane(lds_addr(q_lds)));
@@ -2574,10 +2577,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
     if (lost) __hip_atomic_store(exit_ctr - 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int t = __hip_atomic_fetch_add(exit_ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (t == (int)gridDim.x - 1) {
-      for (int l = 0; l < n_layers; ++l) {
-        __hip_atomic_store(layer_done(a, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(layer_issued(a, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      for (int l = 0; l < n_layers; ++l) __hip_atomic_store(layer_done(a, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(exit_ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(epoch, (int)ftag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -3657,10 +3657,13 @@ int layers_resident(bool tok, int* out) {
 }
 
 // n_layers counters, the exit ticket, the error word, the launch counter
-// n_layers counters, the exit ticket, the error word, the launch counter, n_layers issued counters
-int64_t layers_sync_bytes(int64_t n_layers) { return ctr_bytes(2 * n_layers + 3); }
+// n_layers counters, the exit ticket, the error word, the launch counter
+int64_t layers_sync_bytes(int64_t n_layers) { return ctr_bytes(n_layers + 3); }
 // each layer's output as tagged words (forwarded to the next layer's inputs)
-int64_t layers_fwd_bytes(int64_t hq, int64_t n_layers) { return n_layers * hq * D / 2 * (int64_t)sizeof(uint64_t); }
+// (and, after them, each layer's issue flags: one word per query head)
+int64_t layers_fwd_bytes(int64_t hq, int64_t n_layers) {
+  return n_layers * hq * D / 2 * (int64_t)sizeof(uint64_t) + n_layers * hq * (int64_t)sizeof(uint32_t);
+}
 
 // Streaming parts per KV head: one workgroup per 8 groups at most, and hkv (parts + 1) workgroups
 // resident at once.
@@ -3736,10 +3739,12 @@ int launch_layers(AttnArgs& a, bool tok, const void* layers_dev, int64_t n_layer
   if (!a.ws || !al16(a.ws)) return fail(NKV_ERR_INVALID, "%s: the workspace must be a non-null, 16-byte aligned buffer", what);
   if (workspace_bytes < need)
     return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
+  if (a.dep_all && a.hq > 64) return fail(NKV_ERR_UNSUPPORTED, "%s: the all-head dependency polls at most 64 query heads' flags", what);
   a.n_parts = (int)n_parts;
   a.n_layers = (int)n_layers;
   a.tail_ctr_end = reinterpret_cast<int*>(reinterpret_cast<char*>(a.ws) + (workspace_bytes & ~int64_t(3)));
   a.fwd_out = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(a.ws) + part_bytes);
+  a.flags_base = reinterpret_cast<uint32_t*>(a.fwd_out + n_layers * a.hq * D / 2);
   if (tok) hipLaunchKernelGGL(attn_layers_kernel<CONTIG_TOK>, dim3((unsigned)grid), dim3(THREADS), 0, s, a, layers_dev, (int)n_layers);
   else hipLaunchKernelGGL(attn_layers_kernel<CONTIG_T64>, dim3((unsigned)grid), dim3(THREADS), 0, s, a, layers_dev, (int)n_layers);
   return check_launch(what);

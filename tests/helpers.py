@@ -47,9 +47,12 @@ def ulp(got: np.ndarray, want: np.ndarray) -> np.ndarray:
 
 
 def assert_ulp_or_abs(got, want, max_ulp: float, abs_tol: float, tag: str = "") -> dict:
-    """Every element within ``max_ulp`` fp16 ULP or ``abs_tol`` absolute of ``want``."""
+    """Every element within ``max_ulp`` fp16 ULP or ``abs_tol`` absolute of ``want``; every
+    element of ``got`` and ``want`` finite (a NaN fails the comparisons, so it is checked first)."""
     got = np.asarray(got, dtype=np.float32)
     want = np.asarray(want)
+    assert np.isfinite(got).all(), f"{tag}: {int((~np.isfinite(got)).sum())} non-finite outputs"
+    assert np.isfinite(want.astype(np.float64)).all(), f"{tag}: non-finite reference values"
     u = ulp(got, want)
     diff = np.abs(got.astype(np.float64) - want.astype(np.float16).astype(np.float64))
     bad = (u > max_ulp) & (diff > abs_tol)
