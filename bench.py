@@ -126,7 +126,11 @@ def parse_args():
     ap.add_argument("--traffic-key", choices=sorted(TRAFFIC), default="chain_t64")
     ap.add_argument("--stats-from", metavar="OUT_DIR", help="summarize a rocprofv3 --kernel-trace --stats run")
     ap.add_argument("--stats-name", help="--stats-from: the summary's file name under profiles/")
-    ap.add_argument("--stats-cmd", help="--stats-from: the command that was profiled")
+    ap.add_argument("--stats-cmd", help="--stats-from / --counters-from: the command that was profiled")
+    ap.add_argument("--counters-from", nargs="+", metavar="OUT_DIR",
+                    help="summarize rocprofv3 --pmc runs (one per counter set) of one kernel")
+    ap.add_argument("--counters-kernel", help="--counters-from: the kernel's name (a substring)")
+    ap.add_argument("--counters-name", help="--counters-from: the summary's file name under profiles/")
     return ap.parse_args()
 
 
@@ -188,6 +192,53 @@ def read_traffic(key: str):
         return None
     m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text(), re.M)
     return float(m.group(1)) if m else None
+
+
+def write_counters(dirs: list, kernel: str, name: str, cmd: str) -> None:
+    """Per-dispatch means of every counter that rocprofv3 --pmc runs (one directory per counter
+    set) recorded for ``kernel``, with the derived MFMA, VALU and LDS figures when their counters
+    are present."""
+    import csv
+
+    acc: dict = {}
+    sets = []
+    for d in dirs:
+        names = set()
+        for f in sorted(Path(d).rglob("*counter_collection.csv")):
+            with open(f, newline="") as fh:
+                for row in csv.DictReader(fh):
+                    if kernel in row["Kernel_Name"]:
+                        acc.setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+                        names.add(row["Counter_Name"])
+        sets.append(sorted(names))
+    mean = {k: sum(v) / len(v) for k, v in acc.items()}
+    lines = [f"# rocprofv3 counters of nkv::{kernel}, per dispatch (mean over the dispatches of each pass)",
+             "# made by (from the repository root, one MI355X; one pass per counter set):"]
+    lines += [f"#   rocprofv3 --pmc {' '.join(cs)} -d OUT{i + 1} -o run --output-format csv -- {cmd}"
+              for i, cs in enumerate(sets)]
+    lines.append(f"#   python3 bench.py --counters-from {' '.join(f'OUT{i + 1}' for i in range(len(sets)))} "
+                 f"--counters-kernel '{kernel}' --counters-name {name} --stats-cmd '{cmd}'")
+    lines += [f"{k:<28} {v:>14.4g}" for k, v in sorted(mean.items())]
+    der = []
+    if "GRBM_GUI_ACTIVE" in mean:
+        der.append(f"cycles per XCD: {mean['GRBM_GUI_ACTIVE'] / 8:.4g}")
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in mean and "GRBM_GUI_ACTIVE" in mean:
+        der.append(f"MFMA pipe busy: {mean['SQ_VALU_MFMA_BUSY_CYCLES'] / 1024 / (mean['GRBM_GUI_ACTIVE'] / 8):.3f} of each "
+                   "SIMD's cycles (SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs / cycles per XCD)")
+    if "SQ_INSTS_VALU" in mean and "SQ_INSTS_MFMA" in mean:
+        der.append(f"VALU instructions per MFMA: {mean['SQ_INSTS_VALU'] / mean['SQ_INSTS_MFMA']:.2f}")
+    if "SQ_INSTS_VALU" in mean and "GRBM_GUI_ACTIVE" in mean:
+        der.append(f"VALU issue: {mean['SQ_INSTS_VALU'] / 1024 * 4 / (mean['GRBM_GUI_ACTIVE'] / 8):.3f} of each SIMD's "
+                   "cycles (4 cycles per wave64 instruction)")
+    if "SQ_LDS_BANK_CONFLICT" in mean and "SQ_LDS_IDX_ACTIVE" in mean:
+        der.append(f"LDS bank-conflict share of LDS-active cycles: "
+                   f"{mean['SQ_LDS_BANK_CONFLICT'] / mean['SQ_LDS_IDX_ACTIVE']:.3f}")
+    if "SQ_LDS_IDX_ACTIVE" in mean and "GRBM_GUI_ACTIVE" in mean:
+        der.append(f"LDS active: {mean['SQ_LDS_IDX_ACTIVE'] / 256 / (mean['GRBM_GUI_ACTIVE'] / 8):.3f} of each CU's cycles")
+    if der:
+        lines += ["# derived:"] + [f"#   {x}" for x in der]
+    (PROFILES / name).write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
 
 
 def write_stats(out_dir: str, name: str, cmd: str) -> None:
@@ -765,6 +816,11 @@ def main() -> int:
     args = parse_args()
     if args.traffic_from:
         write_traffic(*args.traffic_from, key=args.traffic_key)
+        return 0
+    if args.counters_from:
+        if not args.counters_kernel or not args.counters_name or not args.stats_cmd:
+            raise SystemExit("--counters-from needs --counters-kernel, --counters-name and --stats-cmd")
+        write_counters(args.counters_from, args.counters_kernel, args.counters_name, args.stats_cmd)
         return 0
     if args.stats_from:
         if not args.stats_name or not args.stats_cmd:

@@ -326,9 +326,11 @@ int nkv_decode_step_combine_tok(const uint16_t* q, const uint16_t* k_new, const 
  *    in the rows of that output that head h's merger writes (its q heads h gq .. h gq + gq - 1).
  *    With NKV_DEP_HEAD nothing else is waited for: each KV head's layers then chain on their
  *    own, and head h may start layer l before another head has finished layer l - 1. With
- *    NKV_DEP_ALL every input of layer l is read only after every head's merger has finished
- *    layer l - 1 (its completion counter, polled in the same rounds as the words), which is the
- *    dependency of a model, where every q head of layer l depends on every head of layer l - 1.
+ *    NKV_DEP_ALL every input of layer l is read only after every query head's output of layer
+ *    l - 1 has been issued: each merging wave sets its head's issue flag of the layer to the
+ *    launch's tag right after its output stores, and the reader polls all hq (<= 64) flags in the
+ *    same rounds as its words. That is the dependency of a model, where every q head of layer l
+ *    depends on every head of layer l - 1.
  *  - Every other input of layer l is read after layer l - 1's completion counter has reached
  *    hkv (an agent-scope release by each merger, acquire by the reader), in either mode.
  *  Inputs these waits do not order are refused (NKV_ERR_INVALID) when layers_host is given:
@@ -345,10 +347,10 @@ int nkv_decode_step_combine_tok(const uint16_t* q, const uint16_t* k_new, const 
  *
  * workspace: nkv_layers_workspace_bytes(hkv, hq, n_parts, n_layers) bytes, zero-filled before
  * its first use and then dedicated to calls with this (hkv, hq, n_parts, n_layers): a call
- * leaves its partial blocks and layer counters at zero, but the tagged copies of the outputs
- * and the launch counter (the tags' source) keep their values, so the buffer must be zero-filled
- * again before it serves another configuration or another entry point. n_parts <= 0 takes
- * nkv_layers_default_parts.
+ * leaves its partial blocks and layer counters at zero, but the tagged copies of the outputs,
+ * the issue flags and the launch counter (the tags' source) keep their values, so the buffer
+ * must be zero-filled again before it serves another configuration or another entry point.
+ * n_parts <= 0 takes nkv_layers_default_parts.
  *
  * Failure mode. The waits assume every workgroup of the grid runs at once. The occupancy check
  * sees the device, not what else runs on it: when another kernel or process holds CUs, some
