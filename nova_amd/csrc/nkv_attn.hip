@@ -149,6 +149,9 @@ struct AttnArgs {
   // it reads (written by its own head's merger); 1, every input of layer l also waits until every
   // head's merger has finished layer l - 1
   int dep_all;
+  // the paged int8t64 decode step: the tail of each (sequence, KV head) also appends the new token
+  // (its ring slot, and the requantized group of pos in its page), so no append launch precedes it
+  int tail_append;
   // the chained step with dep_all: this layer's issue flags, one word per query head, set to the
   // launch's tag (relaxed, agent scope) as soon as that head's output stores are issued; the
   // readers of layer l + 1 wait until all hq carry the tag. Null otherwise.
@@ -942,6 +945,24 @@ __device__ __forceinline__ const uint16_t* ring_of(const AttnArgs& a, int h, int
 __device__ __forceinline__ const uint16_t* fresh_of(const AttnArgs& a, int b, int h, int which) {
   return (which == 0 ? a.k_new : a.v_new) + (int64_t)b * a.kv_ss + (int64_t)h * a.kv_hs;
 }
+// Ring slot `slot` of tensor `which` (0 K, 1 V) of KV head h (of sequence b when paged).
+template <bool PAGED>
+__device__ __forceinline__ uint16_t* ring_row(const AttnArgs& a, int b, int h, int which, int slot) {
+  if constexpr (PAGED) return a.rings + ((((int64_t)b * a.hkv + h) * 2 + which) * GT + slot) * D;
+  else return const_cast<uint16_t*>(ring_of(a, h, which)) + (int64_t)slot * D;
+}
+// Where the append of the token at `pos` rules its group (int8t64): tensor `which`'s code rows
+// (row stride D) and its step / min rulers (one fp16 per channel), and the rows that exist (a
+// contiguous cache ends at its capacity; a page always holds 64). Paged: the group's page of KV
+// head h, K codes | V codes | kst | kmn | vst | vmn (the caller has checked that it exists).
+struct GroupDst {
+  uint8_t* codes;
+  uint16_t* st;
+  uint16_t* mn;
+  int rows;
+};
+template <bool PAGED>
+__device__ __forceinline__ GroupDst group_dst(const AttnArgs& a, int b, int h, int64_t pos, int which);
 
 // The per-token symmetric append of the token at `pos`: waves 0 and 1 of the calling
 // workgroup quantize K and V of KV head h (lanes 0..15, 8 values each) and store the codes
@@ -1347,9 +1368,30 @@ __device__ __forceinline__ uint64_t pub_repoll2(const float* p, uint64_t w, int&
 // the LDS values become the ones the prefix kernel would read back, fp16(code * step16 +
 // min16) with one rounding (when the token completes its group, the tail attends those).
 // Thread t takes channel t & 255 (K, then V) and rows 32 (t >> 8) .. + 31.
-template <bool STORE>
+template <bool PAGED>
+__device__ __forceinline__ GroupDst group_dst(const AttnArgs& a, int b, int h, int64_t pos, int which) {
+  const int64_t gcur = pos / GT;
+  GroupDst g;
+  if constexpr (PAGED) {
+    uint8_t* base = a.pages + ((int64_t)page_of(a, b, gcur) * a.hkv + h) * PAGE_BYTES;
+    uint16_t* rul = reinterpret_cast<uint16_t*>(base + 2 * CODE_BYTES);
+    g.codes = base + which * CODE_BYTES;
+    g.st = rul + (which ? 2 : 0) * D;
+    g.mn = rul + (which ? 3 : 1) * D;
+    g.rows = GT;
+  } else {
+    const int64_t ro = ((int64_t)h * a.ngroups_cap + gcur) * D;
+    g.codes = (which ? a.vq : a.kq) + ((int64_t)h * a.capacity + gcur * GT) * D;
+    g.st = (which ? a.vst : a.kst) + ro;
+    g.mn = (which ? a.vmn : a.kmn) + ro;
+    g.rows = (int)min<int64_t>(GT, a.capacity - gcur * GT);
+  }
+  return g;
+}
+
+template <bool STORE, bool PAGED = false>
 __device__ __forceinline__ void requant_ring_lds(uint8_t* ring_lds, float (&ext)[2][2 * D], bool deq,
-                                                 const AttnArgs* a = nullptr, int h = 0, int64_t pos = 0) {
+                                                 const AttnArgs* a = nullptr, int h = 0, int64_t pos = 0, int b = 0) {
   const int t = tail_tid(), ch = t & (2 * D - 1), half = t >> 8;
   uint8_t* base = ring_lds + (ch >> 7) * RING_BYTES;
   const int c = ch & (D - 1);
@@ -1377,13 +1419,12 @@ __device__ __forceinline__ void requant_ring_lds(uint8_t* ring_lds, float (&ext)
   int rows = 0;
   if constexpr (STORE) {
     // group pos / 64: code rows at the group's first token, rulers at its ruler row
-    const int which = ch >> 7;
-    const int64_t gcur = pos / GT, ro = ((int64_t)h * a->ngroups_cap + gcur) * D + c;
-    codes = (which ? a->vq : a->kq) + ((int64_t)h * a->capacity + gcur * GT) * D + c;
-    rows = (int)min<int64_t>(GT, a->capacity - gcur * GT);
+    const GroupDst g = group_dst<PAGED>(*a, b, h, pos, ch >> 7);
+    codes = g.codes + c;
+    rows = g.rows;
     if (half == 0) {
-      (which ? a->vmn : a->kmn)[ro] = f2h(lo);
-      (which ? a->vst : a->kst)[ro] = f2h(step);
+      g.mn[c] = f2h(lo);
+      g.st[c] = f2h(step);
     }
   }
 #pragma unroll
@@ -1411,8 +1452,9 @@ __device__ __forceinline__ void requant_ring_lds(uint8_t* ring_lds, float (&ext)
 // values; the wave's 64 x 64 codes go through `xpose` (4 KiB of LDS per wave) so that lane r
 // stores row r's 64 codes with four 16-byte stores (rows below the capacity). No workgroup
 // barrier: the caller's waves 0..3 have all staged the ring before.
+template <bool PAGED = false>
 __device__ __forceinline__ void append_ring_channels(const AttnArgs& a, int h, int64_t pos, const uint8_t* ring_lds,
-                                                     uint8_t* xpose) {
+                                                     uint8_t* xpose, int b = 0) {
   const int t = tail_tid(), wave = t >> 6, lane = t & 63, which = t >> 7, c = t & (D - 1);
   const uint8_t* base = ring_lds + which * RING_BYTES;
   float v[GT];
@@ -1424,18 +1466,16 @@ __device__ __forceinline__ void append_ring_channels(const AttnArgs& a, int h, i
     mx = fmaxf(mx, v[r]);
   }
   const float step = ruler_step(mn, mx), inv = ruler_inv(step);
-  const int64_t gcur = pos / GT, ro = ((int64_t)h * a.ngroups_cap + gcur) * D + c;
-  (which ? a.vmn : a.kmn)[ro] = f2h(mn);
-  (which ? a.vst : a.kst)[ro] = f2h(step);
+  const GroupDst g = group_dst<PAGED>(a, b, h, pos, which);
+  g.mn[c] = f2h(mn);
+  g.st[c] = f2h(step);
   // codes: column `lane` of the wave's [64 rows][64 channels] block, then row `lane` of it
   uint8_t* xw = xpose + wave * (GT * 64);
 #pragma unroll
   for (int r = 0; r < GT; ++r) xw[r * 64 + lane] = (uint8_t)ruler_code_rcp(v[r], mn, step, inv);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // (one wave: its LDS accesses run in order)
-  const int rows = (int)min<int64_t>(GT, a.capacity - gcur * GT);
-  if (lane < rows) {
-    uint4* dst = reinterpret_cast<uint4*>((which ? a.vq : a.kq) + ((int64_t)h * a.capacity + gcur * GT + lane) * D +
-                                          64 * (wave & 1));
+  if (lane < g.rows) {
+    uint4* dst = reinterpret_cast<uint4*>(g.codes + (int64_t)lane * D + 64 * (wave & 1));
     const uint4* src = reinterpret_cast<const uint4*>(xw + lane * 64);
 #pragma unroll
     for (int k = 0; k < 4; ++k) dst[k] = src[k];
@@ -1474,7 +1514,8 @@ struct TailLoads {
 };
 
 template <bool PAGED>
-__device__ __forceinline__ void tail_load_rows(const AttnArgs& a, int h, int b, int64_t pos, bool pos_ok, TailLoads& t) {
+__device__ __forceinline__ void tail_load_rows(const AttnArgs& a, int h, int b, int64_t pos, bool pos_ok, TailLoads& t,
+                                               bool fresh_paged = false) {
   const int wave = tail_tid() >> 6, lane = tail_tid() & 63, cl = lane & 15, rl = lane >> 4;
   const bool fused = PAGED || a.tail_mode == TAIL_FUSED;
   const bool ring = (PAGED || a.tail_mode != TAIL_NONE) && (!fused || pos_ok);
@@ -1498,7 +1539,7 @@ __device__ __forceinline__ void tail_load_rows(const AttnArgs& a, int h, int b, 
     t.v[i] = *reinterpret_cast<const uint4*>(rv + o);
   }
   // the new token's slot: from the step's input, not the ring this launch writes
-  if (!PAGED && a.tail_mode == TAIL_FUSED && (int)(pos % GT) >> 4 == wave) {
+  if ((PAGED ? fresh_paged : a.tail_mode == TAIL_FUSED) && (int)(pos % GT) >> 4 == wave) {
     t.fk = *reinterpret_cast<const uint4*>(fresh_of(a, b, h, 0) + 8 * cl);
     t.fv = *reinterpret_cast<const uint4*>(fresh_of(a, b, h, 1) + 8 * cl);
   }
@@ -1535,12 +1576,13 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   // partial words
   const bool completes = fused && pos_ok && !a.tok && (pos + 1) % GT == 0;  // the token completes its group
   const bool tok1 = ring && a.tok;  // per-token symmetric fused step: the tail is the new token
-  const bool fresh_on = ring && !tok1 && !PAGED && a.tail_mode == TAIL_FUSED;
+  // appends: the chained step's merger, or the paged int8t64 step's tail (TB_APPEND)
+  const bool appends = (flags & TB_APPEND) && fused && pos_ok && !(PAGED && a.tok);
+  const bool fresh_on = ring && !tok1 && (PAGED ? appends : a.tail_mode == TAIL_FUSED);
   const int fresh_slot = (int)(pos % GT);
-  const bool appends = !PAGED && (flags & TB_APPEND) && fused && pos_ok;  // (the merger of the chained step)
   TailLoads tl;
   if (pre) tl = *pre;
-  else tail_load_rows<PAGED>(a, h, b, pos, pos_ok, tl);
+  else tail_load_rows<PAGED>(a, h, b, pos, pos_ok, tl, PAGED && appends);
   const int64_t first = (!PAGED && ring && a.first_dev) ? *a.first_dev : 0;
   const bool mask_on = ring && a.tail_mode == TAIL_MASK && lane < a.tail_slots && a.tail_mask[lane] != 0;
   half8_t qb[4];
@@ -1609,8 +1651,8 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
         *reinterpret_cast<uint4*>(ring_k + o) = tl.fk;
         *reinterpret_cast<uint4*>(ring_v + o) = tl.fv;
         if (appends) {  // the ring slot of the new token
-          *reinterpret_cast<uint4*>(const_cast<uint16_t*>(ring_of(a, h, 0)) + fresh_slot * D + 8 * cl) = tl.fk;
-          *reinterpret_cast<uint4*>(const_cast<uint16_t*>(ring_of(a, h, 1)) + fresh_slot * D + 8 * cl) = tl.fv;
+          *reinterpret_cast<uint4*>(ring_row<PAGED>(a, b, h, 0, fresh_slot) + 8 * cl) = tl.fk;
+          *reinterpret_cast<uint4*>(ring_row<PAGED>(a, b, h, 1, fresh_slot) + 8 * cl) = tl.fv;
         }
       }
     }
@@ -1625,7 +1667,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   }
   if (appends && completes) {
     __syncthreads();
-    requant_ring_lds<true>(sm.ring_lds, sm.rq_ext, true, &a, h, pos);
+    requant_ring_lds<true, PAGED>(sm.ring_lds, sm.rq_ext, true, &a, h, pos, b);
     __syncthreads();
   } else if (completes) {
     __syncthreads();
@@ -1654,7 +1696,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     if (ring_append) {
       while (__hip_atomic_load(&sm.ring_staged, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < RING_PARTS)
         __builtin_amdgcn_s_sleep(1);
-      append_ring_channels(a, h, pos, sm.ring_lds, sm.xpose);
+      append_ring_channels<PAGED>(a, h, pos, sm.ring_lds, sm.xpose, b);
     }
   } else if (merging) {
     // (this code runs once per launch on a cold instruction cache, at ~30 ns per 64-byte line:
@@ -2106,9 +2148,11 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
       const int t = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (t == last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       ticket = t;
+      sm.ring_staged = 0;
     }
     __syncthreads();
-    if (ticket == last) tail_body<true>(a, h, b, sm, TAIL_LAST, pos, pos_ok, U);
+    if (ticket == last)
+      tail_body<true>(a, h, b, sm, TAIL_LAST, pos, pos_ok, U, nullptr, nullptr, !TOK && a.tail_append ? TB_APPEND : 0);
   } else {
     tail_body<false>(a, h, b, sm, TAIL_MERGER, pos, pos_ok, U, &tl, &qb);
   }
@@ -3483,13 +3527,13 @@ static int paged_attn(const char* what, const uint16_t* q, const uint16_t* k_new
                       int64_t nseq, int64_t hq,
                       int64_t hkv, int64_t head_dim, const int32_t* wg_map, const int32_t* seq_parts,
                       int64_t total_parts, uint16_t* out, float* lse_out, void* workspace, int64_t workspace_bytes,
-                      void* stream, bool tok = false) {
+                      void* stream, bool tok = false, bool append = false) {
   set_error("");
   if (int rc = check_heads(hq, hkv, head_dim)) return rc;
   AttnArgs a{};
   if (int rc = paged_args(what, a, pages, page_table, table_stride, num_pages, rings, pos_dev, nseq, hkv, head_dim, tok))
     return rc;
-  if (tok) {
+  if (tok || append) {
     if (!k_new || !v_new) return fail(NKV_ERR_INVALID, "%s: null pointer argument", what);
     if (!al16(k_new) || !al16(v_new) || kv_head_stride % 8 || kv_seq_stride % 8)
       return fail(NKV_ERR_UNSUPPORTED, "%s: k_new / v_new must be 16-byte aligned", what);
@@ -3508,6 +3552,7 @@ static int paged_attn(const char* what, const uint16_t* q, const uint16_t* k_new
   a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace);
   // one launch: the last prefix workgroup of each (sequence, KV head) runs its tail
   a.inline_tail = 1;
+  a.tail_append = append ? 1 : 0;
   a.tail_ctr_end = reinterpret_cast<int*>(static_cast<char*>(workspace) + (workspace_bytes & ~int64_t(3)));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (tok) hipLaunchKernelGGL(attn_prefix_kernel<PAGED_TOK>, dim3((unsigned)(hkv * total_parts)), dim3(THREADS), 0, s, a);
@@ -3533,12 +3578,11 @@ extern "C" int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_ne
                                          int64_t hkv, int64_t head_dim, const int32_t* wg_map,
                                          const int32_t* seq_parts, int64_t total_parts, uint16_t* out, float* lse_out,
                                          void* workspace, int64_t workspace_bytes, void* stream) {
-  if (int rc = nkv_paged_append_t64(k_new, v_new, kv_seq_stride, kv_head_stride, pages, page_table, table_stride,
-                                    num_pages, rings, pos_dev, nseq, hkv, head_dim, stream))
-    return rc;
+  // one launch: the tail of each (sequence, KV head) appends the new token from k_new / v_new
+  // (nothing else in the launch reads the ring slot or the group it writes)
   return paged_attn("paged_decode_step_t64", q, k_new, v_new, kv_seq_stride, kv_head_stride, pages, page_table,
                     table_stride, num_pages, rings, pos_dev, nseq, hq, hkv, head_dim, wg_map, seq_parts, total_parts,
-                    out, lse_out, workspace, workspace_bytes, stream);
+                    out, lse_out, workspace, workspace_bytes, stream, false, true);
 }
 
 extern "C" int nkv_paged_decode_step_tok(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
