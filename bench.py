@@ -613,23 +613,18 @@ def run_paged(args, steps: int | None = None, scheme: str = "t64") -> dict:
     step_bytes = sum(sum(step_launch_bytes(n + W + i + 1, scheme) for n in lens) for i in range(K)) / K * L
     gbs = step_bytes / (ms / 1e3) / 1e9
 
-    # ---- the dominant kernel alone (pos fixed): the prefix kernel with its fused tails, 36 launches
-    # (int8t64: the attention launch of each layer's step, without the append launch; per-token
-    # symmetric: the step's only launch, which also stores the new token)
+    # ---- the step's launches alone (pos fixed; each is the layer's only launch): the prefix kernel
+    # with its fused per-(sequence, KV head) tails, which also append the new token
     g_launch = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_launch):
         for layer in range(L):
-            if scheme == "tok":
-                cache.decode_step(ks[layer], vs[layer], qs[layer], layer)
-            else:
-                cache.attend(qs[layer], layer)
+            cache.decode_step(ks[layer], vs[layer], qs[layer], layer)
     per_launch_s = _time_graph(g_launch, stream, K, W) / 1e3 / L
     pos = [n + W + K for n in lens]
-    launch_bytes = sum((step_launch_bytes(p + 1, "tok") if scheme == "tok" else attn_bytes(p + 1)) for p in pos)
+    launch_bytes = sum(step_launch_bytes(p + 1, scheme) for p in pos)
     _calibration_copy(dev)
     kidx = 3 if scheme == "tok" else 2
-    kname = (f"nkv::attn_prefix_kernel<{kidx}> paged "
-             f"{'decode step (store of the new token + attention)' if scheme == 'tok' else 'attention'} of the "
+    kname = (f"nkv::attn_prefix_kernel<{kidx}> paged decode step (append of the new token + attention) of the "
              f"{B} sequences with fused per-(sequence, KV head) tails, one launch per layer")
     res = {"metric": "paged ragged batch int8-KV decode: batch tokens/s + achieved HBM GB/s (% of peak)",
            "value": round(B / (ms / 1e3), 2), "unit": "tokens/s", "steps": K, "ms_per_step": round(ms, 4),
@@ -637,7 +632,7 @@ def run_paged(args, steps: int | None = None, scheme: str = "t64") -> dict:
                                   f"{B} ragged sequences (lengths {lens}), {L} layers x "
                                   "(32 q / 8 kv heads, head_dim 128), 64-token pages, hipGraph-replayed steps",
                       "lengths": lens, "layers": L, "page_tokens": 64, "work_units_per_head": cache.total_parts,
-                      "launches_per_layer": 1 if scheme == "tok" else 2},
+                      "launches_per_layer": 1},
            "step_gbs": round(gbs, 1), "step_pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
            "algorithmic_bytes_per_step": round(step_bytes),
            "roofline": _roofline_hbm(launch_bytes, per_launch_s, f"paged_{scheme}", kname, L)}

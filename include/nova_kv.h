@@ -471,7 +471,11 @@ int nkv_paged_attn_decode_t64(const uint16_t* q, const uint8_t* pages, const int
                               uint16_t* out, float* lse_out, void* workspace, int64_t workspace_bytes,
                               void* stream);
 
-/* nkv_paged_append_t64 then nkv_paged_attn_decode_t64 (two launches). */
+/* What nkv_paged_append_t64 then nkv_paged_attn_decode_t64 compute, bit for bit, in one launch:
+ * the last workgroup of each (sequence, KV head), which merges its partials, takes the new
+ * token from k_new / v_new for its ring slot, stores it there and requantizes the group of pos
+ * into its page from the ring it has staged (nothing else in the launch reads that slot or
+ * that page). */
 int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                               int64_t kv_seq_stride, int64_t kv_head_stride, uint8_t* pages,
                               const int32_t* page_table, int64_t table_stride, int64_t num_pages,

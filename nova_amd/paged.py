@@ -246,8 +246,9 @@ class PagedKVInt8Cache:
         return q.contiguous(), k.contiguous(), v.contiguous()
 
     def decode_step(self, key: torch.Tensor, value: torch.Tensor, query: torch.Tensor, layer: int) -> torch.Tensor:
-        """Append one token per sequence at ``pos`` and attend each sequence over ``[0, pos_b]``.
-        Returns ``merged[:B]`` ``[B, Hq, 1, 128]``; ``lse`` holds the log-sum-exp."""
+        """Append one token per sequence at ``pos`` and attend each sequence over ``[0, pos_b]``, in
+        one launch (``nkv_paged_decode_step_t64``: the tails append). Returns ``merged[:B]``
+        ``[B, Hq, 1, 128]``; ``lse`` holds the log-sum-exp."""
         if self.wg_map is None:
             raise RuntimeError("call plan() before decoding")
         q, k, v = self._step_args(query, key, value)
