@@ -263,7 +263,7 @@ def write_stats(out_dir: str, name: str, cmd: str) -> None:
              f"#   python3 bench.py --stats-from OUT --stats-name {name} --stats-cmd '{cmd}'",
              f"{'kernel':<72} {'calls':>6} {'avg':>11} {'min':>9} {'max':>9} {'median':>11} {'share':>7}"]
     for nm, v in sorted(durs.items(), key=lambda kv: -sum(kv[1])):
-        short = re.sub(r"\(.*", "", nm.replace("void ", ""))[:72]
+        short = re.sub(r"\(.*", "", nm.replace("void ", "").replace("(anonymous namespace)::", ""))[:72]
         lines.append(f"{short:<72} {len(v):>6} {sum(v) / len(v):>11.1f} {min(v):>9} {max(v):>9} "
                      f"{statistics.median(v):>11.1f} {100 * sum(v) / total:>6.2f}%")
     (PROFILES / name).write_text("\n".join(lines) + "\n")

@@ -202,7 +202,10 @@ int nkv_decode_step_combine_t64(const uint16_t* q, const uint16_t* k_new, const 
  * NKV_STATIC_SYNC_BYTES bytes that the library holds on every GPU it runs on until the
  * process ends. Its address is looked up on the first call on a device (the current
  * device), which also clears the publication area with a kernel on `stream`; every
- * call leaves it cleared.
+ * call leaves it cleared. When that first call happens under hipGraph capture, the clear
+ * kernel is recorded into the graph as well; replaying it is harmless (the area is
+ * already clear whenever no call is in flight), but a caller that captures may prefer to
+ * make one eager call first.
  * A call needs hkv * n_parts * 4 * (gq * 128 + ((2 * gq + 3) & ~3)) partial bytes
  * (gq = hq / hkv) <= NKV_STATIC_PART_BYTES and 4 * hkv * (1 + n_parts) publication bytes
  * <= NKV_STATIC_SYNC_BYTES; larger calls return NKV_ERR_UNSUPPORTED.
