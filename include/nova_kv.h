@@ -438,9 +438,13 @@ int nkv_decode_layers_check_tok(const nkv_layer_tok* layers_host, int64_t n_laye
  * pos_dev: int64 [nseq], the position each sequence appends at this step.
  * k_new / v_new: [nseq][hkv][128] fp16 with strides kv_seq_stride / kv_head_stride.
  * Prefix work unit w (w < total_parts) serves sequence wg_map[w] >> 16, part
- * wg_map[w] & 0xffff of its seq_parts[2b + 1] parts; seq_parts[2b] is its first unit. A sequence
- * has at most 256 parts (the tail's merge holds 256 partials; it ignores partials beyond them).
+ * wg_map[w] & 0xffff of its seq_parts[2b + 1] parts; seq_parts[2b] is its first unit (a
+ * sequence's units are consecutive, w = seq_parts[2b] + part). A sequence has at most 256 parts
+ * (the tail's merge holds 256 partials; it ignores partials beyond them).
  * q / out: [nseq][hq][128] fp16; lse_out [nseq][hq] fp32 (may be NULL).
+ * The workspace holds per KV head one partial slot per unit and one per sequence (the int8t64
+ * step's ring partial, after the sequence's prefix partials), then the completion counters;
+ * its size is bounded with nseq <= total_parts.
  */
 int64_t nkv_paged_workspace_bytes(int64_t hkv, int64_t hq, int64_t total_parts);
 
@@ -474,11 +478,13 @@ int nkv_paged_attn_decode_t64(const uint16_t* q, const uint8_t* pages, const int
                               uint16_t* out, float* lse_out, void* workspace, int64_t workspace_bytes,
                               void* stream);
 
-/* What nkv_paged_append_t64 then nkv_paged_attn_decode_t64 compute, bit for bit, in one launch:
- * the last workgroup of each (sequence, KV head), which merges its partials, takes the new
- * token from k_new / v_new for its ring slot, stores it there and requantizes the group of pos
- * into its page from the ring it has staged (nothing else in the launch reads that slot or
- * that page). */
+/* What nkv_paged_append_t64 then nkv_paged_attn_decode_t64 compute in one launch (cache state
+ * bit for bit; outputs up to float summation order): the new token comes from k_new / v_new.
+ * With more than one workgroup for a (sequence, KV head), the first to finish its prefix share
+ * stages the ring with the new token, attends over it, publishes the ring partial and, beside
+ * that, stores the token in its ring slot and requantizes the group of pos into its page; the
+ * last merges the prefix partials with the ring partial. With one workgroup it does all of it.
+ * Nothing else in the launch reads that slot or that page. */
 int nkv_paged_decode_step_t64(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                               int64_t kv_seq_stride, int64_t kv_head_stride, uint8_t* pages,
                               const int32_t* page_table, int64_t table_stride, int64_t num_pages,

@@ -962,7 +962,7 @@ struct GroupDst {
   int rows;
 };
 template <bool PAGED>
-__device__ __forceinline__ GroupDst group_dst(const AttnArgs& a, int b, int h, int64_t pos, int which);
+__device__ __forceinline__ GroupDst group_dst(const AttnArgs& a, int b, int h, int64_t pos, int which, int64_t page = -1);
 
 // The per-token symmetric append of the token at `pos`: waves 0 and 1 of the calling
 // workgroup quantize K and V of KV head h (lanes 0..15, 8 values each) and store the codes
@@ -1369,11 +1369,12 @@ __device__ __forceinline__ uint64_t pub_repoll2(const float* p, uint64_t w, int&
 // min16) with one rounding (when the token completes its group, the tail attends those).
 // Thread t takes channel t & 255 (K, then V) and rows 32 (t >> 8) .. + 31.
 template <bool PAGED>
-__device__ __forceinline__ GroupDst group_dst(const AttnArgs& a, int b, int h, int64_t pos, int which) {
+__device__ __forceinline__ GroupDst group_dst(const AttnArgs& a, int b, int h, int64_t pos, int which, int64_t page) {
   const int64_t gcur = pos / GT;
   GroupDst g;
   if constexpr (PAGED) {
-    uint8_t* base = a.pages + ((int64_t)page_of(a, b, gcur) * a.hkv + h) * PAGE_BYTES;
+    // (page: the group's page when the caller has read it already, else -1)
+    uint8_t* base = a.pages + ((page >= 0 ? page : page_of(a, b, gcur)) * a.hkv + h) * PAGE_BYTES;
     uint16_t* rul = reinterpret_cast<uint16_t*>(base + 2 * CODE_BYTES);
     g.codes = base + which * CODE_BYTES;
     g.st = rul + (which ? 2 : 0) * D;
@@ -1391,7 +1392,8 @@ __device__ __forceinline__ GroupDst group_dst(const AttnArgs& a, int b, int h, i
 
 template <bool STORE, bool PAGED = false>
 __device__ __forceinline__ void requant_ring_lds(uint8_t* ring_lds, float (&ext)[2][2 * D], bool deq,
-                                                 const AttnArgs* a = nullptr, int h = 0, int64_t pos = 0, int b = 0) {
+                                                 const AttnArgs* a = nullptr, int h = 0, int64_t pos = 0, int b = 0,
+                                                 int64_t page = -1) {
   const int t = tail_tid(), ch = t & (2 * D - 1), half = t >> 8;
   uint8_t* base = ring_lds + (ch >> 7) * RING_BYTES;
   const int c = ch & (D - 1);
@@ -1419,7 +1421,7 @@ __device__ __forceinline__ void requant_ring_lds(uint8_t* ring_lds, float (&ext)
   int rows = 0;
   if constexpr (STORE) {
     // group pos / 64: code rows at the group's first token, rulers at its ruler row
-    const GroupDst g = group_dst<PAGED>(*a, b, h, pos, ch >> 7);
+    const GroupDst g = group_dst<PAGED>(*a, b, h, pos, ch >> 7, page);
     codes = g.codes + c;
     rows = g.rows;
     if (half == 0) {
@@ -1447,15 +1449,16 @@ __device__ __forceinline__ void requant_ring_lds(uint8_t* ring_lds, float (&ext)
 }
 
 // The append of the token at `pos` from the ring held in LDS (the 64 slots, the new token in its
-// slot; ring_chunk_pos layout) by the 256 threads of waves 0..3: thread t rules channel t & 127 of K
+// slot; ring_chunk_pos layout) by 256 threads (waves 0..3, or 4..7 with tbase 256): thread t
+// (counted from tbase) rules channel t & 127 of K
 // (t < 128) or V over the 64 slots, exactly as append_unit rules it, and stores its two ruler
 // values; the wave's 64 x 64 codes go through `xpose` (4 KiB of LDS per wave) so that lane r
 // stores row r's 64 codes with four 16-byte stores (rows below the capacity). No workgroup
 // barrier: the caller's waves 0..3 have all staged the ring before.
 template <bool PAGED = false>
 __device__ __forceinline__ void append_ring_channels(const AttnArgs& a, int h, int64_t pos, const uint8_t* ring_lds,
-                                                     uint8_t* xpose, int b = 0) {
-  const int t = tail_tid(), wave = t >> 6, lane = t & 63, which = t >> 7, c = t & (D - 1);
+                                                     uint8_t* xpose, int b = 0, int64_t page = -1, int tbase = 0) {
+  const int t = tail_tid() - tbase, wave = t >> 6, lane = t & 63, which = t >> 7, c = t & (D - 1);
   const uint8_t* base = ring_lds + which * RING_BYTES;
   float v[GT];
   float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
@@ -1466,7 +1469,7 @@ __device__ __forceinline__ void append_ring_channels(const AttnArgs& a, int h, i
     mx = fmaxf(mx, v[r]);
   }
   const float step = ruler_step(mn, mx), inv = ruler_inv(step);
-  const GroupDst g = group_dst<PAGED>(a, b, h, pos, which);
+  const GroupDst g = group_dst<PAGED>(a, b, h, pos, which, page);
   g.mn[c] = f2h(mn);
   g.st[c] = f2h(step);
   // codes: column `lane` of the wave's [64 rows][64 channels] block, then row `lane` of it
@@ -1554,27 +1557,47 @@ __device__ __forceinline__ void tail_load_rows(const AttnArgs& a, int h, int b, 
 // TB_KEEP_BLOCK, the caller having set sm.ring_done to zero), when every merging wave owns one
 // head: each merging wave combines its head with the ring partials and stores the outputs itself
 // as soon as its merge is done (no workgroup barrier; a head whose words never arrived is NaN
-// alone), and the tail returns without a final barrier.
-constexpr int TB_APPEND = 1, TB_KEEP_BLOCK = 2, TB_POISON = 4, TB_DIRECT = 8;
+// alone), and the tail returns without a final barrier; TB_RING_SLOT (paged, with pos_ok): no
+// ring attention here: the ring partial that paged_ring_tail publishes in the sequence's ring
+// slot is merged as one more prefix partial.
+constexpr int TB_APPEND = 1, TB_KEEP_BLOCK = 2, TB_POISON = 4, TB_DIRECT = 8, TB_RING_SLOT = 16;
+
+// The paged workspace: per KV head, per sequence b, its seq_parts[2b + 1] prefix partial slots
+// and one more, the ring slot (the paged int8t64 step's ring partial, published by the first of
+// the sequence's workgroups to finish its prefix share for the last one): total_parts + nseq
+// slots per KV head, so that the ring slot follows the sequence's prefix partials.
+__device__ __forceinline__ float* paged_block(const AttnArgs& a, int h, int b) {
+  return a.ws + ((int64_t)h * (a.total_parts + a.nseq) + a.seq_parts[2 * b] + b) * part_stride(a.gq);
+}
+__device__ __forceinline__ float* paged_ring_slot(const AttnArgs& a, int h, int b) {
+  return paged_block(a, h, b) + (int64_t)a.seq_parts[2 * b + 1] * part_stride(a.gq);
+}
 
 template <bool PAGED>
 __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailSmem& sm, int run, int64_t pos,
                                           bool pos_ok, int64_t U, const TailLoads* pre = nullptr,
-                                          const half8_t (*pre_q)[4] = nullptr, int flags = 0) {
+                                          const half8_t (*pre_q)[4] = nullptr, int flags = 0, int64_t page = -1) {
   const int tid = tail_tid(), wave = tid >> 6, lane = tid & 63;
   const bool poll = run != TAIL_KERNEL;  // partials written in this launch: poll their words
   const int gq = a.gq, pw = part_stride(gq), cols = gq * D;
-  const int P = PAGED ? min(a.seq_parts[2 * b + 1], WTS) : a.n_parts;
+  const int P0 = PAGED ? min(a.seq_parts[2 * b + 1], WTS) : a.n_parts;  // prefix partials
   const bool fused = PAGED || a.tail_mode == TAIL_FUSED;
-  const bool ring = (PAGED || a.tail_mode != TAIL_NONE) && (!fused || pos_ok);
-  float* hws = PAGED ? a.ws + ((int64_t)h * a.total_parts + a.seq_parts[2 * b]) * pw : a.ws + (int64_t)h * P * pw;
+  // TB_RING_SLOT: another workgroup attends over the ring and publishes one ring partial in the
+  // sequence's ring slot, merged here as partial P0
+  const bool ring_slot = PAGED && (flags & TB_RING_SLOT) && pos_ok;
+  const bool ring = (PAGED || a.tail_mode != TAIL_NONE) && (!fused || pos_ok) && !(PAGED && (flags & TB_RING_SLOT));
+  const int P = P0 + (ring_slot ? 1 : 0);
+  float* hws = PAGED ? paged_block(a, h, b) : a.ws + (int64_t)h * P0 * pw;
+  // partial u (the ring slot, u = P0, follows the prefix partials: ring_slot needs P0 equal to
+  // the sequence's parts, which the caller checks)
+  auto pp = [&](int64_t u) -> float* { return hws + u * pw; };
   // while waves 0..3 attend over the ring, the others merge the prefix partials
   const int mbase = ring ? RING_PARTS : 0, nmw = TB_WAVES - mbase;
   const bool direct = (flags & TB_DIRECT) && (flags & TB_KEEP_BLOCK) && P <= 64 && nmw >= gq;
 
   // ---- loads: the ring rows (or the new token) and q of the ring waves, the merging waves'
   // partial words
-  const bool completes = fused && pos_ok && !a.tok && (pos + 1) % GT == 0;  // the token completes its group
+  const bool completes = ring && fused && pos_ok && !a.tok && (pos + 1) % GT == 0;  // the token completes its group
   const bool tok1 = ring && a.tok;  // per-token symmetric fused step: the tail is the new token
   // appends: the chained step's merger, or the paged int8t64 step's tail (TB_APPEND)
   const bool appends = (flags & TB_APPEND) && fused && pos_ok && !(PAGED && a.tok);
@@ -1582,7 +1605,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   const int fresh_slot = (int)(pos % GT);
   TailLoads tl;
   if (pre) tl = *pre;
-  else tail_load_rows<PAGED>(a, h, b, pos, pos_ok, tl, PAGED && appends);
+  else if (ring) tail_load_rows<PAGED>(a, h, b, pos, pos_ok, tl, PAGED && appends);
   const int64_t first = (!PAGED && ring && a.first_dev) ? *a.first_dev : 0;
   const bool mask_on = ring && a.tail_mode == TAIL_MASK && lane < a.tail_slots && a.tail_mask[lane] != 0;
   half8_t qb[4];
@@ -1602,16 +1625,17 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   uint64_t rv[MERGE_PRE];               // and those of its columns 2 lane, 2 lane + 1 of the first MERGE_PRE partials
   int budget = (flags & TB_POISON) ? 0 : MERGER_SPIN_LIMIT;  // (poisoned: the output is NaN anyway)
   if (merging) {
-    // (appending, the words are first loaded by the poll below: their registers would otherwise
-    // stay live across the requantization, which the partials are far from being ready for)
-    const bool pre_ld = !(flags & TB_APPEND);
+    // (the chained step's merger, appending, loads them first in the poll below: their registers
+    // would otherwise stay live across the requantization, which the partials are far from being
+    // ready for; the last workgroup's tail finds them all issued)
+    const bool pre_ld = !(flags & TB_APPEND) || run == TAIL_LAST;
     if (lane < P) {
-      rm = pre_ld ? pub_ld(hws + (int64_t)lane * pw + gq * D + head0) : 0u;
-      rl = pre_ld ? pub_ld(hws + (int64_t)lane * pw + gq * D + gq + head0) : 0u;
+      rm = pre_ld ? pub_ld(pp(lane) + gq * D + head0) : 0u;
+      rl = pre_ld ? pub_ld(pp(lane) + gq * D + gq + head0) : 0u;
     }
 #pragma unroll
     for (int u = 0; u < MERGE_PRE; ++u)
-      rv[u] = u < P ? (pre_ld ? pub_ld2(hws + (int64_t)u * pw + head0 * D + 2 * lane) : 0ull) : PUB_KEY2;
+      rv[u] = u < P ? (pre_ld ? pub_ld2(pp(u) + head0 * D + 2 * lane) : 0ull) : PUB_KEY2;
   }
 
   // ---- each ring wave stages its own 16 slots in LDS (chunk ^ (row & 15) layout), the new token
@@ -1667,7 +1691,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   }
   if (appends && completes) {
     __syncthreads();
-    requant_ring_lds<true, PAGED>(sm.ring_lds, sm.rq_ext, true, &a, h, pos, b);
+    requant_ring_lds<true, PAGED>(sm.ring_lds, sm.rq_ext, true, &a, h, pos, b, page);
     __syncthreads();
   } else if (completes) {
     __syncthreads();
@@ -1696,7 +1720,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     if (ring_append) {
       while (__hip_atomic_load(&sm.ring_staged, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < RING_PARTS)
         __builtin_amdgcn_s_sleep(1);
-      append_ring_channels<PAGED>(a, h, pos, sm.ring_lds, sm.xpose, b);
+      append_ring_channels<PAGED>(a, h, pos, sm.ring_lds, sm.xpose, b, page);
     }
   } else if (merging) {
     // (this code runs once per launch on a cold instruction cache, at ~30 ns per 64-byte line:
@@ -1716,11 +1740,11 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
         }
         --budget;
         __builtin_amdgcn_s_sleep(1);
-        if (rm == 0) rm = pub_ld(hws + (int64_t)lane * pw + gq * D + head0);
-        if (rl == 0) rl = pub_ld(hws + (int64_t)lane * pw + gq * D + gq + head0);
+        if (rm == 0) rm = pub_ld(pp(lane) + gq * D + head0);
+        if (rl == 0) rl = pub_ld(pp(lane) + gq * D + gq + head0);
 #pragma unroll
         for (int u = 0; u < MERGE_PRE; ++u)
-          if (rv[u] == 0) rv[u] = pub_ld2(hws + (int64_t)u * pw + head0 * D + 2 * lane);
+          if (rv[u] == 0) rv[u] = pub_ld2(pp(u) + head0 * D + 2 * lane);
       }
     }
     if (lane < P) {
@@ -1751,11 +1775,11 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
         uint64_t w8[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          w8[j] = sb + j < P ? pub_ld2(hws + (int64_t)(sb + j) * pw + head0 * D + 2 * lane) : 1;
+          w8[j] = sb + j < P ? pub_ld2(pp(sb + j) + head0 * D + 2 * lane) : 1;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           if (sb + j >= P) break;
-          const uint64_t wv = pub_repoll2(hws + (int64_t)(sb + j) * pw + head0 * D + 2 * lane, w8[j], budget);
+          const uint64_t wv = pub_repoll2(pp(sb + j) + head0 * D + 2 * lane, w8[j], budget);
           lost |= wv == 0;
           const float2 vv = pub_f2(wv);
           acc.x += vv.x * wb[sb + j];
@@ -1824,7 +1848,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
             ms = mm;
             ls[k] = ll;
           } else {
-            const float* pm = hws + (int64_t)s * pw + gq * D + head;
+            const float* pm = pp(s) + gq * D + head;
             const uint32_t wm = pub_repoll(pm, pub_ld(pm), budget);
             const uint32_t wl = pub_repoll(pm + gq, pub_ld(pm + gq), budget);
             lost |= wm == 0 || wl == 0;
@@ -1863,11 +1887,11 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
           uint64_t w8[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j)
-            w8[j] = sb + j < P ? pub_ld2(hws + (int64_t)(sb + j) * pw + head * D + 2 * lane) : 1;
+            w8[j] = sb + j < P ? pub_ld2(pp(sb + j) + head * D + 2 * lane) : 1;
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             if (sb + j >= P) break;
-            const uint64_t wv = pub_repoll2(hws + (int64_t)(sb + j) * pw + head * D + 2 * lane, w8[j], budget);
+            const uint64_t wv = pub_repoll2(pp(sb + j) + head * D + 2 * lane, w8[j], budget);
             lost |= wv == 0;
             const float2 vv = pub_f2(wv);
             acc.x += vv.x * wb[sb + j];
@@ -1942,6 +1966,90 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   if (flags & TB_KEEP_BLOCK) return;
   uint4* blk = reinterpret_cast<uint4*>(hws);
   for (int i = tid; i < P * pw / 4; i += TB_THREADS) blk[i] = uint4{0u, 0u, 0u, 0u};
+
+}
+
+// The paged int8t64 step's ring work for (sequence b, KV head h), by the first of the sequence's
+// workgroups to finish its prefix share (pos_ok): the ring rows and the new token staged in LDS as
+// tail_body stages them; then waves 0..3 attend over the ring (4 x 16 tokens) and publish the
+// four ring partials merged into one (pub_st) in the ring slot (paged_ring_slot), while waves
+// 4..7 append the new token (its ring slot; its group's codes and rulers in the page, from the
+// staged ring). A token that completes its group is appended by requantizing the whole ring, by
+// every thread before the attention, the ring then attended as int8 as in tail_body. The last of
+// the sequence's workgroups merges the ring slot with the prefix partials (TB_RING_SLOT).
+__device__ __forceinline__ void paged_ring_tail(const AttnArgs& a, int h, int b, TailSmem& sm, int64_t pos, int64_t U) {
+  const int tid = tail_tid(), wave = tid >> 6, lane = tid & 63;
+  const int gq = a.gq;
+  const int64_t page = page_of(a, b, pos / GT);  // (read here, with the ring rows: the append needs it last)
+  const bool completes = (pos + 1) % GT == 0;
+  const int fresh_slot = (int)(pos % GT);
+  TailLoads tl;
+  tail_load_rows<true>(a, h, b, pos, true, tl, true);
+  half8_t qb[4];
+  if (wave < RING_PARTS) load_q(a.q + ((int64_t)b * a.hq + h * gq) * D, gq, qb);
+  uint8_t* ring_k = sm.ring_lds;
+  uint8_t* ring_v = sm.ring_lds + RING_BYTES;
+  if (wave < RING_PARTS) {
+    const int cl = lane & 15, rw = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * wave + rw + 4 * i, o = r * (2 * D) + (ring_chunk_pos(r, cl) << 4);
+      *reinterpret_cast<uint4*>(ring_k + o) = tl.k[i];
+      *reinterpret_cast<uint4*>(ring_v + o) = tl.v[i];
+    }
+    // (program order: these stores land after the quarter's stores of the same row)
+    if (fresh_slot >> 4 == wave && (fresh_slot & 3) == rw) {
+      const int o = fresh_slot * (2 * D) + (ring_chunk_pos(fresh_slot, cl) << 4);
+      *reinterpret_cast<uint4*>(ring_k + o) = tl.fk;
+      *reinterpret_cast<uint4*>(ring_v + o) = tl.fv;
+      *reinterpret_cast<uint4*>(ring_row<true>(a, b, h, 0, fresh_slot) + 8 * cl) = tl.fk;
+      *reinterpret_cast<uint4*>(ring_row<true>(a, b, h, 1, fresh_slot) + 8 * cl) = tl.fv;
+    }
+  }
+  __syncthreads();  // the whole ring is in LDS
+  if (completes) {
+    requant_ring_lds<true, true>(sm.ring_lds, sm.rq_ext, true, &a, h, pos, b, page);
+    __syncthreads();
+  }
+  if (wave >= RING_PARTS) {
+    // waves 4..7: the append of a token that does not complete its group (one that does was
+    // stored above), beside the ring attention
+    if (!completes) append_ring_channels<true>(a, h, pos, sm.ring_lds, sm.xpose, b, page, 64 * RING_PARTS);
+    return;
+  }
+  WaveState st;
+  state_init(st);
+  attend_ring16(a, st, qb, ring_k, ring_v, wave, completes ? ~0ull : ring_bits(pos + 1, U, 0));
+  store_wave_partial(st, gq, sm.ring_part[wave]);
+  // the four ring waves meet (sm.ring_done, zero before the tail), not the workgroup
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  if (lane == 0) __hip_atomic_fetch_add(&sm.ring_done, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  while (__hip_atomic_load(&sm.ring_done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < RING_PARTS)
+    __builtin_amdgcn_s_sleep(1);
+  // one partial from the four: m = max_r m_r, w_r = 2^(m_r - m), l = sum_r w_r l_r,
+  // acc = sum_r w_r acc_r, two columns a thread of waves 0..3
+  float* dst = paged_ring_slot(a, h, b);
+  for (int e = 2 * tid; e < gq * D; e += 2 * 64 * RING_PARTS) {
+    const int head = e / D;
+    float m = NEG_INF;
+#pragma unroll
+    for (int r = 0; r < RING_PARTS; ++r) m = fmaxf(m, sm.ring_part[r][gq * D + head]);
+    const float mu = m == NEG_INF ? 0.0f : m;
+    float x = 0.0f, y = 0.0f, l = 0.0f;
+#pragma unroll
+    for (int r = 0; r < RING_PARTS; ++r) {
+      const float mr = sm.ring_part[r][gq * D + head];
+      const float w = mr == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mr - mu);
+      l += sm.ring_part[r][gq * D + gq + head] * w;
+      x += sm.ring_part[r][e] * w;
+      y += sm.ring_part[r][e + 1] * w;
+    }
+    pub_st2(dst + e, x, y);
+    if (e % D == 0) {
+      pub_st(dst + gq * D + head, m);
+      pub_st(dst + gq * D + gq + head, l);
+    }
+  }
 }
 
 template <int LAYOUT>
@@ -1953,7 +2061,6 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t q_lds[16 * D];
   __shared__ __attribute__((aligned(16))) float xch[UNIT_CH * 2 * WAVES];
   __shared__ int ticket;
-  float* lds = reinterpret_cast<float*>(lds_raw);
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.x % a.hkv;
@@ -2088,43 +2195,41 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
 
     // the merger's ring rows, loaded while the partial below is merged and published
     if (merger) tail_load_rows<false>(a, h, b, pos, pos_ok, tl);
-    // ---- merge the waves through LDS (the stages are dead once every wave is here): per head
-    // m = max_w m_w and the waves' weights 2^(m_w - m) once (threads < gq, into xch), then the
-    // columns; the partial is published word by word (pub_st)
-    __syncthreads();
+    // ---- merge the waves through LDS and publish the partial word by word (pub_st): each wave
+    // puts its partial into its own stage (free once its own loop has ended), then each thread
+    // merges two columns, computing its head's wave weights 2^(m_w - m) itself (one barrier)
     const int gq = a.gq, pw = part_stride(gq);
-    store_wave_partial(st, gq, lds + wave * pw);
+    store_wave_partial(st, gq, reinterpret_cast<float*>(my_stages));
     __syncthreads();
-    float* dst = a.ws + ((int64_t)h * (PAGED ? a.total_parts : a.n_parts) + pslot) * pw;
-    float* wt = xch;  // [gq][WAVES]
-    float pm = NEG_INF, pl = 0.0f;
-    if (tid < gq) {
-#pragma unroll
-      for (int w = 0; w < WAVES; ++w) pm = fmaxf(pm, lds[w * pw + gq * D + tid]);
-      const float mu = pm == NEG_INF ? 0.0f : pm;
-#pragma unroll
-      for (int w = 0; w < WAVES; ++w) {
-        const float x = __builtin_amdgcn_exp2f(lds[w * pw + gq * D + tid] - mu);
-        wt[tid * WAVES + w] = x;
-        pl += lds[w * pw + gq * D + gq + tid] * x;
-      }
-    }
-    __syncthreads();
+    // (paged: unit pslot is part `part` of sequence b, whose units begin at seq_parts[2b] = pslot - part,
+    // so its slot is that of paged_block without reading seq_parts)
+    float* dst = a.ws + ((int64_t)h * (PAGED ? a.total_parts + a.nseq : a.n_parts) + pslot + (PAGED ? b : 0)) * pw;
+    auto wpart = [&](int w) { return reinterpret_cast<const float*>(lds_raw + w * wave_lds); };
     // (a paged sequence's partials beyond the WTS its tail merges are not published)
     const bool publish = !PAGED || part < WTS;
     for (int e = 2 * tid; e < gq * D && publish; e += 2 * THREADS) {
-      const float* c = wt + (e / D) * WAVES;
+      const int head = e / D;
+      float pm = NEG_INF;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) pm = fmaxf(pm, wpart(w)[gq * D + head]);
+      const float mu = pm == NEG_INF ? 0.0f : pm;
+      float cw[WAVES], pl = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        cw[w] = __builtin_amdgcn_exp2f(wpart(w)[gq * D + head] - mu);
+        pl += wpart(w)[gq * D + gq + head] * cw[w];
+      }
       float x = 0.0f, y = 0.0f;
 #pragma unroll
       for (int w = 0; w < WAVES; ++w) {
-        x += lds[w * pw + e] * c[w];
-        y += lds[w * pw + e + 1] * c[w];
+        x += wpart(w)[e] * cw[w];
+        y += wpart(w)[e + 1] * cw[w];
       }
       pub_st2(dst + e, x, y);
-    }
-    if (tid < gq && publish) {
-      pub_st(dst + gq * D + tid, pm);
-      pub_st(dst + gq * D + gq + tid, pl);
+      if (e % D == 0) {
+        pub_st(dst + gq * D + head, pm);
+        pub_st(dst + gq * D + gq + head, pl);
+      }
     }
   }  // prefix
 
@@ -2149,10 +2254,28 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
       if (t == last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       ticket = t;
       sm.ring_staged = 0;
+      sm.ring_done = 0;
     }
     __syncthreads();
-    if (ticket == last)
-      tail_body<true>(a, h, b, sm, TAIL_LAST, pos, pos_ok, U, nullptr, nullptr, !TOK && a.tail_append ? TB_APPEND : 0);
+    // int8t64 with its append and more than one workgroup for (b, h): the first to take a ticket
+    // attends over the ring, publishes the ring partial and appends the new token while the others
+    // stream; the last merges the prefix partials with that ring partial. Otherwise the last does
+    // all of the tail.
+    const bool split = !TOK && a.tail_append && pos_ok && nparts > 1 && nparts < WTS;
+    if (split && ticket == 0) {
+      paged_ring_tail(a, h, b, sm, pos, U);
+    } else if (ticket == last) {
+      // direct: each merging wave combines its head as soon as the ring partials are in; the ring
+      // waves (if any) append the new token after their partial, not before the combine
+      const int tb = split ? TB_RING_SLOT : (!TOK && a.tail_append ? TB_APPEND : 0);
+      tail_body<true>(a, h, b, sm, TAIL_LAST, pos, pos_ok, U, nullptr, nullptr, tb | TB_DIRECT | TB_KEEP_BLOCK);
+      // every word of the sequence's partials (the first min(parts, WTS)) and of its ring slot was
+      // consumed: back to zero
+      __syncthreads();
+      const int P = min(nparts, WTS) + (split ? 1 : 0), pw = part_stride(a.gq);
+      uint4* blk = reinterpret_cast<uint4*>(paged_block(a, h, b));
+      for (int i = tid; i < P * pw / 4; i += THREADS) blk[i] = uint4{0u, 0u, 0u, 0u};
+    }
   } else {
     tail_body<false>(a, h, b, sm, TAIL_MERGER, pos, pos_ok, U, &tl, &qb);
   }
@@ -3471,7 +3594,8 @@ extern "C" int nkv_decode_step_combine_tok(NKV_STEP_TOK_PARAMS) {
 
 extern "C" int64_t nkv_paged_workspace_bytes(int64_t hkv, int64_t hq, int64_t total_parts) {
   if (hkv <= 0 || hq <= 0 || total_parts <= 0 || hq % hkv) return 0;
-  return hkv * total_parts * part_floats(hq, hkv) * (int64_t)sizeof(float) + ctr_bytes(hkv * total_parts);
+  // per KV head total_parts prefix partial slots and a ring slot per sequence (nseq <= total_parts)
+  return 2 * hkv * total_parts * part_floats(hq, hkv) * (int64_t)sizeof(float) + ctr_bytes(hkv * total_parts);
 }
 
 // (`rings` is NULL for the per-token symmetric format, which keeps none)

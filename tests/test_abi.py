@@ -67,7 +67,9 @@ def test_abi_version_and_host_helpers(lib):
     assert lib.nkv_attn_workspace_bytes(8, 32, 32) == 32 * per_part + 1280
     assert lib.nkv_attn_workspace_bytes(8, 32, 0) == per_part + sync(8, 1)
     assert lib.nkv_attn_workspace_bytes(128, 128, 1) == 128 * (128 + 4) * 4 + sync(128, 1)
-    assert lib.nkv_paged_workspace_bytes(8, 32, 40) == 40 * per_part + 8 * 40 * 4  # one counter per (unit, head) bound
+    # per KV head: total_parts prefix partial slots and up to as many ring slots (one per sequence);
+    # one counter per (unit, head) bound
+    assert lib.nkv_paged_workspace_bytes(8, 32, 40) == 2 * 40 * per_part + 8 * 40 * 4
 
 
 def test_only_one_hip_runtime_is_mapped(lib):
