@@ -1970,23 +1970,21 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
 }
 
 // The paged int8t64 step's ring work for (sequence b, KV head h), by the first of the sequence's
-// workgroups to finish its prefix share (pos_ok): the ring rows and the new token staged in LDS as
-// tail_body stages them; then waves 0..3 attend over the ring (4 x 16 tokens) and publish the
+// workgroups to finish its prefix share (pos_ok): the ring rows and the new token (`tl`, loaded by
+// tail_load_rows as its prefix loop ended; q the loop's operand `qb`) staged in LDS as tail_body
+// stages them; then waves 0..3 attend over the ring (4 x 16 tokens) and publish the
 // four ring partials merged into one (pub_st) in the ring slot (paged_ring_slot), while waves
 // 4..7 append the new token (its ring slot; its group's codes and rulers in the page, from the
 // staged ring). A token that completes its group is appended by requantizing the whole ring, by
 // every thread before the attention, the ring then attended as int8 as in tail_body. The last of
 // the sequence's workgroups merges the ring slot with the prefix partials (TB_RING_SLOT).
-__device__ __forceinline__ void paged_ring_tail(const AttnArgs& a, int h, int b, TailSmem& sm, int64_t pos, int64_t U) {
+__device__ __forceinline__ void paged_ring_tail(const AttnArgs& a, int h, int b, TailSmem& sm, int64_t pos, int64_t U,
+                                                const TailLoads& tl, const half8_t (&qb)[4]) {
   const int tid = tail_tid(), wave = tid >> 6, lane = tid & 63;
   const int gq = a.gq;
-  const int64_t page = page_of(a, b, pos / GT);  // (read here, with the ring rows: the append needs it last)
+  const int64_t page = page_of(a, b, pos / GT);  // (the append needs it last)
   const bool completes = (pos + 1) % GT == 0;
   const int fresh_slot = (int)(pos % GT);
-  TailLoads tl;
-  tail_load_rows<true>(a, h, b, pos, true, tl, true);
-  half8_t qb[4];
-  if (wave < RING_PARTS) load_q(a.q + ((int64_t)b * a.hq + h * gq) * D, gq, qb);
   uint8_t* ring_k = sm.ring_lds;
   uint8_t* ring_v = sm.ring_lds + RING_BYTES;
   if (wave < RING_PARTS) {
@@ -2195,6 +2193,12 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
 
     // the merger's ring rows, loaded while the partial below is merged and published
     if (merger) tail_load_rows<false>(a, h, b, pos, pos_ok, tl);
+    // the paged int8t64 step with its ring work split off: every workgroup of the (sequence, KV
+    // head) loads the ring rows and the new token here, for the case that its ticket makes it the
+    // ring workgroup (paged_ring_tail)
+    if constexpr (PAGED && !TOK) {
+      if (a.tail_append && pos_ok && nparts > 1 && nparts < WTS) tail_load_rows<true>(a, h, b, pos, pos_ok, tl, true);
+    }
     // ---- merge the waves through LDS and publish the partial word by word (pub_st): each wave
     // puts its partial into its own stage (free once its own loop has ended), then each thread
     // merges two columns, computing its head's wave weights 2^(m_w - m) itself (one barrier)
@@ -2263,7 +2267,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
     // all of the tail.
     const bool split = !TOK && a.tail_append && pos_ok && nparts > 1 && nparts < WTS;
     if (split && ticket == 0) {
-      paged_ring_tail(a, h, b, sm, pos, U);
+      paged_ring_tail(a, h, b, sm, pos, U, tl, qb);
     } else if (ticket == last) {
       // direct: each merging wave combines its head as soon as the ring partials are in; the ring
       // waves (if any) append the new token after their partial, not before the combine
