@@ -2928,9 +2928,10 @@ struct PrefillArgs {
 // Online softmax of one 16-row block over 64 tokens, from the raw scores S[b][i] (token
 // 16b + 4g + i, row c; -inf where masked): m is a reference maximum in the log2 domain, within
 // PF_TAU below the row's maximum of S * sl2, and P comes out as exp2(S sl2 - m + 15 - PF_TAU)
-// <= 2^15 in two fp16 A operands (tokens of blocks 0,1 and 2,3). l accumulates the same scaled
-// weights, so acc / l needs no rescaling; l is rescaled here and acc by pf_rescale (the caller
-// runs it before the next PV product), both only when m moves.
+// <= 2^15 in two fp16 A operands (tokens of blocks 0,1 and 2,3). The row sums of P are taken on
+// the matrix core by the caller (P times a ones operand, in the accumulator layout), which leaves
+// the VALU the maximum, the exponentials and the conversions; the caller rescales the
+// accumulators and those sums by alpha, only when m moves.
 __device__ __forceinline__ void pf_softmax(WaveState& st, const float (&S)[4][4], float sl2, half8_t (&ph)[2],
                                            float& alpha_out, bool& moved_out) {
   float smax = NEG_INF;
@@ -2939,41 +2940,23 @@ __device__ __forceinline__ void pf_softmax(WaveState& st, const float (&S)[4][4]
 #pragma unroll
     for (int i = 0; i < 4; ++i) smax = fmaxf(smax, S[b][i]);
   smax = max4rows(smax);
-  // the reference maximum moves only when the row's maximum grows by more than PF_TAU (log2):
-  // P = 2^(S sl2 - m + 15 - PF_TAU) <= 2^15 still, and the accumulators are rescaled rarely
   const float m_cand = fmaxf(st.m, smax * sl2);
   const float m_new = m_cand > st.m + PF_TAU ? m_cand : st.m;
   const float m_use = m_new == NEG_INF ? 0.0f : m_new;
   const float alpha = __builtin_amdgcn_exp2f(st.m - m_use);
   const float off = 15.0f - PF_TAU - m_use;
-  float lsum = 0.0f;
   _Float16 p16[2][8];
 #pragma unroll
   for (int b = 0; b < 4; ++b)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(S[b][i], sl2, off));
-      lsum += p;
-      p16[b >> 1][4 * (b & 1) + i] = (_Float16)p;
-    }
+    for (int i = 0; i < 4; ++i)
+      p16[b >> 1][4 * (b & 1) + i] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(S[b][i], sl2, off));
 #pragma unroll
   for (int B = 0; B < 2; ++B)
     ph[B] = half8_t{p16[B][0], p16[B][1], p16[B][2], p16[B][3], p16[B][4], p16[B][5], p16[B][6], p16[B][7]};
-  st.l = st.l * alpha + sum4rows(lsum);
   moved_out = st.m != m_new;
   alpha_out = alpha;
   st.m = m_new;
-}
-// the accumulator rescale that goes with pf_softmax, when any row's reference maximum moved
-__device__ __forceinline__ void pf_rescale(WaveState& st, float alpha, bool moved) {
-  const int g = (threadIdx.x & 63) >> 4;
-  if (__builtin_amdgcn_ballot_w64(moved) == 0) return;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float ai = shfl(alpha, 4 * g + i);
-#pragma unroll
-    for (int cb = 0; cb < 8; ++cb) st.acc[cb][i] *= ai;
-  }
 }
 
 __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel(PrefillArgs a) {
@@ -3004,8 +2987,14 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
   asm volatile("" ::"v"(qb[0][0]), "v"(qb[0][1]), "v"(qb[0][2]), "v"(qb[0][3]), "v"(qb[PF_RB - 1][0]),
                "v"(qb[PF_RB - 1][1]), "v"(qb[PF_RB - 1][2]), "v"(qb[PF_RB - 1][3]));
   WaveState st[PF_RB];
+  float4_t lsum[PF_RB];  // rows 4g + i of each row block: the sums of P, on the matrix core
 #pragma unroll
-  for (int rb = 0; rb < PF_RB; ++rb) state_init(st[rb]);
+  for (int rb = 0; rb < PF_RB; ++rb) {
+    state_init(st[rb]);
+    lsum[rb] = float4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  const _Float16 one = (_Float16)1.0f;
+  const half8_t ones = half8_t{one, one, one, one, one, one, one, one};
 
   const int64_t G = a.U / GT;
   const int64_t cs = (int64_t)split * G / a.splits, ce = (int64_t)(split + 1) * G / a.splits;
@@ -3070,6 +3059,19 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
           const half8_t vb = *reinterpret_cast<const half8_t*>(vtile + (16 * cb + c) * PF_VROW + 32 * B + 8 * g);
           st[rb].acc[cb] = mfma32(ph[rb][B], vb, st[rb].acc[cb]);
         }
+#pragma unroll
+      for (int B = 0; B < 2; ++B) lsum[rb] = mfma32(ph[rb][B], ones, lsum[rb]);
+    };
+    // the accumulator rescale with the row sums (rare: only when a row's reference maximum moved)
+    auto rescale = [&](int rb) {
+      if (__builtin_amdgcn_ballot_w64(moved[rb]) == 0) return;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float ai = shfl(alpha[rb], 4 * g + i);
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb) st[rb].acc[cb][i] *= ai;
+        lsum[rb][i] *= ai;
+      }
     };
     // QK(1) beside softmax(0), PV(0) beside softmax(1): the matrix core and the VALU each have
     // the other row block's work (the rescales, rare, between)
@@ -3077,10 +3079,10 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
     qk(0);
     qk(1);
     softmax(0);
-    pf_rescale(st[0], alpha[0], moved[0]);
+    rescale(0);
     pv(0);
     softmax(1);
-    pf_rescale(st[1], alpha[1], moved[1]);
+    rescale(1);
     pv(1);
   };
 
@@ -3157,10 +3159,10 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
   for (int rb = 0; rb < PF_RB; ++rb) {
     const int rbase = row0 + 16 * rb;
     float* dst = a.ws + ((int64_t)split * total_rows + (int64_t)h * rows_h) * PF_PART;
-    if (g == 0 && rbase + c < rows_h) {
-      dst[(int64_t)(rbase + c) * PF_PART + D] = st[rb].m;
-      dst[(int64_t)(rbase + c) * PF_PART + D + 1] = st[rb].l;
-    }
+    if (g == 0 && rbase + c < rows_h) dst[(int64_t)(rbase + c) * PF_PART + D] = st[rb].m;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (c == 0 && rbase + 4 * g + i < rows_h) dst[(int64_t)(rbase + 4 * g + i) * PF_PART + D + 1] = lsum[rb][i];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = rbase + 4 * g + i;
