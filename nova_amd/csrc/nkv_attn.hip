@@ -1583,17 +1583,19 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   const int P0 = PAGED ? min(a.seq_parts[2 * b + 1], WTS) : a.n_parts;  // prefix partials
   const bool fused = PAGED || a.tail_mode == TAIL_FUSED;
   // TB_RING_SLOT: another workgroup attends over the ring and publishes one ring partial in the
-  // sequence's ring slot, merged here as partial P0
+  // sequence's ring slot (the slot after its P0 prefix partials: ring_slot needs P0 equal to the
+  // sequence's parts, which the caller checks). The direct path merges the prefix partials
+  // first and polls the ring slot in its combine, where the ring partials go; otherwise the slot
+  // is merged as prefix partial P0.
   const bool ring_slot = PAGED && (flags & TB_RING_SLOT) && pos_ok;
   const bool ring = (PAGED || a.tail_mode != TAIL_NONE) && (!fused || pos_ok) && !(PAGED && (flags & TB_RING_SLOT));
-  const int P = P0 + (ring_slot ? 1 : 0);
-  float* hws = PAGED ? paged_block(a, h, b) : a.ws + (int64_t)h * P0 * pw;
-  // partial u (the ring slot, u = P0, follows the prefix partials: ring_slot needs P0 equal to
-  // the sequence's parts, which the caller checks)
-  auto pp = [&](int64_t u) -> float* { return hws + u * pw; };
   // while waves 0..3 attend over the ring, the others merge the prefix partials
   const int mbase = ring ? RING_PARTS : 0, nmw = TB_WAVES - mbase;
-  const bool direct = (flags & TB_DIRECT) && (flags & TB_KEEP_BLOCK) && P <= 64 && nmw >= gq;
+  const bool direct = (flags & TB_DIRECT) && (flags & TB_KEEP_BLOCK) && P0 + 1 <= 64 && nmw >= gq;
+  const bool slot_in_combine = ring_slot && direct;
+  const int P = P0 + (ring_slot && !direct ? 1 : 0);
+  float* hws = PAGED ? paged_block(a, h, b) : a.ws + (int64_t)h * P0 * pw;
+  auto pp = [&](int64_t u) -> float* { return hws + u * pw; };
 
   // ---- loads: the ring rows (or the new token) and q of the ring waves, the merging waves'
   // partial words
@@ -1791,7 +1793,6 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
         if (ring)
           while (__hip_atomic_load(&sm.ring_done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < RING_PARTS)
             __builtin_amdgcn_s_sleep(1);
-        const bool failed = (flags & TB_POISON) != 0 || __builtin_amdgcn_ballot_w64(lost) != 0;
         const int col = head0 * D + 2 * lane;
         float M = m, mr[RING_PARTS], lr[RING_PARTS];
         float2 ar[RING_PARTS];
@@ -1800,8 +1801,21 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
           mr[r] = ring ? sm.ring_part[r][gq * D + head0] : NEG_INF;
           lr[r] = ring ? sm.ring_part[r][gq * D + gq + head0] : 0.0f;
           ar[r] = ring ? *reinterpret_cast<const float2*>(sm.ring_part[r] + col) : float2{0.0f, 0.0f};
-          M = fmaxf(M, mr[r]);
         }
+        if (slot_in_combine) {
+          // the ring workgroup's partial, in place of the four ring partials
+          const float* rs = pp(P0);
+          const uint32_t wm = pub_repoll(rs + gq * D + head0, pub_ld(rs + gq * D + head0), budget);
+          const uint32_t wl = pub_repoll(rs + gq * D + gq + head0, pub_ld(rs + gq * D + gq + head0), budget);
+          const uint64_t wv = pub_repoll2(rs + col, pub_ld2(rs + col), budget);
+          lost |= wm == 0 || wl == 0 || wv == 0;
+          mr[0] = pub_f(wm);
+          lr[0] = pub_f(wl);
+          ar[0] = pub_f2(wv);
+        }
+#pragma unroll
+        for (int r = 0; r < RING_PARTS; ++r) M = fmaxf(M, mr[r]);
+        const bool failed = (flags & TB_POISON) != 0 || __builtin_amdgcn_ballot_w64(lost) != 0;
         const float Mu = M == NEG_INF ? 0.0f : M;
         const float alpha = m == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m - Mu);
         float ox = alpha * acc.x, oy = alpha * acc.y, lt = alpha * l;
