@@ -1559,7 +1559,8 @@ __device__ __forceinline__ void tail_load_rows(const AttnArgs& a, int h, int b, 
 // as soon as its merge is done (no workgroup barrier; a head whose words never arrived is NaN
 // alone), and the tail returns without a final barrier; TB_RING_SLOT (paged, with pos_ok): no
 // ring attention here: the ring partial that paged_ring_tail publishes in the sequence's ring
-// slot is merged as one more prefix partial.
+// slot takes the ring partials' place in the direct combine (without the direct path it is
+// merged as one more prefix partial).
 constexpr int TB_APPEND = 1, TB_KEEP_BLOCK = 2, TB_POISON = 4, TB_DIRECT = 8, TB_RING_SLOT = 16;
 
 // The paged workspace: per KV head, per sequence b, its seq_parts[2b + 1] prefix partial slots
@@ -1980,7 +1981,6 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   if (flags & TB_KEEP_BLOCK) return;
   uint4* blk = reinterpret_cast<uint4*>(hws);
   for (int i = tid; i < P * pw / 4; i += TB_THREADS) blk[i] = uint4{0u, 0u, 0u, 0u};
-
 }
 
 // The paged int8t64 step's ring work for (sequence b, KV head h), by the first of the sequence's
