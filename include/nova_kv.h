@@ -5,7 +5,8 @@
  * hipStream_t passed as `void*` (the caller's current stream; pass the stream
  * that torch is capturing on to record the launch into a hipGraph). Nothing
  * here allocates device memory, synchronizes the device or reads device memory
- * on the host, so every call is safe inside stream capture. Scratch memory
+ * on the host, so every call is safe inside stream capture (except the two
+ * nkv_l2_handover calls, which are made once, outside capture). Scratch memory
  * (`workspace`) is owned by the caller, except for nkv_decode_step_static_t64, whose
  * scratch is a fixed array the library holds on each GPU.
  *
@@ -29,7 +30,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 8
+#define NKV_ABI_VERSION 9
 
 #define NKV_OK 0
 #define NKV_ERR_INVALID 1     /* argument outside what the reference accepts */
@@ -590,6 +591,30 @@ int nkv_read_bw(const void* src, int64_t nbytes, uint32_t* sink, int64_t blocks,
  * Counterpart of the reference's read + unpack ceiling (src/diagnostics/bench_int8_unpack.py:58-102).
  */
 int nkv_read_bw_lds(const void* src, int64_t nbytes, uint32_t* sink, int64_t blocks, void* stream);
+
+/*
+ * XCD-local hand-over (no counterpart in the reference: a placement property of this GPU).
+ * The split-K launches hand each workgroup's partial (and, in the chained step, each layer's
+ * forwarded output) to a workgroup of the same KV head. The device deals the workgroups of a
+ * launch to its n XCDs (each with its own L2) in turn: workgroup b runs on XCD (b + k) mod n,
+ * the start k varying between launches (graph replays rotate it). The workgroups of KV head h
+ * are b = h mod hkv, so when n divides hkv they share one XCD: the words are then stored into
+ * that L2 (plain stores) instead of being written through to memory, and the reader's
+ * agent-scope loads find them there (0.25 us per hand-over between idle workgroups against
+ * 0.43 us; the 36-layer chained step at 32k runs ~10% faster). Writes that other XCDs read
+ * (issue flags, counters) stay agent-scope.
+ *
+ * nkv_l2_handover(1, ..) probes the current device (a launch of 4096 workgroups that record
+ * their XCD, read back synchronously: call it outside stream capture) and turns the hand-over
+ * on for that device when workgroup b ran on the XCD of workgroup b mod n for every b, the
+ * first n on distinct XCDs, with n = the device's XCD count, a power of two <= 8; *xcds = n,
+ * or 0 when it stays off. nkv_l2_handover(0, ..) turns it off (every hand-over through memory).
+ * A device that was never probed hands over through memory. Were the dealing rule broken in a
+ * later launch, a reader would not see a writer's L2: its bounded wait gives up and its outputs
+ * are NaN (the chained step also sets its error word), and the workspace is then to be
+ * zero-filled again before reuse.
+ */
+int nkv_l2_handover(int enable, int64_t* xcds, void* stream);
 
 /* ---------------------------------------------------------------- decode-step projections
  *

@@ -11,6 +11,7 @@ calls raise ``RuntimeError``.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from ctypes import c_float, c_int, c_int64, c_void_p
 from pathlib import Path
@@ -92,15 +93,17 @@ SIGNATURES = {
     "nkv_copy_bytes": (c_int, [P, P, I64, P]),
     "nkv_read_bw": (c_int, [P, I64, P, I64, P]),
     "nkv_read_bw_lds": (c_int, [P, I64, P, I64, P]),
+    "nkv_l2_handover": (c_int, [c_int, P, P]),
     "nkv_gemv": (c_int, [P, P, c_float, P, I64, I64, P, P, P]),
     "nkv_swiglu_gemv": (c_int, [P, P, c_float, P, I64, I64, P, P]),
     "nkv_qk_norm_rope": (c_int, [P, I64, I64, I64, P, P, c_float, P, P, P]),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lib = None
 _lock = threading.Lock()
+_l2_probed = False
 
 
 class NovaKVError(RuntimeError):
@@ -117,6 +120,8 @@ def load(require_gpu: bool = True):
     if require_gpu and not torch.cuda.is_available():
         raise RuntimeError("nova_amd needs a ROCm GPU (gfx950); none is visible to torch")
     if _lib is not None:
+        if not _l2_probed and require_gpu:
+            _probe_l2()
         return _lib
     with _lock:
         if _lib is None:
@@ -130,7 +135,31 @@ def load(require_gpu: bool = True):
             if lib.nkv_abi_version() != ABI_VERSION:
                 raise RuntimeError(f"libnova_kv ABI {lib.nkv_abi_version()} != {ABI_VERSION}: rebuild it")
             _lib = lib
+    if require_gpu:
+        _probe_l2()
     return _lib
+
+
+def _probe_l2() -> None:
+    """Turn on the XCD-local hand-over for the current device (``nkv_l2_handover``), unless
+    ``NKV_L2_HANDOVER=0``. The probe synchronizes, so under stream capture it waits for the
+    next call outside capture."""
+    global _l2_probed
+    if torch.cuda.is_current_stream_capturing():
+        return
+    with _lock:
+        if _l2_probed:
+            return
+        _l2_probed = True
+    l2_handover(os.environ.get("NKV_L2_HANDOVER", "1") != "0")
+
+
+def l2_handover(enable: bool = True) -> int:
+    """Probe the current device and turn the XCD-local hand-over on (``enable``) or off; returns
+    the XCD count it runs with (0: off). Call outside stream capture."""
+    n = ctypes.c_int64(0)
+    call("nkv_l2_handover", 1 if enable else 0, ctypes.byref(n), stream_ptr())
+    return int(n.value)
 
 
 def call(name: str, *args) -> None:

@@ -36,6 +36,7 @@
 #include "nkv_common.h"
 
 #include <mutex>
+#include <vector>
 
 namespace nkv {
 
@@ -158,6 +159,9 @@ struct AttnArgs {
   uint32_t* issue_flags;
   uint32_t* flags_base;  // layer 0's issue flags; layer l's at flags_base + l hq
   int n_layers;
+  // the L2 hand-over: l2_xcc = the device's XCD count n when workgroups b and b + n share an XCD
+  // and n divides hkv (the workgroups of a KV head then share one XCD), 0 when off
+  int l2_xcc;
 };
 
 // XOR key of the 16-byte chunk positions of LDS row `row` (a token within its group).
@@ -1319,16 +1323,38 @@ __device__ __forceinline__ uint16_t ld_u16(const uint16_t* p, bool co) {
 // producers polls the words themselves (relaxed agent-scope atomic loads): per-location
 // coherence hands it each producer's value once the word is non-zero, without a flag, fence or
 // counter (a flag would need release / acquire ordering, i.e. L2 writeback and invalidation).
+// ---- XCD-local hand-over. The workgroups of one launch are dealt to the device's n XCDs in
+// turn (workgroup b on XCD (b + k) mod n, the start k varying between launches), and every
+// workgroup of KV head h has b = h mod hkv, so with n dividing hkv they share one XCD and its L2.
+// Words handed between them are then plain stores into that L2, read by agent-scope loads that
+// hit the L2's dirty line (0.25 us per hand-over between idle workgroups, against 0.43 us through
+// memory). The host turns this on per device (l2_xcc) after a probe has seen the dealing rule
+// (nkv_l2_handover). Were a reader on another XCD than its writer, it would not see the word:
+// its wait is bounded, gives up, and poisons its outputs with NaN.
+__device__ __forceinline__ uint32_t xcc_id() {
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v;
+}
+
+__device__ __forceinline__ bool l2_local(const AttnArgs& a) { return a.l2_xcc != 0; }
+
 constexpr uint32_t PUB_KEY = 0x7FBADBADu;
 constexpr uint64_t PUB_KEY2 = ((uint64_t)PUB_KEY << 32) | PUB_KEY;
 
-__device__ __forceinline__ void pub_st(float* p, float v) {
-  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v) ^ PUB_KEY, __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
+// A word handed to a workgroup on the same XCD (`l2`, l2_local) is a plain store: it stays in the
+// XCD's L2, where the reader's agent-scope loads find it (they miss the CU's L1 and hit lines the
+// L2 holds dirty); otherwise an agent-scope store, written through to memory.
+template <typename T>
+__device__ __forceinline__ void hand_st(T* p, T w, bool l2) {
+  if (l2) __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+  else __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void pub_st2(float* p, float x, float y) {
-  const uint64_t w = (((uint64_t)__float_as_uint(y) << 32) | __float_as_uint(x)) ^ PUB_KEY2;
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void pub_st(float* p, float v, bool l2) {
+  hand_st(reinterpret_cast<uint32_t*>(p), __float_as_uint(v) ^ PUB_KEY, l2);
+}
+__device__ __forceinline__ void pub_st2(float* p, float x, float y, bool l2) {
+  hand_st(reinterpret_cast<uint64_t*>(p), (((uint64_t)__float_as_uint(y) << 32) | __float_as_uint(x)) ^ PUB_KEY2, l2);
 }
 __device__ __forceinline__ uint32_t pub_ld(const float* p) {
   return __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1833,8 +1859,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
         const uint32_t pair = (uint32_t)f2h(ox) | ((uint32_t)f2h(oy) << 16);
         *reinterpret_cast<uint32_t*>(a.out + qh * D + 2 * lane) = pair;
         if (a.fwd_out)
-          __hip_atomic_store(a.fwd_out + qh * D / 2 + lane, ((uint64_t)a.ftag << 32) | pair, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+          hand_st(a.fwd_out + qh * D / 2 + lane, ((uint64_t)a.ftag << 32) | pair, l2_local(a));
         if (a.lse && lane == 0)
           a.lse[qh] = failed ? __builtin_nanf("") : (lt > 0.0f ? (M + __log2f(lt) - P_SCALE_LOG2) * LN2 : NEG_INF);
         // this head's outputs are issued: count it for the readers of the next layer (they
@@ -1965,8 +1990,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     if (a.fwd_out) {  // (columns come in pairs of neighbouring lanes: d even in the even lane)
       const uint32_t pair = (uint32_t)__shfl_xor((int)o16, 1, 64);
       if ((d & 1) == 0)
-        __hip_atomic_store(a.fwd_out + ((int64_t)qh * D + d) / 2, ((uint64_t)a.ftag << 32) | o16 | (pair << 16),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        hand_st(a.fwd_out + ((int64_t)qh * D + d) / 2, ((uint64_t)a.ftag << 32) | o16 | (pair << 16), l2_local(a));
     }
     if (a.lse && d == 0) a.lse[qh] = failed ? __builtin_nanf("") : (l > 0.0f ? (M + __log2f(l) - P_SCALE_LOG2) * LN2 : NEG_INF);
   }
@@ -2041,6 +2065,7 @@ __device__ __forceinline__ void paged_ring_tail(const AttnArgs& a, int h, int b,
   // one partial from the four: m = max_r m_r, w_r = 2^(m_r - m), l = sum_r w_r l_r,
   // acc = sum_r w_r acc_r, two columns a thread of waves 0..3
   float* dst = paged_ring_slot(a, h, b);
+  const bool l2 = l2_local(a);
   for (int e = 2 * tid; e < gq * D; e += 2 * 64 * RING_PARTS) {
     const int head = e / D;
     float m = NEG_INF;
@@ -2056,10 +2081,10 @@ __device__ __forceinline__ void paged_ring_tail(const AttnArgs& a, int h, int b,
       x += sm.ring_part[r][e] * w;
       y += sm.ring_part[r][e + 1] * w;
     }
-    pub_st2(dst + e, x, y);
+    pub_st2(dst + e, x, y, l2);
     if (e % D == 0) {
-      pub_st(dst + gq * D + head, m);
-      pub_st(dst + gq * D + gq + head, l);
+      pub_st(dst + gq * D + head, m, l2);
+      pub_st(dst + gq * D + gq + head, l, l2);
     }
   }
 }
@@ -2225,6 +2250,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
     auto wpart = [&](int w) { return reinterpret_cast<const float*>(lds_raw + w * wave_lds); };
     // (a paged sequence's partials beyond the WTS its tail merges are not published)
     const bool publish = !PAGED || part < WTS;
+    const bool l2 = l2_local(a);
     for (int e = 2 * tid; e < gq * D && publish; e += 2 * THREADS) {
       const int head = e / D;
       float pm = NEG_INF;
@@ -2243,10 +2269,10 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
         x += wpart(w)[e] * cw[w];
         y += wpart(w)[e + 1] * cw[w];
       }
-      pub_st2(dst + e, x, y);
+      pub_st2(dst + e, x, y, l2);
       if (e % D == 0) {
-        pub_st(dst + gq * D + head, pm);
-        pub_st(dst + gq * D + gq + head, pl);
+        pub_st(dst + gq * D + head, pm, l2);
+        pub_st(dst + gq * D + gq + head, pl, l2);
       }
     }
   }  // prefix
@@ -2716,6 +2742,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
     {
       float* dst = la.ws + ((int64_t)h * P + part) * pw;
       auto wpart = [&](int w) { return reinterpret_cast<const float*>(lds_raw + w * wave_lds); };
+      const bool l2 = l2_local(la);
       for (int e = 2 * ptid; e < gq * D; e += 2 * THREADS) {
         const int head = e / D;
         float pm = NEG_INF;
@@ -2734,10 +2761,10 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
           x += wpart(w)[e] * cw[w];
           y += wpart(w)[e + 1] * cw[w];
         }
-        pub_st2(dst + e, x, y);
+        pub_st2(dst + e, x, y, l2);
         if (e % D == 0) {
-          pub_st(dst + gq * D + head, pm);
-          pub_st(dst + gq * D + gq + head, lost ? __builtin_nanf("") : pl);  // a lost wait poisons the merge
+          pub_st(dst + gq * D + head, pm, l2);
+          pub_st(dst + gq * D + gq + head, lost ? __builtin_nanf("") : pl, l2);  // a lost wait poisons the merge
         }
       }
     }
@@ -3218,6 +3245,29 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
 
 // ---------------------------------------------------------------- host side
 
+// ---- the XCD-local hand-over per device: the XCD count when on, 0 (off) until nkv_l2_handover
+// has probed the device
+constexpr int L2_DEVICES = 64;
+constexpr int XCD_PROBE_WGS = 4096;
+static std::mutex g_l2_mu;
+static int g_l2_xcc[L2_DEVICES];
+static __device__ uint32_t g_xcd_probe[XCD_PROBE_WGS];
+
+__global__ __launch_bounds__(64) void xcd_probe_kernel(uint32_t* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+
+// The launch's hand-over fields: on when the current device was probed and its XCD count divides
+// hkv (so that workgroups b = h mod hkv of KV head h share XCD b mod n).
+static void l2_args(AttnArgs& a) {
+  a.l2_xcc = 0;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= L2_DEVICES) return;
+  std::lock_guard<std::mutex> lock(g_l2_mu);
+  const int n = g_l2_xcc[dev];
+  if (n > 0 && a.hkv % n == 0) a.l2_xcc = n;
+}
+
 // Prefix work units per KV head: at least 8 groups (one per wave) per workgroup, and at
 // most one workgroup per CU (256 CUs).
 static int64_t default_parts(int64_t hkv, int64_t groups) {
@@ -3260,6 +3310,7 @@ static int launch_attn(AttnArgs& a, int64_t n_parts, int64_t workspace_bytes, hi
     return fail(NKV_ERR_UNSUPPORTED, "%s: capacity %lld exceeds 16M tokens", what, (long long)a.capacity);
   a.inline_tail = fuse ? 1 : 0;
   a.tail_ctr_end = reinterpret_cast<int*>(reinterpret_cast<char*>(a.ws) + (workspace_bytes & ~int64_t(3)));
+  l2_args(a);
   if (n_parts > 0 && (launches & LAUNCH_PREFIX)) {
     const int64_t parts = a.tail_mode == TAIL_FUSED && !a.tok ? std::max<int64_t>(n_parts, APPEND_UNITS) : n_parts;
     if (a.tok) hipLaunchKernelGGL(attn_prefix_kernel<CONTIG_TOK>, dim3((unsigned)(a.hkv * parts)), dim3(THREADS), 0, s, a);
@@ -3487,6 +3538,41 @@ extern "C" int nkv_decode_step_static_t64(const uint16_t* q, const uint16_t* k_n
                      out, lse_out, ws, STATIC_BYTES, n_parts, stream);
 }
 
+extern "C" int nkv_l2_handover(int enable, int64_t* xcds, void* stream) {
+  if (xcds) *xcds = 0;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= L2_DEVICES)
+    return fail(NKV_ERR_HIP, "l2_handover: no usable current device (%d)", dev);
+  int on = 0;
+  if (enable) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess) n = 0;
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_xcd_probe));
+    if (e != hipSuccess || !p) return fail(NKV_ERR_HIP, "l2_handover: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    std::vector<uint32_t> got(XCD_PROBE_WGS);
+    hipLaunchKernelGGL(xcd_probe_kernel, dim3(XCD_PROBE_WGS), dim3(64), 0, s, static_cast<uint32_t*>(p));
+    if (int rc = check_launch("l2_handover: probe")) return rc;
+    e = hipMemcpyAsync(got.data(), p, sizeof(uint32_t) * XCD_PROBE_WGS, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return fail(NKV_ERR_HIP, "l2_handover: probe readback: %s", hipGetErrorString(e));
+    // on only for 1..8 XCDs (a power of two) dealt in turn: workgroup b on the XCD of workgroup
+    // b mod n, the first n on n distinct XCDs
+    bool ok = n >= 1 && n <= 8 && (n & (n - 1)) == 0;
+    for (int b = 0; ok && b < XCD_PROBE_WGS; ++b) ok = got[b] == got[b % n];
+    for (int i = 0; ok && i < n; ++i)
+      for (int j = 0; j < i; ++j) ok = ok && got[i] != got[j];
+    if (ok) on = n;
+  }
+  {
+    std::lock_guard<std::mutex> lock(g_l2_mu);
+    g_l2_xcc[dev] = on;
+  }
+  if (xcds) *xcds = on;
+  return NKV_OK;
+}
+
 extern "C" int nkv_tail_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                const uint8_t* mask, int64_t hq, int64_t hkv, int64_t head_dim,
                                int64_t slots, uint16_t* out, float* lse, void* stream) {
@@ -3698,6 +3784,7 @@ static int paged_attn(const char* what, const uint16_t* q, const uint16_t* k_new
   a.inline_tail = 1;
   a.tail_append = append ? 1 : 0;
   a.tail_ctr_end = reinterpret_cast<int*>(static_cast<char*>(workspace) + (workspace_bytes & ~int64_t(3)));
+  l2_args(a);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (tok) hipLaunchKernelGGL(attn_prefix_kernel<PAGED_TOK>, dim3((unsigned)(hkv * total_parts)), dim3(THREADS), 0, s, a);
   else hipLaunchKernelGGL(attn_prefix_kernel<PAGED_T64>, dim3((unsigned)(hkv * total_parts)), dim3(THREADS), 0, s, a);
@@ -3933,6 +4020,7 @@ int launch_layers(AttnArgs& a, bool tok, const void* layers_dev, int64_t n_layer
   a.tail_ctr_end = reinterpret_cast<int*>(reinterpret_cast<char*>(a.ws) + (workspace_bytes & ~int64_t(3)));
   a.fwd_out = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(a.ws) + part_bytes);
   a.flags_base = reinterpret_cast<uint32_t*>(a.fwd_out + n_layers * a.hq * D / 2);
+  l2_args(a);
   if (tok) hipLaunchKernelGGL(attn_layers_kernel<CONTIG_TOK>, dim3((unsigned)grid), dim3(THREADS), 0, s, a, layers_dev, (int)n_layers);
   else hipLaunchKernelGGL(attn_layers_kernel<CONTIG_T64>, dim3((unsigned)grid), dim3(THREADS), 0, s, a, layers_dev, (int)n_layers);
   return check_launch(what);
