@@ -351,9 +351,11 @@ int nkv_decode_step_combine_tok(const uint16_t* q, const uint16_t* k_new, const 
  *
  * workspace: nkv_layers_workspace_bytes(hkv, hq, n_parts, n_layers) bytes, zero-filled before
  * its first use and then dedicated to calls with this (hkv, hq, n_parts, n_layers): a call
- * leaves its partial blocks and layer counters at zero, but the tagged copies of the outputs,
- * the issue flags and the launch counter (the tags' source) keep their values, so the buffer
- * must be zero-filled again before it serves another configuration or another entry point.
+ * leaves layer 0's partial block and the layer counters at zero, but the later layers' partial
+ * blocks (each set back to zero by its head's merger before the layer is published), the tagged
+ * copies of the outputs, the issue flags and the launch counter (the tags' source) keep their
+ * values, so the buffer must be zero-filled again before it serves another configuration or
+ * another entry point.
  * n_parts <= 0 takes nkv_layers_default_parts.
  *
  * Failure mode. The waits assume every workgroup of the grid runs at once. The occupancy check

@@ -168,11 +168,13 @@ class ChainedStep:
                                "its grid must be resident at once, so nothing else may hold the GPU's CUs")
 
     def idle_state(self) -> dict:
-        """Between launches: whether the partial blocks and the counters are back at zero, and the
-        number of launches so far (the forwarding tags' counter). Synchronizes."""
+        """Between launches: whether layer 0's partial block (the one the next launch polls first;
+        each later layer's block is set back to zero by its merger before that layer is published)
+        and the counters are back at zero, and the number of launches so far (the forwarding tags'
+        counter). Synchronizes."""
         c = self.cache
-        part_words = self.n_layers * c.num_kv_heads * self.n_parts * (c.num_q_heads // c.num_kv_heads * 128 +
-                                                                      ((2 * (c.num_q_heads // c.num_kv_heads) + 3) & ~3))
+        part_words = c.num_kv_heads * self.n_parts * (c.num_q_heads // c.num_kv_heads * 128 +
+                                                      ((2 * (c.num_q_heads // c.num_kv_heads) + 3) & ~3))
         w = self._sync_words()
         n = self.n_layers
         return {"partials_zero": bool(int(self.workspace[:part_words].abs().sum().item()) == 0),

@@ -1350,6 +1350,15 @@ __device__ __forceinline__ void hand_st(T* p, T w, bool l2) {
   if (l2) __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
   else __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// 16 zero bytes, handed over like a published word
+__device__ __forceinline__ void zero_st16(uint4* p, bool l2) {
+  if (l2) {
+    *p = uint4{0u, 0u, 0u, 0u};
+  } else {
+    hand_st(reinterpret_cast<uint64_t*>(p), uint64_t(0), false);
+    hand_st(reinterpret_cast<uint64_t*>(p) + 1, uint64_t(0), false);
+  }
+}
 __device__ __forceinline__ void pub_st(float* p, float v, bool l2) {
   hand_st(reinterpret_cast<uint32_t*>(p), __float_as_uint(v) ^ PUB_KEY, l2);
 }
@@ -2344,13 +2353,18 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
 //  - forwarded: q is the whole of layer l - 1's output, and (for a merger) head h's k_new / v_new
 //    rows lie in the rows head h's merger wrote. The reader reloads the tagged words it needs
 //    until they carry this launch's tag (per-location coherence, no fence). Without dep_all
-//    nothing else is waited for: each head's layers then chain on their own. With dep_all, lane
-//    0 also polls layer l - 1's counter in the same rounds until every head's merger is done.
+//    nothing else is waited for: each head's layers then chain on their own. With dep_all, lanes
+//    0 .. hq - 1 also poll layer l - 1's issue flags in the same rounds until every query head's
+//    output is issued.
 //  - otherwise one lane waits for layer l - 1's counter to reach hkv (relaxed agent-scope polls,
 //    then an agent-scope acquire fence) and the inputs are plain loads.
 // The host refuses inputs that these waits do not order (nkv_decode_layers_t64). The prefix
 // partials use the published-word protocol of the fused tail (per-location coherence, no flag);
-// each layer has its own partial block.
+// each layer has its own partial block. Head h's merger sets its layer-(l + 1) block back to
+// zero before its layer-l output, which no part of head h can publish layer l + 1 without;
+// layer 0's slots are set back to zero by their writers at the end of the launch. The partials
+// and the forwarded outputs are handed between workgroups of one KV head, which share an XCD:
+// with the XCD-local hand-over (l2_xcc) they stay in its L2.
 //
 // Overlap. Nothing in a layer's prefix depends on an earlier layer (the append writes only the
 // current group, which the prefix does not read), so as soon as a streaming workgroup has
@@ -2495,7 +2509,11 @@ __device__ __forceinline__ bool wait_layer(const AttnArgs& a, int l, int target,
 
 // One layer of head h's merger (workgroup (h, 0) of the chained kernel): wait for layer l - 1,
 // append + ring + merge of layer l into out / lse, count itself on layer l's counter. Returns
-// whether its wait gave up. (The consumed partial block is zeroed at the end of the launch.)
+// whether its wait gave up. It first sets head h's partial block of layer l + 1 back to zero
+// (it was consumed in the previous launch): no part of head h publishes into it before this
+// merger's layer-l output, which follows these stores' completion. With the XCD-local hand-over
+// the block's lines are then dirty in the L2 when the merger polls them, so every poll is an L2
+// hit. Layer 0's block is set back to zero by its writers at the end of the launch.
 template <bool TOK>
 __device__ __forceinline__ bool merger_layer(const AttnArgs& args, const void* layers, int l, int h, uint8_t* lds_raw,
                                           int64_t pos, bool pos_ok, int64_t U, bool lost) {
@@ -2519,6 +2537,13 @@ __device__ __forceinline__ bool merger_layer(const AttnArgs& args, const void* l
   if (tid == 0) {
     sm.ring_staged = 0;
     sm.ring_done = 0;
+  }
+  if (l + 1 < la.n_layers) {
+    const int P = la.n_parts, pw = part_stride(gq);
+    uint4* nb = reinterpret_cast<uint4*>(la.ws + ((int64_t)la.hkv * P + (int64_t)h * P) * pw);
+    const bool l2 = l2_local(la);
+    for (int i = tid; i < P * pw / 4; i += THREADS) zero_st16(nb + i, l2);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // (before the barrier below)
   }
   if (wave == IN_WAVE) {
     bool ok = true;
@@ -2615,10 +2640,12 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
   };
   if (merger) {
     for (int l = 0; l < n_layers; ++l) lost |= merger_layer<TOK>(layer_args<TOK>(a, layers, l, ftag), layers, l, h, lds_raw, pos, pos_ok, U, lost);
-    // the last layer's consumed partial block back to zero (the earlier layers' slots are zeroed
-    // by their writers, below)
-    uint4* blk = reinterpret_cast<uint4*>(layer_args<TOK>(a, layers, n_layers - 1, ftag).ws + (int64_t)h * P * pw);
-    for (int i = tid; i < P * pw / 4; i += THREADS) blk[i] = uint4{0u, 0u, 0u, 0u};
+    // one layer: its consumed partial block back to zero (with more, layer 0's slots are zeroed by
+    // their writers, below, and every later block by this merger in the next launch)
+    if (n_layers == 1) {
+      uint4* blk = reinterpret_cast<uint4*>(a.ws + (int64_t)h * P * pw);
+      for (int i = tid; i < P * pw / 4; i += THREADS) blk[i] = uint4{0u, 0u, 0u, 0u};
+    }
   } else {
   if (wave != IN_WAVE) issue_first(layer_args<TOK>(a, layers, 0, ftag));
   for (int l = 0; l < n_layers; ++l) {
@@ -2772,12 +2799,12 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
     __syncthreads();
     if (l + 1 < n_layers) issue_first(layer_args<TOK>(a, layers, l + 1, ftag));
   }
-  // head h's merger has consumed this part's partials of layers 0 .. n_layers - 2: this workgroup
-  // read layer n_layers - 1's q after that merger finished layer n_layers - 2 (from its tagged
-  // words, or after the counter that it joins only once it has merged). Those slots back to zero,
-  // read again by the next launch
-  for (int l = 0; l + 1 < n_layers; ++l) {
-    uint4* slot = reinterpret_cast<uint4*>(a.ws + ((int64_t)l * a.hkv * P + (int64_t)h * P + part) * pw);
+  // head h's merger has consumed this part's partial of layer 0: this workgroup read layer
+  // n_layers - 1's q after that merger finished layer n_layers - 2 >= 0 (from its tagged words,
+  // or after the counter that it joins only once it has merged). That slot back to zero, polled
+  // first by the next launch (the later layers' blocks are zeroed by the merger before use)
+  if (n_layers > 1) {
+    uint4* slot = reinterpret_cast<uint4*>(a.ws + ((int64_t)h * P + part) * pw);
     for (int i = tid; i < pw / 4; i += THREADS) slot[i] = uint4{0u, 0u, 0u, 0u};
   }
   }
