@@ -121,6 +121,8 @@ def parse_args():
                     help="--mode chain: every layer waits for every head of the layer before (all), or forwarded "
                          "inputs wait only for their own head (head)")
     ap.add_argument("--e2e-steps", type=int, default=32, help="steps of the end-to-end workload in the default run")
+    ap.add_argument("--e2e-separate", action="store_true",
+                    help="e2e: the attention block as three launches (qkv GEMV, q/k norm + RoPE, decode step)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarize two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into a traffic file")
     ap.add_argument("--traffic-key", choices=sorted(TRAFFIC), default="chain_t64")
@@ -753,9 +755,9 @@ def bench_e2e(args, steps: int | None = None) -> dict:
     """End-to-end graph decode of the random-weight decoder with Qwen3-4B geometry (36 layers,
     hidden 2560, 32 q / 8 KV heads of 128, SwiGLU 9728, vocab 151936, fp16 weights) over the
     int8t64 cache: the prompt (``--ctx`` random ids) is prefilled in streamed chunks, then each
-    step (embed, 36 x [qkv GEMV + RMSNorm, q/k norm + RoPE, fused int8 append + attention, o_proj +
-    residual, SwiGLU gate/up + RMSNorm, down + residual], final RMSNorm + lm_head, argmax,
-    pos += 1) is one hipGraph replay."""
+    step (embed, 36 x [attention block: RMSNorm + qkv projection, q/k norm + RoPE, int8 append +
+    attention, in one launch (``--e2e-separate``: three); o_proj + residual, SwiGLU gate/up +
+    RMSNorm, down + residual], final RMSNorm + lm_head, argmax, pos += 1) is one hipGraph replay."""
     import torch
 
     from nova_amd.decode import GraphDecoder
@@ -765,7 +767,8 @@ def bench_e2e(args, steps: int | None = None) -> dict:
     L, ctx, W, K = args.layers, args.ctx, args.warmup, steps or args.steps
     cfg = SkeletonConfig(num_hidden_layers=L, vocab_size=VOCAB_QWEN3_4B)
     model = SkeletonForCausalLM(cfg, seed=5, device=dev, dtype=torch.float16).eval()
-    model.use_decode_kernels(True)
+    fused = not getattr(args, "e2e_separate", False)
+    model.use_decode_kernels(True, fused_qkv=fused)
     max_len = -(-(ctx + 4 + W + K + 1) // 64) * 64
     dec = GraphDecoder(model, max_len=max_len, quant="int8", device=dev)
     if args.parts:
@@ -798,7 +801,10 @@ def bench_e2e(args, steps: int | None = None) -> dict:
             "config": {"workload": f"greedy decode, {L} layers (hidden {cfg.hidden_size}, SwiGLU "
                                    f"{cfg.intermediate_size}), vocab {cfg.vocab_size}, int8t64 KV, {ctx}-token "
                                    f"prompt prefilled in {args.chunk}-token streamed chunks",
-                       "layers": L, "context": ctx, "prefill_chunk": args.chunk},
+                       "layers": L, "context": ctx, "prefill_chunk": args.chunk,
+                       "attention_block": ("one launch per layer (input RMSNorm + qkv projection, q/k norm + RoPE, "
+                                           "append + attention)" if fused else
+                                           "three launches per layer (qkv GEMV, q/k norm + RoPE, append + attention)")},
             "algorithmic_bytes_per_step": round(step_bytes), "step_gbs": round(gbs, 1),
             "step_pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2), "prefill_s": round(prefill_s, 3),
             "prefill_tokens_per_s": round(ctx / prefill_s, 1)}

@@ -188,6 +188,42 @@ int nkv_decode_step_combine_t64(const uint16_t* q, const uint16_t* k_new, const 
                                 float* lse_out, void* workspace, int64_t workspace_bytes,
                                 int64_t n_parts, void* stream);
 
+/*
+ * A decoder layer's attention block for one decode token in one launch: the input RMSNorm and
+ * the stacked q/k/v projection, the per-head q and k RMSNorm and the rotary embedding at
+ * *pos_dev, then nkv_decode_step_t64's append and attention of the token. Replaces the
+ * `q_proj` / `k_proj` / `v_proj`, `q_norm` / `k_norm`, `apply_rotary_pos_emb` and
+ * `update` + `attend` sequence of `LeanAttention.forward` (src/nova/layers.py:99-137) for one
+ * token, with the input norm of `LeanDecoderLayer` (src/nova/layers.py:177-218).
+ *
+ * x [hidden] fp16 (the residual stream), x_gamma [hidden] (its RMSNorm weight, x_eps),
+ * w_qkv [(hq + 2 hkv) * 128][hidden] fp16 (q heads, then k heads, then v heads); hidden a
+ * multiple of 8, at most 3072. q_gamma / k_gamma [128] fp16 (the head norms, qk_eps),
+ * inv_freq [64] fp32 (the RoPE frequencies). qkv_out, when not NULL, receives the normalized
+ * and rotated q and k and the v rows [(hq + 2 hkv) * 128] fp16. The cache, scalar, output and
+ * n_parts arguments are nkv_decode_step_t64's; hq / hkv <= 4.
+ * The results are those of nkv_gemv(x, x_gamma, x_eps, w_qkv) + nkv_qk_norm_rope +
+ * nkv_decode_step_t64, bit for bit. While the first K/V groups stream in, the workgroups of
+ * each KV head compute that head's (hq / hkv + 2) * 128 rows between them and hand them over
+ * (tagged words, through the XCD's L2 when the hand-over is on, nkv_l2_handover), so every
+ * workgroup of a KV head waits for the others: the grid (hkv * max(n_parts, 32) workgroups)
+ * must fit the device at once, or the call returns NKV_ERR_UNSUPPORTED.
+ * workspace: nkv_decode_step_qkv_workspace_bytes(hkv, hq, capacity, n_parts) bytes,
+ * zero-filled before its first use; it may also serve nkv_decode_step_t64 with the same
+ * n_parts (the same partials and counters, which both leave at zero; the row words and
+ * their tags lie beyond the partials). A wait for rows is bounded (0.2 s): the outputs are
+ * then NaN.
+ */
+int64_t nkv_decode_step_qkv_workspace_bytes(int64_t hkv, int64_t hq, int64_t capacity, int64_t n_parts);
+int nkv_decode_step_qkv_t64(const uint16_t* x, const uint16_t* x_gamma, float x_eps, const uint16_t* w_qkv,
+                            int64_t hidden, const uint16_t* q_gamma, const uint16_t* k_gamma, float qk_eps,
+                            const float* inv_freq, uint16_t* qkv_out, uint8_t* kq, uint16_t* kmn,
+                            uint16_t* kst, uint8_t* vq, uint16_t* vmn, uint16_t* vst, uint16_t* tail_k,
+                            uint16_t* tail_v, const int64_t* pos_dev, const int64_t* first_dev,
+                            int64_t* written_dev, int64_t* qlen_dev, int64_t* pg_dev, int64_t hq,
+                            int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out, float* lse_out,
+                            void* workspace, int64_t workspace_bytes, int64_t n_parts, void* stream);
+
 /* Limits of nkv_decode_step_static_t64's scratch: partial results, and the publication
  * area (completion counters and flags). */
 #define NKV_STATIC_PART_BYTES (4 << 20)

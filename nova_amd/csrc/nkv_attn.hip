@@ -162,6 +162,22 @@ struct AttnArgs {
   // the L2 hand-over: l2_xcc = the device's XCD count n when workgroups b and b + n share an XCD
   // and n divides hkv (the workgroups of a KV head then share one XCD), 0 when off
   int l2_xcc;
+  // the fused projection step (attn_prefix_kernel with QKV): the layer's input x [hidden] and its
+  // RMSNorm gamma, the stacked projection w_qkv [(hq + 2 hkv) D][hidden], the q/k head-norm
+  // gammas [D], the RoPE frequencies [D / 2]; hand: the tagged row words [hkv][QKV_HAND_ROWS],
+  // qkv_epoch [hkv]: the tags' source per KV head; qkv_out: the normalized and rotated q / k and
+  // v [(hq + 2 hkv) D], or null
+  const uint16_t* x;
+  const uint16_t* x_gamma;
+  const uint16_t* w_qkv;
+  const uint16_t* q_gamma;
+  const uint16_t* k_gamma;
+  const float* inv_freq;
+  float eps_x, eps_qk;
+  int hidden;
+  uint64_t* hand;
+  int* qkv_epoch;
+  uint16_t* qkv_out;
 };
 
 // XOR key of the 16-byte chunk positions of LDS row `row` (a token within its group).
@@ -2098,7 +2114,158 @@ __device__ __forceinline__ void paged_ring_tail(const AttnArgs& a, int h, int b,
   }
 }
 
-template <int LAYOUT>
+// ---------------------------------------------------------------- the fused projection step
+//
+// nkv_decode_step_qkv_t64 runs a decoder layer's input RMSNorm, its stacked q/k/v projection and
+// the q/k head norms with the rotary embedding in the fused decode step's launch, ahead of the
+// append, prefix and tail: the first K/V groups stream in while the projection is computed. The
+// (gq + 2) D rows of KV head h's block (its gq q heads, its k and v head) are split over the
+// head's workgroups; each computes its rows exactly as gemv_kernel does (the same input chunks
+// per thread, reduction and summation order, fp16 results), publishes them as tagged words (the
+// launch's tag in the high half: qkv_epoch[h] + 1) and reads back the head's vectors. Waves
+// QKV_WAVES.. compute nothing: they issue every wave's first group and the append unit's ring
+// rows, so that the computing waves' load counters hold no LDS-DMA while they wait for rows.
+constexpr uint64_t LAYER_WAIT_TICKS = 20000000ull;  // 0.2 s of the 100 MHz real-time counter per wait
+constexpr int QKV_WAVES = 6;                   // waves computing rows
+constexpr int QKV_MAX_NL = 6;                  // 16-byte input chunks per lane and row
+constexpr int QKV_MAX_HIDDEN = 64 * 8 * QKV_MAX_NL;  // 3072: the input chunks fit one chunk per thread
+constexpr int QKV_ROWS = 4;                    // rows of a wave in flight at once
+constexpr int QKV_MAX_GQ = 4;                 // q heads per KV head (waves 0..3 fetch them)
+constexpr int QKV_HAND_ROWS = (QKV_MAX_GQ + 2) * D;  // tagged row words per KV head
+
+// The append unit's ring rows (the new token comes from the prologue, in LDS).
+__device__ __forceinline__ void issue_unit_ring(const UnitIO& io, int unit, uint32_t src) {
+  const int lane = threadIdx.x & 63, ch0 = unit % (D / UNIT_CH) * UNIT_CH;
+  dma16(uniform_ptr(io.ring + ch0), (uint32_t)(lane * D * 2), src);
+}
+
+// The prologue (`issued`: an LDS counter at zero, which each computing wave increments once its
+// first rows' weight loads are issued): this workgroup's rows of head h's block, computed and
+// published; then the head's
+// q vectors (normalized, rotated) into q_lds, k (normalized, rotated) and v into kv_lds [2][D],
+// the append unit's 8 channels of the new token into unit_src's last row (`unit` >= 0), and, in
+// part 0, k / v into the step's k_new / v_new and every vector into qkv_out. No workgroup barrier:
+// each computing wave normalizes its own copy of the input, in the order gemv_kernel does
+// (lane l holds input chunks l + 64 u, which gemv_kernel's wave u holds in lane l: the wave sums
+// of the squares are its waves' sums, added in the same order). Returns false when a wait for
+// rows gave up (its vectors are then NaN).
+__device__ bool qkv_prologue(const AttnArgs& a, int h, int part, int parts, int64_t pos, uint32_t tag, int unit,
+                             uint16_t* q_lds, uint16_t* kv_lds, uint16_t* unit_src, int* issued) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nch = a.hidden / 8, nl = (nch + 63) / 64;
+  const int gq = a.gq, nrows = (gq + 2) * D;
+  const int rw = (nrows + parts - 1) / parts, r0 = min(part * rw, nrows), r1 = min(r0 + rw, nrows);
+  const int rpw = (rw + QKV_WAVES - 1) / QKV_WAVES;
+  const bool l2 = l2_local(a);
+  uint64_t* hw = a.hand + (int64_t)h * QKV_HAND_ROWS;
+  if (wave < QKV_WAVES) {
+    const int wr0 = min(r0 + wave * rpw, r1), wr1 = min(wr0 + rpw, r1);
+    // head h's row r of the stacked weight: its gq q heads, then its k head, then its v head
+    auto row_ptr = [&](int r) -> const uint16_t* {
+      const int vec = r / D, d = r % D;
+      const int64_t g = vec < gq ? (int64_t)h * gq + vec : (vec == gq ? a.hq + h : a.hq + a.hkv + h);
+      return a.w_qkv + (g * D + d) * (int64_t)a.hidden;
+    };
+    uint4 xn[QKV_MAX_NL], gm[QKV_MAX_NL];
+#pragma unroll
+    for (int u = 0; u < QKV_MAX_NL; ++u) {
+      const int c = lane + 64 * u;
+      const bool in = u < nl && c < nch;
+      xn[u] = in ? *reinterpret_cast<const uint4*>(a.x + 8 * c) : uint4{0u, 0u, 0u, 0u};
+      gm[u] = in ? *reinterpret_cast<const uint4*>(a.x_gamma + 8 * c) : uint4{0u, 0u, 0u, 0u};
+    }
+    uint4 wv[QKV_ROWS][QKV_MAX_NL];
+    auto issue = [&](int rb) {
+#pragma unroll
+      for (int j = 0; j < QKV_ROWS; ++j)
+#pragma unroll
+        for (int u = 0; u < QKV_MAX_NL; ++u) {
+          const int c = lane + 64 * u;
+          wv[j][u] = (u < nl && rb + j < wr1 && c < nch) ? ld_weight(row_ptr(rb + j) + 8 * c) : uint4{0u, 0u, 0u, 0u};
+        }
+    };
+    issue(wr0);  // the first rows' weights fly while the input is normalized
+    // (counted once issued: the other waves hold the first groups' loads back until every
+    // computing wave's weights are requested, so that HBM serves the rows first)
+    if (lane == 0) __hip_atomic_fetch_add(issued, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    float tot = 0.0f;
+#pragma unroll
+    for (int u = 0; u < QKV_MAX_NL; ++u) tot += hsum64(sumsq8(xn[u], 0.0f));  // (chunks past the input are 0)
+    const float r = rsqrtf(tot * (1.0f / (float)a.hidden) + a.eps_x);  // torch: mean = sum * (1/n), then rsqrt
+#pragma unroll
+    for (int u = 0; u < QKV_MAX_NL; ++u) xn[u] = rms_scale8(xn[u], gm[u], r);
+    // the rows: fp32 dot products in gemv_kernel's order, rounded to fp16, published as tagged words
+    for (int rb = wr0; rb < wr1; rb += QKV_ROWS) {
+      if (rb != wr0) issue(rb);
+      float acc[QKV_ROWS];
+#pragma unroll
+      for (int j = 0; j < QKV_ROWS; ++j) acc[j] = 0.0f;
+#pragma unroll
+      for (int u = 0; u < QKV_MAX_NL; ++u) {
+        if (u < nl && lane + 64 * u < nch) {
+#pragma unroll
+          for (int j = 0; j < QKV_ROWS; ++j) acc[j] = dot8(wv[j][u], xn[u], acc[j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < QKV_ROWS; ++j) {
+        const float sum = hsum64(acc[j]);
+        if (lane == 0 && rb + j < wr1) hand_st(hw + rb + j, ((uint64_t)tag << 32) | f2h(sum), l2);
+      }
+    }
+  }
+  // the head's vectors: wave v < gq takes q head v, wave 4 k, wave 5 v; lane l its elements l and
+  // l + 64 (the pair the rotary embedding mixes)
+  bool ok = true;
+  const int vec = wave < gq ? wave : (wave == 4 ? gq : (wave == 5 ? gq + 1 : -1));
+  if (vec >= 0) {
+    const uint64_t* src = hw + vec * D;
+    uint64_t w0 = 0, w1 = 0;  // (tag 0 is never current)
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+      if ((uint32_t)(w0 >> 32) != tag) w0 = __hip_atomic_load(src + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((uint32_t)(w1 >> 32) != tag) w1 = __hip_atomic_load(src + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool miss = (uint32_t)(w0 >> 32) != tag || (uint32_t)(w1 >> 32) != tag;
+      if (!__builtin_amdgcn_ballot_w64(miss)) break;
+      if (__builtin_amdgcn_s_memrealtime() - t0 > LAYER_WAIT_TICKS) {
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    uint16_t lo = (uint16_t)w0, hi = (uint16_t)w1;
+    if (vec <= gq) {
+      const uint16_t* g = vec < gq ? a.q_gamma : a.k_gamma;
+      qk_norm_rope_lane(h2f(lo), h2f(hi), h2f(g[lane]), h2f(g[lane + 64]), a.eps_qk, (float)pos * a.inv_freq[lane],
+                        lo, hi);
+    }
+    if (!ok) lo = hi = 0x7E00u;  // NaN
+    uint16_t* dst = vec < gq ? q_lds + vec * D : kv_lds + (vec - gq) * D;
+    dst[lane] = lo;
+    dst[lane + 64] = hi;
+    // the append unit's channels of the new token (unit u: channels 8 (u % 16) .. + 7 of k (u < 16) or v)
+    const int which = vec - gq, ch0 = unit % (D / UNIT_CH) * UNIT_CH;
+    if (which >= 0 && unit >= 0 && unit / (D / UNIT_CH) == which) {
+      if (lane - ch0 >= 0 && lane - ch0 < UNIT_CH) unit_src[GT * UNIT_CH + lane - ch0] = lo;
+      if (lane + 64 - ch0 >= 0 && lane + 64 - ch0 < UNIT_CH) unit_src[GT * UNIT_CH + lane + 64 - ch0] = hi;
+    }
+    if (part == 0) {
+      if (which >= 0) {  // the step's new token, read by this workgroup's tail
+        uint16_t* kv = const_cast<uint16_t*>(which == 0 ? a.k_new : a.v_new) + (int64_t)h * a.kv_hs;
+        kv[lane] = lo;
+        kv[lane + 64] = hi;
+      }
+      if (a.qkv_out) {
+        const int64_t g = vec < gq ? (int64_t)h * gq + vec : (vec == gq ? a.hq + h : a.hq + a.hkv + h);
+        a.qkv_out[g * D + lane] = lo;
+        a.qkv_out[g * D + lane + 64] = hi;
+      }
+    }
+  }
+  return ok;
+}
+
+template <int LAYOUT, bool QKV = false>
 __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   constexpr bool TOK = LAYOUT == CONTIG_TOK || LAYOUT == PAGED_TOK;
   constexpr bool PAGED = LAYOUT == PAGED_T64 || LAYOUT == PAGED_TOK;
@@ -2152,12 +2319,41 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   // alternating); the next group's halves are issued as each slot is freed.
   const int ng = (int)(ge - gs);
   const uint32_t rul_lds = my_lds + 2 * HALF_SLOT;
+  UnitIO uio{};
+  if (!TOK && !PAGED && append) uio = unit_io(a, h, part, pos);
+  [[maybe_unused]] uint32_t qkv_tag = 0;
+  if constexpr (QKV) {
+    // the projection first (q, and the new token's k / v, come from it); the first groups and the
+    // append unit's ring rows are issued by the waves that do not compute, and have landed when
+    // the workgroup meets below
+    __shared__ __attribute__((aligned(16))) uint16_t kv_lds[2 * D];
+    __shared__ int issued;
+    if (tid == 0) issued = 0;
+    __syncthreads();
+    qkv_tag = (uint32_t)__hip_atomic_load(a.qkv_epoch + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    if (wave >= QKV_WAVES) {
+      // after every computing wave's first weight loads (bounded: 2^16 short sleeps)
+      for (int n = 0; n < (1 << 16); ++n) {
+        if (__hip_atomic_load(&issued, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= QKV_WAVES) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      for (int w = wave - QKV_WAVES; w < WAVES; w += WAVES - QKV_WAVES) {
+        if (w >= ng) break;
+        const uint32_t wl = __builtin_amdgcn_readfirstlane(lds_addr(lds_raw + w * wave_lds));
+        issue_half(a, h, gs + w, 0, wl, wl + 2 * HALF_SLOT);
+        issue_half(a, h, gs + w, 1, wl + HALF_SLOT, wl + 2 * HALF_SLOT);
+      }
+      if (wave == QKV_WAVES && append) issue_unit_ring(uio, part, src_lds);
+    }
+    const bool ok = qkv_prologue(a, h, part, (int)(gridDim.x / a.hkv), pos, qkv_tag, append ? part : -1, q_lds,
+                                 kv_lds, unit_src, &issued);
+    (void)ok;  // (a wait that gave up leaves NaN vectors: the outputs are NaN)
+    if (wave >= QKV_WAVES) wait_groups_all();
+  } else {
   // Q and the append unit's rows are loaded ahead of the groups, so that waiting for them
   // leaves the groups in flight
   if (wave == 0 && prefix)
     issue_q(a.q + ((int64_t)b * a.hq + h * a.gq) * D, a.gq, __builtin_amdgcn_readfirstlane(lds_addr(q_lds)));
-  UnitIO uio{};
-  if (!TOK && !PAGED && append) uio = unit_io(a, h, part, pos);
   if (!TOK && wave == 0 && append) issue_unit_rows(uio, part, src_lds);
 
   if (wave < ng) {
@@ -2177,6 +2373,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   } else {
     wait_groups_all();
   }
+  }  // QKV
   __syncthreads();
 
   if (append) {
@@ -2331,6 +2528,11 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
     }
   } else {
     tail_body<false>(a, h, b, sm, TAIL_MERGER, pos, pos_ok, U, &tl, &qb);
+    // every workgroup of head h has read its rows (before publishing the partials just merged):
+    // the next launch's tag
+    if constexpr (QKV) {
+      if (tid == 0) __hip_atomic_store(a.qkv_epoch + h, (int)qkv_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -2377,7 +2579,6 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
 // end every workgroup takes an exit ticket (acquire-release); the last one sets the layer
 // counters and the ticket back to zero, so every launch starts and ends with them at zero.
 constexpr int IN_WAVE = WAVES - 1;                 // a streaming workgroup's input wave
-constexpr uint64_t LAYER_WAIT_TICKS = 20000000ull;  // 0.2 s of the 100 MHz real-time counter per wait
 
 // The sync words of a chained launch at the workspace's end (tail_ctr_end): done[l] at
 // end[-1 - l], the exit ticket at end[-1 - n_layers], the error word at end[-2 - n_layers], the
@@ -3351,6 +3552,40 @@ static int launch_attn(AttnArgs& a, int64_t n_parts, int64_t workspace_bytes, hi
 
 static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The fused projection step's workspace: the decode step's partials (n_parts per KV head), the
+// tagged row words [hkv][QKV_HAND_ROWS], the tags' epochs [hkv] (256-byte padded), the new token's
+// k / v [hkv][2][D] fp16, and the step's counters at the end.
+static int64_t up256(int64_t n) { return (n + 255) / 256 * 256; }
+static int64_t qkv_part_bytes(int64_t hkv, int64_t hq, int64_t n_parts) {
+  return up256(hkv * std::max<int64_t>(1, n_parts) * part_floats(hq, hkv) * (int64_t)sizeof(float));
+}
+static int64_t qkv_workspace_bytes(int64_t hkv, int64_t hq, int64_t n_parts) {
+  return qkv_part_bytes(hkv, hq, n_parts) + hkv * QKV_HAND_ROWS * 8 + up256(hkv * 4) + up256(hkv * 2 * D * 2) +
+         sync_bytes(hkv, n_parts);
+}
+
+// Workgroups of the fused projection step resident at once on the current device (every
+// workgroup of a KV head waits for rows the others compute, so the grid must fit at once).
+static std::mutex g_qkv_mu;
+static int g_qkv_resident[L2_DEVICES];
+static int qkv_resident(int* out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= L2_DEVICES)
+    return fail(NKV_ERR_HIP, "decode_step_qkv_t64: no usable current device (%d)", dev);
+  std::lock_guard<std::mutex> lock(g_qkv_mu);
+  int& r = g_qkv_resident[dev];
+  if (!r) {
+    int cus = 0, per_cu = 0;
+    hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess)
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_prefix_kernel<CONTIG_T64, true>, THREADS, 0);
+    if (e != hipSuccess) return fail(NKV_ERR_HIP, "decode_step_qkv_t64: occupancy query: %s", hipGetErrorString(e));
+    r = cus * per_cu;
+  }
+  *out = r;
+  return NKV_OK;
+}
+
 }  // namespace nkv
 
 using namespace nkv;
@@ -3598,6 +3833,76 @@ extern "C" int nkv_l2_handover(int enable, int64_t* xcds, void* stream) {
   }
   if (xcds) *xcds = on;
   return NKV_OK;
+}
+
+extern "C" int64_t nkv_decode_step_qkv_workspace_bytes(int64_t hkv, int64_t hq, int64_t capacity, int64_t n_parts) {
+  if (hkv <= 0 || hq <= 0 || capacity <= 0) return 0;
+  if (n_parts <= 0) n_parts = default_parts(hkv, cdiv(capacity, GT));
+  return qkv_workspace_bytes(hkv, hq, n_parts);
+}
+
+extern "C" int nkv_decode_step_qkv_t64(const uint16_t* x, const uint16_t* x_gamma, float x_eps, const uint16_t* w_qkv,
+                                       int64_t hidden, const uint16_t* q_gamma, const uint16_t* k_gamma, float qk_eps,
+                                       const float* inv_freq, uint16_t* qkv_out, uint8_t* kq, uint16_t* kmn,
+                                       uint16_t* kst, uint8_t* vq, uint16_t* vmn, uint16_t* vst, uint16_t* tail_k,
+                                       uint16_t* tail_v, const int64_t* pos_dev, const int64_t* first_dev,
+                                       int64_t* written_dev, int64_t* qlen_dev, int64_t* pg_dev, int64_t hq,
+                                       int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out, float* lse_out,
+                                       void* workspace, int64_t workspace_bytes, int64_t n_parts, void* stream) {
+  const char* what = "decode_step_qkv_t64";
+  set_error("");
+  if (int rc = check_heads(hq, hkv, head_dim)) return rc;
+  if (hq / hkv > QKV_MAX_GQ)
+    return fail(NKV_ERR_UNSUPPORTED, "%s: %lld q heads per KV head (at most %d)", what, (long long)(hq / hkv), QKV_MAX_GQ);
+  if (capacity <= 0) return fail(NKV_ERR_INVALID, "%s: capacity must be positive", what);
+  if (hidden <= 0 || hidden % 8 || hidden > QKV_MAX_HIDDEN)
+    return fail(NKV_ERR_UNSUPPORTED, "%s: hidden size %lld (a positive multiple of 8, at most %d)", what,
+                (long long)hidden, QKV_MAX_HIDDEN);
+  if (!x || !x_gamma || !w_qkv || !q_gamma || !k_gamma || !inv_freq || !kq || !kmn || !kst || !vq || !vmn || !vst ||
+      !tail_k || !tail_v || !pos_dev || !written_dev || !qlen_dev || !pg_dev || !out || !workspace)
+    return fail(NKV_ERR_INVALID, "%s: null pointer argument", what);
+  if (!al16(x) || !al16(x_gamma) || !al16(w_qkv) || !al16(tail_k) || !al16(tail_v) || !al16(kq) || !al16(vq) ||
+      !al16(kmn) || !al16(kst) || !al16(vmn) || !al16(vst) || !al16(workspace))
+    return fail(NKV_ERR_UNSUPPORTED, "%s: buffers must be 16-byte aligned", what);
+  if (capacity > (int64_t(1) << 24)) return fail(NKV_ERR_UNSUPPORTED, "%s: capacity %lld exceeds 16M tokens", what, (long long)capacity);
+  const int64_t ngroups = cdiv(capacity, GT);
+  if (n_parts <= 0) n_parts = default_parts(hkv, ngroups);
+  if (n_parts > MERGER_MAX_PARTS || hkv > MERGER_MAX_HEADS)
+    return fail(NKV_ERR_UNSUPPORTED, "%s: %lld parts per KV head, %lld KV heads (at most %d and %d)", what,
+                (long long)n_parts, (long long)hkv, MERGER_MAX_PARTS, MERGER_MAX_HEADS);
+  const int64_t parts = std::max<int64_t>(n_parts, APPEND_UNITS), grid = hkv * parts;
+  int resident = 0;
+  if (int rc = qkv_resident(&resident)) return rc;
+  if (grid > resident)
+    return fail(NKV_ERR_UNSUPPORTED, "%s: %lld workgroups exceed the %d this device holds at once (the workgroups of a "
+                "KV head wait for each other's rows)", what, (long long)grid, resident);
+  const int64_t need = qkv_workspace_bytes(hkv, hq, n_parts);
+  if (workspace_bytes < need)
+    return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
+  char* ws = static_cast<char*>(workspace);
+  uint64_t* hand = reinterpret_cast<uint64_t*>(ws + qkv_part_bytes(hkv, hq, n_parts));
+  int* epoch = reinterpret_cast<int*>(hand + hkv * QKV_HAND_ROWS);
+  uint16_t* kvbuf = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(epoch) + up256(hkv * 4));
+  AttnArgs a{};
+  a.k_new = kvbuf; a.v_new = kvbuf + D; a.kv_hs = 2 * D;
+  a.kq = kq; a.kmn = kmn; a.kst = kst; a.vq = vq; a.vmn = vmn; a.vst = vst;
+  a.tail_k = tail_k; a.tail_v = tail_v; a.pos_dev = pos_dev; a.first_dev = first_dev;
+  a.written_out = written_dev; a.qlen_out = qlen_dev; a.pg_out = pg_dev;
+  a.capacity = capacity; a.ngroups_cap = ngroups; a.tail_slots = GT;
+  a.hq = (int)hq; a.hkv = (int)hkv; a.gq = (int)(hq / hkv);
+  a.tail_mode = TAIL_FUSED;
+  a.sl2 = LOG2E / sqrtf((float)head_dim);
+  a.out = out; a.lse = lse_out; a.ws = static_cast<float*>(workspace);
+  a.n_parts = (int)n_parts;
+  a.inline_tail = 1;
+  a.tail_ctr_end = reinterpret_cast<int*>(ws + (workspace_bytes & ~int64_t(3)));
+  a.x = x; a.x_gamma = x_gamma; a.w_qkv = w_qkv; a.q_gamma = q_gamma; a.k_gamma = k_gamma; a.inv_freq = inv_freq;
+  a.eps_x = x_eps; a.eps_qk = qk_eps; a.hidden = (int)hidden;
+  a.hand = hand; a.qkv_epoch = epoch; a.qkv_out = qkv_out;
+  l2_args(a);
+  hipLaunchKernelGGL((attn_prefix_kernel<CONTIG_T64, true>), dim3((unsigned)grid), dim3(THREADS), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch(what);
 }
 
 extern "C" int nkv_tail_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v,

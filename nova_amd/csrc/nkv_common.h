@@ -122,6 +122,79 @@ __device__ __forceinline__ uint2 sym_quant8(const float (&v)[8], float& scale) {
   return uint2{c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24), c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24)};
 }
 
+// ---- the decode-step projections' arithmetic, shared by the GEMV kernels and the fused
+// projection + attention step, so that both compute the same bits
+
+// Wave sum (every lane gets it), in a fixed order.
+__device__ __forceinline__ float hsum64(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// acc + the dot product of 8 fp16 weights and 8 fp16 inputs (fp32 accumulation, pairwise).
+__device__ __forceinline__ float dot8(uint4 w, uint4 x, float acc) {
+  acc = __builtin_amdgcn_fdot2(as_h2(w.x), as_h2(x.x), acc, false);
+  acc = __builtin_amdgcn_fdot2(as_h2(w.y), as_h2(x.y), acc, false);
+  acc = __builtin_amdgcn_fdot2(as_h2(w.z), as_h2(x.z), acc, false);
+  acc = __builtin_amdgcn_fdot2(as_h2(w.w), as_h2(x.w), acc, false);
+  return acc;
+}
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// A weight load: 16 bytes, nontemporal (weights stream through once per decode step).
+__device__ __forceinline__ uint4 ld_weight(const uint16_t* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return uint4{v.x, v.y, v.z, v.w};
+}
+
+// The sum of squares of 8 fp16 inputs, added to ss in element order.
+__device__ __forceinline__ float sumsq8(uint4 x, float ss) {
+  const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const half2_t h = as_h2(u[e]);
+    ss += (float)h.x * (float)h.x;
+    ss += (float)h.y * (float)h.y;
+  }
+  return ss;
+}
+
+// 8 inputs normalized as torch's fp16 RMSNorm evaluates them: fp16(fp16(x * r) * gamma).
+__device__ __forceinline__ uint4 rms_scale8(uint4 x, uint4 g, float r) {
+  uint32_t u[4] = {x.x, x.y, x.z, x.w};
+  const uint32_t gu[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const half2_t h = as_h2(u[e]), gg = as_h2(gu[e]);
+    half2_t o;
+    o.x = (_Float16)((float)(_Float16)((float)h.x * r) * (float)gg.x);
+    o.y = (_Float16)((float)(_Float16)((float)h.y * r) * (float)gg.y);
+    u[e] = as_u32(o);
+  }
+  return uint4{u[0], u[1], u[2], u[3]};
+}
+
+// One head vector's q/k RMSNorm and rotary embedding in torch's fp16 order, for the lane that
+// holds elements l and l + 64 (a, b; the pair rotate_half mixes): the mean of squares over the
+// wave, x * cos + rotate_half(x) * sin with cos/sin of f = pos * inv_freq[l] rounded to fp16
+// and every product and sum rounded to fp16. Returns the two fp16 results (lo: element l).
+__device__ __forceinline__ void qk_norm_rope_lane(float a, float b, float ga, float gb, float eps, float f,
+                                                  uint16_t& lo16, uint16_t& hi16) {
+  // torch rounds each product to fp16 before the sum: no fusing into an fp16 fma here
+#pragma clang fp contract(off)
+  const float ss = hsum64(a * a + b * b);
+  const float r = rsqrtf(ss * (1.0f / 128.0f) + eps);
+  const float na = (float)(_Float16)((float)(_Float16)(a * r) * ga);
+  const float nb = (float)(_Float16)((float)(_Float16)(b * r) * gb);
+  const float c = (float)(_Float16)cosf(f), s = (float)(_Float16)sinf(f);
+  const float lo = (float)(_Float16)(na * c) + (float)(_Float16)(-nb * s);
+  const float hi = (float)(_Float16)(nb * c) + (float)(_Float16)(na * s);
+  lo16 = f2h(lo);
+  hi16 = f2h(hi);
+}
+
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace nkv

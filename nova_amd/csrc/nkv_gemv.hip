@@ -22,30 +22,8 @@ namespace {
 constexpr int GV_MAX_IN = 16384;  // input features (the LDS copy takes 2 bytes each)
 constexpr int GV_WAVES = 8;       // rows (waves) per workgroup
 
-__device__ __forceinline__ float hsum64(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-__device__ __forceinline__ float dot8(uint4 w, uint4 x, float acc) {
-  acc = __builtin_amdgcn_fdot2(as_h2(w.x), as_h2(x.x), acc, false);
-  acc = __builtin_amdgcn_fdot2(as_h2(w.y), as_h2(x.y), acc, false);
-  acc = __builtin_amdgcn_fdot2(as_h2(w.z), as_h2(x.z), acc, false);
-  acc = __builtin_amdgcn_fdot2(as_h2(w.w), as_h2(x.w), acc, false);
-  return acc;
-}
-
 __device__ __forceinline__ _Float16 as_half(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ uint16_t half_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
-
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-
-// A weight load: 16 bytes, nontemporal (weights stream through once per decode step).
-__device__ __forceinline__ uint4 ld_weight(const uint16_t* p) {
-  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
-  return uint4{v.x, v.y, v.z, v.w};
-}
 
 // The workgroup's share of the input vector: thread t holds 16-byte chunks t + 64 W k of x (and
 // of gamma when NORM), k < XC, so that XC 64 W >= 64 NL >= the input's chunk count.
@@ -73,15 +51,7 @@ struct InputChunks {
     if (NORM) {
       float ss = 0.0f;
 #pragma unroll
-      for (int k = 0; k < XC; ++k) {
-        const uint32_t u[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const half2_t h = as_h2(u[e]);
-          ss += (float)h.x * (float)h.x;
-          ss += (float)h.y * (float)h.y;
-        }
-      }
+      for (int k = 0; k < XC; ++k) ss = sumsq8(x[k], ss);
       ss = hsum64(ss);
       if (lane == 0) part[wave] = ss;
       __syncthreads();
@@ -94,20 +64,7 @@ struct InputChunks {
     for (int k = 0; k < XC; ++k) {
       const int c = tid + 64 * W * k;
       if (c < nch) {
-        uint4 v = x[k];
-        if (NORM) {
-          uint32_t u[4] = {v.x, v.y, v.z, v.w};
-          const uint32_t gu[4] = {g[k].x, g[k].y, g[k].z, g[k].w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const half2_t h = as_h2(u[e]), gg = as_h2(gu[e]);
-            half2_t o;
-            o.x = (_Float16)((float)(_Float16)((float)h.x * r) * (float)gg.x);
-            o.y = (_Float16)((float)(_Float16)((float)h.y * r) * (float)gg.y);
-            u[e] = as_u32(o);
-          }
-          v = uint4{u[0], u[1], u[2], u[3]};
-        }
+        const uint4 v = NORM ? rms_scale8(x[k], g[k], r) : x[k];
         *reinterpret_cast<uint4*>(xs + 8 * c) = v;
       }
     }
@@ -203,22 +160,14 @@ __global__ __launch_bounds__(64 * W) void swiglu_kernel(const uint16_t* x, const
 __global__ __launch_bounds__(64) void qk_norm_rope_kernel(uint16_t* qkv, int hq, const uint16_t* q_gamma,
                                                           const uint16_t* k_gamma, float eps, const float* inv_freq,
                                                           const int64_t* pos) {
-  // torch rounds each product to fp16 before the sum: no fusing into an fp16 fma here
-#pragma clang fp contract(off)
   const int head = blockIdx.x, l = threadIdx.x;
   uint16_t* p = qkv + (int64_t)head * 128;
   const uint16_t* g = head < hq ? q_gamma : k_gamma;
-  const float a = (float)as_half(p[l]), b = (float)as_half(p[l + 64]);
-  const float ss = hsum64(a * a + b * b);
-  const float r = rsqrtf(ss * (1.0f / 128.0f) + eps);
-  const float na = (float)(_Float16)((float)(_Float16)(a * r) * (float)as_half(g[l]));
-  const float nb = (float)(_Float16)((float)(_Float16)(b * r) * (float)as_half(g[l + 64]));
-  const float f = (float)*pos * inv_freq[l];
-  const float c = (float)(_Float16)cosf(f), s = (float)(_Float16)sinf(f);
-  const float lo = (float)(_Float16)(na * c) + (float)(_Float16)(-nb * s);
-  const float hi = (float)(_Float16)(nb * c) + (float)(_Float16)(na * s);
-  p[l] = half_bits((_Float16)lo);
-  p[l + 64] = half_bits((_Float16)hi);
+  uint16_t lo, hi;
+  qk_norm_rope_lane((float)as_half(p[l]), (float)as_half(p[l + 64]), (float)as_half(g[l]), (float)as_half(g[l + 64]),
+                    eps, (float)*pos * inv_freq[l], lo, hi);
+  p[l] = lo;
+  p[l + 64] = hi;
 }
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

@@ -712,15 +712,65 @@ class KVInt8Cache:
         _lib.call("nkv_decode_step_t64", *args)
         return self._output(out)
 
+    def update_attend_qkv(self, x: torch.Tensor, w_qkv: torch.Tensor, x_gamma: torch.Tensor, x_eps: float,
+                          q_gamma: torch.Tensor, k_gamma: torch.Tensor, qk_eps: float, inv_freq: torch.Tensor,
+                          layer_idx: int, out: torch.Tensor | None = None,
+                          qkv_out: torch.Tensor | None = None) -> torch.Tensor:
+        """One decode token of a decoder layer's attention block in one launch
+        (``nkv_decode_step_qkv_t64``): ``qkv = w_qkv @ rms_norm(x, x_gamma)`` (the stacked q, k, v
+        projection of ``LeanAttention``, src/nova/layers.py:99-137), the per-head q / k RMSNorm and
+        the rotary embedding at ``self.pos`` (``inv_freq``: fp32 ``[D / 2]``), then ``update`` +
+        ``attend`` of the token. The same bits as ``nkv_gemv`` + ``nkv_qk_norm_rope`` +
+        ``update_attend``. ``x``: fp16 ``[hidden]`` (hidden a multiple of 8, at most 3072);
+        ``w_qkv``: ``[(H_q + 2 H_kv) D, hidden]``; ``qkv_out`` (optional, fp16 ``[(H_q + 2 H_kv) D]``)
+        receives the normalized, rotated q and k and v."""
+        if self.prefilling:
+            raise RuntimeError("update_attend_qkv decodes one token; finish the prefill first")
+        hq, hkv, d = self.num_q_heads, self.num_kv_heads, self.head_dim
+        rows = (hq + 2 * hkv) * d
+        for name, t in (("x", x), ("x_gamma", x_gamma), ("w_qkv", w_qkv), ("q_gamma", q_gamma), ("k_gamma", k_gamma)):
+            if t.dtype != torch.float16 or not t.is_contiguous() or t.device != self.pos.device:
+                raise ValueError(f"{name} must be a contiguous fp16 tensor on {self.pos.device}")
+        hidden = x.numel()
+        if tuple(w_qkv.shape) != (rows, hidden) or x_gamma.numel() != hidden:
+            raise ValueError(f"w_qkv must be [{rows}, {hidden}] and x_gamma [{hidden}] for x of {hidden} elements")
+        if q_gamma.numel() != d or k_gamma.numel() != d:
+            raise ValueError(f"q_gamma and k_gamma must have {d} elements")
+        if inv_freq.dtype != torch.float32 or not inv_freq.is_contiguous() or inv_freq.numel() != d // 2:
+            raise ValueError(f"inv_freq must be a contiguous fp32 tensor of {d // 2} elements")
+        if qkv_out is not None and (qkv_out.dtype != torch.float16 or not qkv_out.is_contiguous()
+                                    or qkv_out.numel() != rows):
+            raise ValueError(f"qkv_out must be a contiguous fp16 tensor of {rows} elements")
+        lib = _lib.load()
+        need = int(lib.nkv_decode_step_qkv_workspace_bytes(hkv, hq, self.max_len, self._n_parts))
+        if need > self._ws_bytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("update_attend_qkv: call it once outside graph capture (its workspace grows)")
+            ws = torch.zeros(max(self.pa.numel(), _cdiv(need, 4)), dtype=torch.float32, device=self._ws.device)
+            self._ws, self._ws_bytes = ws, ws.numel() * 4
+            self.pa = ws[:self.pa.numel()].view(self.pa.shape)
+        o, i = self._output(out), layer_idx
+        _lib.call("nkv_decode_step_qkv_t64", x.data_ptr(), x_gamma.data_ptr(), float(x_eps), w_qkv.data_ptr(), hidden,
+                  q_gamma.data_ptr(), k_gamma.data_ptr(), float(qk_eps), inv_freq.data_ptr(), _lib.ptr(qkv_out),
+                  self.kq[i].data_ptr(), self.kmn[i].data_ptr(), self.kst[i].data_ptr(), self.vq[i].data_ptr(),
+                  self.vmn[i].data_ptr(), self.vst[i].data_ptr(), self.tail_k[i].data_ptr(), self.tail_v[i].data_ptr(),
+                  self.pos.data_ptr(), self.first.data_ptr(), self._written.data_ptr(), self._qlen.data_ptr(),
+                  self._pg.data_ptr(), hq, hkv, d, self.max_len, o.data_ptr(), self.lse.data_ptr(),
+                  self._ws.data_ptr(), self._ws_bytes, self._n_parts, _lib.stream_ptr(self.pos.device))
+        return o
+
     def set_parts(self, n_parts: int) -> None:
         """Prefix work units per KV head of the decode launches (before any capture); grows the
-        zero-filled workspace when needed."""
+        zero-filled workspace when needed, and zero-fills it (the fused projection step's tagged
+        words move with the partials' size)."""
         n_parts = int(n_parts)
         need = int(_lib.load().nkv_attn_workspace_bytes(self.num_kv_heads, self.num_q_heads, n_parts))
         if need > self._ws_bytes:
             ws = torch.zeros(max(self.pa.numel(), _cdiv(need, 4)), dtype=torch.float32, device=self._ws.device)
             self._ws, self._ws_bytes = ws, ws.numel() * 4
             self.pa = ws[:self.pa.numel()].view(self.pa.shape)
+        else:
+            self._ws.zero_()
         self._n_parts = n_parts
 
     # ---- memory accounting

@@ -12,11 +12,13 @@ Two ways to run a layer:
 
 - torch (default): projections, norms and lm_head are plain torch ops around the KV path;
 - ``use_decode_kernels()``: a one-token decode step (batch 1, int8 cache) runs each layer as
-  five launches of this package's HIP kernels around the fused int8 decode step — qkv GEMV
-  with the input RMSNorm, q/k head norms + RoPE, ``update_attend``, o_proj GEMV with the
-  residual add, gate/up GEMV with SwiGLU and the post-attention RMSNorm, down GEMV with the
-  residual add — and the final RMSNorm is fused into the lm_head GEMV. The same fp16 roundings
-  as the torch path, up to fp32 summation order.
+  four launches of this package's HIP kernels: the attention block in one
+  (``update_attend_qkv``: the input RMSNorm and qkv projection, the q/k head norms + RoPE, the
+  append and the attention of the token), o_proj GEMV with the residual add, gate/up GEMV with
+  SwiGLU and the post-attention RMSNorm, down GEMV with the residual add; the final RMSNorm is
+  fused into the lm_head GEMV. ``use_decode_kernels(fused_qkv=False)`` splits the attention
+  block into the qkv GEMV, the head norms + RoPE and ``update_attend`` (the same bits). The
+  same fp16 roundings as the torch path, up to fp32 summation order.
 """
 
 from __future__ import annotations
@@ -154,20 +156,29 @@ class SkeletonLayer(nn.Module):
             if self.mlp is not None:
                 self.w_gate_up = _stack_linears(self.mlp.gate_proj, self.mlp.up_proj)
 
-    def decode_kernels(self, h: torch.Tensor, cache, pos: torch.Tensor, inv_freq: torch.Tensor) -> torch.Tensor:
+    def decode_kernels(self, h: torch.Tensor, cache, pos: torch.Tensor, inv_freq: torch.Tensor,
+                       fused_qkv: bool = True) -> torch.Tensor:
         """One decode token (``h`` of ``hidden_size`` elements) through the layer on the HIP
-        kernels; returns the new residual stream (a new tensor)."""
+        kernels; returns the new residual stream (a new tensor). With ``fused_qkv`` (and a cache
+        that has it) the projection, head norms, RoPE and attention step are one launch
+        (``update_attend_qkv``), bit for bit the same as the separate launches."""
         from . import gemv as G
 
         cfg, a = self.attn.cfg, self.attn
         hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
         x = h.reshape(-1)
-        qkv = G.rms_gemv(x, self.w_qkv, self.norm, self.eps)
-        G.qk_norm_rope_(qkv, hq, hkv, a.q_norm, a.k_norm, cfg.rms_eps, inv_freq, pos)
-        q = qkv[:hq * d].view(1, hq, 1, d)
-        k = qkv[hq * d:(hq + hkv) * d].view(1, hkv, 1, d)
-        v = qkv[(hq + hkv) * d:].view(1, hkv, 1, d)
-        o = cache.update_attend(k, v, q, a.layer_idx)
+        if fused_qkv and hasattr(cache, "update_attend_qkv") and hq // hkv <= 4 and x.numel() % 8 == 0 \
+                and x.numel() <= 3072:
+            # the projection, the head norms + RoPE and the attention step in one launch
+            o = cache.update_attend_qkv(x, self.w_qkv, self.norm, self.eps, a.q_norm, a.k_norm, cfg.rms_eps,
+                                        inv_freq, a.layer_idx)
+        else:
+            qkv = G.rms_gemv(x, self.w_qkv, self.norm, self.eps)
+            G.qk_norm_rope_(qkv, hq, hkv, a.q_norm, a.k_norm, cfg.rms_eps, inv_freq, pos)
+            q = qkv[:hq * d].view(1, hq, 1, d)
+            k = qkv[hq * d:(hq + hkv) * d].view(1, hkv, 1, d)
+            v = qkv[(hq + hkv) * d:].view(1, hkv, 1, d)
+            o = cache.update_attend(k, v, q, a.layer_idx)
         h1 = G.rms_gemv(o.reshape(-1), a.o_proj.weight, residual=x)
         if self.mlp is not None:
             act = G.swiglu_gemv(h1, self.w_gate_up, self.post_norm, self.eps)
@@ -187,6 +198,7 @@ class SkeletonText(nn.Module):
         # kernel mode: one-token steps over an int8 cache run on the HIP kernels, and the final
         # RMSNorm moves into the lm_head (``forward`` then returns the pre-norm hidden states)
         self.decode_kernels = False
+        self.fused_qkv = True
 
     @property
     def num_cache_layers(self) -> int:
@@ -209,7 +221,7 @@ class SkeletonText(nn.Module):
                 h = self.embed_tokens(input_ids)
                 pos = position_ids.reshape(-1)[:1]
                 for layer in self.layers:
-                    h = layer.decode_kernels(h, past_key_values, pos, self.inv_freq32)
+                    h = layer.decode_kernels(h, past_key_values, pos, self.inv_freq32, self.fused_qkv)
                 return h
             return self._layers_torch(input_ids, position_ids, attention_mask, past_key_values)
         return _rms(self._layers_torch(input_ids, position_ids, attention_mask, past_key_values), self.norm,
@@ -247,8 +259,10 @@ class SkeletonForCausalLM(nn.Module):
                     p.copy_(r.mul_(p.shape[-1] ** -0.5))
                     del r
 
-    def use_decode_kernels(self, on: bool = True) -> "SkeletonForCausalLM":
-        """Run one-token decode steps on the HIP kernels (fp16 CUDA model, int8 cache)."""
+    def use_decode_kernels(self, on: bool = True, fused_qkv: bool = True) -> "SkeletonForCausalLM":
+        """Run one-token decode steps on the HIP kernels (fp16 CUDA model, int8 cache); with
+        ``fused_qkv`` each layer's projection, head norms, RoPE and attention step are one launch."""
+        self.model.fused_qkv = bool(fused_qkv)
         if on:
             w = self.lm_head.weight
             if not w.is_cuda or w.dtype != torch.float16:
