@@ -90,6 +90,8 @@ typedef __attribute__((address_space(3))) v2i_t lds_v2i_t;
 enum TailMode : int { TAIL_NONE = 0, TAIL_MASK = 1, TAIL_SCALARS = 2, TAIL_FUSED = 3 };
 // TAIL_FUSED with `tok`: the new token itself is the tail (its codes written by the prefix kernel).
 
+constexpr int FLAG_COPIES = 8;  // copies of the chained step's issue flags (one per polling KV head group)
+
 struct AttnArgs {
   const uint16_t* q;
   uint8_t* kq;
@@ -157,7 +159,7 @@ struct AttnArgs {
   // launch's tag (relaxed, agent scope) as soon as that head's output stores are issued; the
   // readers of layer l + 1 wait until all hq carry the tag. Null otherwise.
   uint32_t* issue_flags;
-  uint32_t* flags_base;  // layer 0's issue flags; layer l's at flags_base + l hq
+  uint32_t* flags_base;  // layer 0's issue flags; layer l's at flags_base + l FLAG_COPIES hq
   int n_layers;
   // the L2 hand-over: l2_xcc = the device's XCD count n when workgroups b and b + n share an XCD
   // and n divides hkv (the workgroups of a KV head then share one XCD), 0 when off
@@ -1889,8 +1891,11 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
           a.lse[qh] = failed ? __builtin_nanf("") : (lt > 0.0f ? (M + __log2f(lt) - P_SCALE_LOG2) * LN2 : NEG_INF);
         // this head's outputs are issued: count it for the readers of the next layer (they
         // validate the words themselves, so no ordering is needed)
-        if (a.issue_flags && lane == 0)
-          __hip_atomic_store(a.issue_flags + qh, a.ftag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a.issue_flags && lane == 0) {
+#pragma unroll
+          for (int c = 0; c < FLAG_COPIES; ++c)
+            __hip_atomic_store(a.issue_flags + c * a.hq + qh, a.ftag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       } else {
         *reinterpret_cast<float2*>(sm.pre_acc + head0 * D + 2 * lane) = acc;
         if (lane == 0) {
@@ -2021,7 +2026,9 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   }
   if (a.issue_flags) {  // every column issued: the workgroup's gq heads flagged at once
     __syncthreads();
-    if (tid < gq) __hip_atomic_store(a.issue_flags + qh0 + tid, a.ftag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < gq * FLAG_COPIES)
+      __hip_atomic_store(a.issue_flags + (tid / gq) * a.hq + qh0 + tid % gq, a.ftag, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
   }
   // ---- every word of the head's partials was consumed before the barrier above: the whole
   // block [hws, hws + P pw) goes back to zero (plain 16-byte stores by every thread; pw is a
@@ -2586,7 +2593,11 @@ constexpr int IN_WAVE = WAVES - 1;                 // a streaming workgroup's in
 __device__ __forceinline__ int* layer_done(const AttnArgs& a, int l) { return a.tail_ctr_end - 1 - l; }
 // issued[l] (dep_all) below them: at end[-4 - n_layers - l]
 // issue flags of layer l (dep_all): hq words after the tagged outputs of every layer
-__device__ __forceinline__ uint32_t* layer_flags(const AttnArgs& a, int l) { return a.flags_base + (int64_t)l * a.hq; }
+// (every flag is stored in FLAG_COPIES copies, [layer][copy][hq], and KV head h's readers poll copy
+// h mod FLAG_COPIES: each 128-byte line of flags is polled by one head's workgroups, not by all)
+__device__ __forceinline__ uint32_t* layer_flags(const AttnArgs& a, int l) {
+  return a.flags_base + (int64_t)l * FLAG_COPIES * a.hq;
+}
 
 // Layer l's arguments: the cache and step pointers of its table entry (nkv_layer_t64, or
 // nkv_layer_tok for the per-token symmetric format), and its own partial block.
@@ -2752,7 +2763,7 @@ __device__ __forceinline__ bool merger_layer(const AttnArgs& args, const void* l
       const uint64_t* src = la.fwd_out - (int64_t)la.hq * D / 2;  // layer l - 1's tagged words
       ok = fwd_fetch(src + (int64_t)h * gq * D / 2, src + ((la.k_new - prev) + (int64_t)h * la.kv_hs) / 2,
                      src + ((la.v_new - prev) + (int64_t)h * la.kv_hs) / 2, gq, la.ftag, sm.fwd, lost,
-                     la.dep_all ? layer_flags(la, l - 1) : nullptr, la.hq);
+                     la.dep_all ? layer_flags(la, l - 1) + (h % FLAG_COPIES) * la.hq : nullptr, la.hq);
     } else if (l > 0) {
       ok = wait_layer(la, l - 1, la.hkv, lost);
     }
@@ -2861,7 +2872,8 @@ __global__ __launch_bounds__(THREADS, 1) void attn_layers_kernel(AttnArgs a, con
         // q is layer l - 1's output: its tagged words (head h's rows, written by head h's merger),
         // and with dep_all layer l - 1's counter as well
         ok = fwd_fetch(la.fwd_out - (int64_t)la.hq * D / 2 + (int64_t)h * gq * D / 2, nullptr, nullptr, gq, la.ftag,
-                       reinterpret_cast<uint32_t*>(q_lds), lost, a.dep_all ? layer_flags(a, l - 1) : nullptr, a.hq);
+                       reinterpret_cast<uint32_t*>(q_lds), lost,
+                       a.dep_all ? layer_flags(a, l - 1) + (h % FLAG_COPIES) * a.hq : nullptr, a.hq);
       } else {
         ok = l == 0 || wait_layer(a, l - 1, a.hkv, lost);
         issue_q(la.q + (int64_t)h * gq * D, gq, __builtin_amdgcn_readfirstlane(lds_addr(q_lds)));
@@ -4269,7 +4281,7 @@ int64_t layers_sync_bytes(int64_t n_layers) { return ctr_bytes(n_layers + 3); }
 // each layer's output as tagged words (forwarded to the next layer's inputs)
 // (and, after them, each layer's issue flags: one word per query head)
 int64_t layers_fwd_bytes(int64_t hq, int64_t n_layers) {
-  return n_layers * hq * D / 2 * (int64_t)sizeof(uint64_t) + n_layers * hq * (int64_t)sizeof(uint32_t);
+  return n_layers * hq * D / 2 * (int64_t)sizeof(uint64_t) + n_layers * FLAG_COPIES * hq * (int64_t)sizeof(uint32_t);
 }
 
 // Streaming parts per KV head: one workgroup per 8 groups at most, and hkv (parts + 1) workgroups
