@@ -64,12 +64,12 @@ TRAFFIC = {
     "chain_t64": (PROFILES / "decode_chain_32k_traffic.txt", "attn_layers_kernel<0>", _DEC + " --mode chain"),
     "chain_tok": (PROFILES / "decode_chain_tok_32k_traffic.txt", "attn_layers_kernel<1>",
                   _DEC + " --mode chain --scheme tok"),
-    "layers_t64": (PROFILES / "decode_step_32k_traffic.txt", "attn_prefix_kernel<0>", _DEC + " --mode layers"),
-    "layers_tok": (PROFILES / "decode_step_tok_32k_traffic.txt", "attn_prefix_kernel<1>",
+    "layers_t64": (PROFILES / "decode_step_32k_traffic.txt", "attn_prefix_kernel<0, false>", _DEC + " --mode layers"),
+    "layers_tok": (PROFILES / "decode_step_tok_32k_traffic.txt", "attn_prefix_kernel<1, false>",
                    _DEC + " --mode layers --scheme tok"),
-    "paged_t64": (PROFILES / "paged_batch_decode_traffic.txt", "attn_prefix_kernel<2>",
+    "paged_t64": (PROFILES / "paged_batch_decode_traffic.txt", "attn_prefix_kernel<2, false>",
                   "python3 bench.py --workload paged --steps 4 --warmup 1 --no-clock"),
-    "paged_tok": (PROFILES / "paged_batch_decode_tok_traffic.txt", "attn_prefix_kernel<3>",
+    "paged_tok": (PROFILES / "paged_batch_decode_tok_traffic.txt", "attn_prefix_kernel<3, false>",
                   "python3 bench.py --workload paged --scheme tok --steps 4 --warmup 1 --no-clock"),
     "prefill": (PROFILES / "prefill_chunk_512_over_16k_traffic.txt", "prefill_chunk_kernel",
                 "python3 bench.py --workload prefill --steps 4 --warmup 1 --no-clock"),
