@@ -9,7 +9,8 @@ attention output (q = the whole output, k = q heads 0, 4, .., v = q heads 1, 5, 
 the previous step's last output), and with the default ``--dep all`` no input of layer l is read
 before every KV head of layer l-1 has finished (the all-head dependency of a model, where every
 q head of layer l depends on every head of layer l-1 through o_proj). The step is captured once
-as a hipGraph; W untimed replays, then K timed replays bracketed by ``torch.cuda.synchronize()``
+as a hipGraph; SETTLE_STEPS + W untimed replays (the first SETTLE_STEPS let the clocks reach their
+steady state), then K timed replays bracketed by ``torch.cuda.synchronize()``
 and HIP events on the replay stream; afterwards the launch's error word is checked.
 
 One JSON line (the driver's contract). ``value`` = decode tokens/s of the whole job.
@@ -75,6 +76,10 @@ TRAFFIC = {
                 "python3 bench.py --workload prefill --steps 4 --warmup 1 --no-clock"),
 }
 VOCAB_QWEN3_4B = 151936
+# Untimed step replays before the W warmup steps of a decode measurement: after the prefill and the
+# graph capture the GPU's clocks ramp up over the first few dozen steps (with 5 warmup steps the
+# timed 20 ran 9% slower than with 60), so the timed steps are taken at the steady state.
+SETTLE_STEPS = 128
 
 
 def attn_bytes(u: int) -> int:
@@ -385,11 +390,12 @@ def clock_under_load(replay) -> dict:
 # ---------------------------------------------------------------- the decode workloads
 
 
-def _time_graph(graph, stream, reps: int, warmup: int) -> float:
-    """ms per replay of ``graph`` over ``reps`` replays, HIP events on ``stream``."""
+def _time_graph(graph, stream, reps: int, warmup: int, settle: int = 0) -> float:
+    """ms per replay of ``graph`` over ``reps`` replays after ``settle + warmup`` untimed ones, HIP
+    events on ``stream``."""
     import torch
 
-    for _ in range(warmup):
+    for _ in range(settle + warmup):
         graph.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -445,7 +451,7 @@ def run_decode(args, scheme: str, headline: bool, mode: str = "chain", dep: str 
 
     dev = torch.device("cuda:0")
     L, ctx, W, K = args.layers, args.ctx, args.warmup, args.steps
-    max_len = -(-(ctx + 3 * (W + K) + 8) // 64) * 64
+    max_len = -(-(ctx + 3 * (W + K) + SETTLE_STEPS + 8) // 64) * 64
     cls = KVInt8TokCache if scheme == "tok" else KVInt8Cache
     cache = cls(num_slots=L, num_kv_heads=HKV, head_dim=D, max_len=max_len, num_q_heads=HQ, device=dev)
     if args.parts:
@@ -496,7 +502,7 @@ def run_decode(args, scheme: str, headline: bool, mode: str = "chain", dep: str 
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         step()
-    for _ in range(W):
+    for _ in range(SETTLE_STEPS + W):  # the clocks settle, then the W warmup steps
         graph.replay()
     torch.cuda.synchronize()
     pos0 = int(cache.pos.item())
@@ -519,7 +525,7 @@ def run_decode(args, scheme: str, headline: bool, mode: str = "chain", dep: str 
     with torch.cuda.graph(g_launch):
         launches()
     pos_l = int(cache.pos.item())
-    ms_launches = _time_graph(g_launch, stream, K, W)
+    ms_launches = _time_graph(g_launch, stream, K, W, SETTLE_STEPS)  # (pos fixed: settling moves nothing)
     if chain is not None:
         chain.check()
     clock = None if args.no_clock else clock_under_load(graph.replay)
@@ -546,7 +552,7 @@ def run_decode(args, scheme: str, headline: bool, mode: str = "chain", dep: str 
         "metric": "int8-KV decode attention tokens/s + achieved HBM GB/s (% of peak) at 32k ctx",
         "value": round(K / (ms / 1e3), 2), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp16", "data": "synthetic",
+        "dtype": "fp16", "data": "synthetic", "settle_steps": SETTLE_STEPS,
         "config": {"workload": f"{'per-token symmetric int8' if scheme == 'tok' else 'int8t64'} KV decode step, "
                                f"{L} layers x (32 q / 8 kv heads, head_dim 128), batch 1, {ctx}-token prefilled "
                                f"cache, layers chained through their outputs, {K} hipGraph-replayed steps, {how}",
@@ -621,7 +627,7 @@ def run_paged(args, steps: int | None = None, scheme: str = "t64") -> dict:
     with torch.cuda.graph(g_launch):
         for layer in range(L):
             cache.decode_step(ks[layer], vs[layer], qs[layer], layer)
-    per_launch_s = _time_graph(g_launch, stream, K, W) / 1e3 / L
+    per_launch_s = _time_graph(g_launch, stream, K, W, SETTLE_STEPS) / 1e3 / L
     pos = [n + W + K for n in lens]
     launch_bytes = sum(step_launch_bytes(p + 1, scheme) for p in pos)
     _calibration_copy(dev)

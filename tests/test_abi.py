@@ -159,8 +159,9 @@ def test_chained_step_sizes_and_checks(lib):
     per_part = 8 * (4 * 128 + 8) * 4  # one partial of 4 query heads, per KV head
     # n layer counters, the exit ticket, the error word and the launch counter
     sync = lambda n: -(-((n + 3) * 4) // 256) * 256  # noqa: E731
-    # one layer's output as tagged words (two fp16 values per 8 bytes), then its 32 issue flags
-    fwd = 32 * 128 // 2 * 8 + 32 * 4
+    # one layer's output as tagged words (two fp16 values per 8 bytes), then its 32 issue flags in
+    # 8 copies (one per group of polling workgroups)
+    fwd = 32 * 128 // 2 * 8 + 8 * 32 * 4
     assert lib.nkv_layers_workspace_bytes(8, 32, 31, 36) == 36 * (31 * per_part + fwd) + sync(36)
     assert lib.nkv_layers_workspace_bytes(8, 32, 1, 1) == per_part + fwd + 256
     assert lib.nkv_layers_workspace_bytes(8, 30, 31, 36) == 0 and lib.nkv_layers_workspace_bytes(8, 32, 0, 4) == 0
