@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 9
+#define NKV_ABI_VERSION 10
 
 #define NKV_OK 0
 #define NKV_ERR_INVALID 1     /* argument outside what the reference accepts */
@@ -208,6 +208,15 @@ int nkv_decode_step_combine_t64(const uint16_t* q, const uint16_t* k_new, const 
  * (tagged words, through the XCD's L2 when the hand-over is on, nkv_l2_handover), so every
  * workgroup of a KV head waits for the others: the grid (hkv * max(n_parts, 32) workgroups)
  * must fit the device at once, or the call returns NKV_ERR_UNSUPPORTED.
+ * With w_o (not NULL) the launch also runs the block's output projection and residual add
+ * (`o_proj` and the residual of LeanDecoderLayer, src/nova/layers.py:137,207):
+ * h1_out[hidden] = x + w_o out, w_o [hidden][hq * 128] fp16, bit for bit what
+ * nkv_gemv(out, NULL, 0, w_o, hidden, hq * 128, x, h1) computes after the step; hq <= 32,
+ * hidden at most two rows per wave of the workgroups beyond the first of each KV head
+ * (2 * 8 * (grid - hkv)). The merging workgroups publish out as tagged words; the others,
+ * done with their part of the cache, stream w_o meanwhile and wait for them. h1_out may be x
+ * itself (the residual stream updated in place) but must not overlap out. NULL w_o: no
+ * projection, h1_out unused.
  * workspace: nkv_decode_step_qkv_workspace_bytes(hkv, hq, capacity, n_parts) bytes,
  * zero-filled before its first use; it may also serve nkv_decode_step_t64 with the same
  * n_parts (the same partials and counters, which both leave at zero; the row words and
@@ -222,7 +231,8 @@ int nkv_decode_step_qkv_t64(const uint16_t* x, const uint16_t* x_gamma, float x_
                             uint16_t* tail_v, const int64_t* pos_dev, const int64_t* first_dev,
                             int64_t* written_dev, int64_t* qlen_dev, int64_t* pg_dev, int64_t hq,
                             int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out, float* lse_out,
-                            void* workspace, int64_t workspace_bytes, int64_t n_parts, void* stream);
+                            const uint16_t* w_o, uint16_t* h1_out, void* workspace, int64_t workspace_bytes,
+                            int64_t n_parts, void* stream);
 
 /* Limits of nkv_decode_step_static_t64's scratch: partial results, and the publication
  * area (completion counters and flags). */

@@ -96,16 +96,16 @@ SIGNATURES = {
     "nkv_l2_handover": (c_int, [c_int, P, P]),
     "nkv_decode_step_qkv_workspace_bytes": (I64, [I64, I64, I64, I64]),
     # x, x_gamma, x_eps, w_qkv, hidden, q_gamma, k_gamma, qk_eps, inv_freq, qkv_out, kq, kmn, kst, vq, vmn,
-    # vst, tail_k, tail_v, pos, first, written, qlen, pg, hq, hkv, head_dim, capacity, out, lse,
-    # workspace, workspace_bytes, n_parts, stream
+    # vst, tail_k, tail_v, pos, first, written, qlen, pg, hq, hkv, head_dim, capacity, out, lse, w_o,
+    # h1_out, workspace, workspace_bytes, n_parts, stream
     "nkv_decode_step_qkv_t64": (c_int, [P, P, c_float, P, I64, P, P, c_float, P, P, P, P, P, P, P, P, P, P, P, P, P,
-                                        P, P, I64, I64, I64, I64, P, P, P, I64, I64, P]),
+                                        P, P, I64, I64, I64, I64, P, P, P, P, P, I64, I64, P]),
     "nkv_gemv": (c_int, [P, P, c_float, P, I64, I64, P, P, P]),
     "nkv_swiglu_gemv": (c_int, [P, P, c_float, P, I64, I64, P, P]),
     "nkv_qk_norm_rope": (c_int, [P, I64, I64, I64, P, P, c_float, P, P, P]),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _lib = None
 _lock = threading.Lock()

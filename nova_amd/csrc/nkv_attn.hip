@@ -180,6 +180,12 @@ struct AttnArgs {
   uint64_t* hand;
   int* qkv_epoch;
   uint16_t* qkv_out;
+  // the fused projection step with the output projection: w_o [hidden][hq D] and h1 = x + w_o out
+  // [hidden] (the merging workgroups publish out as tagged words through fwd_out, stored at agent
+  // scope (fwd_agent) since every workgroup reads every head's words, with issue_flags)
+  const uint16_t* w_o;
+  uint16_t* h1_out;
+  int fwd_agent;
 };
 
 // XOR key of the 16-byte chunk positions of LDS row `row` (a token within its group).
@@ -1886,7 +1892,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
         const uint32_t pair = (uint32_t)f2h(ox) | ((uint32_t)f2h(oy) << 16);
         *reinterpret_cast<uint32_t*>(a.out + qh * D + 2 * lane) = pair;
         if (a.fwd_out)
-          hand_st(a.fwd_out + qh * D / 2 + lane, ((uint64_t)a.ftag << 32) | pair, l2_local(a));
+          hand_st(a.fwd_out + qh * D / 2 + lane, ((uint64_t)a.ftag << 32) | pair, l2_local(a) && !a.fwd_agent);
         if (a.lse && lane == 0)
           a.lse[qh] = failed ? __builtin_nanf("") : (lt > 0.0f ? (M + __log2f(lt) - P_SCALE_LOG2) * LN2 : NEG_INF);
         // this head's outputs are issued: count it for the readers of the next layer (they
@@ -2020,7 +2026,8 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     if (a.fwd_out) {  // (columns come in pairs of neighbouring lanes: d even in the even lane)
       const uint32_t pair = (uint32_t)__shfl_xor((int)o16, 1, 64);
       if ((d & 1) == 0)
-        hand_st(a.fwd_out + ((int64_t)qh * D + d) / 2, ((uint64_t)a.ftag << 32) | o16 | (pair << 16), l2_local(a));
+        hand_st(a.fwd_out + ((int64_t)qh * D + d) / 2, ((uint64_t)a.ftag << 32) | o16 | (pair << 16),
+                l2_local(a) && !a.fwd_agent);
     }
     if (a.lse && d == 0) a.lse[qh] = failed ? __builtin_nanf("") : (l > 0.0f ? (M + __log2f(l) - P_SCALE_LOG2) * LN2 : NEG_INF);
   }
@@ -2272,6 +2279,91 @@ __device__ bool qkv_prologue(const AttnArgs& a, int h, int part, int parts, int6
   return ok;
 }
 
+// ---- the output projection in the attention block's launch (w_o): h1 = x + W_o out, where out
+// is every head's attention output of this launch. The mergers (part 0 of each head) finish
+// last; the other workgroups, done with their partials, stream W_o meanwhile: reader wave g of the
+// R WAVES (R = the workgroups of parts 1..) takes rows g and g + R WAVES. A row is computed as
+// nkv_gemv computes it (lane l holds 16-byte chunks l + 64 u, fp32 dot products in chunk order,
+// the wave sum in hsum64's order, the fp16 result, then the residual added in fp16), so h1 is
+// bit for bit that launch's. out arrives as the mergers' tagged words (agent scope): each wave
+// polls the hq issue flags of its copy, then every thread fetches its words (reloading those
+// still stale) into LDS. A wait that gives up leaves NaN in the row.
+constexpr int OP_NL = 8;  // 16-byte chunks per lane of a W_o row: hq D <= 4096
+
+__device__ __forceinline__ void oproj_rows(const AttnArgs& a, int h, int part, uint32_t tag, uint8_t* lds_raw) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nw = ((int)gridDim.x - a.hkv) * WAVES;
+  const int g = ((part - 1) * a.hkv + h) * WAVES + wave;
+  const int nch = a.hq * D / 8;
+  const int r0 = g, r1 = g + nw;
+  const bool v0 = r0 < a.hidden, v1 = r1 < a.hidden;
+  // (the barrier waits for the partial's stores: W_o then goes out ~2 us after the partial,
+  // when fewer parts still stream; issued before it, the step measured 0.6% slower)
+  __syncthreads();  // every wave is past the partial's merge: the stages are free for out
+  uint4 w0[OP_NL], w1[OP_NL];
+#pragma unroll
+  for (int u = 0; u < OP_NL; ++u) {
+    const int c = lane + 64 * u;
+    w0[u] = v0 && c < nch ? ld_weight(a.w_o + (int64_t)r0 * nch * 8 + 8 * c) : uint4{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int u = 0; u < OP_NL; ++u) {
+    const int c = lane + 64 * u;
+    w1[u] = v1 && c < nch ? ld_weight(a.w_o + (int64_t)r1 * nch * 8 + 8 * c) : uint4{0, 0, 0, 0};
+  }
+  const uint16_t x0 = v0 ? a.x[r0] : (uint16_t)0, x1 = v1 ? a.x[r1] : (uint16_t)0;
+  // every head's output issued: the hq flags of copy h mod FLAG_COPIES (hq <= 64, one per lane)
+  const uint32_t* flags = a.issue_flags + (h % FLAG_COPIES) * a.hq;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  bool ok = true;
+  uint32_t f = lane < a.hq ? 0u : tag;
+  for (;;) {
+    if (f != tag) f = __hip_atomic_load(flags + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!__builtin_amdgcn_ballot_w64(f != tag)) break;
+    if (__builtin_amdgcn_s_memrealtime() - t0 > LAYER_WAIT_TICKS) {
+      ok = false;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  // the words (hq D / 2 of them): thread t takes t + THREADS j
+  uint32_t* o32 = reinterpret_cast<uint32_t*>(lds_raw);
+  const int nwords = nch * 4;
+  for (int e = tid; e < nwords; e += THREADS) {
+    uint64_t w = __hip_atomic_load(a.fwd_out + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    while (ok && (uint32_t)(w >> 32) != tag) {  // (a flag seen before its head's words)
+      if (__builtin_amdgcn_s_memrealtime() - t0 > LAYER_WAIT_TICKS) {
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      w = __hip_atomic_load(a.fwd_out + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    o32[e] = (uint32_t)(w >> 32) == tag ? (uint32_t)w : 0x7E007E00u;
+  }
+  __syncthreads();
+  const uint4* o4 = reinterpret_cast<const uint4*>(lds_raw);
+  float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+  for (int u = 0; u < OP_NL; ++u) {
+    const int c = lane + 64 * u;
+    if (c < nch) {
+      const uint4 xv = o4[c];
+      acc0 = dot8(w0[u], xv, acc0);
+      acc1 = dot8(w1[u], xv, acc1);
+    }
+  }
+  acc0 = hsum64(acc0);
+  acc1 = hsum64(acc1);
+  if (lane == 0) {  // the projection's fp16 result, then the residual added in fp16
+    if (v0)
+      a.h1_out[r0] = f2h((float)(_Float16)((float)(_Float16)acc0 + (float)__builtin_bit_cast(_Float16, x0)));
+    if (v1)
+      a.h1_out[r1] = f2h((float)(_Float16)((float)(_Float16)acc1 + (float)__builtin_bit_cast(_Float16, x1)));
+  }
+}
+
 template <int LAYOUT, bool QKV = false>
 __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   constexpr bool TOK = LAYOUT == CONTIG_TOK || LAYOUT == PAGED_TOK;
@@ -2338,6 +2430,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
     if (tid == 0) issued = 0;
     __syncthreads();
     qkv_tag = (uint32_t)__hip_atomic_load(a.qkv_epoch + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    a.ftag = qkv_tag;  // (the merger's tagged output words, when w_o)
     if (wave >= QKV_WAVES) {
       // after every computing wave's first weight loads (bounded: 2^16 short sleeps)
       for (int n = 0; n < (1 << 16); ++n) {
@@ -2489,6 +2582,13 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
       }
     }
   }  // prefix
+
+  if constexpr (QKV) {
+    if (a.w_o && part >= 1) {  // the output projection's rows, while the mergers finish
+      oproj_rows(a, h, part, qkv_tag, lds_raw);
+      return;
+    }
+  }
 
   // ---- fused tail. The contiguous layouts: part 0 of each head merges, polling the other
   // partials' words (the other workgroups never wait, and the hkv merging workgroups leave the
@@ -3564,16 +3664,23 @@ static int launch_attn(AttnArgs& a, int64_t n_parts, int64_t workspace_bytes, hi
 
 static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Whether the byte ranges [a, a + an) and [b, b + bn) share a byte.
+static bool overlaps(const void* a, int64_t an, const void* b, int64_t bn) {
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return pa < pb + (uintptr_t)bn && pb < pa + (uintptr_t)an;
+}
+
 // The fused projection step's workspace: the decode step's partials (n_parts per KV head), the
 // tagged row words [hkv][QKV_HAND_ROWS], the tags' epochs [hkv] (256-byte padded), the new token's
-// k / v [hkv][2][D] fp16, and the step's counters at the end.
+// k / v [hkv][2][D] fp16, the output's tagged words [hq D / 2] and issue flags [FLAG_COPIES][hq]
+// (with w_o), and the step's counters at the end.
 static int64_t up256(int64_t n) { return (n + 255) / 256 * 256; }
 static int64_t qkv_part_bytes(int64_t hkv, int64_t hq, int64_t n_parts) {
   return up256(hkv * std::max<int64_t>(1, n_parts) * part_floats(hq, hkv) * (int64_t)sizeof(float));
 }
 static int64_t qkv_workspace_bytes(int64_t hkv, int64_t hq, int64_t n_parts) {
   return qkv_part_bytes(hkv, hq, n_parts) + hkv * QKV_HAND_ROWS * 8 + up256(hkv * 4) + up256(hkv * 2 * D * 2) +
-         sync_bytes(hkv, n_parts);
+         up256(hq * D / 2 * 8) + up256(FLAG_COPIES * hq * 4) + sync_bytes(hkv, n_parts);
 }
 
 // Workgroups of the fused projection step resident at once on the current device (every
@@ -3860,7 +3967,8 @@ extern "C" int nkv_decode_step_qkv_t64(const uint16_t* x, const uint16_t* x_gamm
                                        uint16_t* tail_v, const int64_t* pos_dev, const int64_t* first_dev,
                                        int64_t* written_dev, int64_t* qlen_dev, int64_t* pg_dev, int64_t hq,
                                        int64_t hkv, int64_t head_dim, int64_t capacity, uint16_t* out, float* lse_out,
-                                       void* workspace, int64_t workspace_bytes, int64_t n_parts, void* stream) {
+                                       const uint16_t* w_o, uint16_t* h1_out, void* workspace, int64_t workspace_bytes,
+                                       int64_t n_parts, void* stream) {
   const char* what = "decode_step_qkv_t64";
   set_error("");
   if (int rc = check_heads(hq, hkv, head_dim)) return rc;
@@ -3891,10 +3999,26 @@ extern "C" int nkv_decode_step_qkv_t64(const uint16_t* x, const uint16_t* x_gamm
   const int64_t need = qkv_workspace_bytes(hkv, hq, n_parts);
   if (workspace_bytes < need)
     return fail(NKV_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", what, (long long)workspace_bytes, (long long)need);
+  if (w_o) {
+    const int64_t readers = grid - hkv;
+    if (!h1_out) return fail(NKV_ERR_INVALID, "%s: w_o without h1_out", what);
+    if (!al16(w_o)) return fail(NKV_ERR_UNSUPPORTED, "%s: w_o must be 16-byte aligned", what);
+    if (hq * D > OP_NL * 64 * 8 || hq > 64)
+      return fail(NKV_ERR_UNSUPPORTED, "%s: the output projection takes at most %d query heads", what, OP_NL * 64 * 8 / D);
+    if (hidden > 2 * readers * WAVES)
+      return fail(NKV_ERR_UNSUPPORTED, "%s: hidden size %lld exceeds two rows per reader wave (%lld)", what,
+                  (long long)hidden, (long long)(2 * readers * WAVES));
+    // h1 is written after every workgroup has read x: it may be x itself, or apart from it and from out
+    if (h1_out != x && overlaps(h1_out, hidden * 2, x, hidden * 2))
+      return fail(NKV_ERR_INVALID, "%s: h1_out must be x itself or not overlap it", what);
+    if (overlaps(h1_out, hidden * 2, out, hq * D * 2)) return fail(NKV_ERR_INVALID, "%s: h1_out overlaps out", what);
+  }
   char* ws = static_cast<char*>(workspace);
   uint64_t* hand = reinterpret_cast<uint64_t*>(ws + qkv_part_bytes(hkv, hq, n_parts));
   int* epoch = reinterpret_cast<int*>(hand + hkv * QKV_HAND_ROWS);
   uint16_t* kvbuf = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(epoch) + up256(hkv * 4));
+  uint64_t* owords = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(kvbuf) + up256(hkv * 2 * D * 2));
+  uint32_t* oflags = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(owords) + up256(hq * D / 2 * 8));
   AttnArgs a{};
   a.k_new = kvbuf; a.v_new = kvbuf + D; a.kv_hs = 2 * D;
   a.kq = kq; a.kmn = kmn; a.kst = kst; a.vq = vq; a.vmn = vmn; a.vst = vst;
@@ -3911,6 +4035,9 @@ extern "C" int nkv_decode_step_qkv_t64(const uint16_t* x, const uint16_t* x_gamm
   a.x = x; a.x_gamma = x_gamma; a.w_qkv = w_qkv; a.q_gamma = q_gamma; a.k_gamma = k_gamma; a.inv_freq = inv_freq;
   a.eps_x = x_eps; a.eps_qk = qk_eps; a.hidden = (int)hidden;
   a.hand = hand; a.qkv_epoch = epoch; a.qkv_out = qkv_out;
+  if (w_o) {
+    a.w_o = w_o; a.h1_out = h1_out; a.fwd_out = owords; a.issue_flags = oflags; a.fwd_agent = 1;
+  }
   l2_args(a);
   hipLaunchKernelGGL((attn_prefix_kernel<CONTIG_T64, true>), dim3((unsigned)grid), dim3(THREADS), 0,
                      static_cast<hipStream_t>(stream), a);

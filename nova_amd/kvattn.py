@@ -712,6 +712,28 @@ class KVInt8Cache:
         _lib.call("nkv_decode_step_t64", *args)
         return self._output(out)
 
+    def update_attend_block(self, x: torch.Tensor, w_qkv: torch.Tensor, x_gamma: torch.Tensor, x_eps: float,
+                            q_gamma: torch.Tensor, k_gamma: torch.Tensor, qk_eps: float, inv_freq: torch.Tensor,
+                            w_o: torch.Tensor, layer_idx: int, out: torch.Tensor | None = None,
+                            h1_out: torch.Tensor | None = None, qkv_out: torch.Tensor | None = None) -> torch.Tensor:
+        """``update_attend_qkv`` plus the block's output projection and residual add in the same
+        launch: returns ``h1 = x + w_o @ o`` (fp16 ``[hidden]``, into ``h1_out`` when given, which
+        may be ``x`` itself), ``o`` being the attention output (also written to ``out``). ``w_o``:
+        ``[hidden, H_q D]`` fp16. The same bits as ``update_attend_qkv`` followed by
+        ``gemv.rms_gemv(o, w_o, residual=x)``."""
+        hidden = x.numel()
+        if w_o.dtype != torch.float16 or not w_o.is_contiguous() or w_o.device != self.pos.device \
+                or tuple(w_o.shape) != (hidden, self.num_q_heads * self.head_dim):
+            raise ValueError(f"w_o must be a contiguous fp16 [{hidden}, {self.num_q_heads * self.head_dim}] tensor "
+                             f"on {self.pos.device}")
+        if h1_out is None:
+            h1_out = torch.empty_like(x)
+        if h1_out.dtype != torch.float16 or not h1_out.is_contiguous() or h1_out.numel() != hidden:
+            raise ValueError(f"h1_out must be a contiguous fp16 tensor of {hidden} elements")
+        self._qkv_step(x, w_qkv, x_gamma, x_eps, q_gamma, k_gamma, qk_eps, inv_freq, layer_idx, out, qkv_out, w_o,
+                       h1_out)
+        return h1_out
+
     def update_attend_qkv(self, x: torch.Tensor, w_qkv: torch.Tensor, x_gamma: torch.Tensor, x_eps: float,
                           q_gamma: torch.Tensor, k_gamma: torch.Tensor, qk_eps: float, inv_freq: torch.Tensor,
                           layer_idx: int, out: torch.Tensor | None = None,
@@ -724,6 +746,11 @@ class KVInt8Cache:
         ``update_attend``. ``x``: fp16 ``[hidden]`` (hidden a multiple of 8, at most 3072);
         ``w_qkv``: ``[(H_q + 2 H_kv) D, hidden]``; ``qkv_out`` (optional, fp16 ``[(H_q + 2 H_kv) D]``)
         receives the normalized, rotated q and k and v."""
+        return self._qkv_step(x, w_qkv, x_gamma, x_eps, q_gamma, k_gamma, qk_eps, inv_freq, layer_idx, out, qkv_out,
+                              None, None)
+
+    def _qkv_step(self, x, w_qkv, x_gamma, x_eps, q_gamma, k_gamma, qk_eps, inv_freq, layer_idx, out, qkv_out, w_o,
+                  h1_out) -> torch.Tensor:
         if self.prefilling:
             raise RuntimeError("update_attend_qkv decodes one token; finish the prefill first")
         hq, hkv, d = self.num_q_heads, self.num_kv_heads, self.head_dim
@@ -755,8 +782,8 @@ class KVInt8Cache:
                   self.kq[i].data_ptr(), self.kmn[i].data_ptr(), self.kst[i].data_ptr(), self.vq[i].data_ptr(),
                   self.vmn[i].data_ptr(), self.vst[i].data_ptr(), self.tail_k[i].data_ptr(), self.tail_v[i].data_ptr(),
                   self.pos.data_ptr(), self.first.data_ptr(), self._written.data_ptr(), self._qlen.data_ptr(),
-                  self._pg.data_ptr(), hq, hkv, d, self.max_len, o.data_ptr(), self.lse.data_ptr(),
-                  self._ws.data_ptr(), self._ws_bytes, self._n_parts, _lib.stream_ptr(self.pos.device))
+                  self._pg.data_ptr(), hq, hkv, d, self.max_len, o.data_ptr(), self.lse.data_ptr(), _lib.ptr(w_o),
+                  _lib.ptr(h1_out), self._ws.data_ptr(), self._ws_bytes, self._n_parts, _lib.stream_ptr(self.pos.device))
         return o
 
     def set_parts(self, n_parts: int) -> None:

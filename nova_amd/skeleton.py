@@ -12,13 +12,13 @@ Two ways to run a layer:
 
 - torch (default): projections, norms and lm_head are plain torch ops around the KV path;
 - ``use_decode_kernels()``: a one-token decode step (batch 1, int8 cache) runs each layer as
-  four launches of this package's HIP kernels: the attention block in one
-  (``update_attend_qkv``: the input RMSNorm and qkv projection, the q/k head norms + RoPE, the
-  append and the attention of the token), o_proj GEMV with the residual add, gate/up GEMV with
+  three launches of this package's HIP kernels: the attention block in one
+  (``update_attend_block``: the input RMSNorm and qkv projection, the q/k head norms + RoPE,
+  the append and the attention of the token, o_proj with the residual add), gate/up GEMV with
   SwiGLU and the post-attention RMSNorm, down GEMV with the residual add; the final RMSNorm is
   fused into the lm_head GEMV. ``use_decode_kernels(fused_qkv=False)`` splits the attention
-  block into the qkv GEMV, the head norms + RoPE and ``update_attend`` (the same bits). The
-  same fp16 roundings as the torch path, up to fp32 summation order.
+  block into the qkv GEMV, the head norms + RoPE, ``update_attend`` and the o_proj GEMV (the
+  same bits). The same fp16 roundings as the torch path, up to fp32 summation order.
 """
 
 from __future__ import annotations
@@ -160,13 +160,23 @@ class SkeletonLayer(nn.Module):
                        fused_qkv: bool = True) -> torch.Tensor:
         """One decode token (``h`` of ``hidden_size`` elements) through the layer on the HIP
         kernels; returns the new residual stream (a new tensor). With ``fused_qkv`` (and a cache
-        that has it) the projection, head norms, RoPE and attention step are one launch
-        (``update_attend_qkv``), bit for bit the same as the separate launches."""
+        that has it) the projection, head norms, RoPE, attention step, o_proj and residual add are
+        one launch (``update_attend_block``), bit for bit the same as the separate launches."""
         from . import gemv as G
 
         cfg, a = self.attn.cfg, self.attn
         hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
         x = h.reshape(-1)
+        if fused_qkv and hasattr(cache, "update_attend_block") and hq // hkv <= 4 and x.numel() % 8 == 0 \
+                and x.numel() <= 3072 and hq * d <= 4096:
+            # the projection, the head norms + RoPE, the attention step, o_proj and the residual
+            # add in one launch
+            h1 = cache.update_attend_block(x, self.w_qkv, self.norm, self.eps, a.q_norm, a.k_norm, cfg.rms_eps,
+                                           inv_freq, a.o_proj.weight, a.layer_idx)
+            if self.mlp is not None:
+                act = G.swiglu_gemv(h1, self.w_gate_up, self.post_norm, self.eps)
+                G.rms_gemv(act, self.mlp.down_proj.weight, residual=h1, out=h1)
+            return h1.view(h.shape)
         if fused_qkv and hasattr(cache, "update_attend_qkv") and hq // hkv <= 4 and x.numel() % 8 == 0 \
                 and x.numel() <= 3072:
             # the projection, the head norms + RoPE and the attention step in one launch

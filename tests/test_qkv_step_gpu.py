@@ -1,6 +1,7 @@
 """GPU parity of the fused attention-block step (``nkv_decode_step_qkv_t64``,
-``KVInt8Cache.update_attend_qkv``): the input RMSNorm and stacked q/k/v projection, the q/k head
-norms with the rotary embedding, and the append + attention of the token, in one launch.
+``KVInt8Cache.update_attend_qkv`` / ``update_attend_block``): the input RMSNorm and stacked q/k/v
+projection, the q/k head norms with the rotary embedding, the append + attention of the token and
+(``update_attend_block``) the output projection with the residual add, in one launch.
 
 The step computes every value exactly as the separate launches do (``nkv_gemv`` with the input
 norm, ``nkv_qk_norm_rope``, ``nkv_decode_step_t64``: the same input chunks per thread, the same
@@ -86,6 +87,103 @@ def test_fused_step_equals_separate_launches(hidden, n0, steps, cap):
         fused.pos.add_(1)
         sep.pos.add_(1)
     _assert_same_state(fused, sep)
+
+
+def _w_o(hidden: int, seed: int) -> torch.Tensor:
+    return (torch.randn(hidden, HQ * D, generator=_gen(seed), device="cuda") * (HQ * D) ** -0.5).half()
+
+
+@pytest.mark.parametrize("hidden,n0,steps,cap", [(2560, 4000, 60, 4200), (2560, 200, 40, 512), (1024, 1990, 40, 2112),
+                                                 (2560, 32765, 4, 32832)])
+def test_block_with_o_proj_equals_separate_launches(hidden, n0, steps, cap):
+    """The attention block with its output projection (``update_attend_block``): h1 = x + W_o o,
+    the attention output o and the cache state, bit for bit the separate launches' (the GEMV
+    computes o_proj with the residual), over steps; every other step updates x in place."""
+    from nova_amd import gemv as G
+    from nova_amd.kvattn import KVInt8Cache
+
+    print(f"case attention block + o_proj hidden={hidden} n0={n0} steps={steps} cap={cap}", flush=True)
+    w, xg, qg, kg, inv = _params(hidden, 80)
+    w_o = _w_o(hidden, 81)
+    fused = KVInt8Cache(num_slots=1, num_kv_heads=H_KV, head_dim=D, max_len=cap, num_q_heads=HQ)
+    sep = KVInt8Cache(num_slots=1, num_kv_heads=H_KV, head_dim=D, max_len=cap, num_q_heads=HQ)
+    _prefill_t64(fused, 1, n0, seed=82)
+    _prefill_t64(sep, 1, n0, seed=82)
+    qkv_out = torch.empty((HQ + 2 * H_KV) * D, dtype=torch.float16, device="cuda")
+    o_f = torch.empty(1, HQ, 1, D, dtype=torch.float16, device="cuda")
+    for s in range(steps):
+        x = _x(hidden, 300 + s)
+        qkv, o_s = _separate(sep, x, w, xg, qg, kg, inv)
+        want = G.rms_gemv(o_s.reshape(-1), w_o, residual=x)
+        xin = x.clone()
+        h1 = fused.update_attend_block(xin, w, xg, EPS, qg, kg, EPS, inv, w_o, 0, out=o_f, qkv_out=qkv_out,
+                                       h1_out=xin if s % 2 else None)
+        torch.cuda.synchronize()
+        assert torch.equal(qkv_out, qkv), f"step {s}: q/k/v differ"
+        assert torch.equal(o_f, o_s), f"step {s}: attention output differs"
+        assert torch.isfinite(h1.float()).all(), f"step {s}: non-finite h1"
+        assert torch.equal(h1, want), f"step {s}: h1 differs from the separate launches"
+        if s % 2:
+            assert h1.data_ptr() == xin.data_ptr()
+        fused.pos.add_(1)
+        sep.pos.add_(1)
+    _assert_same_state(fused, sep)
+
+
+def test_block_with_o_proj_graph_replay_equals_eager():
+    """The block with o_proj captured once and replayed (x from a fixed buffer, h1 into a buffer
+    of its own) equals eager calls on a twin cache, bit for bit."""
+    from nova_amd.kvattn import KVInt8Cache
+
+    print("case attention block + o_proj graph replay", flush=True)
+    hidden, n0, cap = 2560, 3000, 3200
+    w, xg, qg, kg, inv = _params(hidden, 90)
+    w_o = _w_o(hidden, 91)
+    caches = [KVInt8Cache(num_slots=1, num_kv_heads=H_KV, head_dim=D, max_len=cap, num_q_heads=HQ) for _ in range(2)]
+    for c in caches:
+        _prefill_t64(c, 1, n0, seed=92)
+    g_cache, e_cache = caches
+    xbuf = _x(hidden, 0)
+    h1 = torch.empty(hidden, dtype=torch.float16, device="cuda")
+    for c in caches:  # one eager step each (the workspace grows outside the capture)
+        c.update_attend_block(xbuf, w, xg, EPS, qg, kg, EPS, inv, w_o, 0, h1_out=h1)
+        c.pos.add_(1)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            g_cache.update_attend_block(xbuf, w, xg, EPS, qg, kg, EPS, inv, w_o, 0, h1_out=h1)
+            g_cache.pos.add_(1)
+    torch.cuda.current_stream().wait_stream(stream)
+    for s in range(40):
+        x = _x(hidden, 400 + s)
+        xbuf.copy_(x)
+        graph.replay()
+        want = e_cache.update_attend_block(x, w, xg, EPS, qg, kg, EPS, inv, w_o, 0)
+        e_cache.pos.add_(1)
+        torch.cuda.synchronize()
+        assert torch.equal(h1, want), f"step {s}: replay differs from eager"
+    _assert_same_state(g_cache, e_cache)
+
+
+def test_block_with_o_proj_argument_checks():
+    from nova_amd.kvattn import KVInt8Cache
+
+    hidden = 2560
+    w, xg, qg, kg, inv = _params(hidden, 95)
+    c = KVInt8Cache(num_slots=1, num_kv_heads=H_KV, head_dim=D, max_len=512, num_q_heads=HQ)
+    _prefill_t64(c, 1, 100, seed=96)
+    x = _x(hidden, 1)
+    with pytest.raises(ValueError):  # w_o of the wrong shape
+        c.update_attend_block(x, w, xg, EPS, qg, kg, EPS, inv, _w_o(hidden, 97)[:, :2048].contiguous(), 0)
+    with pytest.raises(ValueError):  # h1_out of the wrong size
+        c.update_attend_block(x, w, xg, EPS, qg, kg, EPS, inv, _w_o(hidden, 98), 0,
+                              h1_out=torch.empty(100, dtype=torch.float16, device="cuda"))
+    o = torch.empty(1, HQ, 1, D, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):  # h1_out overlapping the attention output
+        c.update_attend_block(x, w, xg, EPS, qg, kg, EPS, inv, _w_o(hidden, 99), 0, out=o, h1_out=o.view(-1)[:hidden])
 
 
 def test_fused_step_graph_replay_equals_eager():
