@@ -2705,8 +2705,11 @@ template <bool TOK>
 __device__ __forceinline__ AttnArgs layer_args(const AttnArgs& a, const void* layers, int l, uint32_t ftag) {
   AttnArgs la = a;
   la.ftag = ftag;
+  // the table through the constant address space: scalar loads (the host wrote it before the
+  // launch), which do not queue behind the workgroup's vector loads and DMA
   if constexpr (TOK) {
-    const nkv_layer_tok& e = static_cast<const nkv_layer_tok*>(layers)[l];
+    const __attribute__((address_space(4))) nkv_layer_tok& e =
+        ((const __attribute__((address_space(4))) nkv_layer_tok*)(uintptr_t)layers)[l];
     la.q = e.q;
     la.k_new = e.k_new;
     la.v_new = e.v_new;
@@ -2717,7 +2720,8 @@ __device__ __forceinline__ AttnArgs layer_args(const AttnArgs& a, const void* la
     la.out = e.out;
     la.lse = e.lse;
   } else {
-    const nkv_layer_t64& e = static_cast<const nkv_layer_t64*>(layers)[l];
+    const __attribute__((address_space(4))) nkv_layer_t64& e =
+        ((const __attribute__((address_space(4))) nkv_layer_t64*)(uintptr_t)layers)[l];
     la.q = e.q;
     la.k_new = e.k_new;
     la.v_new = e.v_new;
