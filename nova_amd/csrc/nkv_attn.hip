@@ -2422,9 +2422,10 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   if (!TOK && !PAGED && append) uio = unit_io(a, h, part, pos);
   [[maybe_unused]] uint32_t qkv_tag = 0;
   if constexpr (QKV) {
-    // the projection first (q, and the new token's k / v, come from it); the first groups and the
-    // append unit's ring rows are issued by the waves that do not compute, and have landed when
-    // the workgroup meets below
+    // the projection first (q, and the new token's k / v, come from it); the first groups' first
+    // halves and the append unit's ring rows are issued by the waves that do not compute, and have
+    // landed when the workgroup meets below; each wave issues its second half after that (the
+    // workgroup's loads leave in issue order, so a shallower queue lets the q polls through sooner)
     __shared__ __attribute__((aligned(16))) uint16_t kv_lds[2 * D];
     __shared__ int issued;
     if (tid == 0) issued = 0;
@@ -2441,7 +2442,6 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
         if (w >= ng) break;
         const uint32_t wl = __builtin_amdgcn_readfirstlane(lds_addr(lds_raw + w * wave_lds));
         issue_half(a, h, gs + w, 0, wl, wl + 2 * HALF_SLOT);
-        issue_half(a, h, gs + w, 1, wl + HALF_SLOT, wl + 2 * HALF_SLOT);
       }
       if (wave == QKV_WAVES && append) issue_unit_ring(uio, part, src_lds);
     }
@@ -2475,6 +2475,9 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
   }
   }  // QKV
   __syncthreads();
+  if constexpr (QKV) {
+    if (wave < ng) issue_half(a, h, gs + wave, 1, my_lds + HALF_SLOT, rul_lds);
+  }
 
   if (append) {
     if constexpr (PAGED) append_tok_rows_paged(a, b, h, pos);
