@@ -1636,8 +1636,11 @@ __device__ __forceinline__ float* paged_ring_slot(const AttnArgs& a, int h, int 
 template <bool PAGED>
 __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailSmem& sm, int run, int64_t pos,
                                           bool pos_ok, int64_t U, const TailLoads* pre = nullptr,
-                                          const half8_t (*pre_q)[4] = nullptr, int flags = 0, int64_t page = -1) {
+                                          const half8_t (*pre_q)[4] = nullptr, int flags = 0, int64_t page = -1,
+                                          int64_t tag_in = -1) {
   const int tid = tail_tid(), wave = tid >> 6, lane = tid & 63;
+  // the tag of the tagged output words and flags: the caller's, else a.ftag
+  const uint32_t ftag = tag_in >= 0 ? (uint32_t)tag_in : a.ftag;
   const bool poll = run != TAIL_KERNEL;  // partials written in this launch: poll their words
   const int gq = a.gq, pw = part_stride(gq), cols = gq * D;
   const int P0 = PAGED ? min(a.seq_parts[2 * b + 1], WTS) : a.n_parts;  // prefix partials
@@ -1892,7 +1895,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
         const uint32_t pair = (uint32_t)f2h(ox) | ((uint32_t)f2h(oy) << 16);
         *reinterpret_cast<uint32_t*>(a.out + qh * D + 2 * lane) = pair;
         if (a.fwd_out)
-          hand_st(a.fwd_out + qh * D / 2 + lane, ((uint64_t)a.ftag << 32) | pair, l2_local(a) && !a.fwd_agent);
+          hand_st(a.fwd_out + qh * D / 2 + lane, ((uint64_t)ftag << 32) | pair, l2_local(a) && !a.fwd_agent);
         if (a.lse && lane == 0)
           a.lse[qh] = failed ? __builtin_nanf("") : (lt > 0.0f ? (M + __log2f(lt) - P_SCALE_LOG2) * LN2 : NEG_INF);
         // this head's outputs are issued: count it for the readers of the next layer (they
@@ -1900,7 +1903,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
         if (a.issue_flags && lane == 0) {
 #pragma unroll
           for (int c = 0; c < FLAG_COPIES; ++c)
-            __hip_atomic_store(a.issue_flags + c * a.hq + qh, a.ftag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.issue_flags + c * a.hq + qh, ftag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       } else {
         *reinterpret_cast<float2*>(sm.pre_acc + head0 * D + 2 * lane) = acc;
@@ -2026,7 +2029,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
     if (a.fwd_out) {  // (columns come in pairs of neighbouring lanes: d even in the even lane)
       const uint32_t pair = (uint32_t)__shfl_xor((int)o16, 1, 64);
       if ((d & 1) == 0)
-        hand_st(a.fwd_out + ((int64_t)qh * D + d) / 2, ((uint64_t)a.ftag << 32) | o16 | (pair << 16),
+        hand_st(a.fwd_out + ((int64_t)qh * D + d) / 2, ((uint64_t)ftag << 32) | o16 | (pair << 16),
                 l2_local(a) && !a.fwd_agent);
     }
     if (a.lse && d == 0) a.lse[qh] = failed ? __builtin_nanf("") : (l > 0.0f ? (M + __log2f(l) - P_SCALE_LOG2) * LN2 : NEG_INF);
@@ -2034,7 +2037,7 @@ __device__ __forceinline__ void tail_body(const AttnArgs& a, int h, int b, TailS
   if (a.issue_flags) {  // every column issued: the workgroup's gq heads flagged at once
     __syncthreads();
     if (tid < gq * FLAG_COPIES)
-      __hip_atomic_store(a.issue_flags + (tid / gq) * a.hq + qh0 + tid % gq, a.ftag, __ATOMIC_RELAXED,
+      __hip_atomic_store(a.issue_flags + (tid / gq) * a.hq + qh0 + tid % gq, ftag, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
   // ---- every word of the head's partials was consumed before the barrier above: the whole
@@ -2163,7 +2166,9 @@ __device__ __forceinline__ void issue_unit_ring(const UnitIO& io, int unit, uint
 // (lane l holds input chunks l + 64 u, which gemv_kernel's wave u holds in lane l: the wave sums
 // of the squares are its waves' sums, added in the same order). Returns false when a wait for
 // rows gave up (its vectors are then NaN).
-__device__ bool qkv_prologue(const AttnArgs& a, int h, int part, int parts, int64_t pos, uint32_t tag, int unit,
+// (always inlined: called out of line, it takes the kernel's arguments by reference, which then
+// live in scratch memory for the whole launch)
+__device__ __forceinline__ bool qkv_prologue(const AttnArgs& a, int h, int part, int parts, int64_t pos, uint32_t tag, int unit,
                              uint16_t* q_lds, uint16_t* kv_lds, uint16_t* unit_src, int* issued) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nch = a.hidden / 8, nl = (nch + 63) / 64;
@@ -2431,7 +2436,6 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
     if (tid == 0) issued = 0;
     __syncthreads();
     qkv_tag = (uint32_t)__hip_atomic_load(a.qkv_epoch + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-    a.ftag = qkv_tag;  // (the merger's tagged output words, when w_o)
     if (wave >= QKV_WAVES) {
       // after every computing wave's first weight loads (bounded: 2^16 short sleeps)
       for (int n = 0; n < (1 << 16); ++n) {
@@ -2637,7 +2641,7 @@ __global__ __launch_bounds__(THREADS, 1) void attn_prefix_kernel(AttnArgs a) {
       for (int i = tid; i < P * pw / 4; i += THREADS) blk[i] = uint4{0u, 0u, 0u, 0u};
     }
   } else {
-    tail_body<false>(a, h, b, sm, TAIL_MERGER, pos, pos_ok, U, &tl, &qb);
+    tail_body<false>(a, h, b, sm, TAIL_MERGER, pos, pos_ok, U, &tl, &qb, 0, -1, QKV ? (int64_t)qkv_tag : -1);
     // every workgroup of head h has read its rows (before publishing the partials just merged):
     // the next launch's tag
     if constexpr (QKV) {
