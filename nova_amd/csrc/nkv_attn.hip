@@ -3290,6 +3290,14 @@ constexpr int PF_KROW = D + 8;                       // fp16 K tile row stride (
 constexpr int PF_VROW = GT + 8;                      // fp16 V^T tile row stride (halves, 16-byte rows)
 constexpr float PF_TAU = 8.0f;                       // lazy softmax rescaling threshold (log2)
 constexpr int PF_PART = D + 4;                       // floats per row partial: acc[128], m, l, pad
+#ifndef PF_SCHED
+#define PF_SCHED 1
+#endif
+#ifndef PF_SCHED_V
+#define PF_SCHED_V 3  // VALU instructions scheduled after each interleaved MFMA
+#endif
+// instruction classes of __builtin_amdgcn_sched_group_barrier
+constexpr int PF_SG_VALU = 0x2, PF_SG_MFMA = 0x8, PF_SG_DSR = 0x100;
 
 // token slot of the V^T tile: P's k-slot order (slot 8g + r of a 32-token block <-> token
 // 16 (r >> 2) + 4g + (r & 3))
@@ -3353,8 +3361,8 @@ __device__ __forceinline__ void pf_softmax(WaveState& st, const float (&S)[4][4]
 
 __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t stage[2][2 * CODE_BYTES + RULER_BYTES];
-  __shared__ __attribute__((aligned(16))) uint16_t ktile[GT * PF_KROW];
-  __shared__ __attribute__((aligned(16))) uint16_t vtile[D * PF_VROW];
+  __shared__ __attribute__((aligned(16))) uint16_t ktile_buf[2][GT * PF_KROW];
+  __shared__ __attribute__((aligned(16))) uint16_t vtile_buf[2][D * PF_VROW];
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.x % a.hkv, tile = (blockIdx.x / a.hkv) % a.tiles, split = blockIdx.x / (a.hkv * a.tiles);
@@ -3411,7 +3419,9 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
   constexpr int DMA_PF = 3;  // loads per wave and group
 
   // ---- MFMA phase over the tiles in LDS; `mask_base` >= 0: chunk tokens from that index (causal)
-  auto attend_tiles = [&](int mask_base) {
+  auto attend_tiles = [&](int mask_base, int tb, auto&& tail_work) {
+    const uint16_t* ktile = ktile_buf[tb];
+    const uint16_t* vtile = vtile_buf[tb];
     float4_t S[PF_RB][4];
 #pragma unroll
     for (int rb = 0; rb < PF_RB; ++rb)
@@ -3420,14 +3430,27 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
     half8_t ph[PF_RB][2];
     float alpha[PF_RB];
     bool moved[PF_RB];
+    // the K and V operands of the group, each read from LDS once for both row blocks
+    half8_t kop[4][4], vop[2][8];
+    auto load_k = [&]() {
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          kop[b][k] = *reinterpret_cast<const half8_t*>(ktile + (16 * b + c) * PF_KROW + 16 * g + 64 * (k >> 1) + 8 * (k & 1));
+    };
+    auto load_v = [&]() {
+#pragma unroll
+      for (int B = 0; B < 2; ++B)
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb)
+          vop[B][cb] = *reinterpret_cast<const half8_t*>(vtile + (16 * cb + c) * PF_VROW + 32 * B + 8 * g);
+    };
     auto qk = [&](int rb) {
 #pragma unroll
       for (int b = 0; b < 4; ++b)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const half8_t ka = *reinterpret_cast<const half8_t*>(ktile + (16 * b + c) * PF_KROW + 16 * g + 64 * (k >> 1) + 8 * (k & 1));
-          S[rb][b] = mfma32(ka, qb[rb][k], S[rb][b]);
-        }
+        for (int k = 0; k < 4; ++k) S[rb][b] = mfma32(kop[b][k], qb[rb][k], S[rb][b]);
     };
     auto softmax = [&](int rb) {
       float sc[4][4];
@@ -3442,15 +3465,16 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
       // rows of the S^T layout are q rows c; the causal test above needs the row of column
       // c, which is lane-independent of g: scores of lane (c, g) all belong to row c
       pf_softmax(st[rb], sc, a.sl2, ph[rb], alpha[rb], moved[rb]);
+#if PF_SCHED
+      // P is computed here, beside the other row block's products, not sunk past the rescale
+      asm volatile("" : "+v"(ph[rb][0]), "+v"(ph[rb][1]));
+#endif
     };
     auto pv = [&](int rb) {
 #pragma unroll
       for (int B = 0; B < 2; ++B)
 #pragma unroll
-        for (int cb = 0; cb < 8; ++cb) {
-          const half8_t vb = *reinterpret_cast<const half8_t*>(vtile + (16 * cb + c) * PF_VROW + 32 * B + 8 * g);
-          st[rb].acc[cb] = mfma32(ph[rb][B], vb, st[rb].acc[cb]);
-        }
+        for (int cb = 0; cb < 8; ++cb) st[rb].acc[cb] = mfma32(ph[rb][B], vop[B][cb], st[rb].acc[cb]);
 #pragma unroll
       for (int B = 0; B < 2; ++B) lsum[rb] = mfma32(ph[rb][B], ones, lsum[rb]);
     };
@@ -3468,63 +3492,103 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
     // QK(1) beside softmax(0), PV(0) beside softmax(1): the matrix core and the VALU each have
     // the other row block's work (the rescales, rare, between)
     static_assert(PF_RB == 2, "two row blocks per wave");
+    load_k();
     qk(0);
+#if PF_SCHED
+    // a wave issues in order: without an explicit interleave the compiler emits QK(1) as one run
+    // of MFMAs and softmax(0) as one run of VALU instructions, and the matrix core idles through
+    // the softmax. QK(0) (with the K operand reads) first, then QK(1) one MFMA at a time between
+    // softmax(0)'s instructions
+    __builtin_amdgcn_sched_barrier(0);
+#endif
     qk(1);
     softmax(0);
+#if PF_SCHED
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(PF_SG_MFMA, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(PF_SG_VALU, PF_SCHED_V, 0);
+    }
+#endif
     rescale(0);
+    load_v();
     pv(0);
     softmax(1);
+#if PF_SCHED
+    // PV(0) between softmax(1)'s instructions, after the V operand reads
+    __builtin_amdgcn_sched_group_barrier(PF_SG_DSR, 16, 1);
+#pragma unroll
+    for (int i = 0; i < 18; ++i) {
+      __builtin_amdgcn_sched_group_barrier(PF_SG_MFMA, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(PF_SG_VALU, PF_SCHED_V, 1);
+    }
+#endif
     rescale(1);
+    // PV(1) and the caller's work (the next group's dequantization) in one basic block: the
+    // compiler interleaves the two by itself
+    tail_work();
     pv(1);
   };
 
-  // ---- cache groups: double-buffered LDS stages, dequantized once into the fp16 tiles
-  if (cs < ce) issue(cs, 0);
-  for (int64_t grp = cs; grp < ce; ++grp) {
-    const int sb = (int)((grp - cs) & 1);
-    if (grp + 1 < ce) {
-      issue(grp + 1, sb ^ 1);
+  // ---- cache groups: two LDS stages of int8 codes and two fp16 tile buffers. Group t's codes
+  // are dequantized into tile buffer t & 1 during group t - 1's last product (PV of the second
+  // row block), so a group takes one workgroup barrier: after it, tile buffer t & 1 is complete,
+  // the codes of group t + 1 have landed, and every wave is done with tile buffer (t + 1) & 1 and
+  // with the stage of group t
+  auto dequant = [&](const uint8_t* sg, uint16_t* ktile, uint16_t* vtile) {
+    const uint16_t* rks = reinterpret_cast<const uint16_t*>(sg + 2 * CODE_BYTES);
+    // K: thread t dequantizes row t >> 3, dims 16 (t & 7) .. + 15
+    const int row = tid >> 3, key = swz(row);
+    {
+      const int ch = tid & 7;  // 16-dim chunk
+      const uint4 kw = *reinterpret_cast<const uint4*>(sg + row * D + ((ch ^ key) << 4));
+      const uint4 s0 = *reinterpret_cast<const uint4*>(rks + 16 * ch), s1 = *reinterpret_cast<const uint4*>(rks + 16 * ch + 8);
+      const uint4 m0 = *reinterpret_cast<const uint4*>(rks + D + 16 * ch), m1 = *reinterpret_cast<const uint4*>(rks + D + 16 * ch + 8);
+      *reinterpret_cast<half8_t*>(ktile + row * PF_KROW + 16 * ch) = dq8(kw.x, kw.y, s0, m0);
+      *reinterpret_cast<half8_t*>(ktile + row * PF_KROW + 16 * ch + 8) = dq8(kw.z, kw.w, s1, m1);
+    }
+    // V: transposed reads; wave w covers dim block w of both 32-token blocks
+    const int r = c >> 1;
+#pragma unroll
+    for (int B = 0; B < 2; ++B)
+      {
+        const int cb = wave;
+        const int vrow = 16 * (2 * B + (r >> 2)) + 4 * g + (r & 3);
+        const u32x2 vw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (lds_v2i_t*)(const lds_void_t*)(sg + CODE_BYTES + vrow * D + 8 * (c & 1) + ((cb ^ swz(vrow)) << 4))));
+        const _Float16 vs = __builtin_bit_cast(_Float16, rks[2 * D + 16 * cb + c]);
+        const _Float16 vm = __builtin_bit_cast(_Float16, rks[3 * D + 16 * cb + c]);
+        *reinterpret_cast<half8_t*>(vtile + (16 * cb + c) * PF_VROW + 32 * B + 8 * g) =
+            dq8_splat(vw.x, vw.y, half2_t{vs, vs}, half2_t{vm, vm});
+      }
+  };
+  if (cs < ce) {
+    issue(cs, 0);
+    if (cs + 1 < ce) {
+      issue(cs + 1, 1);
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_PF) : "memory");
     } else {
       wait_groups_all();
     }
-    __syncthreads();  // stage sb is complete; every wave is done with the tiles
-    {
-      const uint8_t* sg = stage[sb];
-      const uint16_t* rks = reinterpret_cast<const uint16_t*>(sg + 2 * CODE_BYTES);
-      // K: thread t dequantizes row t >> 3, dims 16 (t & 7) .. + 15
-      const int row = tid >> 3, key = swz(row);
-      {
-        const int ch = tid & 7;  // 16-dim chunk
-        const uint4 kw = *reinterpret_cast<const uint4*>(sg + row * D + ((ch ^ key) << 4));
-        const uint4 s0 = *reinterpret_cast<const uint4*>(rks + 16 * ch), s1 = *reinterpret_cast<const uint4*>(rks + 16 * ch + 8);
-        const uint4 m0 = *reinterpret_cast<const uint4*>(rks + D + 16 * ch), m1 = *reinterpret_cast<const uint4*>(rks + D + 16 * ch + 8);
-        *reinterpret_cast<half8_t*>(ktile + row * PF_KROW + 16 * ch) = dq8(kw.x, kw.y, s0, m0);
-        *reinterpret_cast<half8_t*>(ktile + row * PF_KROW + 16 * ch + 8) = dq8(kw.z, kw.w, s1, m1);
-      }
-      // V: transposed reads; wave w covers dim block w of both 32-token blocks
-      const int r = c >> 1;
-#pragma unroll
-      for (int B = 0; B < 2; ++B)
-        {
-          const int cb = wave;
-          const int vrow = 16 * (2 * B + (r >> 2)) + 4 * g + (r & 3);
-          const u32x2 vw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-              (lds_v2i_t*)(const lds_void_t*)(sg + CODE_BYTES + vrow * D + 8 * (c & 1) + ((cb ^ swz(vrow)) << 4))));
-          const _Float16 vs = __builtin_bit_cast(_Float16, rks[2 * D + 16 * cb + c]);
-          const _Float16 vm = __builtin_bit_cast(_Float16, rks[3 * D + 16 * cb + c]);
-          *reinterpret_cast<half8_t*>(vtile + (16 * cb + c) * PF_VROW + 32 * B + 8 * g) =
-              dq8_splat(vw.x, vw.y, half2_t{vs, vs}, half2_t{vm, vm});
-        }
-    }
-    __syncthreads();  // tiles complete
-    attend_tiles(-1);
+    __syncthreads();  // stage 0 is complete
+    dequant(stage[0], ktile_buf[0], vtile_buf[0]);
+  }
+  for (int64_t grp = cs; grp < ce; ++grp) {
+    const int tb = (int)((grp - cs) & 1);  // tile buffer and stage of group grp
+    wait_groups_all();                     // the codes of group grp + 1 (the only loads in flight)
+    __syncthreads();
+    if (grp + 2 < ce) issue(grp + 2, tb);  // into the stage of group grp, dequantized before the barrier
+    // (after the last group the dequantization reads a stale stage into a tile buffer nothing
+    // reads again: unconditional, so that it stays in one basic block with the product)
+    attend_tiles(-1, tb, [&]() { dequant(stage[tb ^ 1], ktile_buf[tb ^ 1], vtile_buf[tb ^ 1]); });
   }
 
   // ---- fp16 groups (causal): j = split, split + S, ...
   for (int j = split; j < nchunk; j += a.splits) {
     __syncthreads();  // every wave is done with the tiles
     {
+      uint16_t* ktile = ktile_buf[0];
+      uint16_t* vtile = vtile_buf[0];
       const int row = tid >> 3, cp = tid & 7, t = GT * j + row;
       const bool ok = t < a.Mk;
       const uint16_t* kr = a.kc + (int64_t)h * a.kc_hs + (int64_t)(ok ? t : 0) * D + 16 * cp;
@@ -3542,7 +3606,7 @@ __global__ __launch_bounds__(PF_THREADS, PF_WG_PER_CU) void prefill_chunk_kernel
       }
     }
     __syncthreads();
-    attend_tiles(GT * j);
+    attend_tiles(GT * j, 0, []() {});
   }
 
   // ---- one partial per row: acc[128] and l (both x 2^15), m (log2 domain)
