@@ -3287,7 +3287,7 @@ constexpr int PF_RB = 2;                             // MFMA row blocks per wave
 constexpr int PF_WG_PER_CU = 1;                      // workgroups resident per CU (~206 VGPRs per lane)
 constexpr int PF_ROWS = PF_WAVES * PF_RB * 16;       // 256 query rows per workgroup
 constexpr int PF_KROW = D + 8;                       // fp16 K tile row stride (halves)
-constexpr int PF_VROW = GT + 8;                      // fp16 V^T tile row stride (halves, 16-byte rows)
+constexpr int PF_VROW = GT + 16;                     // fp16 V^T tile row stride (halves, 16-byte rows)
 constexpr float PF_TAU = 8.0f;                       // lazy softmax rescaling threshold (log2)
 constexpr int PF_PART = D + 4;                       // floats per row partial: acc[128], m, l, pad
 #ifndef PF_SCHED
