@@ -20,8 +20,10 @@ committed rocprofv3 --pmc summary of that kernel (FETCH_SIZE + WRITE_SIZE per di
 scaled by what the counter reads for the library's copy kernel of known size). ``cpu_baseline``
 times the repo's torch fp32 restatement of the reference algorithm (dequantize the int8 prefix,
 append the ring, repeat KV heads, softmax attention) on the host cores for one layer and a few
-steps, scaled to the 36-layer step. ``gpu_clock`` is read with amd-smi while the step graph
-replays. ``workloads`` carries the other configurations measured in the same run: the per-head
+steps, scaled to the 36-layer step. ``core_clock`` is each XCD's core clock right after the timed
+replays, from the device's core and 100 MHz real-time counters (``nkv_clock_probe``);
+``gpu_clock`` is what amd-smi reports while the launches replay (on some hosts it reports an
+idle clock under load). ``workloads`` carries the other configurations measured in the same run: the per-head
 dependency, one launch per layer (what a model's layer loop calls), the per-token symmetric
 format, the paged ragged batch, the MFMA chunked prefill, the read ceiling of the decode path's
 load pattern and the end-to-end random-weight decoder.
@@ -375,6 +377,29 @@ def read_gpu_clock(timeout: float = 30.0) -> dict:
     return {"source": "amd-smi metric --clock --json", "gfx_mhz": gfx[:8] or None, "mem_mhz": mem[:1] or None}
 
 
+CLOCK_PROBE_WGS, CLOCK_PROBE_ITERS = 64, 20000  # ~70 us of one wave per workgroup
+
+
+def core_clock(dev) -> dict:
+    """Each XCD's core clock in MHz, from ``nkv_clock_probe`` launched now, right after a timed run
+    (the clocks move over milliseconds, the probe takes ~70 us): per workgroup the core clock
+    counter's advance (s_memtime) over the 100 MHz real-time counter's (s_memrealtime), averaged
+    over the workgroups of each XCD."""
+    import torch
+
+    from nova_amd import _lib
+
+    buf = torch.zeros(3 * CLOCK_PROBE_WGS, dtype=torch.int64, device=dev)
+    _lib.call("nkv_clock_probe", buf.data_ptr(), CLOCK_PROBE_WGS, CLOCK_PROBE_ITERS, _lib.stream_ptr(dev))
+    by_xcd: dict = {}
+    for xcc, dm, dr in buf.view(CLOCK_PROBE_WGS, 3).cpu().tolist():
+        if dr > 0:
+            by_xcd.setdefault(int(xcc), []).append(100.0 * dm / dr)
+    mhz = [round(sum(v) / len(v)) for _, v in sorted(by_xcd.items())]
+    return {"source": "nkv_clock_probe: s_memtime over s_memrealtime (100 MHz), right after the timed replays",
+            "gfx_mhz_by_xcd": mhz, "gfx_mhz_mean": round(sum(mhz) / len(mhz)) if mhz else None}
+
+
 def clock_under_load(replay) -> dict:
     """Read the clock in a thread while ``replay()`` keeps the GPU busy (bounded to ~40 s)."""
     box: dict = {}
@@ -514,6 +539,7 @@ def run_decode(args, scheme: str, headline: bool, mode: str = "chain", dep: str 
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
+    core_clk = core_clock(dev)
     ms = e0.elapsed_time(e1)
     assert int(cache.pos.item()) == pos0 + K
     if chain is not None:
@@ -528,7 +554,9 @@ def run_decode(args, scheme: str, headline: bool, mode: str = "chain", dep: str 
     ms_launches = _time_graph(g_launch, stream, K, W, SETTLE_STEPS)  # (pos fixed: settling moves nothing)
     if chain is not None:
         chain.check()
-    clock = None if args.no_clock else clock_under_load(graph.replay)
+    # (the launches' graph: pos stays fixed, so every replay does the whole step's work; the step
+    # graph would run past the cache's capacity during amd-smi's run and then attend nothing)
+    clock = None if args.no_clock else clock_under_load(g_launch.replay)
     _calibration_copy(dev)
 
     ms_step = ms / K
@@ -564,6 +592,7 @@ def run_decode(args, scheme: str, headline: bool, mode: str = "chain", dep: str 
         "step_pct_of_hbm_peak": round(100 * step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS, 2),
         "wall_s_timed": round(wall, 4),
         "roofline": _roofline_hbm(launch_bytes, per_launch_s, f"{mode}_{scheme}", kname, n_launch),
+        "core_clock": core_clk,
         "gpu_clock": clock,
     }
     del graph, g_launch, cache, outs, chain
@@ -681,6 +710,7 @@ def run_prefill(args, steps: int | None = None) -> dict:
         int8_prefill_attend(q, kc, vc, *packed, used=U, out=out, scratch=scratch, splits=splits)
     # (every replay recomputes the same chunk, so the settle replays change nothing but the clocks)
     ms = _time_graph(graph, torch.cuda.current_stream(dev), K, W, SETTLE_STEPS)
+    core_clk = core_clock(dev)
     assert torch.isfinite(out).all()
     _calibration_copy(dev)
     flop = 2 * 2 * D * HQ * (M * U + M * (M + 1) // 2)
@@ -699,7 +729,7 @@ def run_prefill(args, steps: int | None = None) -> dict:
                          "kernel": "nkv::prefill_chunk_kernel + nkv::prefill_combine_kernel (the chunk's two "
                                    "launches, timed together)",
                          "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(ms * 1e3, 3)},
-            "gbs": round(nbytes / (ms / 1e3) / 1e9, 1), "settle_steps": SETTLE_STEPS}
+            "gbs": round(nbytes / (ms / 1e3) / 1e9, 1), "settle_steps": SETTLE_STEPS, "core_clock": core_clk}
 
 
 def run_read_ceiling(args, steps: int | None = None) -> dict:

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 10
+#define NKV_ABI_VERSION 11
 
 #define NKV_OK 0
 #define NKV_ERR_INVALID 1     /* argument outside what the reference accepts */
@@ -630,6 +630,17 @@ int nkv_copy_bytes(const void* src, void* dst, int64_t nbytes, void* stream);
  * nbytes must be a multiple of 16.
  */
 int nkv_read_bw(const void* src, int64_t nbytes, uint32_t* sink, int64_t blocks, void* stream);
+
+/*
+ * Core clock probe: `blocks` workgroups of one wave each run `iters` rounds of two dependent
+ * FMAs; workgroup b writes out[3b] = its XCD, out[3b+1] = the core clock counter's advance
+ * (s_memtime) and out[3b+2] = the 100 MHz real-time counter's advance (s_memrealtime), so
+ * that 100 * out[3b+1] / out[3b+2] is its XCD's core clock in MHz while it ran. Launched right
+ * after a timed run, it reads the clock that run left (the clocks move over milliseconds).
+ * out holds 3 * blocks words; 1 <= blocks <= 1024, 1 <= iters <= 2^24. No counterpart in the
+ * reference (measurement only).
+ */
+int nkv_clock_probe(uint64_t* out, int64_t blocks, int64_t iters, void* stream);
 
 /*
  * The same ceiling for the decode kernels' own load pattern: `blocks` workgroups of 8 waves

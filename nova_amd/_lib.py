@@ -92,6 +92,7 @@ SIGNATURES = {
                                           I64, I64, P]),
     "nkv_copy_bytes": (c_int, [P, P, I64, P]),
     "nkv_read_bw": (c_int, [P, I64, P, I64, P]),
+    "nkv_clock_probe": (c_int, [P, I64, I64, P]),
     "nkv_read_bw_lds": (c_int, [P, I64, P, I64, P]),
     "nkv_l2_handover": (c_int, [c_int, P, P]),
     "nkv_decode_step_qkv_workspace_bytes": (I64, [I64, I64, I64, I64]),
@@ -105,7 +106,7 @@ SIGNATURES = {
     "nkv_qk_norm_rope": (c_int, [P, I64, I64, I64, P, P, c_float, P, P, P]),
 }
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _lib = None
 _lock = threading.Lock()

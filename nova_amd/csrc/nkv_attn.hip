@@ -3672,6 +3672,34 @@ __global__ __launch_bounds__(64) void xcd_probe_kernel(uint32_t* out) {
   if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
 }
 
+// Core clock probe: workgroup b (one wave) runs `iters` rounds of two dependent FMAs and records
+// its XCD and how far the core clock counter (s_memtime) and the 100 MHz real-time counter
+// (s_memrealtime) advanced meanwhile: out[3 b .. 3 b + 2]. The FMAs' result is kept by a
+// comparison that never holds, so the loop stays.
+__global__ __launch_bounds__(64) void clock_probe_kernel(uint64_t* out, int iters) {
+  const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  float x = threadIdx.x * 1e-3f, y = 1.0001f;
+  for (int i = 0; i < iters; ++i) {
+    x = __builtin_fmaf(x, y, 1e-7f);
+    y = __builtin_fmaf(y, 0.99999f, 1e-6f);
+  }
+  const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) {
+    out[3 * blockIdx.x] = xcc_id();
+    out[3 * blockIdx.x + 1] = t1 - t0 + (x == -1.0f ? (uint64_t)y : 0);
+    out[3 * blockIdx.x + 2] = r1 - r0;
+  }
+}
+
+extern "C" int nkv_clock_probe(uint64_t* out, int64_t blocks, int64_t iters, void* stream) {
+  set_error("");
+  if (!out || blocks <= 0 || blocks > 1024 || iters <= 0 || iters > (1 << 24))
+    return fail(NKV_ERR_INVALID, "clock_probe: out required, 1 <= blocks <= 1024, 1 <= iters <= 2^24");
+  hipLaunchKernelGGL(clock_probe_kernel, dim3((unsigned)blocks), dim3(64), 0, static_cast<hipStream_t>(stream), out,
+                     (int)iters);
+  return check_launch("clock_probe");
+}
+
 // The launch's hand-over fields: on when the current device was probed and its XCD count divides
 // hkv (so that workgroups b = h mod hkv of KV head h share XCD b mod n).
 static void l2_args(AttnArgs& a) {

@@ -97,6 +97,9 @@ def test_validation_errors_return_before_launch(lib):
     assert lib.nkv_attn_decode_t64(*args) == _lib.NKV_ERR_UNSUPPORTED
     assert b"head_dim" in lib.nkv_last_error()
     assert lib.nkv_copy_bytes(None, None, 15, None) == _lib.NKV_ERR_INVALID
+    assert lib.nkv_clock_probe(None, 8, 100, None) == _lib.NKV_ERR_INVALID
+    assert lib.nkv_clock_probe(ctypes.c_void_p(16), 0, 100, None) == _lib.NKV_ERR_INVALID
+    assert lib.nkv_clock_probe(ctypes.c_void_p(16), 8, 0, None) == _lib.NKV_ERR_INVALID
     assert lib.nkv_ring_mask(None, None, None, 64, None, None) == _lib.NKV_ERR_INVALID
     # decode-step projections: sizes and layouts are checked before anything is launched
     # (the non-null pointers below are never dereferenced)

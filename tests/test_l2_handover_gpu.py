@@ -129,3 +129,20 @@ def test_fused_step_on_equals_off(lib):
     for s, (a, b) in enumerate(zip(o_on, o_off)):
         assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), f"step {s}: outputs differ"
     _assert_same_state(c_on, c_off)
+
+
+def test_clock_probe_reads_every_xcd(lib):
+    """``nkv_clock_probe`` (measurement only): 64 one-wave workgroups dealt over the device's XCDs,
+    each with a core clock (core counter over the 100 MHz real-time counter) between the
+    device's idle floor and its 2.4 GHz maximum."""
+    dev = torch.device("cuda:0")
+    n = 64
+    buf = torch.zeros(3 * n, dtype=torch.int64, device=dev)
+    lib.call("nkv_clock_probe", buf.data_ptr(), n, 20000, lib.stream_ptr(dev))
+    torch.cuda.synchronize()
+    w = buf.view(n, 3).cpu()
+    assert (w[:, 1] > 0).all() and (w[:, 2] > 0).all()
+    mhz = 100.0 * w[:, 1].double() / w[:, 2].double()
+    assert ((mhz > 50) & (mhz < 2600)).all(), mhz
+    n_xcd = len(set(w[:, 0].tolist()))
+    assert n_xcd >= 1 and n % n_xcd == 0
