@@ -73,6 +73,19 @@ def test_prefill_split_settings_agree():
     assert (outs[0].float() - outs[1].float()).abs().max().item() <= 1e-3
 
 
+@pytest.mark.parametrize("used,splits", [(128, 1), (192, 1), (256, 2)])
+def test_prefill_few_groups_per_split(used, splits):
+    """Splits of two and three cache groups: the loop's start (two stages loaded before the first
+    group) and its end (no further load; the last group dequantizes a stale stage into a tile
+    buffer nothing reads) meet within a few groups."""
+    from nova_amd.kvattn import int8_prefill_attend
+
+    print(f"case used={used} splits={splits}", flush=True)
+    q, kch, vch, packed = _case(32, 8, used, 40, seed=90 + used)
+    got = int8_prefill_attend(q, kch, vch, *packed, used=used, splits=splits)
+    _check(got, q, kch, vch, packed, used, tag=f"used={used} splits={splits}")
+
+
 def test_prefill_chunk_512_over_16k():
     """The chunked-prefill workload: a 512-token chunk over a 16384-token int8 cache, 32 q /
     8 KV heads; checked on KV heads 0 and 7 (the fp64 oracle over all heads is slow)."""
