@@ -806,7 +806,7 @@ def bench_e2e(args, steps: int | None = None) -> dict:
     model = SkeletonForCausalLM(cfg, seed=5, device=dev, dtype=torch.float16).eval()
     fused = not getattr(args, "e2e_separate", False)
     model.use_decode_kernels(True, fused_qkv=fused)
-    max_len = -(-(ctx + 4 + W + K + 1) // 64) * 64
+    max_len = -(-(ctx + 4 + SETTLE_STEPS + W + K + 1) // 64) * 64
     dec = GraphDecoder(model, max_len=max_len, quant="int8", device=dev)
     if args.parts:
         dec.cache.set_parts(args.parts)
@@ -817,7 +817,7 @@ def bench_e2e(args, steps: int | None = None) -> dict:
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
     dec.capture(warmup=3)
-    for _ in range(W):
+    for _ in range(SETTLE_STEPS + W):  # the clocks settle (as for the decode), then the W warmup steps
         dec.step()
     torch.cuda.synchronize()
     pos0 = int(dec.cache.pos.item())
@@ -844,7 +844,7 @@ def bench_e2e(args, steps: int | None = None) -> dict:
                                            "three launches per layer (qkv GEMV, q/k norm + RoPE, append + attention)")},
             "algorithmic_bytes_per_step": round(step_bytes), "step_gbs": round(gbs, 1),
             "step_pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2), "prefill_s": round(prefill_s, 3),
-            "prefill_tokens_per_s": round(ctx / prefill_s, 1)}
+            "prefill_tokens_per_s": round(ctx / prefill_s, 1), "settle_steps": SETTLE_STEPS}
 
 
 # ---------------------------------------------------------------- main
