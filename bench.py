@@ -618,13 +618,14 @@ def run_paged(args, steps: int | None = None, scheme: str = "t64") -> dict:
     L, B, W = args.layers, 8, args.warmup
     K = steps or 128
     lens = [int(x) for x in torch.randint(1024, 16385, (B,), generator=torch.Generator().manual_seed(3))]
-    per_seq = max(-(-(n + W + K + 2) // 64) for n in lens)
-    total_pages = sum(-(-(n + W + K + 2) // 64) for n in lens)
+    S = SETTLE_STEPS  # untimed step replays before the W warmup ones: the clocks settle, as for the decode
+    per_seq = max(-(-(n + S + W + K + 2) // 64) for n in lens)
+    total_pages = sum(-(-(n + S + W + K + 2) // 64) for n in lens)
     cls = PagedKVInt8TokCache if scheme == "tok" else PagedKVInt8Cache
     cache = cls(L, HKV, D, HQ, max_seqs=B, num_pages=total_pages, max_pages_per_seq=per_seq, device=dev)
     g = torch.Generator(device=dev).manual_seed(3)
     for b, n in enumerate(lens):
-        cache.reserve(b, n + W + K + 1)
+        cache.reserve(b, n + S + W + K + 1)
         for layer in range(L):
             k = torch.randn(1, HKV, n, D, generator=g, device=dev).half()
             v = torch.randn(1, HKV, n, D, generator=g, device=dev).half()
@@ -640,14 +641,14 @@ def run_paged(args, steps: int | None = None, scheme: str = "t64") -> dict:
             cache.decode_step(ks[layer], vs[layer], qs[layer], layer)
         cache.pos[:B].add_(1)
     stream = torch.cuda.current_stream(dev)
-    for _ in range(W):
+    for _ in range(S + W):
         graph.replay()
-    cache.note_advanced(W)
+    cache.note_advanced(S + W)
     torch.cuda.synchronize()
     ms = _time_graph(graph, stream, K, 0)
     cache.note_advanced(K)
     assert torch.isfinite(cache.merged[:B]).all()
-    step_bytes = sum(sum(step_launch_bytes(n + W + i + 1, scheme) for n in lens) for i in range(K)) / K * L
+    step_bytes = sum(sum(step_launch_bytes(n + S + W + i + 1, scheme) for n in lens) for i in range(K)) / K * L
     gbs = step_bytes / (ms / 1e3) / 1e9
 
     # ---- the step's launches alone (pos fixed; each is the layer's only launch): the prefix kernel
@@ -657,7 +658,7 @@ def run_paged(args, steps: int | None = None, scheme: str = "t64") -> dict:
         for layer in range(L):
             cache.decode_step(ks[layer], vs[layer], qs[layer], layer)
     per_launch_s = _time_graph(g_launch, stream, K, W, SETTLE_STEPS) / 1e3 / L
-    pos = [n + W + K for n in lens]
+    pos = [n + S + W + K for n in lens]
     launch_bytes = sum(step_launch_bytes(p + 1, scheme) for p in pos)
     _calibration_copy(dev)
     kidx = 3 if scheme == "tok" else 2
@@ -671,7 +672,7 @@ def run_paged(args, steps: int | None = None, scheme: str = "t64") -> dict:
                       "lengths": lens, "layers": L, "page_tokens": 64, "work_units_per_head": cache.total_parts,
                       "launches_per_layer": 1},
            "step_gbs": round(gbs, 1), "step_pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-           "algorithmic_bytes_per_step": round(step_bytes),
+           "algorithmic_bytes_per_step": round(step_bytes), "settle_steps": S,
            "roofline": _roofline_hbm(launch_bytes, per_launch_s, f"paged_{scheme}", kname, L)}
     del graph, g_launch, cache
     torch.cuda.empty_cache()
