@@ -3279,8 +3279,10 @@ __global__ void ring_mask_kernel(const int64_t* written, const int64_t* qlen, co
 // groups j = split (mod S) up to its last query token. Per group, the 8 waves dequantize
 // the int8 codes once into fp16 LDS tiles (K row-major, V transposed, both padded against
 // bank conflicts), then every wave runs QK^T and PV on v_mfma_f32_16x16x32_f16 for its 32
-// rows. P is a single fp16 operand (scaled by 2^15), as a fused fp16 attention kernel
-// computes it. Each workgroup writes one partial per row; a combine kernel merges the splits.
+// rows. The cache groups take one workgroup barrier each: the tiles are double-buffered and
+// the next group is dequantized beside the current group's last product. P is a single fp16
+// operand (scaled by 2^15), as a fused fp16 attention kernel computes it. Each workgroup
+// writes one partial per row; a combine kernel merges the splits.
 constexpr int PF_WAVES = 8;
 constexpr int PF_THREADS = 64 * PF_WAVES;
 constexpr int PF_RB = 2;                             // MFMA row blocks per wave
