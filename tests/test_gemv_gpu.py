@@ -81,6 +81,7 @@ def _check(got, want, x, w, gamma, residual, tag):
     (2560, 9728, False, True),     # down_proj + residual
     (151936, 2560, True, False),   # lm_head with the final RMSNorm (4 rows per wave)
     (1001, 40, True, True),        # ragged: rows off the workgroup size, 5 chunks per row
+    (1029, 2560, True, True),      # ten-wave workgroups with the fused RMSNorm, a partial last workgroup
     (16389, 8, False, False),      # 4-row path with a partial last wave, one chunk per row
     (37, 16384, True, False),      # the largest input
 ])
